@@ -1,0 +1,189 @@
+/*
+ * splosh_q4.h -- C ABI of the MI355X (gfx950) quantized-weight matmul library.
+ *
+ * The library replaces the quantized GEMV/GEMM hot path of Splosh (the SploshQuant format
+ * contract and the GEMM entry points of SploshRuntime) with hand-written HIP kernels. Every entry
+ * point takes caller-owned device pointers and a hipStream_t, validates its arguments before it
+ * launches anything, returns a splosh_status, and is stream-ordered and asynchronous (except the
+ * pure host helpers, which touch no device). Nothing is allocated per call: kernels that need
+ * scratch memory take a caller workspace sized by splosh_workspace_bytes().
+ *
+ * Each declaration names the reference interface it stands in for (file:line in the Splosh tree).
+ *
+ * Formats
+ *   MLX affine q4 (SploshQuant/MlxAffine.swift:21-86): w[n][k] = bf16(scale) * q + bf16(bias),
+ *     q the 4-bit code at bits 4 (k % 8) of a uint32 word, one scale/bias per group of 64 k.
+ *     ROW_MAJOR: word (n * row_stride_words + k / 8), sidecar (n * groups + k / 64)
+ *       (Q4BufferLayout.swift:82-104), rows padded to 128 bytes by default.
+ *     TILED128: Converter.tile (Model/Retile.swift:135-153): codes
+ *       [n / 128][k / 64][n % 128][8 words], sidecars [n / 128][k / 64][n % 128].
+ *   GGUF Q5_K (Model/GgufQuant.swift:191-212) in GgufPlanes form (Model/GgufPlanes.swift:8-20):
+ *     plane0 [n/128][k/32][128][16 B], plane1 [n/128][k/32][128][4 B], meta [n/128][k/256][128][16 B].
+ *
+ * GEMM convention (Model/Gemm.swift:7): out[m][n] = sum_k a[m][k] * w[n][k] (+ residual[m][n]),
+ * a bf16 [rows][inner] with row stride lda, accumulated in fp32, out fp32 or bf16 (RNE).
+ */
+#ifndef SPLOSH_Q4_H
+#define SPLOSH_Q4_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t *hipStream_t;
+
+/* Status codes. 1..8 are GemmQ4Error's cases (Model/Gemm.swift:43-52); the rest are
+ * Q4BufferLayoutError (Quant/Q4BufferLayout.swift:16-23) and runtime failures
+ * (SploshError.capabilityGateFailure, Runtime/Q4Runtime.swift:141-143). */
+typedef enum splosh_status {
+    SPLOSH_OK = 0,
+    SPLOSH_ERR_INVALID_SHAPE = 1,
+    SPLOSH_ERR_LAYOUT_MISMATCH = 2,
+    SPLOSH_ERR_INVALID_ROW_STRIDE = 3,
+    SPLOSH_ERR_ORIENTATION_MISMATCH = 4,
+    SPLOSH_ERR_INVALID_GROUP_SIZE = 5,
+    SPLOSH_ERR_SIDECAR_GEOMETRY_MISMATCH = 6,
+    SPLOSH_ERR_SIDECAR_MISMATCH = 7,
+    SPLOSH_ERR_BUFFER_TOO_SMALL = 8,
+    SPLOSH_ERR_INVALID_DIMENSIONS = 9,
+    SPLOSH_ERR_ARITHMETIC_OVERFLOW = 10,
+    SPLOSH_ERR_INVALID_INDEX = 11,
+    SPLOSH_ERR_NULL_POINTER = 12,
+    SPLOSH_ERR_UNSUPPORTED = 13,
+    SPLOSH_ERR_WORKSPACE_TOO_SMALL = 14,
+    SPLOSH_ERR_HIP = 15
+} splosh_status;
+
+typedef enum splosh_orientation { SPLOSH_ROWS_BY_K = 0, SPLOSH_K_BY_COLUMNS = 1 } splosh_orientation;
+typedef enum splosh_q4_order { SPLOSH_Q4_ROW_MAJOR = 0, SPLOSH_Q4_TILED128 = 1 } splosh_q4_order;
+typedef enum splosh_dtype { SPLOSH_F32 = 0, SPLOSH_BF16 = 1 } splosh_dtype;
+
+/* Kernel choice (the reference selects kernels through SPLOSH_* environment variables,
+ * Runtime/Engine.swift:380-440; here the caller names one, or AUTO picks by rows). */
+typedef enum splosh_kernel {
+    SPLOSH_KERNEL_AUTO = 0,
+    SPLOSH_KERNEL_STREAM = 1,   /* rows <= 64: weight-streaming MFMA kernel on raw codes */
+    SPLOSH_KERNEL_DEQUANT = 2,  /* rows <= 64: weight-streaming MFMA kernel on dequantized bf16 */
+    SPLOSH_KERNEL_TILE = 3,     /* any rows: LDS-tiled dequant-to-bf16 MFMA GEMM (prefill) */
+    SPLOSH_KERNEL_SCALAR = 4    /* one thread per output (gemm_q4.metal semantics) */
+} splosh_kernel;
+
+/* Q4BufferLayout (Quant/Q4BufferLayout.swift:29-79). */
+typedef struct splosh_q4_layout {
+    int64_t rows;
+    int64_t logical_k;
+    int32_t orientation;           /* splosh_orientation */
+    int32_t reserved;
+    int64_t packed_words_per_row;
+    int64_t row_stride_bytes;
+    int64_t row_stride_words;
+    int64_t padding_words_per_row;
+    int64_t groups_per_row;
+    int64_t group_stride;
+} splosh_q4_layout;
+
+/* A resident q4 weight: the reference's Q4Handle (Runtime/Engine.swift, bound at
+ * engine.metal buffers 0..2). rows = outputs N, inner = K. For TILED128, row_stride_words is
+ * ignored (the tiled records are 8 words) and rows % 128 == 0, inner % 64 == 0. */
+typedef struct splosh_q4_weight {
+    const uint32_t *packed;
+    const uint16_t *scales;
+    const uint16_t *biases;
+    int64_t rows;
+    int64_t inner;
+    int64_t row_stride_words;
+    int32_t order;                 /* splosh_q4_order */
+    int32_t reserved;
+} splosh_q4_weight;
+
+/* A GGUF Q5_K weight in plane form (Model/GgufPlanes.swift:8-20, geometry :62-74). */
+typedef struct splosh_q5k_weight {
+    const uint8_t *plane0;
+    const uint8_t *plane1;
+    const uint8_t *meta;
+    int64_t rows;
+    int64_t inner;
+} splosh_q5k_weight;
+
+/* ---- host helpers (no device work) ------------------------------------------------------ */
+
+/* Q4BufferLayout.init (Quant/Q4BufferLayout.swift:43-79). row_stride_bytes 0 = aligned
+ * default; row_alignment 0 = 128. */
+int splosh_q4_layout_init(int64_t rows, int64_t logical_k, int orientation, int64_t row_stride_bytes,
+                          int64_t row_alignment, splosh_q4_layout *out);
+/* Q4BufferLayout.wordIndex / nibbleShift / sidecarIndex (Q4BufferLayout.swift:82-104). */
+int splosh_q4_layout_word_index(const splosh_q4_layout *layout, int64_t row, int64_t k, int64_t *out);
+int splosh_q4_layout_nibble_shift(const splosh_q4_layout *layout, int64_t row, int64_t k, uint32_t *out);
+int splosh_q4_layout_sidecar_index(const splosh_q4_layout *layout, int64_t row, int64_t k, int64_t *out);
+/* GemmQ4Shape.init + validate(layout:) (Model/Gemm.swift:13-40). */
+int splosh_q4_shape_validate(int64_t rows, int64_t columns, int64_t inner, const splosh_q4_layout *layout);
+
+/* Scratch bytes the GEMM entry points need for `rows` x `columns` x `inner` (0 when none). The
+ * reference's engine owns its scratch (Runtime/Engine.swift:460-486); here the caller does. */
+size_t splosh_workspace_bytes(int64_t rows, int64_t columns, int64_t inner);
+
+const char *splosh_status_string(int status);
+/* The message of the last failure on this thread ("" after success). */
+const char *splosh_last_error(void);
+const char *splosh_version(void);
+
+/* ---- MLX affine q4 ---------------------------------------------------------------------- */
+
+/* Q4GemmRuntime.dispatch (Runtime/Q4Runtime.swift:94-145) running gemm_q4
+ * (Shaders/gemm_q4.metal:31-54): c fp32 [rows][columns], one thread per output, either
+ * orientation. Validation is GemmQ4Shape.validate (which requires rowsByK). */
+int splosh_gemm_q4(const uint16_t *a, const uint32_t *packed, const uint16_t *scales,
+                   const uint16_t *biases, float *c, int64_t rows, int64_t columns, int64_t inner,
+                   const splosh_q4_layout *layout, hipStream_t stream);
+
+/* Engine.gemm(w, input:, output:, residual:, rows:) (Runtime/Engine.swift:1652-1806): one
+ * projection. residual may be NULL or alias out; it has out's dtype and ldc. */
+int splosh_q4_gemm(const splosh_q4_weight *w, const uint16_t *a, int64_t lda, void *out, int64_t ldc,
+                   int out_dtype, const void *residual, int64_t rows, int kernel, void *workspace,
+                   size_t workspace_bytes, hipStream_t stream);
+
+/* Engine.mlpIn(gate:up:input:output:scratch:rows:) (Runtime/Engine.swift:1911-1966) with the
+ * fused lane form sp_mlp_in_tiled_* (Shaders/engine.metal:1987-2055): out = silu(gate(a)) * up(a),
+ * both weights read in one pass over a. */
+int splosh_q4_mlp_in(const splosh_q4_weight *gate, const splosh_q4_weight *up, const uint16_t *a,
+                     int64_t lda, void *out, int64_t ldc, int out_dtype, int64_t rows, int kernel,
+                     void *workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* DequantOracle.dequantize (Oracle/DequantOracle.swift:11-25) on the device: out fp32
+ * [rows][inner], bit-identical to the CPU reference. */
+int splosh_q4_dequant(const splosh_q4_weight *w, float *out, hipStream_t stream);
+
+/* Converter.tile (Model/Retile.swift:135-153) and its inverse on the device:
+ * [row][group][element] <-> [row/128][group][row%128][element]. rows % 128 == 0,
+ * element_bytes % 2 == 0. src and dst must not overlap. */
+int splosh_tile128(const void *src, void *dst, int64_t rows, int64_t groups, int64_t element_bytes,
+                   hipStream_t stream);
+int splosh_untile128(const void *src, void *dst, int64_t rows, int64_t groups, int64_t element_bytes,
+                     hipStream_t stream);
+
+/* ---- GGUF Q5_K ---------------------------------------------------------------------------- */
+
+/* Engine.gemm on a GGUF weight (Runtime/Engine.swift:1671-1697, kernels
+ * Shaders/engine_gguf.metal:82-221 instantiated _q5k at :332-349). */
+int splosh_q5k_gemm(const splosh_q5k_weight *w, const uint16_t *a, int64_t lda, void *out, int64_t ldc,
+                    int out_dtype, const void *residual, int64_t rows, int kernel, void *workspace,
+                    size_t workspace_bytes, hipStream_t stream);
+
+/* GgufTensorType.decode for Q5_K (Model/GgufQuant.swift:191-212) read from the planes: out fp32
+ * [rows][inner], bit-identical to the CPU reference. */
+int splosh_q5k_dequant(const splosh_q5k_weight *w, float *out, hipStream_t stream);
+
+/* GgufPlanes.repack / unpack for Q5_K (Model/GgufPlanes.swift:103-194) on the device.
+ * native: rows x (inner / 256) blocks of 176 bytes. */
+int splosh_q5k_repack(const uint8_t *native, int64_t rows, int64_t inner, uint8_t *plane0,
+                      uint8_t *plane1, uint8_t *meta, hipStream_t stream);
+int splosh_q5k_unpack(const uint8_t *plane0, const uint8_t *plane1, const uint8_t *meta, int64_t rows,
+                      int64_t inner, uint8_t *native, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SPLOSH_Q4_H */

@@ -1,0 +1,55 @@
+"""Build libsplosh_q4.so (the HIP kernels and the C ABI) in-tree for gfx950 with hipcc.
+
+    python -m splosh_amd.build          # or splosh_amd.build.build()
+
+Objects go to splosh_amd/_build/, the library to splosh_amd/libsplosh_q4.so.
+"""
+import os
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+BUILD = PKG / "_build"
+LIB = PKG / "libsplosh_q4.so"
+SOURCES = ["api.cpp", "q4_basic.hip", "stream.hip", "q5k.hip"]
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+# Packed fp32 instructions are disabled for every device pass (see the build notes in DESIGN.md).
+DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+COMMON = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Wall", "-Wno-unused-result",
+          f"-I{ROOT / 'include'}"]
+
+
+def _compile(src):
+    obj = BUILD / (src.replace(".", "_") + ".o")
+    cmd = [HIPCC, *COMMON, *DEVICE_FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
+    if src.endswith(".cpp"):
+        cmd[1:1] = ["-x", "hip"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src}:\n{res.stderr}")
+    return obj
+
+
+def build(verbose=True):
+    BUILD.mkdir(exist_ok=True)
+    jobs = min(len(SOURCES), max(1, os.cpu_count() or 1))
+    with ThreadPoolExecutor(jobs) as pool:
+        objs = list(pool.map(_compile, SOURCES))
+    cmd = [HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *map(str, objs), "-o", str(LIB)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed:\n{res.stderr}")
+    if verbose:
+        print(f"built {LIB}")
+    return LIB
+
+
+if __name__ == "__main__":
+    build()
+    sys.exit(0)

@@ -1,0 +1,372 @@
+// api.cpp -- the C ABI (include/splosh_q4.h): argument validation with the reference's error
+// semantics, the kernel-choice policy, and launches. Everything here is host code; it never
+// allocates device memory and never synchronises a stream.
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/splosh_q4.h"
+#include "launch.hpp"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int status, const std::string &message) {
+    g_last_error = message;
+    return status;
+}
+
+int ok() {
+    g_last_error.clear();
+    return SPLOSH_OK;
+}
+
+int hip_status(hipError_t err, const char *what) {
+    if (err != hipSuccess)
+        return fail(SPLOSH_ERR_HIP, std::string(what) + ": " + hipGetErrorString(err));
+    return ok();
+}
+
+bool mul_overflows(int64_t a, int64_t b) { return a != 0 && b > INT64_MAX / a; }
+
+bool aligned(const void *p, uintptr_t bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
+
+constexpr int64_t kGroupSize = 64;
+constexpr int64_t kWordBytes = 4;
+constexpr int64_t kDefaultRowAlignment = 128;
+
+// Shared checks of the GEMM entry points on a q4 weight (the geometry GemmQ4Shape.validate and
+// Converter.isTiledWeight require, Model/Gemm.swift:19-40, Model/Retile.swift:33-36).
+int check_q4_weight(const splosh_q4_weight *w, const char *name) {
+    if (!w || !w->packed || !w->scales || !w->biases)
+        return fail(SPLOSH_ERR_NULL_POINTER, std::string(name) + ": null weight pointer");
+    if (w->rows <= 0 || w->inner <= 0)
+        return fail(SPLOSH_ERR_INVALID_SHAPE, std::string(name) + ": rows and inner must be positive");
+    if (w->inner > INT64_MAX - 63) return fail(SPLOSH_ERR_INVALID_SHAPE, "inner overflows");
+    if (w->order == SPLOSH_Q4_ROW_MAJOR) {
+        if (w->row_stride_words < (w->inner + 7) / 8)
+            return fail(SPLOSH_ERR_INVALID_ROW_STRIDE,
+                        std::string(name) + ": row_stride_words is shorter than the packed row");
+        if (mul_overflows(w->rows, w->row_stride_words))
+            return fail(SPLOSH_ERR_ARITHMETIC_OVERFLOW, "packed size overflows");
+    } else if (w->order == SPLOSH_Q4_TILED128) {
+        if (w->rows % 128 != 0 || w->inner % kGroupSize != 0)
+            return fail(SPLOSH_ERR_LAYOUT_MISMATCH,
+                        std::string(name) + ": the tiled layout needs rows % 128 == 0 and inner % 64 == 0");
+    } else {
+        return fail(SPLOSH_ERR_LAYOUT_MISMATCH, std::string(name) + ": unknown weight order");
+    }
+    return SPLOSH_OK;
+}
+
+int check_io(const uint16_t *a, int64_t lda, const void *out, int64_t ldc, int out_dtype, int64_t rows,
+             int64_t n, int64_t k) {
+    if (!a || !out) return fail(SPLOSH_ERR_NULL_POINTER, "null activation or output pointer");
+    if (rows <= 0) return fail(SPLOSH_ERR_INVALID_SHAPE, "rows must be positive");
+    if (lda < k) return fail(SPLOSH_ERR_INVALID_SHAPE, "lda is shorter than inner");
+    if (ldc < n) return fail(SPLOSH_ERR_INVALID_SHAPE, "ldc is shorter than the weight's rows");
+    if (out_dtype != SPLOSH_F32 && out_dtype != SPLOSH_BF16) return fail(SPLOSH_ERR_UNSUPPORTED, "unknown out_dtype");
+    if (mul_overflows(rows, lda) || mul_overflows(rows, ldc)) return fail(SPLOSH_ERR_ARITHMETIC_OVERFLOW, "size overflows");
+    return SPLOSH_OK;
+}
+
+// Whether the streaming kernels can take this call: whole 64-groups, 16-byte aligned activation
+// rows, 8-byte aligned code records.
+bool q4_stream_eligible(const splosh_q4_weight &w, const uint16_t *a, int64_t lda) {
+    if (w.inner % kGroupSize != 0) return false;
+    if (lda % 8 != 0 || !aligned(a, 16)) return false;
+    if (!aligned(w.packed, 8)) return false;
+    if (w.order == SPLOSH_Q4_ROW_MAJOR && w.row_stride_words % 2 != 0) return false;
+    return true;
+}
+
+int q4_gemm_impl(const splosh_q4_weight *w, const splosh_q4_weight *up, const uint16_t *a, int64_t lda, void *out,
+                 int64_t ldc, int out_dtype, const void *residual, int64_t rows, int kernel, hipStream_t stream) {
+    int st = check_q4_weight(w, up ? "gate" : "weight");
+    if (st) return st;
+    if (up) {
+        if ((st = check_q4_weight(up, "up"))) return st;
+        if (up->rows != w->rows || up->inner != w->inner || up->order != w->order ||
+            (w->order == SPLOSH_Q4_ROW_MAJOR && up->row_stride_words != w->row_stride_words))
+            return fail(SPLOSH_ERR_LAYOUT_MISMATCH, "gate and up weights differ in geometry");
+    }
+    if ((st = check_io(a, lda, out, ldc, out_dtype, rows, w->rows, w->inner))) return st;
+    const bool eligible = q4_stream_eligible(*w, a, lda) && (!up || q4_stream_eligible(*up, a, lda));
+    int choice = kernel;
+    if (choice == SPLOSH_KERNEL_AUTO) choice = eligible ? SPLOSH_KERNEL_STREAM : SPLOSH_KERNEL_SCALAR;
+    switch (choice) {
+        case SPLOSH_KERNEL_STREAM: {
+            if (!eligible)
+                return fail(SPLOSH_ERR_UNSUPPORTED,
+                            "stream kernel needs inner % 64 == 0, lda % 8 == 0 and aligned operands");
+            const splosh::StreamPlan plan = splosh::plan_stream(rows, w->rows, w->inner / kGroupSize, up != nullptr, 4);
+            if (plan.row_chunks > 65535) return fail(SPLOSH_ERR_UNSUPPORTED, "too many rows for one launch");
+            return hip_status(splosh::launch_q4_stream(plan, *w, up, a, lda, out, ldc, out_dtype, residual, rows, stream),
+                              "q4 stream launch");
+        }
+        case SPLOSH_KERNEL_SCALAR:
+            if (rows > 65535) return fail(SPLOSH_ERR_UNSUPPORTED, "scalar kernel takes at most 65535 rows");
+            return hip_status(splosh::launch_q4_gemm_scalar(*w, up, a, lda, out, ldc, out_dtype, residual, rows, stream),
+                              "q4 scalar launch");
+        case SPLOSH_KERNEL_DEQUANT:
+        case SPLOSH_KERNEL_TILE:
+            return fail(SPLOSH_ERR_UNSUPPORTED, "kernel not available in this build");
+        default:
+            return fail(SPLOSH_ERR_UNSUPPORTED, "unknown kernel choice");
+    }
+}
+
+int check_q5k_weight(const splosh_q5k_weight *w) {
+    if (!w || !w->plane0 || !w->plane1 || !w->meta) return fail(SPLOSH_ERR_NULL_POINTER, "null Q5_K plane pointer");
+    if (w->rows <= 0 || w->inner <= 0) return fail(SPLOSH_ERR_INVALID_SHAPE, "rows and inner must be positive");
+    // GgufPlanes.sizes: whole tiles of 128 rows, whole 256-element blocks (GgufPlanes.swift:78-86).
+    if (w->rows % 128 != 0 || w->inner % 256 != 0)
+        return fail(SPLOSH_ERR_LAYOUT_MISMATCH, "Q5_K planes need rows % 128 == 0 and inner % 256 == 0");
+    return SPLOSH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *splosh_version(void) { return "splosh-amd 0.1.0 (gfx950)"; }
+
+const char *splosh_last_error(void) { return g_last_error.c_str(); }
+
+const char *splosh_status_string(int status) {
+    switch (status) {
+        case SPLOSH_OK: return "ok";
+        case SPLOSH_ERR_INVALID_SHAPE: return "invalidShape";
+        case SPLOSH_ERR_LAYOUT_MISMATCH: return "layoutMismatch";
+        case SPLOSH_ERR_INVALID_ROW_STRIDE: return "invalidRowStride";
+        case SPLOSH_ERR_ORIENTATION_MISMATCH: return "orientationMismatch";
+        case SPLOSH_ERR_INVALID_GROUP_SIZE: return "invalidGroupSize";
+        case SPLOSH_ERR_SIDECAR_GEOMETRY_MISMATCH: return "sidecarGeometryMismatch";
+        case SPLOSH_ERR_SIDECAR_MISMATCH: return "sidecarMismatch";
+        case SPLOSH_ERR_BUFFER_TOO_SMALL: return "bufferTooSmall";
+        case SPLOSH_ERR_INVALID_DIMENSIONS: return "invalidDimensions";
+        case SPLOSH_ERR_ARITHMETIC_OVERFLOW: return "arithmeticOverflow";
+        case SPLOSH_ERR_INVALID_INDEX: return "invalidIndex";
+        case SPLOSH_ERR_NULL_POINTER: return "nullPointer";
+        case SPLOSH_ERR_UNSUPPORTED: return "unsupported";
+        case SPLOSH_ERR_WORKSPACE_TOO_SMALL: return "workspaceTooSmall";
+        case SPLOSH_ERR_HIP: return "hipError";
+        default: return "unknown";
+    }
+}
+
+// Q4BufferLayout.init (Quant/Q4BufferLayout.swift:43-79).
+int splosh_q4_layout_init(int64_t rows, int64_t logical_k, int orientation, int64_t row_stride_bytes,
+                          int64_t row_alignment, splosh_q4_layout *out) {
+    if (!out) return fail(SPLOSH_ERR_NULL_POINTER, "null layout");
+    if (row_alignment == 0) row_alignment = kDefaultRowAlignment;
+    if (rows <= 0 || logical_k <= 0 || row_alignment <= 0 ||
+        (orientation != SPLOSH_ROWS_BY_K && orientation != SPLOSH_K_BY_COLUMNS))
+        return fail(SPLOSH_ERR_INVALID_DIMENSIONS, "rows, logical_k and alignment must be positive");
+    if (logical_k > INT64_MAX - 7 || rows > INT64_MAX - 7) return fail(SPLOSH_ERR_ARITHMETIC_OVERFLOW, "overflow");
+    const int64_t packed = orientation == SPLOSH_ROWS_BY_K ? (logical_k + 7) / 8 : (rows + 7) / 8;
+    if (packed > INT64_MAX / kWordBytes) return fail(SPLOSH_ERR_ARITHMETIC_OVERFLOW, "overflow");
+    const int64_t minimum = packed * kWordBytes;
+    int64_t stride;
+    if (row_stride_bytes != 0) {
+        stride = row_stride_bytes;
+    } else {
+        if (minimum > INT64_MAX - row_alignment + 1) return fail(SPLOSH_ERR_ARITHMETIC_OVERFLOW, "overflow");
+        const int64_t blocks = (minimum + row_alignment - 1) / row_alignment;
+        if (blocks > INT64_MAX / row_alignment) return fail(SPLOSH_ERR_ARITHMETIC_OVERFLOW, "overflow");
+        stride = blocks * row_alignment;
+    }
+    if (stride < minimum || stride % kWordBytes != 0)
+        return fail(SPLOSH_ERR_INVALID_ROW_STRIDE, "row stride is shorter than the row or not whole words");
+    if (logical_k > INT64_MAX - (kGroupSize - 1)) return fail(SPLOSH_ERR_ARITHMETIC_OVERFLOW, "overflow");
+    const int64_t groups = (logical_k + kGroupSize - 1) / kGroupSize;
+    const int64_t physical_rows = orientation == SPLOSH_ROWS_BY_K ? rows : logical_k;
+    if (physical_rows > INT64_MAX / (stride / kWordBytes) || rows > INT64_MAX / groups)
+        return fail(SPLOSH_ERR_ARITHMETIC_OVERFLOW, "overflow");
+    out->rows = rows;
+    out->logical_k = logical_k;
+    out->orientation = orientation;
+    out->reserved = 0;
+    out->packed_words_per_row = packed;
+    out->row_stride_bytes = stride;
+    out->row_stride_words = stride / kWordBytes;
+    out->padding_words_per_row = stride / kWordBytes - packed;
+    out->groups_per_row = groups;
+    out->group_stride = groups;
+    return ok();
+}
+
+static int validate_index(const splosh_q4_layout *l, int64_t row, int64_t k) {
+    if (!l) return fail(SPLOSH_ERR_NULL_POINTER, "null layout");
+    if (row < 0 || row >= l->rows || k < 0 || k >= l->logical_k)
+        return fail(SPLOSH_ERR_INVALID_INDEX, "index out of the logical matrix");
+    return SPLOSH_OK;
+}
+
+// Q4BufferLayout.wordIndex (Q4BufferLayout.swift:82-92).
+int splosh_q4_layout_word_index(const splosh_q4_layout *l, int64_t row, int64_t k, int64_t *out) {
+    int st = validate_index(l, row, k);
+    if (st) return st;
+    if (!out) return fail(SPLOSH_ERR_NULL_POINTER, "null output");
+    *out = l->orientation == SPLOSH_ROWS_BY_K ? row * l->row_stride_words + k / 8 : k * l->row_stride_words + row / 8;
+    return ok();
+}
+
+// Q4BufferLayout.nibbleShift (Q4BufferLayout.swift:94-98).
+int splosh_q4_layout_nibble_shift(const splosh_q4_layout *l, int64_t row, int64_t k, uint32_t *out) {
+    int st = validate_index(l, row, k);
+    if (st) return st;
+    if (!out) return fail(SPLOSH_ERR_NULL_POINTER, "null output");
+    *out = (uint32_t)((l->orientation == SPLOSH_ROWS_BY_K ? k % 8 : row % 8) * 4);
+    return ok();
+}
+
+// Q4BufferLayout.sidecarIndex (Q4BufferLayout.swift:100-104).
+int splosh_q4_layout_sidecar_index(const splosh_q4_layout *l, int64_t row, int64_t k, int64_t *out) {
+    int st = validate_index(l, row, k);
+    if (st) return st;
+    if (!out) return fail(SPLOSH_ERR_NULL_POINTER, "null output");
+    *out = row * l->group_stride + k / kGroupSize;
+    return ok();
+}
+
+// GemmQ4Shape.init + validate(layout:) (Model/Gemm.swift:13-40).
+int splosh_q4_shape_validate(int64_t rows, int64_t columns, int64_t inner, const splosh_q4_layout *l) {
+    if (rows <= 0 || columns <= 0 || inner <= 0) return fail(SPLOSH_ERR_INVALID_SHAPE, "invalidShape");
+    if (!l) return fail(SPLOSH_ERR_NULL_POINTER, "null layout");
+    if (l->rows != columns || l->logical_k != inner) return fail(SPLOSH_ERR_LAYOUT_MISMATCH, "layoutMismatch");
+    if (l->orientation != SPLOSH_ROWS_BY_K) return fail(SPLOSH_ERR_ORIENTATION_MISMATCH, "orientationMismatch");
+    if (l->row_stride_bytes < kDefaultRowAlignment || l->row_stride_bytes % kDefaultRowAlignment != 0 ||
+        l->row_stride_bytes % kWordBytes != 0 || l->row_stride_bytes < l->packed_words_per_row * kWordBytes)
+        return fail(SPLOSH_ERR_INVALID_ROW_STRIDE, "invalidRowStride");
+    if (inner > INT64_MAX - (kGroupSize - 1)) return fail(SPLOSH_ERR_INVALID_SHAPE, "invalidShape");
+    if (l->groups_per_row != (inner + kGroupSize - 1) / kGroupSize || l->group_stride != l->groups_per_row)
+        return fail(SPLOSH_ERR_SIDECAR_GEOMETRY_MISMATCH, "sidecarGeometryMismatch");
+    return ok();
+}
+
+size_t splosh_workspace_bytes(int64_t rows, int64_t columns, int64_t inner) {
+    (void)rows;
+    (void)columns;
+    (void)inner;
+    return 0;
+}
+
+// Q4GemmRuntime.dispatch (Runtime/Q4Runtime.swift:94-145).
+int splosh_gemm_q4(const uint16_t *a, const uint32_t *packed, const uint16_t *scales, const uint16_t *biases,
+                   float *c, int64_t rows, int64_t columns, int64_t inner, const splosh_q4_layout *layout,
+                   hipStream_t stream) {
+    int st = splosh_q4_shape_validate(rows, columns, inner, layout);
+    if (st) return st;
+    if (mul_overflows(rows, inner) || mul_overflows(rows, columns) || rows > 65535)
+        return fail(SPLOSH_ERR_INVALID_SHAPE, "invalidShape");
+    if (!a || !packed || !scales || !biases || !c) return fail(SPLOSH_ERR_NULL_POINTER, "null buffer");
+    return hip_status(splosh::launch_gemm_q4_scalar(a, packed, scales, biases, c, rows, columns, inner,
+                                                    layout->row_stride_words, layout->orientation,
+                                                    layout->groups_per_row, stream),
+                      "gemm_q4 launch");
+}
+
+int splosh_q4_gemm(const splosh_q4_weight *w, const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype,
+                   const void *residual, int64_t rows, int kernel, void *workspace, size_t workspace_bytes,
+                   hipStream_t stream) {
+    (void)workspace;
+    (void)workspace_bytes;
+    return q4_gemm_impl(w, nullptr, a, lda, out, ldc, out_dtype, residual, rows, kernel, stream);
+}
+
+int splosh_q4_mlp_in(const splosh_q4_weight *gate, const splosh_q4_weight *up, const uint16_t *a, int64_t lda,
+                     void *out, int64_t ldc, int out_dtype, int64_t rows, int kernel, void *workspace,
+                     size_t workspace_bytes, hipStream_t stream) {
+    (void)workspace;
+    (void)workspace_bytes;
+    if (!up) return fail(SPLOSH_ERR_NULL_POINTER, "null up weight");
+    return q4_gemm_impl(gate, up, a, lda, out, ldc, out_dtype, nullptr, rows, kernel, stream);
+}
+
+int splosh_q4_dequant(const splosh_q4_weight *w, float *out, hipStream_t stream) {
+    int st = check_q4_weight(w, "weight");
+    if (st) return st;
+    if (!out) return fail(SPLOSH_ERR_NULL_POINTER, "null output");
+    return hip_status(splosh::launch_q4_dequant(*w, out, stream), "q4 dequant launch");
+}
+
+static int tile_common(const void *src, void *dst, int64_t rows, int64_t groups, int64_t element_bytes, bool inverse,
+                       hipStream_t stream) {
+    if (!src || !dst) return fail(SPLOSH_ERR_NULL_POINTER, "null buffer");
+    if (rows <= 0 || groups <= 0 || element_bytes <= 0 || rows % 128 != 0 || element_bytes % 2 != 0)
+        return fail(SPLOSH_ERR_INVALID_SHAPE, "tile needs rows % 128 == 0 and even element bytes");
+    if (mul_overflows(rows, groups) || mul_overflows(rows * groups, element_bytes))
+        return fail(SPLOSH_ERR_ARITHMETIC_OVERFLOW, "size overflows");
+    return hip_status(splosh::launch_tile128(src, dst, rows, groups, element_bytes, inverse, stream), "tile launch");
+}
+
+int splosh_tile128(const void *src, void *dst, int64_t rows, int64_t groups, int64_t element_bytes, hipStream_t stream) {
+    return tile_common(src, dst, rows, groups, element_bytes, false, stream);
+}
+
+int splosh_untile128(const void *src, void *dst, int64_t rows, int64_t groups, int64_t element_bytes,
+                     hipStream_t stream) {
+    return tile_common(src, dst, rows, groups, element_bytes, true, stream);
+}
+
+int splosh_q5k_gemm(const splosh_q5k_weight *w, const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype,
+                    const void *residual, int64_t rows, int kernel, void *workspace, size_t workspace_bytes,
+                    hipStream_t stream) {
+    (void)workspace;
+    (void)workspace_bytes;
+    int st = check_q5k_weight(w);
+    if (st) return st;
+    if ((st = check_io(a, lda, out, ldc, out_dtype, rows, w->rows, w->inner))) return st;
+    const bool eligible = lda % 4 == 0 && aligned(a, 8) && aligned(w->plane0, 16) && aligned(w->plane1, 4) &&
+                          aligned(w->meta, 16);
+    int choice = kernel == SPLOSH_KERNEL_AUTO ? (eligible ? SPLOSH_KERNEL_STREAM : SPLOSH_KERNEL_SCALAR) : kernel;
+    switch (choice) {
+        case SPLOSH_KERNEL_STREAM: {
+            if (!eligible) return fail(SPLOSH_ERR_UNSUPPORTED, "stream kernel needs lda % 4 == 0 and aligned planes");
+            const splosh::StreamPlan plan = splosh::plan_stream(rows, w->rows, w->inner / 256, false, 2);
+            if (plan.row_chunks > 65535) return fail(SPLOSH_ERR_UNSUPPORTED, "too many rows for one launch");
+            return hip_status(splosh::launch_q5k_stream(plan, *w, a, lda, out, ldc, out_dtype, residual, rows, stream),
+                              "q5k stream launch");
+        }
+        case SPLOSH_KERNEL_SCALAR:
+            if (rows > 65535) return fail(SPLOSH_ERR_UNSUPPORTED, "scalar kernel takes at most 65535 rows");
+            return hip_status(splosh::launch_q5k_gemm_scalar(*w, a, lda, out, ldc, out_dtype, residual, rows, stream),
+                              "q5k scalar launch");
+        default:
+            return fail(SPLOSH_ERR_UNSUPPORTED, "kernel not available for Q5_K in this build");
+    }
+}
+
+int splosh_q5k_dequant(const splosh_q5k_weight *w, float *out, hipStream_t stream) {
+    int st = check_q5k_weight(w);
+    if (st) return st;
+    if (!out) return fail(SPLOSH_ERR_NULL_POINTER, "null output");
+    return hip_status(splosh::launch_q5k_dequant(*w, out, stream), "q5k dequant launch");
+}
+
+int splosh_q5k_repack(const uint8_t *native, int64_t rows, int64_t inner, uint8_t *plane0, uint8_t *plane1,
+                      uint8_t *meta, hipStream_t stream) {
+    if (!native || !plane0 || !plane1 || !meta) return fail(SPLOSH_ERR_NULL_POINTER, "null buffer");
+    if (rows <= 0 || inner <= 0 || rows % 128 != 0 || inner % 256 != 0)
+        return fail(SPLOSH_ERR_LAYOUT_MISMATCH, "Q5_K planes need rows % 128 == 0 and inner % 256 == 0");
+    return hip_status(splosh::launch_q5k_repack(native, rows, inner, plane0, plane1, meta, false, stream),
+                      "q5k repack launch");
+}
+
+int splosh_q5k_unpack(const uint8_t *plane0, const uint8_t *plane1, const uint8_t *meta, int64_t rows, int64_t inner,
+                      uint8_t *native, hipStream_t stream) {
+    if (!native || !plane0 || !plane1 || !meta) return fail(SPLOSH_ERR_NULL_POINTER, "null buffer");
+    if (rows <= 0 || inner <= 0 || rows % 128 != 0 || inner % 256 != 0)
+        return fail(SPLOSH_ERR_LAYOUT_MISMATCH, "Q5_K planes need rows % 128 == 0 and inner % 256 == 0");
+    return hip_status(splosh::launch_q5k_repack(native, rows, inner, const_cast<uint8_t *>(plane0),
+                                                const_cast<uint8_t *>(plane1), const_cast<uint8_t *>(meta), true,
+                                                stream),
+                      "q5k unpack launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,56 @@
+// common.hpp -- device types and helpers shared by the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace splosh {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+constexpr int kGroup = 64;       // MLX affine group size (Quant/MlxAffine.swift:22)
+constexpr int kTileRows = 128;   // Converter.tileRows (Model/Retile.swift:17)
+
+// bf16 bit pattern -> fp32: the value is the top half of the float (Q4BufferLayout.swift:123-125).
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits) {
+    return __uint_as_float(bits << 16);
+}
+
+// IEEE binary16 bit pattern -> fp32 (exact widening, v_cvt_f32_f16).
+__device__ __forceinline__ float half_bits_to_f32(uint32_t bits) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(bits & 0xffffu));
+}
+
+// fp32 -> bf16 with round-to-nearest-even (NaN stays NaN), one instruction on gfx950.
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2(float lo, float hi) {
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    f32x2 v = {lo, hi};
+    bf16x2 r = __builtin_convertvector(v, bf16x2);
+    return __builtin_bit_cast(uint32_t, r);
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16(float v) {
+    return (uint16_t)(f32x2_to_bf16x2(v, 0.0f) & 0xffffu);
+}
+
+// The tiled record of (row n, group g) for `groups` groups a row (Model/Retile.swift:142-147).
+__device__ __forceinline__ int64_t tiled_record(int64_t n, int64_t g, int64_t groups) {
+    return ((n >> 7) * groups + g) * kTileRows + (n & (kTileRows - 1));
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// v_perm_b32: byte i of the result is byte sel[i] of the 8-byte value {hi, lo} (lo = bytes 0..3).
+__device__ __forceinline__ uint32_t perm_bytes(uint32_t hi, uint32_t lo, uint32_t sel) {
+    return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
+
+}  // namespace splosh

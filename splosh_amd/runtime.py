@@ -1,0 +1,260 @@
+"""Operator entry points of the q4 / Q5_K path on torch device tensors.
+
+PyTorch-ROCm supplies device memory and streams only; every computation is a call into
+libsplosh_q4.so through its C ABI. The names follow the reference's host API:
+
+* ``Q4GemmRuntime.dispatch`` -- Runtime/Q4Runtime.swift:94-145 (gemm_q4, fp32 out, synchronous).
+* ``Engine.gemm`` / ``Engine.mlp_in`` -- Runtime/Engine.swift:1652, :1911 (stream-ordered).
+* ``dequant``, ``tile128``, ``q5k_repack`` -- DequantOracle.dequantize, Converter.tile,
+  GgufPlanes.repack on the device.
+
+Buffer-size checks (GemmQ4Error.bufferTooSmall) happen here because the C ABI sees raw pointers.
+"""
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from ._lib import GemmQ4Error, SploshError
+from .quant import GROUP_SIZE, TILE_ROWS, GemmQ4Shape, Q4BufferLayout
+
+AUTO = _lib.KERNEL_AUTO
+STREAM = _lib.KERNEL_STREAM
+DEQUANT = _lib.KERNEL_DEQUANT
+TILE = _lib.KERNEL_TILE
+SCALAR = _lib.KERNEL_SCALAR
+ROW_MAJOR = _lib.ROW_MAJOR
+TILED128 = _lib.TILED128
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _stream(stream=None):
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def _require(t, nbytes, name):
+    have = t.numel() * t.element_size()
+    if have < nbytes:
+        raise GemmQ4Error(8, f"bufferTooSmall(name: {name}, expected: {nbytes}, observed: {have})")
+    if not t.is_cuda:
+        raise SploshError(12, f"{name} is not a device tensor")
+
+
+def _dtype_code(dtype):
+    if dtype == torch.float32:
+        return _lib.F32
+    if dtype == torch.bfloat16:
+        return _lib.BF16
+    raise SploshError(13, f"unsupported output dtype {dtype}")
+
+
+@dataclass
+class Q4Weight:
+    """A resident MLX affine q4 weight (the reference's Q4Handle): int32 packed words, bf16 scale
+    and bias sidecars (as int16 or bfloat16 tensors), `rows` outputs x `inner` inputs."""
+
+    packed: torch.Tensor
+    scales: torch.Tensor
+    biases: torch.Tensor
+    rows: int
+    inner: int
+    order: int = TILED128
+    row_stride_words: int = 0
+
+    def __post_init__(self):
+        groups = (self.inner + GROUP_SIZE - 1) // GROUP_SIZE
+        if self.order == TILED128:
+            words = self.rows * groups * 8
+        else:
+            if self.row_stride_words == 0:
+                self.row_stride_words = ((self.inner + 7) // 8 * 4 + 127) // 128 * 32
+            words = self.rows * self.row_stride_words
+        _require(self.packed, words * 4, "packed")
+        _require(self.scales, self.rows * groups * 2, "scales")
+        _require(self.biases, self.rows * groups * 2, "biases")
+
+    def c(self):
+        return _lib.Q4Weight(self.packed.data_ptr(), self.scales.data_ptr(), self.biases.data_ptr(), self.rows,
+                             self.inner, self.row_stride_words, self.order, 0)
+
+    @property
+    def nbytes(self):
+        """Algorithmic bytes: N K / 2 codes + N (K / 64) * 4 sidecar bytes."""
+        return self.rows * self.inner // 2 + self.rows * (self.inner // GROUP_SIZE) * 4
+
+
+@dataclass
+class Q5KWeight:
+    """A GGUF Q5_K weight in plane form (Model/GgufPlanes.swift:8-20)."""
+
+    plane0: torch.Tensor
+    plane1: torch.Tensor
+    meta: torch.Tensor
+    rows: int
+    inner: int
+
+    def __post_init__(self):
+        groups = self.inner // 32
+        _require(self.plane0, self.rows * groups * 16, "plane0")
+        _require(self.plane1, self.rows * groups * 4, "plane1")
+        _require(self.meta, self.rows * (self.inner // 256) * 16, "meta")
+
+    def c(self):
+        return _lib.Q5KWeight(self.plane0.data_ptr(), self.plane1.data_ptr(), self.meta.data_ptr(), self.rows,
+                              self.inner)
+
+    @property
+    def nbytes(self):
+        return self.rows * (self.inner // 256) * 176
+
+
+def _out(a, rows, n, out, out_dtype):
+    if out is None:
+        out = torch.empty((rows, n), dtype=out_dtype, device=a.device)
+    return out
+
+
+def gemm(w, a, out=None, residual=None, out_dtype=torch.bfloat16, kernel=AUTO, rows=None, stream=None):
+    """Engine.gemm (Runtime/Engine.swift:1652-1806): out = a @ dequant(w)^T (+ residual).
+
+    ``a`` is bf16 [rows, inner] (row stride a.stride(0)); ``out`` [rows, w.rows] in fp32 or bf16;
+    ``residual`` may be ``out`` itself."""
+    rows = a.shape[0] if rows is None else rows
+    if a.dtype != torch.bfloat16:
+        raise SploshError(13, "activations must be bf16")
+    if a.stride(-1) != 1:
+        raise SploshError(1, "activation rows must be contiguous")
+    out = _out(a, rows, w.rows, out, out_dtype)
+    _require(a, ((rows - 1) * a.stride(0) + w.inner) * 2, "a")
+    _require(out, ((rows - 1) * out.stride(0) + w.rows) * out.element_size(), "output")
+    if residual is not None:
+        if residual.dtype != out.dtype or residual.stride(0) != out.stride(0):
+            raise SploshError(13, "residual must match the output's dtype and row stride")
+    wc = w.c()
+    if isinstance(w, Q4Weight):
+        st = _lib.lib().splosh_q4_gemm(ctypes.byref(wc), _ptr(a), a.stride(0), _ptr(out), out.stride(0),
+                                       _dtype_code(out.dtype), _ptr(residual), rows, kernel, None, 0,
+                                       _stream(stream))
+    else:
+        st = _lib.lib().splosh_q5k_gemm(ctypes.byref(wc), _ptr(a), a.stride(0), _ptr(out), out.stride(0),
+                                        _dtype_code(out.dtype), _ptr(residual), rows, kernel, None, 0,
+                                        _stream(stream))
+    _lib.check(st)
+    return out
+
+
+def mlp_in(gate, up, a, out=None, out_dtype=torch.bfloat16, kernel=AUTO, rows=None, stream=None):
+    """Engine.mlpIn (Runtime/Engine.swift:1911-1966): out = silu(a @ gate^T) * (a @ up^T), one
+    pass over the activations for both weights."""
+    rows = a.shape[0] if rows is None else rows
+    if a.dtype != torch.bfloat16 or a.stride(-1) != 1:
+        raise SploshError(13, "activations must be contiguous bf16 rows")
+    out = _out(a, rows, gate.rows, out, out_dtype)
+    _require(a, ((rows - 1) * a.stride(0) + gate.inner) * 2, "a")
+    _require(out, ((rows - 1) * out.stride(0) + gate.rows) * out.element_size(), "output")
+    gc, uc = gate.c(), up.c()
+    st = _lib.lib().splosh_q4_mlp_in(ctypes.byref(gc), ctypes.byref(uc), _ptr(a), a.stride(0), _ptr(out),
+                                     out.stride(0), _dtype_code(out.dtype), rows, kernel, None, 0, _stream(stream))
+    _lib.check(st)
+    return out
+
+
+def dequant(w, out=None, stream=None):
+    """DequantOracle.dequantize / GgufTensorType.decode on the device: fp32 [rows, inner]."""
+    if out is None:
+        dev = w.packed.device if isinstance(w, Q4Weight) else w.plane0.device
+        out = torch.empty((w.rows, w.inner), dtype=torch.float32, device=dev)
+    _require(out, w.rows * w.inner * 4, "output")
+    wc = w.c()
+    fn = _lib.lib().splosh_q4_dequant if isinstance(w, Q4Weight) else _lib.lib().splosh_q5k_dequant
+    _lib.check(fn(ctypes.byref(wc), _ptr(out), _stream(stream)))
+    return out
+
+
+def tile128(src, rows, groups, element_bytes, inverse=False, out=None, stream=None):
+    """Converter.tile (Model/Retile.swift:135-153) on the device (or its inverse)."""
+    if out is None:
+        out = torch.empty_like(src)
+    nbytes = rows * groups * element_bytes
+    _require(src, nbytes, "src")
+    _require(out, nbytes, "dst")
+    fn = _lib.lib().splosh_untile128 if inverse else _lib.lib().splosh_tile128
+    _lib.check(fn(_ptr(src), _ptr(out), rows, groups, element_bytes, _stream(stream)))
+    return out
+
+
+def q4_to_tiled(w, stream=None):
+    """A row-major (unpadded) q4 weight retiled to the 128-row layout the kernels prefer."""
+    if w.order == TILED128:
+        return w
+    groups = w.inner // GROUP_SIZE
+    if w.row_stride_words != w.inner // 8:
+        packed = w.packed.view(w.rows, -1)[:, : w.inner // 8].contiguous()
+    else:
+        packed = w.packed
+    tp = tile128(packed, w.rows, groups, 32, stream=stream)
+    ts = tile128(w.scales, w.rows, groups, 2, stream=stream)
+    tb = tile128(w.biases, w.rows, groups, 2, stream=stream)
+    return Q4Weight(tp, ts, tb, w.rows, w.inner, TILED128)
+
+
+def q5k_repack(native, rows, inner, stream=None):
+    """GgufPlanes.repack for Q5_K on the device: native uint8 blocks -> Q5KWeight."""
+    groups = inner // 32
+    dev = native.device
+    p0 = torch.empty(rows * groups * 16, dtype=torch.uint8, device=dev)
+    p1 = torch.empty(rows * groups * 4, dtype=torch.uint8, device=dev)
+    meta = torch.empty(rows * (inner // 256) * 16, dtype=torch.uint8, device=dev)
+    _require(native, rows * (inner // 256) * 176, "native")
+    _lib.check(_lib.lib().splosh_q5k_repack(_ptr(native), rows, inner, _ptr(p0), _ptr(p1), _ptr(meta),
+                                            _stream(stream)))
+    return Q5KWeight(p0, p1, meta, rows, inner)
+
+
+def q5k_unpack(w, stream=None):
+    native = torch.empty(w.rows * (w.inner // 256) * 176, dtype=torch.uint8, device=w.plane0.device)
+    _lib.check(_lib.lib().splosh_q5k_unpack(_ptr(w.plane0), _ptr(w.plane1), _ptr(w.meta), w.rows, w.inner,
+                                            _ptr(native), _stream(stream)))
+    return native
+
+
+class Q4GemmRuntime:
+    """Q4GemmRuntime (Runtime/Q4Runtime.swift:29-157): the oracle-grade gemm_q4 submission API."""
+
+    def dispatch(self, shape: GemmQ4Shape, layout: Q4BufferLayout, a, packed, scales, biases, output, stream=None):
+        """Validate, encode gemm_q4 (one thread per output), and wait (Q4Runtime.swift:94-145)."""
+        shape.validate(layout)
+        _require(a, shape.rows * shape.inner * 2, "a")
+        _require(packed, layout.packed_word_count * 4, "packed")
+        _require(scales, layout.sidecar_count * 2, "scales")
+        _require(biases, layout.sidecar_count * 2, "biases")
+        _require(output, shape.rows * shape.columns * 4, "output")
+        st = _lib.lib().splosh_gemm_q4(_ptr(a), _ptr(packed), _ptr(scales), _ptr(biases), _ptr(output), shape.rows,
+                                       shape.columns, shape.inner, ctypes.byref(layout.c), _stream(stream))
+        _lib.check(st)
+        (stream or torch.cuda.current_stream()).synchronize()
+
+
+class Engine:
+    """The GEMM entry points of the reference's Engine (Runtime/Engine.swift:1652, :1911), stream
+    ordered; `kernel` replaces the reference's SPLOSH_* kernel-selection environment variables."""
+
+    def __init__(self, kernel=AUTO, stream=None):
+        self.kernel = kernel
+        self.stream = stream
+
+    def gemm(self, w, input, output, residual=False, rows=None):
+        return gemm(w, input, out=output, residual=output if residual else None, kernel=self.kernel, rows=rows,
+                    stream=self.stream)
+
+    def mlp_in(self, gate, up, input, output, rows=None):
+        return mlp_in(gate, up, input, out=output, kernel=self.kernel, rows=rows, stream=self.stream)
+
+
+def version():
+    return _lib.lib().splosh_version().decode()

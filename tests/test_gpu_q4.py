@@ -1,0 +1,182 @@
+"""q4 (MLX affine, group 64) on the GPU against the CPU oracle.
+
+Dequantization and retiling are bit-exact; GEMMs are held to the path's tolerance and the
+streaming kernel to one bf16 rounding of the fp32-accumulate reference (qcheck.check_close)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from qcheck import Q4Case, bf16_tensor, check_close, dev_u16, dev_u32, to_f32
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def rt():
+    from splosh_amd import runtime
+    return runtime
+
+
+def test_q4_dequant_bit_exact(rt):
+    case = Q4Case(256, 320, seed=1)
+    got = rt.dequant(case.w_rm).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), case.dense.view(np.uint32))
+    case = Q4Case(256, 512, seed=2)
+    got = rt.dequant(case.w_tiled).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), case.dense.view(np.uint32))
+
+
+def test_tile128_matches_converter(rt):
+    rows, groups = 384, 5
+    src = np.random.default_rng(3).integers(0, 2**32, size=rows * groups * 8, dtype=np.uint64).astype(np.uint32)
+    want = oracle.tile128(src.view(np.uint8), rows, groups, 32).view(np.uint32)
+    got = rt.tile128(dev_u32(src), rows, groups, 32).cpu().numpy().view(np.uint32)
+    assert np.array_equal(got, want)
+    back = rt.tile128(dev_u32(want), rows, groups, 32, inverse=True).cpu().numpy().view(np.uint32)
+    assert np.array_equal(back, src)
+    s16 = np.arange(rows * groups, dtype=np.uint16)
+    assert np.array_equal(rt.tile128(dev_u16(s16), rows, groups, 2).cpu().numpy().view(np.uint16),
+                          oracle.tile128(s16.view(np.uint8), rows, groups, 2).view(np.uint16))
+
+
+def test_device_retile_of_a_weight(rt):
+    case = Q4Case(256, 512, seed=4)
+    tiled = rt.q4_to_tiled(case.w_rm)
+    ref = case.w_tiled
+    for name in ("packed", "scales", "biases"):
+        assert torch.equal(getattr(tiled, name).view(-1)[: getattr(ref, name).numel()], getattr(ref, name).view(-1))
+
+
+@pytest.mark.parametrize("rows,columns,inner", [(2, 3, 65), (3, 2, 128), (1, 1, 64)])
+def test_gemm_q4_named_cases(rt, rows, columns, inner):
+    """GemmOracleTests.swift:160-214 through Q4GemmRuntime.dispatch (fp32 out)."""
+    from test_oracle import named_q4_case
+    from splosh_amd.quant import GemmQ4Shape, Q4BufferLayout
+    words, stride, sc, bi, a = named_q4_case(oracle, rows, columns, inner)
+    layout = Q4BufferLayout(rows=columns, logical_k=inner)
+    out = torch.full((rows, columns), float("nan"), device="cuda")
+    rt.Q4GemmRuntime().dispatch(GemmQ4Shape(rows, columns, inner), layout, bf16_tensor(a), dev_u32(words),
+                                dev_u16(sc), dev_u16(bi), out)
+    w = oracle.q4_dequant_rowmajor(words, stride, sc, bi, columns, inner)
+    ref = oracle.gemm_a_bf16_w_f32(a, w)
+    assert np.allclose(out.cpu().numpy(), ref, rtol=1e-5, atol=1e-5)
+
+
+def test_gemm_q4_runtime_rejects_small_buffers(rt):
+    from splosh_amd.quant import GemmQ4Shape, Q4BufferLayout
+    layout = Q4BufferLayout(rows=3, logical_k=65)
+    small = torch.zeros(4, dtype=torch.int32, device="cuda")
+    with pytest.raises(rt.GemmQ4Error) as e:
+        rt.Q4GemmRuntime().dispatch(GemmQ4Shape(2, 3, 65), layout, torch.zeros(130, dtype=torch.int16, device="cuda"),
+                                    small, torch.zeros(6, dtype=torch.int16, device="cuda"),
+                                    torch.zeros(6, dtype=torch.int16, device="cuda"),
+                                    torch.zeros(6, device="cuda"))
+    assert e.value.case == "bufferTooSmall"
+
+
+ROWS = [1, 2, 3, 4, 5, 8, 16, 17, 31, 33, 64, 65, 100]
+
+
+@pytest.mark.parametrize("order", ["tiled", "rowmajor"])
+@pytest.mark.parametrize("rows", ROWS)
+def test_stream_gemm_rows(rt, order, rows):
+    case = Q4Case(384, 768, seed=10 + rows)
+    w = case.w_tiled if order == "tiled" else case.w_rm
+    a_bits = oracle.bf16_normal((rows, case.k), seed=100 + rows)
+    ref = oracle.gemm_a_bf16_w_f32(a_bits, case.dense)
+    for out_dtype in (torch.bfloat16, torch.float32):
+        got = rt.gemm(w, bf16_tensor(a_bits), out_dtype=out_dtype, kernel=rt.STREAM)
+        check_close(to_f32(got), ref, bf16_out=out_dtype == torch.bfloat16, tight=True,
+                    label=f"{order} rows={rows} {out_dtype}")
+
+
+def test_stream_gemm_odd_columns_and_strides(rt):
+    """Row-major weight with N not a multiple of 16, padded activation rows, output written into a
+    wider buffer whose other columns and rows must stay untouched."""
+    n, k, rows = 200, 448, 7
+    case = Q4Case(n, k, seed=21)
+    a_full = oracle.bf16_normal((rows, k + 64), seed=22)
+    ref = oracle.gemm_a_bf16_w_f32(np.ascontiguousarray(a_full[:, :k]), case.dense)
+    a = bf16_tensor(a_full)
+    out = torch.full((rows + 2, n + 40), 7.0, dtype=torch.float32, device="cuda")
+    rt.gemm(case.w_rm, a, out=out[:, :], rows=rows, kernel=rt.STREAM)
+    o = out.cpu().numpy()
+    check_close(o[:rows, :n], ref, bf16_out=False, tight=True)
+    assert np.all(o[:rows, n:] == 7.0) and np.all(o[rows:] == 7.0)
+
+
+def test_residual_in_place(rt):
+    case = Q4Case(256, 512, seed=23)
+    rows = 5
+    a_bits = oracle.bf16_normal((rows, case.k), seed=24)
+    base = np.random.default_rng(25).normal(size=(rows, case.n)).astype(np.float32)
+    ref = oracle.gemm_a_bf16_w_f32(a_bits, case.dense) + base
+    out = torch.from_numpy(base.copy()).cuda()
+    rt.Engine(kernel=rt.STREAM).gemm(case.w_tiled, bf16_tensor(a_bits), out, residual=True)
+    check_close(out.cpu().numpy(), ref, bf16_out=False, tight=True)
+
+
+def test_scalar_kernel_any_shape(rt):
+    """K not a multiple of 64 goes to the generic kernel under AUTO."""
+    case = Q4Case(96, 200, seed=26)
+    a_bits = oracle.bf16_normal((3, case.k), seed=27)
+    ref = oracle.gemm_a_bf16_w_f32(a_bits, case.dense)
+    got = rt.gemm(case.w_rm, bf16_tensor(a_bits), out_dtype=torch.float32)
+    assert np.allclose(got.cpu().numpy(), ref, rtol=1e-5, atol=1e-5)
+    with pytest.raises(rt.SploshError) as e:
+        rt.gemm(case.w_rm, bf16_tensor(a_bits), kernel=rt.STREAM)
+    assert e.value.case == "unsupported"
+
+
+@pytest.mark.parametrize("rows", [1, 2, 8, 64])
+def test_mlp_in_fused(rt, rows):
+    k, n = 512, 384
+    gate, up = Q4Case(n, k, seed=30), Q4Case(n, k, seed=31)
+    a_bits = oracle.bf16_normal((rows, k), seed=32)
+    g = oracle.gemm_a_bf16_w_f32(a_bits, gate.dense)
+    u = oracle.gemm_a_bf16_w_f32(a_bits, up.dense)
+    ref = oracle.silu_mul(g, u)
+    for w_g, w_u in ((gate.w_tiled, up.w_tiled), (gate.w_rm, up.w_rm)):
+        got = rt.mlp_in(w_g, w_u, bf16_tensor(a_bits), out_dtype=torch.float32)
+        check_close(got.cpu().numpy(), ref, bf16_out=False, label=f"mlp rows={rows}")
+        got = rt.mlp_in(w_g, w_u, bf16_tensor(a_bits))
+        check_close(to_f32(got), ref, bf16_out=True, label=f"mlp bf16 rows={rows}")
+
+
+def _full_size_weight(rt, n, k, seed):
+    """A BASELINE-size tiled q4 weight generated on the device (uniform code words,
+    scale = bf16(|N(0, 0.02)|), bias = bf16(N(0, 0.01)))."""
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    groups = k // 64
+    packed = torch.randint(-2**31, 2**31, (n * groups * 8,), dtype=torch.int64, device="cuda", generator=gen).to(torch.int32)
+    scales = (torch.randn(n * groups, device="cuda", generator=gen) * 0.02).abs().to(torch.bfloat16).view(torch.int16)
+    biases = (torch.randn(n * groups, device="cuda", generator=gen) * 0.01).to(torch.bfloat16).view(torch.int16)
+    return rt.Q4Weight(packed, scales, biases, n, k, rt.TILED128)
+
+
+def _sampled_reference(w, a_bits, cols):
+    """The oracle on a sample of output columns of a device tiled weight (untiled on the host)."""
+    n, k = w.rows, w.inner
+    g = k // 64
+    tw = w.packed.cpu().numpy().view(np.uint32)
+    ts = w.scales.cpu().numpy().view(np.uint16)
+    tb = w.biases.cpu().numpy().view(np.uint16)
+    words = oracle.untile128(tw.view(np.uint8), n, g, 32).view(np.uint32).reshape(n, k // 8)
+    sc = oracle.untile128(ts.view(np.uint8), n, g, 2).view(np.uint16).reshape(n, g)
+    bi = oracle.untile128(tb.view(np.uint8), n, g, 2).view(np.uint16).reshape(n, g)
+    dense = oracle.q4_dequant_rowmajor(words[cols], k // 8, sc[cols], bi[cols], len(cols), k)
+    return oracle.gemm_a_bf16_w_f32(a_bits, dense)
+
+
+@pytest.mark.parametrize("rows", [1, 64])
+def test_baseline_shapes_sampled(rt, rows):
+    """Config 0/1 shapes (K=5120 -> N=17408, K=17408 -> N=5120) at full size, 512 sampled output
+    columns checked against the oracle."""
+    for n, k in ((17408, 5120), (5120, 17408)):
+        w = _full_size_weight(rt, n, k, seed=n + k + rows)
+        a_bits = oracle.bf16_normal((rows, k), seed=rows)
+        got = rt.gemm(w, bf16_tensor(a_bits))
+        cols = np.sort(np.random.default_rng(rows).choice(n, 512, replace=False))
+        ref = _sampled_reference(w, a_bits, cols)
+        check_close(to_f32(got)[:, cols], ref, bf16_out=True, tight=True, label=f"{n}x{k} rows={rows}")

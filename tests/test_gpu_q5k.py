@@ -1,0 +1,93 @@
+"""GGUF Q5_K on the GPU against the CPU oracle: plane repack/unpack and decode bit-exact, GEMM to
+the path's tolerance. Weights follow the reference's kernel-test generator
+(GgufKernelTests.swift:49-82)."""
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from qcheck import bf16_tensor, check_close, dev_u8, to_f32
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden" / "gguf_golden_blocks.json"
+
+
+@pytest.fixture(scope="module")
+def rt():
+    from splosh_amd import runtime
+    return runtime
+
+
+def test_repack_matches_oracle_and_unpacks(rt):
+    n, k = 256, 1024
+    native = oracle.q45k_random_native(n, k, seed=1)
+    w = rt.q5k_repack(dev_u8(native), n, k)
+    p0, p1, meta = oracle.q45k_repack(native, n, k)
+    assert np.array_equal(w.plane0.cpu().numpy(), p0)
+    assert np.array_equal(w.plane1.cpu().numpy(), p1)
+    assert np.array_equal(w.meta.cpu().numpy(), meta)
+    assert np.array_equal(rt.q5k_unpack(w).cpu().numpy(), native)
+
+
+def test_dequant_bit_exact_including_golden_block(rt):
+    n, k = 128, 512
+    native = oracle.q45k_random_native(n, k, seed=2).reshape(n, -1)
+    # Put the real golden block (GgufGoldenBlocks.swift:73-122) at row 5, block 1.
+    golden = json.loads(GOLDEN.read_text())["q5K"]
+    native[5, 176:352] = np.array(golden["bytes"], np.uint8)
+    native = native.reshape(-1)
+    w = rt.q5k_repack(dev_u8(native), n, k)
+    got = rt.dequant(w).cpu().numpy()
+    want = oracle.q45k_decode(native).reshape(n, k)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    values = np.array([np.float32(v) for v in golden["values"]], np.float32)
+    assert np.array_equal(got[5, 256:512].view(np.uint32), values.view(np.uint32))
+
+
+@pytest.mark.parametrize("rows", [1, 2, 3, 16, 17, 64, 100])
+def test_stream_gemm(rt, rows):
+    n, k = 256, 1280
+    native = oracle.q45k_random_native_splitmix(n, k, seed=0x6600 + 13) if rows == 16 else \
+        oracle.q45k_random_native(n, k, seed=rows)
+    w = rt.q5k_repack(dev_u8(native), n, k)
+    dense = oracle.q45k_decode(native).reshape(n, k)
+    a_bits = oracle.bf16_normal((rows, k), seed=50 + rows)
+    ref = oracle.gemm_a_bf16_w_f32(a_bits, dense)
+    for out_dtype in (torch.bfloat16, torch.float32):
+        got = rt.gemm(w, bf16_tensor(a_bits), out_dtype=out_dtype, kernel=rt.STREAM)
+        check_close(to_f32(got), ref, bf16_out=out_dtype == torch.bfloat16, tight=True,
+                    label=f"q5k rows={rows} {out_dtype}")
+    got = rt.gemm(w, bf16_tensor(a_bits), out_dtype=torch.float32, kernel=rt.SCALAR)
+    check_close(got.cpu().numpy(), ref, bf16_out=False, tight=True, label=f"q5k scalar rows={rows}")
+
+
+def test_residual(rt):
+    n, k, rows = 128, 512, 3
+    native = oracle.q45k_random_native(n, k, seed=9)
+    w = rt.q5k_repack(dev_u8(native), n, k)
+    a_bits = oracle.bf16_normal((rows, k), seed=10)
+    base = np.random.default_rng(11).normal(size=(rows, n)).astype(np.float32)
+    ref = oracle.gemm_a_bf16_w_f32(a_bits, oracle.q45k_decode(native).reshape(n, k)) + base
+    out = torch.from_numpy(base.copy()).cuda()
+    rt.gemm(w, bf16_tensor(a_bits), out=out, residual=out)
+    check_close(out.cpu().numpy(), ref, bf16_out=False, tight=True)
+
+
+@pytest.mark.parametrize("rows", [1, 16, 64])
+def test_baseline_shape_sampled(rt, rows):
+    """Config 3: Q5_K down projection K=17408 -> N=5120 at full size, 256 sampled columns."""
+    n, k = 5120, 17408
+    native = oracle.q45k_random_native(n, k, seed=77)
+    w = rt.q5k_repack(dev_u8(native), n, k)
+    a_bits = oracle.bf16_normal((rows, k), seed=rows)
+    got = to_f32(rt.gemm(w, bf16_tensor(a_bits)))
+    cols = np.sort(np.random.default_rng(rows).choice(n, 256, replace=False))
+    blk = k // 256 * 176
+    sub = native.reshape(n, blk)[cols].reshape(-1)
+    dense = oracle.q45k_decode(sub).reshape(len(cols), k)
+    ref = oracle.gemm_a_bf16_w_f32(a_bits, dense)
+    check_close(got[:, cols], ref, bf16_out=True, tight=True, label=f"q5k full rows={rows}")

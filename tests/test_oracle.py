@@ -1,0 +1,245 @@
+"""The CPU oracle pinned against the reference's own known answers and against mathematics.
+
+Each check is chosen so that a plausible slip in the restatement (a dropped term, a wrong shift,
+a swapped operand) fails it: closed forms from the reference's tests, the real GGUF golden
+blocks, fp64 brute force, and structural invariants.
+"""
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+GOLDEN = Path(__file__).resolve().parent / "golden" / "gguf_golden_blocks.json"
+
+
+def f32(x):
+    return np.float32(x)
+
+
+# ---- bf16 helpers (Q4BufferLayout.swift:123-129) ---------------------------------------------
+
+def test_bf16_roundings(oracle):
+    assert oracle.f32_to_bf16_halfup(1.0) == 0x3F80
+    # 1 + 2^-8 is exactly half an ulp of bf16: half-up goes away from zero, RNE to even.
+    half = np.float32(1.0 + 2.0 ** -8)
+    assert oracle.f32_to_bf16_halfup(half) == 0x3F81
+    assert int(oracle.f32_to_bf16_rne(np.array([half]))[0]) == 0x3F80
+    assert int(oracle.f32_to_bf16_rne(np.array([np.float32(1.0 + 3 * 2.0 ** -8)]))[0]) == 0x3F82
+    assert oracle.bf16_to_f32(np.array([0xC000], np.uint16))[0] == -2.0
+
+
+# ---- MLX affine q4 --------------------------------------------------------------------------
+
+def _bf16(x):
+    import oracle
+    return oracle.f32_to_bf16_halfup(x)
+
+
+def test_mlx_affine_group64_closed_form(oracle):
+    """QuantDequantOracleTests.swift:31-48: a 65-column row, scales [2, 3], biases [-1, 10]."""
+    columns = 65
+    words = np.zeros(32, np.uint32)  # 128-byte padded row
+    for c in range(columns):
+        words[c // 8] |= np.uint32((c % 16) << ((c % 8) * 4))
+    scales = np.array([_bf16(2), _bf16(3)], np.uint16)
+    biases = np.array([_bf16(-1), _bf16(10)], np.uint16)
+    got = oracle.q4_dequant_rowmajor(words, 32, scales, biases, 1, columns)[0]
+    expected = np.array([(2 if c < 64 else 3) * (c % 16) + (-1 if c < 64 else 10) for c in range(columns)],
+                        np.float32)
+    assert np.array_equal(got, expected)
+
+
+def test_q4_buffer_layout_padded_rows(oracle):
+    """Q4BufferLayoutTests.swift:7-27: K=65 -> 9 words, stride 128 B (23 padding words);
+    decode(0,0)=0, decode(0,64)=-1, decode(1,64)=2."""
+    rows, K = 2, 65
+    stride = 32
+    words = np.zeros(rows * stride, np.uint32)
+    for r in range(rows):
+        for k in range(K):
+            words[r * stride + k // 8] |= np.uint32(((k + r) & 15) << (4 * (k % 8)))
+    sidecars = rows * 2
+    scales = np.array([_bf16(2 + i) for i in range(sidecars)], np.uint16)
+    biases = np.array([_bf16(-i) for i in range(sidecars)], np.uint16)
+    w = oracle.q4_dequant_rowmajor(words, stride, scales, biases, rows, K)
+    assert w[0, 0] == 0 and w[0, 64] == -1 and w[1, 64] == 2
+    from splosh_amd.quant import Q4BufferLayout
+    layout = Q4BufferLayout(rows=2, logical_k=65)
+    assert (layout.packed_words_per_row, layout.row_stride_bytes, layout.padding_words_per_row) == (9, 128, 23)
+
+
+def test_tile_roundtrip_and_addressing(oracle):
+    rows, groups, eb = 256, 3, 32
+    src = np.arange(rows * groups * eb, dtype=np.uint32).astype(np.uint8)
+    t = oracle.tile128(src, rows, groups, eb)
+    assert np.array_equal(oracle.untile128(t, rows, groups, eb), src)
+    # Record (row 130, group 2) lands at ((1 * groups + 2) * 128 + 2) (Retile.swift:142-147).
+    row, g = 130, 2
+    dst_rec = (1 * groups + 2) * 128 + 2
+    assert np.array_equal(t[dst_rec * eb:(dst_rec + 1) * eb], src[(row * groups + g) * eb:(row * groups + g + 1) * eb])
+
+
+def test_tiled_dequant_matches_rowmajor(oracle):
+    N, K = 256, 192
+    words, stride, scales, biases = oracle.q4_random_weight(N, K, seed=7)
+    ref = oracle.q4_dequant_rowmajor(words, stride, scales, biases, N, K)
+    groups = K // 64
+    tw = oracle.tile128(words[:, :K // 8].reshape(-1).view(np.uint8), N, groups, 32).view(np.uint32)
+    ts = oracle.tile128(scales.reshape(-1).view(np.uint8), N, groups, 2).view(np.uint16)
+    tb = oracle.tile128(biases.reshape(-1).view(np.uint8), N, groups, 2).view(np.uint16)
+    assert np.array_equal(oracle.q4_dequant_tiled(tw, ts, tb, N, K), ref)
+
+
+def test_dequant_against_float64(oracle):
+    """s*q is exact in fp32 (8-bit mantissa times a 4-bit integer), so s*q+b rounded once equals
+    the fp64 value rounded to fp32."""
+    N, K = 64, 320
+    words, stride, scales, biases = oracle.q4_random_weight(N, K, seed=11)
+    got = oracle.q4_dequant_rowmajor(words, stride, scales, biases, N, K)
+    k = np.arange(K)
+    q = (words[:, k // 8] >> (4 * (k % 8)).astype(np.uint32)) & 15
+    s = oracle.bf16_to_f32(scales).astype(np.float64)[:, k // 64]
+    b = oracle.bf16_to_f32(biases).astype(np.float64)[:, k // 64]
+    assert np.array_equal(got, (s * q + b).astype(np.float32))
+
+
+# ---- GEMM -----------------------------------------------------------------------------------
+
+def test_gemm_bf16_known_answer(oracle):
+    """GemmOracleTests.swift:27-28,76-84: [-8, -4.5, 7, 39]."""
+    a = np.array([0x3f80, 0xc000, 0x4040, 0x3e80, 0x4120, 0xbf00], np.uint16)
+    b = np.array([0x4000, 0xbf80, 0x3f00, 0x4080, 0xc040, 0x3fc0], np.uint16)
+    assert oracle.gemm_bf16(a, b, 2, 2, 3).reshape(-1).tolist() == [-8.0, -4.5, 7.0, 39.0]
+
+
+def named_q4_case(oracle, rows, columns, inner):
+    """The inputs of GemmOracleTests.swift:165-191 (codes (n + 3k) & 15, scales 0.25 + 0.125 i,
+    biases -0.5 + 0.25 i, A ((i % 11) - 5) * 0.125)."""
+    stride = ((inner + 7) // 8 * 4 + 127) // 128 * 32
+    groups = (inner + 63) // 64
+    words = np.zeros(columns * stride, np.uint32)
+    for n in range(columns):
+        for k in range(inner):
+            words[n * stride + k // 8] |= np.uint32(((n + 3 * k) & 15) << (4 * (k % 8)))
+    sc = np.array([_bf16(0.25 + i * 0.125) for i in range(columns * groups)], np.uint16)
+    bi = np.array([_bf16(-0.5 + i * 0.25) for i in range(columns * groups)], np.uint16)
+    a = np.array([_bf16(((i % 11) - 5) * 0.125) for i in range(rows * inner)], np.uint16).reshape(rows, inner)
+    return words, stride, sc, bi, a
+
+
+@pytest.mark.parametrize("rows,columns,inner", [(2, 3, 65), (3, 2, 128), (1, 1, 64)])
+def test_named_q4_cases_against_float64(oracle, rows, columns, inner):
+    words, stride, sc, bi, a = named_q4_case(oracle, rows, columns, inner)
+    w = oracle.q4_dequant_rowmajor(words, stride, sc, bi, columns, inner)
+    got = oracle.gemm_a_bf16_w_f32(a, w)
+    exact = oracle.bf16_to_f32(a).astype(np.float64) @ w.astype(np.float64).T
+    assert np.allclose(got, exact, rtol=1e-6, atol=1e-6)
+    fused = oracle.q4_gemm_rowmajor(a, words, stride, sc, bi, columns, inner)
+    assert np.array_equal(fused, got)
+
+
+def test_per_group_identity(oracle):
+    """sum_k a (s q + b) = s sum(a q) + b sum(a) per 64-group (MlpFusedTests.swift:200-212)."""
+    M, N, K = 3, 8, 256
+    words, stride, sc, bi = oracle.q4_random_weight(N, K, seed=3)
+    a = oracle.bf16_normal((M, K), seed=4)
+    got = oracle.gemm_a_bf16_w_f32(a, oracle.q4_dequant_rowmajor(words, stride, sc, bi, N, K)).astype(np.float64)
+    k = np.arange(K)
+    q = ((words[:, k // 8] >> (4 * (k % 8)).astype(np.uint32)) & 15).astype(np.float64)
+    af = oracle.bf16_to_f32(a).astype(np.float64)
+    s = oracle.bf16_to_f32(sc).astype(np.float64)
+    b = oracle.bf16_to_f32(bi).astype(np.float64)
+    ident = np.zeros((M, N))
+    for g in range(K // 64):
+        sl = slice(64 * g, 64 * g + 64)
+        ident += s[:, g] * (af[:, sl] @ q[:, sl].T) + b[:, g] * af[:, sl].sum(1, keepdims=True)
+    assert np.allclose(got, ident, rtol=1e-5, atol=1e-4)
+
+
+def test_silu_mul(oracle):
+    g = np.array([-3.0, -0.5, 0.0, 0.5, 2.0, 20.0], np.float32)
+    u = np.array([1.0, 2.0, 3.0, -1.0, 0.25, 1.0], np.float32)
+    ref = (g.astype(np.float64) / (1 + np.exp(-g.astype(np.float64)))) * u
+    assert np.allclose(oracle.silu_mul(g, u), ref, rtol=2e-7, atol=0)
+
+
+# ---- GGUF -----------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("name,fifth", [("q5K", True), ("q4K", False)])
+def test_gguf_golden_blocks(oracle, name, fifth):
+    """GgufTests.swift:237-247 over GgufGoldenBlocks (real blocks of Qwen3.8-27B): bit-exact."""
+    block = json.loads(GOLDEN.read_text())[name]
+    expected = np.array([np.float32(v) for v in block["values"]], np.float32)
+    got = oracle.q45k_decode(np.array(block["bytes"], np.uint8), fifth_bit=fifth)
+    assert np.array_equal(got.view(np.uint32), expected.view(np.uint32))
+
+
+def test_q4k_group_layout_contract(oracle):
+    """The inputs of QuantDequantOracleTests.swift:17-29 (d = 1, dmin = 0, 6-bit scales 1 for
+    groups 0..3, code bytes 0x10) decoded with GgufQuant's layout (group 2h = low nibbles of run h,
+    2h+1 = high nibbles): groups 0 and 2 are 0, 1 and 3 are 1, 4..7 have scale 0.
+    DequantOracle.q4_K reads elements 16..31 from the other nibble; llama.cpp and GgufQuant do not."""
+    block = np.array([0x00, 0x3c, 0x00, 0x00] + [1] * 8 + [0] * 4 + [0x10] * 128, np.uint8)
+    v = oracle.q45k_decode(block, fifth_bit=False)
+    assert v[0] == 0 and v[1] == 0 and v[32] == 1
+    expected = np.repeat(np.array([0, 1, 0, 1, 0, 0, 0, 0], np.float32), 32)
+    assert np.array_equal(v, expected)
+
+
+def test_q5k_fifth_bit_and_high_scales(oracle):
+    """Hand-built Q5_K block: d = 1, dmin = 0.5 (fp16 0x3800). Group 5 takes scale
+    (packed[9] & 15) | (packed[1] >> 6) << 4 and min (packed[9] >> 4) | (packed[5] >> 6) << 4
+    (GgufQuant.swift:200-202); element 3 of group 5 has its fifth bit set."""
+    b = np.zeros(176, np.uint8)
+    b[0:2] = [0x00, 0x3c]
+    b[2:4] = [0x00, 0x38]
+    b[4 + 1] = 0b10_000000   # top bits of scale 5 = 2 -> scale 5 = 2 << 4 | low
+    b[4 + 5] = 0b01_000000   # top bits of min 5 = 1
+    b[4 + 9] = 0x3_5         # low nibble 5 of scale 5, high nibble 3 of min 5
+    b[16 + 3] = 1 << 5       # fifth bit of element 3 of group 5
+    b[48 + 32 * 2 + 3] = 0x70  # group 5 = high nibble of run 2: code 7
+    v = oracle.q45k_decode(b, fifth_bit=True)
+    scale = (2 << 4) | 5
+    minimum = (1 << 4) | 3
+    assert v[32 * 5 + 3] == np.float32((7 + 16) * scale - 0.5 * minimum)
+    assert v[32 * 5 + 0] == np.float32(-0.5 * minimum)
+
+
+def test_gguf_slot_matches_chunk_order(oracle):
+    """gguf_formats.h:17-21: chunk c holds elements 4c..4c+3 and 16+4c..16+4c+3 as four pairs,
+    pair p's first element e0 = 16 (p >> 1) + 4c + 2 (p & 1), element e at slot 8c + 2p + (e & 1)."""
+    expected = {}
+    for c in range(4):
+        for p in range(4):
+            e0 = 16 * (p >> 1) + 4 * c + 2 * (p & 1)
+            for e in (e0, e0 + 1):
+                expected[e] = 8 * c + 2 * p + (e & 1)
+    assert sorted(expected) == list(range(32))
+    assert [oracle.gguf_slot(e) for e in range(32)] == [expected[e] for e in range(32)]
+
+
+def test_q5k_planes_roundtrip_and_bit_positions(oracle):
+    N, K = 128, 512
+    native = oracle.q45k_random_native(N, K, seed=5)
+    p0, p1, meta = oracle.q45k_repack(native, N, K)
+    assert (p0.size, p1.size, meta.size) == oracle.q45k_plane_sizes(N, K)
+    assert p0.size + p1.size + meta.size == native.size
+    assert np.array_equal(oracle.q45k_unpack(p0, p1, meta, N, K), native)
+    # A single set code bit: element 5 of group 1 of row 3 (high nibble of run 0, code 0xF).
+    nat = np.zeros_like(native)
+    nat[3 * (K // 256) * 176 + 48 + 5] = 0xF0
+    q0, q1, qm = oracle.q45k_repack(nat, N, K)
+    # slot(5) = 9: word 1, pair index 1 -> bits 16..19; record (row 3, group 1) = 1 * 128 + 3.
+    rec = (0 * (K // 32) + 1) * 128 + 3
+    word = q0[rec * 16 + 4: rec * 16 + 8].view(np.uint32)[0]
+    assert word == 0xF << 16
+    assert np.count_nonzero(q0) == 1 and np.count_nonzero(q1) == 0
+
+
+def test_q5k_splitmix_generator_matches_reference_shape(oracle):
+    nat = oracle.q45k_random_native_splitmix(128, 256, seed=0x6600 + 13)
+    d = nat.reshape(-1, 176)[:, 0:2].copy().view(np.float16).astype(np.float32).reshape(-1)
+    assert np.all((np.abs(d) >= 0.75e-4 * 0.999) & (np.abs(d) <= 1.25e-4 * 1.001))
+    vals = oracle.q45k_decode(nat)
+    assert np.all(np.isfinite(vals))
