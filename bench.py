@@ -1,0 +1,243 @@
+"""Benchmark of the quantized-matmul hot path on one MI355X.
+
+Default workload (the draft-verify step the metric is quoted on): M = 64
+activation rows (8 sessions x 8 drafted tokens), 4-bit g64 affine weights, the fused gate+up
+projection (two K=5120 -> N=17408 weights sharing one activation read, out = silu(g) * u) followed
+by the down projection (K=17408 -> N=5120) on that output. One "step" is that pair of launches.
+
+    python bench.py [--steps K] [--warmup W] [--workload verify64|decode1|q5k|prefill2048|layerset]
+
+Inputs are synthetic (seeded, on the device): code words uniform random, scale = bf16(|N(0,0.02)|),
+bias = bf16(N(0,0.01)), activations bf16(N(0,1)). Several copies of the weight set are rotated so
+that the working set (>= 1.5 GB) is far larger than the 256 MB Infinity Cache and every step
+streams its weights from HBM. `value` is algorithmic bytes per step / step time (TB/s, effective):
+each operand counted once, weights N K / 2 + N (K / 64) * 4 bytes.
+
+Prints ONE JSON line. --gpus N > 1 is refused: the path is measured on one GPU.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
+
+# HBM bytes per launch of the dominant kernel measured with rocprofv3 --pmc (FETCH_SIZE and
+# WRITE_SIZE, scaled by a plain copy kernel), keyed by workload; None until measured.
+MEASURED_TRAFFIC = {}
+
+
+def q4_bytes(n, k):
+    return n * k // 2 + n * (k // 64) * 4
+
+
+def make_q4(rt, n, k, gen):
+    import torch
+    groups = k // 64
+    packed = torch.randint(-2**31, 2**31, (n * groups * 8,), dtype=torch.int64, device="cuda",
+                           generator=gen).to(torch.int32)
+    scales = (torch.randn(n * groups, device="cuda", generator=gen) * 0.02).abs().to(torch.bfloat16).view(torch.int16)
+    biases = (torch.randn(n * groups, device="cuda", generator=gen) * 0.01).to(torch.bfloat16).view(torch.int16)
+    return rt.Q4Weight(packed, scales, biases, n, k, rt.TILED128)
+
+
+def make_q5k(rt, n, k, gen):
+    """Q5_K planes with every bit random except the fp16 d / dmin fields, drawn like the reference's
+    kernel test (GgufKernelTests.swift:49-82): d ~ 1e-4 (1 +- 0.25), dmin ~ 1.5e-3, 1 in 4 negative."""
+    import torch
+    blocks = n * (k // 256)
+    native = torch.randint(0, 256, (blocks, 176), dtype=torch.uint8, device="cuda", generator=gen)
+    for field, mag in ((0, 1e-4), (2, 1.5e-3)):
+        v = mag * (1 + 0.25 * (torch.rand(blocks, device="cuda", generator=gen) * 2 - 1))
+        neg = torch.randint(0, 4, (blocks,), device="cuda", generator=gen) == 0
+        v = torch.where(neg, -v, v).to(torch.float16).view(torch.uint8).view(blocks, 2)
+        native[:, field:field + 2] = v
+    w = rt.q5k_repack(native.view(-1), n, k)
+    return w, native
+
+
+def copies_for(bytes_per_set, minimum=1.5e9, cap=16):
+    return max(2, min(cap, int(-(-minimum // bytes_per_set))))
+
+
+class Timer:
+    """HIP events on the stream the library launches on (torch's current stream)."""
+
+    def __init__(self):
+        import torch
+        self.torch = torch
+
+    def event(self):
+        e = self.torch.cuda.Event(enable_timing=True)
+        e.record()
+        return e
+
+
+def build_workload(name, rt, torch, gen):
+    """Returns (steps: list of callables over copies, bytes_per_step, flops_per_step, kernels, config)."""
+    if name == "verify64":
+        m, h, inter = 64, 5120, 17408
+        one = 2 * q4_bytes(inter, h) + q4_bytes(h, inter)
+        ncopy = copies_for(one)
+        sets = [(make_q4(rt, inter, h, gen), make_q4(rt, inter, h, gen), make_q4(rt, h, inter, gen))
+                for _ in range(ncopy)]
+        x = (torch.randn(m, h, device="cuda", generator=gen)).to(torch.bfloat16)
+        act = torch.empty(m, inter, dtype=torch.bfloat16, device="cuda")
+        out = torch.empty(m, h, dtype=torch.bfloat16, device="cuda")
+        gate_up_bytes = 2 * q4_bytes(inter, h) + m * h * 2 + m * inter * 2
+        down_bytes = q4_bytes(h, inter) + m * inter * 2 + m * h * 2
+
+        def launches(i):
+            g, u, d = sets[i % ncopy]
+            return [("mlp_in", lambda: rt.mlp_in(g, u, x, out=act)),
+                    ("down", lambda: rt.gemm(d, act, out=out))]
+
+        cfg = {"workload": "draft-verify step: fused gate+up (2x K5120->N17408) + down (K17408->N5120)",
+               "rows": m, "format": "mlx affine q4 g64, tiled128", "weight_copies": ncopy}
+        return launches, gate_up_bytes + down_bytes, 2 * m * (2 * inter * h + h * inter), \
+            {"mlp_in": gate_up_bytes, "down": down_bytes}, cfg
+    if name == "decode1":
+        m, k, n = 1, 5120, 17408
+        ncopy = copies_for(q4_bytes(n, k))
+        ws = [make_q4(rt, n, k, gen) for _ in range(ncopy)]
+        x = torch.randn(m, k, device="cuda", generator=gen).to(torch.bfloat16)
+        out = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+        b = q4_bytes(n, k) + m * k * 2 + m * n * 2
+
+        def launches(i):
+            w = ws[i % ncopy]
+            return [("gemv", lambda: rt.gemm(w, x, out=out))]
+
+        cfg = {"workload": "decode GEMV K5120->N17408", "rows": 1, "format": "mlx affine q4 g64, tiled128",
+               "weight_copies": ncopy}
+        return launches, b, 2 * m * n * k, {"gemv": b}, cfg
+    if name.startswith("q5k"):
+        m = int(name[3:] or 64)
+        k, n = 17408, 5120
+        one = n * (k // 256) * 176
+        ncopy = copies_for(one)
+        ws = [make_q5k(rt, n, k, gen)[0] for _ in range(ncopy)]
+        x = torch.randn(m, k, device="cuda", generator=gen).to(torch.bfloat16)
+        out = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+        b = one + m * k * 2 + m * n * 2
+
+        def launches(i):
+            w = ws[i % ncopy]
+            return [("q5k", lambda: rt.gemm(w, x, out=out))]
+
+        cfg = {"workload": f"Q5_K down K17408->N5120", "rows": m, "format": "gguf q5_k planes",
+               "weight_copies": ncopy}
+        return launches, b, 2 * m * n * k, {"q5k": b}, cfg
+    raise SystemExit(f"unknown workload {name}")
+
+
+def cpu_baseline(workload, seconds=8.0):
+    """The CPU oracle (oracle/: dequantize each weight row to fp32, sequential fp32 dot per
+    activation row -- DequantOracle.dequantize + the fp32 GEMM loop) timed on a bounded sample of
+    output columns of the same workload and extrapolated to the whole step."""
+    import numpy as np
+    import oracle
+    threads = max(1, min(16, os.cpu_count() or 1))
+    if workload == "verify64":
+        mats = [(17408, 5120), (17408, 5120), (5120, 17408)]
+        m = 64
+    elif workload == "decode1":
+        mats = [(17408, 5120)]
+        m = 1
+    else:
+        return None
+    total_bytes = sum(q4_bytes(n, k) for n, k in mats) + 0
+    # A seeded sample weight per shape; a column's cost does not depend on its values.
+    frac = 1 / 64
+    elapsed = 0.0
+    while True:
+        t_total = 0.0
+        for idx, (n, k) in enumerate(mats):
+            cols = max(threads, int(n * frac))
+            words, stride, sc, bi = oracle.q4_random_weight(cols, k, seed=idx)
+            a = oracle.bf16_normal((m, k), seed=99)
+            t0 = time.perf_counter()
+            oracle.q4_gemm_rowmajor(a, words, stride, sc, bi, cols, k, threads=threads)
+            t_total += (time.perf_counter() - t0) * n / cols
+            elapsed += time.perf_counter() - t0
+        if elapsed >= 2.0 or frac >= 1.0:
+            break
+        frac = min(1.0, frac * max(2.0, seconds / max(elapsed, 1e-3) / 2))
+    step_bytes = total_bytes + m * 5120 * 2 * (2 if workload == "verify64" else 1)
+    return {"value": step_bytes / t_total / 1e12, "unit": "TB/s", "cores": threads, "kind": "port",
+            "sample": f"{frac * 100:.2f}% of each weight's output columns at M={m}, extrapolated to the full step",
+            "step_seconds": t_total}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="verify64")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU's share of the path; --gpus {args.gpus} is not supported "
+              "(the multi-GPU design is sharding along N, described in DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from splosh_amd import runtime as rt
+
+    gen = torch.Generator(device="cuda").manual_seed(0x5EED0001)
+    launches, step_bytes, step_flops, kernel_bytes, cfg = build_workload(args.workload, rt, torch, gen)
+    timer = Timer()
+    torch.cuda.synchronize()
+    for i in range(args.warmup):
+        for _, fn in launches(i):
+            fn()
+    torch.cuda.synchronize()
+
+    names = [nm for nm, _ in launches(0)]
+    events = []
+    start = timer.event()
+    for i in range(args.steps):
+        evs = [timer.event()]
+        for _, fn in launches(args.warmup + i):
+            fn()
+            evs.append(timer.event())
+        events.append(evs)
+    end = timer.event()
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(end)
+    ms_per_step = total_ms / args.steps
+    per_kernel = {nm: sum(evs[j].elapsed_time(evs[j + 1]) for evs in events) / args.steps
+                  for j, nm in enumerate(names)}
+
+    dominant = max(per_kernel, key=per_kernel.get)
+    dom_ms = per_kernel[dominant]
+    achieved = kernel_bytes[dominant] / (dom_ms * 1e-3) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": MEASURED_TRAFFIC.get(args.workload),
+                "kernel": dominant, "kernel_us": round(dom_ms * 1e3, 2),
+                "algorithmic_bytes": kernel_bytes[dominant]}
+    value = step_bytes / (ms_per_step * 1e-3) / 1e12
+    cpu = None if args.no_cpu else cpu_baseline(args.workload)
+    result = {
+        "metric": "quant GEMM effective HBM TB/s at M=1/64; TFLOP/s at M=2048 prefill",
+        "value": round(value, 4), "unit": "TB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16 x q4 -> fp32 acc, bf16 out", "data": "synthetic (seeded, on device)",
+        "config": cfg,
+        "kernels_us": {k: round(v * 1e3, 2) for k, v in per_kernel.items()},
+        "tflops": round(step_flops / (ms_per_step * 1e-3) / 1e12, 1),
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()
