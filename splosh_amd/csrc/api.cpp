@@ -103,6 +103,26 @@ int q4_gemm_impl(const splosh_q4_weight *w, const splosh_q4_weight *up, const ui
             if (!eligible)
                 return fail(SPLOSH_ERR_UNSUPPORTED,
                             "stream kernel needs inner % 64 == 0, lda % 8 == 0 and aligned operands");
+            const bool wide16 = aligned(w->packed, 16) && (!up || aligned(up->packed, 16)) &&
+                                (w->order == SPLOSH_Q4_TILED128 || w->row_stride_words % 4 == 0);
+            if (wide16 && splosh::lanes_fit(rows, w->rows, w->inner, w->row_stride_words, up != nullptr)) {
+                const splosh::StreamPlan plan = splosh::plan_lanes(rows, w->rows, w->inner / kGroupSize, up != nullptr);
+                return hip_status(splosh::launch_q4_lanes(plan, *w, up, a, lda, out, ldc, out_dtype, residual, rows,
+                                                          stream),
+                                  "q4 lanes launch");
+            }
+            if (wide16 && splosh::gemv_fits(rows, w->inner)) {
+                const splosh::StreamPlan plan = splosh::plan_gemv(rows, w->rows, w->inner / kGroupSize, up != nullptr);
+                return hip_status(splosh::launch_q4_gemv(plan, *w, up, a, lda, out, ldc, out_dtype, residual, rows,
+                                                         stream),
+                                  "q4 gemv launch");
+            }
+            if (rows <= 32 && wide16) {
+                const splosh::StreamPlan plan = splosh::plan_stream32(rows, w->rows, w->inner / kGroupSize, up != nullptr);
+                return hip_status(splosh::launch_q4_stream32(plan, *w, up, a, lda, out, ldc, out_dtype, residual, rows,
+                                                             stream),
+                                  "q4 stream32 launch");
+            }
             const splosh::StreamPlan plan = splosh::plan_stream(rows, w->rows, w->inner / kGroupSize, up != nullptr, 4);
             if (plan.row_chunks > 65535) return fail(SPLOSH_ERR_UNSUPPORTED, "too many rows for one launch");
             return hip_status(splosh::launch_q4_stream(plan, *w, up, a, lda, out, ldc, out_dtype, residual, rows, stream),

@@ -41,6 +41,26 @@ hipError_t launch_q4_stream(const StreamPlan &plan, const splosh_q4_weight &w, c
                             const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype,
                             const void *residual, int64_t rows, hipStream_t stream);
 
+// The 32x32x16 MFMA streaming kernel for rows <= 32 (stream32.hip).
+StreamPlan plan_stream32(int64_t rows, int64_t columns, int64_t groups, bool mlp);
+hipError_t launch_q4_stream32(const StreamPlan &plan, const splosh_q4_weight &w, const splosh_q4_weight *up,
+                              const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype,
+                              const void *residual, int64_t rows, hipStream_t stream);
+
+// The decode kernel for rows <= 8 with activations staged in LDS (gemv.hip).
+bool gemv_fits(int64_t rows, int64_t inner);
+StreamPlan plan_gemv(int64_t rows, int64_t columns, int64_t groups, bool mlp);
+hipError_t launch_q4_gemv(const StreamPlan &plan, const splosh_q4_weight &w, const splosh_q4_weight *up,
+                          const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype,
+                          const void *residual, int64_t rows, hipStream_t stream);
+
+// The lane-per-row decode kernel for one or two rows (lanes.hip).
+bool lanes_fit(int64_t rows, int64_t columns, int64_t inner, int64_t stride_words, bool mlp);
+StreamPlan plan_lanes(int64_t rows, int64_t columns, int64_t groups, bool mlp);
+hipError_t launch_q4_lanes(const StreamPlan &plan, const splosh_q4_weight &w, const splosh_q4_weight *up,
+                           const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype,
+                           const void *residual, int64_t rows, hipStream_t stream);
+
 hipError_t launch_q5k_dequant(const splosh_q5k_weight &w, float *out, hipStream_t stream);
 hipError_t launch_q5k_repack(const uint8_t *native, int64_t rows, int64_t inner, uint8_t *p0,
                              uint8_t *p1, uint8_t *meta, bool inverse, hipStream_t stream);
