@@ -79,8 +79,28 @@ class Timer:
         return e
 
 
-def build_workload(name, rt, torch, gen):
+def build_workload(name, rt, torch, gen, kernel):
     """Returns (steps: list of callables over copies, bytes_per_step, flops_per_step, kernels, config)."""
+    def workspace(rows, n, k):
+        need = rt.workspace_bytes(rows, n, k)
+        return torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
+
+    if name == "prefill2048":
+        m, k, n = 2048, 5120, 17408
+        ncopy = copies_for(q4_bytes(n, k), minimum=0.5e9)
+        ws = [make_q4(rt, n, k, gen) for _ in range(ncopy)]
+        x = torch.randn(m, k, device="cuda", generator=gen).to(torch.bfloat16)
+        out = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+        scratch = workspace(m, n, k)
+        b = q4_bytes(n, k) + m * k * 2 + m * n * 2
+
+        def launches(i):
+            w = ws[i % ncopy]
+            return [("prefill", lambda: rt.gemm(w, x, out=out, kernel=kernel, workspace=scratch))]
+
+        cfg = {"workload": "prefill GEMM M=2048 K5120->N17408", "rows": m, "format": "mlx affine q4 g64, tiled128",
+               "weight_copies": ncopy}
+        return launches, b, 2 * m * n * k, {"prefill": b}, cfg
     if name == "verify64":
         m, h, inter = 64, 5120, 17408
         one = 2 * q4_bytes(inter, h) + q4_bytes(h, inter)
@@ -88,6 +108,7 @@ def build_workload(name, rt, torch, gen):
         sets = [(make_q4(rt, inter, h, gen), make_q4(rt, inter, h, gen), make_q4(rt, h, inter, gen))
                 for _ in range(ncopy)]
         x = (torch.randn(m, h, device="cuda", generator=gen)).to(torch.bfloat16)
+        ws_in, ws_down = workspace(m, inter, h), workspace(m, h, inter)
         act = torch.empty(m, inter, dtype=torch.bfloat16, device="cuda")
         out = torch.empty(m, h, dtype=torch.bfloat16, device="cuda")
         gate_up_bytes = 2 * q4_bytes(inter, h) + m * h * 2 + m * inter * 2
@@ -95,8 +116,8 @@ def build_workload(name, rt, torch, gen):
 
         def launches(i):
             g, u, d = sets[i % ncopy]
-            return [("mlp_in", lambda: rt.mlp_in(g, u, x, out=act)),
-                    ("down", lambda: rt.gemm(d, act, out=out))]
+            return [("mlp_in", lambda: rt.mlp_in(g, u, x, out=act, kernel=kernel, workspace=ws_in)),
+                    ("down", lambda: rt.gemm(d, act, out=out, kernel=kernel, workspace=ws_down))]
 
         cfg = {"workload": "draft-verify step: fused gate+up (2x K5120->N17408) + down (K17408->N5120)",
                "rows": m, "format": "mlx affine q4 g64, tiled128", "weight_copies": ncopy}
@@ -112,7 +133,7 @@ def build_workload(name, rt, torch, gen):
 
         def launches(i):
             w = ws[i % ncopy]
-            return [("gemv", lambda: rt.gemm(w, x, out=out))]
+            return [("gemv", lambda: rt.gemm(w, x, out=out, kernel=kernel))]
 
         cfg = {"workload": "decode GEMV K5120->N17408", "rows": 1, "format": "mlx affine q4 g64, tiled128",
                "weight_copies": ncopy}
@@ -150,11 +171,14 @@ def cpu_baseline(workload, seconds=8.0):
     elif workload == "decode1":
         mats = [(17408, 5120)]
         m = 1
+    elif workload == "prefill2048":
+        mats = [(17408, 5120)]
+        m = 2048
     else:
         return None
     total_bytes = sum(q4_bytes(n, k) for n, k in mats) + 0
     # A seeded sample weight per shape; a column's cost does not depend on its values.
-    frac = 1 / 64
+    frac = 1 / 64 if m <= 64 else 1 / 4096
     elapsed = 0.0
     while True:
         t_total = 0.0
@@ -169,10 +193,14 @@ def cpu_baseline(workload, seconds=8.0):
         if elapsed >= 2.0 or frac >= 1.0:
             break
         frac = min(1.0, frac * max(2.0, seconds / max(elapsed, 1e-3) / 2))
+    sample = f"{frac * 100:.2f}% of each weight's output columns at M={m}, extrapolated to the full step"
+    if workload == "prefill2048":
+        flops = 2 * m * sum(n * k for n, k in mats)
+        return {"value": flops / t_total / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+                "sample": sample, "step_seconds": t_total}
     step_bytes = total_bytes + m * 5120 * 2 * (2 if workload == "verify64" else 1)
     return {"value": step_bytes / t_total / 1e12, "unit": "TB/s", "cores": threads, "kind": "port",
-            "sample": f"{frac * 100:.2f}% of each weight's output columns at M={m}, extrapolated to the full step",
-            "step_seconds": t_total}
+            "sample": sample, "step_seconds": t_total}
 
 
 def main():
@@ -182,6 +210,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="verify64")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--kernel", default="AUTO", choices=["AUTO", "STREAM", "DEQUANT", "TILE", "SCALAR"])
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU's share of the path; --gpus {args.gpus} is not supported "
@@ -192,7 +221,8 @@ def main():
     from splosh_amd import runtime as rt
 
     gen = torch.Generator(device="cuda").manual_seed(0x5EED0001)
-    launches, step_bytes, step_flops, kernel_bytes, cfg = build_workload(args.workload, rt, torch, gen)
+    launches, step_bytes, step_flops, kernel_bytes, cfg = build_workload(args.workload, rt, torch, gen,
+                                                                               getattr(rt, args.kernel))
     timer = Timer()
     torch.cuda.synchronize()
     for i in range(args.warmup):
@@ -218,16 +248,25 @@ def main():
 
     dominant = max(per_kernel, key=per_kernel.get)
     dom_ms = per_kernel[dominant]
-    achieved = kernel_bytes[dominant] / (dom_ms * 1e-3) / 1e9
-    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": MEASURED_TRAFFIC.get(args.workload),
-                "kernel": dominant, "kernel_us": round(dom_ms * 1e3, 2),
-                "algorithmic_bytes": kernel_bytes[dominant]}
-    value = step_bytes / (ms_per_step * 1e-3) / 1e12
+    compute_bound = args.workload == "prefill2048"
+    if compute_bound:
+        achieved = step_flops / (dom_ms * 1e-3) / 1e12
+        roofline = {"bound": "mfma", "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS,
+                    "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
+                    "traffic": MEASURED_TRAFFIC.get(args.workload), "kernel": dominant,
+                    "kernel_us": round(dom_ms * 1e3, 2), "algorithmic_flops": step_flops}
+        value, unit = step_flops / (ms_per_step * 1e-3) / 1e12, "TFLOP/s"
+    else:
+        achieved = kernel_bytes[dominant] / (dom_ms * 1e-3) / 1e9
+        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": MEASURED_TRAFFIC.get(args.workload),
+                    "kernel": dominant, "kernel_us": round(dom_ms * 1e3, 2),
+                    "algorithmic_bytes": kernel_bytes[dominant]}
+        value, unit = step_bytes / (ms_per_step * 1e-3) / 1e12, "TB/s"
     cpu = None if args.no_cpu else cpu_baseline(args.workload)
     result = {
         "metric": "quant GEMM effective HBM TB/s at M=1/64; TFLOP/s at M=2048 prefill",
-        "value": round(value, 4), "unit": "TB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "value": round(value, 4), "unit": unit, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16 x q4 -> fp32 acc, bf16 out", "data": "synthetic (seeded, on device)",
         "config": cfg,

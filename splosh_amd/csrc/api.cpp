@@ -85,7 +85,8 @@ bool q4_stream_eligible(const splosh_q4_weight &w, const uint16_t *a, int64_t ld
 }
 
 int q4_gemm_impl(const splosh_q4_weight *w, const splosh_q4_weight *up, const uint16_t *a, int64_t lda, void *out,
-                 int64_t ldc, int out_dtype, const void *residual, int64_t rows, int kernel, hipStream_t stream) {
+                 int64_t ldc, int out_dtype, const void *residual, int64_t rows, int kernel, void *workspace,
+                 size_t workspace_bytes, hipStream_t stream) {
     int st = check_q4_weight(w, up ? "gate" : "weight");
     if (st) return st;
     if (up) {
@@ -96,15 +97,35 @@ int q4_gemm_impl(const splosh_q4_weight *w, const splosh_q4_weight *up, const ui
     }
     if ((st = check_io(a, lda, out, ldc, out_dtype, rows, w->rows, w->inner))) return st;
     const bool eligible = q4_stream_eligible(*w, a, lda) && (!up || q4_stream_eligible(*up, a, lda));
+    const bool wide16 = eligible && aligned(w->packed, 16) && (!up || aligned(up->packed, 16)) &&
+                        (w->order == SPLOSH_Q4_TILED128 || w->row_stride_words % 4 == 0);
+    const bool tile_ok = wide16 && splosh::tile_fits(rows, w->rows, lda, w->row_stride_words);
+    const bool mma_ok = wide16 && splosh::mma_fits(rows, w->rows, w->inner, w->row_stride_words, lda);
     int choice = kernel;
-    if (choice == SPLOSH_KERNEL_AUTO) choice = eligible ? SPLOSH_KERNEL_STREAM : SPLOSH_KERNEL_SCALAR;
+    if (choice == SPLOSH_KERNEL_AUTO) {
+        if (!eligible) choice = SPLOSH_KERNEL_SCALAR;
+        else if (wide16 && splosh::lanes_fit(rows, w->rows, w->inner, w->row_stride_words, up != nullptr))
+            choice = SPLOSH_KERNEL_STREAM;
+        else if (mma_ok) choice = SPLOSH_KERNEL_DEQUANT;
+        else if (tile_ok) choice = SPLOSH_KERNEL_TILE;
+        else choice = SPLOSH_KERNEL_STREAM;
+    }
     switch (choice) {
+        case SPLOSH_KERNEL_TILE: {
+            if (!tile_ok)
+                return fail(SPLOSH_ERR_UNSUPPORTED,
+                            "tile kernel needs inner % 64 == 0, lda % 8 == 0, 16-byte aligned operands and "
+                            "32-bit element offsets");
+            const splosh::TilePlan plan =
+                splosh::plan_tile(rows, w->rows, w->inner / kGroupSize, up != nullptr, workspace ? workspace_bytes : 0);
+            return hip_status(splosh::launch_q4_tile(plan, *w, up, a, lda, out, ldc, out_dtype, residual, rows,
+                                                     workspace, stream),
+                              "q4 tile launch");
+        }
         case SPLOSH_KERNEL_STREAM: {
             if (!eligible)
                 return fail(SPLOSH_ERR_UNSUPPORTED,
                             "stream kernel needs inner % 64 == 0, lda % 8 == 0 and aligned operands");
-            const bool wide16 = aligned(w->packed, 16) && (!up || aligned(up->packed, 16)) &&
-                                (w->order == SPLOSH_Q4_TILED128 || w->row_stride_words % 4 == 0);
             if (wide16 && splosh::lanes_fit(rows, w->rows, w->inner, w->row_stride_words, up != nullptr)) {
                 const splosh::StreamPlan plan = splosh::plan_lanes(rows, w->rows, w->inner / kGroupSize, up != nullptr);
                 return hip_status(splosh::launch_q4_lanes(plan, *w, up, a, lda, out, ldc, out_dtype, residual, rows,
@@ -132,9 +153,14 @@ int q4_gemm_impl(const splosh_q4_weight *w, const splosh_q4_weight *up, const ui
             if (rows > 65535) return fail(SPLOSH_ERR_UNSUPPORTED, "scalar kernel takes at most 65535 rows");
             return hip_status(splosh::launch_q4_gemm_scalar(*w, up, a, lda, out, ldc, out_dtype, residual, rows, stream),
                               "q4 scalar launch");
-        case SPLOSH_KERNEL_DEQUANT:
-        case SPLOSH_KERNEL_TILE:
-            return fail(SPLOSH_ERR_UNSUPPORTED, "kernel not available in this build");
+        case SPLOSH_KERNEL_DEQUANT: {
+            if (!mma_ok) return fail(SPLOSH_ERR_UNSUPPORTED, "dequant kernel needs rows <= 64 and aligned operands");
+            const splosh::MmaPlan plan =
+                splosh::plan_mma(rows, w->rows, w->inner / kGroupSize, up != nullptr, workspace ? workspace_bytes : 0);
+            return hip_status(splosh::launch_q4_mma(plan, *w, up, a, lda, out, ldc, out_dtype, residual, rows,
+                                                    workspace, stream),
+                              "q4 mma launch");
+        }
         default:
             return fail(SPLOSH_ERR_UNSUPPORTED, "unknown kernel choice");
     }
@@ -270,10 +296,11 @@ int splosh_q4_shape_validate(int64_t rows, int64_t columns, int64_t inner, const
 }
 
 size_t splosh_workspace_bytes(int64_t rows, int64_t columns, int64_t inner) {
-    (void)rows;
-    (void)columns;
-    (void)inner;
-    return 0;
+    if (rows <= 0 || columns <= 0 || inner < kGroupSize) return 0;
+    const int64_t groups = inner / kGroupSize;
+    const size_t tile = splosh::tile_workspace_bytes(rows, columns, groups, true);
+    const size_t mma = rows <= 64 ? splosh::mma_workspace_bytes(rows, columns, groups, true) : 0;
+    return tile > mma ? tile : mma;
 }
 
 // Q4GemmRuntime.dispatch (Runtime/Q4Runtime.swift:94-145).
@@ -294,18 +321,16 @@ int splosh_gemm_q4(const uint16_t *a, const uint32_t *packed, const uint16_t *sc
 int splosh_q4_gemm(const splosh_q4_weight *w, const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype,
                    const void *residual, int64_t rows, int kernel, void *workspace, size_t workspace_bytes,
                    hipStream_t stream) {
-    (void)workspace;
-    (void)workspace_bytes;
-    return q4_gemm_impl(w, nullptr, a, lda, out, ldc, out_dtype, residual, rows, kernel, stream);
+    return q4_gemm_impl(w, nullptr, a, lda, out, ldc, out_dtype, residual, rows, kernel, workspace, workspace_bytes,
+                        stream);
 }
 
 int splosh_q4_mlp_in(const splosh_q4_weight *gate, const splosh_q4_weight *up, const uint16_t *a, int64_t lda,
                      void *out, int64_t ldc, int out_dtype, int64_t rows, int kernel, void *workspace,
                      size_t workspace_bytes, hipStream_t stream) {
-    (void)workspace;
-    (void)workspace_bytes;
     if (!up) return fail(SPLOSH_ERR_NULL_POINTER, "null up weight");
-    return q4_gemm_impl(gate, up, a, lda, out, ldc, out_dtype, nullptr, rows, kernel, stream);
+    return q4_gemm_impl(gate, up, a, lda, out, ldc, out_dtype, nullptr, rows, kernel, workspace, workspace_bytes,
+                        stream);
 }
 
 int splosh_q4_dequant(const splosh_q4_weight *w, float *out, hipStream_t stream) {

@@ -51,6 +51,31 @@ __device__ __forceinline__ uint32_t perm_bytes(uint32_t hi, uint32_t lo, uint32_
     return __builtin_amdgcn_perm(hi, lo, sel);
 }
 
+// Raw buffer access: a 128-bit resource (base, byte size) in SGPRs, a 32-bit per-lane offset and a
+// wave-uniform offset, no 64-bit address arithmetic. Reads at per-lane offsets past `bytes` return
+// zero; the uniform offset is kept in bounds by the callers.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ __forceinline__ rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4 buffer_load16(rsrc_t r, uint32_t voffset, uint32_t soffset) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, (int)voffset, (int)soffset, 0);
+}
+__device__ __forceinline__ uint32_t buffer_load_u16(rsrc_t r, uint32_t voffset, uint32_t soffset) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, (int)voffset, (int)soffset, 0);
+}
+
+// 16 bytes a lane from the buffer at voffset + soffset straight into LDS, without registers: lane l
+// writes bytes [lds_base + 16 l, + 16). lds_base must be wave-uniform. Counted by vmcnt.
+__device__ __forceinline__ void buffer_load16_lds(rsrc_t r, void *lds_base, uint32_t voffset, uint32_t soffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds_base, 16, (int)voffset,
+                                             (int)soffset, 0, 0);
+}
+
+// Workgroup barrier for LDS hand-offs only: waits for this wave's LDS operations, not for its
+// outstanding global loads (which __syncthreads' fence would drain), so prefetches stay in flight.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 __device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
 
 }  // namespace splosh

@@ -61,6 +61,42 @@ hipError_t launch_q4_lanes(const StreamPlan &plan, const splosh_q4_weight &w, co
                            const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype,
                            const void *residual, int64_t rows, hipStream_t stream);
 
+// The dequant-to-bf16 weight-streaming MFMA kernel for up to 64 rows (mma.hip). Split K over
+// workgroups (stream-K) uses a caller workspace of mma_workspace_bytes(); without one every band
+// is computed whole by one workgroup.
+struct MmaPlan {
+    int fm;            // 32-row blocks (1 or 2)
+    int bands;         // column bands of 64
+    int grid;          // workgroups
+    int dp_bands;      // bands computed whole (a multiple of grid)
+    int64_t sk_units;  // (band, group) pairs of the other bands, split evenly over the grid
+};
+bool mma_fits(int64_t rows, int64_t columns, int64_t inner, int64_t stride_words, int64_t lda);
+MmaPlan plan_mma(int64_t rows, int64_t columns, int64_t groups, bool mlp, size_t workspace_bytes);
+size_t mma_workspace_bytes(int64_t rows, int64_t columns, int64_t groups, bool mlp);
+hipError_t launch_q4_mma(const MmaPlan &plan, const splosh_q4_weight &w, const splosh_q4_weight *up,
+                         const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype, const void *residual,
+                         int64_t rows, void *workspace, hipStream_t stream);
+
+// Sums split-K partials [splits][nw][rows][n] in slice order and applies the epilogue
+// (silu(g) * u for nw = 2, then the optional residual, then the output conversion).
+hipError_t launch_splitk_finish(const float *partial, int splits, int nw, int64_t rows, int64_t n, void *out,
+                                int64_t ldc, int out_dtype, const void *residual, hipStream_t stream);
+
+// The LDS-tiled dequant-to-bf16 MFMA GEMM for any rows (tile.hip). Split K uses a caller workspace
+// of tile_workspace_bytes(); without one (or a smaller one) the plan does not split.
+struct TilePlan {
+    int kind;     // tile shape: 0 = 64 x 64, 1 = 256 x 256, 2 = 128 x 128
+    int grid_m, grid_n;
+    int splits;   // K slices (1 = no workspace use)
+};
+bool tile_fits(int64_t rows, int64_t columns, int64_t lda, int64_t stride_words);
+TilePlan plan_tile(int64_t rows, int64_t columns, int64_t groups, bool mlp, size_t workspace_bytes);
+size_t tile_workspace_bytes(int64_t rows, int64_t columns, int64_t groups, bool mlp);
+hipError_t launch_q4_tile(const TilePlan &plan, const splosh_q4_weight &w, const splosh_q4_weight *up,
+                          const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype, const void *residual,
+                          int64_t rows, void *workspace, hipStream_t stream);
+
 hipError_t launch_q5k_dequant(const splosh_q5k_weight &w, float *out, hipStream_t stream);
 hipError_t launch_q5k_repack(const uint8_t *native, int64_t rows, int64_t inner, uint8_t *p0,
                              uint8_t *p1, uint8_t *meta, bool inverse, hipStream_t stream);

@@ -1,0 +1,529 @@
+// mma.hip -- q4 GEMM for batched draft-verify (3..64 activation rows) on v_mfma_f32_32x32x16_bf16.
+//
+// At 64 rows a K=5120 -> N=17408 pair (gate and up, 95 MB of codes and sidecars) needs 22.8 GFLOP:
+// about 9 us of MFMA at the dense bf16 peak and 12 us of VALU to dequantize, against 12-17 us of
+// HBM. So every unit has to stay busy, and enough loads have to be in flight to cover HBM latency
+// (about 16 MB across the chip). The structure:
+//
+//  * A wave owns 32 output columns of each of NW weights (NW = 2: fused gate+up, silu(g) * u) for
+//    all rows (FM blocks of 32). Each weight is therefore dequantized exactly once, in registers,
+//    straight into the MFMA B operand. Lane (r, h) = (lane & 31, lane >> 5) feeds column r and uses
+//    words 4h .. 4h + 3 of the column's 32-byte record in the four 16-deep MFMA steps of a group
+//    (one 16-byte load; a wave reads 32 consecutive records, a contiguous kilobyte of the tiled
+//    layout). A word becomes eight bf16 weights RNE(s q + b): two ANDs split the nibbles,
+//    v_cvt_f32_ubyte0..3 converts, v_fma_f32 scales, v_cvt_pk_bf16_f32 packs -- 22 VALU.
+//  * The A operand of step i is eight activations of row r at k = 32 h + 8 i (the same k
+//    permutation as the weights). The KW waves of a column slice split K by groups (wave kw takes
+//    every KW-th group) and the CW column slices of a workgroup share one activation chunk of KW
+//    groups, staged in LDS once per step: activations are read from L2 once per workgroup.
+//  * Weight codes and sidecars are loaded D steps ahead into a register ring (D groups per wave in
+//    flight); the activation chunk one step ahead (it is L2-resident), through registers into
+//    the other of two LDS buffers. One barrier per step.
+//  * The KW partial sums reduce through LDS by halving. When the shape has too few column blocks
+//    to give every CU a workgroup, gridDim.z workgroups split K further and write fp32 partials to
+//    the caller's workspace, summed in slice order by launch_splitk_finish.
+//
+// Numerics: w is the fp32 dequantized weight (one rounding, as DequantOracle.swift:20-21) rounded
+// to bf16 (RNE), products exact in fp32, fp32 accumulation.
+#include "common.hpp"
+#include "launch.hpp"
+
+#include <cstdlib>
+
+namespace splosh {
+
+struct MmaArgs {
+    const uint32_t *packed[2];
+    const uint16_t *scales[2];
+    const uint16_t *biases[2];
+    int64_t stride_words;
+    int64_t n;
+    int64_t groups;
+    const uint16_t *a;
+    int64_t lda;
+    void *out;
+    int64_t ldc;
+    const void *residual;
+    int64_t rows;
+    int out_dtype;
+    float *partial;     // stream-K partials [gridDim.x][2][NW][rows][band columns]
+    int dp_bands;       // bands computed whole (a multiple of gridDim.x)
+    int64_t sk_units;   // (band, group) pairs of the remaining bands
+    uint32_t code_bytes, sidecar_bytes, a_bytes;  // buffer extents (mma_fits keeps them < 4 GiB)
+};
+
+__device__ __forceinline__ float cvt_byte(uint32_t x, int j) {
+    float r;
+    switch (j) {
+        case 0: asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(x)); break;
+        case 1: asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(x)); break;
+        case 2: asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(x)); break;
+        default: asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(x)); break;
+    }
+    return r;
+}
+
+// Eight weights of one code word, dequantized and rounded to bf16 in k order.
+__device__ __forceinline__ bf16x8 dequant_word(uint32_t w, float s, float b) {
+    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+    u32x4 d;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        d[j] = f32x2_to_bf16x2(__builtin_fmaf(s, cvt_byte(lo, j), b), __builtin_fmaf(s, cvt_byte(hi, j), b));
+    return as_bf16x8(d);
+}
+
+template <int FM, int NW, int CW, int KW, int D>
+struct MmaShape {
+    static constexpr int kThreads = CW * KW * 64;
+    static constexpr int kRows = FM * 32;
+    static constexpr int kBandCols = CW * 32;
+    static constexpr int kKc = KW * 8;                             // 16-byte pieces per chunk row
+    static constexpr int kAPieces = kRows * kKc;
+    static_assert(kAPieces % kThreads == 0, "whole activation pieces per thread");
+    static constexpr int kAPer = kAPieces / kThreads;              // LDS-DMA loads per wave and step
+    static constexpr int kABuf = kAPieces * 16;                    // bytes of one chunk buffer
+    static constexpr int kNB = D + 1;                              // chunk buffers
+    static constexpr int kAcc = FM * NW * 16;                      // accumulator floats per lane
+    static constexpr size_t kRedBytes = (size_t)KW * CW * kAcc * 64 * sizeof(float);
+    static constexpr size_t kABytes = (size_t)kNB * kABuf;
+    static constexpr size_t kLds = kRedBytes > kABytes ? kRedBytes : kABytes;
+    static constexpr int kWLoads = NW * 3;                         // weight loads per wave and step
+    // Loads a wave issues after step s's activation chunk up to the end of step s + D - 1, when
+    // that chunk must have landed: the rest of step s (its weights) and D - 1 further steps.
+    static constexpr int kChunkWait = kWLoads + (D - 1) * (kAPer + kWLoads);
+    static_assert(kChunkWait < 64, "vmcnt range");
+    static_assert(D >= 2 && D <= 5, "the final steps' waits are written out for D <= 5");
+};
+
+// s_waitcnt with only vmcnt bounded (expcnt and lgkmcnt left at their maxima), gfx9 encoding.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Work split. The N columns form `bands` bands of CW * 32. Bands [0, dp_bands) are computed whole
+// by workgroup (band mod gridDim.x), written straight to the output. The remaining bands' (band,
+// group) pairs, sk_units of them, are cut into gridDim.x equal contiguous ranges (stream-K), one a
+// workgroup; a range covers at most two bands, and a band it covers in part is written as an fp32
+// partial to slot 0 (the range's first band) or 1 of the workgroup's workspace, summed later by
+// q4_mma_finish. dp_bands is a multiple of gridDim.x, so every workgroup gets the same work.
+//
+// Pipeline of a job (groups [ga, gb) of one band), in steps of KW groups, D steps deep:
+//  * the activation chunk of step t (rows x KW groups) is copied global -> LDS by the waves
+//    themselves with buffer_load ... lds (no registers), into buffer t mod (D + 1), XOR-swizzled
+//    (16-byte piece kc of row m at position kc ^ (m & 7)) so the MFMA operand reads do not
+//    conflict; weight codes and sidecars go to a D-slot register ring;
+//  * every wave issues exactly the same loads each step, so the chunk needed next is waited for
+//    with a fixed vmcnt that leaves the younger D - 1 steps of loads in flight; the last D steps
+//    issue nothing. Barriers wait for LDS traffic only, never for global stores.
+template <int FM, int NW, bool TILED, int CW, int KW, int D>
+__global__ void __launch_bounds__(CW * KW * 64)
+q4_mma_kernel(MmaArgs args) {
+    using S = MmaShape<FM, NW, CW, KW, D>;
+    extern __shared__ __align__(16) uint16_t lds[];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int cw = wave % CW, kw = wave / CW;
+    const int r = lane & 31, h = lane >> 5;
+    const int G = (int)args.groups;
+    const uint32_t G32 = (uint32_t)G;
+
+    const rsrc_t a_rsrc = make_rsrc(args.a, args.a_bytes);
+    rsrc_t q_rsrc[NW], s_rsrc[NW], b_rsrc[NW];
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+        q_rsrc[w] = make_rsrc(args.packed[w], args.code_bytes);
+        s_rsrc[w] = make_rsrc(args.scales[w], args.sidecar_bytes);
+        b_rsrc[w] = make_rsrc(args.biases[w], args.sidecar_bytes);
+    }
+    // LDS-DMA source of this lane's pieces: load j of the wave fills buffer positions
+    // (wave * kAPer + j) * 64 + lane, i.e. row m = pos / kKc and piece kc = (pos % kKc) ^ (m & 7),
+    // at byte (m lda + 64 g + 8 kc) * 2. Rows past the last are clamped (their outputs are not
+    // stored); groups past the job belong to inactive waves; reads past the buffer return zero.
+    uint32_t a_src[S::kAPer];
+#pragma unroll
+    for (int j = 0; j < S::kAPer; ++j) {
+        const int pos = (wave * S::kAPer + j) * 64 + lane;
+        const int row = pos / S::kKc, kc = (pos % S::kKc) ^ (row & 7);
+        const int64_t rc = row < args.rows ? row : args.rows - 1;
+        a_src[j] = (uint32_t)((rc * args.lda + kc * 8) * 2);
+    }
+    // MFMA operand reads: sub-step i of block f takes row 32 f + r, piece kw * 8 + 4 h + i.
+    uint32_t a_rd[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a_rd[i] = (uint32_t)((r * S::kKc + ((kw * 8 + 4 * h + i) ^ (r & 7))) * 16);
+    char *lds_bytes = (char *)lds;
+
+    // One job: column band `band`, groups [ga, gb); slot < 0 writes the output, else a partial.
+    auto run_job = [&](int band, int ga, int gb, int slot) {
+        const int T = (gb - ga + KW - 1) / KW;  // steps of KW groups
+        const int64_t ncol = (int64_t)band * S::kBandCols + cw * 32 + r;
+        const uint32_t col = (uint32_t)(ncol < args.n ? ncol : args.n - 1);
+        uint32_t q_lane, side_lane, q_group, side_group;
+        if (TILED) {
+            const uint32_t rec0 = (col >> 7) * G32 * 128u + (col & 127u);  // record of group 0
+            q_lane = rec0 * 32u + 16u * h;
+            side_lane = rec0 * 2u;
+            q_group = 128u * 32u;
+            side_group = 128u * 2u;
+        } else {
+            q_lane = col * (uint32_t)args.stride_words * 4u + 16u * h;
+            side_lane = col * G32 * 2u;
+            q_group = 32u;
+            side_group = 2u;
+        }
+
+        auto issue_a = [&](int t, int buf) {
+            const uint32_t gbyte = (uint32_t)(ga + t * KW) * 128u;
+#pragma unroll
+            for (int j = 0; j < S::kAPer; ++j)
+                buffer_load16_lds(a_rsrc, lds_bytes + buf * S::kABuf + (wave * S::kAPer + j) * 1024, a_src[j] + gbyte, 0);
+        };
+        // Weight ring: step t's codes and sidecars in slot t % D; the group is a wave-uniform
+        // offset, clamped into the job so it stays in bounds.
+        u32x4 wq[D][NW];
+        uint32_t wsc[D][NW], wbi[D][NW];
+        auto load_w = [&](int slot_, int t) {
+            int g = ga + t * KW + kw;
+            g = g < gb ? g : gb - 1;
+            const uint32_t ug = (uint32_t)__builtin_amdgcn_readfirstlane(g);
+#pragma unroll
+            for (int w = 0; w < NW; ++w) {
+                wq[slot_][w] = buffer_load16(q_rsrc[w], q_lane, ug * q_group);
+                wsc[slot_][w] = buffer_load_u16(s_rsrc[w], side_lane, ug * side_group);
+                wbi[slot_][w] = buffer_load_u16(b_rsrc[w], side_lane, ug * side_group);
+            }
+        };
+        // Dequantized weights of the current step; word i is replaced by the next step's word i as
+        // soon as the MFMAs of sub-step i have been issued.
+        bf16x8 bw[NW][4];
+        auto dequant = [&](int slot_) {
+#pragma unroll
+            for (int w = 0; w < NW; ++w) {
+                const float s = bf16_bits_to_f32(wsc[slot_][w]), b = bf16_bits_to_f32(wbi[slot_][w]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) bw[w][i] = dequant_word(wq[slot_][w][i], s, b);
+            }
+        };
+
+        f32x16 acc[NW][FM];
+#pragma unroll
+        for (int w = 0; w < NW; ++w)
+#pragma unroll
+            for (int f = 0; f < FM; ++f)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[w][f][e] = 0.0f;
+
+        // The step count is padded to a multiple of D: steps past T compute nothing but keep the
+        // load pattern regular (their loads re-read in-bounds data). Every step but the last D
+        // issues the loads of step t + D, so the chunk needed next is waited for with a fixed vmcnt
+        // that leaves the younger D - 1 steps of loads in flight; the last D steps issue nothing
+        // and wait for exactly what they need.
+        const int Tp = (T + D - 1) / D * D;
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            issue_a(d, d);
+            load_w(d, d);
+        }
+        wait_vmcnt<S::kChunkWait>();
+        dequant(0);
+        lds_barrier();
+
+        // Step t: the MFMAs of step t with the dequantization of step t + 1 interleaved (only the
+        // dequantization when the wave has no group in step t).
+        auto compute = [&](int t, int d, int abuf) {
+            const int next = (d + 1) % D;
+            const char *ap = lds_bytes + abuf * S::kABuf;
+            if (t < T && ga + t * KW + kw < gb) {
+                float sn[NW], bn[NW];
+#pragma unroll
+                for (int w = 0; w < NW; ++w) {
+                    sn[w] = bf16_bits_to_f32(wsc[next][w]);
+                    bn[w] = bf16_bits_to_f32(wbi[next][w]);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    bf16x8 af[FM];
+#pragma unroll
+                    for (int f = 0; f < FM; ++f) af[f] = as_bf16x8(*(const u32x4 *)(ap + a_rd[i] + f * 32 * S::kKc * 16));
+#pragma unroll
+                    for (int w = 0; w < NW; ++w)
+#pragma unroll
+                        for (int f = 0; f < FM; ++f)
+                            acc[w][f] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[f], bw[w][i], acc[w][f], 0, 0, 0);
+#pragma unroll
+                    for (int w = 0; w < NW; ++w) bw[w][i] = dequant_word(wq[next][w][i], sn[w], bn[w]);
+                    __builtin_amdgcn_sched_group_barrier(0x100, FM, 0);  // this sub-step's LDS reads
+#pragma unroll
+                    for (int j = 0; j < NW * FM; ++j) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);        // one MFMA
+                        __builtin_amdgcn_sched_group_barrier(0x002, 22 / FM, 0);  // dequant VALU
+                    }
+                }
+            } else {
+                dequant(next);
+            }
+        };
+
+        int abuf = 0;  // buffer of step t's chunk
+        for (int t0 = 0; t0 < Tp - D; t0 += D) {
+#pragma unroll
+            for (int d = 0; d < D; ++d) {
+                const int t = t0 + d;
+                compute(t, d, abuf);
+                // Refill: chunk t + D into the buffer read in step t - 1, weights into slot t % D.
+                issue_a(t + D, abuf == 0 ? S::kNB - 1 : abuf - 1);
+                load_w(d, t + D);
+                abuf = abuf == S::kNB - 1 ? 0 : abuf + 1;
+                wait_vmcnt<S::kChunkWait>();  // chunk t + 1 has landed
+                lds_barrier();
+            }
+        }
+        // The last D steps: in step Tp - D + d the loads of the D - 2 - d younger steps may stay in
+        // flight; the last step drains.
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            compute(Tp - D + d, d, abuf);
+            abuf = abuf == S::kNB - 1 ? 0 : abuf + 1;
+            if (d == D - 1) {
+                wait_vmcnt<0>();
+            } else if (d == D - 2) {
+                wait_vmcnt<S::kWLoads>();
+            } else if (d == D - 3) {
+                wait_vmcnt<S::kWLoads + (S::kAPer + S::kWLoads)>();
+            } else {
+                wait_vmcnt<S::kWLoads + 2 * (S::kAPer + S::kWLoads)>();
+            }
+            lds_barrier();
+        }
+        // No load is in flight now; the last barrier also ended every read of the chunk buffers.
+
+        // Every wave parks its partial sums in LDS (element e of block f of weight w at
+        // [kw][cw][(w FM + f) 16 + e][lane]); then the whole workgroup sums the KW slices per output
+        // and writes whole rows: thread (m0, c) = (tid / band columns, tid % band columns) takes
+        // rows m0, m0 + kThreads / band columns, ...
+        {
+            float *red = (float *)lds + (size_t)(kw * CW + cw) * S::kAcc * 64 + lane;
+#pragma unroll
+            for (int w = 0; w < NW; ++w)
+#pragma unroll
+                for (int f = 0; f < FM; ++f)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) red[((w * FM + f) * 16 + e) * 64] = acc[w][f][e];
+        }
+        lds_barrier();
+        constexpr int kRowStep = S::kThreads / S::kBandCols;
+        const int c = tid % S::kBandCols;
+        const int64_t ocol = (int64_t)band * S::kBandCols + c;
+        const int rows = (int)args.rows;
+        const float *red = (const float *)lds + (size_t)(c / 32) * S::kAcc * 64 + (c % 32);
+#pragma unroll
+        for (int m = tid / S::kBandCols; m < S::kRows; m += kRowStep) {
+            if (m >= rows) break;
+            const int f = m / 32, mm = m % 32;
+            const int e = (mm / 8) * 4 + (mm % 4), lane_h = ((mm / 4) % 2) * 32;
+            float v[NW];
+#pragma unroll
+            for (int w = 0; w < NW; ++w) {
+                float sum = 0.0f;
+#pragma unroll
+                for (int k = 0; k < KW; ++k) sum += red[(size_t)k * CW * S::kAcc * 64 + ((w * FM + f) * 16 + e) * 64 + lane_h];
+                v[w] = sum;
+            }
+            if (ocol >= args.n) continue;
+            if (slot >= 0) {
+                float *dst = args.partial + ((int64_t)(blockIdx.x * 2 + slot) * NW * rows + m) * S::kBandCols + c;
+#pragma unroll
+                for (int w = 0; w < NW; ++w) dst[(int64_t)w * rows * S::kBandCols] = v[w];
+                continue;
+            }
+            float value = v[0];
+            if constexpr (NW == 2) value = silu(v[0]) * v[1];
+            const int64_t index = (int64_t)m * args.ldc + ocol;
+            if (args.out_dtype == SPLOSH_F32) {
+                if (args.residual) value += ((const float *)args.residual)[index];
+                ((float *)args.out)[index] = value;
+            } else {
+                if (args.residual) value += bf16_bits_to_f32(((const uint16_t *)args.residual)[index]);
+                ((uint16_t *)args.out)[index] = f32_to_bf16(value);
+            }
+        }
+    };
+
+    const int P = gridDim.x;
+    for (int band = blockIdx.x; band < args.dp_bands; band += P) {
+        run_job(band, 0, G, -1);
+        lds_barrier();  // the next job's loads overwrite the reduction area; stores need not drain
+    }
+    if (args.sk_units > 0) {
+        int64_t u = args.sk_units * blockIdx.x / P;
+        const int64_t u_end = args.sk_units * (blockIdx.x + 1) / P;
+        int slot = 0;
+        while (u < u_end) {
+            const int band = args.dp_bands + (int)(u / G);
+            const int ga = (int)(u % G);
+            const int gb = (int)((int64_t)ga + (u_end - u) < G ? ga + (u_end - u) : G);
+            run_job(band, ga, gb, (ga == 0 && gb == G) ? -1 : slot);
+            lds_barrier();
+            u += gb - ga;
+            slot = 1;
+        }
+    }
+}
+
+// Sums the stream-K partials of the remainder bands (see q4_mma_kernel) in workgroup order and
+// applies the epilogue. One thread per output of the remainder bands.
+__global__ void __launch_bounds__(256)
+q4_mma_finish(const float *__restrict__ partial, int nw, int band_cols, int dp_bands, int64_t sk_units, int P,
+              int64_t groups, int64_t rows, int64_t n, void *out, int64_t ldc, int out_dtype, const void *residual) {
+    const int64_t per_band = rows * band_cols;
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t rbands = sk_units / groups;
+    if (idx >= rbands * per_band) return;
+    const int64_t rb = idx / per_band, rem = idx % per_band;
+    const int64_t m = rem / band_cols, bc = rem % band_cols;
+    const int64_t col = (int64_t)(dp_bands + rb) * band_cols + bc;
+    if (col >= n) return;
+    const int64_t lo = rb * groups, hi = lo + groups;  // the band's units
+    // Workgroup i covers units [U i / P, U (i + 1) / P); the one holding unit u is
+    // floor(((u + 1) P - 1) / U); ranges may be empty when there are fewer units than workgroups.
+    const int i_lo = (int)(((lo + 1) * P - 1) / sk_units), i_hi = (int)((hi * P - 1) / sk_units);
+    float v[2] = {0.0f, 0.0f};
+    int contributors = 0;
+    for (int i = i_lo; i <= i_hi; ++i) {
+        const int64_t s = sk_units * i / P, e = sk_units * (i + 1) / P;
+        if (s == e) continue;  // an empty range wrote nothing
+        const int slot = s < lo ? 1 : 0;
+        const float *src = partial + ((int64_t)(i * 2 + slot) * nw * rows + m) * band_cols + bc;
+        for (int w = 0; w < nw; ++w) v[w] += src[(int64_t)w * rows * band_cols];
+        ++contributors;
+    }
+    if (contributors <= 1) return;  // one workgroup covered the band and wrote it
+    float value = nw == 2 ? silu(v[0]) * v[1] : v[0];
+    const int64_t index = m * ldc + col;
+    if (out_dtype == SPLOSH_F32) {
+        if (residual) value += ((const float *)residual)[index];
+        ((float *)out)[index] = value;
+    } else {
+        if (residual) value += bf16_bits_to_f32(((const uint16_t *)residual)[index]);
+        ((uint16_t *)out)[index] = f32_to_bf16(value);
+    }
+}
+
+constexpr int kMmaCW = 2, kMmaKW = 4;
+
+// Pipeline depth: chunk buffers take (D + 1) x rows x 512 bytes of LDS.
+template <int FM>
+constexpr int mma_depth() { return FM == 2 ? 3 : 4; }
+
+// Activation and code offsets are 32-bit; 64 rows at most.
+bool mma_fits(int64_t rows, int64_t columns, int64_t inner, int64_t stride_words, int64_t lda) {
+    const int64_t limit = ((int64_t)1 << 32) - 256;  // byte extents of the buffer resources
+    const int64_t groups = inner / kGroup;
+    return rows >= 1 && rows <= 64 && columns > 0 && groups > 0 && (rows * lda + inner) * 2 < limit &&
+           columns * stride_words * 4 < limit && columns * groups * 32 < limit;
+}
+
+// Compute units of the current device (the stream-K grid), cached per device.
+static int device_cus() {
+    static int cache[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cache[dev]) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+        cache[dev] = cus;
+    }
+    return cache[dev];
+}
+
+static size_t sk_bytes(int grid, int64_t rows, bool mlp) {
+    return (size_t)grid * 2 * (mlp ? 2 : 1) * rows * (kMmaCW * 32) * sizeof(float);
+}
+
+MmaPlan plan_mma(int64_t rows, int64_t columns, int64_t groups, bool mlp, size_t workspace_bytes) {
+    MmaPlan p;
+    p.fm = rows <= 32 ? 1 : 2;
+    p.bands = (int)((columns + kMmaCW * 32 - 1) / (kMmaCW * 32));
+    int grid = device_cus();
+    if (const char *env = getenv("SPLOSH_MMA_GRID")) grid = atoi(env) > 0 ? atoi(env) : grid;
+    p.grid = grid;
+    p.dp_bands = (p.bands / grid) * grid;
+    p.sk_units = (int64_t)(p.bands - p.dp_bands) * groups;
+    if (p.sk_units > 0 && sk_bytes(grid, rows, mlp) > workspace_bytes) {
+        // No room for partials: every band whole, one workgroup each.
+        p.grid = p.bands;
+        p.dp_bands = p.bands;
+        p.sk_units = 0;
+    }
+    return p;
+}
+
+size_t mma_workspace_bytes(int64_t rows, int64_t columns, int64_t groups, bool mlp) {
+    const MmaPlan p = plan_mma(rows, columns, groups, mlp, (size_t)-1);
+    return p.sk_units > 0 ? sk_bytes(p.grid, rows, mlp) : 0;
+}
+
+template <int FM, int NW, bool TILED>
+static hipError_t launch_mma_v(const MmaPlan &p, const MmaArgs &args, hipStream_t stream) {
+    constexpr int D = mma_depth<FM>();
+    using S = MmaShape<FM, NW, kMmaCW, kMmaKW, D>;
+    auto kernel = q4_mma_kernel<FM, NW, TILED, kMmaCW, kMmaKW, D>;
+    static bool once = [&] {
+        (void)hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)S::kLds);
+        return true;
+    }();
+    (void)once;
+    hipLaunchKernelGGL(kernel, dim3((unsigned)p.grid), dim3(S::kThreads), S::kLds, stream, args);
+    return hipGetLastError();
+}
+
+template <int NW, bool TILED>
+static hipError_t launch_mma_fm(const MmaPlan &p, const MmaArgs &args, hipStream_t stream) {
+    return p.fm == 1 ? launch_mma_v<1, NW, TILED>(p, args, stream) : launch_mma_v<2, NW, TILED>(p, args, stream);
+}
+
+hipError_t launch_q4_mma(const MmaPlan &plan, const splosh_q4_weight &w, const splosh_q4_weight *up,
+                         const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype, const void *residual,
+                         int64_t rows, void *workspace, hipStream_t stream) {
+    MmaArgs args;
+    args.packed[0] = w.packed;
+    args.scales[0] = w.scales;
+    args.biases[0] = w.biases;
+    args.packed[1] = up ? up->packed : w.packed;
+    args.scales[1] = up ? up->scales : w.scales;
+    args.biases[1] = up ? up->biases : w.biases;
+    args.stride_words = w.row_stride_words;
+    args.n = w.rows;
+    args.groups = w.inner / kGroup;
+    args.a = a;
+    args.lda = lda;
+    args.out = out;
+    args.ldc = ldc;
+    args.residual = residual;
+    args.rows = rows;
+    args.out_dtype = out_dtype;
+    args.partial = plan.sk_units > 0 ? (float *)workspace : nullptr;
+    args.dp_bands = plan.dp_bands;
+    args.sk_units = plan.sk_units;
+    const bool tiled = w.order == SPLOSH_Q4_TILED128;
+    const int64_t groups = w.inner / kGroup;
+    args.code_bytes = (uint32_t)(tiled ? w.rows * groups * 32 : w.rows * w.row_stride_words * 4);
+    args.sidecar_bytes = (uint32_t)(w.rows * groups * 2);
+    args.a_bytes = (uint32_t)(((rows - 1) * lda + w.inner) * 2);
+    hipError_t err;
+    if (up)
+        err = tiled ? launch_mma_fm<2, true>(plan, args, stream) : launch_mma_fm<2, false>(plan, args, stream);
+    else
+        err = tiled ? launch_mma_fm<1, true>(plan, args, stream) : launch_mma_fm<1, false>(plan, args, stream);
+    if (err != hipSuccess || plan.sk_units == 0) return err;
+    const int64_t total = (plan.sk_units / groups) * rows * (kMmaCW * 32);
+    hipLaunchKernelGGL(q4_mma_finish, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream,
+                       (const float *)workspace, up ? 2 : 1, kMmaCW * 32, plan.dp_bands, plan.sk_units, plan.grid, groups,
+                       rows, w.rows, out, ldc, out_dtype, residual);
+    return hipGetLastError();
+}
+
+}  // namespace splosh

@@ -119,7 +119,25 @@ def _out(a, rows, n, out, out_dtype):
     return out
 
 
-def gemm(w, a, out=None, residual=None, out_dtype=torch.bfloat16, kernel=AUTO, rows=None, stream=None):
+def workspace_bytes(rows, columns, inner):
+    """splosh_workspace_bytes: the split-K scratch the tiled kernel can use for this shape (0: none)."""
+    return _lib.lib().splosh_workspace_bytes(rows, columns, inner)
+
+
+def _workspace(workspace, rows, n, inner, device):
+    """The split-K scratch of the tiled kernel: the caller's tensor, or a fresh one from torch's
+    stream-ordered allocator sized by splosh_workspace_bytes."""
+    if workspace is not None:
+        return _ptr(workspace), workspace.numel() * workspace.element_size()
+    need = _lib.lib().splosh_workspace_bytes(rows, n, inner)
+    if need == 0:
+        return None, 0
+    buf = torch.empty(need, dtype=torch.uint8, device=device)
+    return _ptr(buf), need
+
+
+def gemm(w, a, out=None, residual=None, out_dtype=torch.bfloat16, kernel=AUTO, rows=None, stream=None,
+         workspace=None):
     """Engine.gemm (Runtime/Engine.swift:1652-1806): out = a @ dequant(w)^T (+ residual).
 
     ``a`` is bf16 [rows, inner] (row stride a.stride(0)); ``out`` [rows, w.rows] in fp32 or bf16;
@@ -137,8 +155,9 @@ def gemm(w, a, out=None, residual=None, out_dtype=torch.bfloat16, kernel=AUTO, r
             raise SploshError(13, "residual must match the output's dtype and row stride")
     wc = w.c()
     if isinstance(w, Q4Weight):
+        ws, ws_bytes = _workspace(workspace, rows, w.rows, w.inner, a.device)
         st = _lib.lib().splosh_q4_gemm(ctypes.byref(wc), _ptr(a), a.stride(0), _ptr(out), out.stride(0),
-                                       _dtype_code(out.dtype), _ptr(residual), rows, kernel, None, 0,
+                                       _dtype_code(out.dtype), _ptr(residual), rows, kernel, ws, ws_bytes,
                                        _stream(stream))
     else:
         st = _lib.lib().splosh_q5k_gemm(ctypes.byref(wc), _ptr(a), a.stride(0), _ptr(out), out.stride(0),
@@ -148,7 +167,7 @@ def gemm(w, a, out=None, residual=None, out_dtype=torch.bfloat16, kernel=AUTO, r
     return out
 
 
-def mlp_in(gate, up, a, out=None, out_dtype=torch.bfloat16, kernel=AUTO, rows=None, stream=None):
+def mlp_in(gate, up, a, out=None, out_dtype=torch.bfloat16, kernel=AUTO, rows=None, stream=None, workspace=None):
     """Engine.mlpIn (Runtime/Engine.swift:1911-1966): out = silu(a @ gate^T) * (a @ up^T), one
     pass over the activations for both weights."""
     rows = a.shape[0] if rows is None else rows
@@ -158,8 +177,10 @@ def mlp_in(gate, up, a, out=None, out_dtype=torch.bfloat16, kernel=AUTO, rows=No
     _require(a, ((rows - 1) * a.stride(0) + gate.inner) * 2, "a")
     _require(out, ((rows - 1) * out.stride(0) + gate.rows) * out.element_size(), "output")
     gc, uc = gate.c(), up.c()
+    ws, ws_bytes = _workspace(workspace, rows, gate.rows, gate.inner, a.device)
     st = _lib.lib().splosh_q4_mlp_in(ctypes.byref(gc), ctypes.byref(uc), _ptr(a), a.stride(0), _ptr(out),
-                                     out.stride(0), _dtype_code(out.dtype), rows, kernel, None, 0, _stream(stream))
+                                     out.stride(0), _dtype_code(out.dtype), rows, kernel, ws, ws_bytes,
+                                     _stream(stream))
     _lib.check(st)
     return out
 

@@ -117,3 +117,17 @@ def test_entry_points_validate_before_launch():
     st = lib.splosh_q4_mlp_in(ctypes.byref(g), ctypes.byref(u), ctypes.c_void_p(0x4000), 512, ctypes.c_void_p(0x5000),
                               256, _lib.BF16, 1, _lib.KERNEL_AUTO, None, 0, None)
     assert _lib.STATUS_NAMES[st] == "layoutMismatch"
+
+
+def test_no_undefined_kernel_symbols():
+    """Every kernel the launchers reference is defined in the library (a host stub that the
+    compiler silently dropped would only show up as a load failure on the GPU box)."""
+    import shutil
+    import subprocess
+    from splosh_amd import _lib
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("nm not available")
+    out = subprocess.run([nm, "-D", "--undefined-only", str(_lib.LIB_PATH)], capture_output=True, text=True,
+                         check=True).stdout
+    assert "splosh" not in out, out

@@ -7,7 +7,7 @@ import pytest
 import torch
 
 import oracle
-from qcheck import Q4Case, bf16_tensor, check_close, dev_u16, dev_u32, to_f32
+from qcheck import Q4Case, abs_gemm, bf16_tensor, check_close, dev_u16, dev_u32, to_f32
 
 pytestmark = pytest.mark.gpu
 
@@ -78,20 +78,64 @@ def test_gemm_q4_runtime_rejects_small_buffers(rt):
 ROWS = [1, 2, 3, 4, 5, 8, 16, 17, 31, 33, 64, 65, 100]
 
 
+@pytest.mark.parametrize("kernel", ["STREAM", "TILE"])
 @pytest.mark.parametrize("order", ["tiled", "rowmajor"])
 @pytest.mark.parametrize("rows", ROWS)
-def test_stream_gemm_rows(rt, order, rows):
+def test_stream_gemm_rows(rt, kernel, order, rows):
     case = Q4Case(384, 768, seed=10 + rows)
     w = case.w_tiled if order == "tiled" else case.w_rm
     a_bits = oracle.bf16_normal((rows, case.k), seed=100 + rows)
     ref = oracle.gemm_a_bf16_w_f32(a_bits, case.dense)
+    absref = abs_gemm(a_bits, case.dense)
     for out_dtype in (torch.bfloat16, torch.float32):
-        got = rt.gemm(w, bf16_tensor(a_bits), out_dtype=out_dtype, kernel=rt.STREAM)
-        check_close(to_f32(got), ref, bf16_out=out_dtype == torch.bfloat16, tight=True,
-                    label=f"{order} rows={rows} {out_dtype}")
+        got = rt.gemm(w, bf16_tensor(a_bits), out_dtype=out_dtype, kernel=getattr(rt, kernel))
+        check_close(to_f32(got), ref, bf16_out=out_dtype == torch.bfloat16, tight=True, absref=absref,
+                    label=f"{kernel} {order} rows={rows} {out_dtype}")
 
 
-def test_stream_gemm_odd_columns_and_strides(rt):
+@pytest.mark.parametrize("order", ["tiled", "rowmajor"])
+@pytest.mark.parametrize("rows", [1, 3, 32, 33, 64])
+def test_dequant_kernel(rt, order, rows):
+    """Group counts that are not a multiple of the workgroup's K waves (K = 1216: 19 groups)."""
+    case = Q4Case(384, 1216, seed=40 + rows)
+    w = case.w_tiled if order == "tiled" else case.w_rm
+    a_bits = oracle.bf16_normal((rows, case.k), seed=41)
+    ref = oracle.gemm_a_bf16_w_f32(a_bits, case.dense)
+    got = rt.gemm(w, bf16_tensor(a_bits), kernel=rt.DEQUANT)
+    check_close(to_f32(got), ref, bf16_out=True, tight=True, absref=abs_gemm(a_bits, case.dense))
+
+
+@pytest.mark.parametrize("kernel", ["TILE", "DEQUANT"])
+@pytest.mark.parametrize("mlp", [False, True])
+def test_split_k(rt, kernel, mlp):
+    """Few output blocks and a long K: the tiled kernel splits K over a workspace and sums the
+    slices in a second pass; with a workspace that is too small it must not split. Both agree with
+    the oracle, and the split result is deterministic."""
+    rows, n, k = 64, 256, 4096
+    gate, up = Q4Case(n, k, seed=50), Q4Case(n, k, seed=51)
+    a_bits = oracle.bf16_normal((rows, k), seed=52)
+    g = oracle.gemm_a_bf16_w_f32(a_bits, gate.dense)
+    ref = oracle.silu_mul(g, oracle.gemm_a_bf16_w_f32(a_bits, up.dense)) if mlp else g
+    absref = abs_gemm(a_bits, gate.dense)
+    need = rt.workspace_bytes(rows, n, k)
+    assert need > 0
+    a = bf16_tensor(a_bits)
+    outs = []
+    for ws in (torch.empty(need, dtype=torch.uint8, device="cuda"), torch.empty(16, dtype=torch.uint8, device="cuda"),
+               None):
+        if mlp:
+            got = rt.mlp_in(gate.w_tiled, up.w_tiled, a, out_dtype=torch.float32, kernel=getattr(rt, kernel),
+                            workspace=ws)
+            check_close(got.cpu().numpy(), ref, bf16_out=False, label="split mlp")
+        else:
+            got = rt.gemm(gate.w_tiled, a, out_dtype=torch.float32, kernel=getattr(rt, kernel), workspace=ws)
+            check_close(got.cpu().numpy(), ref, bf16_out=False, tight=True, absref=absref, label="split")
+        outs.append(got.cpu().numpy())
+    assert np.array_equal(outs[0], outs[2])
+
+
+@pytest.mark.parametrize("kernel", ["STREAM", "DEQUANT", "TILE"])
+def test_stream_gemm_odd_columns_and_strides(rt, kernel):
     """Row-major weight with N not a multiple of 16, padded activation rows, output written into a
     wider buffer whose other columns and rows must stay untouched."""
     n, k, rows = 200, 448, 7
@@ -100,9 +144,10 @@ def test_stream_gemm_odd_columns_and_strides(rt):
     ref = oracle.gemm_a_bf16_w_f32(np.ascontiguousarray(a_full[:, :k]), case.dense)
     a = bf16_tensor(a_full)
     out = torch.full((rows + 2, n + 40), 7.0, dtype=torch.float32, device="cuda")
-    rt.gemm(case.w_rm, a, out=out[:, :], rows=rows, kernel=rt.STREAM)
+    rt.gemm(case.w_rm, a, out=out[:, :], rows=rows, kernel=getattr(rt, kernel))
     o = out.cpu().numpy()
-    check_close(o[:rows, :n], ref, bf16_out=False, tight=True)
+    check_close(o[:rows, :n], ref, bf16_out=False, tight=True,
+                absref=abs_gemm(np.ascontiguousarray(a_full[:, :k]), case.dense))
     assert np.all(o[:rows, n:] == 7.0) and np.all(o[rows:] == 7.0)
 
 
@@ -114,7 +159,7 @@ def test_residual_in_place(rt):
     ref = oracle.gemm_a_bf16_w_f32(a_bits, case.dense) + base
     out = torch.from_numpy(base.copy()).cuda()
     rt.Engine(kernel=rt.STREAM).gemm(case.w_tiled, bf16_tensor(a_bits), out, residual=True)
-    check_close(out.cpu().numpy(), ref, bf16_out=False, tight=True)
+    check_close(out.cpu().numpy(), ref, bf16_out=False, tight=True, absref=abs_gemm(a_bits, case.dense))
 
 
 def test_scalar_kernel_any_shape(rt):
@@ -129,8 +174,9 @@ def test_scalar_kernel_any_shape(rt):
     assert e.value.case == "unsupported"
 
 
-@pytest.mark.parametrize("rows", [1, 2, 8, 64])
-def test_mlp_in_fused(rt, rows):
+@pytest.mark.parametrize("kernel", ["AUTO", "STREAM", "TILE"])
+@pytest.mark.parametrize("rows", [1, 2, 8, 64, 130])
+def test_mlp_in_fused(rt, kernel, rows):
     k, n = 512, 384
     gate, up = Q4Case(n, k, seed=30), Q4Case(n, k, seed=31)
     a_bits = oracle.bf16_normal((rows, k), seed=32)
@@ -138,9 +184,9 @@ def test_mlp_in_fused(rt, rows):
     u = oracle.gemm_a_bf16_w_f32(a_bits, up.dense)
     ref = oracle.silu_mul(g, u)
     for w_g, w_u in ((gate.w_tiled, up.w_tiled), (gate.w_rm, up.w_rm)):
-        got = rt.mlp_in(w_g, w_u, bf16_tensor(a_bits), out_dtype=torch.float32)
+        got = rt.mlp_in(w_g, w_u, bf16_tensor(a_bits), out_dtype=torch.float32, kernel=getattr(rt, kernel))
         check_close(got.cpu().numpy(), ref, bf16_out=False, label=f"mlp rows={rows}")
-        got = rt.mlp_in(w_g, w_u, bf16_tensor(a_bits))
+        got = rt.mlp_in(w_g, w_u, bf16_tensor(a_bits), kernel=getattr(rt, kernel))
         check_close(to_f32(got), ref, bf16_out=True, label=f"mlp bf16 rows={rows}")
 
 
@@ -166,7 +212,7 @@ def _sampled_reference(w, a_bits, cols):
     sc = oracle.untile128(ts.view(np.uint8), n, g, 2).view(np.uint16).reshape(n, g)
     bi = oracle.untile128(tb.view(np.uint8), n, g, 2).view(np.uint16).reshape(n, g)
     dense = oracle.q4_dequant_rowmajor(words[cols], k // 8, sc[cols], bi[cols], len(cols), k)
-    return oracle.gemm_a_bf16_w_f32(a_bits, dense)
+    return oracle.gemm_a_bf16_w_f32(a_bits, dense), abs_gemm(a_bits, dense)
 
 
 @pytest.mark.parametrize("rows", [1, 64])
@@ -178,5 +224,19 @@ def test_baseline_shapes_sampled(rt, rows):
         a_bits = oracle.bf16_normal((rows, k), seed=rows)
         got = rt.gemm(w, bf16_tensor(a_bits))
         cols = np.sort(np.random.default_rng(rows).choice(n, 512, replace=False))
-        ref = _sampled_reference(w, a_bits, cols)
-        check_close(to_f32(got)[:, cols], ref, bf16_out=True, tight=True, label=f"{n}x{k} rows={rows}")
+        ref, absref = _sampled_reference(w, a_bits, cols)
+        check_close(to_f32(got)[:, cols], ref, bf16_out=True, tight=True, absref=absref, label=f"{n}x{k} rows={rows}")
+
+
+def test_prefill_shape_sampled(rt):
+    """Config 2 (M=2048 prefill, K=5120 -> N=17408) at full size through the tiled kernel:
+    256 sampled output columns of 512 sampled rows against the oracle."""
+    n, k, rows = 17408, 5120, 2048
+    w = _full_size_weight(rt, n, k, seed=7)
+    a_bits = oracle.bf16_normal((rows, k), seed=8)
+    got = to_f32(rt.gemm(w, bf16_tensor(a_bits)))
+    rng = np.random.default_rng(9)
+    cols = np.sort(rng.choice(n, 256, replace=False))
+    sel = np.sort(rng.choice(rows, 512, replace=False))
+    ref, absref = _sampled_reference(w, np.ascontiguousarray(a_bits[sel]), cols)
+    check_close(got[sel][:, cols], ref, bf16_out=True, tight=True, absref=absref, label="prefill")
