@@ -16,12 +16,11 @@
 //    permutation as the weights). The KW waves of a column slice split K by groups (wave kw takes
 //    every KW-th group) and the CW column slices of a workgroup share one activation chunk of KW
 //    groups, staged in LDS once per step: activations are read from L2 once per workgroup.
-//  * Weight codes and sidecars are loaded D steps ahead into a register ring (D groups per wave in
-//    flight); the activation chunk one step ahead (it is L2-resident), through registers into
-//    the other of two LDS buffers. One barrier per step.
-//  * The KW partial sums reduce through LDS by halving. When the shape has too few column blocks
-//    to give every CU a workgroup, gridDim.z workgroups split K further and write fp32 partials to
-//    the caller's workspace, summed in slice order by launch_splitk_finish.
+//  * Weight codes and sidecars are loaded D steps ahead into a register ring; the activation
+//    chunks D steps ahead by LDS DMA into D + 1 buffers. One barrier per step.
+//  * At the end of a job the KW partial sums meet in LDS and the workgroup writes whole output
+//    rows. Bands beyond a whole number per CU are split over all workgroups (stream-K) and their
+//    fp32 partials summed by q4_mma_finish.
 //
 // Numerics: w is the fp32 dequantized weight (one rounding, as DequantOracle.swift:20-21) rounded
 // to bf16 (RNE), products exact in fp32, fp32 accumulation.
@@ -272,10 +271,12 @@ q4_mma_kernel(MmaArgs args) {
 #pragma unroll
             for (int d = 0; d < D; ++d) {
                 const int t = t0 + d;
-                compute(t, d, abuf);
-                // Refill: chunk t + D into the buffer read in step t - 1, weights into slot t % D.
+                // Refill first, so the address units work while this step computes: chunk t + D
+                // into the buffer read in step t - 1, weights of step t + D into slot t % D (step
+                // t's weights there were dequantized in step t - 1).
                 issue_a(t + D, abuf == 0 ? S::kNB - 1 : abuf - 1);
                 load_w(d, t + D);
+                compute(t, d, abuf);
                 abuf = abuf == S::kNB - 1 ? 0 : abuf + 1;
                 wait_vmcnt<S::kChunkWait>();  // chunk t + 1 has landed
                 lds_barrier();
@@ -374,33 +375,59 @@ q4_mma_kernel(MmaArgs args) {
 }
 
 // Sums the stream-K partials of the remainder bands (see q4_mma_kernel) in workgroup order and
-// applies the epilogue. One thread per output of the remainder bands.
+// applies the epilogue. Block (rb, y) covers outputs [256 y, 256 y + 256) of remainder band rb;
+// its first thread lists the band's contributing workgroups once.
+constexpr int kFinishMaxContributors = 1024;
 __global__ void __launch_bounds__(256)
 q4_mma_finish(const float *__restrict__ partial, int nw, int band_cols, int dp_bands, int64_t sk_units, int P,
               int64_t groups, int64_t rows, int64_t n, void *out, int64_t ldc, int out_dtype, const void *residual) {
-    const int64_t per_band = rows * band_cols;
-    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int64_t rbands = sk_units / groups;
-    if (idx >= rbands * per_band) return;
-    const int64_t rb = idx / per_band, rem = idx % per_band;
-    const int64_t m = rem / band_cols, bc = rem % band_cols;
+    __shared__ int wg[kFinishMaxContributors];
+    __shared__ int slot_of[kFinishMaxContributors];
+    __shared__ int count;
+    const int64_t rb = blockIdx.x;
+    const int64_t lo = rb * groups, hi = lo + groups;  // the band's units
+    if (threadIdx.x == 0) {
+        // Workgroup i covers units [U i / P, U (i + 1) / P); the one holding unit u is
+        // floor(((u + 1) P - 1) / U). Ranges may be empty when there are fewer units than workgroups.
+        const int i_lo = (int)(((lo + 1) * P - 1) / sk_units), i_hi = (int)((hi * P - 1) / sk_units);
+        int c = 0;
+        for (int i = i_lo; i <= i_hi && c < kFinishMaxContributors; ++i) {
+            const int64_t s = sk_units * i / P, e = sk_units * (i + 1) / P;
+            if (s == e) continue;
+            wg[c] = i;
+            slot_of[c] = s < lo ? 1 : 0;
+            ++c;
+        }
+        count = c;
+    }
+    __syncthreads();
+    const int contributors = count;
+    if (contributors <= 1) return;  // one workgroup covered the band and wrote it
+    const int64_t idx = (int64_t)blockIdx.y * blockDim.x + threadIdx.x;
+    if (idx >= rows * band_cols) return;
+    const int64_t m = idx / band_cols, bc = idx % band_cols;
     const int64_t col = (int64_t)(dp_bands + rb) * band_cols + bc;
     if (col >= n) return;
-    const int64_t lo = rb * groups, hi = lo + groups;  // the band's units
-    // Workgroup i covers units [U i / P, U (i + 1) / P); the one holding unit u is
-    // floor(((u + 1) P - 1) / U); ranges may be empty when there are fewer units than workgroups.
-    const int i_lo = (int)(((lo + 1) * P - 1) / sk_units), i_hi = (int)((hi * P - 1) / sk_units);
+    // Loads in batches of eight so that their latencies overlap; the sum stays in order.
     float v[2] = {0.0f, 0.0f};
-    int contributors = 0;
-    for (int i = i_lo; i <= i_hi; ++i) {
-        const int64_t s = sk_units * i / P, e = sk_units * (i + 1) / P;
-        if (s == e) continue;  // an empty range wrote nothing
-        const int slot = s < lo ? 1 : 0;
-        const float *src = partial + ((int64_t)(i * 2 + slot) * nw * rows + m) * band_cols + bc;
-        for (int w = 0; w < nw; ++w) v[w] += src[(int64_t)w * rows * band_cols];
-        ++contributors;
+    const int64_t wstride = rows * band_cols;
+    for (int j0 = 0; j0 < contributors; j0 += 8) {
+        float x[8][2];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int jj = j0 + j < contributors ? j0 + j : contributors - 1;
+            const float *src = partial + ((int64_t)(wg[jj] * 2 + slot_of[jj]) * nw * rows + m) * band_cols + bc;
+            x[j][0] = src[0];
+            x[j][1] = nw == 2 ? src[wstride] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (j0 + j < contributors) {
+                v[0] += x[j][0];
+                v[1] += x[j][1];
+            }
+        }
     }
-    if (contributors <= 1) return;  // one workgroup covered the band and wrote it
     float value = nw == 2 ? silu(v[0]) * v[1] : v[0];
     const int64_t index = m * ldc + col;
     if (out_dtype == SPLOSH_F32) {
@@ -449,6 +476,7 @@ MmaPlan plan_mma(int64_t rows, int64_t columns, int64_t groups, bool mlp, size_t
     p.bands = (int)((columns + kMmaCW * 32 - 1) / (kMmaCW * 32));
     int grid = device_cus();
     if (const char *env = getenv("SPLOSH_MMA_GRID")) grid = atoi(env) > 0 ? atoi(env) : grid;
+    grid = grid < kFinishMaxContributors ? grid : kFinishMaxContributors;  // q4_mma_finish's list
     p.grid = grid;
     p.dp_bands = (p.bands / grid) * grid;
     p.sk_units = (int64_t)(p.bands - p.dp_bands) * groups;
@@ -519,8 +547,9 @@ hipError_t launch_q4_mma(const MmaPlan &plan, const splosh_q4_weight &w, const s
     else
         err = tiled ? launch_mma_fm<1, true>(plan, args, stream) : launch_mma_fm<1, false>(plan, args, stream);
     if (err != hipSuccess || plan.sk_units == 0) return err;
-    const int64_t total = (plan.sk_units / groups) * rows * (kMmaCW * 32);
-    hipLaunchKernelGGL(q4_mma_finish, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream,
+    const int64_t per_band = rows * (kMmaCW * 32);
+    hipLaunchKernelGGL(q4_mma_finish, dim3((unsigned)(plan.sk_units / groups), (unsigned)((per_band + 255) / 256)),
+                       dim3(256), 0, stream,
                        (const float *)workspace, up ? 2 : 1, kMmaCW * 32, plan.dp_bands, plan.sk_units, plan.grid, groups,
                        rows, w.rows, out, ldc, out_dtype, residual);
     return hipGetLastError();
