@@ -28,9 +28,15 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
 
-# HBM bytes per launch of the dominant kernel measured with rocprofv3 --pmc (FETCH_SIZE and
-# WRITE_SIZE, scaled by a plain copy kernel), keyed by workload; None until measured.
-MEASURED_TRAFFIC = {}
+# HBM bytes per launch of the dominant kernel measured with rocprofv3 --pmc, keyed by (workload,
+# call): FETCH_SIZE x 2 + WRITE_SIZE (KiB x 1024), the factors being what the two counters read for
+# a plain 256 MiB device copy (FETCH_SIZE reads half the bytes moved, WRITE_SIZE all of them).
+# The readings and commands are in profiles/; calls not listed are unmeasured (None).
+MEASURED_TRAFFIC = {
+    ("verify64", "mlp_in"): 52988.3 * 2 * 1024 + 11264.0 * 1024,   # q4_mma_kernel<2, 2, ...>
+    ("verify64", "down"): 30676.4 * 2 * 1024 + 5120.0 * 1024,      # q4_mma_kernel<2, 1, ...>
+    ("decode1", "gemv"): 24605.8 * 2 * 1024 + 34.0 * 1024,         # q4_lane_kernel<1, 1, ...>
+}
 
 
 def q4_bytes(n, k):
@@ -86,21 +92,30 @@ def build_workload(name, rt, torch, gen, kernel):
         return torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
 
     if name == "prefill2048":
-        m, k, n = 2048, 5120, 17408
-        ncopy = copies_for(q4_bytes(n, k), minimum=0.5e9)
-        ws = [make_q4(rt, n, k, gen) for _ in range(ncopy)]
-        x = torch.randn(m, k, device="cuda", generator=gen).to(torch.bfloat16)
-        out = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
-        scratch = workspace(m, n, k)
-        b = q4_bytes(n, k) + m * k * 2 + m * n * 2
+        # Config 2: both prefill shapes, K=5120 -> N=17408 (up) and K=17408 -> N=5120 (down).
+        m = 2048
+        shapes = (("prefill_up", 17408, 5120), ("prefill_down", 5120, 17408))
+        mats, xs, outs, scratch = {}, {}, {}, {}
+        for nm, n, k in shapes:
+            ncopy = copies_for(q4_bytes(n, k), minimum=0.5e9)
+            mats[nm] = [make_q4(rt, n, k, gen) for _ in range(ncopy)]
+            xs[nm] = torch.randn(m, k, device="cuda", generator=gen).to(torch.bfloat16)
+            outs[nm] = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+            scratch[nm] = workspace(m, n, k)
 
         def launches(i):
-            w = ws[i % ncopy]
-            return [("prefill", lambda: rt.gemm(w, x, out=out, kernel=kernel, workspace=scratch))]
+            calls = []
+            for nm, _, _ in shapes:
+                w = mats[nm][i % len(mats[nm])]
+                calls.append((nm, lambda w=w, nm=nm: rt.gemm(w, xs[nm], out=outs[nm], kernel=kernel,
+                                                             workspace=scratch[nm])))
+            return calls
 
-        cfg = {"workload": "prefill GEMM M=2048 K5120->N17408", "rows": m, "format": "mlx affine q4 g64, tiled128",
-               "weight_copies": ncopy}
-        return launches, b, 2 * m * n * k, {"prefill": b}, cfg
+        kb = {nm: q4_bytes(n, k) + m * k * 2 + m * n * 2 for nm, n, k in shapes}
+        kf = {nm: 2 * m * n * k for nm, n, k in shapes}
+        cfg = {"workload": "prefill M=2048: K5120->N17408 and K17408->N5120", "rows": m,
+               "format": "mlx affine q4 g64, tiled128", "weight_copies": {nm: len(v) for nm, v in mats.items()}}
+        return launches, sum(kb.values()), sum(kf.values()), kb, cfg, kf
     if name == "verify64":
         m, h, inter = 64, 5120, 17408
         one = 2 * q4_bytes(inter, h) + q4_bytes(h, inter)
@@ -122,7 +137,7 @@ def build_workload(name, rt, torch, gen, kernel):
         cfg = {"workload": "draft-verify step: fused gate+up (2x K5120->N17408) + down (K17408->N5120)",
                "rows": m, "format": "mlx affine q4 g64, tiled128", "weight_copies": ncopy}
         return launches, gate_up_bytes + down_bytes, 2 * m * (2 * inter * h + h * inter), \
-            {"mlp_in": gate_up_bytes, "down": down_bytes}, cfg
+            {"mlp_in": gate_up_bytes, "down": down_bytes}, cfg, {"mlp_in": 4 * m * inter * h, "down": 2 * m * h * inter}
     if name == "decode1":
         m, k, n = 1, 5120, 17408
         ncopy = copies_for(q4_bytes(n, k))
@@ -137,7 +152,7 @@ def build_workload(name, rt, torch, gen, kernel):
 
         cfg = {"workload": "decode GEMV K5120->N17408", "rows": 1, "format": "mlx affine q4 g64, tiled128",
                "weight_copies": ncopy}
-        return launches, b, 2 * m * n * k, {"gemv": b}, cfg
+        return launches, b, 2 * m * n * k, {"gemv": b}, cfg, {"gemv": 2 * m * n * k}
     if name.startswith("q5k"):
         m = int(name[3:] or 64)
         k, n = 17408, 5120
@@ -154,7 +169,7 @@ def build_workload(name, rt, torch, gen, kernel):
 
         cfg = {"workload": f"Q5_K down K17408->N5120", "rows": m, "format": "gguf q5_k planes",
                "weight_copies": ncopy}
-        return launches, b, 2 * m * n * k, {"q5k": b}, cfg
+        return launches, b, 2 * m * n * k, {"q5k": b}, cfg, {"q5k": 2 * m * n * k}
     raise SystemExit(f"unknown workload {name}")
 
 
@@ -172,7 +187,7 @@ def cpu_baseline(workload, seconds=8.0):
         mats = [(17408, 5120)]
         m = 1
     elif workload == "prefill2048":
-        mats = [(17408, 5120)]
+        mats = [(17408, 5120), (5120, 17408)]
         m = 2048
     else:
         return None
@@ -210,8 +225,22 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="verify64")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--eager", action="store_true", help="launch from the host every step (no HIP graph)")
     ap.add_argument("--kernel", default="AUTO", choices=["AUTO", "STREAM", "DEQUANT", "TILE", "SCALAR"])
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB ten times (the reference kernel for "
+                         "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings) and exit")
     args = ap.parse_args()
+    if args.copy_calibration:
+        import torch
+        n = args.copy_calibration << 20
+        src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": n, "launches": 10}))
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU's share of the path; --gpus {args.gpus} is not supported "
               "(the multi-GPU design is sharding along N, described in DESIGN.md)", file=sys.stderr)
@@ -221,45 +250,75 @@ def main():
     from splosh_amd import runtime as rt
 
     gen = torch.Generator(device="cuda").manual_seed(0x5EED0001)
-    launches, step_bytes, step_flops, kernel_bytes, cfg = build_workload(args.workload, rt, torch, gen,
+    launches, step_bytes, step_flops, kernel_bytes, cfg, kernel_flops = build_workload(args.workload, rt, torch, gen,
                                                                                getattr(rt, args.kernel))
     timer = Timer()
+    names = [nm for nm, _ in launches(0)]
     torch.cuda.synchronize()
     for i in range(args.warmup):
         for _, fn in launches(i):
             fn()
     torch.cuda.synchronize()
 
-    names = [nm for nm, _ in launches(0)]
-    events = []
-    start = timer.event()
-    for i in range(args.steps):
-        evs = [timer.event()]
-        for _, fn in launches(args.warmup + i):
-            fn()
-            evs.append(timer.event())
-        events.append(evs)
-    end = timer.event()
-    torch.cuda.synchronize()
-    total_ms = start.elapsed_time(end)
+    if args.eager:
+        # Host-launched: includes the Python/ctypes call overhead between launches.
+        events = []
+        start = timer.event()
+        for i in range(args.steps):
+            evs = [timer.event()]
+            for _, fn in launches(args.warmup + i):
+                fn()
+                evs.append(timer.event())
+            events.append(evs)
+        end = timer.event()
+        torch.cuda.synchronize()
+        total_ms = start.elapsed_time(end)
+        per_kernel = {nm: sum(evs[j].elapsed_time(evs[j + 1]) for evs in events) / args.steps
+                      for j, nm in enumerate(names)}
+    else:
+        # The K steps are captured once into a HIP graph (as a serving loop replays a layer) and the
+        # timed region is one replay of it: GPU time without host launch gaps. Each kernel's own
+        # time comes from a graph of its K launches alone, replayed the same way.
+        def capture(kinds):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for i in range(args.steps):
+                    for nm, fn in launches(args.warmup + i):
+                        if nm in kinds:
+                            fn()
+            return g
+
+        def replay_ms(g):
+            g.replay()  # warm replay
+            torch.cuda.synchronize()
+            start, end = timer.event(), None
+            g.replay()
+            end = timer.event()
+            torch.cuda.synchronize()
+            return start.elapsed_time(end)
+
+        g_all = capture(set(names))
+        total_ms = replay_ms(g_all)
+        per_kernel = {nm: replay_ms(capture({nm})) / args.steps for nm in names}
     ms_per_step = total_ms / args.steps
-    per_kernel = {nm: sum(evs[j].elapsed_time(evs[j + 1]) for evs in events) / args.steps
-                  for j, nm in enumerate(names)}
 
     dominant = max(per_kernel, key=per_kernel.get)
     dom_ms = per_kernel[dominant]
     compute_bound = args.workload == "prefill2048"
+    traffic = MEASURED_TRAFFIC.get((args.workload, dominant))
+    traffic = int(traffic) if traffic is not None else None
     if compute_bound:
-        achieved = step_flops / (dom_ms * 1e-3) / 1e12
+        achieved = kernel_flops[dominant] / (dom_ms * 1e-3) / 1e12
         roofline = {"bound": "mfma", "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS,
                     "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
-                    "traffic": MEASURED_TRAFFIC.get(args.workload), "kernel": dominant,
-                    "kernel_us": round(dom_ms * 1e3, 2), "algorithmic_flops": step_flops}
+                    "traffic": traffic, "kernel": dominant,
+                    "kernel_us": round(dom_ms * 1e3, 2), "algorithmic_flops": kernel_flops[dominant]}
         value, unit = step_flops / (ms_per_step * 1e-3) / 1e12, "TFLOP/s"
     else:
         achieved = kernel_bytes[dominant] / (dom_ms * 1e-3) / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": MEASURED_TRAFFIC.get(args.workload),
+                    "frac": round(achieved / HBM_PEAK_GBS, 4),
+                    "traffic": traffic,
                     "kernel": dominant, "kernel_us": round(dom_ms * 1e3, 2),
                     "algorithmic_bytes": kernel_bytes[dominant]}
         value, unit = step_bytes / (ms_per_step * 1e-3) / 1e12, "TB/s"
@@ -274,6 +333,7 @@ def main():
         "tflops": round(step_flops / (ms_per_step * 1e-3) / 1e12, 1),
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "launch": "eager" if args.eager else "hip graph of the K steps, one replay timed",
     }
     print(json.dumps(result))
 
