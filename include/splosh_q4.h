@@ -64,9 +64,11 @@ typedef enum splosh_dtype { SPLOSH_F32 = 0, SPLOSH_BF16 = 1 } splosh_dtype;
 /* Kernel choice (the reference selects kernels through SPLOSH_* environment variables,
  * Runtime/Engine.swift:380-440; here the caller names one, or AUTO picks by rows). */
 typedef enum splosh_kernel {
-    SPLOSH_KERNEL_AUTO = 0,
-    SPLOSH_KERNEL_STREAM = 1,   /* rows <= 64: weight-streaming MFMA kernel on raw codes */
-    SPLOSH_KERNEL_DEQUANT = 2,  /* rows <= 64: weight-streaming MFMA kernel on dequantized bf16 */
+    SPLOSH_KERNEL_AUTO = 0,     /* rows <= 2: STREAM; 3..64: DEQUANT; more: TILE; else SCALAR */
+    SPLOSH_KERNEL_STREAM = 1,   /* weight streaming on raw codes: lane-per-row VALU kernel for
+                                   1-2 rows, raw-code MFMA kernels above */
+    SPLOSH_KERNEL_DEQUANT = 2,  /* rows <= 64: stream-K MFMA kernel on weights dequantized to bf16 in
+                                   registers; uses the workspace for split bands when given one */
     SPLOSH_KERNEL_TILE = 3,     /* any rows: LDS-tiled dequant-to-bf16 MFMA GEMM (prefill) */
     SPLOSH_KERNEL_SCALAR = 4    /* one thread per output (gemm_q4.metal semantics) */
 } splosh_kernel;
@@ -121,8 +123,12 @@ int splosh_q4_layout_sidecar_index(const splosh_q4_layout *layout, int64_t row, 
 /* GemmQ4Shape.init + validate(layout:) (Model/Gemm.swift:13-40). */
 int splosh_q4_shape_validate(int64_t rows, int64_t columns, int64_t inner, const splosh_q4_layout *layout);
 
-/* Scratch bytes the GEMM entry points need for `rows` x `columns` x `inner` (0 when none). The
- * reference's engine owns its scratch (Runtime/Engine.swift:460-486); here the caller does. */
+/* Scratch bytes the GEMM entry points can use for `rows` x `columns` x `inner` (0 when none): fp32
+ * partial sums of output bands whose K is split across workgroups. The reference's engine owns
+ * its scratch (Runtime/Engine.swift:460-486); here the caller does, and the library allocates
+ * nothing. Without a workspace (or with a smaller one) the kernels do not split K: the results
+ * agree up to the fp32 summation order, with less parallelism. Calls that share one workspace
+ * must be ordered on one stream. */
 size_t splosh_workspace_bytes(int64_t rows, int64_t columns, int64_t inner);
 
 const char *splosh_status_string(int status);

@@ -243,3 +243,21 @@ def test_q5k_splitmix_generator_matches_reference_shape(oracle):
     assert np.all((np.abs(d) >= 0.75e-4 * 0.999) & (np.abs(d) <= 1.25e-4 * 1.001))
     vals = oracle.q45k_decode(nat)
     assert np.all(np.isfinite(vals))
+
+
+@pytest.mark.parametrize("fifth", [True, False])
+def test_q45k_fused_gemm_equals_decode_then_gemm(oracle, fifth):
+    """The fused Q4_K/Q5_K GEMM (decode a block row on the fly) against the composition of the two
+    separately pinned steps: golden-pinned block decode, then the fp32 sequential-k GEMM. Both sum
+    in the same k order, so the results are bit-identical; a wrong block or column index would not be."""
+    n, k, rows = 6, 512, 3
+    nat = oracle.q45k_random_native_splitmix(n, k, seed=0x6600 + (1 if fifth else 2))
+    if not fifth:  # a Q4_K block is the Q5_K block without the 32-byte fifth-bit plane
+        nat = np.concatenate([b[:16].tolist() + b[48:].tolist() for b in nat.reshape(-1, 176)]).astype(np.uint8)
+    dense = oracle.q45k_decode(nat, fifth_bit=fifth).reshape(n, k)
+    a = oracle.bf16_normal((rows, k), seed=5)
+    want = oracle.gemm_a_bf16_w_f32(a, dense)
+    got = oracle.q45k_gemm_native(a, nat, n, k, fifth_bit=fifth)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    part = oracle.q45k_gemm_native(a, nat, n, k, fifth_bit=fifth, n0=2, n1=5)
+    assert np.array_equal(part[:, 2:5], want[:, 2:5]) and np.all(np.isnan(part[:, :2]))
