@@ -65,13 +65,6 @@ __device__ __forceinline__ uint32_t buffer_load_u16(rsrc_t r, uint32_t voffset, 
     return __builtin_amdgcn_raw_buffer_load_b16(r, (int)voffset, (int)soffset, 0);
 }
 
-// 16 bytes a lane from the buffer at voffset + soffset straight into LDS, without registers: lane l
-// writes bytes [lds_base + 16 l, + 16). lds_base must be wave-uniform. Counted by vmcnt.
-__device__ __forceinline__ void buffer_load16_lds(rsrc_t r, void *lds_base, uint32_t voffset, uint32_t soffset) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds_base, 16, (int)voffset,
-                                             (int)soffset, 0, 0);
-}
-
 // Workgroup barrier for LDS hand-offs only: waits for this wave's LDS operations, not for its
 // outstanding global loads (which __syncthreads' fence would drain), so prefetches stay in flight.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }

@@ -16,8 +16,9 @@
 //    permutation as the weights). The KW waves of a column slice split K by groups (wave kw takes
 //    every KW-th group) and the CW column slices of a workgroup share one activation chunk of KW
 //    groups, staged in LDS once per step: activations are read from L2 once per workgroup.
-//  * Weight codes and sidecars are loaded D steps ahead into a register ring; the activation
-//    chunks D steps ahead by LDS DMA into D + 1 buffers. One barrier per step.
+//  * Weight codes and sidecars are loaded three steps ahead into a register ring; the
+//    activation chunk one step ahead into registers, then stored to one of three LDS buffers.
+//    One barrier per step, in its middle.
 //  * At the end of a job the KW partial sums meet in LDS and the workgroup writes whole output
 //    rows. Bands beyond a whole number per CU are split over all workgroups (stream-K) and their
 //    fp32 partials summed by q4_mma_finish.
@@ -80,19 +81,15 @@ struct MmaShape {
     static constexpr int kKc = KW * 8;                             // 16-byte pieces per chunk row
     static constexpr int kAPieces = kRows * kKc;
     static_assert(kAPieces % kThreads == 0, "whole activation pieces per thread");
-    static constexpr int kAPer = kAPieces / kThreads;              // LDS-DMA loads per wave and step
+    static constexpr int kAPer = kAPieces / kThreads;              // activation loads per wave and step
     static constexpr int kABuf = kAPieces * 16;                    // bytes of one chunk buffer
-    static constexpr int kNB = D + 1;                              // chunk buffers
+    static constexpr int kNB = 3;                                  // chunk buffers
     static constexpr int kAcc = FM * NW * 16;                      // accumulator floats per lane
     static constexpr size_t kRedBytes = (size_t)KW * CW * kAcc * 64 * sizeof(float);
     static constexpr size_t kABytes = (size_t)kNB * kABuf;
     static constexpr size_t kLds = kRedBytes > kABytes ? kRedBytes : kABytes;
     static constexpr int kWLoads = NW * 3;                         // weight loads per wave and step
-    // Loads a wave issues after step s's activation chunk up to the end of step s + D - 1, when
-    // that chunk must have landed: the rest of step s (its weights) and D - 1 further steps.
-    static constexpr int kChunkWait = kWLoads + (D - 1) * (kAPer + kWLoads);
-    static_assert(kChunkWait < 64, "vmcnt range");
-    static_assert(D >= 2 && D <= 5, "the final steps' waits are written out for D <= 5");
+    static_assert(D == 3, "the pipeline below is written for weights three steps ahead");
 };
 
 // s_waitcnt with only vmcnt bounded (expcnt and lgkmcnt left at their maxima), gfx9 encoding.
@@ -137,10 +134,11 @@ q4_mma_kernel(MmaArgs args) {
         s_rsrc[w] = make_rsrc(args.scales[w], args.sidecar_bytes);
         b_rsrc[w] = make_rsrc(args.biases[w], args.sidecar_bytes);
     }
-    // LDS-DMA source of this lane's pieces: load j of the wave fills buffer positions
-    // (wave * kAPer + j) * 64 + lane, i.e. row m = pos / kKc and piece kc = (pos % kKc) ^ (m & 7),
-    // at byte (m lda + 64 g + 8 kc) * 2. Rows past the last are clamped (their outputs are not
-    // stored); groups past the job belong to inactive waves; reads past the buffer return zero.
+    // Activation staging: this thread's piece j of a chunk sits at buffer position
+    // (wave * kAPer + j) * 64 + lane, i.e. row m = pos / kKc, holding piece kc = (pos % kKc) ^ (m & 7)
+    // of the row (an XOR swizzle, so the MFMA operand reads do not conflict), read from byte
+    // (m lda + 64 g + 8 kc) * 2. Rows past the last are clamped (their outputs are not stored);
+    // groups past the job belong to inactive waves; reads past the buffer return zero.
     uint32_t a_src[S::kAPer];
 #pragma unroll
     for (int j = 0; j < S::kAPer; ++j) {
@@ -174,11 +172,16 @@ q4_mma_kernel(MmaArgs args) {
             side_group = 2u;
         }
 
-        auto issue_a = [&](int t, int buf) {
+        u32x4 ar[S::kAPer];  // the next chunk's pieces, on their way to LDS
+        auto load_a = [&](int t) {
             const uint32_t gbyte = (uint32_t)(ga + t * KW) * 128u;
 #pragma unroll
+            for (int j = 0; j < S::kAPer; ++j) ar[j] = buffer_load16(a_rsrc, a_src[j] + gbyte, 0);
+        };
+        auto store_a = [&](int buf) {
+#pragma unroll
             for (int j = 0; j < S::kAPer; ++j)
-                buffer_load16_lds(a_rsrc, lds_bytes + buf * S::kABuf + (wave * S::kAPer + j) * 1024, a_src[j] + gbyte, 0);
+                *(u32x4 *)(lds_bytes + buf * S::kABuf + ((wave * S::kAPer + j) * 64 + lane) * 16) = ar[j];
         };
         // Weight ring: step t's codes and sidecars in slot t % D; the group is a wave-uniform
         // offset, clamped into the job so it stays in bounds.
@@ -215,90 +218,98 @@ q4_mma_kernel(MmaArgs args) {
 #pragma unroll
                 for (int e = 0; e < 16; ++e) acc[w][f][e] = 0.0f;
 
-        // The step count is padded to a multiple of D: steps past T compute nothing but keep the
-        // load pattern regular (their loads re-read in-bounds data). Every step but the last D
-        // issues the loads of step t + D, so the chunk needed next is waited for with a fixed vmcnt
-        // that leaves the younger D - 1 steps of loads in flight; the last D steps issue nothing
-        // and wait for exactly what they need.
+        // The step count is padded to a multiple of 3: steps past T compute nothing but keep the
+        // load pattern regular (their loads re-read in-bounds data). Each step has its barrier in
+        // the middle, between MFMA sub-steps 1 and 2. There the wave waits for its pieces of the
+        // next step's chunk (loaded a step earlier), stores them to LDS, passes the barrier, reads
+        // the next step's first activation fragments and issues the loads of chunk t + 2 and of
+        // the weights of step t + 3. Loads return in order, so "chunk t + 1 has arrived" is
+        // "at most the weight loads issued after it are outstanding". The chunk buffer written
+        // (t + 1 mod 3) last held chunk t - 2, which every wave finished before the previous
+        // barrier. LDS latency and the barrier hide behind sub-steps 2 and 3.
         const int Tp = (T + D - 1) / D * D;
-#pragma unroll
-        for (int d = 0; d < D; ++d) {
-            issue_a(d, d);
-            load_w(d, d);
-        }
-        wait_vmcnt<S::kChunkWait>();
-        dequant(0);
+        load_a(0);
+        load_w(0, 0);
+        load_w(1, 1);
+        wait_vmcnt<2 * S::kWLoads>();
+        store_a(0);
+        load_a(1);
+        load_w(2, 2);
         lds_barrier();
+        dequant(0);
+        auto read_af = [&](bf16x8 *dst, int buf, int i) {
+            const char *ap = lds_bytes + buf * S::kABuf;
+#pragma unroll
+            for (int f = 0; f < FM; ++f) dst[f] = as_bf16x8(*(const u32x4 *)(ap + a_rd[i] + f * 32 * S::kKc * 16));
+        };
+        bf16x8 af_pre[FM];  // sub-step 0 fragments of the current step
+        read_af(af_pre, 0, 0);
 
-        // Step t: the MFMAs of step t with the dequantization of step t + 1 interleaved (only the
-        // dequantization when the wave has no group in step t).
-        auto compute = [&](int t, int d, int abuf) {
+        // Step t: MFMA sub-steps with the dequantization of step t + 1 interleaved, `mid` between
+        // sub-steps 1 and 2. Inactive waves (no group in step t) only dequantize.
+        auto step = [&](int t, int d, int abuf, auto &&mid) {
             const int next = (d + 1) % D;
-            const char *ap = lds_bytes + abuf * S::kABuf;
-            if (t < T && ga + t * KW + kw < gb) {
-                float sn[NW], bn[NW];
+            const bool active = t < T && ga + t * KW + kw < gb;
+            float sn[NW], bn[NW];
 #pragma unroll
-                for (int w = 0; w < NW; ++w) {
-                    sn[w] = bf16_bits_to_f32(wsc[next][w]);
-                    bn[w] = bf16_bits_to_f32(wbi[next][w]);
-                }
+            for (int w = 0; w < NW; ++w) {
+                sn[w] = bf16_bits_to_f32(wsc[next][w]);
+                bn[w] = bf16_bits_to_f32(wbi[next][w]);
+            }
+            bf16x8 af[2][FM];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    bf16x8 af[FM];
+            for (int f = 0; f < FM; ++f) af[0][f] = af_pre[f];
 #pragma unroll
-                    for (int f = 0; f < FM; ++f) af[f] = as_bf16x8(*(const u32x4 *)(ap + a_rd[i] + f * 32 * S::kKc * 16));
+            for (int i = 0; i < 4; ++i) {
+                if (i == 2) mid();
+                if (i < 3) read_af(af[(i + 1) & 1], abuf, i + 1);
+                if (active) {
 #pragma unroll
                     for (int w = 0; w < NW; ++w)
 #pragma unroll
                         for (int f = 0; f < FM; ++f)
-                            acc[w][f] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[f], bw[w][i], acc[w][f], 0, 0, 0);
-#pragma unroll
-                    for (int w = 0; w < NW; ++w) bw[w][i] = dequant_word(wq[next][w][i], sn[w], bn[w]);
-                    __builtin_amdgcn_sched_group_barrier(0x100, FM, 0);  // this sub-step's LDS reads
-#pragma unroll
-                    for (int j = 0; j < NW * FM; ++j) {
-                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);        // one MFMA
-                        __builtin_amdgcn_sched_group_barrier(0x002, 22 / FM, 0);  // dequant VALU
-                    }
+                            acc[w][f] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i & 1][f], bw[w][i], acc[w][f], 0, 0, 0);
                 }
-            } else {
-                dequant(next);
+#pragma unroll
+                for (int w = 0; w < NW; ++w) bw[w][i] = dequant_word(wq[next][w][i], sn[w], bn[w]);
             }
         };
 
         int abuf = 0;  // buffer of step t's chunk
+        auto nbuf = [&](int b) { return b == S::kNB - 1 ? 0 : b + 1; };
         for (int t0 = 0; t0 < Tp - D; t0 += D) {
 #pragma unroll
             for (int d = 0; d < D; ++d) {
                 const int t = t0 + d;
-                // Refill first, so the address units work while this step computes: chunk t + D
-                // into the buffer read in step t - 1, weights of step t + D into slot t % D (step
-                // t's weights there were dequantized in step t - 1).
-                issue_a(t + D, abuf == 0 ? S::kNB - 1 : abuf - 1);
-                load_w(d, t + D);
-                compute(t, d, abuf);
-                abuf = abuf == S::kNB - 1 ? 0 : abuf + 1;
-                wait_vmcnt<S::kChunkWait>();  // chunk t + 1 has landed
-                lds_barrier();
+                step(t, d, abuf, [&] {
+                    wait_vmcnt<S::kWLoads>();  // chunk t + 1 has arrived (weights t + 2 may not)
+                    store_a(nbuf(abuf));
+                    lds_barrier();
+                    read_af(af_pre, nbuf(abuf), 0);
+                    load_a(t + 2);
+                    load_w(d, t + D);
+                });
+                abuf = nbuf(abuf);
             }
         }
-        // The last D steps: in step Tp - D + d the loads of the D - 2 - d younger steps may stay in
-        // flight; the last step drains.
+        // The last three steps: chunk Tp - 1 is loaded in the first of them, no weights after.
 #pragma unroll
         for (int d = 0; d < D; ++d) {
-            compute(Tp - D + d, d, abuf);
-            abuf = abuf == S::kNB - 1 ? 0 : abuf + 1;
-            if (d == D - 1) {
-                wait_vmcnt<0>();
-            } else if (d == D - 2) {
-                wait_vmcnt<S::kWLoads>();
-            } else if (d == D - 3) {
-                wait_vmcnt<S::kWLoads + (S::kAPer + S::kWLoads)>();
-            } else {
-                wait_vmcnt<S::kWLoads + 2 * (S::kAPer + S::kWLoads)>();
-            }
-            lds_barrier();
+            const int t = Tp - D + d;
+            step(t, d, abuf, [&] {
+                if (d == 0) {
+                    wait_vmcnt<S::kWLoads>();
+                } else {
+                    wait_vmcnt<0>();
+                }
+                if (d < 2) store_a(nbuf(abuf));
+                lds_barrier();
+                if (d < 2) read_af(af_pre, nbuf(abuf), 0);
+                if (d == 0) load_a(t + 2);
+            });
+            abuf = nbuf(abuf);
         }
+        lds_barrier();  // every wave is past its last fragment read
         // No load is in flight now; the last barrier also ended every read of the chunk buffers.
 
         // Every wave parks its partial sums in LDS (element e of block f of weight w at
@@ -441,9 +452,9 @@ q4_mma_finish(const float *__restrict__ partial, int nw, int band_cols, int dp_b
 
 constexpr int kMmaCW = 2, kMmaKW = 4;
 
-// Pipeline depth: chunk buffers take (D + 1) x rows x 512 bytes of LDS.
+// Weight ring depth (steps the weight loads run ahead).
 template <int FM>
-constexpr int mma_depth() { return FM == 2 ? 3 : 4; }
+constexpr int mma_depth() { return 3; }
 
 // Activation and code offsets are 32-bit; 64 rows at most.
 bool mma_fits(int64_t rows, int64_t columns, int64_t inner, int64_t stride_words, int64_t lda) {
