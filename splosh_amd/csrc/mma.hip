@@ -83,12 +83,16 @@ struct MmaShape {
     static_assert(kAPieces % kThreads == 0, "whole activation pieces per thread");
     static constexpr int kAPer = kAPieces / kThreads;              // activation loads per wave and step
     static constexpr int kABuf = kAPieces * 16;                    // bytes of one chunk buffer
+    // Tiled weights: a step's sidecars for the band (NW weights x {scale, bias} x KW groups x
+    // kBandCols columns of bf16) go through LDS too, loaded by waves 0 .. 2 NW - 1 (32 lanes x
+    // 16 bytes each: the 4 groups x 128 bytes of one array of one weight).
+    static constexpr int kSBuf = NW * 2 * KW * kBandCols * 2;
     static constexpr int kNB = 3;                                  // chunk buffers
     static constexpr int kAcc = FM * NW * 16;                      // accumulator floats per lane
     static constexpr size_t kRedBytes = (size_t)KW * CW * kAcc * 64 * sizeof(float);
-    static constexpr size_t kABytes = (size_t)kNB * kABuf;
+    static constexpr size_t kABytes = (size_t)kNB * (kABuf + kSBuf);
     static constexpr size_t kLds = kRedBytes > kABytes ? kRedBytes : kABytes;
-    static constexpr int kWLoads = NW * 3;                         // weight loads per wave and step
+    static_assert(KW * (kBandCols * 2 / 16) <= 64, "one wave-wide load covers an array's step");
     static_assert(D == 3, "the pipeline below is written for weights three steps ahead");
 };
 
@@ -117,6 +121,10 @@ template <int FM, int NW, bool TILED, int CW, int KW, int D>
 __global__ void __launch_bounds__(CW * KW * 64)
 q4_mma_kernel(MmaArgs args) {
     using S = MmaShape<FM, NW, CW, KW, D>;
+    // Sidecars: staged through LDS for the tiled layout (a band's are contiguous there); loaded
+    // per wave with the codes for row-major weights.
+    constexpr bool kStageSide = TILED;
+    constexpr int kWLoads = kStageSide ? NW : NW * 3;  // weight loads per wave and step
     extern __shared__ __align__(16) uint16_t lds[];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -134,6 +142,10 @@ q4_mma_kernel(MmaArgs args) {
         s_rsrc[w] = make_rsrc(args.scales[w], args.sidecar_bytes);
         b_rsrc[w] = make_rsrc(args.biases[w], args.sidecar_bytes);
     }
+    // The sidecar array this wave stages (waves 0 .. 2 NW - 1): weight wave / 2, bias if odd.
+    const int side_w = (wave >> 1) < NW ? (wave >> 1) : 0;
+    const rsrc_t side_rsrc =
+        make_rsrc((wave & 1) ? (const void *)args.biases[side_w] : (const void *)args.scales[side_w], args.sidecar_bytes);
     // Activation staging: this thread's piece j of a chunk sits at buffer position
     // (wave * kAPer + j) * 64 + lane, i.e. row m = pos / kKc, holding piece kc = (pos % kKc) ^ (m & 7)
     // of the row (an XOR swizzle, so the MFMA operand reads do not conflict), read from byte
@@ -183,6 +195,31 @@ q4_mma_kernel(MmaArgs args) {
             for (int j = 0; j < S::kAPer; ++j)
                 *(u32x4 *)(lds_bytes + buf * S::kABuf + ((wave * S::kAPer + j) * 64 + lane) * 16) = ar[j];
         };
+        // Staged sidecars: wave v < 2 NW loads array (v & 1 ? bias : scale) of weight v >> 1 for the
+        // step's KW groups: lane l < 8 KW takes group l >> 3, bytes 16 (l & 7) .. of the band's
+        // 128-byte run (groups past the job re-read the last one). LDS layout per buffer:
+        // [weight][array][group][column] bf16.
+        char *side_lds = lds_bytes + S::kNB * S::kABuf;
+        const bool side_loader = kStageSide && wave < 2 * NW && lane < 8 * KW;
+        uint32_t side_src = 0;
+        if (kStageSide) {
+            const uint32_t n0 = (uint32_t)band * S::kBandCols;
+            side_src = (((n0 >> 7) * G32 * 128u + (n0 & 127u)) * 2u) + 16u * (lane & 7);
+        }
+        u32x4 sr = {0u, 0u, 0u, 0u};
+        auto load_s = [&](int t) {
+            if (!side_loader) return;
+            int g = ga + t * KW + (lane >> 3);
+            g = g < gb ? g : gb - 1;
+            sr = buffer_load16(side_rsrc, side_src + (uint32_t)g * 256u, 0);
+        };
+        auto store_s = [&](int buf) {
+            if (side_loader) *(u32x4 *)(side_lds + buf * S::kSBuf + (wave * 8 * KW + lane) * 16) = sr;
+        };
+        auto side_at = [&](int buf, int w, int arr) -> uint32_t {
+            return *(const uint16_t *)(side_lds + buf * S::kSBuf +
+                                       ((((w * 2 + arr) * KW + kw) * S::kBandCols) + cw * 32 + r) * 2);
+        };
         // Weight ring: step t's codes and sidecars in slot t % D; the group is a wave-uniform
         // offset, clamped into the job so it stays in bounds.
         u32x4 wq[D][NW];
@@ -194,19 +231,33 @@ q4_mma_kernel(MmaArgs args) {
 #pragma unroll
             for (int w = 0; w < NW; ++w) {
                 wq[slot_][w] = buffer_load16(q_rsrc[w], q_lane, ug * q_group);
-                wsc[slot_][w] = buffer_load_u16(s_rsrc[w], side_lane, ug * side_group);
-                wbi[slot_][w] = buffer_load_u16(b_rsrc[w], side_lane, ug * side_group);
+                if (!kStageSide) {
+                    wsc[slot_][w] = buffer_load_u16(s_rsrc[w], side_lane, ug * side_group);
+                    wbi[slot_][w] = buffer_load_u16(b_rsrc[w], side_lane, ug * side_group);
+                }
+            }
+        };
+        // Scale and bias of weight w for the step whose weights sit in slot `slot_` and whose
+        // sidecars sit in LDS buffer `sbuf`.
+        auto sidecars = [&](int slot_, int sbuf, int w, float &sv, float &bv) {
+            if (kStageSide) {
+                sv = bf16_bits_to_f32(side_at(sbuf, w, 0));
+                bv = bf16_bits_to_f32(side_at(sbuf, w, 1));
+            } else {
+                sv = bf16_bits_to_f32(wsc[slot_][w]);
+                bv = bf16_bits_to_f32(wbi[slot_][w]);
             }
         };
         // Dequantized weights of the current step; word i is replaced by the next step's word i as
         // soon as the MFMAs of sub-step i have been issued.
         bf16x8 bw[NW][4];
-        auto dequant = [&](int slot_) {
+        auto dequant = [&](int slot_, int sbuf) {
 #pragma unroll
             for (int w = 0; w < NW; ++w) {
-                const float s = bf16_bits_to_f32(wsc[slot_][w]), b = bf16_bits_to_f32(wbi[slot_][w]);
+                float sv, bv;
+                sidecars(slot_, sbuf, w, sv, bv);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) bw[w][i] = dequant_word(wq[slot_][w][i], s, b);
+                for (int i = 0; i < 4; ++i) bw[w][i] = dequant_word(wq[slot_][w][i], sv, bv);
             }
         };
 
@@ -228,15 +279,22 @@ q4_mma_kernel(MmaArgs args) {
         // (t + 1 mod 3) last held chunk t - 2, which every wave finished before the previous
         // barrier. LDS latency and the barrier hide behind sub-steps 2 and 3.
         const int Tp = (T + D - 1) / D * D;
+        auto nbuf = [&](int b) { return b == S::kNB - 1 ? 0 : b + 1; };
         load_a(0);
+        load_s(0);
         load_w(0, 0);
-        load_w(1, 1);
-        wait_vmcnt<2 * S::kWLoads>();
+        wait_vmcnt<kWLoads>();
         store_a(0);
+        store_s(0);
+        load_s(1);
+        load_w(1, 1);
+        wait_vmcnt<kWLoads>();
+        store_s(1);
         load_a(1);
+        load_s(2);
         load_w(2, 2);
         lds_barrier();
-        dequant(0);
+        dequant(0, 0);
         auto read_af = [&](bf16x8 *dst, int buf, int i) {
             const char *ap = lds_bytes + buf * S::kABuf;
 #pragma unroll
@@ -252,57 +310,62 @@ q4_mma_kernel(MmaArgs args) {
             const bool active = t < T && ga + t * KW + kw < gb;
             float sn[NW], bn[NW];
 #pragma unroll
-            for (int w = 0; w < NW; ++w) {
-                sn[w] = bf16_bits_to_f32(wsc[next][w]);
-                bn[w] = bf16_bits_to_f32(wbi[next][w]);
-            }
-            bf16x8 af[2][FM];
-#pragma unroll
-            for (int f = 0; f < FM; ++f) af[0][f] = af_pre[f];
+            for (int w = 0; w < NW; ++w) sidecars(next, nbuf(abuf), w, sn[w], bn[w]);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 if (i == 2) mid();
-                if (i < 3) read_af(af[(i + 1) & 1], abuf, i + 1);
+                bf16x8 af[FM];
+                if (i == 0) {
+#pragma unroll
+                    for (int f = 0; f < FM; ++f) af[f] = af_pre[f];
+                } else {
+                    read_af(af, abuf, i);
+                }
                 if (active) {
 #pragma unroll
                     for (int w = 0; w < NW; ++w)
 #pragma unroll
                         for (int f = 0; f < FM; ++f)
-                            acc[w][f] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i & 1][f], bw[w][i], acc[w][f], 0, 0, 0);
+                            acc[w][f] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[f], bw[w][i], acc[w][f], 0, 0, 0);
                 }
 #pragma unroll
                 for (int w = 0; w < NW; ++w) bw[w][i] = dequant_word(wq[next][w][i], sn[w], bn[w]);
             }
         };
 
+        // Sidecars run one step ahead of the chunks: those of step t + 2 are stored at the middle
+        // of step t (buffer t + 2 mod 3, last used for step t - 1's dequantization in step t - 2)
+        // and read while step t + 1 dequantizes step t + 2.
         int abuf = 0;  // buffer of step t's chunk
-        auto nbuf = [&](int b) { return b == S::kNB - 1 ? 0 : b + 1; };
         for (int t0 = 0; t0 < Tp - D; t0 += D) {
 #pragma unroll
             for (int d = 0; d < D; ++d) {
                 const int t = t0 + d;
                 step(t, d, abuf, [&] {
-                    wait_vmcnt<S::kWLoads>();  // chunk t + 1 has arrived (weights t + 2 may not)
+                    wait_vmcnt<kWLoads>();  // chunk t + 1, sidecars t + 2 have arrived
                     store_a(nbuf(abuf));
+                    store_s(nbuf(nbuf(abuf)));
                     lds_barrier();
                     read_af(af_pre, nbuf(abuf), 0);
                     load_a(t + 2);
+                    load_s(t + 3);
                     load_w(d, t + D);
                 });
                 abuf = nbuf(abuf);
             }
         }
-        // The last three steps: chunk Tp - 1 is loaded in the first of them, no weights after.
+        // The last three steps: chunk Tp - 1 is loaded in the first of them, nothing after.
 #pragma unroll
         for (int d = 0; d < D; ++d) {
             const int t = Tp - D + d;
             step(t, d, abuf, [&] {
                 if (d == 0) {
-                    wait_vmcnt<S::kWLoads>();
+                    wait_vmcnt<kWLoads>();
                 } else {
                     wait_vmcnt<0>();
                 }
                 if (d < 2) store_a(nbuf(abuf));
+                if (d == 0) store_s(nbuf(nbuf(abuf)));
                 lds_barrier();
                 if (d < 2) read_af(af_pre, nbuf(abuf), 0);
                 if (d == 0) load_a(t + 2);
