@@ -162,10 +162,11 @@ def build_workload(name, rt, torch, gen, kernel):
         x = torch.randn(m, k, device="cuda", generator=gen).to(torch.bfloat16)
         out = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
         b = one + m * k * 2 + m * n * 2
+        ws_q5 = workspace(m, n, k)
 
         def launches(i):
             w = ws[i % ncopy]
-            return [("q5k", lambda: rt.gemm(w, x, out=out))]
+            return [("q5k", lambda: rt.gemm(w, x, out=out, kernel=kernel, workspace=ws_q5))]
 
         cfg = {"workload": f"Q5_K down K17408->N5120", "rows": m, "format": "gguf q5_k planes",
                "weight_copies": ncopy}

@@ -173,7 +173,10 @@ int splosh_untile128(const void *src, void *dst, int64_t rows, int64_t groups, i
 /* ---- GGUF Q5_K ---------------------------------------------------------------------------- */
 
 /* Engine.gemm on a GGUF weight (Runtime/Engine.swift:1671-1697, kernels
- * Shaders/engine_gguf.metal:82-221 instantiated _q5k at :332-349). */
+ * Shaders/engine_gguf.metal:82-221 instantiated _q5k at :332-349). AUTO: 1..64 rows take the
+ * dequant-to-bf16 MFMA kernel (DEQUANT; lda % 8 == 0 and 16-byte aligned activations), which uses
+ * a workspace of splosh_workspace_bytes(rows, w->rows, w->inner) to split K; other row counts take
+ * the streaming kernel (STREAM). Odd alignments fall back to SCALAR. */
 int splosh_q5k_gemm(const splosh_q5k_weight *w, const uint16_t *a, int64_t lda, void *out, int64_t ldc,
                     int out_dtype, const void *residual, int64_t rows, int kernel, void *workspace,
                     size_t workspace_bytes, hipStream_t stream);

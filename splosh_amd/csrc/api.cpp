@@ -362,14 +362,18 @@ int splosh_untile128(const void *src, void *dst, int64_t rows, int64_t groups, i
 int splosh_q5k_gemm(const splosh_q5k_weight *w, const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype,
                     const void *residual, int64_t rows, int kernel, void *workspace, size_t workspace_bytes,
                     hipStream_t stream) {
-    (void)workspace;
-    (void)workspace_bytes;
     int st = check_q5k_weight(w);
     if (st) return st;
     if ((st = check_io(a, lda, out, ldc, out_dtype, rows, w->rows, w->inner))) return st;
     const bool eligible = lda % 4 == 0 && aligned(a, 8) && aligned(w->plane0, 16) && aligned(w->plane1, 4) &&
                           aligned(w->meta, 16);
-    int choice = kernel == SPLOSH_KERNEL_AUTO ? (eligible ? SPLOSH_KERNEL_STREAM : SPLOSH_KERNEL_SCALAR) : kernel;
+    const bool mma_ok = eligible && lda % 8 == 0 && aligned(a, 16) && splosh::q5k_mma_fits(rows, w->rows, w->inner, lda);
+    int choice = kernel;
+    if (kernel == SPLOSH_KERNEL_AUTO) {
+        if (!eligible) choice = SPLOSH_KERNEL_SCALAR;
+        else if (mma_ok) choice = SPLOSH_KERNEL_DEQUANT;
+        else choice = SPLOSH_KERNEL_STREAM;
+    }
     switch (choice) {
         case SPLOSH_KERNEL_STREAM: {
             if (!eligible) return fail(SPLOSH_ERR_UNSUPPORTED, "stream kernel needs lda % 4 == 0 and aligned planes");
@@ -377,6 +381,14 @@ int splosh_q5k_gemm(const splosh_q5k_weight *w, const uint16_t *a, int64_t lda, 
             if (plan.row_chunks > 65535) return fail(SPLOSH_ERR_UNSUPPORTED, "too many rows for one launch");
             return hip_status(splosh::launch_q5k_stream(plan, *w, a, lda, out, ldc, out_dtype, residual, rows, stream),
                               "q5k stream launch");
+        }
+        case SPLOSH_KERNEL_DEQUANT: {
+            if (!mma_ok) return fail(SPLOSH_ERR_UNSUPPORTED, "dequant kernel needs rows <= 64 and aligned operands");
+            const splosh::MmaPlan plan =
+                splosh::plan_mma(rows, w->rows, w->inner / 256, false, workspace ? workspace_bytes : 0);
+            return hip_status(splosh::launch_q5k_mma(plan, *w, a, lda, out, ldc, out_dtype, residual, rows, workspace,
+                                                     stream),
+                              "q5k dequant launch");
         }
         case SPLOSH_KERNEL_SCALAR:
             if (rows > 65535) return fail(SPLOSH_ERR_UNSUPPORTED, "scalar kernel takes at most 65535 rows");

@@ -69,7 +69,7 @@ struct MmaPlan {
     int bands;         // column bands of 64
     int grid;          // workgroups
     int dp_bands;      // bands computed whole (a multiple of grid)
-    int64_t sk_units;  // (band, group) pairs of the other bands, split evenly over the grid
+    int64_t sk_units;  // (band, unit) pairs of the other bands, split evenly over the grid
 };
 bool mma_fits(int64_t rows, int64_t columns, int64_t inner, int64_t stride_words, int64_t lda);
 MmaPlan plan_mma(int64_t rows, int64_t columns, int64_t groups, bool mlp, size_t workspace_bytes);
@@ -77,6 +77,12 @@ size_t mma_workspace_bytes(int64_t rows, int64_t columns, int64_t groups, bool m
 hipError_t launch_q4_mma(const MmaPlan &plan, const splosh_q4_weight &w, const splosh_q4_weight *up,
                          const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype, const void *residual,
                          int64_t rows, void *workspace, hipStream_t stream);
+
+// The same kernel over Q5_K planes; the plan's units are 256-element blocks.
+bool q5k_mma_fits(int64_t rows, int64_t columns, int64_t inner, int64_t lda);
+hipError_t launch_q5k_mma(const MmaPlan &plan, const splosh_q5k_weight &w, const uint16_t *a, int64_t lda, void *out,
+                          int64_t ldc, int out_dtype, const void *residual, int64_t rows, void *workspace,
+                          hipStream_t stream);
 
 // Sums split-K partials [splits][nw][rows][n] in slice order and applies the epilogue
 // (silu(g) * u for nw = 2, then the optional residual, then the output conversion).

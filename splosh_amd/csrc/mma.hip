@@ -1,4 +1,5 @@
-// mma.hip -- q4 GEMM for batched draft-verify (3..64 activation rows) on v_mfma_f32_32x32x16_bf16.
+// mma.hip -- quantized GEMM for batched draft-verify (up to 64 activation rows) on
+// v_mfma_f32_32x32x16_bf16, for q4 (MLX affine, group 64) and GGUF Q5_K weights.
 //
 // At 64 rows a K=5120 -> N=17408 pair (gate and up, 95 MB of codes and sidecars) needs 22.8 GFLOP:
 // about 9 us of MFMA at the dense bf16 peak and 12 us of VALU to dequantize, against 12-17 us of
@@ -7,24 +8,24 @@
 //
 //  * A wave owns 32 output columns of each of NW weights (NW = 2: fused gate+up, silu(g) * u) for
 //    all rows (FM blocks of 32). Each weight is therefore dequantized exactly once, in registers,
-//    straight into the MFMA B operand. Lane (r, h) = (lane & 31, lane >> 5) feeds column r and uses
-//    words 4h .. 4h + 3 of the column's 32-byte record in the four 16-deep MFMA steps of a group
-//    (one 16-byte load; a wave reads 32 consecutive records, a contiguous kilobyte of the tiled
-//    layout). A word becomes eight bf16 weights RNE(s q + b): two ANDs split the nibbles,
-//    v_cvt_f32_ubyte0..3 converts, v_fma_f32 scales, v_cvt_pk_bf16_f32 packs -- 22 VALU.
-//  * The A operand of step i is eight activations of row r at k = 32 h + 8 i (the same k
-//    permutation as the weights). The KW waves of a column slice split K by groups (wave kw takes
-//    every KW-th group) and the CW column slices of a workgroup share one activation chunk of KW
-//    groups, staged in LDS once per step: activations are read from L2 once per workgroup.
-//  * Weight codes and sidecars are loaded three steps ahead into a register ring; the
-//    activation chunk one step ahead into registers, then stored to one of three LDS buffers.
-//    One barrier per step, in its middle.
+//    straight into the MFMA B operand: lane (r, h) = (lane & 31, lane >> 5) feeds column r with the
+//    eight weights of 16-byte activation piece 4 h + piece(i) of its wave's 64-element K slice in
+//    sub-step i. The format class (Q4Format, Q5Format below) loads the codes and turns them into
+//    those bf16 operands; everything else is shared.
+//  * The A operand of sub-step i is the matching eight activations of row r. The KW waves of a
+//    column slice split a step's K by 64-element slices and the CW column slices of a workgroup
+//    share one activation chunk of KW slices, staged in LDS once per step: activations are read
+//    from L2 once per workgroup.
+//  * Weight codes are loaded three steps ahead into a register ring; the activation chunk one step
+//    ahead into registers, then stored to one of three LDS buffers, and so are per-band sidecars
+//    or block metadata. One barrier per step, in its middle.
 //  * At the end of a job the KW partial sums meet in LDS and the workgroup writes whole output
 //    rows. Bands beyond a whole number per CU are split over all workgroups (stream-K) and their
 //    fp32 partials summed by q4_mma_finish.
 //
-// Numerics: w is the fp32 dequantized weight (one rounding, as DequantOracle.swift:20-21) rounded
-// to bf16 (RNE), products exact in fp32, fp32 accumulation.
+// Numerics: w is the fp32 dequantized weight (one rounding, as DequantOracle.swift:20-21 for q4 and
+// GgufQuant.swift:205-210 for Q5_K) rounded to bf16 (RNE), products exact in fp32, fp32
+// accumulation.
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -33,12 +34,15 @@
 namespace splosh {
 
 struct MmaArgs {
+    // q4: the weight (gate) and, for the fused pair, up.
     const uint32_t *packed[2];
     const uint16_t *scales[2];
     const uint16_t *biases[2];
     int64_t stride_words;
+    // Q5_K planes.
+    const uint8_t *plane0, *plane1, *meta;
     int64_t n;
-    int64_t groups;
+    int64_t units;      // K units of a band: q4 groups of 64, Q5_K blocks of 256
     const uint16_t *a;
     int64_t lda;
     void *out;
@@ -48,8 +52,10 @@ struct MmaArgs {
     int out_dtype;
     float *partial;     // stream-K partials [gridDim.x][2][NW][rows][band columns]
     int dp_bands;       // bands computed whole (a multiple of gridDim.x)
-    int64_t sk_units;   // (band, group) pairs of the remaining bands
-    uint32_t code_bytes, sidecar_bytes, a_bytes;  // buffer extents (mma_fits keeps them < 4 GiB)
+    int64_t sk_units;   // (band, unit) pairs of the remaining bands
+    // Buffer extents (the fits checks keep them < 4 GiB): q4 codes and sidecars, or Q5_K plane0,
+    // plane1 and meta; activations.
+    uint32_t code_bytes, sidecar_bytes, meta_bytes, a_bytes;
 };
 
 __device__ __forceinline__ float cvt_byte(uint32_t x, int j) {
@@ -73,7 +79,243 @@ __device__ __forceinline__ bf16x8 dequant_word(uint32_t w, float s, float b) {
     return as_bf16x8(d);
 }
 
-template <int FM, int NW, int CW, int KW, int D>
+// q4 (MLX affine): a step is KW groups of 64; wave kw takes group ga + t KW + kw and lane (r, h)
+// feeds column r from words 4 h .. 4 h + 3 of the group's 32-byte record (one 16-byte load; a
+// wave reads 32 consecutive records, a contiguous kilobyte of the tiled layout). A word becomes
+// eight bf16 weights RNE(s q + b): two ANDs split the nibbles, v_cvt_f32_ubyte0..3 converts,
+// v_fma_f32 scales, v_cvt_pk_bf16_f32 packs -- 22 VALU.
+//
+// Tiled weights stage a step's sidecars for the band (NW weights x {scale, bias} x KW groups x
+// band columns of bf16) through LDS: waves 0 .. 2 NW - 1 each load one array of one weight, lane
+// l < 8 KW bytes 16 (l & 7) .. of group l >> 3's 128-byte run (groups past the job re-read the
+// last one). LDS layout per buffer: [weight][array][group][column]. Row-major weights load the
+// sidecars per lane with the codes.
+template <int NW_, bool TILED, int CW, int KW, int D>
+struct Q4Format {
+    static constexpr int NW = NW_;
+    static constexpr bool kStageSide = TILED;
+    static constexpr int kWLoads = kStageSide ? NW : NW * 3;  // weight loads per wave and step
+    static constexpr int kUnitK = kGroup;
+    static constexpr int kBandCols = CW * 32;
+    static constexpr int kSBuf = kStageSide ? NW * 2 * KW * kBandCols * 2 : 0;
+    static_assert(KW * (kBandCols * 2 / 16) <= 64, "one wave-wide load covers an array's step");
+    static constexpr int piece(int i) { return i; }
+
+    rsrc_t q_rsrc[NW], s_rsrc[NW], b_rsrc[NW], side_rsrc;
+    int wave, lane, kw, cw, r, h, ga, gb;
+    uint32_t G32, q_lane, side_lane, q_group, side_group, side_src;
+    bool side_loader;
+    u32x4 sr;
+    u32x4 wq[D][NW];
+    uint32_t wsc[D][NW], wbi[D][NW];
+    float sv[NW], bv[NW];  // scale and bias of the step being dequantized
+
+    __device__ Q4Format(const MmaArgs &args, int wave_, int lane_) : wave(wave_), lane(lane_) {
+        kw = wave / CW;
+        cw = wave % CW;
+        r = lane & 31;
+        h = lane >> 5;
+        G32 = (uint32_t)args.units;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            q_rsrc[w] = make_rsrc(args.packed[w], args.code_bytes);
+            s_rsrc[w] = make_rsrc(args.scales[w], args.sidecar_bytes);
+            b_rsrc[w] = make_rsrc(args.biases[w], args.sidecar_bytes);
+        }
+        // The sidecar array this wave stages (waves 0 .. 2 NW - 1): weight wave / 2, bias if odd.
+        const int side_w = (wave >> 1) < NW ? (wave >> 1) : 0;
+        side_rsrc = make_rsrc((wave & 1) ? (const void *)args.biases[side_w] : (const void *)args.scales[side_w],
+                              args.sidecar_bytes);
+        side_loader = kStageSide && wave < 2 * NW && lane < 8 * KW;
+        sr = u32x4{0u, 0u, 0u, 0u};
+    }
+    __device__ int steps(int ga_, int gb_) const { return (gb_ - ga_ + KW - 1) / KW; }
+    __device__ bool active(int t) const { return ga + t * KW + kw < gb; }
+    __device__ void begin(const MmaArgs &args, int band, int ga_, int gb_) {
+        ga = ga_;
+        gb = gb_;
+        const int64_t ncol = (int64_t)band * kBandCols + cw * 32 + r;
+        const uint32_t col = (uint32_t)(ncol < args.n ? ncol : args.n - 1);
+        if (TILED) {
+            const uint32_t rec0 = (col >> 7) * G32 * 128u + (col & 127u);  // record of group 0
+            q_lane = rec0 * 32u + 16u * h;
+            side_lane = rec0 * 2u;
+            q_group = 128u * 32u;
+            side_group = 128u * 2u;
+            const uint32_t n0 = (uint32_t)band * kBandCols;
+            side_src = (((n0 >> 7) * G32 * 128u + (n0 & 127u)) * 2u) + 16u * (lane & 7);
+        } else {
+            q_lane = col * (uint32_t)args.stride_words * 4u + 16u * h;
+            side_lane = col * G32 * 2u;
+            q_group = 32u;
+            side_group = 2u;
+            side_src = 0;
+        }
+    }
+    __device__ void load_s(int t) {
+        if (!side_loader) return;
+        int g = ga + t * KW + (lane >> 3);
+        g = g < gb ? g : gb - 1;
+        sr = buffer_load16(side_rsrc, side_src + (uint32_t)g * 256u, 0);
+    }
+    __device__ void store_s(char *sbuf) {
+        if (side_loader) *(u32x4 *)(sbuf + (wave * 8 * KW + lane) * 16) = sr;
+    }
+    // Codes (and row-major sidecars) of step t into ring slot `slot`; the group is a wave-uniform
+    // offset, clamped into the job so it stays in bounds.
+    __device__ void load_w(int slot, int t) {
+        int g = ga + t * KW + kw;
+        g = g < gb ? g : gb - 1;
+        const uint32_t ug = (uint32_t)__builtin_amdgcn_readfirstlane(g);
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            wq[slot][w] = buffer_load16(q_rsrc[w], q_lane, ug * q_group);
+            if (!kStageSide) {
+                wsc[slot][w] = buffer_load_u16(s_rsrc[w], side_lane, ug * side_group);
+                wbi[slot][w] = buffer_load_u16(b_rsrc[w], side_lane, ug * side_group);
+            }
+        }
+    }
+    // Sidecars of the step whose codes sit in `slot` and whose staged sidecars sit in `sbuf`.
+    __device__ void prepare(int slot, const char *sbuf) {
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            if (kStageSide) {
+                const char *base = sbuf + (((w * 2) * KW + kw) * kBandCols + cw * 32 + r) * 2;
+                sv[w] = bf16_bits_to_f32(*(const uint16_t *)base);
+                bv[w] = bf16_bits_to_f32(*(const uint16_t *)(base + KW * kBandCols * 2));
+            } else {
+                sv[w] = bf16_bits_to_f32(wsc[slot][w]);
+                bv[w] = bf16_bits_to_f32(wbi[slot][w]);
+            }
+        }
+    }
+    __device__ bf16x8 operand(int w, int i, int slot) { return dequant_word(wq[slot][w][i], sv[w], bv[w]); }
+};
+
+// GGUF Q5_K in plane form (GgufPlanes.swift:8-20): a step is one 256-element block; wave kw takes
+// its 32-element groups 2 kw and 2 kw + 1, lane (r, h) group j = 2 kw + h of column r: a 16-byte
+// plane0 record of low nibbles and a 4-byte plane1 record of fifth bits. The block's 16-byte meta
+// record (fp16 d and dmin, twelve bytes of packed 6-bit scales and minimums) of each band column
+// is staged through LDS by wave 0, a step ahead, like the q4 sidecars.
+//
+// Chunk order (gguf_formats.h:17-21): word c of a plane0 record holds elements 4c..4c+3 in its
+// nibbles at bits 0, 16, 4, 20 and 16+4c..16+4c+3 at bits 8, 24, 12, 28; the fifth bit of the
+// nibble at bit 4p + 16l sits at plane1 bit 8c + 2p + l. So w & 0x0F0F0F0F has the codes of
+// elements (4c, 16+4c, 4c+1, 16+4c+1) in its bytes and (w >> 4) & 0x0F0F0F0F those of
+// (4c+2, 16+4c+2, 4c+3, 16+4c+3), and the fifth bits reach bit 4 of those bytes by one multiply:
+// byte x = plane1 >> 8c, ((x & 0x33) * 0x880110) & 0x10101010 moves bits 0, 4, 1, 5 to bits 4, 12,
+// 20, 28 (the other partial products and their carries stay below or between them), and x >> 2
+// does the same for the second set. Words 0 and 1 thus give elements 0..7 (bytes 0 and 2) and
+// 16..23 (bytes 1 and 3) of the group, words 2 and 3 elements 8..15 and 24..31: sub-step i takes
+// activation piece ((i & 1) << 1) | (i >> 1). w = code d sc - dmin mn as one fma (d sc, code d sc
+// and dmin mn are exact in fp32), then RNE to bf16.
+template <int CW, int KW, int D>
+struct Q5Format {
+    static constexpr int NW = 1;
+    static constexpr int kWLoads = 2;
+    static constexpr int kUnitK = 256;
+    static constexpr int kBandCols = CW * 32;
+    static constexpr int kSBuf = kBandCols * 16;
+    static_assert(KW == 4, "four waves cover the eight groups of a block");
+    static_assert(kBandCols <= 64, "one wave loads the band's meta records");
+    static constexpr int piece(int i) { return ((i & 1) << 1) | (i >> 1); }
+
+    rsrc_t p0_rsrc, p1_rsrc, m_rsrc;
+    int wave, lane, kw, cw, r, h, ga, gb;
+    uint32_t blocks, p0_lane, p1_lane, m_lane;
+    u32x4 wq[D];
+    uint32_t wh[D];
+    u32x4 mr;
+    float scaled, offset;  // d sc and -(dmin mn) of the lane's group in the step being dequantized
+    uint32_t lo[2], hi[2]; // 5-bit codes of two words, shared by two sub-steps
+
+    __device__ Q5Format(const MmaArgs &args, int wave_, int lane_) : wave(wave_), lane(lane_) {
+        kw = wave / CW;
+        cw = wave % CW;
+        r = lane & 31;
+        h = lane >> 5;
+        blocks = (uint32_t)args.units;
+        p0_rsrc = make_rsrc(args.plane0, args.code_bytes);
+        p1_rsrc = make_rsrc(args.plane1, args.sidecar_bytes);
+        m_rsrc = make_rsrc(args.meta, args.meta_bytes);
+        mr = u32x4{0u, 0u, 0u, 0u};
+    }
+    __device__ int steps(int ga_, int gb_) const { return gb_ - ga_; }
+    __device__ bool active(int) const { return true; }
+    // Records are ((row / 128) units + unit) 128 + row % 128 (GgufPlanes.swift:62-74), 8 groups
+    // a block; a block step moves plane0 by 8 x 128 x 16 bytes, plane1 by 8 x 128 x 4, meta by
+    // 128 x 16.
+    __device__ void begin(const MmaArgs &args, int band, int ga_, int gb_) {
+        ga = ga_;
+        gb = gb_;
+        const int64_t ncol = (int64_t)band * kBandCols + cw * 32 + r;
+        const uint32_t col = (uint32_t)(ncol < args.n ? ncol : args.n - 1);
+        const uint32_t rec0 = ((col >> 7) * blocks * 8u + 2u * kw + h) * 128u + (col & 127u);
+        p0_lane = rec0 * 16u;
+        p1_lane = rec0 * 4u;
+        const int64_t mcol64 = (int64_t)band * kBandCols + lane;
+        const uint32_t mcol = (uint32_t)(mcol64 < args.n ? mcol64 : args.n - 1);
+        m_lane = ((mcol >> 7) * blocks * 128u + (mcol & 127u)) * 16u;
+    }
+    __device__ uint32_t block(int t) const {
+        const int b = ga + t < gb ? ga + t : gb - 1;
+        return (uint32_t)__builtin_amdgcn_readfirstlane(b);
+    }
+    __device__ void load_s(int t) {
+        if (wave == 0) mr = buffer_load16(m_rsrc, m_lane, block(t) * (128u * 16u));
+    }
+    __device__ void store_s(char *sbuf) {
+        if (wave == 0 && lane < kBandCols) *(u32x4 *)(sbuf + lane * 16) = mr;
+    }
+    __device__ void load_w(int slot, int t) {
+        const uint32_t b = block(t);
+        wq[slot] = buffer_load16(p0_rsrc, p0_lane, b * (8u * 128u * 16u));
+        wh[slot] = buffer_load_u32(p1_rsrc, p1_lane, b * (8u * 128u * 4u));
+    }
+    // Scale and minimum of group j = 2 kw + h (GgufQuant.swift:196-203): packed byte k is meta byte
+    // 4 + k, so for j < 4 (kw < 2, wave-uniform) sc and mn are the low six bits of meta bytes 4 + j
+    // and 8 + j; for j >= 4 they are the nibbles of byte 12 + (j - 4) joined with the top two bits
+    // of bytes 4 + (j - 4) and 8 + (j - 4). Either way the byte within its word is 2 (kw & 1) + h.
+    __device__ void prepare(int, const char *sbuf) {
+        const u32x4 m = *(const u32x4 *)(sbuf + (cw * 32 + r) * 16);
+        const float d = half_bits_to_f32(m[0]), dmin = half_bits_to_f32(m[0] >> 16);
+        const uint32_t sh = 8u * (2u * (kw & 1) + h);
+        uint32_t sc, mn;
+        if (kw < 2) {
+            sc = __builtin_amdgcn_ubfe(m[1], sh, 6);
+            mn = __builtin_amdgcn_ubfe(m[2], sh, 6);
+        } else {
+            sc = __builtin_amdgcn_ubfe(m[3], sh, 4) | (__builtin_amdgcn_ubfe(m[1], sh + 6, 2) << 4);
+            mn = __builtin_amdgcn_ubfe(m[3], sh + 4, 4) | (__builtin_amdgcn_ubfe(m[2], sh + 6, 2) << 4);
+        }
+        scaled = d * (float)sc;
+        offset = -(dmin * (float)mn);
+    }
+    __device__ float weight(uint32_t codes, int j) const { return __builtin_fmaf(cvt_byte(codes, j), scaled, offset); }
+    __device__ bf16x8 operand(int, int i, int slot) {
+        if ((i & 1) == 0) {
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const int c = i + e;
+                const uint32_t w = wq[slot][c];
+                const uint32_t x = __builtin_amdgcn_ubfe(wh[slot], 8 * c, 8);
+                lo[e] = (w & 0x0F0F0F0Fu) | (((x & 0x33u) * 0x880110u) & 0x10101010u);
+                hi[e] = ((w >> 4) & 0x0F0F0F0Fu) | ((((x >> 2) & 0x33u) * 0x880110u) & 0x10101010u);
+            }
+        }
+        const int b = i & 1;  // byte b and b + 2: the lower (0) or upper (1) four elements of a word
+        u32x4 d;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            d[2 * e] = f32x2_to_bf16x2(weight(lo[e], b), weight(lo[e], b + 2));
+            d[2 * e + 1] = f32x2_to_bf16x2(weight(hi[e], b), weight(hi[e], b + 2));
+        }
+        return as_bf16x8(d);
+    }
+};
+
+template <int FM, int NW, int CW, int KW, int D, int SBUF>
 struct MmaShape {
     static constexpr int kThreads = CW * KW * 64;
     static constexpr int kRows = FM * 32;
@@ -83,16 +325,12 @@ struct MmaShape {
     static_assert(kAPieces % kThreads == 0, "whole activation pieces per thread");
     static constexpr int kAPer = kAPieces / kThreads;              // activation loads per wave and step
     static constexpr int kABuf = kAPieces * 16;                    // bytes of one chunk buffer
-    // Tiled weights: a step's sidecars for the band (NW weights x {scale, bias} x KW groups x
-    // kBandCols columns of bf16) go through LDS too, loaded by waves 0 .. 2 NW - 1 (32 lanes x
-    // 16 bytes each: the 4 groups x 128 bytes of one array of one weight).
-    static constexpr int kSBuf = NW * 2 * KW * kBandCols * 2;
+    static constexpr int kSBuf = SBUF;                             // bytes of one staged-sidecar buffer
     static constexpr int kNB = 3;                                  // chunk buffers
     static constexpr int kAcc = FM * NW * 16;                      // accumulator floats per lane
     static constexpr size_t kRedBytes = (size_t)KW * CW * kAcc * 64 * sizeof(float);
     static constexpr size_t kABytes = (size_t)kNB * (kABuf + kSBuf);
     static constexpr size_t kLds = kRedBytes > kABytes ? kRedBytes : kABytes;
-    static_assert(KW * (kBandCols * 2 / 16) <= 64, "one wave-wide load covers an array's step");
     static_assert(D == 3, "the pipeline below is written for weights three steps ahead");
 };
 
@@ -104,53 +342,38 @@ __device__ __forceinline__ void wait_vmcnt() {
 
 // Work split. The N columns form `bands` bands of CW * 32. Bands [0, dp_bands) are computed whole
 // by workgroup (band mod gridDim.x), written straight to the output. The remaining bands' (band,
-// group) pairs, sk_units of them, are cut into gridDim.x equal contiguous ranges (stream-K), one a
+// unit) pairs, sk_units of them, are cut into gridDim.x equal contiguous ranges (stream-K), one a
 // workgroup; a range covers at most two bands, and a band it covers in part is written as an fp32
 // partial to slot 0 (the range's first band) or 1 of the workgroup's workspace, summed later by
 // q4_mma_finish. dp_bands is a multiple of gridDim.x, so every workgroup gets the same work.
 //
-// Pipeline of a job (groups [ga, gb) of one band), in steps of KW groups, D steps deep:
-//  * the activation chunk of step t (rows x KW groups) is copied global -> LDS by the waves
-//    themselves with buffer_load ... lds (no registers), into buffer t mod (D + 1), XOR-swizzled
-//    (16-byte piece kc of row m at position kc ^ (m & 7)) so the MFMA operand reads do not
-//    conflict; weight codes and sidecars go to a D-slot register ring;
-//  * every wave issues exactly the same loads each step, so the chunk needed next is waited for
-//    with a fixed vmcnt that leaves the younger D - 1 steps of loads in flight; the last D steps
-//    issue nothing. Barriers wait for LDS traffic only, never for global stores.
-template <int FM, int NW, bool TILED, int CW, int KW, int D>
+// Pipeline of a job (units [ga, gb) of one band), in steps of KW x 64 elements of K, D steps deep:
+// weight codes go to a D-slot register ring, the activation chunk of a step (rows x KW x 64) and
+// its sidecars via registers to LDS buffer t mod 3, the chunk XOR-swizzled (16-byte piece kc of
+// row m at position kc ^ (m & 7)) so the MFMA operand reads do not conflict. Barriers wait for LDS
+// traffic only, never for global stores.
+template <class F, int FM, int CW, int KW, int D>
 __global__ void __launch_bounds__(CW * KW * 64)
-q4_mma_kernel(MmaArgs args) {
-    using S = MmaShape<FM, NW, CW, KW, D>;
-    // Sidecars: staged through LDS for the tiled layout (a band's are contiguous there); loaded
-    // per wave with the codes for row-major weights.
-    constexpr bool kStageSide = TILED;
-    constexpr int kWLoads = kStageSide ? NW : NW * 3;  // weight loads per wave and step
+mma_kernel(MmaArgs args) {
+    constexpr int NW = F::NW;
+    using S = MmaShape<FM, NW, CW, KW, D, F::kSBuf>;
+    static_assert(F::kBandCols == S::kBandCols, "one band geometry");
+    constexpr int kWLoads = F::kWLoads;
     extern __shared__ __align__(16) uint16_t lds[];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int cw = wave % CW, kw = wave / CW;
     const int r = lane & 31, h = lane >> 5;
-    const int G = (int)args.groups;
-    const uint32_t G32 = (uint32_t)G;
+    const int U = (int)args.units;
 
     const rsrc_t a_rsrc = make_rsrc(args.a, args.a_bytes);
-    rsrc_t q_rsrc[NW], s_rsrc[NW], b_rsrc[NW];
-#pragma unroll
-    for (int w = 0; w < NW; ++w) {
-        q_rsrc[w] = make_rsrc(args.packed[w], args.code_bytes);
-        s_rsrc[w] = make_rsrc(args.scales[w], args.sidecar_bytes);
-        b_rsrc[w] = make_rsrc(args.biases[w], args.sidecar_bytes);
-    }
-    // The sidecar array this wave stages (waves 0 .. 2 NW - 1): weight wave / 2, bias if odd.
-    const int side_w = (wave >> 1) < NW ? (wave >> 1) : 0;
-    const rsrc_t side_rsrc =
-        make_rsrc((wave & 1) ? (const void *)args.biases[side_w] : (const void *)args.scales[side_w], args.sidecar_bytes);
+    F fmt(args, wave, lane);
     // Activation staging: this thread's piece j of a chunk sits at buffer position
     // (wave * kAPer + j) * 64 + lane, i.e. row m = pos / kKc, holding piece kc = (pos % kKc) ^ (m & 7)
     // of the row (an XOR swizzle, so the MFMA operand reads do not conflict), read from byte
-    // (m lda + 64 g + 8 kc) * 2. Rows past the last are clamped (their outputs are not stored);
-    // groups past the job belong to inactive waves; reads past the buffer return zero.
+    // (m lda + k0 + 8 kc) * 2. Rows past the last are clamped (their outputs are not stored);
+    // K past the job belongs to inactive waves; reads past the buffer return zero.
     uint32_t a_src[S::kAPer];
 #pragma unroll
     for (int j = 0; j < S::kAPer; ++j) {
@@ -159,34 +382,22 @@ q4_mma_kernel(MmaArgs args) {
         const int64_t rc = row < args.rows ? row : args.rows - 1;
         a_src[j] = (uint32_t)((rc * args.lda + kc * 8) * 2);
     }
-    // MFMA operand reads: sub-step i of block f takes row 32 f + r, piece kw * 8 + 4 h + i.
+    // MFMA operand reads: sub-step i of block f takes row 32 f + r, piece kw * 8 + 4 h + piece(i).
     uint32_t a_rd[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) a_rd[i] = (uint32_t)((r * S::kKc + ((kw * 8 + 4 * h + i) ^ (r & 7))) * 16);
+    for (int i = 0; i < 4; ++i)
+        a_rd[i] = (uint32_t)((r * S::kKc + ((kw * 8 + 4 * h + F::piece(i)) ^ (r & 7))) * 16);
     char *lds_bytes = (char *)lds;
+    char *side_lds = lds_bytes + S::kNB * S::kABuf;
 
-    // One job: column band `band`, groups [ga, gb); slot < 0 writes the output, else a partial.
+    // One job: column band `band`, units [ga, gb); slot < 0 writes the output, else a partial.
     auto run_job = [&](int band, int ga, int gb, int slot) {
-        const int T = (gb - ga + KW - 1) / KW;  // steps of KW groups
-        const int64_t ncol = (int64_t)band * S::kBandCols + cw * 32 + r;
-        const uint32_t col = (uint32_t)(ncol < args.n ? ncol : args.n - 1);
-        uint32_t q_lane, side_lane, q_group, side_group;
-        if (TILED) {
-            const uint32_t rec0 = (col >> 7) * G32 * 128u + (col & 127u);  // record of group 0
-            q_lane = rec0 * 32u + 16u * h;
-            side_lane = rec0 * 2u;
-            q_group = 128u * 32u;
-            side_group = 128u * 2u;
-        } else {
-            q_lane = col * (uint32_t)args.stride_words * 4u + 16u * h;
-            side_lane = col * G32 * 2u;
-            q_group = 32u;
-            side_group = 2u;
-        }
+        const int T = fmt.steps(ga, gb);
+        fmt.begin(args, band, ga, gb);
 
         u32x4 ar[S::kAPer];  // the next chunk's pieces, on their way to LDS
         auto load_a = [&](int t) {
-            const uint32_t gbyte = (uint32_t)(ga + t * KW) * 128u;
+            const uint32_t gbyte = (uint32_t)(ga * F::kUnitK + t * KW * 64) * 2u;
 #pragma unroll
             for (int j = 0; j < S::kAPer; ++j) ar[j] = buffer_load16(a_rsrc, a_src[j] + gbyte, 0);
         };
@@ -195,70 +406,18 @@ q4_mma_kernel(MmaArgs args) {
             for (int j = 0; j < S::kAPer; ++j)
                 *(u32x4 *)(lds_bytes + buf * S::kABuf + ((wave * S::kAPer + j) * 64 + lane) * 16) = ar[j];
         };
-        // Staged sidecars: wave v < 2 NW loads array (v & 1 ? bias : scale) of weight v >> 1 for the
-        // step's KW groups: lane l < 8 KW takes group l >> 3, bytes 16 (l & 7) .. of the band's
-        // 128-byte run (groups past the job re-read the last one). LDS layout per buffer:
-        // [weight][array][group][column] bf16.
-        char *side_lds = lds_bytes + S::kNB * S::kABuf;
-        const bool side_loader = kStageSide && wave < 2 * NW && lane < 8 * KW;
-        uint32_t side_src = 0;
-        if (kStageSide) {
-            const uint32_t n0 = (uint32_t)band * S::kBandCols;
-            side_src = (((n0 >> 7) * G32 * 128u + (n0 & 127u)) * 2u) + 16u * (lane & 7);
-        }
-        u32x4 sr = {0u, 0u, 0u, 0u};
-        auto load_s = [&](int t) {
-            if (!side_loader) return;
-            int g = ga + t * KW + (lane >> 3);
-            g = g < gb ? g : gb - 1;
-            sr = buffer_load16(side_rsrc, side_src + (uint32_t)g * 256u, 0);
-        };
-        auto store_s = [&](int buf) {
-            if (side_loader) *(u32x4 *)(side_lds + buf * S::kSBuf + (wave * 8 * KW + lane) * 16) = sr;
-        };
-        auto side_at = [&](int buf, int w, int arr) -> uint32_t {
-            return *(const uint16_t *)(side_lds + buf * S::kSBuf +
-                                       ((((w * 2 + arr) * KW + kw) * S::kBandCols) + cw * 32 + r) * 2);
-        };
-        // Weight ring: step t's codes and sidecars in slot t % D; the group is a wave-uniform
-        // offset, clamped into the job so it stays in bounds.
-        u32x4 wq[D][NW];
-        uint32_t wsc[D][NW], wbi[D][NW];
-        auto load_w = [&](int slot_, int t) {
-            int g = ga + t * KW + kw;
-            g = g < gb ? g : gb - 1;
-            const uint32_t ug = (uint32_t)__builtin_amdgcn_readfirstlane(g);
-#pragma unroll
-            for (int w = 0; w < NW; ++w) {
-                wq[slot_][w] = buffer_load16(q_rsrc[w], q_lane, ug * q_group);
-                if (!kStageSide) {
-                    wsc[slot_][w] = buffer_load_u16(s_rsrc[w], side_lane, ug * side_group);
-                    wbi[slot_][w] = buffer_load_u16(b_rsrc[w], side_lane, ug * side_group);
-                }
-            }
-        };
-        // Scale and bias of weight w for the step whose weights sit in slot `slot_` and whose
-        // sidecars sit in LDS buffer `sbuf`.
-        auto sidecars = [&](int slot_, int sbuf, int w, float &sv, float &bv) {
-            if (kStageSide) {
-                sv = bf16_bits_to_f32(side_at(sbuf, w, 0));
-                bv = bf16_bits_to_f32(side_at(sbuf, w, 1));
-            } else {
-                sv = bf16_bits_to_f32(wsc[slot_][w]);
-                bv = bf16_bits_to_f32(wbi[slot_][w]);
-            }
-        };
-        // Dequantized weights of the current step; word i is replaced by the next step's word i as
+        auto load_s = [&](int t) { fmt.load_s(t); };
+        auto store_s = [&](int buf) { fmt.store_s(side_lds + buf * S::kSBuf); };
+        auto load_w = [&](int slot_, int t) { fmt.load_w(slot_, t); };
+        // Dequantized weights of the current step; operand i is replaced by the next step's as
         // soon as the MFMAs of sub-step i have been issued.
         bf16x8 bw[NW][4];
         auto dequant = [&](int slot_, int sbuf) {
+            fmt.prepare(slot_, side_lds + sbuf * S::kSBuf);
 #pragma unroll
-            for (int w = 0; w < NW; ++w) {
-                float sv, bv;
-                sidecars(slot_, sbuf, w, sv, bv);
+            for (int w = 0; w < NW; ++w)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) bw[w][i] = dequant_word(wq[slot_][w][i], sv, bv);
-            }
+                for (int i = 0; i < 4; ++i) bw[w][i] = fmt.operand(w, i, slot_);
         };
 
         f32x16 acc[NW][FM];
@@ -304,13 +463,11 @@ q4_mma_kernel(MmaArgs args) {
         read_af(af_pre, 0, 0);
 
         // Step t: MFMA sub-steps with the dequantization of step t + 1 interleaved, `mid` between
-        // sub-steps 1 and 2. Inactive waves (no group in step t) only dequantize.
+        // sub-steps 1 and 2. Inactive waves (no unit in step t) only dequantize.
         auto step = [&](int t, int d, int abuf, auto &&mid) {
             const int next = (d + 1) % D;
-            const bool active = t < T && ga + t * KW + kw < gb;
-            float sn[NW], bn[NW];
-#pragma unroll
-            for (int w = 0; w < NW; ++w) sidecars(next, nbuf(abuf), w, sn[w], bn[w]);
+            const bool active = t < T && fmt.active(t);
+            fmt.prepare(next, side_lds + nbuf(abuf) * S::kSBuf);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 if (i == 2) mid();
@@ -329,7 +486,7 @@ q4_mma_kernel(MmaArgs args) {
                             acc[w][f] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[f], bw[w][i], acc[w][f], 0, 0, 0);
                 }
 #pragma unroll
-                for (int w = 0; w < NW; ++w) bw[w][i] = dequant_word(wq[next][w][i], sn[w], bn[w]);
+                for (int w = 0; w < NW; ++w) bw[w][i] = fmt.operand(w, i, next);
             }
         };
 
@@ -429,7 +586,7 @@ q4_mma_kernel(MmaArgs args) {
 
     const int P = gridDim.x;
     for (int band = blockIdx.x; band < args.dp_bands; band += P) {
-        run_job(band, 0, G, -1);
+        run_job(band, 0, U, -1);
         lds_barrier();  // the next job's loads overwrite the reduction area; stores need not drain
     }
     if (args.sk_units > 0) {
@@ -437,10 +594,10 @@ q4_mma_kernel(MmaArgs args) {
         const int64_t u_end = args.sk_units * (blockIdx.x + 1) / P;
         int slot = 0;
         while (u < u_end) {
-            const int band = args.dp_bands + (int)(u / G);
-            const int ga = (int)(u % G);
-            const int gb = (int)((int64_t)ga + (u_end - u) < G ? ga + (u_end - u) : G);
-            run_job(band, ga, gb, (ga == 0 && gb == G) ? -1 : slot);
+            const int band = args.dp_bands + (int)(u / U);
+            const int ga = (int)(u % U);
+            const int gb = (int)((int64_t)ga + (u_end - u) < U ? ga + (u_end - u) : U);
+            run_job(band, ga, gb, (ga == 0 && gb == U) ? -1 : slot);
             lds_barrier();
             u += gb - ga;
             slot = 1;
@@ -448,18 +605,18 @@ q4_mma_kernel(MmaArgs args) {
     }
 }
 
-// Sums the stream-K partials of the remainder bands (see q4_mma_kernel) in workgroup order and
+// Sums the stream-K partials of the remainder bands (see mma_kernel) in workgroup order and
 // applies the epilogue. Block (rb, y) covers outputs [256 y, 256 y + 256) of remainder band rb;
 // its first thread lists the band's contributing workgroups once.
 constexpr int kFinishMaxContributors = 1024;
 __global__ void __launch_bounds__(256)
 q4_mma_finish(const float *__restrict__ partial, int nw, int band_cols, int dp_bands, int64_t sk_units, int P,
-              int64_t groups, int64_t rows, int64_t n, void *out, int64_t ldc, int out_dtype, const void *residual) {
+              int64_t units, int64_t rows, int64_t n, void *out, int64_t ldc, int out_dtype, const void *residual) {
     __shared__ int wg[kFinishMaxContributors];
     __shared__ int slot_of[kFinishMaxContributors];
     __shared__ int count;
     const int64_t rb = blockIdx.x;
-    const int64_t lo = rb * groups, hi = lo + groups;  // the band's units
+    const int64_t lo = rb * units, hi = lo + units;  // the band's units
     if (threadIdx.x == 0) {
         // Workgroup i covers units [U i / P, U (i + 1) / P); the one holding unit u is
         // floor(((u + 1) P - 1) / U). Ranges may be empty when there are fewer units than workgroups.
@@ -515,9 +672,7 @@ q4_mma_finish(const float *__restrict__ partial, int nw, int band_cols, int dp_b
 
 constexpr int kMmaCW = 2, kMmaKW = 4;
 
-// Weight ring depth (steps the weight loads run ahead).
-template <int FM>
-constexpr int mma_depth() { return 3; }
+constexpr int kMmaDepth = 3;  // weight ring depth (steps the weight loads run ahead)
 
 // Activation and code offsets are 32-bit; 64 rows at most.
 bool mma_fits(int64_t rows, int64_t columns, int64_t inner, int64_t stride_words, int64_t lda) {
@@ -525,6 +680,13 @@ bool mma_fits(int64_t rows, int64_t columns, int64_t inner, int64_t stride_words
     const int64_t groups = inner / kGroup;
     return rows >= 1 && rows <= 64 && columns > 0 && groups > 0 && (rows * lda + inner) * 2 < limit &&
            columns * stride_words * 4 < limit && columns * groups * 32 < limit;
+}
+
+// Q5_K: plane0 holds 16 bytes per 32 elements of a row, plane1 4, meta 16 per 256.
+bool q5k_mma_fits(int64_t rows, int64_t columns, int64_t inner, int64_t lda) {
+    const int64_t limit = ((int64_t)1 << 32) - 256;
+    return rows >= 1 && rows <= 64 && columns > 0 && inner >= 256 && (rows * lda + inner) * 2 < limit &&
+           columns * (inner / 32) * 16 < limit;
 }
 
 // Compute units of the current device (the stream-K grid), cached per device.
@@ -568,11 +730,10 @@ size_t mma_workspace_bytes(int64_t rows, int64_t columns, int64_t groups, bool m
     return p.sk_units > 0 ? sk_bytes(p.grid, rows, mlp) : 0;
 }
 
-template <int FM, int NW, bool TILED>
+template <class F, int FM>
 static hipError_t launch_mma_v(const MmaPlan &p, const MmaArgs &args, hipStream_t stream) {
-    constexpr int D = mma_depth<FM>();
-    using S = MmaShape<FM, NW, kMmaCW, kMmaKW, D>;
-    auto kernel = q4_mma_kernel<FM, NW, TILED, kMmaCW, kMmaKW, D>;
+    using S = MmaShape<FM, F::NW, kMmaCW, kMmaKW, kMmaDepth, F::kSBuf>;
+    auto kernel = mma_kernel<F, FM, kMmaCW, kMmaKW, kMmaDepth>;
     static bool once = [&] {
         (void)hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)S::kLds);
         return true;
@@ -582,24 +743,16 @@ static hipError_t launch_mma_v(const MmaPlan &p, const MmaArgs &args, hipStream_
     return hipGetLastError();
 }
 
-template <int NW, bool TILED>
+template <class F>
 static hipError_t launch_mma_fm(const MmaPlan &p, const MmaArgs &args, hipStream_t stream) {
-    return p.fm == 1 ? launch_mma_v<1, NW, TILED>(p, args, stream) : launch_mma_v<2, NW, TILED>(p, args, stream);
+    return p.fm == 1 ? launch_mma_v<F, 1>(p, args, stream) : launch_mma_v<F, 2>(p, args, stream);
 }
 
-hipError_t launch_q4_mma(const MmaPlan &plan, const splosh_q4_weight &w, const splosh_q4_weight *up,
-                         const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype, const void *residual,
-                         int64_t rows, void *workspace, hipStream_t stream) {
-    MmaArgs args;
-    args.packed[0] = w.packed;
-    args.scales[0] = w.scales;
-    args.biases[0] = w.biases;
-    args.packed[1] = up ? up->packed : w.packed;
-    args.scales[1] = up ? up->scales : w.scales;
-    args.biases[1] = up ? up->biases : w.biases;
-    args.stride_words = w.row_stride_words;
-    args.n = w.rows;
-    args.groups = w.inner / kGroup;
+template <int NW, bool TILED>
+using Q4F = Q4Format<NW, TILED, kMmaCW, kMmaKW, kMmaDepth>;
+
+static void set_io(MmaArgs &args, const MmaPlan &plan, const uint16_t *a, int64_t lda, void *out, int64_t ldc,
+                   int out_dtype, const void *residual, int64_t rows, int64_t inner, void *workspace) {
     args.a = a;
     args.lda = lda;
     args.out = out;
@@ -610,23 +763,63 @@ hipError_t launch_q4_mma(const MmaPlan &plan, const splosh_q4_weight &w, const s
     args.partial = plan.sk_units > 0 ? (float *)workspace : nullptr;
     args.dp_bands = plan.dp_bands;
     args.sk_units = plan.sk_units;
-    const bool tiled = w.order == SPLOSH_Q4_TILED128;
+    args.a_bytes = (uint32_t)(((rows - 1) * lda + inner) * 2);
+}
+
+static hipError_t launch_finish(const MmaPlan &plan, int nw, int64_t units, int64_t n, int64_t rows, void *out,
+                                int64_t ldc, int out_dtype, const void *residual, void *workspace,
+                                hipStream_t stream) {
+    const int64_t per_band = rows * (kMmaCW * 32);
+    hipLaunchKernelGGL(q4_mma_finish, dim3((unsigned)(plan.sk_units / units), (unsigned)((per_band + 255) / 256)),
+                       dim3(256), 0, stream, (const float *)workspace, nw, kMmaCW * 32, plan.dp_bands, plan.sk_units,
+                       plan.grid, units, rows, n, out, ldc, out_dtype, residual);
+    return hipGetLastError();
+}
+
+hipError_t launch_q4_mma(const MmaPlan &plan, const splosh_q4_weight &w, const splosh_q4_weight *up,
+                         const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype, const void *residual,
+                         int64_t rows, void *workspace, hipStream_t stream) {
+    MmaArgs args = {};
+    args.packed[0] = w.packed;
+    args.scales[0] = w.scales;
+    args.biases[0] = w.biases;
+    args.packed[1] = up ? up->packed : w.packed;
+    args.scales[1] = up ? up->scales : w.scales;
+    args.biases[1] = up ? up->biases : w.biases;
+    args.stride_words = w.row_stride_words;
+    args.n = w.rows;
     const int64_t groups = w.inner / kGroup;
+    args.units = groups;
+    set_io(args, plan, a, lda, out, ldc, out_dtype, residual, rows, w.inner, workspace);
+    const bool tiled = w.order == SPLOSH_Q4_TILED128;
     args.code_bytes = (uint32_t)(tiled ? w.rows * groups * 32 : w.rows * w.row_stride_words * 4);
     args.sidecar_bytes = (uint32_t)(w.rows * groups * 2);
-    args.a_bytes = (uint32_t)(((rows - 1) * lda + w.inner) * 2);
     hipError_t err;
     if (up)
-        err = tiled ? launch_mma_fm<2, true>(plan, args, stream) : launch_mma_fm<2, false>(plan, args, stream);
+        err = tiled ? launch_mma_fm<Q4F<2, true>>(plan, args, stream) : launch_mma_fm<Q4F<2, false>>(plan, args, stream);
     else
-        err = tiled ? launch_mma_fm<1, true>(plan, args, stream) : launch_mma_fm<1, false>(plan, args, stream);
+        err = tiled ? launch_mma_fm<Q4F<1, true>>(plan, args, stream) : launch_mma_fm<Q4F<1, false>>(plan, args, stream);
     if (err != hipSuccess || plan.sk_units == 0) return err;
-    const int64_t per_band = rows * (kMmaCW * 32);
-    hipLaunchKernelGGL(q4_mma_finish, dim3((unsigned)(plan.sk_units / groups), (unsigned)((per_band + 255) / 256)),
-                       dim3(256), 0, stream,
-                       (const float *)workspace, up ? 2 : 1, kMmaCW * 32, plan.dp_bands, plan.sk_units, plan.grid, groups,
-                       rows, w.rows, out, ldc, out_dtype, residual);
-    return hipGetLastError();
+    return launch_finish(plan, up ? 2 : 1, groups, w.rows, rows, out, ldc, out_dtype, residual, workspace, stream);
+}
+
+hipError_t launch_q5k_mma(const MmaPlan &plan, const splosh_q5k_weight &w, const uint16_t *a, int64_t lda, void *out,
+                          int64_t ldc, int out_dtype, const void *residual, int64_t rows, void *workspace,
+                          hipStream_t stream) {
+    MmaArgs args = {};
+    args.plane0 = w.plane0;
+    args.plane1 = w.plane1;
+    args.meta = w.meta;
+    args.n = w.rows;
+    const int64_t blocks = w.inner / 256;
+    args.units = blocks;
+    set_io(args, plan, a, lda, out, ldc, out_dtype, residual, rows, w.inner, workspace);
+    args.code_bytes = (uint32_t)(w.rows * blocks * 8 * 16);
+    args.sidecar_bytes = (uint32_t)(w.rows * blocks * 8 * 4);
+    args.meta_bytes = (uint32_t)(w.rows * blocks * 16);
+    const hipError_t err = launch_mma_fm<Q5Format<kMmaCW, kMmaKW, kMmaDepth>>(plan, args, stream);
+    if (err != hipSuccess || plan.sk_units == 0) return err;
+    return launch_finish(plan, 1, blocks, w.rows, rows, out, ldc, out_dtype, residual, workspace, stream);
 }
 
 }  // namespace splosh

@@ -120,13 +120,15 @@ def _out(a, rows, n, out, out_dtype):
 
 
 def workspace_bytes(rows, columns, inner):
-    """splosh_workspace_bytes: the split-K scratch the tiled kernel can use for this shape (0: none)."""
+    """splosh_workspace_bytes: the split-K scratch the kernels can use for this shape (0: none)."""
     return _lib.lib().splosh_workspace_bytes(rows, columns, inner)
 
 
 def _workspace(workspace, rows, n, inner, device):
-    """The split-K scratch of the tiled kernel: the caller's tensor, or a fresh one from torch's
-    stream-ordered allocator sized by splosh_workspace_bytes."""
+    """The split-K scratch of the kernels: the caller's tensor (an empty one: none), or a fresh one
+    from torch's stream-ordered allocator sized by splosh_workspace_bytes."""
+    if workspace is not None and workspace.numel() == 0:
+        return None, 0
     if workspace is not None:
         return _ptr(workspace), workspace.numel() * workspace.element_size()
     need = _lib.lib().splosh_workspace_bytes(rows, n, inner)
@@ -154,14 +156,14 @@ def gemm(w, a, out=None, residual=None, out_dtype=torch.bfloat16, kernel=AUTO, r
         if residual.dtype != out.dtype or residual.stride(0) != out.stride(0):
             raise SploshError(13, "residual must match the output's dtype and row stride")
     wc = w.c()
+    ws, ws_bytes = _workspace(workspace, rows, w.rows, w.inner, a.device)
     if isinstance(w, Q4Weight):
-        ws, ws_bytes = _workspace(workspace, rows, w.rows, w.inner, a.device)
         st = _lib.lib().splosh_q4_gemm(ctypes.byref(wc), _ptr(a), a.stride(0), _ptr(out), out.stride(0),
                                        _dtype_code(out.dtype), _ptr(residual), rows, kernel, ws, ws_bytes,
                                        _stream(stream))
     else:
         st = _lib.lib().splosh_q5k_gemm(ctypes.byref(wc), _ptr(a), a.stride(0), _ptr(out), out.stride(0),
-                                        _dtype_code(out.dtype), _ptr(residual), rows, kernel, None, 0,
+                                        _dtype_code(out.dtype), _ptr(residual), rows, kernel, ws, ws_bytes,
                                         _stream(stream))
     _lib.check(st)
     return out

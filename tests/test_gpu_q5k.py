@@ -9,7 +9,7 @@ import pytest
 import torch
 
 import oracle
-from qcheck import bf16_tensor, check_close, dev_u8, to_f32
+from qcheck import abs_gemm, bf16_tensor, check_close, dev_u8, to_f32
 
 pytestmark = pytest.mark.gpu
 
@@ -71,10 +71,11 @@ def test_residual(rt):
     w = rt.q5k_repack(dev_u8(native), n, k)
     a_bits = oracle.bf16_normal((rows, k), seed=10)
     base = np.random.default_rng(11).normal(size=(rows, n)).astype(np.float32)
-    ref = oracle.gemm_a_bf16_w_f32(a_bits, oracle.q45k_decode(native).reshape(n, k)) + base
+    dense = oracle.q45k_decode(native).reshape(n, k)
+    ref = oracle.gemm_a_bf16_w_f32(a_bits, dense) + base
     out = torch.from_numpy(base.copy()).cuda()
     rt.gemm(w, bf16_tensor(a_bits), out=out, residual=out)
-    check_close(out.cpu().numpy(), ref, bf16_out=False, tight=True)
+    check_close(out.cpu().numpy(), ref, bf16_out=False, tight=True, absref=abs_gemm(a_bits, dense))
 
 
 @pytest.mark.parametrize("rows", [1, 16, 64])
@@ -90,4 +91,40 @@ def test_baseline_shape_sampled(rt, rows):
     sub = native.reshape(n, blk)[cols].reshape(-1)
     dense = oracle.q45k_decode(sub).reshape(len(cols), k)
     ref = oracle.gemm_a_bf16_w_f32(a_bits, dense)
-    check_close(got[:, cols], ref, bf16_out=True, tight=True, label=f"q5k full rows={rows}")
+    check_close(got[:, cols], ref, bf16_out=True, tight=True, absref=abs_gemm(a_bits, dense),
+                label=f"q5k full rows={rows}")
+
+
+@pytest.mark.parametrize("rows", [1, 2, 3, 16, 33, 64])
+@pytest.mark.parametrize("split", [True, False])
+def test_dequant_kernel(rt, rows, split):
+    """The MFMA kernel for up to 64 rows, with K split over workgroups (stream-K, a workspace) and
+    without (every band whole)."""
+    n, k = 256, 1280
+    native = oracle.q45k_random_native(n, k, seed=300 + rows)
+    w = rt.q5k_repack(dev_u8(native), n, k)
+    dense = oracle.q45k_decode(native).reshape(n, k)
+    a_bits = oracle.bf16_normal((rows, k), seed=400 + rows)
+    ref = oracle.gemm_a_bf16_w_f32(a_bits, dense)
+    absref = abs_gemm(a_bits, dense)  # the kernel rounds each dequantized weight to bf16
+    ws = None if split else torch.empty(0, dtype=torch.uint8, device="cuda")
+    for out_dtype in (torch.bfloat16, torch.float32):
+        got = rt.gemm(w, bf16_tensor(a_bits), out_dtype=out_dtype, kernel=rt.DEQUANT, workspace=ws)
+        check_close(to_f32(got), ref, bf16_out=out_dtype == torch.bfloat16, tight=True, absref=absref,
+                    label=f"q5k dequant rows={rows} split={split} {out_dtype}")
+
+
+def test_dequant_kernel_remainder_bands_and_residual(rt):
+    """More column bands than compute units with a remainder (whole bands and stream-K ranges in one
+    launch), fp32 residual in place."""
+    n, k, rows = 256 * 64 + 128, 768, 40
+    native = oracle.q45k_random_native(n, k, seed=501)
+    w = rt.q5k_repack(dev_u8(native), n, k)
+    a_bits = oracle.bf16_normal((rows, k), seed=502)
+    base = np.random.default_rng(503).normal(size=(rows, n)).astype(np.float32)
+    dense = oracle.q45k_decode(native).reshape(n, k)
+    ref = oracle.gemm_a_bf16_w_f32(a_bits, dense) + base
+    out = torch.from_numpy(base.copy()).cuda()
+    rt.gemm(w, bf16_tensor(a_bits), out=out, residual=out, kernel=rt.DEQUANT)
+    check_close(out.cpu().numpy(), ref, bf16_out=False, tight=True, absref=abs_gemm(a_bits, dense),
+                label="q5k dequant remainder")
