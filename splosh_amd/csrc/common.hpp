@@ -61,6 +61,12 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void *base, uint32_t bytes) {
 __device__ __forceinline__ u32x4 buffer_load16(rsrc_t r, uint32_t voffset, uint32_t soffset) {
     return __builtin_amdgcn_raw_buffer_load_b128(r, (int)voffset, (int)soffset, 0);
 }
+// A load of streamed data (read once): the cache-policy bits of the instruction (gfx94x: sc0 = 1,
+// nt = 2, sc1 = 16) as a template argument.
+template <int CPOL>
+__device__ __forceinline__ u32x4 buffer_load16_cp(rsrc_t r, uint32_t voffset, uint32_t soffset) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, (int)voffset, (int)soffset, CPOL);
+}
 __device__ __forceinline__ uint32_t buffer_load_u32(rsrc_t r, uint32_t voffset, uint32_t soffset) {
     return __builtin_amdgcn_raw_buffer_load_b32(r, (int)voffset, (int)soffset, 0);
 }

@@ -30,6 +30,9 @@
 #include "launch.hpp"
 
 #include <cstdlib>
+#include <type_traits>
+// Weight codes are read once: non-temporal loads (gfx94x cache policy nt).
+constexpr int kStreamCpol = 2;
 
 namespace splosh {
 
@@ -69,21 +72,57 @@ __device__ __forceinline__ float cvt_byte(uint32_t x, int j) {
     return r;
 }
 
-// Eight weights of one code word, dequantized and rounded to bf16 in k order.
-__device__ __forceinline__ bf16x8 dequant_word(uint32_t w, float s, float b) {
-    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+// fma(x, s, b) with x the binary16 number in the low (HI = false) or high half of `h`, widened
+// exactly: v_fma_mix_f32, one instruction and one rounding.
+template <bool HI>
+__device__ __forceinline__ float fma_mix(uint32_t h, float s, float b) {
+    float r;
+    if (HI)
+        asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h), "v"(s), "v"(b));
+    else
+        asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h), "v"(s), "v"(b));
+    return r;
+}
+
+// Coefficients for dequant_word_mix from a group's scale s and bias b: nibbles become the
+// binary16 numbers 1024 + q (bits 0..3 of a half) or 1024 + 16 q (bits 4..7), so
+// s q + b = fma(1024 + q, s, b - 1024 s) = fma(1024 + 16 q, s / 16, b - 64 s). s / 16 is exact and
+// so is b - 1024 s whenever the exponents of b and 1024 s are less than 16 apart (any practical
+// affine group); then the result is the one-rounding fp32 s q + b exactly.
+struct MixCoef {
+    float s, b0, s16, b1;
+};
+__device__ __forceinline__ MixCoef mix_coef(float s, float b) {
+    return MixCoef{s, __builtin_fmaf(-1024.0f, s, b), s * 0.0625f, __builtin_fmaf(-64.0f, s, b)};
+}
+
+// dequant_word with 17 VALU instead of 22: four AND-ORs and a shift build the binary16 pairs
+// (q0, q4), (16 q1, 16 q5), (q2, q6), (16 q3, 16 q7) with exponent bits 0x6400, eight
+// v_fma_mix_f32 scale them, four v_cvt_pk_bf16_f32 pack.
+// (x & mask) | magic in one v_and_or_b32 (the compiler splits it into two VOP2s, since a VOP3 takes no
+// literal here): the mask comes from an SGPR, the magic from a VGPR.
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t magic) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(mask), "v"(magic));
+    return r;
+}
+
+__device__ __forceinline__ bf16x8 dequant_word_mix(uint32_t w, const MixCoef &c, uint32_t magic) {
+    const uint32_t w8 = w >> 8;
+    const uint32_t t0 = and_or(w, 0x000F000Fu, magic), t1 = and_or(w, 0x00F000F0u, magic);
+    const uint32_t t2 = and_or(w8, 0x000F000Fu, magic), t3 = and_or(w8, 0x00F000F0u, magic);
     u32x4 d;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-        d[j] = f32x2_to_bf16x2(__builtin_fmaf(s, cvt_byte(lo, j), b), __builtin_fmaf(s, cvt_byte(hi, j), b));
+    d[0] = f32x2_to_bf16x2(fma_mix<false>(t0, c.s, c.b0), fma_mix<false>(t1, c.s16, c.b1));
+    d[1] = f32x2_to_bf16x2(fma_mix<false>(t2, c.s, c.b0), fma_mix<false>(t3, c.s16, c.b1));
+    d[2] = f32x2_to_bf16x2(fma_mix<true>(t0, c.s, c.b0), fma_mix<true>(t1, c.s16, c.b1));
+    d[3] = f32x2_to_bf16x2(fma_mix<true>(t2, c.s, c.b0), fma_mix<true>(t3, c.s16, c.b1));
     return as_bf16x8(d);
 }
 
 // q4 (MLX affine): a step is KW groups of 64; wave kw takes group ga + t KW + kw and lane (r, h)
 // feeds column r from words 4 h .. 4 h + 3 of the group's 32-byte record (one 16-byte load; a
 // wave reads 32 consecutive records, a contiguous kilobyte of the tiled layout). A word becomes
-// eight bf16 weights RNE(s q + b): two ANDs split the nibbles, v_cvt_f32_ubyte0..3 converts,
-// v_fma_f32 scales, v_cvt_pk_bf16_f32 packs -- 22 VALU.
+// eight bf16 weights RNE(s q + b) in 17 VALU (dequant_word_mix).
 //
 // Tiled weights stage a step's sidecars for the band (NW weights x {scale, bias} x KW groups x
 // band columns of bf16) through LDS: waves 0 .. 2 NW - 1 each load one array of one weight, lane
@@ -108,7 +147,8 @@ struct Q4Format {
     u32x4 sr;
     u32x4 wq[D][NW];
     uint32_t wsc[D][NW], wbi[D][NW];
-    float sv[NW], bv[NW];  // scale and bias of the step being dequantized
+    MixCoef cf[NW];  // coefficients of the step being dequantized
+    uint32_t magic;  // 0x64006400 (binary16 1024 in both halves), kept in a VGPR
 
     __device__ Q4Format(const MmaArgs &args, int wave_, int lane_) : wave(wave_), lane(lane_) {
         kw = wave / CW;
@@ -128,6 +168,7 @@ struct Q4Format {
                               args.sidecar_bytes);
         side_loader = kStageSide && wave < 2 * NW && lane < 8 * KW;
         sr = u32x4{0u, 0u, 0u, 0u};
+        asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic));
     }
     __device__ int steps(int ga_, int gb_) const { return (gb_ - ga_ + KW - 1) / KW; }
     __device__ bool active(int t) const { return ga + t * KW + kw < gb; }
@@ -169,28 +210,31 @@ struct Q4Format {
         const uint32_t ug = (uint32_t)__builtin_amdgcn_readfirstlane(g);
 #pragma unroll
         for (int w = 0; w < NW; ++w) {
-            wq[slot][w] = buffer_load16(q_rsrc[w], q_lane, ug * q_group);
+            wq[slot][w] = buffer_load16_cp<kStreamCpol>(q_rsrc[w], q_lane, ug * q_group);
             if (!kStageSide) {
                 wsc[slot][w] = buffer_load_u16(s_rsrc[w], side_lane, ug * side_group);
                 wbi[slot][w] = buffer_load_u16(b_rsrc[w], side_lane, ug * side_group);
             }
         }
     }
-    // Sidecars of the step whose codes sit in `slot` and whose staged sidecars sit in `sbuf`.
-    __device__ void prepare(int slot, const char *sbuf) {
+    // Sidecars of the step whose codes sit in `slot` and whose staged sidecars sit in `sbuf`
+    // (zeros when the step has no group for this wave).
+    __device__ void prepare(int slot, const char *sbuf, bool on) {
 #pragma unroll
         for (int w = 0; w < NW; ++w) {
+            uint32_t sb, bb;
             if (kStageSide) {
                 const char *base = sbuf + (((w * 2) * KW + kw) * kBandCols + cw * 32 + r) * 2;
-                sv[w] = bf16_bits_to_f32(*(const uint16_t *)base);
-                bv[w] = bf16_bits_to_f32(*(const uint16_t *)(base + KW * kBandCols * 2));
+                sb = *(const uint16_t *)base;
+                bb = *(const uint16_t *)(base + KW * kBandCols * 2);
             } else {
-                sv[w] = bf16_bits_to_f32(wsc[slot][w]);
-                bv[w] = bf16_bits_to_f32(wbi[slot][w]);
+                sb = wsc[slot][w];
+                bb = wbi[slot][w];
             }
+            cf[w] = mix_coef(on ? bf16_bits_to_f32(sb) : 0.0f, on ? bf16_bits_to_f32(bb) : 0.0f);
         }
     }
-    __device__ bf16x8 operand(int w, int i, int slot) { return dequant_word(wq[slot][w][i], sv[w], bv[w]); }
+    __device__ bf16x8 operand(int w, int i, int slot) { return dequant_word_mix(wq[slot][w][i], cf[w], magic); }
 };
 
 // GGUF Q5_K in plane form (GgufPlanes.swift:8-20): a step is one 256-element block; wave kw takes
@@ -270,14 +314,14 @@ struct Q5Format {
     }
     __device__ void load_w(int slot, int t) {
         const uint32_t b = block(t);
-        wq[slot] = buffer_load16(p0_rsrc, p0_lane, b * (8u * 128u * 16u));
+        wq[slot] = buffer_load16_cp<kStreamCpol>(p0_rsrc, p0_lane, b * (8u * 128u * 16u));
         wh[slot] = buffer_load_u32(p1_rsrc, p1_lane, b * (8u * 128u * 4u));
     }
     // Scale and minimum of group j = 2 kw + h (GgufQuant.swift:196-203): packed byte k is meta byte
     // 4 + k, so for j < 4 (kw < 2, wave-uniform) sc and mn are the low six bits of meta bytes 4 + j
     // and 8 + j; for j >= 4 they are the nibbles of byte 12 + (j - 4) joined with the top two bits
     // of bytes 4 + (j - 4) and 8 + (j - 4). Either way the byte within its word is 2 (kw & 1) + h.
-    __device__ void prepare(int, const char *sbuf) {
+    __device__ void prepare(int, const char *sbuf, bool on) {
         const u32x4 m = *(const u32x4 *)(sbuf + (cw * 32 + r) * 16);
         const float d = half_bits_to_f32(m[0]), dmin = half_bits_to_f32(m[0] >> 16);
         const uint32_t sh = 8u * (2u * (kw & 1) + h);
@@ -289,8 +333,8 @@ struct Q5Format {
             sc = __builtin_amdgcn_ubfe(m[3], sh, 4) | (__builtin_amdgcn_ubfe(m[1], sh + 6, 2) << 4);
             mn = __builtin_amdgcn_ubfe(m[3], sh + 4, 4) | (__builtin_amdgcn_ubfe(m[2], sh + 6, 2) << 4);
         }
-        scaled = d * (float)sc;
-        offset = -(dmin * (float)mn);
+        scaled = on ? d * (float)sc : 0.0f;
+        offset = on ? -(dmin * (float)mn) : 0.0f;
     }
     __device__ float weight(uint32_t codes, int j) const { return __builtin_fmaf(cvt_byte(codes, j), scaled, offset); }
     __device__ bf16x8 operand(int, int i, int slot) {
@@ -396,11 +440,14 @@ mma_kernel(MmaArgs args) {
         fmt.begin(args, band, ga, gb);
 
         u32x4 ar[S::kAPer];  // the next chunk's pieces, on their way to LDS
-        auto load_a = [&](int t) {
+        // Pieces [j0, j1) of chunk t.
+        auto load_a_part = [&](int t, int j0, int j1) {
             const uint32_t gbyte = (uint32_t)(ga * F::kUnitK + t * KW * 64) * 2u;
 #pragma unroll
-            for (int j = 0; j < S::kAPer; ++j) ar[j] = buffer_load16(a_rsrc, a_src[j] + gbyte, 0);
+            for (int j = j0; j < j1; ++j) ar[j] = buffer_load16(a_rsrc, a_src[j] + gbyte, 0);
         };
+        auto load_a = [&](int t) { load_a_part(t, 0, S::kAPer); };
+        constexpr int kAHalf = (S::kAPer + 1) / 2;
         auto store_a = [&](int buf) {
 #pragma unroll
             for (int j = 0; j < S::kAPer; ++j)
@@ -412,8 +459,8 @@ mma_kernel(MmaArgs args) {
         // Dequantized weights of the current step; operand i is replaced by the next step's as
         // soon as the MFMAs of sub-step i have been issued.
         bf16x8 bw[NW][4];
-        auto dequant = [&](int slot_, int sbuf) {
-            fmt.prepare(slot_, side_lds + sbuf * S::kSBuf);
+        auto dequant = [&](int slot_, int sbuf, bool on) {
+            fmt.prepare(slot_, side_lds + sbuf * S::kSBuf, on);
 #pragma unroll
             for (int w = 0; w < NW; ++w)
 #pragma unroll
@@ -431,12 +478,13 @@ mma_kernel(MmaArgs args) {
         // The step count is padded to a multiple of 3: steps past T compute nothing but keep the
         // load pattern regular (their loads re-read in-bounds data). Each step has its barrier in
         // the middle, between MFMA sub-steps 1 and 2. There the wave waits for its pieces of the
-        // next step's chunk (loaded a step earlier), stores them to LDS, passes the barrier, reads
-        // the next step's first activation fragments and issues the loads of chunk t + 2 and of
-        // the weights of step t + 3. Loads return in order, so "chunk t + 1 has arrived" is
-        // "at most the weight loads issued after it are outstanding". The chunk buffer written
-        // (t + 1 mod 3) last held chunk t - 2, which every wave finished before the previous
-        // barrier. LDS latency and the barrier hide behind sub-steps 2 and 3.
+        // next step's chunk (loaded a step earlier), stores them to LDS, passes the barrier and
+        // reads the next step's first activation fragments; the loads of chunk t + 2 and of the
+        // weights of step t + 3 are issued around it (see the hooks below). Loads return in
+        // order, so "chunk t + 1 has arrived" is "at most the weight loads issued after it are
+        // outstanding". The chunk buffer written (t + 1 mod 3) last held chunk t - 2, which every
+        // wave finished before the previous barrier. LDS latency and the barrier hide behind
+        // sub-steps 2 and 3.
         const int Tp = (T + D - 1) / D * D;
         auto nbuf = [&](int b) { return b == S::kNB - 1 ? 0 : b + 1; };
         load_a(0);
@@ -453,7 +501,7 @@ mma_kernel(MmaArgs args) {
         load_s(2);
         load_w(2, 2);
         lds_barrier();
-        dequant(0, 0);
+        dequant(0, 0, T > 0 && fmt.active(0));
         auto read_af = [&](bf16x8 *dst, int buf, int i) {
             const char *ap = lds_bytes + buf * S::kABuf;
 #pragma unroll
@@ -463,11 +511,15 @@ mma_kernel(MmaArgs args) {
         read_af(af_pre, 0, 0);
 
         // Step t: MFMA sub-steps with the dequantization of step t + 1 interleaved, `mid` between
-        // sub-steps 1 and 2. Inactive waves (no unit in step t) only dequantize.
-        auto step = [&](int t, int d, int abuf, auto &&mid) {
+        // sub-steps 1 and 2.
+        // Every step issues its MFMAs; a step with no unit for this wave (stream-K tails, padding)
+        // gets zero coefficients, so its weights dequantize to exact zeros and add nothing (an
+        // infinite activation would turn that into NaN, where its row is not finite anyway). A
+        // branch-free body keeps the register allocation of one path.
+        auto live = [&](int t) { return t < T && fmt.active(t); };
+        auto step = [&](int t, int d, int abuf, auto &&mid, auto &&hook) {
             const int next = (d + 1) % D;
-            const bool active = t < T && fmt.active(t);
-            fmt.prepare(next, side_lds + nbuf(abuf) * S::kSBuf);
+            fmt.prepare(next, side_lds + nbuf(abuf) * S::kSBuf, live(t + 1));
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 if (i == 2) mid();
@@ -478,55 +530,67 @@ mma_kernel(MmaArgs args) {
                 } else {
                     read_af(af, abuf, i);
                 }
-                if (active) {
 #pragma unroll
-                    for (int w = 0; w < NW; ++w)
+                for (int w = 0; w < NW; ++w)
 #pragma unroll
-                        for (int f = 0; f < FM; ++f)
-                            acc[w][f] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[f], bw[w][i], acc[w][f], 0, 0, 0);
-                }
+                    for (int f = 0; f < FM; ++f)
+                        acc[w][f] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[f], bw[w][i], acc[w][f], 0, 0, 0);
 #pragma unroll
                 for (int w = 0; w < NW; ++w) bw[w][i] = fmt.operand(w, i, next);
+                hook(i);
+                __builtin_amdgcn_sched_barrier(0);  // sub-steps stay in order (register pressure)
             }
         };
 
-        // Sidecars run one step ahead of the chunks: those of step t + 2 are stored at the middle
-        // of step t (buffer t + 2 mod 3, last used for step t - 1's dequantization in step t - 2)
-        // and read while step t + 1 dequantizes step t + 2.
+        // Loads are spread over the step so that the workgroup's waves do not all queue at the
+        // texture unit at once: sub-step 0 issues the weights of step t + 3 (their ring slot was
+        // dequantized in step t - 1), sub-steps 2 and 3 the halves of chunk t + 2 and the
+        // sidecars of step t + 3, after `mid` has stored the previous contents of those registers.
+        // So the last loads before "chunk t + 1 and sidecars t + 2" are complete are always the
+        // kWLoads weight loads of the current step. Sidecars run one step ahead of the chunks:
+        // those of step t + 2 are stored at the middle of step t (buffer t + 2 mod 3, last used
+        // for step t - 1's dequantization in step t - 2) and read while step t + 1 dequantizes
+        // step t + 2.
         int abuf = 0;  // buffer of step t's chunk
         for (int t0 = 0; t0 < Tp - D; t0 += D) {
 #pragma unroll
             for (int d = 0; d < D; ++d) {
                 const int t = t0 + d;
-                step(t, d, abuf, [&] {
-                    wait_vmcnt<kWLoads>();  // chunk t + 1, sidecars t + 2 have arrived
-                    store_a(nbuf(abuf));
-                    store_s(nbuf(nbuf(abuf)));
-                    lds_barrier();
-                    read_af(af_pre, nbuf(abuf), 0);
-                    load_a(t + 2);
-                    load_s(t + 3);
-                    load_w(d, t + D);
-                });
+                step(t, d, abuf,
+                     [&] {
+                         wait_vmcnt<kWLoads>();  // chunk t + 1, sidecars t + 2 have arrived
+                         store_a(nbuf(abuf));
+                         store_s(nbuf(nbuf(abuf)));
+                         lds_barrier();
+                         read_af(af_pre, nbuf(abuf), 0);
+                     },
+                     [&](int i) {
+                         if (i == 0) load_w(d, t + D);
+                         if (i == 2) {
+                             load_a_part(t + 2, 0, kAHalf);
+                             load_s(t + 3);
+                         }
+                         if (i == 3) load_a_part(t + 2, kAHalf, S::kAPer);
+                     });
                 abuf = nbuf(abuf);
             }
         }
-        // The last three steps: chunk Tp - 1 is loaded in the first of them, nothing after.
+        // The last three steps load only chunk Tp - 1 (in the first of them).
 #pragma unroll
         for (int d = 0; d < D; ++d) {
             const int t = Tp - D + d;
-            step(t, d, abuf, [&] {
-                if (d == 0) {
-                    wait_vmcnt<kWLoads>();
-                } else {
-                    wait_vmcnt<0>();
-                }
-                if (d < 2) store_a(nbuf(abuf));
-                if (d == 0) store_s(nbuf(nbuf(abuf)));
-                lds_barrier();
-                if (d < 2) read_af(af_pre, nbuf(abuf), 0);
-                if (d == 0) load_a(t + 2);
-            });
+            step(t, d, abuf,
+                 [&] {
+                     wait_vmcnt<0>();
+                     if (d < 2) store_a(nbuf(abuf));
+                     if (d == 0) store_s(nbuf(nbuf(abuf)));
+                     lds_barrier();
+                     if (d < 2) read_af(af_pre, nbuf(abuf), 0);
+                 },
+                 [&](int i) {
+                     if (d == 0 && i == 2) load_a_part(t + 2, 0, kAHalf);
+                     if (d == 0 && i == 3) load_a_part(t + 2, kAHalf, S::kAPer);
+                 });
             abuf = nbuf(abuf);
         }
         lds_barrier();  // every wave is past its last fragment read
