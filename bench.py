@@ -227,7 +227,7 @@ def main():
     ap.add_argument("--workload", default="verify64")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="launch from the host every step (no HIP graph)")
-    ap.add_argument("--kernel", default="AUTO", choices=["AUTO", "STREAM", "DEQUANT", "TILE", "SCALAR"])
+    ap.add_argument("--kernel", default="AUTO", choices=["AUTO", "STREAM", "DEQUANT", "TILE", "SCALAR", "PREFILL"])
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB ten times (the reference kernel for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings) and exit")

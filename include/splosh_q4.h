@@ -64,13 +64,18 @@ typedef enum splosh_dtype { SPLOSH_F32 = 0, SPLOSH_BF16 = 1 } splosh_dtype;
 /* Kernel choice (the reference selects kernels through SPLOSH_* environment variables,
  * Runtime/Engine.swift:380-440; here the caller names one, or AUTO picks by rows). */
 typedef enum splosh_kernel {
-    SPLOSH_KERNEL_AUTO = 0,     /* rows <= 2: STREAM; 3..64: DEQUANT; more: TILE; else SCALAR */
+    SPLOSH_KERNEL_AUTO = 0,     /* rows <= 2: STREAM; 3..64: DEQUANT; more: PREFILL for one tiled
+                                   weight with lda % 8 == 0 and ldc % 4 == 0, else TILE; SCALAR for
+                                   operands no other kernel takes */
     SPLOSH_KERNEL_STREAM = 1,   /* weight streaming on raw codes: lane-per-row VALU kernel for
                                    1-2 rows, raw-code MFMA kernels above */
     SPLOSH_KERNEL_DEQUANT = 2,  /* rows <= 64: stream-K MFMA kernel on weights dequantized to bf16 in
                                    registers; uses the workspace for split bands when given one */
     SPLOSH_KERNEL_TILE = 3,     /* any rows: LDS-tiled dequant-to-bf16 MFMA GEMM (prefill) */
-    SPLOSH_KERNEL_SCALAR = 4    /* one thread per output (gemm_q4.metal semantics) */
+    SPLOSH_KERNEL_SCALAR = 4,   /* one thread per output (gemm_q4.metal semantics) */
+    SPLOSH_KERNEL_PREFILL = 5   /* one TILED128 weight (not mlp_in): 256 x 256 output tiles, one
+                                   wave per SIMD, weights dequantized in registers; uses the
+                                   workspace to split the last round of tiles over all CUs */
 } splosh_kernel;
 
 /* Q4BufferLayout (Quant/Q4BufferLayout.swift:29-79). */

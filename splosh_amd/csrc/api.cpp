@@ -101,16 +101,31 @@ int q4_gemm_impl(const splosh_q4_weight *w, const splosh_q4_weight *up, const ui
                         (w->order == SPLOSH_Q4_TILED128 || w->row_stride_words % 4 == 0);
     const bool tile_ok = wide16 && splosh::tile_fits(rows, w->rows, lda, w->row_stride_words);
     const bool mma_ok = wide16 && splosh::mma_fits(rows, w->rows, w->inner, w->row_stride_words, lda);
+    const bool prefill_ok = wide16 && !up && w->order == SPLOSH_Q4_TILED128 && aligned(out, 16) &&
+                            (!residual || aligned(residual, 16)) &&
+                            splosh::prefill_fits(rows, w->rows, w->inner, lda, ldc);
     int choice = kernel;
     if (choice == SPLOSH_KERNEL_AUTO) {
         if (!eligible) choice = SPLOSH_KERNEL_SCALAR;
         else if (wide16 && splosh::lanes_fit(rows, w->rows, w->inner, w->row_stride_words, up != nullptr))
             choice = SPLOSH_KERNEL_STREAM;
         else if (mma_ok) choice = SPLOSH_KERNEL_DEQUANT;
+        else if (prefill_ok) choice = SPLOSH_KERNEL_PREFILL;
         else if (tile_ok) choice = SPLOSH_KERNEL_TILE;
         else choice = SPLOSH_KERNEL_STREAM;
     }
     switch (choice) {
+        case SPLOSH_KERNEL_PREFILL: {
+            if (!prefill_ok)
+                return fail(SPLOSH_ERR_UNSUPPORTED,
+                            "prefill kernel needs one TILED128 weight, lda % 8 == 0, ldc % 4 == 0 and 16-byte "
+                            "aligned operands");
+            const splosh::PrefillPlan plan =
+                splosh::plan_prefill(rows, w->rows, w->inner / kGroupSize, workspace ? workspace_bytes : 0);
+            return hip_status(splosh::launch_q4_prefill(plan, *w, a, lda, out, ldc, out_dtype, residual, rows,
+                                                        workspace, stream),
+                              "q4 prefill launch");
+        }
         case SPLOSH_KERNEL_TILE: {
             if (!tile_ok)
                 return fail(SPLOSH_ERR_UNSUPPORTED,
@@ -300,7 +315,9 @@ size_t splosh_workspace_bytes(int64_t rows, int64_t columns, int64_t inner) {
     const int64_t groups = inner / kGroupSize;
     const size_t tile = splosh::tile_workspace_bytes(rows, columns, groups, true);
     const size_t mma = rows <= 64 ? splosh::mma_workspace_bytes(rows, columns, groups, true) : 0;
-    return tile > mma ? tile : mma;
+    const size_t prefill = rows > 64 && columns % 128 == 0 ? splosh::prefill_workspace_bytes(rows, columns, groups) : 0;
+    size_t need = tile > mma ? tile : mma;
+    return need > prefill ? need : prefill;
 }
 
 // Q4GemmRuntime.dispatch (Runtime/Q4Runtime.swift:94-145).

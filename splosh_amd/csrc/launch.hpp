@@ -103,6 +103,22 @@ hipError_t launch_q4_tile(const TilePlan &plan, const splosh_q4_weight &w, const
                           const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype, const void *residual,
                           int64_t rows, void *workspace, hipStream_t stream);
 
+// The prefill kernel for one tiled weight (prefill.hip): 256 x 256 tiles, one wave per SIMD,
+// weights dequantized in registers; stream-K over a caller workspace of prefill_workspace_bytes().
+struct PrefillPlan {
+    int mblocks;       // row blocks of 256
+    int tiles;
+    int grid;
+    int dp_tiles;      // tiles computed whole (a multiple of grid)
+    int64_t sk_units;  // (tile, group) pairs of the other tiles, split evenly over the grid
+};
+bool prefill_fits(int64_t rows, int64_t columns, int64_t inner, int64_t lda, int64_t ldc);
+PrefillPlan plan_prefill(int64_t rows, int64_t columns, int64_t groups, size_t workspace_bytes);
+size_t prefill_workspace_bytes(int64_t rows, int64_t columns, int64_t groups);
+hipError_t launch_q4_prefill(const PrefillPlan &plan, const splosh_q4_weight &w, const uint16_t *a, int64_t lda,
+                             void *out, int64_t ldc, int out_dtype, const void *residual, int64_t rows,
+                             void *workspace, hipStream_t stream);
+
 hipError_t launch_q5k_dequant(const splosh_q5k_weight &w, float *out, hipStream_t stream);
 hipError_t launch_q5k_repack(const uint8_t *native, int64_t rows, int64_t inner, uint8_t *p0,
                              uint8_t *p1, uint8_t *meta, bool inverse, hipStream_t stream);

@@ -24,6 +24,7 @@ STREAM = _lib.KERNEL_STREAM
 DEQUANT = _lib.KERNEL_DEQUANT
 TILE = _lib.KERNEL_TILE
 SCALAR = _lib.KERNEL_SCALAR
+PREFILL = _lib.KERNEL_PREFILL
 ROW_MAJOR = _lib.ROW_MAJOR
 TILED128 = _lib.TILED128
 

@@ -240,3 +240,38 @@ def test_prefill_shape_sampled(rt):
     sel = np.sort(rng.choice(rows, 512, replace=False))
     ref, absref = _sampled_reference(w, np.ascontiguousarray(a_bits[sel]), cols)
     check_close(got[sel][:, cols], ref, bf16_out=True, tight=True, absref=absref, label="prefill")
+
+
+@pytest.mark.parametrize("rows,n,k", [(256, 256, 640), (300, 384, 576), (513, 128, 64)])
+@pytest.mark.parametrize("split", [True, False])
+def test_prefill_kernel(rt, rows, n, k, split):
+    """The one-wave-per-SIMD prefill kernel: whole and partial 256 x 256 tiles, with the last round
+    of tiles split over all workgroups (stream-K, a workspace) and without (every tile whole)."""
+    case = Q4Case(n, k, seed=rows + n)
+    a_bits = oracle.bf16_normal((rows, k), seed=k)
+    ref = oracle.gemm_a_bf16_w_f32(a_bits, case.dense)
+    absref = abs_gemm(a_bits, case.dense)
+    ws = None if split else torch.empty(0, dtype=torch.uint8, device="cuda")
+    for out_dtype in (torch.bfloat16, torch.float32):
+        got = rt.gemm(case.w_tiled, bf16_tensor(a_bits), out_dtype=out_dtype, kernel=rt.PREFILL, workspace=ws)
+        check_close(to_f32(got), ref, bf16_out=out_dtype == torch.bfloat16, tight=True, absref=absref,
+                    label=f"prefill {rows}x{n}x{k} split={split} {out_dtype}")
+    base = np.random.default_rng(3).normal(size=(rows, n)).astype(np.float32)
+    out = torch.from_numpy(base.copy()).cuda()
+    rt.gemm(case.w_tiled, bf16_tensor(a_bits), out=out, residual=out, kernel=rt.PREFILL, workspace=ws)
+    check_close(out.cpu().numpy(), ref + base, bf16_out=False, tight=True, absref=absref,
+                label=f"prefill residual {rows}x{n}x{k} split={split}")
+
+
+def test_prefill_down_shape_sampled(rt):
+    """Config 2's second shape (M=2048, K=17408 -> N=5120: 160 tiles, all split over the CUs) at
+    full size, 256 sampled columns of 256 sampled rows."""
+    n, k, rows = 5120, 17408, 2048
+    w = _full_size_weight(rt, n, k, seed=11)
+    a_bits = oracle.bf16_normal((rows, k), seed=12)
+    got = to_f32(rt.gemm(w, bf16_tensor(a_bits)))
+    rng = np.random.default_rng(13)
+    cols = np.sort(rng.choice(n, 256, replace=False))
+    sel = np.sort(rng.choice(rows, 256, replace=False))
+    ref, absref = _sampled_reference(w, np.ascontiguousarray(a_bits[sel]), cols)
+    check_close(got[sel][:, cols], ref, bf16_out=True, tight=True, absref=absref, label="prefill down")
