@@ -150,12 +150,17 @@ q4_prefill_kernel(PrefillArgs args) {
 #pragma unroll
                 for (int e = 0; e < 16; ++e) acc[f][j][e] = 0.0f;
 
+        // Prologue, in the loop's load order (chunk, then codes), so that the wait counts the
+        // compiler derives at the loop head leave the codes in flight.
         load_a(0);
         load_w(0, 0);
         load_w(1, 1);
-        load_w(2, 2);
         store_a(0);
+        __builtin_amdgcn_sched_barrier(0);
         load_a(1);
+        __builtin_amdgcn_sched_barrier(0);
+        load_w(2, 2);
+        __builtin_amdgcn_sched_barrier(0);
         lds_barrier();
         prepare(0, T > 0);
 #pragma unroll
@@ -165,19 +170,31 @@ q4_prefill_kernel(PrefillArgs args) {
         bf16x8 af[8];
         read_af(af, 0, 0);
 
-        // Step t (group ga + t) with d = t mod 3 = its activation buffer and code ring slot. In
-        // MFMA step 1 the wave stores chunk t + 1 (buffer t + 1 mod 3, last read in step t - 2) and
-        // passes the barrier, after which chunk t + 1 is readable and, since every wave has then
-        // finished step t - 1, buffer t + 2 mod 3 may be written in step t + 1. Then it loads
-        // chunk t + 2 and the codes of step t + 3 into the ring slot of step t, whose weights were
-        // dequantized in step t - 1. Loads past the job re-read its last group.
+        // Step t (group ga + t), d = t mod 3 = its activation buffer and code ring slot. Every
+        // MFMA step interleaves its 16 MFMAs with the dequantization of the next group's operand
+        // i (with one wave per SIMD the VALU work only hides under the matrix core when its
+        // instructions sit between the MFMAs), the next MFMA step's fragment reads and a share of
+        // the memory traffic, spread so that no step queues at the texture unit:
+        //  * steps 0 and 1 store chunk t + 1 (loaded in step t - 1) into buffer t + 1 mod 3, half
+        //    each, and steps 1 and 2 load chunk t + 2 into the registers just stored;
+        //  * the barrier before step 2 makes chunk t + 1 readable (step 3 prefetches its first
+        //    fragments); since every wave has then finished step t - 1, buffer t + 2 mod 3 (read
+        //    last in step t - 1) may be written in step t + 1;
+        //  * steps 2 and 3 load the codes of step t + 3 into the ring slot of step t, whose
+        //    weights were dequantized in step t - 1.
+        // Loads past the job re-read its last group.
         auto step = [&](int t, int d) {
             const int next = d == 2 ? 0 : d + 1;
             prepare(next, t + 1 < T);  // zero coefficients for the padding steps
+            const uint32_t ga_next = clampg(t + 2) * 128u, gw = clampg(t + 3);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
+                if (i == 2) {
+                    lds_barrier();
+                    __builtin_amdgcn_sched_barrier(0);
+                }
                 bf16x8 an[8];
-                if (i < 3) read_af(an, d, i + 1);
+                read_af(an, i < 3 ? d : next, i < 3 ? i + 1 : 0);
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -185,16 +202,35 @@ q4_prefill_kernel(PrefillArgs args) {
                         acc[f][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[f], bw[j][i], acc[f][j], 0, 0, 0);
 #pragma unroll
                 for (int j = 0; j < 2; ++j) bw[j][i] = dequant_word_mix(wq[next][j][i], cf[j], magic);
-                if (i == 1) {
-                    store_a(next);
-                    lds_barrier();
-                    load_a(t + 2);
-                    load_w(d, t + 3);
+                // Chunk t + 1: pieces 4 i .. 4 i + 3 stored in steps 0 and 1 and reloaded (for
+                // chunk t + 2) in steps 1 and 2, half the LDS writes in each of the first steps.
+                if (i < 2) {
+#pragma unroll
+                    for (int p = 4 * i; p < 4 * i + 4; ++p) *(u32x4 *)(lds + next * kPABuf + a_lds(p)) = ar[p];
                 }
-                if (i == 3) read_af(an, next, 0);
+                if (i == 1 || i == 2) {
+#pragma unroll
+                    for (int p = 4 * (i - 1); p < 4 * i; ++p) ar[p] = buffer_load16(a_rsrc, a_src[p] + ga_next, 0);
+                }
+                if (i >= 2) {
+                    const int j = i - 2;
+                    wq[d][j] = buffer_load16_cp<2>(q_rsrc, q_lane[j], gw * (128u * 32u));
+                    ws[d][j] = buffer_load_u16(s_rsrc, s_lane[j], gw * 256u);
+                    wb[d][j] = buffer_load_u16(b_rsrc, s_lane[j], gw * 256u);
+                }
+#pragma unroll
+                for (int m = 0; m < 16; ++m) {
+                    if (m < 8) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);             // one MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);             // two VALU
+                    if (m % 2 == 1) {
+                        if (i < 2 && m < 8) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // LDS write
+                        if (i > 0) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);         // VMEM read
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int f = 0; f < 8; ++f) af[f] = an[f];
-                __builtin_amdgcn_sched_barrier(0);
             }
         };
         // The step count is padded to a multiple of three (no early exit, whose extra paths cost
@@ -252,24 +288,34 @@ q4_prefill_kernel(PrefillArgs args) {
         }
     };
 
+    // The jobs: whole tiles blockIdx.x, blockIdx.x + P, ... below dp_tiles, then this workgroup's
+    // range of the remaining (tile, group) pairs, cut at tile boundaries. One call site, so that
+    // run_job is inlined.
     const int P = gridDim.x;
-    for (int tile = blockIdx.x; tile < args.dp_tiles; tile += P) {
-        run_job(tile, 0, G, -1);
-        lds_barrier();  // the next job stores into buffer 0, which slow waves may still read
-    }
-    if (args.sk_units > 0) {
-        int64_t u = args.sk_units * blockIdx.x / P;
-        const int64_t u_end = args.sk_units * (blockIdx.x + 1) / P;
-        int slot = 0;
-        while (u < u_end) {
-            const int tile = args.dp_tiles + (int)(u / G);
-            const int ga = (int)(u % G);
-            const int gb = (int)((int64_t)ga + (u_end - u) < G ? ga + (u_end - u) : G);
-            run_job(tile, ga, gb, (ga == 0 && gb == G) ? -1 : slot);
-            lds_barrier();
+    int dp_tile = blockIdx.x;
+    int64_t u = args.sk_units * blockIdx.x / P;
+    const int64_t u_end = args.sk_units * (blockIdx.x + 1) / P;
+    int slot = 0;
+    for (;;) {
+        int tile, ga, gb, job_slot;
+        if (dp_tile < args.dp_tiles) {
+            tile = dp_tile;
+            ga = 0;
+            gb = G;
+            job_slot = -1;
+            dp_tile += P;
+        } else if (u < u_end) {
+            tile = args.dp_tiles + (int)(u / G);
+            ga = (int)(u % G);
+            gb = (int)((int64_t)ga + (u_end - u) < G ? ga + (u_end - u) : G);
+            job_slot = (ga == 0 && gb == G) ? -1 : slot;
             u += gb - ga;
             slot = 1;
+        } else {
+            break;
         }
+        run_job(tile, ga, gb, job_slot);
+        lds_barrier();  // the next job stores into buffer 0, which slow waves may still read
     }
 }
 
