@@ -3,19 +3,21 @@
 //
 // A workgroup of four waves computes a 256 x 256 output tile; wave w owns all 256 rows of columns
 // 64 w .. 64 w + 63 (8 x 2 MFMA tiles of 32 x 32: 256 fp32 accumulators a lane, held in AGPRs,
-// which is why the kernel runs one wave per SIMD). Per 64-group of K:
-//  * The activation tile A[256][64] (32 KB) is staged global -> registers -> LDS by all threads,
-//    one group ahead, into one of three buffers (row stride 144 bytes: the operand reads do not
-//    conflict), with one barrier per group, in its middle.
-//  * The weights never pass through LDS: lane (r, h) of wave w loads 16 bytes of the 32-byte tiled
-//    record of column n0 + 64 w + 32 j + r (j = 0, 1) -- words 4 h .. 4 h + 3, the B operands of
-//    the group's four 16-deep MFMA steps -- three groups ahead, with its scale and bias, and turns
-//    each word into eight bf16 weights in 17 VALU (dequant_word_mix) while the previous group's
-//    MFMAs run. Every weight is dequantized exactly once.
+// which is why the kernel runs one wave per SIMD). Per 64-group of K, one "chunk":
+//  * The chunk's activations A[256][64] (32 KB), codes (256 columns x 32 bytes) and sidecars are
+//    staged global -> registers -> LDS by all threads, one group ahead, into one of three buffers
+//    (row strides 144 and 48 bytes: the operand and code reads do not conflict), with one barrier
+//    per group, in its middle.
+//  * Lane (r, h) of wave w reads the 16 bytes of the record of column 64 w + 32 j + r (j = 0, 1)
+//    that hold words 4 h .. 4 h + 3 -- the B operands of the group's four 16-deep MFMA steps -- and
+//    turns each word into eight bf16 weights in 17 VALU (dequant_word_mix) one MFMA step ahead.
+//    Every weight is dequantized exactly once, in registers.
 //  * MFMA step i uses k = 32 h + 8 i .. + 7 for both operands (the order of the code words), so the
 //    A operand of row r is the 16-byte LDS piece 4 h + i of that row.
-// Per group a wave issues 64 MFMAs (2048 cycles of the matrix core) against 136 VALU, 32 LDS
-// operand reads and 16 KB of L2 and HBM traffic per workgroup: the kernel is MFMA-bound.
+// Per group a wave issues 64 MFMAs (2048 cycles of the matrix core) against about 160 VALU, 32 LDS
+// operand reads and 41 KB of L2 and HBM traffic per workgroup: the kernel is MFMA-bound. Within one
+// wave every VALU instruction placed between MFMAs delays the matrix core by about three cycles
+// (measured), so the VALU count per group matters.
 //
 // Work split. Tiles are numbered row block first (tile t: row block t mod MB, column block t / MB),
 // so that with eight row blocks every XCD (workgroup id mod 8) works on one row block and keeps
@@ -53,20 +55,33 @@ struct PrefillArgs {
 };
 
 constexpr int kPB = 256;                       // tile rows and columns
-constexpr int kPThreads = 256;                 // four waves
 constexpr int kPRow = 144;                     // LDS bytes per activation row (128 + 16)
 constexpr int kPABuf = kPB * kPRow;            // one activation buffer
 constexpr int kPEpiRow = 68;                   // floats per row of a wave's epilogue staging
 constexpr int kPEpi = 32 * kPEpiRow * 4;       // bytes of a wave's epilogue staging (32 rows)
-constexpr size_t kPLds = 3 * kPABuf + 4 * kPEpi;
+constexpr int kPCodeRow = 48;                  // LDS bytes per column of a code chunk (32 + 16)
+constexpr int kPCodeBytes = kPB * kPCodeRow;   // the codes of a chunk
+constexpr int kPBuf = kPABuf + kPCodeBytes + 2 * kPB * 2;  // activations, codes, scales and biases
+constexpr size_t kPLds = 3 * kPBuf;            // the epilogue staging reuses the buffers
+static_assert(8 * kPEpi <= (int)kPLds, "eight waves' epilogue staging fits the activation buffers");
 constexpr int kPFinishMax = 1024;              // contributors q4_prefill_finish can list
 
-__global__ void __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+// WM waves per SIMD: 4 WM waves, wave (wm, wn) = (wave / 4, wave % 4) owns rows
+// 256 / WM * wm .. of columns 64 wn ..; the WM waves sharing a SIMD (equal wn) dequantize the same
+// weights, each for its own rows. Only WM = 1 is launched: with two waves per SIMD (128
+// accumulators each) the doubled dequantization costs more than the second wave hides.
+template <int WM>
+__global__ void __launch_bounds__(256 * WM) __attribute__((amdgpu_waves_per_eu(WM, WM)))
 q4_prefill_kernel(PrefillArgs args) {
+    constexpr int kPThreads = 256 * WM;
+    constexpr int FM = 8 / WM;     // 32-row blocks per wave
+    constexpr int kAPer = 8 / WM;  // activation pieces per thread and chunk
+    constexpr int kCPer = 2 / WM;  // code pieces per thread and chunk
     extern __shared__ __align__(16) char lds[];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / 4, wn = wave % 4;
     const int r = lane & 31, h = lane >> 5;
     const int G = (int)args.groups;
     const uint32_t G32 = (uint32_t)G;
@@ -76,161 +91,201 @@ q4_prefill_kernel(PrefillArgs args) {
     const rsrc_t b_rsrc = make_rsrc(args.biases, args.sidecar_bytes);
     uint32_t magic;
     asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic));
-    char *epi = lds + 3 * kPABuf + wave * kPEpi;
+    {
+        // An AGPR operand makes the compiler select the AGPR form of the MFMAs even where a wave's
+        // register budget is 256 (two waves per SIMD): the accumulators then live in AGPRs.
+        float agpr_use;
+        asm volatile("v_accvgpr_write_b32 %0, 0" : "=a"(agpr_use));
+        (void)agpr_use;
+    }
+    char *epi = lds + wave * kPEpi;  // after the main loop, over the activation buffers
 
     // Tile `tile`, groups [ga, gb); slot < 0 writes the output, else a partial.
     auto run_job = [&](int tile, int ga, int gb, int slot) {
         const int mb = tile % args.mblocks, nb = tile / args.mblocks;
         const int64_t m0 = (int64_t)mb * kPB, n0 = (int64_t)nb * kPB;
         const int T = gb - ga;
-        // Activation staging: piece p of this thread is chunk c = p * 256 + tid of the tile, row
-        // c / 8, 16-byte chunk c % 8 of the group's 128 bytes; rows past the last are clamped.
-        uint32_t a_src[8];
+        // Chunk staging (group g of the tile, global -> registers -> LDS buffer):
+        //  * activation piece p of this thread: c = p * threads + tid, row c / 8, 16-byte piece
+        //    c % 8 of the row's 128 bytes (rows past the last clamped);
+        //  * code piece p: c = p * threads + tid, half c % 2 of column c / 2's 32-byte record
+        //    (columns past the last clamped);
+        //  * sidecars: lanes 0..31 of wave 0 (scales) and wave 1 (biases), 8 columns a lane.
+        uint32_t a_src[kAPer], c_src[kCPer];
 #pragma unroll
-        for (int p = 0; p < 8; ++p) {
+        for (int p = 0; p < kAPer; ++p) {
             const int c = p * kPThreads + tid;
             const int64_t m = m0 + (c >> 3);
             a_src[p] = (uint32_t)(((m < args.rows ? m : args.rows - 1) * args.lda + (c & 7) * 8) * 2);
         }
-        auto a_lds = [&](int p) { return (uint32_t)(((p * kPThreads + tid) >> 3) * kPRow + (tid & 7) * 16); };
-        uint32_t q_lane[2], s_lane[2];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int64_t nc = n0 + 64 * wave + 32 * j + r;
+        for (int p = 0; p < kCPer; ++p) {
+            const int c = p * kPThreads + tid;
+            const int64_t nc = n0 + (c >> 1);
             const uint32_t col = (uint32_t)(nc < args.n ? nc : args.n - 1);
-            const uint32_t rec0 = (col >> 7) * G32 * 128u + (col & 127u);
-            q_lane[j] = rec0 * 32u + 16u * h;
-            s_lane[j] = rec0 * 2u;
+            c_src[p] = ((col >> 7) * G32 * 128u + (col & 127u)) * 32u + 16u * (c & 1);
         }
+        const bool side_loader = wave < 2 && lane < 32;
+        uint32_t side_src;
+        {
+            const int64_t nc = n0 + 8 * (lane & 31);
+            const uint32_t col = (uint32_t)(nc < args.n ? nc : args.n - 8);
+            side_src = ((col >> 7) * G32 * 128u + (col & 127u)) * 2u;
+        }
+        const rsrc_t side_rsrc = wave == 1 ? b_rsrc : s_rsrc;
+        auto a_lds = [&](int p) { return (uint32_t)(((p * kPThreads + tid) >> 3) * kPRow + (tid & 7) * 16); };
+        auto c_lds = [&](int p) {
+            const int c = p * kPThreads + tid;
+            return (uint32_t)(kPABuf + (c >> 1) * kPCodeRow + 16 * (c & 1));
+        };
         auto clampg = [&](int t) {
             const int g = ga + t < gb ? ga + t : gb - 1;
             return (uint32_t)__builtin_amdgcn_readfirstlane(g);
         };
 
-        u32x4 ar[8];
-        auto load_a = [&](int t) {
-            const uint32_t off = clampg(t) * 128u;
-#pragma unroll
-            for (int p = 0; p < 8; ++p) ar[p] = buffer_load16(a_rsrc, a_src[p] + off, 0);
-        };
-        auto store_a = [&](int buf) {
-#pragma unroll
-            for (int p = 0; p < 8; ++p) *(u32x4 *)(lds + buf * kPABuf + a_lds(p)) = ar[p];
-        };
-        u32x4 wq[3][2];
-        uint32_t ws[3][2], wb[3][2];
-        auto load_w = [&](int slot, int t) {
+        u32x4 ar[kAPer], cr[kCPer], sr = {0u, 0u, 0u, 0u};
+        // Half 0: the first activation pieces and the codes; half 1: the others and the sidecars.
+        constexpr int kHalf = kAPer / 2;
+        auto load_half = [&](int t, int half) {
             const uint32_t g = clampg(t);
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                wq[slot][j] = buffer_load16_cp<2>(q_rsrc, q_lane[j], g * (128u * 32u));
-                ws[slot][j] = buffer_load_u16(s_rsrc, s_lane[j], g * 256u);
-                wb[slot][j] = buffer_load_u16(b_rsrc, s_lane[j], g * 256u);
+            for (int p = kHalf * half; p < kHalf * (half + 1); ++p) ar[p] = buffer_load16(a_rsrc, a_src[p] + g * 128u, 0);
+            if (half == 0) {
+#pragma unroll
+                for (int p = 0; p < kCPer; ++p) cr[p] = buffer_load16_cp<2>(q_rsrc, c_src[p] + g * (128u * 32u), 0);
+            } else if (side_loader) {
+                sr = buffer_load16(side_rsrc, side_src + g * 256u, 0);
             }
         };
-        MixCoef cf[2];
-        auto prepare = [&](int slot, bool on) {
+        auto store_half = [&](int buf, int half) {
+            char *b = lds + buf * kPBuf;
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
-                cf[j] = mix_coef(on ? bf16_bits_to_f32(ws[slot][j]) : 0.0f, on ? bf16_bits_to_f32(wb[slot][j]) : 0.0f);
+            for (int p = kHalf * half; p < kHalf * (half + 1); ++p) *(u32x4 *)(b + a_lds(p)) = ar[p];
+            if (half == 0) {
+#pragma unroll
+                for (int p = 0; p < kCPer; ++p) *(u32x4 *)(b + c_lds(p)) = cr[p];
+            } else if (side_loader) {
+                *(u32x4 *)(b + kPABuf + kPCodeBytes + wave * 512 + lane * 16) = sr;
+            }
         };
-        bf16x8 bw[2][4];
-        // Operand reads: MFMA step i of row block f takes row 32 f + r, piece 4 h + i.
-        auto read_af = [&](bf16x8 *dst, int buf, int i) {
-            const char *p = lds + buf * kPABuf + r * kPRow + (4 * h + i) * 16;
+        // A wave's codes of a chunk (16 bytes of column 64 wn + 32 j + r: words 4 h .. 4 h + 3) and
+        // their coefficients (zero for the padding steps).
+        auto read_codes = [&](u32x4 *dst, int buf) {
+            const char *b = lds + buf * kPBuf + kPABuf + (64 * wn + r) * kPCodeRow + 16 * h;
 #pragma unroll
-            for (int f = 0; f < 8; ++f) dst[f] = as_bf16x8(*(const u32x4 *)(p + f * 32 * kPRow));
+            for (int j = 0; j < 2; ++j) dst[j] = *(const u32x4 *)(b + 32 * j * kPCodeRow);
+        };
+        MixCoef cf[2];
+        auto read_coef = [&](int buf, bool on) {
+            const char *b = lds + buf * kPBuf + kPABuf + kPCodeBytes + (64 * wn + r) * 2;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const float sc = bf16_bits_to_f32(*(const uint16_t *)(b + 64 * j));
+                const float bi = bf16_bits_to_f32(*(const uint16_t *)(b + 512 + 64 * j));
+                cf[j] = mix_coef(on ? sc : 0.0f, on ? bi : 0.0f);
+            }
+        };
+        // Operand reads: MFMA step i of row block f takes row 32 (FM wm + f) + r, piece 4 h + i.
+        auto read_af = [&](bf16x8 *dst, int buf, int i) {
+            const char *p = lds + buf * kPBuf + (FM * wm * 32 + r) * kPRow + (4 * h + i) * 16;
+#pragma unroll
+            for (int f = 0; f < FM; ++f) dst[f] = as_bf16x8(*(const u32x4 *)(p + f * 32 * kPRow));
         };
 
-        f32x16 acc[8][2];
+        f32x16 acc[FM][2];
 #pragma unroll
-        for (int f = 0; f < 8; ++f)
+        for (int f = 0; f < FM; ++f)
 #pragma unroll
             for (int j = 0; j < 2; ++j)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) acc[f][j][e] = 0.0f;
 
-        // Prologue, in the loop's load order (chunk, then codes), so that the wait counts the
-        // compiler derives at the loop head leave the codes in flight.
-        load_a(0);
-        load_w(0, 0);
-        load_w(1, 1);
-        store_a(0);
+        // Prologue, loads in the loop's order (so that the wait counts the compiler derives at the
+        // loop head leave the younger loads in flight).
+        load_half(0, 0);
+        load_half(0, 1);
+        store_half(0, 0);
+        store_half(0, 1);
         __builtin_amdgcn_sched_barrier(0);
-        load_a(1);
+        load_half(1, 0);
         __builtin_amdgcn_sched_barrier(0);
-        load_w(2, 2);
+        load_half(1, 1);
         __builtin_amdgcn_sched_barrier(0);
         lds_barrier();
-        prepare(0, T > 0);
+        u32x4 cq[2];  // codes of the current group
+        read_codes(cq, 0);
+        read_coef(0, T > 0);
+        bf16x8 bw[2];  // B operands of the current MFMA step
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) bw[j][i] = dequant_word_mix(wq[0][j][i], cf[j], magic);
-        bf16x8 af[8];
-        read_af(af, 0, 0);
+        for (int j = 0; j < 2; ++j) bw[j] = dequant_word_mix(cq[j][0], cf[j], magic);
+        bf16x8 af[FM];
+        if (WM == 1) read_af(af, 0, 0);
 
-        // Step t (group ga + t), d = t mod 3 = its activation buffer and code ring slot. Every
-        // MFMA step interleaves its 16 MFMAs with the dequantization of the next group's operand
-        // i (with one wave per SIMD the VALU work only hides under the matrix core when its
-        // instructions sit between the MFMAs), the next MFMA step's fragment reads and a share of
-        // the memory traffic, spread so that no step queues at the texture unit:
+        // Step t (group ga + t), d = t mod 3 = its LDS buffer. Every MFMA step interleaves its
+        // MFMAs with the dequantization of the next MFMA step's operands (with one wave per SIMD
+        // the VALU work only hides under the matrix core when its instructions sit between the
+        // MFMAs), its fragment reads and a share of the chunk traffic, spread so that no step
+        // queues at the texture unit:
         //  * steps 0 and 1 store chunk t + 1 (loaded in step t - 1) into buffer t + 1 mod 3, half
         //    each, and steps 1 and 2 load chunk t + 2 into the registers just stored;
-        //  * the barrier before step 2 makes chunk t + 1 readable (step 3 prefetches its first
-        //    fragments); since every wave has then finished step t - 1, buffer t + 2 mod 3 (read
-        //    last in step t - 1) may be written in step t + 1;
-        //  * steps 2 and 3 load the codes of step t + 3 into the ring slot of step t, whose
-        //    weights were dequantized in step t - 1.
+        //  * the barrier before step 2 makes chunk t + 1 readable: step 2 reads its codes and
+        //    coefficients, step 3 dequantizes its first operands (and, with one wave per SIMD,
+        //    prefetches its first fragments). Every wave has then finished step t - 1, so buffer
+        //    t + 2 mod 3 (last read in step t - 1) may be written in step t + 1.
         // Loads past the job re-read its last group.
         auto step = [&](int t, int d) {
             const int next = d == 2 ? 0 : d + 1;
-            prepare(next, t + 1 < T);  // zero coefficients for the padding steps
-            const uint32_t ga_next = clampg(t + 2) * 128u, gw = clampg(t + 3);
+            u32x4 cn[2];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 if (i == 2) {
                     lds_barrier();
                     __builtin_amdgcn_sched_barrier(0);
                 }
-                bf16x8 an[8];
-                read_af(an, i < 3 ? d : next, i < 3 ? i + 1 : 0);
+                // One wave per SIMD prefetches the next MFMA step's fragments; with two, the other
+                // wave covers the read latency and the registers are short.
+                constexpr bool kPrefetch = WM == 1;
+                bf16x8 an[FM];
+                if (kPrefetch)
+                    read_af(an, i < 3 ? d : next, i < 3 ? i + 1 : 0);
+                else
+                    read_af(af, d, i);
+                if (i == 2) read_codes(cn, next);
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
 #pragma unroll
-                    for (int f = 0; f < 8; ++f)
-                        acc[f][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[f], bw[j][i], acc[f][j], 0, 0, 0);
+                    for (int f = 0; f < FM; ++f)
+                        acc[f][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[f], bw[j], acc[f][j], 0, 0, 0);
+                // The next MFMA step's operands: word i + 1 of this group, or word 0 of the next.
+                if (i < 3) {
 #pragma unroll
-                for (int j = 0; j < 2; ++j) bw[j][i] = dequant_word_mix(wq[next][j][i], cf[j], magic);
-                // Chunk t + 1: pieces 4 i .. 4 i + 3 stored in steps 0 and 1 and reloaded (for
-                // chunk t + 2) in steps 1 and 2, half the LDS writes in each of the first steps.
-                if (i < 2) {
+                    for (int j = 0; j < 2; ++j) bw[j] = dequant_word_mix(cq[j][i + 1], cf[j], magic);
+                } else {
+                    read_coef(next, t + 1 < T);
 #pragma unroll
-                    for (int p = 4 * i; p < 4 * i + 4; ++p) *(u32x4 *)(lds + next * kPABuf + a_lds(p)) = ar[p];
+                    for (int j = 0; j < 2; ++j) {
+                        cq[j] = cn[j];
+                        bw[j] = dequant_word_mix(cq[j][0], cf[j], magic);
+                    }
                 }
-                if (i == 1 || i == 2) {
+                if (i < 2) store_half(next, i);
+                if (i == 1 || i == 2) load_half(t + 2, i - 1);
+                constexpr int kMfma = 2 * FM, kValu = (36 + kMfma - 1) / kMfma;
 #pragma unroll
-                    for (int p = 4 * (i - 1); p < 4 * i; ++p) ar[p] = buffer_load16(a_rsrc, a_src[p] + ga_next, 0);
-                }
-                if (i >= 2) {
-                    const int j = i - 2;
-                    wq[d][j] = buffer_load16_cp<2>(q_rsrc, q_lane[j], gw * (128u * 32u));
-                    ws[d][j] = buffer_load_u16(s_rsrc, s_lane[j], gw * 256u);
-                    wb[d][j] = buffer_load_u16(b_rsrc, s_lane[j], gw * 256u);
-                }
-#pragma unroll
-                for (int m = 0; m < 16; ++m) {
-                    if (m < 8) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);             // one MFMA
-                    __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);             // two VALU
-                    if (m % 2 == 1) {
-                        if (i < 2 && m < 8) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // LDS write
-                        if (i > 0) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);         // VMEM read
+                for (int m = 0; m < kMfma; ++m) {
+                    if (m < FM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);     // one LDS read
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                 // one MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x002, kValu, 0);             // VALU
+                    if (m < 8 / WM && (WM == 2 || m % 2 == 1)) {
+                        if (i < 2) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // LDS write
+                        if (i == 1 || i == 2) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM
                     }
                 }
                 __builtin_amdgcn_sched_barrier(0);
+                if (kPrefetch) {
 #pragma unroll
-                for (int f = 0; f < 8; ++f) af[f] = an[f];
+                    for (int f = 0; f < FM; ++f) af[f] = an[f];
+                }
             }
         };
         // The step count is padded to a multiple of three (no early exit, whose extra paths cost
@@ -242,12 +297,15 @@ q4_prefill_kernel(PrefillArgs args) {
             step(t0 + 2, 2);
         }
 
-        // Epilogue, one 32-row block at a time through the wave's own LDS area: lane (r, h) holds
-        // row 8 (e / 4) + 4 h + e % 4, column 32 j + r; the rows are then written 16 bytes (4
-        // columns) a lane.
-        const int64_t nw0 = n0 + 64 * wave;
+        // Epilogue, one 32-row block at a time through the wave's own LDS area (over the
+        // activation buffers, once every wave is done with them): lane (r, h) holds row
+        // 8 (e / 4) + 4 h + e % 4, column 32 j + r; the rows are then written 16 bytes (4 columns)
+        // a lane.
+        lds_barrier();
+        const int64_t nw0 = n0 + 64 * wn;
 #pragma unroll
-        for (int f = 0; f < 8; ++f) {
+        for (int f = 0; f < FM; ++f) {
+            const int tr0 = 32 * (FM * wm + f);  // the block's first row in the tile
 #pragma unroll
             for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -259,11 +317,11 @@ q4_prefill_kernel(PrefillArgs args) {
             for (int p = 0; p < 8; ++p) {
                 const int idx = p * 64 + lane, row = idx >> 4, c4 = (idx & 15) * 4;
                 const f32x4 v = *(const f32x4 *)(epi + (row * kPEpiRow + c4) * 4);
-                const int64_t m = m0 + 32 * f + row, n = nw0 + c4;
+                const int64_t m = m0 + tr0 + row, n = nw0 + c4;
                 if (m >= args.rows || n >= args.n) continue;
                 if (slot >= 0) {
-                    float *dst = args.partial + ((int64_t)(blockIdx.x * 2 + slot) * kPB + 32 * f + row) * kPB +
-                                 64 * wave + c4;
+                    float *dst = args.partial + ((int64_t)(blockIdx.x * 2 + slot) * kPB + tr0 + row) * kPB +
+                                 64 * wn + c4;
                     *(f32x4 *)dst = v;
                     continue;
                 }
@@ -421,6 +479,17 @@ size_t prefill_workspace_bytes(int64_t rows, int64_t columns, int64_t groups) {
     return p.sk_units > 0 ? prefill_sk_bytes(p.grid) : 0;
 }
 
+template <int WM>
+static void launch_prefill_wm(const PrefillPlan &plan, const PrefillArgs &args, hipStream_t stream) {
+    static bool once = [] {
+        (void)hipFuncSetAttribute((const void *)q4_prefill_kernel<WM>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)kPLds);
+        return true;
+    }();
+    (void)once;
+    hipLaunchKernelGGL(q4_prefill_kernel<WM>, dim3((unsigned)plan.grid), dim3(256 * WM), kPLds, stream, args);
+}
+
 hipError_t launch_q4_prefill(const PrefillPlan &plan, const splosh_q4_weight &w, const uint16_t *a, int64_t lda,
                              void *out, int64_t ldc, int out_dtype, const void *residual, int64_t rows,
                              void *workspace, hipStream_t stream) {
@@ -444,13 +513,7 @@ hipError_t launch_q4_prefill(const PrefillPlan &plan, const splosh_q4_weight &w,
     args.code_bytes = (uint32_t)(w.rows * args.groups * 32);
     args.sidecar_bytes = (uint32_t)(w.rows * args.groups * 2);
     args.a_bytes = (uint32_t)(((rows - 1) * lda + w.inner) * 2);
-    static bool once = [] {
-        (void)hipFuncSetAttribute((const void *)q4_prefill_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  (int)kPLds);
-        return true;
-    }();
-    (void)once;
-    hipLaunchKernelGGL(q4_prefill_kernel, dim3((unsigned)plan.grid), dim3(kPThreads), kPLds, stream, args);
+    launch_prefill_wm<1>(plan, args, stream);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess || plan.sk_units == 0) return err;
     const int remainder = plan.tiles - plan.dp_tiles;
