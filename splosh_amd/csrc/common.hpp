@@ -78,6 +78,8 @@ __device__ __forceinline__ uint32_t buffer_load_u16(rsrc_t r, uint32_t voffset, 
 // outstanding global loads (which __syncthreads' fence would drain), so prefetches stay in flight.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-__device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
+// x sigmoid(x) with the hardware reciprocal (v_rcp_f32, about 1 ulp) instead of a full-precision
+// divide: the result is rounded to bf16 or summed in fp32 afterwards.
+__device__ __forceinline__ float silu(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 
 }  // namespace splosh

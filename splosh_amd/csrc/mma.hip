@@ -569,8 +569,12 @@ mma_kernel(MmaArgs args) {
         const int64_t ocol = (int64_t)band * S::kBandCols + c;
         const int rows = (int)args.rows;
         const float *red = (const float *)lds + (size_t)(c / 32) * S::kAcc * 64 + (c % 32);
+        // With 64-column bands a thread's rows are the same for its whole wave: scalar row
+        // arithmetic (a per-lane 64-bit row offset per iteration would be hoisted and spilled).
+        static_assert(S::kBandCols % 64 == 0, "a wave's threads share their rows");
+        const int m_first = __builtin_amdgcn_readfirstlane(tid / S::kBandCols);
 #pragma unroll
-        for (int m = tid / S::kBandCols; m < S::kRows; m += kRowStep) {
+        for (int m = m_first; m < S::kRows; m += kRowStep) {
             if (m >= rows) break;
             const int f = m / 32, mm = m % 32;
             const int e = (mm / 8) * 4 + (mm % 4), lane_h = ((mm / 4) % 2) * 32;
