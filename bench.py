@@ -33,9 +33,10 @@ BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
 # a plain 256 MiB device copy (FETCH_SIZE reads half the bytes moved, WRITE_SIZE all of them).
 # The readings and commands are in profiles/; calls not listed are unmeasured (None).
 MEASURED_TRAFFIC = {
-    ("verify64", "mlp_in"): 52988.3 * 2 * 1024 + 11264.0 * 1024,   # q4_mma_kernel<2, 2, ...>
-    ("verify64", "down"): 30676.4 * 2 * 1024 + 5120.0 * 1024,      # q4_mma_kernel<2, 1, ...>
+    ("verify64", "mlp_in"): 51895.6 * 2 * 1024 + 10240.0 * 1024,   # mma_kernel<Q4Format<2, ...>, 2, ...>
+    ("verify64", "down"): 30763.3 * 2 * 1024 + 5120.0 * 1024,      # mma_kernel<Q4Format<1, ...>, 2, ...>
     ("decode1", "gemv"): 24605.8 * 2 * 1024 + 34.0 * 1024,         # q4_lane_kernel<1, 1, ...>
+    ("q5k64", "q5k"): 35955.3 * 2 * 1024 + 5120.0 * 1024,          # mma_kernel<Q5Format<...>, 2, ...>
 }
 
 
