@@ -90,7 +90,7 @@ def build_workload(name, rt, torch, gen, kernel):
     """Returns (steps: list of callables over copies, bytes_per_step, flops_per_step, kernels, config)."""
     def workspace(rows, n, k):
         need = rt.workspace_bytes(rows, n, k)
-        return torch.empty(max(need, 1), dtype=torch.uint8, device="cuda")
+        return torch.zeros(max(need, 1), dtype=torch.uint8, device="cuda")  # zero-filled before first use
 
     if name == "prefill2048":
         # Config 2: both prefill shapes, K=5120 -> N=17408 (up) and K=17408 -> N=5120 (down).
@@ -146,10 +146,11 @@ def build_workload(name, rt, torch, gen, kernel):
         x = torch.randn(m, k, device="cuda", generator=gen).to(torch.bfloat16)
         out = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
         b = q4_bytes(n, k) + m * k * 2 + m * n * 2
+        ws_dec = workspace(m, n, k)
 
         def launches(i):
             w = ws[i % ncopy]
-            return [("gemv", lambda: rt.gemm(w, x, out=out, kernel=kernel))]
+            return [("gemv", lambda: rt.gemm(w, x, out=out, kernel=kernel, workspace=ws_dec))]
 
         cfg = {"workload": "decode GEMV K5120->N17408", "rows": 1, "format": "mlx affine q4 g64, tiled128",
                "weight_copies": ncopy}

@@ -68,7 +68,9 @@ typedef enum splosh_kernel {
                                    weight with lda % 8 == 0 and ldc % 4 == 0, else TILE; SCALAR for
                                    operands no other kernel takes */
     SPLOSH_KERNEL_STREAM = 1,   /* weight streaming on raw codes: lane-per-row VALU kernel for
-                                   1-2 rows, raw-code MFMA kernels above */
+                                   1-2 rows (with SPLOSH_DECODE=1 in the environment and a
+                                   workspace, the every-CU decode kernel), raw-code MFMA kernels
+                                   above */
     SPLOSH_KERNEL_DEQUANT = 2,  /* rows <= 64: stream-K MFMA kernel on weights dequantized to bf16 in
                                    registers; uses the workspace for split bands when given one */
     SPLOSH_KERNEL_TILE = 3,     /* any rows: LDS-tiled dequant-to-bf16 MFMA GEMM (prefill) */
@@ -133,7 +135,9 @@ int splosh_q4_shape_validate(int64_t rows, int64_t columns, int64_t inner, const
  * its scratch (Runtime/Engine.swift:460-486); here the caller does, and the library allocates
  * nothing. Without a workspace (or with a smaller one) the kernels do not split K: the results
  * agree up to the fp32 summation order, with less parallelism. Calls that share one workspace
- * must be ordered on one stream. */
+ * must be ordered on one stream. The workspace must be zero-filled before its first use: it holds
+ * per-band arrival counters that the kernels return to zero before they exit, so later calls
+ * reuse it as it is (zero it again after a call that failed or was aborted). */
 size_t splosh_workspace_bytes(int64_t rows, int64_t columns, int64_t inner);
 
 const char *splosh_status_string(int status);

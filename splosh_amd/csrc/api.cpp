@@ -6,6 +6,7 @@
 #include <climits>
 #include <cstdint>
 #include <cstdio>
+#include <cstdlib>
 #include <string>
 
 #include "../../include/splosh_q4.h"
@@ -104,9 +105,14 @@ int q4_gemm_impl(const splosh_q4_weight *w, const splosh_q4_weight *up, const ui
     const bool prefill_ok = wide16 && !up && w->order == SPLOSH_Q4_TILED128 && aligned(out, 16) &&
                             (!residual || aligned(residual, 16)) &&
                             splosh::prefill_fits(rows, w->rows, w->inner, lda, ldc);
+    const char *decode_env = getenv("SPLOSH_DECODE");
+    const bool decode_ok = wide16 && workspace && decode_env && atoi(decode_env) != 0 &&
+                           splosh::decode_fits(rows, w->rows, w->inner, w->order) &&
+                           splosh::decode_plan_ok(w->rows, w->inner / kGroupSize, workspace_bytes);
     int choice = kernel;
     if (choice == SPLOSH_KERNEL_AUTO) {
         if (!eligible) choice = SPLOSH_KERNEL_SCALAR;
+        else if (decode_ok) choice = SPLOSH_KERNEL_STREAM;
         else if (wide16 && splosh::lanes_fit(rows, w->rows, w->inner, w->row_stride_words, up != nullptr))
             choice = SPLOSH_KERNEL_STREAM;
         else if (mma_ok) choice = SPLOSH_KERNEL_DEQUANT;
@@ -141,6 +147,11 @@ int q4_gemm_impl(const splosh_q4_weight *w, const splosh_q4_weight *up, const ui
             if (!eligible)
                 return fail(SPLOSH_ERR_UNSUPPORTED,
                             "stream kernel needs inner % 64 == 0, lda % 8 == 0 and aligned operands");
+            if (wide16 && decode_ok) {
+                return hip_status(splosh::launch_q4_decode(*w, up, a, lda, out, ldc, out_dtype, residual, rows,
+                                                           workspace, stream),
+                                  "q4 decode launch");
+            }
             if (wide16 && splosh::lanes_fit(rows, w->rows, w->inner, w->row_stride_words, up != nullptr)) {
                 const splosh::StreamPlan plan = splosh::plan_lanes(rows, w->rows, w->inner / kGroupSize, up != nullptr);
                 return hip_status(splosh::launch_q4_lanes(plan, *w, up, a, lda, out, ldc, out_dtype, residual, rows,
@@ -316,8 +327,10 @@ size_t splosh_workspace_bytes(int64_t rows, int64_t columns, int64_t inner) {
     const size_t tile = splosh::tile_workspace_bytes(rows, columns, groups, true);
     const size_t mma = rows <= 64 ? splosh::mma_workspace_bytes(rows, columns, groups, true) : 0;
     const size_t prefill = rows > 64 && columns % 128 == 0 ? splosh::prefill_workspace_bytes(rows, columns, groups) : 0;
+    const size_t decode = rows <= 2 && columns % 128 == 0 ? splosh::decode_workspace_bytes(columns) : 0;
     size_t need = tile > mma ? tile : mma;
-    return need > prefill ? need : prefill;
+    need = need > prefill ? need : prefill;
+    return need > decode ? need : decode;
 }
 
 // Q4GemmRuntime.dispatch (Runtime/Q4Runtime.swift:94-145).

@@ -661,20 +661,20 @@ q4_mma_finish(const float *__restrict__ partial, int nw, int band_cols, int dp_b
     const int64_t m = idx / band_cols, bc = idx % band_cols;
     const int64_t col = (int64_t)(dp_bands + rb) * band_cols + bc;
     if (col >= n) return;
-    // Loads in batches of eight so that their latencies overlap; the sum stays in order.
+    // Loads in batches of sixteen so that their latencies overlap; the sum stays in order.
     float v[2] = {0.0f, 0.0f};
     const int64_t wstride = rows * band_cols;
-    for (int j0 = 0; j0 < contributors; j0 += 8) {
-        float x[8][2];
+    for (int j0 = 0; j0 < contributors; j0 += 16) {
+        float x[16][2];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        for (int j = 0; j < 16; ++j) {
             const int jj = j0 + j < contributors ? j0 + j : contributors - 1;
             const float *src = partial + ((int64_t)(wg[jj] * 2 + slot_of[jj]) * nw * rows + m) * band_cols + bc;
             x[j][0] = src[0];
             x[j][1] = nw == 2 ? src[wstride] : 0.0f;
         }
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        for (int j = 0; j < 16; ++j) {
             if (j0 + j < contributors) {
                 v[0] += x[j][0];
                 v[1] += x[j][1];

@@ -410,15 +410,15 @@ q4_prefill_finish(const float *__restrict__ partial, int dp_tiles, int64_t sk_un
     const int64_t m = m0 + tr, col = n0 + tc;
     if (m >= rows || col >= n) return;
     f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int j0 = 0; j0 < contributors; j0 += 4) {
-        f32x4 x[4];
+    for (int j0 = 0; j0 < contributors; j0 += 8) {
+        f32x4 x[8];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < 8; ++j) {
             const int jj = j0 + j < contributors ? j0 + j : contributors - 1;
             x[j] = *(const f32x4 *)(partial + ((int64_t)(wg[jj] * 2 + slot_of[jj]) * kPB + tr) * kPB + tc);
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < 8; ++j)
             if (j0 + j < contributors) v += x[j];
     }
     const int64_t index = m * ldc + col;

@@ -135,7 +135,7 @@ def _workspace(workspace, rows, n, inner, device):
     need = _lib.lib().splosh_workspace_bytes(rows, n, inner)
     if need == 0:
         return None, 0
-    buf = torch.empty(need, dtype=torch.uint8, device=device)
+    buf = torch.zeros(need, dtype=torch.uint8, device=device)  # zero-filled before first use
     return _ptr(buf), need
 
 

@@ -28,8 +28,8 @@ def test_graph_replays_match_eager(rt):
     act = torch.empty(rows, inter, dtype=torch.bfloat16, device="cuda")
     out = torch.empty(rows, h, dtype=torch.bfloat16, device="cuda")
     out1 = torch.empty(1, inter, dtype=torch.bfloat16, device="cuda")
-    ws_in = torch.empty(max(rt.workspace_bytes(rows, inter, h), 1), dtype=torch.uint8, device="cuda")
-    ws_down = torch.empty(max(rt.workspace_bytes(rows, h, inter), 1), dtype=torch.uint8, device="cuda")
+    ws_in = torch.zeros(max(rt.workspace_bytes(rows, inter, h), 1), dtype=torch.uint8, device="cuda")
+    ws_down = torch.zeros(max(rt.workspace_bytes(rows, h, inter), 1), dtype=torch.uint8, device="cuda")
 
     def step():
         rt.mlp_in(gate.w_tiled, up.w_tiled, x, out=act, workspace=ws_in)

@@ -121,7 +121,7 @@ def test_split_k(rt, kernel, mlp):
     assert need > 0
     a = bf16_tensor(a_bits)
     outs = []
-    for ws in (torch.empty(need, dtype=torch.uint8, device="cuda"), torch.empty(16, dtype=torch.uint8, device="cuda"),
+    for ws in (torch.zeros(need, dtype=torch.uint8, device="cuda"), torch.zeros(16, dtype=torch.uint8, device="cuda"),
                None):
         if mlp:
             got = rt.mlp_in(gate.w_tiled, up.w_tiled, a, out_dtype=torch.float32, kernel=getattr(rt, kernel),
@@ -275,3 +275,35 @@ def test_prefill_down_shape_sampled(rt):
     sel = np.sort(rng.choice(rows, 256, replace=False))
     ref, absref = _sampled_reference(w, np.ascontiguousarray(a_bits[sel]), cols)
     check_close(got[sel][:, cols], ref, bf16_out=True, tight=True, absref=absref, label="prefill down")
+
+
+@pytest.mark.parametrize("rows", [1, 2])
+@pytest.mark.parametrize("mlp", [False, True])
+def test_decode_kernel(rt, rows, mlp, monkeypatch):
+    """The every-CU decode kernel (opt-in with SPLOSH_DECODE=1, rows <= 2, a zero-filled workspace): blocks shared by several
+    workgroups are summed by the last one in workgroup order, so two calls give the same bits and
+    leave the block counters at zero."""
+    monkeypatch.setenv("SPLOSH_DECODE", "1")
+    n, k = 4096, 4096
+    g, u = Q4Case(n, k, seed=700 + rows), Q4Case(n, k, seed=710 + rows)
+    a_bits = oracle.bf16_normal((rows, k), seed=720 + rows)
+    ws = torch.zeros(rt.workspace_bytes(rows, n, k), dtype=torch.uint8, device="cuda")
+    if mlp:
+        ref = oracle.silu_mul(oracle.gemm_a_bf16_w_f32(a_bits, g.dense), oracle.gemm_a_bf16_w_f32(a_bits, u.dense))
+        run = lambda dt: rt.mlp_in(g.w_tiled, u.w_tiled, bf16_tensor(a_bits), out_dtype=dt, kernel=rt.STREAM, workspace=ws)
+    else:
+        ref = oracle.gemm_a_bf16_w_f32(a_bits, g.dense)
+        run = lambda dt: rt.gemm(g.w_tiled, bf16_tensor(a_bits), out_dtype=dt, kernel=rt.STREAM, workspace=ws)
+    for out_dtype in (torch.bfloat16, torch.float32):
+        first = run(out_dtype)
+        second = run(out_dtype)
+        assert torch.equal(first.view(torch.uint8), second.view(torch.uint8)), "calls differ"
+        check_close(to_f32(first), ref, bf16_out=out_dtype == torch.bfloat16, tight=not mlp,
+                    label=f"decode rows={rows} mlp={mlp} {out_dtype}")
+    counters = ws[-(n // 32) * 4:].view(torch.int32)
+    assert int(counters.abs().sum()) == 0, "block counters not reset"
+    if not mlp:
+        base = np.random.default_rng(5).normal(size=(rows, n)).astype(np.float32)
+        out = torch.from_numpy(base.copy()).cuda()
+        rt.gemm(g.w_tiled, bf16_tensor(a_bits), out=out, residual=out, kernel=rt.STREAM, workspace=ws)
+        check_close(out.cpu().numpy(), ref + base, bf16_out=False, tight=True, label="decode residual")
