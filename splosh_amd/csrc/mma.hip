@@ -20,8 +20,9 @@
 //    ahead into registers, then stored to one of three LDS buffers, and so are per-band sidecars
 //    or block metadata. One barrier per step, in its middle.
 //  * At the end of a job the KW partial sums meet in LDS and the workgroup writes whole output
-//    rows. Bands beyond a whole number per CU are split over all workgroups (stream-K) and their
-//    fp32 partials summed by q4_mma_finish.
+//    rows. With a workspace, the (band, unit) pairs of all bands form one stream cut into equal
+//    contiguous ranges, one a workgroup (stream-K); a band shared by several workgroups is summed
+//    by the last of them to arrive.
 //
 // Numerics: w is the fp32 dequantized weight (one rounding, as DequantOracle.swift:20-21 for q4 and
 // GgufQuant.swift:205-210 for Q5_K) rounded to bf16 (RNE), products exact in fp32, fp32
@@ -34,8 +35,12 @@
 #include <type_traits>
 // Weight codes are read once: non-temporal loads (gfx94x cache policy nt).
 constexpr int kStreamCpol = 2;
+// Stream-K partials cross XCDs: written and read through to memory (cache policy sc0 sc1).
+constexpr int kDeviceCpol = 1 | 16;
 
 namespace splosh {
+
+constexpr int kMmaMaxGrid = 1024;  // workgroups of a stream-K launch
 
 struct MmaArgs {
     // q4: the weight (gate) and, for the fused pair, up.
@@ -55,6 +60,8 @@ struct MmaArgs {
     int64_t rows;
     int out_dtype;
     float *partial;     // stream-K partials [gridDim.x][2][NW][rows][band columns]
+    int *counters;      // arrivals per stream-K band (zero between calls)
+    uint32_t partial_bytes;
     int dp_bands;       // bands computed whole (a multiple of gridDim.x)
     int64_t sk_units;   // (band, unit) pairs of the remaining bands
     // Buffer extents (the fits checks keep them < 4 GiB): q4 codes and sidecars, or Q5_K plane0,
@@ -339,11 +346,11 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 // Work split. The N columns form `bands` bands of CW * 32. Bands [0, dp_bands) are computed whole
-// by workgroup (band mod gridDim.x), written straight to the output. The remaining bands' (band,
-// unit) pairs, sk_units of them, are cut into gridDim.x equal contiguous ranges (stream-K), one a
-// workgroup; a range covers at most two bands, and a band it covers in part is written as an fp32
-// partial to slot 0 (the range's first band) or 1 of the workgroup's workspace, summed later by
-// q4_mma_finish. dp_bands is a multiple of gridDim.x, so every workgroup gets the same work.
+// by workgroup (band mod gridDim.x), written straight to the output. The (band, unit) pairs of the
+// other bands, sk_units of them, are cut into gridDim.x equal contiguous ranges (stream-K), one a
+// workgroup. Only a range's first and last band can be partial: their fp32 partials go to slot 0
+// and 1 of the workgroup's workspace. The workgroups sharing a band count their arrivals on the
+// band's counter, and the last one sums the partials and writes the band.
 //
 // Pipeline of a job (units [ga, gb) of one band), in steps of KW x 64 elements of K, D steps deep:
 // weight codes go to a D-slot register ring, the activation chunk of a step (rows x KW x 64) and
@@ -366,6 +373,12 @@ mma_kernel(MmaArgs args) {
     const int U = (int)args.units;
 
     const rsrc_t a_rsrc = make_rsrc(args.a, args.a_bytes);
+    const int P = gridDim.x;
+    const rsrc_t p_rsrc = make_rsrc(args.partial, args.partial_bytes);
+    // Workgroup i takes stream-K units [sk_start(i), sk_start(i + 1)).
+    auto sk_start = [&](int i) { return args.sk_units * i / P; };
+    __shared__ int fix_count;
+    __shared__ uint16_t fix_list[kMmaMaxGrid];  // contributors of a shared band: 2 wg + slot
     F fmt(args, wave, lane);
     // Activation staging: this thread's piece j of a chunk sits at buffer position
     // (wave * kAPer + j) * 64 + lane, i.e. row m = pos / kKc, holding piece kc = (pos % kKc) ^ (m & 7)
@@ -529,10 +542,12 @@ mma_kernel(MmaArgs args) {
                 abuf = nbuf(abuf);
             }
         }
-        // The last three steps load only chunk Tp - 1 (in the first of them).
+        // The last three steps load only chunk Tp - 1 (in the first of them). Steps past T (at most
+        // the last two; T is uniform over the workgroup) are skipped: they would add nothing.
 #pragma unroll
         for (int d = 0; d < D; ++d) {
             const int t = Tp - D + d;
+            if (t >= T) break;
             step(t, d, abuf,
                  [&] {
                      wait_vmcnt<0>();
@@ -573,6 +588,22 @@ mma_kernel(MmaArgs args) {
         // arithmetic (a per-lane 64-bit row offset per iteration would be hoisted and spilled).
         static_assert(S::kBandCols % 64 == 0, "a wave's threads share their rows");
         const int m_first = __builtin_amdgcn_readfirstlane(tid / S::kBandCols);
+        auto store_out = [&](int m, const float *v) {
+            float value = v[0];
+            if constexpr (NW == 2) value = silu(v[0]) * v[1];
+            const int64_t index = (int64_t)m * args.ldc + ocol;
+            if (args.out_dtype == SPLOSH_F32) {
+                if (args.residual) value += ((const float *)args.residual)[index];
+                ((float *)args.out)[index] = value;
+            } else {
+                if (args.residual) value += bf16_bits_to_f32(((const uint16_t *)args.residual)[index]);
+                ((uint16_t *)args.out)[index] = f32_to_bf16(value);
+            }
+        };
+        // Partial of slot s, weight w, row m, this thread's column: a byte offset into the workspace.
+        auto part_off = [&](int wg, int sl, int w, int m) {
+            return (uint32_t)((((wg * 2 + sl) * NW + w) * rows + m) * S::kBandCols + c) * 4u;
+        };
 #pragma unroll
         for (int m = m_first; m < S::kRows; m += kRowStep) {
             if (m >= rows) break;
@@ -586,34 +617,89 @@ mma_kernel(MmaArgs args) {
                 for (int k = 0; k < KW; ++k) sum += red[(size_t)k * CW * S::kAcc * 64 + ((w * FM + f) * 16 + e) * 64 + lane_h];
                 v[w] = sum;
             }
-            if (ocol >= args.n) continue;
             if (slot >= 0) {
-                float *dst = args.partial + ((int64_t)(blockIdx.x * 2 + slot) * NW * rows + m) * S::kBandCols + c;
+                // Written through to memory (gfx94x cache policy sc0 sc1): the workgroup that sums
+                // the band may run on another XCD, whose L2 is not coherent with this one's.
 #pragma unroll
-                for (int w = 0; w < NW; ++w) dst[(int64_t)w * rows * S::kBandCols] = v[w];
+                for (int w = 0; w < NW; ++w)
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v[w]), p_rsrc, part_off(blockIdx.x, slot, w, m), 0, kDeviceCpol);
                 continue;
             }
-            float value = v[0];
-            if constexpr (NW == 2) value = silu(v[0]) * v[1];
-            const int64_t index = (int64_t)m * args.ldc + ocol;
-            if (args.out_dtype == SPLOSH_F32) {
-                if (args.residual) value += ((const float *)args.residual)[index];
-                ((float *)args.out)[index] = value;
-            } else {
-                if (args.residual) value += bf16_bits_to_f32(((const uint16_t *)args.residual)[index]);
-                ((uint16_t *)args.out)[index] = f32_to_bf16(value);
+            if (ocol < args.n) store_out(m, v);
+        }
+        if (slot < 0) return;
+        // A shared band: the last of its workgroups to arrive sums every partial in workgroup
+        // order (so the result does not depend on who is last), applies the epilogue and returns
+        // the band's counter to zero for the next call.
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this workgroup's partial is in memory
+        __syncthreads();
+        const int64_t lo = (int64_t)(band - args.dp_bands) * U, hi = lo + U;  // the band's units
+        const int i_lo = (int)(((lo + 1) * P - 1) / args.sk_units), i_hi = (int)((hi * P - 1) / args.sk_units);
+        if (tid == 0) {
+            // The band's contributors (workgroups with a non-empty range meeting it), in order, and
+            // the slot each one used for it: 1 if its range began in an earlier band.
+            int count = 0;
+            for (int i = i_lo; i <= i_hi; ++i) {
+                const int64_t st = sk_start(i);
+                if (st == sk_start(i + 1)) continue;
+                fix_list[count++] = (uint16_t)(i * 2 + (st < lo ? 1 : 0));
+            }
+            int *counter = args.counters + (band - args.dp_bands);
+            const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            const bool last = old == count - 1;
+            if (last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            fix_count = last ? count : 0;
+        }
+        __syncthreads();
+        const int count = fix_count;
+        if (count == 0) return;
+        // Partials are read in batches of four contributors for every row of the thread at once,
+        // so that their memory latencies overlap; each sum still runs in contributor order.
+        constexpr int kMine = S::kRows / kRowStep;  // rows of this thread (those past `rows` idle)
+        float v[kMine][NW];
+#pragma unroll
+        for (int j = 0; j < kMine; ++j)
+#pragma unroll
+            for (int w = 0; w < NW; ++w) v[j][w] = 0.0f;
+        for (int c0 = 0; c0 < count; c0 += 4) {
+            float x[4][kMine][NW];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int entry = fix_list[c0 + q < count ? c0 + q : count - 1];
+#pragma unroll
+                for (int j = 0; j < kMine; ++j) {
+                    const int m = m_first + j * kRowStep;
+                    const int mc = m < rows ? m : rows - 1;
+#pragma unroll
+                    for (int w = 0; w < NW; ++w)
+                        x[q][j][w] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                                   p_rsrc, part_off(entry >> 1, entry & 1, w, mc), 0, kDeviceCpol));
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                if (c0 + q < count)
+#pragma unroll
+                    for (int j = 0; j < kMine; ++j)
+#pragma unroll
+                        for (int w = 0; w < NW; ++w) v[j][w] += x[q][j][w];
+        }
+        if (ocol < args.n) {
+#pragma unroll
+            for (int j = 0; j < kMine; ++j) {
+                const int m = m_first + j * kRowStep;
+                if (m < rows) store_out(m, v[j]);
             }
         }
     };
 
-    const int P = gridDim.x;
     for (int band = blockIdx.x; band < args.dp_bands; band += P) {
         run_job(band, 0, U, -1);
         lds_barrier();  // the next job's loads overwrite the reduction area; stores need not drain
     }
     if (args.sk_units > 0) {
-        int64_t u = args.sk_units * blockIdx.x / P;
-        const int64_t u_end = args.sk_units * (blockIdx.x + 1) / P;
+        int64_t u = sk_start(blockIdx.x);
+        const int64_t u_end = sk_start(blockIdx.x + 1);
         int slot = 0;
         while (u < u_end) {
             const int band = args.dp_bands + (int)(u / U);
@@ -624,71 +710,6 @@ mma_kernel(MmaArgs args) {
             u += gb - ga;
             slot = 1;
         }
-    }
-}
-
-// Sums the stream-K partials of the remainder bands (see mma_kernel) in workgroup order and
-// applies the epilogue. Block (rb, y) covers outputs [256 y, 256 y + 256) of remainder band rb;
-// its first thread lists the band's contributing workgroups once.
-constexpr int kFinishMaxContributors = 1024;
-__global__ void __launch_bounds__(256)
-q4_mma_finish(const float *__restrict__ partial, int nw, int band_cols, int dp_bands, int64_t sk_units, int P,
-              int64_t units, int64_t rows, int64_t n, void *out, int64_t ldc, int out_dtype, const void *residual) {
-    __shared__ int wg[kFinishMaxContributors];
-    __shared__ int slot_of[kFinishMaxContributors];
-    __shared__ int count;
-    const int64_t rb = blockIdx.x;
-    const int64_t lo = rb * units, hi = lo + units;  // the band's units
-    if (threadIdx.x == 0) {
-        // Workgroup i covers units [U i / P, U (i + 1) / P); the one holding unit u is
-        // floor(((u + 1) P - 1) / U). Ranges may be empty when there are fewer units than workgroups.
-        const int i_lo = (int)(((lo + 1) * P - 1) / sk_units), i_hi = (int)((hi * P - 1) / sk_units);
-        int c = 0;
-        for (int i = i_lo; i <= i_hi && c < kFinishMaxContributors; ++i) {
-            const int64_t s = sk_units * i / P, e = sk_units * (i + 1) / P;
-            if (s == e) continue;
-            wg[c] = i;
-            slot_of[c] = s < lo ? 1 : 0;
-            ++c;
-        }
-        count = c;
-    }
-    __syncthreads();
-    const int contributors = count;
-    if (contributors <= 1) return;  // one workgroup covered the band and wrote it
-    const int64_t idx = (int64_t)blockIdx.y * blockDim.x + threadIdx.x;
-    if (idx >= rows * band_cols) return;
-    const int64_t m = idx / band_cols, bc = idx % band_cols;
-    const int64_t col = (int64_t)(dp_bands + rb) * band_cols + bc;
-    if (col >= n) return;
-    // Loads in batches of sixteen so that their latencies overlap; the sum stays in order.
-    float v[2] = {0.0f, 0.0f};
-    const int64_t wstride = rows * band_cols;
-    for (int j0 = 0; j0 < contributors; j0 += 16) {
-        float x[16][2];
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const int jj = j0 + j < contributors ? j0 + j : contributors - 1;
-            const float *src = partial + ((int64_t)(wg[jj] * 2 + slot_of[jj]) * nw * rows + m) * band_cols + bc;
-            x[j][0] = src[0];
-            x[j][1] = nw == 2 ? src[wstride] : 0.0f;
-        }
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            if (j0 + j < contributors) {
-                v[0] += x[j][0];
-                v[1] += x[j][1];
-            }
-        }
-    }
-    float value = nw == 2 ? silu(v[0]) * v[1] : v[0];
-    const int64_t index = m * ldc + col;
-    if (out_dtype == SPLOSH_F32) {
-        if (residual) value += ((const float *)residual)[index];
-        ((float *)out)[index] = value;
-    } else {
-        if (residual) value += bf16_bits_to_f32(((const uint16_t *)residual)[index]);
-        ((uint16_t *)out)[index] = f32_to_bf16(value);
     }
 }
 
@@ -724,8 +745,12 @@ static int device_cus() {
     return cache[dev];
 }
 
-static size_t sk_bytes(int grid, int64_t rows, bool mlp) {
-    return (size_t)grid * 2 * (mlp ? 2 : 1) * rows * (kMmaCW * 32) * sizeof(float);
+// Partials [grid][2][nw][rows][band columns] fp32, then one arrival counter per band.
+static size_t sk_partial_bytes(int grid, int64_t rows, bool mlp) {
+    return ((size_t)grid * 2 * (mlp ? 2 : 1) * rows * (kMmaCW * 32) * sizeof(float) + 255) / 256 * 256;
+}
+static size_t sk_bytes(int grid, int64_t rows, int bands, bool mlp) {
+    return sk_partial_bytes(grid, rows, mlp) + (size_t)bands * sizeof(int);
 }
 
 MmaPlan plan_mma(int64_t rows, int64_t columns, int64_t groups, bool mlp, size_t workspace_bytes) {
@@ -734,11 +759,17 @@ MmaPlan plan_mma(int64_t rows, int64_t columns, int64_t groups, bool mlp, size_t
     p.bands = (int)((columns + kMmaCW * 32 - 1) / (kMmaCW * 32));
     int grid = device_cus();
     if (const char *env = getenv("SPLOSH_MMA_GRID")) grid = atoi(env) > 0 ? atoi(env) : grid;
-    grid = grid < kFinishMaxContributors ? grid : kFinishMaxContributors;  // q4_mma_finish's list
+    grid = grid < kMmaMaxGrid ? grid : kMmaMaxGrid;  // the fix-up's contributor list
     p.grid = grid;
-    p.dp_bands = (p.bands / grid) * grid;
-    p.sk_units = (int64_t)(p.bands - p.dp_bands) * groups;
-    if (p.sk_units > 0 && sk_bytes(grid, rows, mlp) > workspace_bytes) {
+    // Every band's units go into one stream, cut into `grid` equal contiguous ranges: a band is
+    // shared by at most a few workgroups and no step is wasted on a partial round of bands.
+    p.dp_bands = 0;
+    p.sk_units = (int64_t)p.bands * groups;
+    if (p.bands % grid == 0) {
+        // Whole bands per workgroup already balance: no partials.
+        p.dp_bands = p.bands;
+        p.sk_units = 0;
+    } else if (sk_bytes(grid, rows, p.bands, mlp) > workspace_bytes) {
         // No room for partials: every band whole, one workgroup each.
         p.grid = p.bands;
         p.dp_bands = p.bands;
@@ -749,7 +780,7 @@ MmaPlan plan_mma(int64_t rows, int64_t columns, int64_t groups, bool mlp, size_t
 
 size_t mma_workspace_bytes(int64_t rows, int64_t columns, int64_t groups, bool mlp) {
     const MmaPlan p = plan_mma(rows, columns, groups, mlp, (size_t)-1);
-    return p.sk_units > 0 ? sk_bytes(p.grid, rows, mlp) : 0;
+    return p.sk_units > 0 ? sk_bytes(p.grid, rows, p.bands, mlp) : 0;
 }
 
 template <class F, int FM>
@@ -774,7 +805,7 @@ template <int NW, bool TILED>
 using Q4F = Q4Format<NW, TILED, kMmaCW, kMmaKW, kMmaDepth>;
 
 static void set_io(MmaArgs &args, const MmaPlan &plan, const uint16_t *a, int64_t lda, void *out, int64_t ldc,
-                   int out_dtype, const void *residual, int64_t rows, int64_t inner, void *workspace) {
+                   int out_dtype, const void *residual, int64_t rows, int64_t inner, void *workspace, bool mlp) {
     args.a = a;
     args.lda = lda;
     args.out = out;
@@ -783,19 +814,11 @@ static void set_io(MmaArgs &args, const MmaPlan &plan, const uint16_t *a, int64_
     args.rows = rows;
     args.out_dtype = out_dtype;
     args.partial = plan.sk_units > 0 ? (float *)workspace : nullptr;
+    args.partial_bytes = plan.sk_units > 0 ? (uint32_t)sk_partial_bytes(plan.grid, rows, mlp) : 0;
+    args.counters = plan.sk_units > 0 ? (int *)((char *)workspace + args.partial_bytes) : nullptr;
     args.dp_bands = plan.dp_bands;
     args.sk_units = plan.sk_units;
     args.a_bytes = (uint32_t)(((rows - 1) * lda + inner) * 2);
-}
-
-static hipError_t launch_finish(const MmaPlan &plan, int nw, int64_t units, int64_t n, int64_t rows, void *out,
-                                int64_t ldc, int out_dtype, const void *residual, void *workspace,
-                                hipStream_t stream) {
-    const int64_t per_band = rows * (kMmaCW * 32);
-    hipLaunchKernelGGL(q4_mma_finish, dim3((unsigned)(plan.sk_units / units), (unsigned)((per_band + 255) / 256)),
-                       dim3(256), 0, stream, (const float *)workspace, nw, kMmaCW * 32, plan.dp_bands, plan.sk_units,
-                       plan.grid, units, rows, n, out, ldc, out_dtype, residual);
-    return hipGetLastError();
 }
 
 hipError_t launch_q4_mma(const MmaPlan &plan, const splosh_q4_weight &w, const splosh_q4_weight *up,
@@ -812,7 +835,7 @@ hipError_t launch_q4_mma(const MmaPlan &plan, const splosh_q4_weight &w, const s
     args.n = w.rows;
     const int64_t groups = w.inner / kGroup;
     args.units = groups;
-    set_io(args, plan, a, lda, out, ldc, out_dtype, residual, rows, w.inner, workspace);
+    set_io(args, plan, a, lda, out, ldc, out_dtype, residual, rows, w.inner, workspace, up != nullptr);
     const bool tiled = w.order == SPLOSH_Q4_TILED128;
     args.code_bytes = (uint32_t)(tiled ? w.rows * groups * 32 : w.rows * w.row_stride_words * 4);
     args.sidecar_bytes = (uint32_t)(w.rows * groups * 2);
@@ -821,8 +844,7 @@ hipError_t launch_q4_mma(const MmaPlan &plan, const splosh_q4_weight &w, const s
         err = tiled ? launch_mma_fm<Q4F<2, true>>(plan, args, stream) : launch_mma_fm<Q4F<2, false>>(plan, args, stream);
     else
         err = tiled ? launch_mma_fm<Q4F<1, true>>(plan, args, stream) : launch_mma_fm<Q4F<1, false>>(plan, args, stream);
-    if (err != hipSuccess || plan.sk_units == 0) return err;
-    return launch_finish(plan, up ? 2 : 1, groups, w.rows, rows, out, ldc, out_dtype, residual, workspace, stream);
+    return err;
 }
 
 hipError_t launch_q5k_mma(const MmaPlan &plan, const splosh_q5k_weight &w, const uint16_t *a, int64_t lda, void *out,
@@ -835,13 +857,11 @@ hipError_t launch_q5k_mma(const MmaPlan &plan, const splosh_q5k_weight &w, const
     args.n = w.rows;
     const int64_t blocks = w.inner / 256;
     args.units = blocks;
-    set_io(args, plan, a, lda, out, ldc, out_dtype, residual, rows, w.inner, workspace);
+    set_io(args, plan, a, lda, out, ldc, out_dtype, residual, rows, w.inner, workspace, false);
     args.code_bytes = (uint32_t)(w.rows * blocks * 8 * 16);
     args.sidecar_bytes = (uint32_t)(w.rows * blocks * 8 * 4);
     args.meta_bytes = (uint32_t)(w.rows * blocks * 16);
-    const hipError_t err = launch_mma_fm<Q5Format<kMmaCW, kMmaKW, kMmaDepth>>(plan, args, stream);
-    if (err != hipSuccess || plan.sk_units == 0) return err;
-    return launch_finish(plan, 1, blocks, w.rows, rows, out, ldc, out_dtype, residual, workspace, stream);
+    return launch_mma_fm<Q5Format<kMmaCW, kMmaKW, kMmaDepth>>(plan, args, stream);
 }
 
 }  // namespace splosh
