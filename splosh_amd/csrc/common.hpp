@@ -74,6 +74,18 @@ __device__ __forceinline__ uint32_t buffer_load_u16(rsrc_t r, uint32_t voffset, 
     return __builtin_amdgcn_raw_buffer_load_b16(r, (int)voffset, (int)soffset, 0);
 }
 
+// 16 bytes a lane from a buffer straight into LDS (the load's LDS modifier, gfx950): lane l of
+// the wave writes bytes [16 l, 16 l + 16) after `lds_dst`, which must be wave-uniform. The load
+// counts in vmcnt; once it has been waited for, the data is in LDS. (The host pass compiles no
+// kernel code, and has no LDS address space, hence the guard.)
+__device__ __forceinline__ void buffer_load_lds16(rsrc_t r, void *lds_dst, uint32_t voffset) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds_dst, 16, (int)voffset, 0, 0, 0);
+#else
+    (void)r, (void)lds_dst, (void)voffset;
+#endif
+}
+
 // Workgroup barrier for LDS hand-offs only: waits for this wave's LDS operations, not for its
 // outstanding global loads (which __syncthreads' fence would drain), so prefetches stay in flight.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }

@@ -180,20 +180,24 @@ struct Q4Format {
     }
     // Sidecars of the step whose codes sit in `slot` and whose staged sidecars sit in `sbuf`
     // (zeros when the step has no group for this wave).
+    // The sidecars are read whatever `on` says and then scaled by 0 or 1 (exact), so that the
+    // reads of both weights are issued together instead of behind a branch each.
     __device__ void prepare(int slot, const char *sbuf, bool on) {
+        uint32_t sb[NW], bb[NW];
 #pragma unroll
         for (int w = 0; w < NW; ++w) {
-            uint32_t sb, bb;
             if (kStageSide) {
                 const char *base = sbuf + (((w * 2) * KW + kw) * kBandCols + cw * 32 + r) * 2;
-                sb = *(const uint16_t *)base;
-                bb = *(const uint16_t *)(base + KW * kBandCols * 2);
+                sb[w] = *(const uint16_t *)base;
+                bb[w] = *(const uint16_t *)(base + KW * kBandCols * 2);
             } else {
-                sb = wsc[slot][w];
-                bb = wbi[slot][w];
+                sb[w] = wsc[slot][w];
+                bb[w] = wbi[slot][w];
             }
-            cf[w] = mix_coef(on ? bf16_bits_to_f32(sb) : 0.0f, on ? bf16_bits_to_f32(bb) : 0.0f);
         }
+        const float one = on ? 1.0f : 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) cf[w] = mix_coef(bf16_bits_to_f32(sb[w]) * one, bf16_bits_to_f32(bb[w]) * one);
     }
     __device__ bf16x8 operand(int w, int i, int slot) { return dequant_word_mix(wq[slot][w][i], cf[w], magic); }
 };
@@ -406,20 +410,17 @@ mma_kernel(MmaArgs args) {
         const int T = fmt.steps(ga, gb);
         fmt.begin(args, band, ga, gb);
 
-        u32x4 ar[S::kAPer];  // the next chunk's pieces, on their way to LDS
-        // Pieces [j0, j1) of chunk t.
-        auto load_a_part = [&](int t, int j0, int j1) {
+        // Pieces [j0, j1) of chunk t, straight from memory into LDS buffer `buf` (buffer loads with
+        // the LDS modifier: lane l of the wave's piece j lands at ((wave kAPer + j) 64 + l) 16).
+        // They count in vmcnt like any load and are complete in LDS when it says so.
+        auto load_a_part = [&](int t, int buf, int j0, int j1) {
             const uint32_t gbyte = (uint32_t)(ga * F::kUnitK + t * KW * 64) * 2u;
 #pragma unroll
-            for (int j = j0; j < j1; ++j) ar[j] = buffer_load16(a_rsrc, a_src[j] + gbyte, 0);
+            for (int j = j0; j < j1; ++j)
+                buffer_load_lds16(a_rsrc, lds_bytes + buf * S::kABuf + (wave * S::kAPer + j) * 1024, a_src[j] + gbyte);
         };
-        auto load_a = [&](int t) { load_a_part(t, 0, S::kAPer); };
+        auto load_a = [&](int t, int buf) { load_a_part(t, buf, 0, S::kAPer); };
         constexpr int kAHalf = (S::kAPer + 1) / 2;
-        auto store_a = [&](int buf) {
-#pragma unroll
-            for (int j = 0; j < S::kAPer; ++j)
-                *(u32x4 *)(lds_bytes + buf * S::kABuf + ((wave * S::kAPer + j) * 64 + lane) * 16) = ar[j];
-        };
         auto load_s = [&](int t) { fmt.load_s(t); };
         auto store_s = [&](int buf) { fmt.store_s(side_lds + buf * S::kSBuf); };
         auto load_w = [&](int slot_, int t) { fmt.load_w(slot_, t); };
@@ -454,17 +455,16 @@ mma_kernel(MmaArgs args) {
         // sub-steps 2 and 3.
         const int Tp = (T + D - 1) / D * D;
         auto nbuf = [&](int b) { return b == S::kNB - 1 ? 0 : b + 1; };
-        load_a(0);
+        load_a(0, 0);
         load_s(0);
         load_w(0, 0);
         wait_vmcnt<kWLoads>();
-        store_a(0);
         store_s(0);
         load_s(1);
         load_w(1, 1);
         wait_vmcnt<kWLoads>();
         store_s(1);
-        load_a(1);
+        load_a(1, 1);
         load_s(2);
         load_w(2, 2);
         lds_barrier();
@@ -487,21 +487,20 @@ mma_kernel(MmaArgs args) {
         auto step = [&](int t, int d, int abuf, auto &&mid, auto &&hook) {
             const int next = (d + 1) % D;
             fmt.prepare(next, side_lds + nbuf(abuf) * S::kSBuf, live(t + 1));
+            // Fragments of sub-step i + 1 are read as soon as sub-step i's MFMAs are issued, so their
+            // LDS latency hides behind the dequantization (two alternating register sets; sub-step 0
+            // uses af_pre, read at the previous step's barrier).
+            bf16x8 af_odd[FM], af_even[FM];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 if (i == 2) mid();
-                bf16x8 af[FM];
-                if (i == 0) {
-#pragma unroll
-                    for (int f = 0; f < FM; ++f) af[f] = af_pre[f];
-                } else {
-                    read_af(af, abuf, i);
-                }
+                bf16x8 *af = i == 0 ? af_pre : (i & 1) ? af_odd : af_even;
 #pragma unroll
                 for (int w = 0; w < NW; ++w)
 #pragma unroll
                     for (int f = 0; f < FM; ++f)
                         acc[w][f] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[f], bw[w][i], acc[w][f], 0, 0, 0);
+                if (i < 3) read_af(((i + 1) & 1) ? af_odd : af_even, abuf, i + 1);
 #pragma unroll
                 for (int w = 0; w < NW; ++w) bw[w][i] = fmt.operand(w, i, next);
                 hook(i);
@@ -526,7 +525,6 @@ mma_kernel(MmaArgs args) {
                 step(t, d, abuf,
                      [&] {
                          wait_vmcnt<kWLoads>();  // chunk t + 1, sidecars t + 2 have arrived
-                         store_a(nbuf(abuf));
                          store_s(nbuf(nbuf(abuf)));
                          lds_barrier();
                          read_af(af_pre, nbuf(abuf), 0);
@@ -534,10 +532,10 @@ mma_kernel(MmaArgs args) {
                      [&](int i) {
                          if (i == 0) load_w(d, t + D);
                          if (i == 2) {
-                             load_a_part(t + 2, 0, kAHalf);
+                             load_a_part(t + 2, nbuf(nbuf(abuf)), 0, kAHalf);
                              load_s(t + 3);
                          }
-                         if (i == 3) load_a_part(t + 2, kAHalf, S::kAPer);
+                         if (i == 3) load_a_part(t + 2, nbuf(nbuf(abuf)), kAHalf, S::kAPer);
                      });
                 abuf = nbuf(abuf);
             }
@@ -551,14 +549,13 @@ mma_kernel(MmaArgs args) {
             step(t, d, abuf,
                  [&] {
                      wait_vmcnt<0>();
-                     if (d < 2) store_a(nbuf(abuf));
                      if (d == 0) store_s(nbuf(nbuf(abuf)));
                      lds_barrier();
                      if (d < 2) read_af(af_pre, nbuf(abuf), 0);
                  },
                  [&](int i) {
-                     if (d == 0 && i == 2) load_a_part(t + 2, 0, kAHalf);
-                     if (d == 0 && i == 3) load_a_part(t + 2, kAHalf, S::kAPer);
+                     if (d == 0 && i == 2) load_a_part(t + 2, nbuf(nbuf(abuf)), 0, kAHalf);
+                     if (d == 0 && i == 3) load_a_part(t + 2, nbuf(nbuf(abuf)), kAHalf, S::kAPer);
                  });
             abuf = nbuf(abuf);
         }
@@ -653,7 +650,7 @@ mma_kernel(MmaArgs args) {
         __syncthreads();
         const int count = fix_count;
         if (count == 0) return;
-        // Partials are read in batches of four contributors for every row of the thread at once,
+        // Partials are read in batches of contributors for every row of the thread at once,
         // so that their memory latencies overlap; each sum still runs in contributor order.
         constexpr int kMine = S::kRows / kRowStep;  // rows of this thread (those past `rows` idle)
         float v[kMine][NW];
@@ -661,10 +658,11 @@ mma_kernel(MmaArgs args) {
         for (int j = 0; j < kMine; ++j)
 #pragma unroll
             for (int w = 0; w < NW; ++w) v[j][w] = 0.0f;
-        for (int c0 = 0; c0 < count; c0 += 4) {
-            float x[4][kMine][NW];
+        constexpr int kBatch = kMine * NW >= 32 ? 1 : 32 / (kMine * NW) < 4 ? 32 / (kMine * NW) : 4;
+        for (int c0 = 0; c0 < count; c0 += kBatch) {
+            float x[kBatch][kMine][NW];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
+            for (int q = 0; q < kBatch; ++q) {
                 const int entry = fix_list[c0 + q < count ? c0 + q : count - 1];
 #pragma unroll
                 for (int j = 0; j < kMine; ++j) {
@@ -677,7 +675,7 @@ mma_kernel(MmaArgs args) {
                 }
             }
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
+            for (int q = 0; q < kBatch; ++q)
                 if (c0 + q < count)
 #pragma unroll
                     for (int j = 0; j < kMine; ++j)
