@@ -106,9 +106,8 @@ int q4_gemm_impl(const splosh_q4_weight *w, const splosh_q4_weight *up, const ui
                             (!residual || aligned(residual, 16)) &&
                             splosh::prefill_fits(rows, w->rows, w->inner, lda, ldc);
     const char *decode_env = getenv("SPLOSH_DECODE");
-    const bool decode_ok = wide16 && workspace && decode_env && atoi(decode_env) != 0 &&
-                           splosh::decode_fits(rows, w->rows, w->inner, w->order) &&
-                           splosh::decode_plan_ok(w->rows, w->inner / kGroupSize, workspace_bytes);
+    const bool decode_ok = wide16 && !(decode_env && atoi(decode_env) == 0) &&
+                           splosh::decode_fits(rows, w->rows, w->inner, w->order);
     int choice = kernel;
     if (choice == SPLOSH_KERNEL_AUTO) {
         if (!eligible) choice = SPLOSH_KERNEL_SCALAR;
@@ -149,7 +148,7 @@ int q4_gemm_impl(const splosh_q4_weight *w, const splosh_q4_weight *up, const ui
                             "stream kernel needs inner % 64 == 0, lda % 8 == 0 and aligned operands");
             if (wide16 && decode_ok) {
                 return hip_status(splosh::launch_q4_decode(*w, up, a, lda, out, ldc, out_dtype, residual, rows,
-                                                           workspace, stream),
+                                                           stream),
                                   "q4 decode launch");
             }
             if (wide16 && splosh::lanes_fit(rows, w->rows, w->inner, w->row_stride_words, up != nullptr)) {
@@ -327,10 +326,8 @@ size_t splosh_workspace_bytes(int64_t rows, int64_t columns, int64_t inner) {
     const size_t tile = splosh::tile_workspace_bytes(rows, columns, groups, true);
     const size_t mma = rows <= 64 ? splosh::mma_workspace_bytes(rows, columns, groups, true) : 0;
     const size_t prefill = rows > 64 && columns % 128 == 0 ? splosh::prefill_workspace_bytes(rows, columns, groups) : 0;
-    const size_t decode = rows <= 2 && columns % 128 == 0 ? splosh::decode_workspace_bytes(columns) : 0;
     size_t need = tile > mma ? tile : mma;
-    need = need > prefill ? need : prefill;
-    return need > decode ? need : decode;
+    return need > prefill ? need : prefill;
 }
 
 // Q4GemmRuntime.dispatch (Runtime/Q4Runtime.swift:94-145).

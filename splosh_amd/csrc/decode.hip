@@ -1,27 +1,33 @@
 // decode.hip -- decode GEMV (one or two activation rows) over tiled q4 weights on every CU.
 //
-// The decode step reads a 50 MB weight once; the kernel has to spread that read evenly over all
-// compute units and keep it in flight while the arithmetic of the groups already loaded runs.
+// The decode step reads a 50 MB weight once. The kernel spreads that read over many small
+// workgroups, keeps it in flight while the arithmetic of the groups already loaded runs, and needs
+// no reduction across workgroups.
 //
-// Work split. The output rows form blocks of 32 (one wave's worth: lane l owns row l >> 1 of the
-// block and half h = l & 1 of every group), and the (block, group) pairs -- "units" -- are cut into
-// gridDim.x equal contiguous ranges, one a workgroup (4 per CU). A range covers parts of two or
-// three blocks; within a block segment the four waves take every fourth group. A block that one
-// workgroup covers whole is written directly; a block shared by several writes fp32 partials to
-// the caller's workspace, and the last of its workgroups to finish (an atomic counter per block,
-// reset by that workgroup for the next call) sums them in workgroup order -- deterministic -- and
-// applies the epilogue. No second kernel.
+// Mapping. A workgroup owns a block of B output rows (B = 16 or 32, inside one 128-row tile) over
+// the whole of K: N / B workgroups, several a CU, so the read is spread evenly. In the tiled layout
+// (Model/Retile.swift:135-153) the block's records of one group are B * 32 contiguous bytes. Lane l
+// of a wave takes half h = l & 1 of row (l >> 1) % B of the group (l >> 1) / B of a step of
+// 64 / (2 B) groups, so one 16-byte load a lane reads the step's records in order. The four waves
+// take every fourth step.
 //
-// Arithmetic. The workgroup first stages the activation rows in LDS in the form the math wants:
-// for every code word (8 consecutive k), the four bf16 pairs (x_j, x_{j+4}), j = 0..3, and for
-// every half group the sum of its 32 activations. A code word becomes four pairs
-// (128 + q_j, 128 + q_{j+4}) with one v_and_or_b32 each, which meet the activation pairs in
-// v_dot2_f32_bf16: with P = sum x (128 + q) and S = sum x over a half group,
-// acc += s P + (b - 128 s) S (the per-group identity of engine_na.metal:8-20, split over the two
-// halves). Eight VALU instructions per eight weights and row, plus two per half group.
+// Activations. The workgroup first stages the activation rows in LDS in the form the arithmetic
+// wants: for every 8 consecutive k the four bf16 pairs (x_j, x_{j+4}), and for every half group the
+// sum of its 32 activations. Their loads go out before the weight loads (loads complete in order,
+// so staging waits for nothing else).
 //
-// Loads in flight. A wave walks its groups in chunks of CH, with the next chunk's codes and
-// sidecars loaded before the current chunk is computed.
+// Arithmetic. A code word becomes four bf16 pairs (128 + q_j, 128 + q_{j+4}) with one v_and_or_b32
+// each (after a shift), which meet the activation pairs in v_dot2_f32_bf16: with P = sum x (128 + q)
+// and S = sum x over the lane's half group, acc += s P + (b - 128 s) S (the per-group identity of
+// engine_na.metal:8-20, split over the two halves). Eleven VALU instructions per eight weights and
+// row.
+//
+// Loads in flight. Each wave keeps D steps in flight in a register ring; the loads of a step are
+// issued D steps before its arithmetic. Groups past K read an out-of-range buffer offset, which
+// returns zero (scale and bias zero: no contribution) without touching memory.
+//
+// Reduction. The two half lanes of a row meet in a DPP swap, then the waves (and the groups of a
+// step) in LDS, and the workgroup writes its B rows (silu(g) * u for the fused gate+up).
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -36,28 +42,20 @@ struct DecodeArgs {
     const uint16_t *scales[2];
     const uint16_t *biases[2];
     int64_t n;
-    int64_t groups;
+    int groups;
     const uint16_t *a;
     int64_t lda;
     void *out;
     int64_t ldc;
     const void *residual;
-    int64_t rows;
+    int rows;
     int out_dtype;
-    float *partial;     // [gridDim.x][2][NW][R][32]
-    int *counters;      // [n / 32], zero between calls
-    int64_t units;      // (n / 32) * groups
     uint32_t code_bytes, sidecar_bytes;
 };
 
-#ifndef SPLOSH_DECODE_WGPC
-#define SPLOSH_DECODE_WGPC 4
-#endif
-#ifndef SPLOSH_DECODE_CH
-#define SPLOSH_DECODE_CH 4
-#endif
-constexpr int kDecodeWgPerCu = SPLOSH_DECODE_WGPC;
-constexpr int kDecodeFinishMax = 64;  // contributors a block can have (checked on the host)
+constexpr int kDecodeDepth = 2;  // steps in flight a wave (measured: 2 beats 1, 3, 4, 6 and 8)
+constexpr int kDecodeWg = 256;   // threads a workgroup
+constexpr int kDecodeWaves = kDecodeWg / 64;
 
 __device__ __forceinline__ float ddot2(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_d, a), __builtin_bit_cast(bf16x2_d, b), c, false);
@@ -72,127 +70,128 @@ __device__ __forceinline__ uint32_t dswap_pair(uint32_t v) {
     return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);
 }
 
-// Workgroup i of P covers units [U i / P, U (i + 1) / P).
-__device__ __forceinline__ int64_t range_start(int64_t units, int i, int P) { return units * i / P; }
-
-template <int R, int NW, int CH>
-__global__ void __launch_bounds__(256)
+template <int R, int NW, int B, int D>
+__global__ void __launch_bounds__(kDecodeWg)
 q4_decode_kernel(DecodeArgs args) {
-    extern __shared__ __align__(16) uint32_t lds32[];
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int h = lane & 1, rl = lane >> 1;
-    const int G = (int)args.groups;
-    const uint32_t G32 = (uint32_t)G;
+    extern __shared__ __align__(16) unsigned char lds[];
+    constexpr int GPS = 64 / (2 * B);  // groups a step
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int h = lane & 1, row = (lane >> 1) % B, gsub = (lane >> 1) / B;
+    const int G = args.groups;
     const int K = G * kGroup;
-    const int words = K / 8;  // code words (and activation pair quads) per row
+    const int steps = (G + GPS - 1) / GPS;
 
-    // LDS: xp[R][words] (16 bytes each: the four activation pairs of a code word), xs[R][K / 32]
-    // (half-group sums), then the reduction area red[4][NW][R][32] and the fix-up flag.
-    u32x4 *xp = (u32x4 *)lds32;
-    float *xs = (float *)(lds32 + 4 * R * words);
+    // LDS: xp[R][K / 8] (16 bytes: the four activation pairs of a code word), xs[R][K / 32]
+    // (half-group sums), red[waves][GPS][NW][R][B] (the partial sums).
+    u32x4 *xp = (u32x4 *)lds;
+    float *xs = (float *)(xp + R * (K / 8));
     float *red = xs + R * (K / 32);
-    int *flag = (int *)(red + 4 * NW * R * 32);
 
-    const uint32_t kMask = 0x000F000Fu;
-    uint32_t magic;
-    asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(magic));
-    rsrc_t q_rsrc[NW];
-    const uint16_t *side[NW];  // lane h = 0 fetches the scale, h = 1 the bias; they swap at use
+    // 1. This thread's first activation slices (a half group: 32 values, four 16-byte loads).
+    const int items = R * (K / 32);
+    constexpr int kStage = 2;
+    u32x4 xin[kStage][4];
+#pragma unroll
+    for (int t = 0; t < kStage; ++t) {
+        const int e = threadIdx.x + t * kDecodeWg;
+        const int m = e < items ? e / (K / 32) : 0, hg = e < items ? e % (K / 32) : 0;
+        const u32x4 *src = (const u32x4 *)(args.a + (int64_t)(m < args.rows ? m : 0) * args.lda + hg * 32);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xin[t][j] = src[j];
+    }
+    auto stage = [&](int e, const u32x4 (&v)[4]) {
+        float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            u32x4 pq;
+            pq.x = perm_bytes(v[j].z, v[j].x, 0x05040100u);  // (x0, x4)
+            pq.y = perm_bytes(v[j].z, v[j].x, 0x07060302u);  // (x1, x5)
+            pq.z = perm_bytes(v[j].w, v[j].y, 0x05040100u);  // (x2, x6)
+            pq.w = perm_bytes(v[j].w, v[j].y, 0x07060302u);  // (x3, x7)
+            xp[e * 4 + j] = pq;
+            s0 = ddot2(v[j].x, 0x3F803F80u, s0);
+            s1 = ddot2(v[j].y, 0x3F803F80u, s1);
+            s0 = ddot2(v[j].z, 0x3F803F80u, s0);
+            s1 = ddot2(v[j].w, 0x3F803F80u, s1);
+        }
+        xs[e] = s0 + s1;
+    };
+
+    // 2. The first D steps' weight loads.
+    rsrc_t q_rsrc[NW], s_rsrc[NW], b_rsrc[NW];
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
         q_rsrc[w] = make_rsrc(args.packed[w], args.code_bytes);
-        side[w] = h == 0 ? args.scales[w] : args.biases[w];
+        s_rsrc[w] = make_rsrc(args.scales[w], args.sidecar_bytes);
+        b_rsrc[w] = make_rsrc(args.biases[w], args.sidecar_bytes);
     }
-
-    const int P = gridDim.x;
-    const rsrc_t p_rsrc = make_rsrc(args.partial, (uint32_t)P * 2u * (uint32_t)(NW * R * 32) * 4u);
-    const int64_t u_begin = range_start(args.units, blockIdx.x, P), u_stop = range_start(args.units, blockIdx.x + 1, P);
-    // Segment state: block blk, groups [ga, gb) of which this wave takes ga + wave + 4 i, i < ng.
-    int blk = 0, ga = 0, gb = 0, ng = 0;
-    uint32_t rec0 = 0;
-    auto begin_segment = [&](int64_t u) {
-        blk = (int)(u / G);
-        ga = (int)(u % G);
-        gb = (int)((int64_t)ga + (u_stop - u) < G ? ga + (u_stop - u) : G);
-        ng = (gb - ga - wave + 3) / 4;
-        const int64_t rr = (int64_t)blk * 32 + rl;
-        const uint32_t row = (uint32_t)(rr < args.n ? rr : args.n - 1);
-        rec0 = (row >> 7) * G32 * 128u + (row & 127u);  // record of group 0
-    };
-    u32x4 cq[2][CH][NW];
-    uint32_t cs[2][CH][NW];
-    auto load_chunk = [&](int buf, int c0) {
+    const int64_t r0 = (int64_t)blockIdx.x * B;
+    const uint32_t tile_base = (uint32_t)(r0 >> 7) * (uint32_t)G * 128u + (uint32_t)(r0 & 127) + (uint32_t)row;
+    u32x4 cq[D][NW];
+    uint32_t cs[D][NW], cb[D][NW];
+    auto issue = [&](int slot, int t) {
+        // Step t of this wave: groups (wave + 4 t) GPS + gsub.
+        const int g = (wave + kDecodeWaves * t) * GPS + gsub;
+        const bool live = g < G;
+        const uint32_t rec = tile_base + (uint32_t)(live ? g : 0) * 128u;
+        // Out of range: zero, no memory traffic. (Every load is unconditional: a load under a branch
+        // makes the compiler's wait counts conservative, which stalls the ring.)
+        const uint32_t off = live ? rec * 32u + 16u * h : 0xFFFFFFF0u;
+        const uint32_t soff = live ? rec * 2u : 0xFFFFFFF0u;
 #pragma unroll
-        for (int k = 0; k < CH; ++k) {
-            int i = c0 + k;
-            i = i < ng ? i : (ng > 0 ? ng - 1 : 0);
-            const uint32_t g = (uint32_t)(ga + wave + 4 * i < gb ? ga + wave + 4 * i : gb - 1);
-            const uint32_t rec = rec0 + g * 128u;
-#pragma unroll
-            for (int w = 0; w < NW; ++w) {
-                cq[buf][k][w] = buffer_load16_cp<2>(q_rsrc[w], rec * 32u + 16u * h, 0);
-                cs[buf][k][w] = side[w][rec];
-            }
+        for (int w = 0; w < NW; ++w) {
+            cq[slot][w] = buffer_load16_cp<2>(q_rsrc[w], off, 0);
+            cs[slot][w] = buffer_load_u16(s_rsrc[w], soff, 0);
+            cb[slot][w] = buffer_load_u16(b_rsrc[w], soff, 0);
         }
     };
-
-    // The first segment's first loads go out before the activations are staged.
-    if (u_begin < u_stop) {
-        begin_segment(u_begin);
-        load_chunk(0, 0);
+    // Every wave runs the same number of steps (those past K load zeros and add nothing), so the
+    // loop body is straight-line code and the compiler's wait counts keep D steps in flight.
+    const int my_steps = (steps + kDecodeWaves - 1) / kDecodeWaves;
+#pragma unroll
+    for (int k = 0; k < D; ++k) {
+        issue(k, k);
+        __builtin_amdgcn_sched_barrier(0);  // the same load order as the loop's refills
     }
-    // ---- stage the activations: thread j of the workgroup takes half groups j, j + 256, ... ----
-    for (int e = tid; e < R * (K / 32); e += 256) {
+
+    // 3. Stage the activations (the rest of them, for long K, after the weight loads went out).
+#pragma unroll
+    for (int t = 0; t < kStage; ++t)
+        if (threadIdx.x + t * kDecodeWg < items) stage(threadIdx.x + t * kDecodeWg, xin[t]);
+    for (int e = threadIdx.x + kStage * kDecodeWg; e < items; e += kDecodeWg) {
         const int m = e / (K / 32), hg = e % (K / 32);
-        const int mr = m < args.rows ? m : 0;
-        const u32x4 *src = (const u32x4 *)(args.a + (int64_t)mr * args.lda + hg * 32);
-        float s0 = 0.0f, s1 = 0.0f;
+        const u32x4 *src = (const u32x4 *)(args.a + (int64_t)(m < args.rows ? m : 0) * args.lda + hg * 32);
+        u32x4 v[4];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const u32x4 v = src[k];  // elements 8k .. 8k + 7 of the half group
-            u32x4 pq;
-            pq.x = perm_bytes(v.z, v.x, 0x05040100u);  // (x0, x4)
-            pq.y = perm_bytes(v.z, v.x, 0x07060302u);  // (x1, x5)
-            pq.z = perm_bytes(v.w, v.y, 0x05040100u);  // (x2, x6)
-            pq.w = perm_bytes(v.w, v.y, 0x07060302u);  // (x3, x7)
-            xp[m * words + hg * 4 + k] = pq;
-            s0 = ddot2(v.x, 0x3F803F80u, s0);
-            s1 = ddot2(v.y, 0x3F803F80u, s1);
-            s0 = ddot2(v.z, 0x3F803F80u, s0);
-            s1 = ddot2(v.w, 0x3F803F80u, s1);
-        }
-        xs[m * (K / 32) + hg] = s0 + s1;
+        for (int j = 0; j < 4; ++j) v[j] = src[j];
+        stage(e, v);
     }
-    __syncthreads();
+    lds_barrier();  // LDS only: the weight loads stay in flight
 
+    const uint32_t kMask = 0x000F000Fu;
+    uint32_t magic;  // the bf16 exponent of 128 in both halves
+    asm("v_mov_b32 %0, 0x43004300" : "=v"(magic));
 
-    int slot = 0;
-    for (int64_t u = u_begin; u < u_stop;) {
-        const int64_t u_seg = u;
-        const bool whole = ga == 0 && gb == G;
-        const int seg_blk = blk;
-        slot = u_seg == u_begin ? 0 : 1;  // the first segment of the range uses slot 0
-        u += gb - ga;
-        float acc[NW][R];
+    float acc[NW][R];
 #pragma unroll
-        for (int w = 0; w < NW; ++w)
+    for (int w = 0; w < NW; ++w)
 #pragma unroll
-            for (int m = 0; m < R; ++m) acc[w][m] = 0.0f;
-        auto compute_chunk = [&](int buf, int c0) {
+        for (int m = 0; m < R; ++m) acc[w][m] = 0.0f;
+
+    for (int t0 = 0; t0 < my_steps; t0 += D) {
 #pragma unroll
-            for (int k = 0; k < CH; ++k) {
-                const int i = c0 + k;
-                const bool live = i < ng;
-                const int g = ga + wave + 4 * (live ? i : 0);
-                const int hg = 2 * g + h;  // half group of this lane
-                u32x4 xv[R][4];
+        for (int k = 0; k < D; ++k) {
+            const int t = t0 + k;
+            {
+                const int g = (wave + kDecodeWaves * t) * GPS + gsub;
+                const int hg = 2 * (g < G ? g : G - 1) + h;  // the lane's half group
+                u32x4 xq[R][4];
                 float sx[R];
 #pragma unroll
                 for (int m = 0; m < R; ++m) {
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) xv[m][j] = xp[m * words + hg * 4 + j];
+                    for (int j = 0; j < 4; ++j) xq[m][j] = xp[(m * (K / 32) + hg) * 4 + j];
                     sx[m] = xs[m * (K / 32) + hg];
                 }
 #pragma unroll
@@ -202,71 +201,61 @@ q4_decode_kernel(DecodeArgs args) {
                     for (int m = 0; m < R; ++m) pq[m] = pr[m] = 0.0f;
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
-                        const uint32_t word = cq[buf][k][w][j];
+                        const uint32_t word = cq[k][w][j];
                         const uint32_t b0 = dand_or(word, kMask, magic);
                         const uint32_t b1 = dand_or(word >> 4, kMask, magic);
                         const uint32_t b2 = dand_or(word >> 8, kMask, magic);
                         const uint32_t b3 = dand_or(word >> 12, kMask, magic);
 #pragma unroll
                         for (int m = 0; m < R; ++m) {
-                            pq[m] = ddot2(b0, xv[m][j][0], pq[m]);
-                            pr[m] = ddot2(b1, xv[m][j][1], pr[m]);
-                            pq[m] = ddot2(b2, xv[m][j][2], pq[m]);
-                            pr[m] = ddot2(b3, xv[m][j][3], pr[m]);
+                            pq[m] = ddot2(b0, xq[m][j].x, pq[m]);
+                            pr[m] = ddot2(b1, xq[m][j].y, pr[m]);
+                            pq[m] = ddot2(b2, xq[m][j].z, pq[m]);
+                            pr[m] = ddot2(b3, xq[m][j].w, pr[m]);
                         }
                     }
-                    const uint32_t mine = cs[buf][k][w];
-                    const uint32_t other = dswap_pair(mine);
-                    const float s = live ? bf16_bits_to_f32(h == 0 ? mine : other) : 0.0f;
-                    const float b = bf16_bits_to_f32(h == 0 ? other : mine);
-                    const float bp = live ? __builtin_fmaf(-128.0f, s, b) : 0.0f;
+                    const float s = bf16_bits_to_f32(cs[k][w]);
+                    const float bp = __builtin_fmaf(-128.0f, s, bf16_bits_to_f32(cb[k][w]));
 #pragma unroll
                     for (int m = 0; m < R; ++m)
                         acc[w][m] = __builtin_fmaf(s, pq[m] + pr[m], __builtin_fmaf(bp, sx[m], acc[w][m]));
                 }
             }
-        };
-        // Chunks of CH groups, the next one's loads issued before the current one's arithmetic.
-        for (int c0 = 0; c0 < ng; c0 += 2 * CH) {
-            load_chunk(1, c0 + CH);
-            compute_chunk(0, c0);
-            load_chunk(0, c0 + 2 * CH);
-            compute_chunk(1, c0 + CH);
+            issue(k, t + D);
+            // Keep the refill here, in the prologue's order: left to itself the scheduler sinks all of
+            // them to the end of the unrolled body (and the merged wait counts at the loop head turn
+            // conservative), which drains the ring every D steps.
+            __builtin_amdgcn_sched_barrier(0);
         }
+    }
 
-        // The next segment's first loads go out before this one's reduction and fix-up.
-        if (u < u_stop) {
-            begin_segment(u);
-            load_chunk(0, 0);
-        }
-        const int blk_next = blk;
-        blk = seg_blk;
-
-        // ---- reduce: the two half lanes of a row, then the four waves in LDS ----
+    // 4. Sum the half lanes, then the waves and the groups of a step in LDS; write the B rows.
+#pragma unroll
+    for (int w = 0; w < NW; ++w)
+#pragma unroll
+        for (int m = 0; m < R; ++m)
+            acc[w][m] += __builtin_bit_cast(float, dswap_pair(__builtin_bit_cast(uint32_t, acc[w][m])));
+    if (h == 0) {
 #pragma unroll
         for (int w = 0; w < NW; ++w)
 #pragma unroll
-            for (int m = 0; m < R; ++m)
-                acc[w][m] += __builtin_bit_cast(float, dswap_pair(__builtin_bit_cast(uint32_t, acc[w][m])));
-        if (h == 0) {
+            for (int m = 0; m < R; ++m) red[(((wave * GPS + gsub) * NW + w) * R + m) * B + row] = acc[w][m];
+    }
+    __syncthreads();
+    if ((int)threadIdx.x < R * B) {
+        const int m = threadIdx.x / B, rr = threadIdx.x % B;
+        const int64_t nn = r0 + rr;
+        float v[NW];
 #pragma unroll
-            for (int w = 0; w < NW; ++w)
+        for (int w = 0; w < NW; ++w) {
+            float sum = 0.0f;
 #pragma unroll
-                for (int m = 0; m < R; ++m) red[((wave * NW + w) * R + m) * 32 + rl] = acc[w][m];
+            for (int p = 0; p < kDecodeWaves * GPS; ++p) sum += red[((p * NW + w) * R + m) * B + rr];
+            v[w] = sum;
         }
-        __syncthreads();
-        constexpr int kOut = NW * R * 32;  // values of a block segment
-        float v = 0.0f;
-        if (tid < kOut) {
-#pragma unroll
-            for (int wv = 0; wv < 4; ++wv) v += red[wv * kOut + tid];
-        }
-        // Value tid = (w R + m) 32 + row of the block.
-        auto epilogue = [&](float v0, float v1, int m, int rrow) {
-            const int64_t nn = (int64_t)blk * 32 + rrow;
-            if (m >= args.rows || nn >= args.n) return;
-            float value = v0;
-            if constexpr (NW == 2) value = silu(v0) * v1;
+        if (m < args.rows && nn < args.n) {
+            float value = v[0];
+            if constexpr (NW == 2) value = silu(v[0]) * v[1];
             const int64_t index = m * args.ldc + nn;
             if (args.out_dtype == SPLOSH_F32) {
                 if (args.residual) value += ((const float *)args.residual)[index];
@@ -275,112 +264,47 @@ q4_decode_kernel(DecodeArgs args) {
                 if (args.residual) value += bf16_bits_to_f32(((const uint16_t *)args.residual)[index]);
                 ((uint16_t *)args.out)[index] = f32_to_bf16(value);
             }
-        };
-        if (whole) {
-            // red is reused: park the sums, then the first R * 32 threads apply the epilogue.
-            __syncthreads();
-            if (tid < kOut) red[tid] = v;
-            __syncthreads();
-            if (tid < R * 32) {
-                const int m = tid / 32, rrow = tid % 32;
-                epilogue(red[m * 32 + rrow], NW == 2 ? red[(R + m) * 32 + rrow] : 0.0f, m, rrow);
-            }
-        } else {
-            // A shared block: this workgroup's partial, then the fix-up by the last contributor.
-            // The partials cross XCDs, whose L2 caches are not coherent with each other: they are
-            // written and read with device-scope cache policy (sc0 sc1: through to memory), and the
-            // counter is a system-scope atomic (also sc0 sc1), so no L2 write-back or invalidation is needed.
-            constexpr int kDevice = 1 | 16;  // gfx94x cache policy sc0 | sc1
-            const uint32_t pbase = (uint32_t)(((int64_t)blockIdx.x * 2 + slot) * kOut) * 4u;
-            if (tid < kOut) __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), p_rsrc, pbase + tid * 4u, 0, kDevice);
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the partial has reached memory
-            __syncthreads();
-            if (tid == 0) {
-                // Contributors: the workgroups whose ranges meet [blk G, (blk + 1) G).
-                const int64_t lo = (int64_t)blk * G, hi = lo + G;
-                const int i_lo = (int)(((lo + 1) * P - 1) / args.units), i_hi = (int)((hi * P - 1) / args.units);
-                int count = 0;
-                for (int i = i_lo; i <= i_hi; ++i)
-                    if (range_start(args.units, i, P) != range_start(args.units, i + 1, P)) ++count;
-                const int old = __hip_atomic_fetch_add(args.counters + blk, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                *flag = old == count - 1 ? 1 : 0;
-            }
-            __syncthreads();
-            if (*flag) {
-                const int64_t lo = (int64_t)blk * G, hi = lo + G;
-                const int i_lo = (int)(((lo + 1) * P - 1) / args.units), i_hi = (int)((hi * P - 1) / args.units);
-                float sum = 0.0f;
-                if (tid < kOut) {
-                    for (int i = i_lo; i <= i_hi; ++i) {
-                        const int64_t s = range_start(args.units, i, P);
-                        if (s == range_start(args.units, i + 1, P)) continue;
-                        const int sl = s < lo ? 1 : 0;
-                        const uint32_t off = (uint32_t)(((int64_t)i * 2 + sl) * kOut + tid) * 4u;
-                        sum += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(p_rsrc, off, 0, kDevice));
-                    }
-                }
-                __syncthreads();
-                if (tid < kOut) red[tid] = sum;
-                __syncthreads();
-                if (tid < R * 32) {
-                    const int m = tid / 32, rrow = tid % 32;
-                    epilogue(red[m * 32 + rrow], NW == 2 ? red[(R + m) * 32 + rrow] : 0.0f, m, rrow);
-                }
-                if (tid == 0) __hip_atomic_store(args.counters + blk, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-            }
         }
-        __syncthreads();  // red is reused by the next segment
-        blk = blk_next;
     }
 }
 
-// Shapes the kernel takes: tiled weights, 32-row blocks, K staged whole in LDS.
-bool decode_fits(int64_t rows, int64_t columns, int64_t inner, int order) {
-    if (order != SPLOSH_Q4_TILED128 || rows < 1 || rows > 2 || inner % kGroup != 0 || columns % 128 != 0) return false;
-    const int64_t lds = 2 * inner * 2 + 2 * (inner / 32) * 4 + 4 * 2 * 2 * 32 * 4 + 16;
-    return lds <= 150 * 1024 && columns * (inner / kGroup) * 32 < ((int64_t)1 << 32) - 256;
-}
-
-static int decode_grid() {
+static int decode_cus() {
     int dev = 0, cus = 256;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
         cus = 256;
-    return cus * kDecodeWgPerCu;
+    return cus;
 }
 
-// Workspace: partials [grid][2][2][2][32] floats, then a counter per 32-row block (zero-filled by
-// the caller once; every call leaves them zero).
-static size_t decode_partial_bytes(int grid) { return (size_t)grid * 2 * 2 * 2 * 32 * sizeof(float); }
+// Row block: 32 rows when that gives at least two workgroups a CU, else 16 (more workgroups).
+static int decode_block(int64_t columns) { return columns / 32 >= 2 * decode_cus() ? 32 : 16; }
 
-size_t decode_workspace_bytes(int64_t columns) {
-    return decode_partial_bytes(decode_grid()) + (size_t)(columns / 32) * sizeof(int);
+static size_t decode_lds(int64_t rows, int64_t inner, int nw, int block) {
+    return (size_t)rows * inner * 2 + (size_t)rows * (inner / 32) * 4 +
+           (size_t)kDecodeWaves * (64 / (2 * block)) * nw * rows * block * 4;
 }
 
-bool decode_plan_ok(int64_t columns, int64_t groups, size_t workspace_bytes) {
-    const int grid = decode_grid();
-    const int64_t units = columns / 32 * groups;
-    // Contributors per block: about grid * groups / units + 2.
-    return workspace_bytes >= decode_workspace_bytes(columns) && units >= grid &&
-           (int64_t)grid * groups / units + 2 <= kDecodeFinishMax;
+// Shapes the kernel takes: tiled weights, 32-bit offsets, staged activations within 64 KB of LDS.
+bool decode_fits(int64_t rows, int64_t columns, int64_t inner, int order) {
+    if (order != SPLOSH_Q4_TILED128 || rows < 1 || rows > 2 || inner % kGroup != 0 || columns % 128 != 0) return false;
+    return decode_lds(rows, inner, 2, 16) <= 64 * 1024 && columns * (inner / kGroup) * 32 < ((int64_t)1 << 32) - 4096;
 }
 
-template <int R, int NW>
-static hipError_t launch_decode_v(const DecodeArgs &args, int grid, hipStream_t stream) {
-    const int K = (int)(args.groups * kGroup);
-    const size_t lds = (size_t)R * K * 2 + (size_t)R * (K / 32) * 4 + 4 * NW * R * 32 * 4 + 16;
-    auto kernel = q4_decode_kernel<R, NW, SPLOSH_DECODE_CH>;
-    static bool once = [&] {
-        (void)hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
-        return true;
-    }();
-    (void)once;
-    hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(256), lds, stream, args);
+template <int R, int NW, int B>
+static hipError_t launch_decode_v(const DecodeArgs &args, hipStream_t stream) {
+    const size_t lds = decode_lds(R, (int64_t)args.groups * kGroup, NW, B);
+    hipLaunchKernelGGL((q4_decode_kernel<R, NW, B, kDecodeDepth>), dim3((unsigned)(args.n / B)), dim3(kDecodeWg), lds,
+                       stream, args);
     return hipGetLastError();
 }
 
+template <int R, int NW>
+static hipError_t launch_decode_rn(const DecodeArgs &args, hipStream_t stream) {
+    return decode_block(args.n) == 32 ? launch_decode_v<R, NW, 32>(args, stream) : launch_decode_v<R, NW, 16>(args, stream);
+}
+
 hipError_t launch_q4_decode(const splosh_q4_weight &w, const splosh_q4_weight *up, const uint16_t *a, int64_t lda,
-                            void *out, int64_t ldc, int out_dtype, const void *residual, int64_t rows, void *workspace,
+                            void *out, int64_t ldc, int out_dtype, const void *residual, int64_t rows,
                             hipStream_t stream) {
     DecodeArgs args;
     args.packed[0] = w.packed;
@@ -390,23 +314,19 @@ hipError_t launch_q4_decode(const splosh_q4_weight &w, const splosh_q4_weight *u
     args.scales[1] = up ? up->scales : w.scales;
     args.biases[1] = up ? up->biases : w.biases;
     args.n = w.rows;
-    args.groups = w.inner / kGroup;
+    args.groups = (int)(w.inner / kGroup);
     args.a = a;
     args.lda = lda;
     args.out = out;
     args.ldc = ldc;
     args.residual = residual;
-    args.rows = rows;
+    args.rows = (int)rows;
     args.out_dtype = out_dtype;
-    const int grid = decode_grid();
-    args.partial = (float *)workspace;
-    args.counters = (int *)((char *)workspace + decode_partial_bytes(grid));
-    args.units = w.rows / 32 * args.groups;
     args.code_bytes = (uint32_t)(w.rows * args.groups * 32);
     args.sidecar_bytes = (uint32_t)(w.rows * args.groups * 2);
     if (rows == 1)
-        return up ? launch_decode_v<1, 2>(args, grid, stream) : launch_decode_v<1, 1>(args, grid, stream);
-    return up ? launch_decode_v<2, 2>(args, grid, stream) : launch_decode_v<2, 1>(args, grid, stream);
+        return up ? launch_decode_rn<1, 2>(args, stream) : launch_decode_rn<1, 1>(args, stream);
+    return up ? launch_decode_rn<2, 2>(args, stream) : launch_decode_rn<2, 1>(args, stream);
 }
 
 }  // namespace splosh
