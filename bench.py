@@ -5,7 +5,8 @@ activation rows (8 sessions x 8 drafted tokens), 4-bit g64 affine weights, the f
 projection (two K=5120 -> N=17408 weights sharing one activation read, out = silu(g) * u) followed
 by the down projection (K=17408 -> N=5120) on that output. One "step" is that pair of launches.
 
-    python bench.py [--steps K] [--warmup W] [--workload verify64|decode1|q5k|prefill2048|layerset]
+    python bench.py [--steps K] [--warmup W]
+                    [--workload verify64|decode1|q5k1|q5k16|q5k64|prefill2048|layerset|lmhead1|lmhead64]
 
 Inputs are synthetic (seeded, on the device): code words uniform random, scale = bf16(|N(0,0.02)|),
 bias = bf16(N(0,0.01)), activations bf16(N(0,1)). Several copies of the weight set are rotated so
@@ -155,6 +156,54 @@ def build_workload(name, rt, torch, gen, kernel):
         cfg = {"workload": "decode GEMV K5120->N17408", "rows": 1, "format": "mlx affine q4 g64, tiled128",
                "weight_copies": ncopy}
         return launches, b, 2 * m * n * k, {"gemv": b}, cfg, {"gemv": 2 * m * n * k}
+    if name == "layerset":
+        # Config 4: every linear projection of one hybrid layer set at M=64 (shapes as BASELINE.json
+        # states them): attention q, k, v, o; gated-delta input (qkv+z+b/a, 12288 outputs) and
+        # output (6144 -> 5120); the MLP's fused gate+up and down. One step is all nine launches.
+        m, h = 64, 5120
+        shapes = [("attn_q", 5120, h), ("attn_k", 1024, h), ("attn_v", 1024, h), ("attn_o", 5120, h),
+                  ("gdn_in", 12288, h), ("gdn_out", 5120, 6144), ("mlp_gate", 17408, h), ("mlp_up", 17408, h),
+                  ("mlp_down", 5120, 17408)]
+        one = sum(q4_bytes(n, k) for _, n, k in shapes)
+        ncopy = copies_for(one)
+        sets = [{nm: make_q4(rt, n, k, gen) for nm, n, k in shapes} for _ in range(ncopy)]
+        xs = {k: torch.randn(m, k, device="cuda", generator=gen).to(torch.bfloat16) for k in (h, 6144, 17408)}
+        outs = {nm: torch.empty(m, n, dtype=torch.bfloat16, device="cuda") for nm, n, _ in shapes}
+        scratch = {nm: workspace(m, n, k) for nm, n, k in shapes}
+        calls = [(nm, n, k) for nm, n, k in shapes if nm not in ("mlp_gate", "mlp_up")]
+
+        def launches(i):
+            ws_ = sets[i % ncopy]
+            out = [(nm, lambda nm=nm, k=k: rt.gemm(ws_[nm], xs[k], out=outs[nm], kernel=kernel, workspace=scratch[nm]))
+                   for nm, n, k in calls]
+            out.append(("mlp_in", lambda: rt.mlp_in(ws_["mlp_gate"], ws_["mlp_up"], xs[h], out=outs["mlp_gate"],
+                                                    kernel=kernel, workspace=scratch["mlp_gate"])))
+            return out
+
+        kb = {nm: q4_bytes(n, k) + m * k * 2 + m * n * 2 for nm, n, k in calls}
+        kb["mlp_in"] = 2 * q4_bytes(17408, h) + m * h * 2 + m * 17408 * 2
+        kf = {nm: 2 * m * n * k for nm, n, k in calls}
+        kf["mlp_in"] = 4 * m * 17408 * h
+        cfg = {"workload": "layer set at M=64: attention q/k/v/o, gated-delta in/out, MLP gate+up and down",
+               "rows": m, "format": "mlx affine q4 g64, tiled128", "weight_copies": ncopy}
+        return launches, sum(kb.values()), sum(kf.values()), kb, cfg, kf
+    if name.startswith("lmhead"):
+        # Config 4's lm_head, 5120 -> 248320, at M=1 or M=64.
+        m, k, n = int(name[6:]), 5120, 248320
+        ncopy = copies_for(q4_bytes(n, k))
+        ws = [make_q4(rt, n, k, gen) for _ in range(ncopy)]
+        x = torch.randn(m, k, device="cuda", generator=gen).to(torch.bfloat16)
+        out = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+        ws_lm = workspace(m, n, k)
+        b = q4_bytes(n, k) + m * k * 2 + m * n * 2
+
+        def launches(i):
+            w = ws[i % ncopy]
+            return [("lm_head", lambda: rt.gemm(w, x, out=out, kernel=kernel, workspace=ws_lm))]
+
+        cfg = {"workload": f"lm_head K5120->N248320 at M={m}", "rows": m, "format": "mlx affine q4 g64, tiled128",
+               "weight_copies": ncopy}
+        return launches, b, 2 * m * n * k, {"lm_head": b}, cfg, {"lm_head": 2 * m * n * k}
     if name.startswith("q5k"):
         m = int(name[3:] or 64)
         k, n = 17408, 5120
