@@ -395,9 +395,14 @@ int splosh_q5k_gemm(const splosh_q5k_weight *w, const uint16_t *a, int64_t lda, 
     const bool eligible = lda % 4 == 0 && aligned(a, 8) && aligned(w->plane0, 16) && aligned(w->plane1, 4) &&
                           aligned(w->meta, 16);
     const bool mma_ok = eligible && lda % 8 == 0 && aligned(a, 16) && splosh::q5k_mma_fits(rows, w->rows, w->inner, lda);
+    const char *decode_env = getenv("SPLOSH_DECODE");
+    const bool decode_ok = eligible && aligned(a, 16) && !(decode_env && atoi(decode_env) == 0) &&
+                           splosh::q5k_decode_fits(rows, w->rows, w->inner);
     int choice = kernel;
     if (kernel == SPLOSH_KERNEL_AUTO) {
         if (!eligible) choice = SPLOSH_KERNEL_SCALAR;
+        else if (decode_ok)
+            return hip_status(splosh::launch_q5k_decode(*w, a, out, out_dtype, residual, stream), "q5k decode launch");
         else if (mma_ok) choice = SPLOSH_KERNEL_DEQUANT;
         else choice = SPLOSH_KERNEL_STREAM;
     }

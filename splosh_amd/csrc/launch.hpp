@@ -126,6 +126,11 @@ hipError_t launch_q4_prefill(const PrefillPlan &plan, const splosh_q4_weight &w,
                              void *out, int64_t ldc, int out_dtype, const void *residual, int64_t rows,
                              void *workspace, hipStream_t stream);
 
+// The decode kernel for one activation row of Q5_K planes (q5k_decode.hip).
+bool q5k_decode_fits(int64_t rows, int64_t columns, int64_t inner);
+hipError_t launch_q5k_decode(const splosh_q5k_weight &w, const uint16_t *a, void *out, int out_dtype,
+                             const void *residual, hipStream_t stream);
+
 hipError_t launch_q5k_dequant(const splosh_q5k_weight &w, float *out, hipStream_t stream);
 hipError_t launch_q5k_repack(const uint8_t *native, int64_t rows, int64_t inner, uint8_t *p0,
                              uint8_t *p1, uint8_t *meta, bool inverse, hipStream_t stream);

@@ -1,0 +1,249 @@
+// q5k_decode.hip -- decode GEMV (one activation row) over GGUF Q5_K planes on every CU.
+//
+// The same structure as the q4 decode kernel (decode.hip): a workgroup owns a block of B output
+// rows over the whole of K, stages the activation row in LDS once, and streams the block's records
+// through a short register ring of straight-line loads; no reduction across workgroups.
+//
+// Mapping. Lane l takes row l % B of the block and one 32-element group, (l / B) of the step's
+// 64 / B groups; the four waves take every fourth step. Per group a lane reads its 16-byte plane0
+// record (low nibbles in chunk order), its 4-byte plane1 record (fifth bits) and the 16-byte meta
+// record of the group's block (fp16 d, dmin, packed 6-bit scales and minimums;
+// Model/GgufPlanes.swift:8-20).
+//
+// Arithmetic. In chunk order (gguf_formats.h:17-21) pair p of plane0 word c, (w >> 4p) & 0x000F000F,
+// holds two consecutive elements e0, e0 + 1 (e0 = 16 (p >> 1) + 4 c + 2 (p & 1)) in its 16-bit
+// halves, so the activations need no permutation: the pair meets the bf16 pair (x_e0, x_e0+1) as
+// staged. Their fifth bits are plane1 bits 8 c + 2 p and 8 c + 2 p + 1; with f those two bits,
+// (f * 0x80010) & 0x00100010 puts them at bits 4 and 20, so one more v_and_or_b32 gives
+// the bf16 pair (128 + code_e0, 128 + code_e0+1), code = nibble + 16 bit. With P = sum x (128 + code)
+// and S = sum x over the group, sum x w = ds P - (128 ds + dm) S for w = code ds - dm, ds = d sc,
+// dm = dmin mn (GgufQuant.swift:191-212).
+#include "common.hpp"
+#include "launch.hpp"
+
+namespace splosh {
+
+typedef __bf16 bf16x2_q __attribute__((ext_vector_type(2)));
+
+struct Q5DecodeArgs {
+    const uint8_t *plane0, *plane1, *meta;
+    int64_t n;
+    int groups;  // 32-element groups a row
+    const uint16_t *a;
+    void *out;
+    const void *residual;
+    int out_dtype;
+    uint32_t p0_bytes, p1_bytes, meta_bytes;
+};
+
+constexpr int kQ5DecodeDepth = 2;  // steps in flight a wave
+constexpr int kQ5DecodeWg = 256;
+constexpr int kQ5DecodeWaves = kQ5DecodeWg / 64;
+
+__device__ __forceinline__ float qdot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_q, a), __builtin_bit_cast(bf16x2_q, b), c, false);
+}
+__device__ __forceinline__ uint32_t qand_or(uint32_t a, uint32_t mask, uint32_t c) {
+    uint32_t d;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "s"(mask), "v"(c));
+    return d;
+}
+
+template <int B, int D>
+__global__ void __launch_bounds__(kQ5DecodeWg)
+q5k_decode_kernel(Q5DecodeArgs args) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    constexpr int GPS = 64 / B;  // groups a step
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int row = lane % B, gsub = lane / B;
+    const int G = args.groups;
+    const int K = G * 32;
+    const uint32_t blocks = (uint32_t)G / 8u;
+    const int steps = (G + GPS - 1) / GPS;
+
+    // LDS: xa[K / 8] (16 bytes: 8 activations as staged), xs[G] (group sums), red[waves][GPS][B].
+    u32x4 *xa = (u32x4 *)lds;
+    float *xs = (float *)(xa + K / 8);
+    float *red = xs + G;
+
+    // 1. This thread's first activation groups (32 values, four 16-byte loads each).
+    constexpr int kStage = 2;
+    u32x4 xin[kStage][4];
+#pragma unroll
+    for (int t = 0; t < kStage; ++t) {
+        const int e = threadIdx.x + t * kQ5DecodeWg;
+        const u32x4 *src = (const u32x4 *)(args.a + (e < G ? e : 0) * 32);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xin[t][j] = src[j];
+    }
+    auto stage = [&](int e, const u32x4 (&v)[4]) {
+        float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            xa[e * 4 + j] = v[j];
+            s0 = qdot2(v[j].x, 0x3F803F80u, s0);
+            s1 = qdot2(v[j].y, 0x3F803F80u, s1);
+            s0 = qdot2(v[j].z, 0x3F803F80u, s0);
+            s1 = qdot2(v[j].w, 0x3F803F80u, s1);
+        }
+        xs[e] = s0 + s1;
+    };
+
+    // 2. The first D steps' loads. Every load is unconditional (groups past K read an out-of-range
+    // offset: zeros, no memory traffic), so the compiler's wait counts keep the ring in flight.
+    const rsrc_t p0_rsrc = make_rsrc(args.plane0, args.p0_bytes);
+    const rsrc_t p1_rsrc = make_rsrc(args.plane1, args.p1_bytes);
+    const rsrc_t m_rsrc = make_rsrc(args.meta, args.meta_bytes);
+    const int64_t r0 = (int64_t)blockIdx.x * B;
+    const uint32_t rr = (uint32_t)(r0 & 127) + (uint32_t)row;
+    const uint32_t tile = (uint32_t)(r0 >> 7);
+    u32x4 c0[D], cm[D];
+    uint32_t c1[D];
+    auto issue = [&](int slot, int t) {
+        const int g = (wave + kQ5DecodeWaves * t) * GPS + gsub;
+        const bool live = g < G;
+        const uint32_t gg = live ? (uint32_t)g : 0u;
+        const uint32_t rec = (tile * (uint32_t)G + gg) * 128u + rr;
+        const uint32_t mrec = (tile * blocks + gg / 8u) * 128u + rr;
+        c0[slot] = buffer_load16_cp<2>(p0_rsrc, live ? rec * 16u : 0xFFFFFFF0u, 0);
+        c1[slot] = buffer_load_u32(p1_rsrc, live ? rec * 4u : 0xFFFFFFF0u, 0);
+        cm[slot] = buffer_load16(m_rsrc, live ? mrec * 16u : 0xFFFFFFF0u, 0);
+    };
+    const int my_steps = (steps + kQ5DecodeWaves - 1) / kQ5DecodeWaves;
+#pragma unroll
+    for (int k = 0; k < D; ++k) {
+        issue(k, k);
+        __builtin_amdgcn_sched_barrier(0);  // the same load order as the loop's refills
+    }
+
+    // 3. Stage the activations (the rest, for long K, after the weight loads went out).
+#pragma unroll
+    for (int t = 0; t < kStage; ++t)
+        if (threadIdx.x + t * kQ5DecodeWg < G) stage(threadIdx.x + t * kQ5DecodeWg, xin[t]);
+    for (int e = threadIdx.x + kStage * kQ5DecodeWg; e < G; e += kQ5DecodeWg) {
+        const u32x4 *src = (const u32x4 *)(args.a + e * 32);
+        u32x4 v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = src[j];
+        stage(e, v);
+    }
+    lds_barrier();  // LDS only: the weight loads stay in flight
+
+    const uint32_t kMask = 0x000F000Fu, kFifth = 0x00100010u;
+    uint32_t magic;  // the bf16 exponent of 128 in both halves
+    asm("v_mov_b32 %0, 0x43004300" : "=v"(magic));
+
+    float acc = 0.0f;
+    for (int t0 = 0; t0 < my_steps; t0 += D) {
+#pragma unroll
+        for (int k = 0; k < D; ++k) {
+            const int t = t0 + k;
+            const int g0 = (wave + kQ5DecodeWaves * t) * GPS + gsub;
+            const int g = g0 < G ? g0 : G - 1;  // past K: zero scales, no contribution
+            u32x4 xq[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) xq[j] = xa[g * 4 + j];
+            const float sx = xs[g];
+            // Scale and minimum of group j = g % 8 (GgufQuant.swift:196-203): packed byte k is meta
+            // byte 4 + k; both forms are computed and one is selected (no divergent branch).
+            const u32x4 m = cm[k];
+            const uint32_t j = (uint32_t)g & 7u, sh = 8u * (j & 3u);
+            const uint32_t sc_lo = __builtin_amdgcn_ubfe(m[1], sh, 6), mn_lo = __builtin_amdgcn_ubfe(m[2], sh, 6);
+            const uint32_t sc_hi = __builtin_amdgcn_ubfe(m[3], sh, 4) | (__builtin_amdgcn_ubfe(m[1], sh + 6, 2) << 4);
+            const uint32_t mn_hi = __builtin_amdgcn_ubfe(m[3], sh + 4, 4) | (__builtin_amdgcn_ubfe(m[2], sh + 6, 2) << 4);
+            const bool upper = j >= 4u;
+            const float d = half_bits_to_f32(m[0]), dmin = half_bits_to_f32(m[0] >> 16);
+            const float ds = d * (float)(upper ? sc_hi : sc_lo);
+            const float dm = dmin * (float)(upper ? mn_hi : mn_lo);
+            float pa = 0.0f, pb = 0.0f;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const uint32_t w = c0[k][c];
+#pragma unroll
+                for (int p = 0; p < 4; ++p) {
+                    const uint32_t nib = qand_or(p ? w >> (4 * p) : w, kMask, magic);
+                    // Exactly the two fifth bits (wider input would carry into bit 20).
+                    const uint32_t fb = __builtin_amdgcn_ubfe(c1[k], 8 * c + 2 * p, 2);
+                    const uint32_t pair = qand_or(fb * 0x80010u, kFifth, nib);
+                    const uint32_t xw = xq[(p >> 1) * 2 + (c >> 1)][(c & 1) * 2 + (p & 1)];  // x u32 8(p>>1) + 2c + (p&1)
+                    if (p & 1) pb = qdot2(pair, xw, pb);
+                    else pa = qdot2(pair, xw, pa);
+                }
+            }
+            const float live = g0 < G ? 1.0f : 0.0f;
+            acc = __builtin_fmaf(ds * live, pa + pb, __builtin_fmaf(-__builtin_fmaf(128.0f, ds, dm) * live, sx, acc));
+            issue(k, t + D);
+            // Keep the refill here, in the prologue's order (else the scheduler sinks the refills
+            // to the end of the unrolled body and the ring drains every D steps).
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+
+    // 4. The groups of a step and the waves meet in LDS; the workgroup writes its B rows.
+    red[(wave * GPS + gsub) * B + row] = acc;
+    __syncthreads();
+    if ((int)threadIdx.x < B) {
+        const int64_t nn = r0 + threadIdx.x;
+        float value = 0.0f;
+#pragma unroll
+        for (int p = 0; p < kQ5DecodeWaves * GPS; ++p) value += red[p * B + threadIdx.x];
+        if (nn < args.n) {
+            if (args.out_dtype == SPLOSH_F32) {
+                if (args.residual) value += ((const float *)args.residual)[nn];
+                ((float *)args.out)[nn] = value;
+            } else {
+                if (args.residual) value += bf16_bits_to_f32(((const uint16_t *)args.residual)[nn]);
+                ((uint16_t *)args.out)[nn] = f32_to_bf16(value);
+            }
+        }
+    }
+}
+
+static size_t q5k_decode_lds(int64_t inner, int block) {
+    return (size_t)inner * 2 + (size_t)(inner / 32) * 4 + (size_t)kQ5DecodeWaves * (64 / block) * block * 4;
+}
+
+bool q5k_decode_fits(int64_t rows, int64_t columns, int64_t inner) {
+    return rows == 1 && columns % 128 == 0 && inner % 256 == 0 && q5k_decode_lds(inner, 8) <= 64 * 1024 &&
+           columns * (inner / 32) * 16 < ((int64_t)1 << 32) - 4096;
+}
+
+static int q5k_decode_cus() {
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        cus = 256;
+    return cus;
+}
+
+template <int B>
+static hipError_t launch_q5k_decode_b(const Q5DecodeArgs &args, hipStream_t stream) {
+    hipLaunchKernelGGL((q5k_decode_kernel<B, kQ5DecodeDepth>), dim3((unsigned)(args.n / B)), dim3(kQ5DecodeWg),
+                       q5k_decode_lds((int64_t)args.groups * 32, B), stream, args);
+    return hipGetLastError();
+}
+
+hipError_t launch_q5k_decode(const splosh_q5k_weight &w, const uint16_t *a, void *out, int out_dtype,
+                             const void *residual, hipStream_t stream) {
+    Q5DecodeArgs args;
+    args.plane0 = w.plane0;
+    args.plane1 = w.plane1;
+    args.meta = w.meta;
+    args.n = w.rows;
+    args.groups = (int)(w.inner / 32);
+    args.a = a;
+    args.out = out;
+    args.residual = residual;
+    args.out_dtype = out_dtype;
+    args.p0_bytes = (uint32_t)(w.rows * args.groups * 16);
+    args.p1_bytes = (uint32_t)(w.rows * args.groups * 4);
+    args.meta_bytes = (uint32_t)(w.rows * (args.groups / 8) * 16);
+    // Row block: the largest of 32, 16 and 8 that gives at least two workgroups a CU.
+    const int64_t cus = q5k_decode_cus();
+    if (w.rows / 32 >= 2 * cus) return launch_q5k_decode_b<32>(args, stream);
+    if (w.rows / 16 >= 2 * cus) return launch_q5k_decode_b<16>(args, stream);
+    return launch_q5k_decode_b<8>(args, stream);
+}
+
+}  // namespace splosh

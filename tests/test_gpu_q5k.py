@@ -128,3 +128,29 @@ def test_dequant_kernel_remainder_bands_and_residual(rt):
     rt.gemm(w, bf16_tensor(a_bits), out=out, residual=out, kernel=rt.DEQUANT)
     check_close(out.cpu().numpy(), ref, bf16_out=False, tight=True, absref=abs_gemm(a_bits, dense),
                 label="q5k dequant remainder")
+
+
+@pytest.mark.parametrize("n,k", [(128, 256), (384, 1280), (1024, 4096), (5120, 2048), (256, 17408)])
+def test_decode_kernel(rt, n, k):
+    """The one-row Q5_K decode kernel (AUTO for rows == 1): all three row-block sizes (8, 16, 32 by
+    the column count), K of one block, K past the first staging pass (17408), the golden block in
+    place, a residual, and the same bits from two calls."""
+    native = oracle.q45k_random_native(n, k, seed=900 + n).reshape(n, -1)
+    golden = json.loads(GOLDEN.read_text())["q5K"]
+    native[min(5, n - 1), :176] = np.array(golden["bytes"], np.uint8)
+    native = native.reshape(-1)
+    w = rt.q5k_repack(dev_u8(native), n, k)
+    dense = oracle.q45k_decode(native).reshape(n, k)
+    a_bits = oracle.bf16_normal((1, k), seed=901)
+    ref = oracle.gemm_a_bf16_w_f32(a_bits, dense)
+    absref = abs_gemm(a_bits, dense)
+    for out_dtype in (torch.bfloat16, torch.float32):
+        first = rt.gemm(w, bf16_tensor(a_bits), out_dtype=out_dtype)
+        second = rt.gemm(w, bf16_tensor(a_bits), out_dtype=out_dtype)
+        assert torch.equal(first.view(torch.uint8), second.view(torch.uint8)), "calls differ"
+        check_close(to_f32(first), ref, bf16_out=out_dtype == torch.bfloat16, tight=True, absref=absref,
+                    label=f"q5k decode {n}x{k} {out_dtype}")
+    base = np.random.default_rng(7).normal(size=(1, n)).astype(np.float32)
+    out = torch.from_numpy(base.copy()).cuda()
+    rt.gemm(w, bf16_tensor(a_bits), out=out, residual=out)
+    check_close(out.cpu().numpy(), ref + base, bf16_out=False, tight=True, absref=absref, label="q5k decode residual")
