@@ -34,10 +34,12 @@ BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
 # a plain 256 MiB device copy (FETCH_SIZE reads half the bytes moved, WRITE_SIZE all of them).
 # The readings and commands are in profiles/; calls not listed are unmeasured (None).
 MEASURED_TRAFFIC = {
-    ("verify64", "mlp_in"): 51895.6 * 2 * 1024 + 10240.0 * 1024,   # mma_kernel<Q4Format<2, ...>, 2, ...>
-    ("verify64", "down"): 30763.3 * 2 * 1024 + 5120.0 * 1024,      # mma_kernel<Q4Format<1, ...>, 2, ...>
-    ("decode1", "gemv"): 24605.8 * 2 * 1024 + 34.0 * 1024,         # q4_lane_kernel<1, 1, ...>
-    ("q5k64", "q5k"): 35955.3 * 2 * 1024 + 5120.0 * 1024,          # mma_kernel<Q5Format<...>, 2, ...>
+    ("verify64", "mlp_in"): 59755.1 * 2 * 1024 + 17558.5 * 1024,   # mma_kernel<Q4Format<2, ...>, 2, ...>
+    ("verify64", "down"): 33366.4 * 2 * 1024 + 5772.5 * 1024,      # mma_kernel<Q4Format<1, ...>, 2, ...>
+    ("decode1", "gemv"): 27279.8 * 2 * 1024 + 34.0 * 1024,         # q4_decode_kernel<1, 1, 32, 2>
+    ("lmhead1", "lm_head"): 388081.4 * 2 * 1024 + 485.0 * 1024,    # q4_decode_kernel<1, 1, 32, 2>
+    ("q5k1", "q5k"): 46418.9 * 2 * 1024 + 20.0 * 1024,             # q5k_decode_kernel<8, 2>
+    ("q5k64", "q5k"): 38540.4 * 2 * 1024 + 5772.5 * 1024,          # mma_kernel<Q5Format<...>, 2, ...>
 }
 
 
