@@ -417,7 +417,7 @@ int splosh_q5k_gemm(const splosh_q5k_weight *w, const uint16_t *a, int64_t lda, 
         case SPLOSH_KERNEL_DEQUANT: {
             if (!mma_ok) return fail(SPLOSH_ERR_UNSUPPORTED, "dequant kernel needs rows <= 64 and aligned operands");
             const splosh::MmaPlan plan =
-                splosh::plan_mma(rows, w->rows, w->inner / 256, false, workspace ? workspace_bytes : 0);
+                splosh::plan_mma(rows, w->rows, w->inner / 256, false, workspace ? workspace_bytes : 0, 256);
             return hip_status(splosh::launch_q5k_mma(plan, *w, a, lda, out, ldc, out_dtype, residual, rows, workspace,
                                                      stream),
                               "q5k dequant launch");

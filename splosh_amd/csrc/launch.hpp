@@ -79,7 +79,9 @@ struct MmaPlan {
     int64_t sk_units;  // (band, unit) pairs of the other bands, split evenly over the grid
 };
 bool mma_fits(int64_t rows, int64_t columns, int64_t inner, int64_t stride_words, int64_t lda);
-MmaPlan plan_mma(int64_t rows, int64_t columns, int64_t groups, bool mlp, size_t workspace_bytes);
+// `unit_elems`: K elements of one unit (64 for q4 groups, 256 for Q5_K blocks).
+MmaPlan plan_mma(int64_t rows, int64_t columns, int64_t groups, bool mlp, size_t workspace_bytes,
+                 int64_t unit_elems = 64);
 size_t mma_workspace_bytes(int64_t rows, int64_t columns, int64_t groups, bool mlp);
 hipError_t launch_q4_mma(const MmaPlan &plan, const splosh_q4_weight &w, const splosh_q4_weight *up,
                          const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype, const void *residual,

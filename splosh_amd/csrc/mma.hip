@@ -751,11 +751,17 @@ static size_t sk_bytes(int grid, int64_t rows, int bands, bool mlp) {
     return sk_partial_bytes(grid, rows, mlp) + (size_t)bands * sizeof(int);
 }
 
-MmaPlan plan_mma(int64_t rows, int64_t columns, int64_t groups, bool mlp, size_t workspace_bytes) {
+MmaPlan plan_mma(int64_t rows, int64_t columns, int64_t groups, bool mlp, size_t workspace_bytes, int64_t unit_elems) {
     MmaPlan p;
     p.fm = rows <= 32 ? 1 : 2;
     p.bands = (int)((columns + kMmaCW * 32 - 1) / (kMmaCW * 32));
     int grid = device_cus();
+    // At least 1280 elements of K (five q4 steps) a workgroup: below that the fixed cost of a job
+    // (pipeline fill, reduction, the shared band's fix-up) outweighs the extra CUs (measured on the
+    // 5120 -> 1024 projection at M=64: 19 us on 256 workgroups, 12.4 us on 64).
+    const int64_t min_units = (1280 + unit_elems - 1) / unit_elems;
+    const int64_t want = ((int64_t)p.bands * groups + min_units - 1) / min_units;
+    if (want < grid) grid = (int)(want > 0 ? want : 1);
     if (const char *env = getenv("SPLOSH_MMA_GRID")) grid = atoi(env) > 0 ? atoi(env) : grid;
     grid = grid < kMmaMaxGrid ? grid : kMmaMaxGrid;  // the fix-up's contributor list
     p.grid = grid;
