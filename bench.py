@@ -6,7 +6,7 @@ projection (two K=5120 -> N=17408 weights sharing one activation read, out = sil
 by the down projection (K=17408 -> N=5120) on that output. One "step" is that pair of launches.
 
     python bench.py [--steps K] [--warmup W]
-                    [--workload verify64|decode1|q5k1|q5k16|q5k64|prefill2048|layerset|lmhead1|lmhead64]
+                    [--workload verify64|decode1|q5k1|q5k16|q5k64|prefill2048|layerset|lmhead1|lmhead64|operand64]
 
 Inputs are synthetic (seeded, on the device): code words uniform random, scale = bf16(|N(0,0.02)|),
 bias = bf16(N(0,0.01)), activations bf16(N(0,1)). Several copies of the weight set are rotated so
@@ -189,6 +189,30 @@ def build_workload(name, rt, torch, gen, kernel):
         cfg = {"workload": "layer set at M=64: attention q/k/v/o, gated-delta in/out, MLP gate+up and down",
                "rows": m, "format": "mlx affine q4 g64, tiled128", "weight_copies": ncopy}
         return launches, sum(kb.values()), sum(kf.values()), kb, cfg, kf
+    if name.startswith("operand"):
+        # The operand producers around the draft-verify MLP at M rows (default 64): the input
+        # operand (fp32 -> bf16 + sums, 5120), the down projection's operand (silu(g) u, 17408) and
+        # the emitted next-norm operand of the hidden state (5120). HBM bound.
+        m = int(name[7:] or 64)
+        h, inter = 5120, 17408
+        x = torch.randn(m, h, device="cuda", generator=gen)
+        g = torch.randn(m, inter, device="cuda", generator=gen)
+        u = torch.randn(m, inter, device="cuda", generator=gen)
+        wn = (1 + 0.1 * torch.randn(h, device="cuda", generator=gen)).to(torch.bfloat16)
+        bx, sx = torch.empty(m, h, dtype=torch.bfloat16, device="cuda"), torch.empty(m, h // 64, device="cuda")
+        bd, sd = torch.empty(m, inter, dtype=torch.bfloat16, device="cuda"), torch.empty(m, inter // 64, device="cuda")
+        be, se, qe = torch.empty_like(bx), torch.empty_like(sx), torch.empty_like(sx)
+
+        def launches(i):
+            return [("prepare", lambda: rt.prepare_operand(x, out=bx, sums=sx)),
+                    ("silu_mul", lambda: rt.silu_mul_operand(g, u, out=bd, sums=sd)),
+                    ("emit", lambda: rt.emit_operand(x, wn, values=be, sums=se, squares=qe))]
+
+        kb = {"prepare": m * h * 6 + m * (h // 64) * 4, "silu_mul": m * inter * 10 + m * (inter // 64) * 4,
+              "emit": m * h * 6 + h * 2 + 2 * m * (h // 64) * 4}
+        cfg = {"workload": f"operand producers at M={m}: prepare (5120), silu*mul (17408), emit (5120)", "rows": m,
+               "format": "fp32 in, bf16 operand + per-64 sums out"}
+        return launches, sum(kb.values()), 0, kb, cfg, {k: 0 for k in kb}
     if name.startswith("lmhead"):
         # Config 4's lm_head, 5120 -> 248320, at M=1 or M=64.
         m, k, n = int(name[6:]), 5120, 248320

@@ -201,6 +201,37 @@ int splosh_q5k_repack(const uint8_t *native, int64_t rows, int64_t inner, uint8_
 int splosh_q5k_unpack(const uint8_t *plane0, const uint8_t *plane1, const uint8_t *meta, int64_t rows,
                       int64_t inner, uint8_t *native, hipStream_t stream);
 
+/* ---- Operand producers: the steps either side of a GEMM -------------------------------------
+ *
+ * Each writes a GEMM operand as bf16 (RNE) [rows][dim] (row stride ld_out) plus, per row and per
+ * 64 columns, the fp32 sum of the rounded values ([rows][dim / 64], dense). dim % 64 == 0; fp32
+ * inputs 16-byte aligned with row strides % 4 == 0; the bf16 output 8-byte aligned with
+ * ld_out % 4 == 0. */
+
+/* sp_na_prepare (Shaders/engine_na.metal:38-56): fp32 activations -> the bf16 operand and its sums. */
+int splosh_prepare_operand(const float *x, int64_t ldx, int64_t rows, int64_t dim, uint16_t *out,
+                           int64_t ld_out, float *sums, hipStream_t stream);
+
+/* sp_silu_mul_na (Shaders/engine.metal:200-218): the down projection's operand
+ * bf16(silu(gate s) * (up s)) and its sums, s = row_inv[row] (the deferred RMSNorm scale of the
+ * norm that fed both projections; NULL: 1). gate and up share the row stride ld. */
+int splosh_silu_mul_operand(const float *gate, const float *up, int64_t ld, const float *row_inv, int64_t rows,
+                            int64_t dim, uint16_t *out, int64_t ld_out, float *sums, hipStream_t stream);
+
+/* The operand a residual projection emits for the next RMSNorm-ed GEMM (SpNaEmit,
+ * Shaders/engine_na.metal:26-36, epilogue :365-411): from the fp32 hidden state h (the projection's
+ * output after its residual add) and the norm's bf16 weight: values = bf16(h * weight[col]), their
+ * sums, and squares = per-64 sums of h * h. The norm's row scale is applied later (a GEMM is linear
+ * in its input), from splosh_row_inv. weight: dim bf16 values, 8-byte aligned. */
+int splosh_emit_operand(const float *hidden, int64_t ld_hidden, const uint16_t *norm_weight, int64_t rows,
+                        int64_t dim, uint16_t *values, int64_t ld_values, float *sums, float *squares,
+                        hipStream_t stream);
+
+/* sp_row_inv (Shaders/engine.metal:222-233): inv[row] = 1 / sqrt(sum(squares[row]) / dim + eps),
+ * squares [rows][groups] dense. */
+int splosh_row_inv(const float *squares, int64_t rows, int64_t groups, int64_t dim, float eps, float *inv,
+                   hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

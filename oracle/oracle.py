@@ -56,6 +56,10 @@ def lib():
         L.or_gguf_slot.argtypes = [ctypes.c_int]
         L.or_q45k_gemm_native.argtypes = [_ptr, _i64, _ptr, ctypes.c_int, _i64, _i64, _i64, _i64,
                                           _i64, _ptr, ctypes.c_int]
+        L.or_prepare_operand.argtypes = [_ptr, _i64, _i64, _ptr, _ptr]
+        L.or_silu_mul_operand.argtypes = [_ptr, _ptr, _ptr, _i64, _i64, _ptr, _ptr]
+        L.or_emit_operand.argtypes = [_ptr, _ptr, _i64, _i64, _ptr, _ptr, _ptr]
+        L.or_row_inv.argtypes = [_ptr, _i64, _i64, _i64, ctypes.c_float, _ptr]
     return _lib
 
 
@@ -155,6 +159,50 @@ def silu_mul(gate, up):
     out = np.empty_like(g)
     lib().or_silu_mul(_p(g), _p(u), g.size, _p(out))
     return out
+
+
+# ---- operand producers (engine_na.metal:38-56, engine.metal:200-233, engine_na.metal:365-411) --
+
+def prepare_operand(x):
+    """sp_na_prepare: (bf16 bits [rows, inner], per-64 sums of the rounded values [rows, inner/64])."""
+    x = _c(x, np.float32)
+    rows, inner = x.shape
+    out = np.empty((rows, inner), np.uint16)
+    sums = np.empty((rows, inner // 64), np.float32)
+    lib().or_prepare_operand(_p(x), rows, inner, _p(out), _p(sums))
+    return out, sums
+
+
+def silu_mul_operand(gate, up, row_inv=None):
+    """sp_silu_mul_na: bf16(silu(g s) (u s)) and its per-64 sums; s = row_inv[row] or 1."""
+    g, u = _c(gate, np.float32), _c(up, np.float32)
+    rows, dim = g.shape
+    inv = None if row_inv is None else _c(row_inv, np.float32)
+    out = np.empty((rows, dim), np.uint16)
+    sums = np.empty((rows, dim // 64), np.float32)
+    lib().or_silu_mul_operand(_p(g), _p(u), None if inv is None else _p(inv), rows, dim, _p(out), _p(sums))
+    return out, sums
+
+
+def emit_operand(hidden, norm_weight_bits):
+    """The next RMSNorm-ed GEMM's operand: (bf16 values, per-64 sums, per-64 sums of squares)."""
+    h = _c(hidden, np.float32)
+    w = _c(norm_weight_bits, np.uint16)
+    rows, dim = h.shape
+    values = np.empty((rows, dim), np.uint16)
+    sums = np.empty((rows, dim // 64), np.float32)
+    squares = np.empty((rows, dim // 64), np.float32)
+    lib().or_emit_operand(_p(h), _p(w), rows, dim, _p(values), _p(sums), _p(squares))
+    return values, sums, squares
+
+
+def row_inv(squares, dim, eps):
+    """sp_row_inv: 1 / sqrt(sum(squares[row]) / dim + eps)."""
+    q = _c(squares, np.float32)
+    rows, groups = q.shape
+    inv = np.empty(rows, np.float32)
+    lib().or_row_inv(_p(q), rows, groups, dim, eps, _p(inv))
+    return inv
 
 
 # ---- GGUF Q4_K / Q5_K -----------------------------------------------------------------------

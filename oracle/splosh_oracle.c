@@ -223,6 +223,74 @@ void or_silu_mul(const float *gate, const float *up, int64_t count, float *out) 
     }
 }
 
+/* ---- operand producers ------------------------------------------------------------------------ */
+
+static float or_silu(float x) {
+    const float e = expf(-x);
+    const float d = 1.0f + e;
+    return x / d;
+}
+
+/* Sums of 64 rounded values in column order. */
+static float or_sum64(const uint16_t *bits) {
+    float s = 0.0f;
+    for (int i = 0; i < 64; ++i) s += or_bf16_to_f32(bits[i]);
+    return s;
+}
+
+void or_prepare_operand(const float *in, int64_t rows, int64_t inner, uint16_t *out, float *sums) {
+    const int64_t groups = inner / 64;
+    for (int64_t r = 0; r < rows; ++r) {
+        for (int64_t k = 0; k < inner; ++k) out[r * inner + k] = or_f32_to_bf16_rne(in[r * inner + k]);
+        for (int64_t g = 0; g < groups; ++g) sums[r * groups + g] = or_sum64(out + r * inner + g * 64);
+    }
+}
+
+void or_silu_mul_operand(const float *gate, const float *up, const float *row_inv, int64_t rows, int64_t dim,
+                         uint16_t *out, float *sums) {
+    const int64_t groups = dim / 64;
+    for (int64_t r = 0; r < rows; ++r) {
+        const float s = row_inv ? row_inv[r] : 1.0f;
+        for (int64_t k = 0; k < dim; ++k) {
+            const float g = gate[r * dim + k] * s, u = up[r * dim + k] * s;
+            const float v = or_silu(g) * u;
+            out[r * dim + k] = or_f32_to_bf16_rne(v);
+        }
+        for (int64_t g = 0; g < groups; ++g) sums[r * groups + g] = or_sum64(out + r * dim + g * 64);
+    }
+}
+
+void or_emit_operand(const float *hidden, const uint16_t *norm_weight, int64_t rows, int64_t dim, uint16_t *values,
+                     float *sums, float *squares) {
+    const int64_t groups = dim / 64;
+    for (int64_t r = 0; r < rows; ++r) {
+        for (int64_t k = 0; k < dim; ++k) {
+            const float h = hidden[r * dim + k];
+            const float v = h * or_bf16_to_f32(norm_weight[k]);
+            values[r * dim + k] = or_f32_to_bf16_rne(v);
+        }
+        for (int64_t g = 0; g < groups; ++g) {
+            sums[r * groups + g] = or_sum64(values + r * dim + g * 64);
+            float q = 0.0f;
+            for (int i = 0; i < 64; ++i) {
+                const float h = hidden[r * dim + g * 64 + i];
+                const float hh = h * h;
+                q += hh;
+            }
+            squares[r * groups + g] = q;
+        }
+    }
+}
+
+void or_row_inv(const float *squares, int64_t rows, int64_t groups, int64_t dim, float eps, float *inv) {
+    for (int64_t r = 0; r < rows; ++r) {
+        float total = 0.0f;
+        for (int64_t g = 0; g < groups; ++g) total += squares[r * groups + g];
+        const float mean = total / (float)dim;
+        inv[r] = 1.0f / sqrtf(mean + eps);
+    }
+}
+
 /* ---- GGUF Q4_K / Q5_K --------------------------------------------------------------------- */
 
 /* The 6-bit scale and minimum of group j (GgufQuant.swift:196-203). */

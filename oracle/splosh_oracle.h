@@ -66,6 +66,22 @@ void or_q4_gemm_rowmajor(const uint16_t *a, int64_t lda, const uint32_t *words, 
 /* silu(g) * u with silu(x) = x / (1 + exp(-x)) in fp32 (engine.metal:24, :2050). */
 void or_silu_mul(const float *gate, const float *up, int64_t count, float *out);
 
+/* Operand producers (the steps either side of a GEMM). Every "sums" output is per row and per 64
+ * consecutive columns, of the values after their bf16 rounding, added in column order.
+ * sp_na_prepare (engine_na.metal:38-56): out = RNE(in), sums of out. */
+void or_prepare_operand(const float *in, int64_t rows, int64_t inner, uint16_t *out, float *sums);
+/* sp_silu_mul_na (engine.metal:200-218): out = RNE(silu(g s) * (u s)) with s = row_inv[row] (1 when
+ * row_inv is NULL), silu(x) = x / (1 + exp(-x)) (engine.metal:25); sums of out. */
+void or_silu_mul_operand(const float *gate, const float *up, const float *row_inv, int64_t rows, int64_t dim,
+                         uint16_t *out, float *sums);
+/* The operand a residual projection emits for the next RMSNorm-ed GEMM (engine_na.metal:26-36,
+ * 365-411): values = RNE(h * bf16(weight[col])), sums of values, squares = per-64 sums of h * h
+ * (h the fp32 hidden state, after the residual add). */
+void or_emit_operand(const float *hidden, const uint16_t *norm_weight, int64_t rows, int64_t dim, uint16_t *values,
+                     float *sums, float *squares);
+/* sp_row_inv (engine.metal:222-233): inv[row] = 1 / sqrt(sum_g squares[row][g] / dim + eps). */
+void or_row_inv(const float *squares, int64_t rows, int64_t groups, int64_t dim, float eps, float *inv);
+
 /* GGUF Q4_K (176-byte Q5_K with fifth_bit) block decode, GgufQuant.swift:191-212.
  * blocks: nblocks * (fifth_bit ? 176 : 144) bytes; out: nblocks * 256 floats. */
 void or_q45k_decode(const uint8_t *blocks, int64_t nblocks, int fifth_bit, float *out);

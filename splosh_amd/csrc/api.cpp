@@ -459,3 +459,63 @@ int splosh_q5k_unpack(const uint8_t *plane0, const uint8_t *plane1, const uint8_
 }
 
 }  // extern "C"
+
+// ---- operand producers ---------------------------------------------------------------------
+
+namespace {
+
+int check_operand_io(const void *in, int64_t ld_in, int64_t rows, int64_t dim, const void *out, int64_t ld_out,
+                     const void *sums) {
+    if (!in || !out || !sums) return fail(SPLOSH_ERR_NULL_POINTER, "null operand pointer");
+    if (rows <= 0 || dim <= 0) return fail(SPLOSH_ERR_INVALID_SHAPE, "rows and dim must be positive");
+    if (dim % 64 != 0) return fail(SPLOSH_ERR_INVALID_GROUP_SIZE, "dim must be a multiple of 64");
+    if (ld_in < dim || ld_out < dim) return fail(SPLOSH_ERR_INVALID_ROW_STRIDE, "row stride shorter than dim");
+    if (ld_in % 4 != 0 || !aligned(in, 16) || ld_out % 4 != 0 || !aligned(out, 8))
+        return fail(SPLOSH_ERR_UNSUPPORTED, "operand kernels need 16-byte fp32 rows and 8-byte bf16 rows");
+    if (mul_overflows(rows, ld_in) || mul_overflows(rows, ld_out) || rows * (dim / 4) >= ((int64_t)1 << 40))
+        return fail(SPLOSH_ERR_ARITHMETIC_OVERFLOW, "size overflows");
+    return SPLOSH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int splosh_prepare_operand(const float *x, int64_t ldx, int64_t rows, int64_t dim, uint16_t *out, int64_t ld_out,
+                           float *sums, hipStream_t stream) {
+    int st = check_operand_io(x, ldx, rows, dim, out, ld_out, sums);
+    if (st) return st;
+    return hip_status(splosh::launch_prepare_operand(x, ldx, rows, dim, out, ld_out, sums, stream), "prepare launch");
+}
+
+int splosh_silu_mul_operand(const float *gate, const float *up, int64_t ld, const float *row_inv, int64_t rows,
+                            int64_t dim, uint16_t *out, int64_t ld_out, float *sums, hipStream_t stream) {
+    int st = check_operand_io(gate, ld, rows, dim, out, ld_out, sums);
+    if (st) return st;
+    if (!up) return fail(SPLOSH_ERR_NULL_POINTER, "null up pointer");
+    if (!aligned(up, 16)) return fail(SPLOSH_ERR_UNSUPPORTED, "up must be 16-byte aligned");
+    return hip_status(splosh::launch_silu_mul_operand(gate, up, ld, row_inv, rows, dim, out, ld_out, sums, stream),
+                      "silu_mul launch");
+}
+
+int splosh_emit_operand(const float *hidden, int64_t ld_hidden, const uint16_t *norm_weight, int64_t rows,
+                        int64_t dim, uint16_t *values, int64_t ld_values, float *sums, float *squares,
+                        hipStream_t stream) {
+    int st = check_operand_io(hidden, ld_hidden, rows, dim, values, ld_values, sums);
+    if (st) return st;
+    if (!norm_weight || !squares) return fail(SPLOSH_ERR_NULL_POINTER, "null norm weight or squares");
+    if (!aligned(norm_weight, 8)) return fail(SPLOSH_ERR_UNSUPPORTED, "norm weight must be 8-byte aligned");
+    return hip_status(splosh::launch_emit_operand(hidden, ld_hidden, norm_weight, rows, dim, values, ld_values, sums,
+                                                  squares, stream),
+                      "emit launch");
+}
+
+int splosh_row_inv(const float *squares, int64_t rows, int64_t groups, int64_t dim, float eps, float *inv,
+                   hipStream_t stream) {
+    if (!squares || !inv) return fail(SPLOSH_ERR_NULL_POINTER, "null squares or inv");
+    if (rows <= 0 || groups <= 0 || dim <= 0) return fail(SPLOSH_ERR_INVALID_SHAPE, "rows, groups and dim must be positive");
+    if (rows > 0x7fffffff) return fail(SPLOSH_ERR_UNSUPPORTED, "too many rows for one launch");
+    return hip_status(splosh::launch_row_inv(squares, rows, groups, dim, eps, inv, stream), "row_inv launch");
+}
+
+}  // extern "C"

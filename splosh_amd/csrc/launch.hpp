@@ -133,6 +133,16 @@ bool q5k_decode_fits(int64_t rows, int64_t columns, int64_t inner);
 hipError_t launch_q5k_decode(const splosh_q5k_weight &w, const uint16_t *a, void *out, int out_dtype,
                              const void *residual, hipStream_t stream);
 
+// Operand producers (operand.hip).
+hipError_t launch_prepare_operand(const float *x, int64_t ldx, int64_t rows, int64_t dim, uint16_t *out, int64_t ldo,
+                                  float *sums, hipStream_t stream);
+hipError_t launch_silu_mul_operand(const float *gate, const float *up, int64_t ld, const float *row_inv, int64_t rows,
+                                   int64_t dim, uint16_t *out, int64_t ldo, float *sums, hipStream_t stream);
+hipError_t launch_emit_operand(const float *hidden, int64_t ldh, const uint16_t *weight, int64_t rows, int64_t dim,
+                               uint16_t *values, int64_t ldv, float *sums, float *squares, hipStream_t stream);
+hipError_t launch_row_inv(const float *squares, int64_t rows, int64_t groups, int64_t dim, float eps, float *inv,
+                          hipStream_t stream);
+
 hipError_t launch_q5k_dequant(const splosh_q5k_weight &w, float *out, hipStream_t stream);
 hipError_t launch_q5k_repack(const uint8_t *native, int64_t rows, int64_t inner, uint8_t *p0,
                              uint8_t *p1, uint8_t *meta, bool inverse, hipStream_t stream);

@@ -282,3 +282,68 @@ class Engine:
 
 def version():
     return _lib.lib().splosh_version().decode()
+
+
+# ---- operand producers (the steps either side of a GEMM) ----------------------------------------
+
+
+def _f32_rows(t, name):
+    if t.dtype != torch.float32 or t.dim() != 2 or t.stride(1) != 1:
+        raise SploshError(13, f"{name} must be fp32 [rows, dim] with contiguous rows")
+    return t
+
+
+def _operand_out(x, out, sums):
+    rows, dim = x.shape
+    if out is None:
+        out = torch.empty((rows, dim), dtype=torch.bfloat16, device=x.device)
+    if sums is None:
+        sums = torch.empty((rows, dim // 64), dtype=torch.float32, device=x.device)
+    return out, sums
+
+
+def prepare_operand(x, out=None, sums=None, stream=None):
+    """sp_na_prepare (engine_na.metal:38-56): fp32 [rows, dim] -> (bf16 operand, per-64 sums)."""
+    x = _f32_rows(x, "x")
+    out, sums = _operand_out(x, out, sums)
+    _lib.check(_lib.lib().splosh_prepare_operand(_ptr(x), x.stride(0), x.shape[0], x.shape[1], _ptr(out),
+                                                 out.stride(0), _ptr(sums), _stream(stream)))
+    return out, sums
+
+
+def silu_mul_operand(gate, up, row_inv=None, out=None, sums=None, stream=None):
+    """sp_silu_mul_na (engine.metal:200-218): bf16(silu(g s) (u s)) and its per-64 sums."""
+    gate, up = _f32_rows(gate, "gate"), _f32_rows(up, "up")
+    if up.shape != gate.shape or up.stride(0) != gate.stride(0):
+        raise SploshError(13, "gate and up must share shape and row stride")
+    out, sums = _operand_out(gate, out, sums)
+    _lib.check(_lib.lib().splosh_silu_mul_operand(_ptr(gate), _ptr(up), gate.stride(0), _ptr(row_inv), gate.shape[0],
+                                                  gate.shape[1], _ptr(out), out.stride(0), _ptr(sums),
+                                                  _stream(stream)))
+    return out, sums
+
+
+def emit_operand(hidden, norm_weight, values=None, sums=None, squares=None, stream=None):
+    """The next RMSNorm-ed GEMM's operand (engine_na.metal:26-36, 365-411): (bf16 hidden * weight,
+    per-64 sums of it, per-64 sums of hidden^2)."""
+    hidden = _f32_rows(hidden, "hidden")
+    if norm_weight.dtype != torch.bfloat16 or norm_weight.numel() < hidden.shape[1]:
+        raise SploshError(13, "norm_weight must be bf16 with dim values")
+    values, sums = _operand_out(hidden, values, sums)
+    if squares is None:
+        squares = torch.empty_like(sums)
+    _lib.check(_lib.lib().splosh_emit_operand(_ptr(hidden), hidden.stride(0), _ptr(norm_weight), hidden.shape[0],
+                                              hidden.shape[1], _ptr(values), values.stride(0), _ptr(sums),
+                                              _ptr(squares), _stream(stream)))
+    return values, sums, squares
+
+
+def row_inv(squares, dim, eps, out=None, stream=None):
+    """sp_row_inv (engine.metal:222-233): 1 / sqrt(sum(squares[row]) / dim + eps)."""
+    if squares.dtype != torch.float32 or not squares.is_contiguous():
+        raise SploshError(13, "squares must be contiguous fp32 [rows, groups]")
+    rows, groups = squares.shape
+    if out is None:
+        out = torch.empty(rows, dtype=torch.float32, device=squares.device)
+    _lib.check(_lib.lib().splosh_row_inv(_ptr(squares), rows, groups, dim, float(eps), _ptr(out), _stream(stream)))
+    return out

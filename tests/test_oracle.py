@@ -261,3 +261,70 @@ def test_q45k_fused_gemm_equals_decode_then_gemm(oracle, fifth):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
     part = oracle.q45k_gemm_native(a, nat, n, k, fifth_bit=fifth, n0=2, n1=5)
     assert np.array_equal(part[:, 2:5], want[:, 2:5]) and np.all(np.isnan(part[:, :2]))
+
+
+# ---- operand producers (engine_na.metal:38-56, engine.metal:200-233, engine_na.metal:365-411) ----
+
+
+def _rne_f64(v):
+    """Round-to-nearest-even to bf16 of float32 values, via float64 bit arithmetic (independent of
+    the oracle's C conversion)."""
+    b = np.asarray(v, np.float32).view(np.uint32).astype(np.uint64)
+    return ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def test_prepare_operand_closed_forms(oracle):
+    # A group of equal values sums to 64 x the value; ties round to even.
+    x = np.full((2, 128), 1.5, np.float32)
+    x[1, :64] = 1.0 + 2.0 ** -8            # tie between 1.0 and 1.0078125: even is 1.0
+    x[1, 64:] = 1.0 + 3 * 2.0 ** -8        # tie between 1.0078125 and 1.015625: even is 1.015625
+    out, sums = oracle.prepare_operand(x)
+    assert np.all(out[0] == 0x3FC0) and np.all(sums[0] == 96.0)
+    assert np.all(out[1, :64] == 0x3F80) and sums[1, 0] == 64.0
+    assert np.all(out[1, 64:] == 0x3F82) and sums[1, 1] == 64 * 1.015625
+
+
+def test_prepare_operand_brute_force(oracle):
+    x = (np.random.default_rng(1).normal(size=(5, 320)) * 3).astype(np.float32)
+    out, sums = oracle.prepare_operand(x)
+    assert np.array_equal(out, _rne_f64(x))
+    vals = (out.astype(np.uint32) << 16).view(np.float32).astype(np.float64).reshape(5, 5, 64)
+    np.testing.assert_allclose(sums, vals.sum(-1), rtol=1e-6, atol=1e-6)
+
+
+def test_silu_mul_operand(oracle):
+    rng = np.random.default_rng(2)
+    g = (rng.normal(size=(3, 192)) * 4).astype(np.float32)
+    u = rng.normal(size=(3, 192)).astype(np.float32)
+    out, sums = oracle.silu_mul_operand(g, u)
+    g64, u64 = g.astype(np.float64), u.astype(np.float64)
+    ref = g64 / (1 + np.exp(-g64)) * u64
+    got = (out.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    # Within one bf16 rounding of the exact product, and equal to its rounding almost everywhere.
+    assert np.all(np.abs(got - ref) <= 2.0 ** -8 * np.abs(ref) + 1e-30)
+    assert np.mean(out == _rne_f64(ref.astype(np.float32))) > 0.99
+    np.testing.assert_allclose(sums, got.reshape(3, 3, 64).sum(-1), rtol=1e-6, atol=1e-6)
+    # silu(0) = 0; a power-of-two row scale equals scaling the inputs (exact in fp32).
+    z, _ = oracle.silu_mul_operand(np.zeros((1, 64), np.float32), np.ones((1, 64), np.float32))
+    assert np.all(z == 0)
+    s = np.array([0.5, 2.0, 4.0], np.float32)
+    a, sa = oracle.silu_mul_operand(g, u, s)
+    b, sb = oracle.silu_mul_operand(g * s[:, None], u * s[:, None])
+    assert np.array_equal(a, b) and np.array_equal(sa, sb)
+
+
+def test_emit_operand_and_row_inv(oracle):
+    rng = np.random.default_rng(3)
+    h = rng.normal(size=(4, 256)).astype(np.float32)
+    w = _rne_f64(rng.normal(1.0, 0.1, size=256).astype(np.float32))
+    values, sums, squares = oracle.emit_operand(h, w)
+    wf = (w.astype(np.uint32) << 16).view(np.float32)
+    assert np.array_equal(values, _rne_f64(h * wf))   # one fp32 product, then RNE
+    got = (values.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    np.testing.assert_allclose(sums, got.reshape(4, 4, 64).sum(-1), rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(squares, (h.astype(np.float64) ** 2).reshape(4, 4, 64).sum(-1), rtol=1e-6)
+    # RMSNorm's row scale: constant mean square c gives 1 / sqrt(c + eps) exactly for c = 4, eps = 0.
+    sq = np.full((2, 8), 64 * 4.0, np.float32)
+    assert np.all(oracle.row_inv(sq, 512, 0.0) == 0.5)
+    inv = oracle.row_inv(squares, 256, 1e-6)
+    np.testing.assert_allclose(inv, 1 / np.sqrt((h.astype(np.float64) ** 2).mean(-1) + 1e-6), rtol=1e-6)
