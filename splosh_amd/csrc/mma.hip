@@ -624,10 +624,35 @@ mma_kernel(MmaArgs args) {
             }
             if (ocol < args.n) store_out(m, v);
         }
-        if (slot < 0) return;
-        // A shared band: the last of its workgroups to arrive sums every partial in workgroup
-        // order (so the result does not depend on who is last), applies the epilogue and returns
-        // the band's counter to zero for the next call.
+        // A shared band's fix-up runs in finish_band(), called by the caller: at once for the last
+        // job of the range, at the end of the range for the first (whose partial then has long
+        // reached memory, so the workgroup does not stall on it between its jobs).
+    };
+
+    // The fix-up of a shared band: the last of its workgroups to arrive sums every partial in
+    // workgroup order (so the result does not depend on who is last), applies the epilogue and
+    // returns the band's counter to zero for the next call.
+    auto finish_band = [&](int band) {
+        constexpr int kRowStep = S::kThreads / S::kBandCols;
+        const int c = tid % S::kBandCols;
+        const int64_t ocol = (int64_t)band * S::kBandCols + c;
+        const int rows = (int)args.rows;
+        const int m_first = __builtin_amdgcn_readfirstlane(tid / S::kBandCols);
+        auto store_out = [&](int m, const float *v) {
+            float value = v[0];
+            if constexpr (NW == 2) value = silu(v[0]) * v[1];
+            const int64_t index = (int64_t)m * args.ldc + ocol;
+            if (args.out_dtype == SPLOSH_F32) {
+                if (args.residual) value += ((const float *)args.residual)[index];
+                ((float *)args.out)[index] = value;
+            } else {
+                if (args.residual) value += bf16_bits_to_f32(((const uint16_t *)args.residual)[index]);
+                ((uint16_t *)args.out)[index] = f32_to_bf16(value);
+            }
+        };
+        auto part_off = [&](int wg, int sl, int w, int m) {
+            return (uint32_t)((((wg * 2 + sl) * NW + w) * rows + m) * S::kBandCols + c) * 4u;
+        };
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this workgroup's partial is in memory
         __syncthreads();
         const int64_t lo = (int64_t)(band - args.dp_bands) * U, hi = lo + U;  // the band's units
@@ -698,16 +723,22 @@ mma_kernel(MmaArgs args) {
     if (args.sk_units > 0) {
         int64_t u = sk_start(blockIdx.x);
         const int64_t u_end = sk_start(blockIdx.x + 1);
-        int slot = 0;
+        int slot = 0, deferred = -1;
         while (u < u_end) {
             const int band = args.dp_bands + (int)(u / U);
             const int ga = (int)(u % U);
             const int gb = (int)((int64_t)ga + (u_end - u) < U ? ga + (u_end - u) : U);
-            run_job(band, ga, gb, (ga == 0 && gb == U) ? -1 : slot);
+            const bool whole = ga == 0 && gb == U;
+            run_job(band, ga, gb, whole ? -1 : slot);
             lds_barrier();
             u += gb - ga;
+            if (!whole) {
+                if (slot == 0 && u < u_end) deferred = band;  // more jobs follow: fix up at the end
+                else finish_band(band);
+            }
             slot = 1;
         }
+        if (deferred >= 0) finish_band(deferred);
     }
 }
 
