@@ -171,6 +171,13 @@ int splosh_q4_mlp_in(const splosh_q4_weight *gate, const splosh_q4_weight *up, c
  * [rows][inner], bit-identical to the CPU reference. */
 int splosh_q4_dequant(const splosh_q4_weight *w, float *out, hipStream_t stream);
 
+/* sp_embed_q4 (Shaders/engine.metal:39-57), the embedding lookup on a q4 table (either order):
+ * out[i][k] = dequant(w)[tokens[i]][k] for i < count, fp32 (bit-identical to DequantOracle) or
+ * bf16 (RNE), row stride ldo. tokens: count uint32 ids on the device; an id >= w->rows gives a
+ * row of zeros. */
+int splosh_q4_embed(const splosh_q4_weight *w, const uint32_t *tokens, int64_t count, void *out, int64_t ldo,
+                    int out_dtype, hipStream_t stream);
+
 /* Converter.tile (Model/Retile.swift:135-153) and its inverse on the device:
  * [row][group][element] <-> [row/128][group][row%128][element]. rows % 128 == 0,
  * element_bytes % 2 == 0. src and dst must not overlap. */

@@ -367,6 +367,19 @@ int splosh_q4_dequant(const splosh_q4_weight *w, float *out, hipStream_t stream)
     return hip_status(splosh::launch_q4_dequant(*w, out, stream), "q4 dequant launch");
 }
 
+int splosh_q4_embed(const splosh_q4_weight *w, const uint32_t *tokens, int64_t count, void *out, int64_t ldo,
+                    int out_dtype, hipStream_t stream) {
+    int st = check_q4_weight(w, "embedding");
+    if (st) return st;
+    if (!tokens || !out) return fail(SPLOSH_ERR_NULL_POINTER, "null tokens or output");
+    if (count <= 0) return fail(SPLOSH_ERR_INVALID_SHAPE, "count must be positive");
+    if (ldo < w->inner) return fail(SPLOSH_ERR_INVALID_ROW_STRIDE, "ldo is shorter than inner");
+    if (out_dtype != SPLOSH_F32 && out_dtype != SPLOSH_BF16) return fail(SPLOSH_ERR_UNSUPPORTED, "unknown out_dtype");
+    if (mul_overflows(count, ldo) || count * ((w->inner + 7) / 8) >= ((int64_t)1 << 40))
+        return fail(SPLOSH_ERR_ARITHMETIC_OVERFLOW, "size overflows");
+    return hip_status(splosh::launch_q4_embed(*w, tokens, count, out, ldo, out_dtype, stream), "q4 embed launch");
+}
+
 static int tile_common(const void *src, void *dst, int64_t rows, int64_t groups, int64_t element_bytes, bool inverse,
                        hipStream_t stream) {
     if (!src || !dst) return fail(SPLOSH_ERR_NULL_POINTER, "null buffer");

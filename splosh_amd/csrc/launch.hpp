@@ -26,6 +26,10 @@ hipError_t launch_gemm_q4_scalar(const uint16_t *a, const uint32_t *packed, cons
 
 hipError_t launch_q4_dequant(const splosh_q4_weight &w, float *out, hipStream_t stream);
 
+// Rows tokens[i] of the dequantized weight (the q4 embedding lookup).
+hipError_t launch_q4_embed(const splosh_q4_weight &w, const uint32_t *tokens, int64_t count, void *out, int64_t ldo,
+                           int out_dtype, hipStream_t stream);
+
 hipError_t launch_tile128(const void *src, void *dst, int64_t rows, int64_t groups,
                           int64_t element_bytes, bool inverse, hipStream_t stream);
 

@@ -78,6 +78,50 @@ hipError_t launch_q4_dequant(const splosh_q4_weight &w, float *out, hipStream_t 
     return hipGetLastError();
 }
 
+// sp_embed_q4 (engine.metal:39-57): out[i] = dequant(w)[tokens[i]] for each token, thread per
+// (token, code word); the same one-rounding s * q + b as the dequant above. A token past the
+// weight's rows gives a row of zeros (nothing is read out of bounds).
+__global__ void __launch_bounds__(256)
+q4_embed_kernel(splosh_q4_weight w, const uint32_t *__restrict__ tokens, int64_t count, void *__restrict__ out,
+                int64_t ldo, int out_dtype) {
+    const int64_t words_per_row = (w.inner + 7) / 8;
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= count * words_per_row) return;
+    const int64_t i = idx / words_per_row, wi = idx % words_per_row;
+    const int64_t token = tokens[i];
+    const bool live = token < w.rows;
+    const int64_t groups = (w.inner + kGroup - 1) / kGroup;
+    float v[8];
+    if (live) {
+        int64_t word_index, sidecar;
+        q4_address(w, token, wi, groups, &word_index, &sidecar);
+        const uint32_t word = w.packed[word_index];
+        const float s = bf16_bits_to_f32(w.scales[sidecar]);
+        const float b = bf16_bits_to_f32(w.biases[sidecar]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = __builtin_fmaf(s, (float)((word >> (4 * e)) & 0xfu), b);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = 0.0f;
+    }
+    const int64_t n = w.inner - wi * 8 < 8 ? w.inner - wi * 8 : 8;
+    if (out_dtype == SPLOSH_F32) {
+        float *dst = (float *)out + i * ldo + wi * 8;
+        for (int e = 0; e < n; ++e) dst[e] = v[e];
+    } else {
+        uint16_t *dst = (uint16_t *)out + i * ldo + wi * 8;
+        for (int e = 0; e < n; ++e) dst[e] = f32_to_bf16(v[e]);
+    }
+}
+
+hipError_t launch_q4_embed(const splosh_q4_weight &w, const uint32_t *tokens, int64_t count, void *out, int64_t ldo,
+                           int out_dtype, hipStream_t stream) {
+    const int64_t total = count * ((w.inner + 7) / 8);
+    hipLaunchKernelGGL(q4_embed_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, w, tokens, count,
+                       out, ldo, out_dtype);
+    return hipGetLastError();
+}
+
 // Converter.tile (Model/Retile.swift:135-153) moving 16-bit units: thread per destination unit.
 __global__ void __launch_bounds__(256)
 tile128_kernel(const uint16_t *__restrict__ src, uint16_t *__restrict__ dst, int64_t rows, int64_t groups,

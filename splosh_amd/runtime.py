@@ -347,3 +347,19 @@ def row_inv(squares, dim, eps, out=None, stream=None):
         out = torch.empty(rows, dtype=torch.float32, device=squares.device)
     _lib.check(_lib.lib().splosh_row_inv(_ptr(squares), rows, groups, dim, float(eps), _ptr(out), _stream(stream)))
     return out
+
+
+def embed(w, tokens, out=None, out_dtype=torch.float32, stream=None):
+    """sp_embed_q4 (engine.metal:39-57): rows tokens[i] of the dequantized q4 table, [count, inner].
+    tokens: uint32 ids on the device (int32 tensors are taken as their bits); an id past the table
+    gives zeros."""
+    if tokens.dtype not in (torch.int32,) or not tokens.is_contiguous():
+        raise SploshError(13, "tokens must be a contiguous int32 tensor of uint32 ids")
+    count = tokens.numel()
+    if out is None:
+        out = torch.empty((count, w.inner), dtype=out_dtype, device=tokens.device)
+    _require(out, ((count - 1) * out.stride(0) + w.inner) * out.element_size(), "output")
+    wc = w.c()
+    _lib.check(_lib.lib().splosh_q4_embed(ctypes.byref(wc), _ptr(tokens), count, _ptr(out), out.stride(0),
+                                          _dtype_code(out.dtype), _stream(stream)))
+    return out
