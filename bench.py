@@ -6,7 +6,7 @@ projection (two K=5120 -> N=17408 weights sharing one activation read, out = sil
 by the down projection (K=17408 -> N=5120) on that output. One "step" is that pair of launches.
 
     python bench.py [--steps K] [--warmup W]
-                    [--workload verify64|decode1|q5k1|q5k16|q5k64|prefill2048|layerset|lmhead1|lmhead64|operand64]
+                    [--workload verify64|decode1|q5k1|q5k16|q5k64|q4k1|q4k64|prefill2048|layerset|lmhead1|lmhead64|operand64]
 
 Inputs are synthetic (seeded, on the device): code words uniform random, scale = bf16(|N(0,0.02)|),
 bias = bf16(N(0,0.01)), activations bf16(N(0,1)). Several copies of the weight set are rotated so
@@ -57,18 +57,19 @@ def make_q4(rt, n, k, gen):
     return rt.Q4Weight(packed, scales, biases, n, k, rt.TILED128)
 
 
-def make_q5k(rt, n, k, gen):
-    """Q5_K planes with every bit random except the fp16 d / dmin fields, drawn like the reference's
-    kernel test (GgufKernelTests.swift:49-82): d ~ 1e-4 (1 +- 0.25), dmin ~ 1.5e-3, 1 in 4 negative."""
+def make_q5k(rt, n, k, gen, fifth=True):
+    """Q5_K (or Q4_K) planes with every bit random except the fp16 d / dmin fields, drawn like the
+    reference's kernel test (GgufKernelTests.swift:49-82): d ~ 1e-4 (2e-4 for Q4_K) (1 +- 0.25),
+    dmin ~ 1.5e-3, 1 in 4 negative."""
     import torch
     blocks = n * (k // 256)
-    native = torch.randint(0, 256, (blocks, 176), dtype=torch.uint8, device="cuda", generator=gen)
-    for field, mag in ((0, 1e-4), (2, 1.5e-3)):
+    native = torch.randint(0, 256, (blocks, 176 if fifth else 144), dtype=torch.uint8, device="cuda", generator=gen)
+    for field, mag in ((0, 1e-4 if fifth else 2e-4), (2, 1.5e-3)):
         v = mag * (1 + 0.25 * (torch.rand(blocks, device="cuda", generator=gen) * 2 - 1))
         neg = torch.randint(0, 4, (blocks,), device="cuda", generator=gen) == 0
         v = torch.where(neg, -v, v).to(torch.float16).view(torch.uint8).view(blocks, 2)
         native[:, field:field + 2] = v
-    w = rt.q5k_repack(native.view(-1), n, k)
+    w = rt.q5k_repack(native.view(-1), n, k) if fifth else rt.q4k_repack(native.view(-1), n, k)
     return w, native
 
 
@@ -230,12 +231,15 @@ def build_workload(name, rt, torch, gen, kernel):
         cfg = {"workload": f"lm_head K5120->N248320 at M={m}", "rows": m, "format": "mlx affine q4 g64, tiled128",
                "weight_copies": ncopy}
         return launches, b, 2 * m * n * k, {"lm_head": b}, cfg, {"lm_head": 2 * m * n * k}
-    if name.startswith("q5k"):
+    if name.startswith("q5k") or name.startswith("q4k"):
+        # Config 3's shape (down projection K=17408 -> N=5120) in GGUF Q5_K, or Q4_K (the same
+        # blocks without fifth bits: 144 bytes).
+        fifth = name.startswith("q5k")
         m = int(name[3:] or 64)
         k, n = 17408, 5120
-        one = n * (k // 256) * 176
+        one = n * (k // 256) * (176 if fifth else 144)
         ncopy = copies_for(one)
-        ws = [make_q5k(rt, n, k, gen)[0] for _ in range(ncopy)]
+        ws = [make_q5k(rt, n, k, gen, fifth)[0] for _ in range(ncopy)]
         x = torch.randn(m, k, device="cuda", generator=gen).to(torch.bfloat16)
         out = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
         b = one + m * k * 2 + m * n * 2
@@ -245,7 +249,8 @@ def build_workload(name, rt, torch, gen, kernel):
             w = ws[i % ncopy]
             return [("q5k", lambda: rt.gemm(w, x, out=out, kernel=kernel, workspace=ws_q5))]
 
-        cfg = {"workload": f"Q5_K down K17408->N5120", "rows": m, "format": "gguf q5_k planes",
+        cfg = {"workload": f"{'Q5_K' if fifth else 'Q4_K'} down K17408->N5120", "rows": m,
+               "format": f"gguf {'q5_k' if fifth else 'q4_k'} planes",
                "weight_copies": ncopy}
         return launches, b, 2 * m * n * k, {"q5k": b}, cfg, {"q5k": 2 * m * n * k}
     raise SystemExit(f"unknown workload {name}")

@@ -208,6 +208,20 @@ int splosh_q5k_repack(const uint8_t *native, int64_t rows, int64_t inner, uint8_
 int splosh_q5k_unpack(const uint8_t *plane0, const uint8_t *plane1, const uint8_t *meta, int64_t rows,
                       int64_t inner, uint8_t *native, hipStream_t stream);
 
+/* ---- GGUF Q4_K -----------------------------------------------------------------------------
+ *
+ * Q4_K (GgufQuant.swift:44,151,191-212: decodeQ45K without fifth bits, 144-byte blocks) in its
+ * GgufPlanes form (GgufPlanes.swift:64: plane0 and meta as for Q5_K, no plane1). The weight is a
+ * splosh_q5k_weight whose plane1 is not read (pass NULL). The same kernels as Q5_K. */
+int splosh_q4k_gemm(const splosh_q5k_weight *w, const uint16_t *a, int64_t lda, void *out, int64_t ldc,
+                    int out_dtype, const void *residual, int64_t rows, int kernel, void *workspace,
+                    size_t workspace_bytes, hipStream_t stream);
+int splosh_q4k_dequant(const splosh_q5k_weight *w, float *out, hipStream_t stream);
+int splosh_q4k_repack(const uint8_t *native, int64_t rows, int64_t inner, uint8_t *plane0, uint8_t *meta,
+                      hipStream_t stream);
+int splosh_q4k_unpack(const uint8_t *plane0, const uint8_t *meta, int64_t rows, int64_t inner, uint8_t *native,
+                      hipStream_t stream);
+
 /* ---- Operand producers: the steps either side of a GEMM -------------------------------------
  *
  * Each writes a GEMM operand as bf16 (RNE) [rows][dim] (row stride ld_out) plus, per row and per

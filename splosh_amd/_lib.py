@@ -89,6 +89,11 @@ SIGNATURES = {
     "splosh_q5k_dequant": (_int, [ctypes.POINTER(Q5KWeight), _vp, _vp]),
     "splosh_q5k_repack": (_int, [_vp, _i64, _i64, _vp, _vp, _vp, _vp]),
     "splosh_q5k_unpack": (_int, [_vp, _vp, _vp, _i64, _i64, _vp, _vp]),
+    "splosh_q4k_gemm": (_int, [ctypes.POINTER(Q5KWeight), _vp, _i64, _vp, _i64, _int, _vp, _i64, _int, _vp, _sz,
+                               _vp]),
+    "splosh_q4k_dequant": (_int, [ctypes.POINTER(Q5KWeight), _vp, _vp]),
+    "splosh_q4k_repack": (_int, [_vp, _i64, _i64, _vp, _vp, _vp]),
+    "splosh_q4k_unpack": (_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
     "splosh_q4_embed": (_int, [ctypes.POINTER(Q4Weight), _vp, _i64, _vp, _i64, _int, _vp]),
     "splosh_prepare_operand": (_int, [_vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp]),
     "splosh_silu_mul_operand": (_int, [_vp, _vp, _i64, _vp, _i64, _i64, _vp, _i64, _vp, _vp]),

@@ -191,8 +191,9 @@ int q4_gemm_impl(const splosh_q4_weight *w, const splosh_q4_weight *up, const ui
     }
 }
 
-int check_q5k_weight(const splosh_q5k_weight *w) {
-    if (!w || !w->plane0 || !w->plane1 || !w->meta) return fail(SPLOSH_ERR_NULL_POINTER, "null Q5_K plane pointer");
+// fifth = false: Q4_K planes (no plane1).
+int check_q5k_weight(const splosh_q5k_weight *w, bool fifth = true) {
+    if (!w || !w->plane0 || (fifth && !w->plane1) || !w->meta) return fail(SPLOSH_ERR_NULL_POINTER, "null GGUF plane pointer");
     if (w->rows <= 0 || w->inner <= 0) return fail(SPLOSH_ERR_INVALID_SHAPE, "rows and inner must be positive");
     // GgufPlanes.sizes: whole tiles of 128 rows, whole 256-element blocks (GgufPlanes.swift:78-86).
     if (w->rows % 128 != 0 || w->inner % 256 != 0)
@@ -399,13 +400,16 @@ int splosh_untile128(const void *src, void *dst, int64_t rows, int64_t groups, i
     return tile_common(src, dst, rows, groups, element_bytes, true, stream);
 }
 
-int splosh_q5k_gemm(const splosh_q5k_weight *w, const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype,
-                    const void *residual, int64_t rows, int kernel, void *workspace, size_t workspace_bytes,
-                    hipStream_t stream) {
-    int st = check_q5k_weight(w);
+static int gguf_gemm(const splosh_q5k_weight *w_in, bool fifth, const uint16_t *a, int64_t lda, void *out, int64_t ldc,
+                     int out_dtype, const void *residual, int64_t rows, int kernel, void *workspace,
+                     size_t workspace_bytes, hipStream_t stream) {
+    int st = check_q5k_weight(w_in, fifth);
     if (st) return st;
+    splosh_q5k_weight wv = *w_in;
+    if (!fifth) wv.plane1 = nullptr;  // the kernels read no fifth bits
+    const splosh_q5k_weight *w = &wv;
     if ((st = check_io(a, lda, out, ldc, out_dtype, rows, w->rows, w->inner))) return st;
-    const bool eligible = lda % 4 == 0 && aligned(a, 8) && aligned(w->plane0, 16) && aligned(w->plane1, 4) &&
+    const bool eligible = lda % 4 == 0 && aligned(a, 8) && aligned(w->plane0, 16) && (!fifth || aligned(w->plane1, 4)) &&
                           aligned(w->meta, 16);
     const bool mma_ok = eligible && lda % 8 == 0 && aligned(a, 16) && splosh::q5k_mma_fits(rows, w->rows, w->inner, lda);
     const char *decode_env = getenv("SPLOSH_DECODE");
@@ -444,11 +448,33 @@ int splosh_q5k_gemm(const splosh_q5k_weight *w, const uint16_t *a, int64_t lda, 
     }
 }
 
-int splosh_q5k_dequant(const splosh_q5k_weight *w, float *out, hipStream_t stream) {
-    int st = check_q5k_weight(w);
+static int gguf_dequant(const splosh_q5k_weight *w, bool fifth, float *out, hipStream_t stream) {
+    int st = check_q5k_weight(w, fifth);
     if (st) return st;
     if (!out) return fail(SPLOSH_ERR_NULL_POINTER, "null output");
-    return hip_status(splosh::launch_q5k_dequant(*w, out, stream), "q5k dequant launch");
+    splosh_q5k_weight wv = *w;
+    if (!fifth) wv.plane1 = nullptr;
+    return hip_status(splosh::launch_q5k_dequant(wv, out, stream), "gguf dequant launch");
+}
+
+int splosh_q5k_gemm(const splosh_q5k_weight *w, const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype,
+                    const void *residual, int64_t rows, int kernel, void *workspace, size_t workspace_bytes,
+                    hipStream_t stream) {
+    return gguf_gemm(w, true, a, lda, out, ldc, out_dtype, residual, rows, kernel, workspace, workspace_bytes, stream);
+}
+
+int splosh_q4k_gemm(const splosh_q5k_weight *w, const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype,
+                    const void *residual, int64_t rows, int kernel, void *workspace, size_t workspace_bytes,
+                    hipStream_t stream) {
+    return gguf_gemm(w, false, a, lda, out, ldc, out_dtype, residual, rows, kernel, workspace, workspace_bytes, stream);
+}
+
+int splosh_q5k_dequant(const splosh_q5k_weight *w, float *out, hipStream_t stream) {
+    return gguf_dequant(w, true, out, stream);
+}
+
+int splosh_q4k_dequant(const splosh_q5k_weight *w, float *out, hipStream_t stream) {
+    return gguf_dequant(w, false, out, stream);
 }
 
 int splosh_q5k_repack(const uint8_t *native, int64_t rows, int64_t inner, uint8_t *plane0, uint8_t *plane1,
@@ -458,6 +484,25 @@ int splosh_q5k_repack(const uint8_t *native, int64_t rows, int64_t inner, uint8_
         return fail(SPLOSH_ERR_LAYOUT_MISMATCH, "Q5_K planes need rows % 128 == 0 and inner % 256 == 0");
     return hip_status(splosh::launch_q5k_repack(native, rows, inner, plane0, plane1, meta, false, stream),
                       "q5k repack launch");
+}
+
+int splosh_q4k_repack(const uint8_t *native, int64_t rows, int64_t inner, uint8_t *plane0, uint8_t *meta,
+                      hipStream_t stream) {
+    if (!native || !plane0 || !meta) return fail(SPLOSH_ERR_NULL_POINTER, "null buffer");
+    if (rows <= 0 || inner <= 0 || rows % 128 != 0 || inner % 256 != 0)
+        return fail(SPLOSH_ERR_LAYOUT_MISMATCH, "Q4_K planes need rows % 128 == 0 and inner % 256 == 0");
+    return hip_status(splosh::launch_q5k_repack(native, rows, inner, plane0, nullptr, meta, false, stream, false),
+                      "q4k repack launch");
+}
+
+int splosh_q4k_unpack(const uint8_t *plane0, const uint8_t *meta, int64_t rows, int64_t inner, uint8_t *native,
+                      hipStream_t stream) {
+    if (!native || !plane0 || !meta) return fail(SPLOSH_ERR_NULL_POINTER, "null buffer");
+    if (rows <= 0 || inner <= 0 || rows % 128 != 0 || inner % 256 != 0)
+        return fail(SPLOSH_ERR_LAYOUT_MISMATCH, "Q4_K planes need rows % 128 == 0 and inner % 256 == 0");
+    return hip_status(splosh::launch_q5k_repack(native, rows, inner, const_cast<uint8_t *>(plane0), nullptr,
+                                                const_cast<uint8_t *>(meta), true, stream, false),
+                      "q4k unpack launch");
 }
 
 int splosh_q5k_unpack(const uint8_t *plane0, const uint8_t *plane1, const uint8_t *meta, int64_t rows, int64_t inner,

@@ -148,8 +148,9 @@ hipError_t launch_row_inv(const float *squares, int64_t rows, int64_t groups, in
                           hipStream_t stream);
 
 hipError_t launch_q5k_dequant(const splosh_q5k_weight &w, float *out, hipStream_t stream);
+// fifth = false: Q4_K (144-byte blocks, no plane1).
 hipError_t launch_q5k_repack(const uint8_t *native, int64_t rows, int64_t inner, uint8_t *p0,
-                             uint8_t *p1, uint8_t *meta, bool inverse, hipStream_t stream);
+                             uint8_t *p1, uint8_t *meta, bool inverse, hipStream_t stream, bool fifth = true);
 hipError_t launch_q5k_stream(const StreamPlan &plan, const splosh_q5k_weight &w, const uint16_t *a,
                              int64_t lda, void *out, int64_t ldc, int out_dtype, const void *residual,
                              int64_t rows, hipStream_t stream);

@@ -219,10 +219,11 @@ struct Q4Format {
 // 16..23 (bytes 1 and 3) of the group, words 2 and 3 elements 8..15 and 24..31: sub-step i takes
 // activation piece ((i & 1) << 1) | (i >> 1). w = code d sc - dmin mn as one fma (d sc, code d sc
 // and dmin mn are exact in fp32), then RNE to bf16.
-template <int CW, int KW, int D>
+// FIFTH = false: Q4_K (no plane1; the codes are the nibbles).
+template <int CW, int KW, int D, bool FIFTH = true>
 struct Q5Format {
     static constexpr int NW = 1;
-    static constexpr int kWLoads = 2;
+    static constexpr int kWLoads = FIFTH ? 2 : 1;  // loads per wave and step: the mid-step wait counts them
     static constexpr int kUnitK = 256;
     static constexpr int kBandCols = CW * 32;
     static constexpr int kSBuf = kBandCols * 16;
@@ -246,7 +247,7 @@ struct Q5Format {
         h = lane >> 5;
         blocks = (uint32_t)args.units;
         p0_rsrc = make_rsrc(args.plane0, args.code_bytes);
-        p1_rsrc = make_rsrc(args.plane1, args.sidecar_bytes);
+        p1_rsrc = make_rsrc(FIFTH ? (const void *)args.plane1 : (const void *)args.plane0, FIFTH ? args.sidecar_bytes : 0u);
         m_rsrc = make_rsrc(args.meta, args.meta_bytes);
         mr = u32x4{0u, 0u, 0u, 0u};
     }
@@ -280,7 +281,8 @@ struct Q5Format {
     __device__ void load_w(int slot, int t) {
         const uint32_t b = block(t);
         wq[slot] = buffer_load16_cp<kStreamCpol>(p0_rsrc, p0_lane, b * (8u * 128u * 16u));
-        wh[slot] = buffer_load_u32(p1_rsrc, p1_lane, b * (8u * 128u * 4u));
+        if constexpr (FIFTH) wh[slot] = buffer_load_u32(p1_rsrc, p1_lane, b * (8u * 128u * 4u));
+        else wh[slot] = 0u;
     }
     // Scale and minimum of group j = 2 kw + h (GgufQuant.swift:196-203): packed byte k is meta byte
     // 4 + k, so for j < 4 (kw < 2, wave-uniform) sc and mn are the low six bits of meta bytes 4 + j
@@ -308,9 +310,13 @@ struct Q5Format {
             for (int e = 0; e < 2; ++e) {
                 const int c = i + e;
                 const uint32_t w = wq[slot][c];
-                const uint32_t x = __builtin_amdgcn_ubfe(wh[slot], 8 * c, 8);
-                lo[e] = (w & 0x0F0F0F0Fu) | (((x & 0x33u) * 0x880110u) & 0x10101010u);
-                hi[e] = ((w >> 4) & 0x0F0F0F0Fu) | ((((x >> 2) & 0x33u) * 0x880110u) & 0x10101010u);
+                lo[e] = w & 0x0F0F0F0Fu;
+                hi[e] = (w >> 4) & 0x0F0F0F0Fu;
+                if constexpr (FIFTH) {
+                    const uint32_t x = __builtin_amdgcn_ubfe(wh[slot], 8 * c, 8);
+                    lo[e] |= ((x & 0x33u) * 0x880110u) & 0x10101010u;
+                    hi[e] |= (((x >> 2) & 0x33u) * 0x880110u) & 0x10101010u;
+                }
             }
         }
         const int b = i & 1;  // byte b and b + 2: the lower (0) or upper (1) four elements of a word
@@ -896,6 +902,7 @@ hipError_t launch_q5k_mma(const MmaPlan &plan, const splosh_q5k_weight &w, const
     args.code_bytes = (uint32_t)(w.rows * blocks * 8 * 16);
     args.sidecar_bytes = (uint32_t)(w.rows * blocks * 8 * 4);
     args.meta_bytes = (uint32_t)(w.rows * blocks * 16);
+    if (!w.plane1) return launch_mma_fm<Q5Format<kMmaCW, kMmaKW, kMmaDepth, false>>(plan, args, stream);  // Q4_K
     return launch_mma_fm<Q5Format<kMmaCW, kMmaKW, kMmaDepth>>(plan, args, stream);
 }
 

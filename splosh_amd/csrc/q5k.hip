@@ -6,7 +6,9 @@
 // nibbles; w = code * (d * sc_j) - dmin * mn_j for element e of group j, code = nibble + 16 * bit.
 // The kernels read the GgufPlanes form (Model/GgufPlanes.swift:8-20): per (row, 32-group) a
 // 16-byte plane0 record of nibbles in chunk order and a 4-byte plane1 record of fifth bits, and per
-// (row, block) the block's first 16 bytes as meta, all tiled by 128 rows.
+// (row, block) the block's first 16 bytes as meta, all tiled by 128 rows. Q4_K (decodeQ45K with
+// fifthBit false, GgufQuant.swift:44,151,191-212: 144-byte blocks without the fifth bits;
+// GgufPlanes.swift:64: no plane1) runs through the same kernels with a null plane1.
 //
 // Chunk order (gguf_formats.h:17-21): word c of a plane0 record holds elements 4c..4c+3 and
 // 16+4c..16+4c+3; pair p of the word (bits 4p and 16 + 4p) is elements e0, e0 + 1 with
@@ -18,6 +20,7 @@
 namespace splosh {
 
 constexpr int kQ5BlockBytes = 176;
+constexpr int kQ4KBlockBytes = 144;  // Q4_K: the same block without the 32 bytes of fifth bits
 
 // GgufPlanes.slot (Model/GgufPlanes.swift:93-95).
 __device__ __forceinline__ int gguf_slot(int e) { return 8 * ((e >> 2) & 3) + 4 * (e >> 4) + (e & 3); }
@@ -41,25 +44,26 @@ __device__ __forceinline__ void q5k_scale_min(const uint8_t *packed, int j, uint
 
 __global__ void __launch_bounds__(256)
 q5k_repack_kernel(const uint8_t *__restrict__ native, int64_t rows, int64_t inner, uint8_t *__restrict__ p0,
-                  uint8_t *__restrict__ p1, uint8_t *__restrict__ meta) {
+                  uint8_t *__restrict__ p1, uint8_t *__restrict__ meta, int fifth) {
     const int64_t blocks = inner / 256, groups = inner / 32;
     const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= rows * blocks) return;
     const int64_t row = idx / blocks, block = idx % blocks;
-    const uint8_t *b = native + (row * blocks + block) * kQ5BlockBytes;
+    const int bytes = fifth ? kQ5BlockBytes : kQ4KBlockBytes, qs = fifth ? 48 : 16;
+    const uint8_t *b = native + (row * blocks + block) * bytes;
     for (int j = 0; j < 8; ++j) {
         uint32_t words[4] = {0u, 0u, 0u, 0u}, bits = 0u;
         for (int e = 0; e < 32; ++e) {
             const int slot = gguf_slot(e);
-            const uint32_t low = (b[48 + 32 * (j / 2) + e] >> (4 * (j % 2))) & 15u;
-            const uint32_t high = (b[16 + e] >> j) & 1u;
+            const uint32_t low = (b[qs + 32 * (j / 2) + e] >> (4 * (j % 2))) & 15u;
+            const uint32_t high = fifth ? (b[16 + e] >> j) & 1u : 0u;
             const int i = slot & 7;
             words[slot >> 3] |= low << ((i & 1) * 16 + 4 * (i >> 1));
             bits |= high << slot;
         }
         const int64_t rec = plane_record(row, block * 8 + j, groups);
         *(u32x4 *)(p0 + rec * 16) = u32x4{words[0], words[1], words[2], words[3]};
-        *(uint32_t *)(p1 + rec * 4) = bits;
+        if (fifth) *(uint32_t *)(p1 + rec * 4) = bits;
     }
     const int64_t mrec = plane_record(row, block, blocks);
     for (int i = 0; i < 16; ++i) meta[mrec * 16 + i] = b[i];
@@ -67,11 +71,12 @@ q5k_repack_kernel(const uint8_t *__restrict__ native, int64_t rows, int64_t inne
 
 __global__ void __launch_bounds__(256)
 q5k_unpack_kernel(const uint8_t *__restrict__ p0, const uint8_t *__restrict__ p1, const uint8_t *__restrict__ meta,
-                  int64_t rows, int64_t inner, uint8_t *__restrict__ native) {
+                  int64_t rows, int64_t inner, uint8_t *__restrict__ native, int fifth) {
     const int64_t blocks = inner / 256, groups = inner / 32;
     const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= rows * blocks) return;
     const int64_t row = idx / blocks, block = idx % blocks;
+    const int bytes = fifth ? kQ5BlockBytes : kQ4KBlockBytes, qs = fifth ? 48 : 16;
     uint8_t b[kQ5BlockBytes];
     for (int i = 0; i < kQ5BlockBytes; ++i) b[i] = 0;
     const int64_t mrec = plane_record(row, block, blocks);
@@ -79,28 +84,29 @@ q5k_unpack_kernel(const uint8_t *__restrict__ p0, const uint8_t *__restrict__ p1
     for (int j = 0; j < 8; ++j) {
         const int64_t rec = plane_record(row, block * 8 + j, groups);
         const u32x4 words = *(const u32x4 *)(p0 + rec * 16);
-        const uint32_t bits = *(const uint32_t *)(p1 + rec * 4);
+        const uint32_t bits = fifth ? *(const uint32_t *)(p1 + rec * 4) : 0u;
         for (int e = 0; e < 32; ++e) {
             const int slot = gguf_slot(e);
             const int i = slot & 7;
             const uint32_t low = (words[slot >> 3] >> ((i & 1) * 16 + 4 * (i >> 1))) & 15u;
-            b[48 + 32 * (j / 2) + e] |= (uint8_t)(low << (4 * (j % 2)));
-            b[16 + e] |= (uint8_t)(((bits >> slot) & 1u) << j);
+            b[qs + 32 * (j / 2) + e] |= (uint8_t)(low << (4 * (j % 2)));
+            if (fifth) b[16 + e] |= (uint8_t)(((bits >> slot) & 1u) << j);
         }
     }
-    uint8_t *dst = native + (row * blocks + block) * kQ5BlockBytes;
-    for (int i = 0; i < kQ5BlockBytes; ++i) dst[i] = b[i];
+    uint8_t *dst = native + (row * blocks + block) * bytes;
+    for (int i = 0; i < bytes; ++i) dst[i] = b[i];
 }
 
 hipError_t launch_q5k_repack(const uint8_t *native, int64_t rows, int64_t inner, uint8_t *p0, uint8_t *p1,
-                             uint8_t *meta, bool inverse, hipStream_t stream) {
+                             uint8_t *meta, bool inverse, hipStream_t stream, bool fifth) {
     const int64_t total = rows * (inner / 256);
     const dim3 grid((unsigned)((total + 255) / 256));
     if (inverse)
         hipLaunchKernelGGL(q5k_unpack_kernel, grid, dim3(256), 0, stream, p0, p1, meta, rows, inner,
-                           const_cast<uint8_t *>(native));
+                           const_cast<uint8_t *>(native), fifth ? 1 : 0);
     else
-        hipLaunchKernelGGL(q5k_repack_kernel, grid, dim3(256), 0, stream, native, rows, inner, p0, p1, meta);
+        hipLaunchKernelGGL(q5k_repack_kernel, grid, dim3(256), 0, stream, native, rows, inner, p0, p1, meta,
+                           fifth ? 1 : 0);
     return hipGetLastError();
 }
 
@@ -126,7 +132,7 @@ q5k_dequant_kernel(splosh_q5k_weight w, float *__restrict__ out) {
     const int64_t row = idx / groups, g = idx % groups;
     const int64_t rec = plane_record(row, g, groups);
     const u32x4 words = *(const u32x4 *)(w.plane0 + rec * 16);
-    const uint32_t bits = *(const uint32_t *)(w.plane1 + rec * 4);
+    const uint32_t bits = w.plane1 ? *(const uint32_t *)(w.plane1 + rec * 4) : 0u;  // null: Q4_K
     uint8_t m[16];
     const int64_t mrec = plane_record(row, g / 8, blocks);
     for (int i = 0; i < 16; ++i) m[i] = w.meta[mrec * 16 + i];
@@ -162,7 +168,7 @@ q5k_gemm_scalar_kernel(splosh_q5k_weight w, const uint16_t *__restrict__ a, int6
     for (int64_t g = 0; g < groups; ++g) {
         const int64_t rec = plane_record(n, g, groups);
         const u32x4 words = *(const u32x4 *)(w.plane0 + rec * 16);
-        const uint32_t bits = *(const uint32_t *)(w.plane1 + rec * 4);
+        const uint32_t bits = w.plane1 ? *(const uint32_t *)(w.plane1 + rec * 4) : 0u;  // null: Q4_K
         uint8_t m[16];
         const int64_t mrec = plane_record(n, g / 8, blocks);
         for (int i = 0; i < 16; ++i) m[i] = w.meta[mrec * 16 + i];
@@ -275,7 +281,7 @@ q5k_stream_kernel(Q5StreamArgs args) {
             for (int jj = 0; jj < 8; ++jj) {
                 const int64_t rec = plane_record(col[j], blk * 8 + jj, groups);
                 st.w[jj][j] = *(const uint32_t *)(args.w.plane0 + rec * 16 + 4 * c);
-                st.h[jj][j] = *(const uint32_t *)(args.w.plane1 + rec * 4);
+                st.h[jj][j] = args.w.plane1 ? *(const uint32_t *)(args.w.plane1 + rec * 4) : 0u;  // null: Q4_K
             }
         }
     };

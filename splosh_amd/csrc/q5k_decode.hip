@@ -1,4 +1,4 @@
-// q5k_decode.hip -- decode GEMV (one activation row) over GGUF Q5_K planes on every CU.
+// q5k_decode.hip -- decode GEMV (one activation row) over GGUF Q5_K (and Q4_K) planes on every CU.
 //
 // The same structure as the q4 decode kernel (decode.hip): a workgroup owns a block of B output
 // rows over the whole of K, stages the activation row in LDS once, and streams the block's records
@@ -49,7 +49,8 @@ __device__ __forceinline__ uint32_t qand_or(uint32_t a, uint32_t mask, uint32_t 
     return d;
 }
 
-template <int B, int D>
+// FIFTH = false: Q4_K (no plane1; the codes are the nibbles).
+template <int B, int D, bool FIFTH>
 __global__ void __launch_bounds__(kQ5DecodeWg)
 q5k_decode_kernel(Q5DecodeArgs args) {
     extern __shared__ __align__(16) unsigned char lds[];
@@ -93,13 +94,13 @@ q5k_decode_kernel(Q5DecodeArgs args) {
     // 2. The first D steps' loads. Every load is unconditional (groups past K read an out-of-range
     // offset: zeros, no memory traffic), so the compiler's wait counts keep the ring in flight.
     const rsrc_t p0_rsrc = make_rsrc(args.plane0, args.p0_bytes);
-    const rsrc_t p1_rsrc = make_rsrc(args.plane1, args.p1_bytes);
+    const rsrc_t p1_rsrc = make_rsrc(FIFTH ? args.plane1 : args.plane0, FIFTH ? args.p1_bytes : 0u);
     const rsrc_t m_rsrc = make_rsrc(args.meta, args.meta_bytes);
     const int64_t r0 = (int64_t)blockIdx.x * B;
     const uint32_t rr = (uint32_t)(r0 & 127) + (uint32_t)row;
     const uint32_t tile = (uint32_t)(r0 >> 7);
     u32x4 c0[D], cm[D];
-    uint32_t c1[D];
+    uint32_t c1[D] = {};
     auto issue = [&](int slot, int t) {
         const int g = (wave + kQ5DecodeWaves * t) * GPS + gsub;
         const bool live = g < G;
@@ -107,7 +108,7 @@ q5k_decode_kernel(Q5DecodeArgs args) {
         const uint32_t rec = (tile * (uint32_t)G + gg) * 128u + rr;
         const uint32_t mrec = (tile * blocks + gg / 8u) * 128u + rr;
         c0[slot] = buffer_load16_cp<2>(p0_rsrc, live ? rec * 16u : 0xFFFFFFF0u, 0);
-        c1[slot] = buffer_load_u32(p1_rsrc, live ? rec * 4u : 0xFFFFFFF0u, 0);
+        if constexpr (FIFTH) c1[slot] = buffer_load_u32(p1_rsrc, live ? rec * 4u : 0xFFFFFFF0u, 0);
         cm[slot] = buffer_load16(m_rsrc, live ? mrec * 16u : 0xFFFFFFF0u, 0);
     };
     const int my_steps = (steps + kQ5DecodeWaves - 1) / kQ5DecodeWaves;
@@ -163,9 +164,12 @@ q5k_decode_kernel(Q5DecodeArgs args) {
 #pragma unroll
                 for (int p = 0; p < 4; ++p) {
                     const uint32_t nib = qand_or(p ? w >> (4 * p) : w, kMask, magic);
-                    // Exactly the two fifth bits (wider input would carry into bit 20).
-                    const uint32_t fb = __builtin_amdgcn_ubfe(c1[k], 8 * c + 2 * p, 2);
-                    const uint32_t pair = qand_or(fb * 0x80010u, kFifth, nib);
+                    uint32_t pair = nib;
+                    if constexpr (FIFTH) {
+                        // Exactly the two fifth bits (wider input would carry into bit 20).
+                        const uint32_t fb = __builtin_amdgcn_ubfe(c1[k], 8 * c + 2 * p, 2);
+                        pair = qand_or(fb * 0x80010u, kFifth, nib);
+                    }
                     const uint32_t xw = xq[(p >> 1) * 2 + (c >> 1)][(c & 1) * 2 + (p & 1)];  // x u32 8(p>>1) + 2c + (p&1)
                     if (p & 1) pb = qdot2(pair, xw, pb);
                     else pa = qdot2(pair, xw, pa);
@@ -217,9 +221,9 @@ static int q5k_decode_cus() {
     return cus;
 }
 
-template <int B>
+template <int B, bool FIFTH>
 static hipError_t launch_q5k_decode_b(const Q5DecodeArgs &args, hipStream_t stream) {
-    hipLaunchKernelGGL((q5k_decode_kernel<B, kQ5DecodeDepth>), dim3((unsigned)(args.n / B)), dim3(kQ5DecodeWg),
+    hipLaunchKernelGGL((q5k_decode_kernel<B, kQ5DecodeDepth, FIFTH>), dim3((unsigned)(args.n / B)), dim3(kQ5DecodeWg),
                        q5k_decode_lds((int64_t)args.groups * 32, B), stream, args);
     return hipGetLastError();
 }
@@ -237,13 +241,16 @@ hipError_t launch_q5k_decode(const splosh_q5k_weight &w, const uint16_t *a, void
     args.residual = residual;
     args.out_dtype = out_dtype;
     args.p0_bytes = (uint32_t)(w.rows * args.groups * 16);
-    args.p1_bytes = (uint32_t)(w.rows * args.groups * 4);
+    args.p1_bytes = w.plane1 ? (uint32_t)(w.rows * args.groups * 4) : 0u;
     args.meta_bytes = (uint32_t)(w.rows * (args.groups / 8) * 16);
     // Row block: the largest of 32, 16 and 8 that gives at least two workgroups a CU.
     const int64_t cus = q5k_decode_cus();
-    if (w.rows / 32 >= 2 * cus) return launch_q5k_decode_b<32>(args, stream);
-    if (w.rows / 16 >= 2 * cus) return launch_q5k_decode_b<16>(args, stream);
-    return launch_q5k_decode_b<8>(args, stream);
+    const bool fifth = w.plane1 != nullptr;  // null: Q4_K
+    if (w.rows / 32 >= 2 * cus)
+        return fifth ? launch_q5k_decode_b<32, true>(args, stream) : launch_q5k_decode_b<32, false>(args, stream);
+    if (w.rows / 16 >= 2 * cus)
+        return fifth ? launch_q5k_decode_b<16, true>(args, stream) : launch_q5k_decode_b<16, false>(args, stream);
+    return fifth ? launch_q5k_decode_b<8, true>(args, stream) : launch_q5k_decode_b<8, false>(args, stream);
 }
 
 }  // namespace splosh

@@ -114,6 +114,27 @@ class Q5KWeight:
         return self.rows * (self.inner // 256) * 176
 
 
+@dataclass
+class Q4KWeight:
+    """A GGUF Q4_K weight in plane form (GgufPlanes.swift:64: plane0 and meta, no plane1)."""
+
+    plane0: torch.Tensor
+    meta: torch.Tensor
+    rows: int
+    inner: int
+
+    def __post_init__(self):
+        _require(self.plane0, self.rows * (self.inner // 32) * 16, "plane0")
+        _require(self.meta, self.rows * (self.inner // 256) * 16, "meta")
+
+    def c(self):
+        return _lib.Q5KWeight(self.plane0.data_ptr(), None, self.meta.data_ptr(), self.rows, self.inner)
+
+    @property
+    def nbytes(self):
+        return self.rows * (self.inner // 256) * 144
+
+
 def _out(a, rows, n, out, out_dtype):
     if out is None:
         out = torch.empty((rows, n), dtype=out_dtype, device=a.device)
@@ -163,9 +184,9 @@ def gemm(w, a, out=None, residual=None, out_dtype=torch.bfloat16, kernel=AUTO, r
                                        _dtype_code(out.dtype), _ptr(residual), rows, kernel, ws, ws_bytes,
                                        _stream(stream))
     else:
-        st = _lib.lib().splosh_q5k_gemm(ctypes.byref(wc), _ptr(a), a.stride(0), _ptr(out), out.stride(0),
-                                        _dtype_code(out.dtype), _ptr(residual), rows, kernel, ws, ws_bytes,
-                                        _stream(stream))
+        fn = _lib.lib().splosh_q4k_gemm if isinstance(w, Q4KWeight) else _lib.lib().splosh_q5k_gemm
+        st = fn(ctypes.byref(wc), _ptr(a), a.stride(0), _ptr(out), out.stride(0), _dtype_code(out.dtype),
+                _ptr(residual), rows, kernel, ws, ws_bytes, _stream(stream))
     _lib.check(st)
     return out
 
@@ -195,7 +216,8 @@ def dequant(w, out=None, stream=None):
         out = torch.empty((w.rows, w.inner), dtype=torch.float32, device=dev)
     _require(out, w.rows * w.inner * 4, "output")
     wc = w.c()
-    fn = _lib.lib().splosh_q4_dequant if isinstance(w, Q4Weight) else _lib.lib().splosh_q5k_dequant
+    fn = (_lib.lib().splosh_q4_dequant if isinstance(w, Q4Weight) else
+          _lib.lib().splosh_q4k_dequant if isinstance(w, Q4KWeight) else _lib.lib().splosh_q5k_dequant)
     _lib.check(fn(ctypes.byref(wc), _ptr(out), _stream(stream)))
     return out
 
@@ -244,6 +266,23 @@ def q5k_unpack(w, stream=None):
     native = torch.empty(w.rows * (w.inner // 256) * 176, dtype=torch.uint8, device=w.plane0.device)
     _lib.check(_lib.lib().splosh_q5k_unpack(_ptr(w.plane0), _ptr(w.plane1), _ptr(w.meta), w.rows, w.inner,
                                             _ptr(native), _stream(stream)))
+    return native
+
+
+def q4k_repack(native, rows, inner, stream=None):
+    """GgufPlanes.repack for Q4_K on the device: native 144-byte blocks -> Q4KWeight."""
+    dev = native.device
+    p0 = torch.empty(rows * (inner // 32) * 16, dtype=torch.uint8, device=dev)
+    meta = torch.empty(rows * (inner // 256) * 16, dtype=torch.uint8, device=dev)
+    _require(native, rows * (inner // 256) * 144, "native")
+    _lib.check(_lib.lib().splosh_q4k_repack(_ptr(native), rows, inner, _ptr(p0), _ptr(meta), _stream(stream)))
+    return Q4KWeight(p0, meta, rows, inner)
+
+
+def q4k_unpack(w, stream=None):
+    native = torch.empty(w.rows * (w.inner // 256) * 144, dtype=torch.uint8, device=w.plane0.device)
+    _lib.check(_lib.lib().splosh_q4k_unpack(_ptr(w.plane0), _ptr(w.meta), w.rows, w.inner, _ptr(native),
+                                            _stream(stream)))
     return native
 
 
