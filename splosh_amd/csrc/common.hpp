@@ -86,6 +86,12 @@ __device__ __forceinline__ void buffer_load_lds16(rsrc_t r, void *lds_dst, uint3
 #endif
 }
 
+// s_waitcnt with only vmcnt bounded (expcnt and lgkmcnt left at their maxima), gfx9 encoding.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 // Workgroup barrier for LDS hand-offs only: waits for this wave's LDS operations, not for its
 // outstanding global loads (which __syncthreads' fence would drain), so prefetches stay in flight.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }

@@ -91,6 +91,22 @@ hipError_t launch_q4_mma(const MmaPlan &plan, const splosh_q4_weight &w, const s
                          const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype, const void *residual,
                          int64_t rows, void *workspace, hipStream_t stream);
 
+// The M <= 64 verify kernel for tiled q4 weights (verify.hip): groups of 16-column tiles over
+// K, eight waves splitting K; tiles past a whole number of groups a workgroup are split along K
+// and need verify_workspace_bytes() of workspace.
+struct VerifyPlan {
+    int n1, s1;        // phase 1: groups of T tiles, pieces of K each
+    int n2, s2;        // phase 2: single tiles, pieces of K each
+    int units, grid;
+    size_t partial_floats1, partial_floats2;
+};
+bool verify_fits(int64_t rows, int64_t columns, int64_t inner, int order, int64_t lda);
+VerifyPlan plan_verify(int64_t rows, int64_t columns, int64_t groups, bool mlp);
+size_t verify_workspace_bytes(const VerifyPlan &plan);
+hipError_t launch_q4_verify(const VerifyPlan &plan, const splosh_q4_weight &w, const splosh_q4_weight *up,
+                            const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype,
+                            const void *residual, int64_t rows, void *workspace, hipStream_t stream);
+
 // The same kernel over Q5_K planes; the plan's units are 256-element blocks.
 bool q5k_mma_fits(int64_t rows, int64_t columns, int64_t inner, int64_t lda);
 hipError_t launch_q5k_mma(const MmaPlan &plan, const splosh_q5k_weight &w, const uint16_t *a, int64_t lda, void *out,

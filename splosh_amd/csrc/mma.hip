@@ -349,12 +349,6 @@ struct MmaShape {
     static_assert(D == 3, "the pipeline below is written for weights three steps ahead");
 };
 
-// s_waitcnt with only vmcnt bounded (expcnt and lgkmcnt left at their maxima), gfx9 encoding.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
 // Work split. The N columns form `bands` bands of CW * 32. Bands [0, dp_bands) are computed whole
 // by workgroup (band mod gridDim.x), written straight to the output. The (band, unit) pairs of the
 // other bands, sk_units of them, are cut into gridDim.x equal contiguous ranges (stream-K), one a
