@@ -41,6 +41,10 @@ def lib():
         L.or_q4_dequant_rowmajor.argtypes = [_ptr, _i64, _ptr, _ptr, _i64, _i64, _ptr]
         L.or_q4_dequant_tiled.argtypes = [_ptr, _ptr, _ptr, _i64, _i64, _ptr]
         L.or_tile128.argtypes = [_ptr, _ptr, _i64, _i64, _i64]
+        L.or_gguf_decode.restype = ctypes.c_int
+        L.or_gguf_decode.argtypes = [ctypes.c_int, _ptr, _i64, _ptr]
+        L.or_gguf_block_bytes.restype = ctypes.c_int
+        L.or_gguf_block_bytes.argtypes = [ctypes.c_int]
         L.or_untile128.argtypes = [_ptr, _ptr, _i64, _i64, _i64]
         L.or_gemm_a_bf16_w_f32.argtypes = [_ptr, _i64, _ptr, _i64, _i64, _i64, _ptr]
         L.or_gemm_bf16.argtypes = [_ptr, _ptr, _i64, _i64, _i64, _ptr]
@@ -214,6 +218,35 @@ def q45k_decode(blocks, fifth_bit=True):
     out = np.empty(n * 256, dtype=np.float32)
     lib().or_q45k_decode(_p(blocks), n, int(fifth_bit), _p(out))
     return out
+
+
+GGUF_BLOCK = {8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210), 20: (32, 18), 23: (256, 136)}
+
+
+def gguf_decode(gguf_type, blocks):
+    """Native GGUF blocks to float32 (or_gguf_decode: the reference decoder's op order)."""
+    blocks = _c(blocks, np.uint8)
+    elems, size = GGUF_BLOCK[gguf_type]
+    n = blocks.size // size
+    out = np.empty(n * elems, dtype=np.float32)
+    if lib().or_gguf_decode(int(gguf_type), _p(blocks), n, _p(out)) != 0:
+        raise ValueError(f"ggml type {gguf_type} is not decoded by the oracle")
+    return out
+
+
+def gguf_random_native(gguf_type, n, k, seed):
+    """Rows of random native blocks with sane fp16 scales: every byte random, then each fp16
+    field (Q8_0 / IQ4_NL / IQ4_XS: d at 0; Q6_K: d at 208) set to about 1e-3 (sign random in one
+    block of four)."""
+    elems, size = GGUF_BLOCK[gguf_type]
+    blocks = n * k // elems
+    rng = np.random.default_rng(seed)
+    raw = rng.integers(0, 256, size=(blocks, size), dtype=np.uint8)
+    at = 208 if gguf_type == 14 else 0
+    v = 1e-3 * (1 + 0.25 * rng.uniform(-1, 1, size=blocks))
+    v = np.where(rng.integers(0, 4, size=blocks) == 0, -v, v).astype(np.float16)
+    raw[:, at:at + 2] = v.view(np.uint8).reshape(blocks, 2)
+    return raw.reshape(-1)
 
 
 def gguf_slot(e):

@@ -330,6 +330,89 @@ void or_q45k_decode(const uint8_t *blocks, int64_t nblocks, int fifth_bit, float
     }
 }
 
+/* The sixteen IQ4_NL / IQ4_XS code values, llama.cpp's kvalues_iq4nl (the format's table, as the
+ * reference keeps it at GgufQuant.swift:56). */
+static const int8_t kIq4Values[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+/* One native block of a 32- or 256-element GGUF format to fp32, with the reference decoder's fp32
+ * operation order (GgufQuant.swift): Q8_0 :172-175 (d * int8), IQ4_NL :179-185 (d * table, low
+ * nibbles first), Q6_K :218-230 ((d * scale) * (code - 32) with the 4 low bits from ql and 2 high
+ * from qh), IQ4_XS :261-275 ((d * (scale - 32)) * table). Returns the elements decoded (0 for a
+ * type not handled here). */
+static int gguf_decode_block(int type, const uint8_t *b, float *out) {
+    switch (type) {
+        case 8: { /* Q8_0 */
+            const float d = half_to_f32((uint16_t)(b[0] | (b[1] << 8)));
+            for (int e = 0; e < 32; ++e) out[e] = d * (float)(int8_t)b[2 + e];
+            return 32;
+        }
+        case 20: { /* IQ4_NL */
+            const float d = half_to_f32((uint16_t)(b[0] | (b[1] << 8)));
+            for (int e = 0; e < 16; ++e) {
+                out[e] = d * (float)kIq4Values[b[2 + e] & 15];
+                out[16 + e] = d * (float)kIq4Values[b[2 + e] >> 4];
+            }
+            return 32;
+        }
+        case 14: { /* Q6_K: ql[128], qh[64], scales[16] (int8), d (fp16) at 208 */
+            const float d = half_to_f32((uint16_t)(b[208] | (b[209] << 8)));
+            for (int j = 0; j < 8; ++j) {
+                const int half = j / 4, quarter = j % 4;
+                for (int e = 0; e < 32; ++e) {
+                    const int low = (b[64 * half + 32 * (quarter & 1) + e] >> (4 * (quarter >> 1))) & 15;
+                    const int high = (b[128 + 32 * half + e] >> (2 * quarter)) & 3;
+                    const float code = (float)(low | (high << 4)) - 32.0f;
+                    const float scale = (float)(int8_t)b[192 + 2 * j + e / 16];
+                    const float ds = d * scale;
+                    out[32 * j + e] = ds * code;
+                }
+            }
+            return 256;
+        }
+        case 23: { /* IQ4_XS: d, scales_h (u16), scales_l[4], qs[128] */
+            const float d = half_to_f32((uint16_t)(b[0] | (b[1] << 8)));
+            const uint32_t high = (uint32_t)(b[2] | (b[3] << 8));
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t low = ((uint32_t)b[4 + j / 2] >> (4 * (j % 2))) & 15u;
+                const uint32_t scale = low | (((high >> (2 * j)) & 3u) << 4);
+                const float scaled = d * ((float)scale - 32.0f);
+                for (int e = 0; e < 16; ++e) {
+                    const uint8_t byte = b[8 + 16 * j + e];
+                    out[32 * j + e] = scaled * (float)kIq4Values[byte & 15];
+                    out[32 * j + 16 + e] = scaled * (float)kIq4Values[byte >> 4];
+                }
+            }
+            return 256;
+        }
+        default:
+            return 0;
+    }
+}
+
+int or_gguf_block_bytes(int type) {
+    switch (type) {
+        case 8: return 34;
+        case 20: return 18;
+        case 14: return 210;
+        case 23: return 136;
+        case 12: return 144;
+        case 13: return 176;
+        default: return 0;
+    }
+}
+
+int or_gguf_decode(int type, const uint8_t *blocks, int64_t nblocks, float *out) {
+    if (type == 12 || type == 13) {
+        or_q45k_decode(blocks, nblocks, type == 13, out);
+        return 0;
+    }
+    const int size = or_gguf_block_bytes(type);
+    if (size == 0) return -1;
+    int64_t at = 0;
+    for (int64_t i = 0; i < nblocks; ++i) at += gguf_decode_block(type, blocks + i * size, out + at);
+    return 0;
+}
+
 /* GgufPlanes.slot (GgufPlanes.swift:93-95). */
 int or_gguf_slot(int element) { return 8 * ((element >> 2) & 3) + 4 * (element >> 4) + (element & 3); }
 

@@ -85,6 +85,11 @@ void or_row_inv(const float *squares, int64_t rows, int64_t groups, int64_t dim,
 /* GGUF Q4_K (176-byte Q5_K with fifth_bit) block decode, GgufQuant.swift:191-212.
  * blocks: nblocks * (fifth_bit ? 176 : 144) bytes; out: nblocks * 256 floats. */
 void or_q45k_decode(const uint8_t *blocks, int64_t nblocks, int fifth_bit, float *out);
+/* Native blocks of GGUF type `type` (ggml id: 8 Q8_0, 12 Q4_K, 13 Q5_K, 14 Q6_K, 20 IQ4_NL,
+ * 23 IQ4_XS) to fp32 with the reference decoder's op order (GgufQuant.swift:136-275). Returns -1
+ * for another type. or_gguf_block_bytes: the native block size (0: not handled). */
+int or_gguf_decode(int type, const uint8_t *blocks, int64_t nblocks, float *out);
+int or_gguf_block_bytes(int type);
 
 /* GgufPlanes for Q4_K / Q5_K (GgufPlanes.swift:62-136, 161-194, 221-229, 288-305).
  * plane0 [N/128][K/32][128][16 B], plane1 [N/128][K/32][128][4 B] (Q5_K only),

@@ -1,8 +1,8 @@
 """Write the GGUF golden-block fixtures (tests/golden/gguf_golden_blocks.json).
 
 The reference's test suite holds one real block of each quantised GGUF format together with the
-float32 values its decoder produces for it (Tests/SploshOracleTests/GgufGoldenBlocks.swift:22-330,
-Q4_K at :24-71 and Q5_K at :73-122). This script reads that file as text and copies the bytes and
+float32 values its decoder produces for it (Tests/SploshOracleTests/GgufGoldenBlocks.swift:22-330, one block of each of
+the eight formats). This script reads that file as text and copies the bytes and
 values into a JSON fixture; it imports and runs nothing from the reference. It is run once, in a
 container where the reference tree is mounted, and its output is committed:
 
@@ -32,14 +32,14 @@ def parse(text):
 def main():
     root = Path(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")
     blocks = parse((root / SOURCE).read_text())
-    expected = {"q4K": 144, "q5K": 176}
+    expected = {"q4K": 144, "q5K": 176, "q6K": 210, "q3K": 110, "q8_0": 34, "iq4NL": 18, "iq4XS": 136, "iq3S": 110}
     out = {}
     for name, size in expected.items():
         block = blocks[name]
         assert len(block["bytes"]) == size, (name, len(block["bytes"]))
-        assert len(block["values"]) == 256, (name, len(block["values"]))
+        assert len(block["values"]) == (32 if size in (34, 18) else 256), (name, len(block["values"]))
         out[name] = block
-    out["_source"] = f"{SOURCE} (Q4_K :24-71, Q5_K :73-122); values are float32 printed with 9 digits"
+    out["_source"] = f"{SOURCE} (one block of each of the eight formats); values are float32 printed with 9 digits"
     dest = Path(__file__).with_name("gguf_golden_blocks.json")
     dest.write_text(json.dumps(out) + "\n")
     print(f"wrote {dest}")

@@ -175,6 +175,52 @@ def test_gguf_golden_blocks(oracle, name, fifth):
     assert np.array_equal(got.view(np.uint32), expected.view(np.uint32))
 
 
+@pytest.mark.parametrize("name,gguf_type", [("q6K", 14), ("q8_0", 8), ("iq4NL", 20), ("iq4XS", 23)])
+def test_gguf_golden_blocks_other_formats(oracle, name, gguf_type):
+    """The other formats' golden blocks (GgufGoldenBlocks.swift, GgufTests.swift:237-247): the
+    oracle's decode is bit-exact against the values the reference holds for each real block."""
+    block = json.loads(GOLDEN.read_text())[name]
+    expected = np.array([np.float32(v) for v in block["values"]], np.float32)
+    got = oracle.gguf_decode(gguf_type, np.array(block["bytes"], np.uint8))
+    assert np.array_equal(got.view(np.uint32), expected.view(np.uint32))
+
+
+def _f16(x):
+    return list(np.array([x], np.float16).view(np.uint8))
+
+
+def test_gguf_closed_forms(oracle):
+    """Blocks whose values follow from the format alone: a dropped sign, a swapped nibble order or a
+    wrong bit position each changes one of them."""
+    # Q8_0: d = 0.5, codes -128..127 (bytes 0x80.. wrap): value = code / 2.
+    codes = np.arange(-16, 16, dtype=np.int8)
+    v = oracle.gguf_decode(8, np.array(_f16(0.5) + list(codes.view(np.uint8)), np.uint8))
+    assert np.array_equal(v, codes.astype(np.float32) * 0.5)
+    # IQ4_NL: d = 1, byte e = (15 - e) << 4 | e: element e is table[e], element 16 + e table[15 - e].
+    table = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113], np.float32)
+    qs = [((15 - e) << 4) | e for e in range(16)]
+    v = oracle.gguf_decode(20, np.array(_f16(1.0) + qs, np.uint8))
+    assert np.array_equal(v[:16], table) and np.array_equal(v[16:], table[::-1])
+    # Q6_K: d = 1, scales 1, ql = 0x21 (low codes 1 / 2), qh = 0b11100100 (high bits 0, 1, 2, 3 for
+    # quarters 0..3): group j has code (low | high << 4) - 32 with low = 1 for quarters 0, 1 and 2 for
+    # quarters 2, 3, i.e. -31, -15, 2, 18 in both halves.
+    block = [0x21] * 128 + [0b11100100] * 64 + [1] * 16 + _f16(1.0)
+    v = oracle.gguf_decode(14, np.array(block, np.uint8)).reshape(8, 32)
+    assert np.array_equal(v[:, 0], np.array([-31, -15, 2, 18] * 2, np.float32))
+    assert np.all(v == v[:, :1])
+    # Q6_K scale sign and per-16 split: scale bytes 2j = -1, 2j + 1 = 3.
+    block = [0x21] * 128 + [0] * 64 + [0xFF, 3] * 8 + _f16(1.0)
+    v = oracle.gguf_decode(14, np.array(block, np.uint8)).reshape(8, 32)
+    assert np.all(v[0, :16] == 31) and np.all(v[0, 16:] == -93)
+    # IQ4_XS: d = 2, group j's scale 32 + j (low nibbles j, high bits 2 = 0b10 << 2j), codes 8
+    # (table value 1): group j is 2 j everywhere.
+    high = sum(2 << (2 * j) for j in range(8))
+    low = [(j | ((j + 1) << 4)) for j in range(0, 8, 2)]
+    block = _f16(2.0) + [high & 0xFF, high >> 8] + low + [0x88] * 128
+    v = oracle.gguf_decode(23, np.array(block, np.uint8)).reshape(8, 32)
+    assert np.array_equal(v[:, 0], 2.0 * np.arange(8, dtype=np.float32)) and np.all(v == v[:, :1])
+
+
 def test_q4k_group_layout_contract(oracle):
     """The inputs of QuantDequantOracleTests.swift:17-29 (d = 1, dmin = 0, 6-bit scales 1 for
     groups 0..3, code bytes 0x10) decoded with GgufQuant's layout (group 2h = low nibbles of run h,
