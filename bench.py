@@ -6,7 +6,7 @@ projection (two K=5120 -> N=17408 weights sharing one activation read, out = sil
 by the down projection (K=17408 -> N=5120) on that output. One "step" is that pair of launches.
 
     python bench.py [--steps K] [--warmup W]
-                    [--workload verify64|decode1|q5k1|q5k16|q5k64|q4k1|q4k64|prefill2048|layerset|lmhead1|lmhead64|operand64]
+                    [--workload verify64|decode1|q5k1|q5k16|q5k64|q4k1|q4k64|q6k1|q80_1|iq4nl1|iq4xs1|prefill2048|layerset|lmhead1|lmhead64|operand64]
 
 Inputs are synthetic (seeded, on the device): code words uniform random, scale = bf16(|N(0,0.02)|),
 bias = bf16(N(0,0.01)), activations bf16(N(0,1)). Several copies of the weight set are rotated so
@@ -253,6 +253,36 @@ def build_workload(name, rt, torch, gen, kernel):
                "format": f"gguf {'q5_k' if fifth else 'q4_k'} planes",
                "weight_copies": ncopy}
         return launches, b, 2 * m * n * k, {"q5k": b}, cfg, {"q5k": 2 * m * n * k}
+    native_types = {"q80_": (8, "Q8_0"), "q6k": (14, "Q6_K"), "iq4nl": (20, "IQ4_NL"), "iq4xs": (23, "IQ4_XS")}
+    for prefix, (gtype, label) in native_types.items():
+        if not name.startswith(prefix):
+            continue
+        # Config 3's shape (K=17408 -> N=5120) with the weight in the native blocks of another GGUF
+        # format (random bytes, fp16 scale fields of about 1e-3).
+        m = int(name[len(prefix):] or 1)
+        k, n = 17408, 5120
+        elems, size = rt.GGUF_NATIVE[gtype]
+        one = n * (k // elems) * size
+        ncopy = copies_for(one)
+        at = 208 if gtype == 14 else 0
+        ws = []
+        for _ in range(ncopy):
+            blocks = n * (k // elems)
+            native = torch.randint(0, 256, (blocks, size), dtype=torch.uint8, device="cuda", generator=gen)
+            d = (1e-3 * (1 + 0.25 * (torch.rand(blocks, device="cuda", generator=gen) * 2 - 1))).to(torch.float16)
+            native[:, at:at + 2] = d.view(torch.uint8).view(blocks, 2)
+            ws.append(rt.GgufWeight(native.view(-1), gtype, n, k))
+        x = torch.randn(m, k, device="cuda", generator=gen).to(torch.bfloat16)
+        out = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+        b = one + m * k * 2 + m * n * 2
+
+        def launches(i):
+            w = ws[i % ncopy]
+            return [("gguf", lambda: rt.gemm(w, x, out=out))]
+
+        cfg = {"workload": f"{label} K17408->N5120 (native blocks)", "rows": m, "format": f"gguf {label.lower()}",
+               "weight_copies": ncopy}
+        return launches, b, 2 * m * n * k, {"gguf": b}, cfg, {"gguf": 2 * m * n * k}
     raise SystemExit(f"unknown workload {name}")
 
 

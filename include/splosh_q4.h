@@ -222,6 +222,24 @@ int splosh_q4k_gemm(const splosh_q5k_weight *w, const uint16_t *a, int64_t lda, 
                     int out_dtype, const void *residual, int64_t rows, int kernel, void *workspace,
                     size_t workspace_bytes, hipStream_t stream);
 int splosh_q4k_dequant(const splosh_q5k_weight *w, float *out, hipStream_t stream);
+
+/* ---- Other GGUF formats, native blocks --------------------------------------------------------
+ *
+ * Q8_0 (8), Q6_K (14), IQ4_NL (20) and IQ4_XS (23), ggml type ids as in the file, in the blocks a
+ * GGUF file holds: `rows` rows of `inner` elements, each row inner / block elements native blocks
+ * (GgufQuant.swift:13-48), rows back to back. They replace the reference's staged GGUF kernels
+ * for these formats (Engine.swift:1673-1694 dispatching sp_gguf_* by format,
+ * engine_gguf.metal:332-349) and GgufTensorType.decode (GgufQuant.swift:136-159).
+ *
+ * splosh_gguf_gemm: out[m][n] = sum_k a[m][k] w[n][k] (+ residual), rows of activations in
+ * passes of four over the weight (a streaming kernel for decode-sized row counts).
+ * splosh_gguf_dequant: the weight as fp32 [rows][inner], bit-exact with the reference decoder.
+ * Unsupported types return SPLOSH_ERR_UNSUPPORTED. */
+int splosh_gguf_gemm(int gguf_type, const uint8_t *native, int64_t rows, int64_t inner, const uint16_t *a,
+                     int64_t lda, void *out, int64_t ldc, int out_dtype, const void *residual, int64_t m,
+                     hipStream_t stream);
+int splosh_gguf_dequant(int gguf_type, const uint8_t *native, int64_t rows, int64_t inner, float *out,
+                        hipStream_t stream);
 int splosh_q4k_repack(const uint8_t *native, int64_t rows, int64_t inner, uint8_t *plane0, uint8_t *meta,
                       hipStream_t stream);
 int splosh_q4k_unpack(const uint8_t *plane0, const uint8_t *meta, int64_t rows, int64_t inner, uint8_t *native,

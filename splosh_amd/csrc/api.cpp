@@ -500,6 +500,42 @@ int splosh_q4k_dequant(const splosh_q5k_weight *w, float *out, hipStream_t strea
     return gguf_dequant(w, false, out, stream);
 }
 
+// Shape and geometry checks shared by the native-block GGUF entry points.
+static int check_gguf_native(int type, const uint8_t *native, int64_t rows, int64_t inner) {
+    int elems = 0, bytes = 0;
+    if (!splosh::gguf_native_block(type, &elems, &bytes))
+        return fail(SPLOSH_ERR_UNSUPPORTED, "ggml type not supported in native blocks (Q8_0, Q6_K, IQ4_NL, IQ4_XS)");
+    if (!native) return fail(SPLOSH_ERR_NULL_POINTER, "null weight");
+    if (rows <= 0 || inner <= 0) return fail(SPLOSH_ERR_INVALID_SHAPE, "rows and inner must be positive");
+    if (inner % elems != 0) return fail(SPLOSH_ERR_LAYOUT_MISMATCH, "inner is not a whole number of native blocks");
+    if (mul_overflows(rows, inner / elems * bytes) || rows * (inner / elems * bytes) >= ((int64_t)1 << 32))
+        return fail(SPLOSH_ERR_ARITHMETIC_OVERFLOW, "weight larger than 4 GiB");
+    return ok();
+}
+
+int splosh_gguf_gemm(int gguf_type, const uint8_t *native, int64_t rows, int64_t inner, const uint16_t *a,
+                     int64_t lda, void *out, int64_t ldc, int out_dtype, const void *residual, int64_t m,
+                     hipStream_t stream) {
+    int st = check_gguf_native(gguf_type, native, rows, inner);
+    if (st) return st;
+    if ((st = check_io(a, lda, out, ldc, out_dtype, m, rows, inner))) return st;
+    if (lda % 8 != 0 || !aligned(a, 16))
+        return fail(SPLOSH_ERR_UNSUPPORTED, "GGUF native kernel needs lda % 8 == 0 and 16-byte aligned activations");
+    if (m > ((int64_t)65535 * 4)) return fail(SPLOSH_ERR_UNSUPPORTED, "too many activation rows for one launch");
+    return hip_status(splosh::launch_gguf_gemv(gguf_type, native, rows, inner, a, lda, out, ldc, out_dtype, residual,
+                                               m, stream),
+                      "gguf native gemm launch");
+}
+
+int splosh_gguf_dequant(int gguf_type, const uint8_t *native, int64_t rows, int64_t inner, float *out,
+                        hipStream_t stream) {
+    int st = check_gguf_native(gguf_type, native, rows, inner);
+    if (st) return st;
+    if (!out || !aligned(out, 16)) return fail(SPLOSH_ERR_NULL_POINTER, "null or unaligned output");
+    return hip_status(splosh::launch_gguf_dequant(gguf_type, native, rows, inner, out, stream),
+                      "gguf native dequant launch");
+}
+
 int splosh_q5k_repack(const uint8_t *native, int64_t rows, int64_t inner, uint8_t *plane0, uint8_t *plane1,
                       uint8_t *meta, hipStream_t stream) {
     if (!native || !plane0 || !plane1 || !meta) return fail(SPLOSH_ERR_NULL_POINTER, "null buffer");

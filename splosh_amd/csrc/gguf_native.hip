@@ -1,0 +1,245 @@
+// gguf_native.hip -- GGUF Q8_0, Q6_K, IQ4_NL and IQ4_XS weights read in their native blocks.
+//
+// The reference decodes these formats with GgufTensorType.decode (GgufQuant.swift:136-275) and
+// multiplies them on its staged GGUF path (engine_gguf.metal, one decoder a format). Here a weight
+// stays in the blocks the GGUF file holds ([rows][inner / block elements] blocks, row after row):
+//
+//  * gguf_dequant_kernel: one thread a 32-element group, the reference decoder's fp32 operations
+//    in its order (bit-exact).
+//  * gguf_gemv_kernel: out[m][n] = sum_k a[m][k] w[n][k] for a few rows of activations. A wave
+//    owns one weight row; its lanes take the row's 32-element groups in turn, decode each into
+//    registers exactly as the dequant kernel does and accumulate it against up to MR activation
+//    rows (fp32). The wave's partial sums meet in a shuffle tree. Rows beyond MR take further
+//    passes over the weight (grid.y).
+//
+// Blocks are 2-byte aligned at best (Q8_0: 34 bytes, Q6_K: 210), so their fields are read with
+// 16-bit buffer loads; the bound is issue rate, not HBM, and is measured as such.
+#include "common.hpp"
+#include "launch.hpp"
+
+namespace splosh {
+
+// IQ4_NL / IQ4_XS code values (llama.cpp's kvalues_iq4nl; the format's table).
+__constant__ float kIq4Table[16] = {-127.0f, -104.0f, -83.0f, -65.0f, -49.0f, -35.0f, -22.0f, -10.0f,
+                                    1.0f,    13.0f,   25.0f,  38.0f,  53.0f,  69.0f,  89.0f,  113.0f};
+
+template <int TYPE>
+struct GgufGeom;
+template <> struct GgufGeom<8> { static constexpr int kElems = 32, kBytes = 34; };    // Q8_0
+template <> struct GgufGeom<20> { static constexpr int kElems = 32, kBytes = 18; };   // IQ4_NL
+template <> struct GgufGeom<14> { static constexpr int kElems = 256, kBytes = 210; }; // Q6_K
+template <> struct GgufGeom<23> { static constexpr int kElems = 256, kBytes = 136; }; // IQ4_XS
+
+__device__ __forceinline__ uint32_t ld16(rsrc_t r, uint32_t off) { return buffer_load_u16(r, off, 0); }
+
+// Bytes 2 i and 2 i + 1 of the 16 loaded halves of a 32-byte run starting at `off` (2-aligned).
+__device__ __forceinline__ void load_run32(rsrc_t r, uint32_t off, uint32_t (&h)[16]) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) h[i] = ld16(r, off + 2 * i);
+}
+__device__ __forceinline__ uint32_t byte_of(const uint32_t (&h)[16], int e) { return (h[e >> 1] >> (8 * (e & 1))) & 0xFF; }
+
+// Group g of a row whose blocks start at byte `row` (GgufQuant.swift decode, fp32 op order).
+template <int TYPE>
+__device__ __forceinline__ void decode_group(rsrc_t r, uint32_t row, int g, float (&v)[32]) {
+    if constexpr (TYPE == 8) {  // Q8_0 (GgufQuant.swift:172-175)
+        const uint32_t b = row + (uint32_t)g * 34u;
+        const float d = half_bits_to_f32(ld16(r, b));
+        uint32_t h[16];
+        load_run32(r, b + 2, h);
+#pragma unroll
+        for (int e = 0; e < 32; ++e) v[e] = d * (float)(int8_t)byte_of(h, e);
+    } else if constexpr (TYPE == 20) {  // IQ4_NL (:179-185)
+        const uint32_t b = row + (uint32_t)g * 18u;
+        const float d = half_bits_to_f32(ld16(r, b));
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t two = ld16(r, b + 2 + 2 * i);
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const uint32_t byte = (two >> (8 * k)) & 0xFF;
+                v[2 * i + k] = d * kIq4Table[byte & 15];
+                v[16 + 2 * i + k] = d * kIq4Table[byte >> 4];
+            }
+        }
+    } else if constexpr (TYPE == 14) {  // Q6_K (:218-230): ql[128], qh[64], scales[16], d
+        const int j = g & 7, half = j >> 2, quarter = j & 3;
+        const uint32_t b = row + (uint32_t)(g >> 3) * 210u;
+        const float d = half_bits_to_f32(ld16(r, b + 208));
+        const uint32_t sc = ld16(r, b + 192 + 2 * j);
+        const float ds0 = d * (float)(int8_t)(sc & 0xFF), ds1 = d * (float)(int8_t)(sc >> 8);
+        uint32_t ql[16], qh[16];
+        load_run32(r, b + 64 * half + 32 * (quarter & 1), ql);
+        load_run32(r, b + 128 + 32 * half, qh);
+        const int lsh = 4 * (quarter >> 1), hsh = 2 * quarter;
+#pragma unroll
+        for (int e = 0; e < 32; ++e) {
+            const uint32_t low = (byte_of(ql, e) >> lsh) & 15, high = (byte_of(qh, e) >> hsh) & 3;
+            const float code = (float)(low | (high << 4)) - 32.0f;
+            v[e] = (e < 16 ? ds0 : ds1) * code;
+        }
+    } else {  // IQ4_XS (:261-275): d, scales_h, scales_l[4], qs[128]
+        const int j = g & 7;
+        const uint32_t b = row + (uint32_t)(g >> 3) * 136u;
+        const float d = half_bits_to_f32(ld16(r, b));
+        const uint32_t high = ld16(r, b + 2);
+        const uint32_t lowb = ld16(r, b + 4 + 2 * (j >> 2));   // bytes 4 + 2 (j / 4) .. + 1
+        const uint32_t low = (lowb >> (8 * ((j >> 1) & 1) + 4 * (j & 1))) & 15;
+        const uint32_t scale = low | (((high >> (2 * j)) & 3) << 4);
+        const float scaled = d * ((float)scale - 32.0f);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t two = ld16(r, b + 8 + 16 * j + 2 * i);
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const uint32_t byte = (two >> (8 * k)) & 0xFF;
+                v[2 * i + k] = scaled * kIq4Table[byte & 15];
+                v[16 + 2 * i + k] = scaled * kIq4Table[byte >> 4];
+            }
+        }
+    }
+}
+
+struct GgufNativeArgs {
+    const uint8_t *w;
+    uint32_t w_bytes, row_bytes;
+    int64_t rows, inner;
+    const uint16_t *a;
+    int64_t lda;
+    void *out;
+    int64_t ldc;
+    const void *residual;
+    int64_t m;
+    int out_dtype;
+    float *dense;
+};
+
+template <int TYPE>
+__global__ void __launch_bounds__(256) gguf_dequant_kernel(GgufNativeArgs args) {
+    const int64_t groups = args.inner / 32;
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= args.rows * groups) return;
+    const int64_t n = t / groups;
+    const int g = (int)(t % groups);
+    const rsrc_t r = make_rsrc(args.w, args.w_bytes);
+    float v[32];
+    decode_group<TYPE>(r, (uint32_t)(n * args.row_bytes), g, v);
+    f32x4 *dst = (f32x4 *)(args.dense + n * args.inner + (int64_t)g * 32);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) dst[q] = f32x4{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+}
+
+template <int TYPE, int MR>
+__global__ void __launch_bounds__(256) gguf_gemv_kernel(GgufNativeArgs args) {
+    const int lane = threadIdx.x & 63;
+    const int64_t n = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (n >= args.rows) return;
+    const int64_t m0 = (int64_t)blockIdx.y * MR;
+    const int groups = (int)(args.inner / 32);
+    const rsrc_t r = make_rsrc(args.w, args.w_bytes);
+    const uint32_t row = (uint32_t)(n * args.row_bytes);
+    float acc[MR];
+#pragma unroll
+    for (int i = 0; i < MR; ++i) acc[i] = 0.0f;
+    for (int g = lane; g < groups; g += 64) {
+        float v[32];
+        decode_group<TYPE>(r, row, g, v);
+#pragma unroll
+        for (int i = 0; i < MR; ++i) {
+            if (m0 + i >= args.m) break;
+            const u32x4 *ap = (const u32x4 *)(args.a + (m0 + i) * args.lda + (int64_t)g * 32);
+            float s = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const u32x4 x = ap[q];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    s = __builtin_fmaf(bf16_bits_to_f32(x[e] & 0xffffu), v[8 * q + 2 * e], s);
+                    s = __builtin_fmaf(bf16_bits_to_f32(x[e] >> 16), v[8 * q + 2 * e + 1], s);
+                }
+            }
+            acc[i] += s;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < MR; ++i) {
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) acc[i] += __shfl_xor(acc[i], o, 64);
+    }
+    if (lane != 0) return;
+#pragma unroll
+    for (int i = 0; i < MR; ++i) {
+        if (m0 + i >= args.m) break;
+        const int64_t index = (m0 + i) * args.ldc + n;
+        float value = acc[i];
+        if (args.out_dtype == SPLOSH_F32) {
+            if (args.residual) value += ((const float *)args.residual)[index];
+            ((float *)args.out)[index] = value;
+        } else {
+            if (args.residual) value += bf16_bits_to_f32(((const uint16_t *)args.residual)[index]);
+            ((uint16_t *)args.out)[index] = f32_to_bf16(value);
+        }
+    }
+}
+
+int gguf_native_block(int type, int *elems, int *bytes) {
+    switch (type) {
+        case 8: *elems = 32; *bytes = 34; return 1;
+        case 20: *elems = 32; *bytes = 18; return 1;
+        case 14: *elems = 256; *bytes = 210; return 1;
+        case 23: *elems = 256; *bytes = 136; return 1;
+        default: return 0;
+    }
+}
+
+static void fill_args(GgufNativeArgs &args, int type, const uint8_t *w, int64_t rows, int64_t inner) {
+    int elems = 0, bytes = 0;
+    gguf_native_block(type, &elems, &bytes);
+    args.w = w;
+    args.rows = rows;
+    args.inner = inner;
+    args.row_bytes = (uint32_t)(inner / elems * bytes);
+    args.w_bytes = (uint32_t)(rows * (int64_t)args.row_bytes);
+}
+
+hipError_t launch_gguf_dequant(int type, const uint8_t *w, int64_t rows, int64_t inner, float *dense,
+                               hipStream_t stream) {
+    GgufNativeArgs args = {};
+    fill_args(args, type, w, rows, inner);
+    args.dense = dense;
+    const int64_t threads = rows * (inner / 32);
+    const dim3 grid((unsigned)((threads + 255) / 256));
+    switch (type) {
+        case 8: hipLaunchKernelGGL(gguf_dequant_kernel<8>, grid, dim3(256), 0, stream, args); break;
+        case 20: hipLaunchKernelGGL(gguf_dequant_kernel<20>, grid, dim3(256), 0, stream, args); break;
+        case 14: hipLaunchKernelGGL(gguf_dequant_kernel<14>, grid, dim3(256), 0, stream, args); break;
+        default: hipLaunchKernelGGL(gguf_dequant_kernel<23>, grid, dim3(256), 0, stream, args); break;
+    }
+    return hipGetLastError();
+}
+
+constexpr int kGgufMR = 4;
+
+hipError_t launch_gguf_gemv(int type, const uint8_t *w, int64_t rows, int64_t inner, const uint16_t *a, int64_t lda,
+                            void *out, int64_t ldc, int out_dtype, const void *residual, int64_t m,
+                            hipStream_t stream) {
+    GgufNativeArgs args = {};
+    fill_args(args, type, w, rows, inner);
+    args.a = a;
+    args.lda = lda;
+    args.out = out;
+    args.ldc = ldc;
+    args.out_dtype = out_dtype;
+    args.residual = residual;
+    args.m = m;
+    const dim3 grid((unsigned)((rows + 3) / 4), (unsigned)((m + kGgufMR - 1) / kGgufMR));
+    switch (type) {
+        case 8: hipLaunchKernelGGL((gguf_gemv_kernel<8, kGgufMR>), grid, dim3(256), 0, stream, args); break;
+        case 20: hipLaunchKernelGGL((gguf_gemv_kernel<20, kGgufMR>), grid, dim3(256), 0, stream, args); break;
+        case 14: hipLaunchKernelGGL((gguf_gemv_kernel<14, kGgufMR>), grid, dim3(256), 0, stream, args); break;
+        default: hipLaunchKernelGGL((gguf_gemv_kernel<23, kGgufMR>), grid, dim3(256), 0, stream, args); break;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace splosh

@@ -107,6 +107,14 @@ hipError_t launch_q4_verify(const VerifyPlan &plan, const splosh_q4_weight &w, c
                             const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype,
                             const void *residual, int64_t rows, void *workspace, hipStream_t stream);
 
+// GGUF Q8_0 / Q6_K / IQ4_NL / IQ4_XS in native blocks (gguf_native.hip).
+int gguf_native_block(int type, int *elems, int *bytes);
+hipError_t launch_gguf_dequant(int type, const uint8_t *w, int64_t rows, int64_t inner, float *dense,
+                               hipStream_t stream);
+hipError_t launch_gguf_gemv(int type, const uint8_t *w, int64_t rows, int64_t inner, const uint16_t *a, int64_t lda,
+                            void *out, int64_t ldc, int out_dtype, const void *residual, int64_t m,
+                            hipStream_t stream);
+
 // The same kernel over Q5_K planes; the plan's units are 256-element blocks.
 bool q5k_mma_fits(int64_t rows, int64_t columns, int64_t inner, int64_t lda);
 hipError_t launch_q5k_mma(const MmaPlan &plan, const splosh_q5k_weight &w, const uint16_t *a, int64_t lda, void *out,

@@ -12,7 +12,8 @@ skipped, as there (:292-325).
 
 `load_weight` turns a Q4_K / Q5_K tensor into a runtime.Q5KWeight / Q4KWeight through the device
 repack (GgufPlanes.repack), with the rows rounded up to whole 128-row tiles by zero blocks
-(GgufConvert.storedRows, GgufConvert.swift:259-262). `write_gguf` writes the same form (the tests'
+(GgufConvert.storedRows, GgufConvert.swift:259-262), and a Q8_0 / Q6_K / IQ4_NL / IQ4_XS tensor into
+a runtime.GgufWeight of its native blocks. `write_gguf` writes the same form (the tests'
 fixtures).
 """
 import struct
@@ -170,8 +171,13 @@ def load_weight(f, name, device="cuda"):
     import torch
     from . import runtime as rt
     t = f.tensor(name)
+    if t.type in rt.GGUF_NATIVE:
+        # Q8_0, Q6_K, IQ4_NL, IQ4_XS stay in their native blocks.
+        native = torch.from_numpy(np.array(f.bytes(name))).to(device)
+        return rt.GgufWeight(native, t.type, t.rows, t.inner)
     if t.type not in (Q4_K, Q5_K):
-        raise GgufError(f"tensor {name} has ggml type {t.type}; the planes are built for Q4_K and Q5_K")
+        raise GgufError(f"tensor {name} has ggml type {t.type}; the device kernels take Q4_K, Q5_K, Q6_K, "
+                        "Q8_0, IQ4_NL and IQ4_XS")
     rows, inner = t.rows, t.inner
     stored = -(-rows // 128) * 128
     block = BLOCK[t.type][1]

@@ -142,6 +142,27 @@ def _out(a, rows, n, out, out_dtype):
     return out
 
 
+# ggml type id -> (block elements, block bytes) of the formats kept in native blocks
+# (GgufQuant.swift:13-48): Q8_0, Q6_K, IQ4_NL, IQ4_XS.
+GGUF_NATIVE = {8: (32, 34), 14: (256, 210), 20: (32, 18), 23: (256, 136)}
+
+
+@dataclass
+class GgufWeight:
+    """A GGUF weight in the native blocks its file holds (rows x inner, rows back to back)."""
+
+    native: torch.Tensor
+    gguf_type: int
+    rows: int
+    inner: int
+
+    def __post_init__(self):
+        if self.gguf_type not in GGUF_NATIVE:
+            raise SploshError(13, f"ggml type {self.gguf_type} is not kept in native blocks")
+        elems, size = GGUF_NATIVE[self.gguf_type]
+        _require(self.native, self.rows * (self.inner // elems) * size, "native")
+
+
 def workspace_bytes(rows, columns, inner):
     """splosh_workspace_bytes: the split-K scratch the kernels can use for this shape (0: none)."""
     return _lib.lib().splosh_workspace_bytes(rows, columns, inner)
@@ -178,6 +199,11 @@ def gemm(w, a, out=None, residual=None, out_dtype=torch.bfloat16, kernel=AUTO, r
     if residual is not None:
         if residual.dtype != out.dtype or residual.stride(0) != out.stride(0):
             raise SploshError(13, "residual must match the output's dtype and row stride")
+    if isinstance(w, GgufWeight):
+        _lib.check(_lib.lib().splosh_gguf_gemm(w.gguf_type, _ptr(w.native), w.rows, w.inner, _ptr(a), a.stride(0),
+                                               _ptr(out), out.stride(0), _dtype_code(out.dtype), _ptr(residual),
+                                               rows, _stream(stream)))
+        return out
     wc = w.c()
     ws, ws_bytes = _workspace(workspace, rows, w.rows, w.inner, a.device)
     if isinstance(w, Q4Weight):
@@ -213,9 +239,14 @@ def mlp_in(gate, up, a, out=None, out_dtype=torch.bfloat16, kernel=AUTO, rows=No
 def dequant(w, out=None, stream=None):
     """DequantOracle.dequantize / GgufTensorType.decode on the device: fp32 [rows, inner]."""
     if out is None:
-        dev = w.packed.device if isinstance(w, Q4Weight) else w.plane0.device
+        dev = (w.packed.device if isinstance(w, Q4Weight) else w.native.device if isinstance(w, GgufWeight)
+               else w.plane0.device)
         out = torch.empty((w.rows, w.inner), dtype=torch.float32, device=dev)
     _require(out, w.rows * w.inner * 4, "output")
+    if isinstance(w, GgufWeight):
+        _lib.check(_lib.lib().splosh_gguf_dequant(w.gguf_type, _ptr(w.native), w.rows, w.inner, _ptr(out),
+                                                  _stream(stream)))
+        return out
     wc = w.c()
     fn = (_lib.lib().splosh_q4_dequant if isinstance(w, Q4Weight) else
           _lib.lib().splosh_q4k_dequant if isinstance(w, Q4KWeight) else _lib.lib().splosh_q5k_dequant)

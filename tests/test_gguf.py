@@ -116,5 +116,5 @@ def test_unreadable(tmp_path):
 
 def test_load_weight_rejects_other_types(tmp_path):
     f = gguf.GgufFile(gguf.write_gguf(tmp_path / "o.gguf", [], _tensors()[2:]))
-    with pytest.raises(gguf.GgufError, match="Q4_K and Q5_K"):
+    with pytest.raises(gguf.GgufError, match="device kernels take"):
         gguf.load_weight(f, "output_norm.weight", device="cpu")

@@ -1,0 +1,110 @@
+"""GGUF Q8_0, Q6_K, IQ4_NL and IQ4_XS in native blocks on the GPU against the oracle: the dequant
+is bit-exact (the reference's golden blocks included), the GEMM within one bf16 rounding of the
+fp32-accumulate reference for every pass count of activation rows, the residual and both output
+types, config-0 sizes through sampled columns, and weights read out of a GGUF file."""
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from qcheck import abs_gemm, bf16_tensor, check_close, to_f32
+from splosh_amd import gguf
+
+pytestmark = pytest.mark.gpu
+TYPES = {"q8_0": 8, "q6K": 14, "iq4NL": 20, "iq4XS": 23}
+GOLDEN = Path(__file__).resolve().parent / "golden" / "gguf_golden_blocks.json"
+
+
+@pytest.fixture(scope="module")
+def rt():
+    from splosh_amd import runtime
+    return runtime
+
+
+def _weight(rt, t, n, k, seed):
+    native = oracle.gguf_random_native(t, n, k, seed)
+    w = rt.GgufWeight(torch.from_numpy(native).cuda(), t, n, k)
+    return w, oracle.gguf_decode(t, native).reshape(n, k)
+
+
+@pytest.mark.parametrize("name", list(TYPES))
+def test_golden_block_on_device(rt, name):
+    block = json.loads(GOLDEN.read_text())[name]
+    t = TYPES[name]
+    k = len(block["values"])
+    w = rt.GgufWeight(torch.tensor(block["bytes"], dtype=torch.uint8).cuda(), t, 1, k)
+    expected = np.array([np.float32(v) for v in block["values"]], np.float32)
+    assert np.array_equal(rt.dequant(w).cpu().numpy().reshape(-1).view(np.uint32), expected.view(np.uint32))
+
+
+@pytest.mark.parametrize("name", list(TYPES))
+@pytest.mark.parametrize("rows", [1, 3, 4, 9])
+def test_native_gemm(rt, name, rows):
+    t = TYPES[name]
+    n, k = 200, 1536
+    w, dense = _weight(rt, t, n, k, seed=rows + t)
+    assert np.array_equal(rt.dequant(w).cpu().numpy().view(np.uint32), dense.view(np.uint32))
+    a_bits = oracle.bf16_normal((rows, k), seed=rows)
+    ref = oracle.gemm_a_bf16_w_f32(a_bits, dense)
+    absref = abs_gemm(a_bits, dense)
+    a = bf16_tensor(a_bits)
+    got = rt.gemm(w, a, out_dtype=torch.float32)
+    check_close(got.cpu().numpy(), ref, bf16_out=False, tight=True, absref=absref, label=f"{name} f32 rows={rows}")
+    got = rt.gemm(w, a)
+    check_close(to_f32(got), ref, bf16_out=True, tight=True, absref=absref, label=f"{name} bf16 rows={rows}")
+    res = torch.from_numpy(oracle.bf16_normal((rows, n), seed=5).astype(np.float32)).cuda()
+    got = rt.gemm(w, a, out=res.clone(), out_dtype=torch.float32, residual=res)
+    check_close(got.cpu().numpy(), ref + res.cpu().numpy(), bf16_out=False, label=f"{name} residual rows={rows}")
+
+
+@pytest.mark.parametrize("name", ["q6K", "q8_0"])
+def test_config0_size_sampled(rt, name):
+    """K=5120 -> N=17408 at one row, 256 sampled output columns against the oracle."""
+    t = TYPES[name]
+    n, k = 17408, 5120
+    elems, size = oracle.GGUF_BLOCK[t]
+    native = oracle.gguf_random_native(t, n, k, seed=11)
+    w = rt.GgufWeight(torch.from_numpy(native).cuda(), t, n, k)
+    a_bits = oracle.bf16_normal((1, k), seed=12)
+    got = to_f32(rt.gemm(w, bf16_tensor(a_bits), out_dtype=torch.float32))
+    cols = np.sort(np.random.default_rng(13).choice(n, 256, replace=False))
+    row_bytes = k // elems * size
+    rows = native.reshape(n, row_bytes)[cols]
+    dense = oracle.gguf_decode(t, rows.reshape(-1)).reshape(len(cols), k)
+    check_close(got[:, cols], oracle.gemm_a_bf16_w_f32(a_bits, dense), bf16_out=False, tight=True,
+                absref=abs_gemm(a_bits, dense), label=f"{name} config0")
+
+
+def test_from_gguf_file(rt, tmp_path):
+    n, k = 96, 512
+    tensors, dense = [], {}
+    for name, t in TYPES.items():
+        native = oracle.gguf_random_native(t, n, k, seed=t)
+        tensors.append((f"blk.0.{name}.weight", t, [k, n], native.tobytes()))
+        dense[name] = oracle.gguf_decode(t, native).reshape(n, k)
+    f = gguf.GgufFile(gguf.write_gguf(tmp_path / "m.gguf", [], tensors))
+    a_bits = oracle.bf16_normal((2, k), seed=3)
+    for name in TYPES:
+        w = gguf.load_weight(f, f"blk.0.{name}.weight")
+        assert isinstance(w, rt.GgufWeight) and (w.rows, w.inner) == (n, k)
+        got = rt.gemm(w, bf16_tensor(a_bits), out_dtype=torch.float32)
+        check_close(got.cpu().numpy(), oracle.gemm_a_bf16_w_f32(a_bits, dense[name]), bf16_out=False, tight=True,
+                    absref=abs_gemm(a_bits, dense[name]), label=f"file {name}")
+
+
+def test_rejects_other_types_and_bad_shapes(rt):
+    from splosh_amd import _lib
+    a = bf16_tensor(oracle.bf16_normal((1, 512), seed=1))
+    out = torch.empty((1, 64), dtype=torch.float32, device="cuda")
+    native = torch.zeros(64 * 16 * 34, dtype=torch.uint8, device="cuda")
+    lib = _lib.lib()
+    for t in (0, 2, 11, 21):   # f32, Q4_0, Q3_K, IQ3_S: not in native form here
+        st = lib.splosh_gguf_gemm(t, native.data_ptr(), 64, 512, a.data_ptr(), 512, out.data_ptr(), 64,
+                                  _lib.F32, None, 1, None)
+        assert st != 0
+    st = lib.splosh_gguf_gemm(8, native.data_ptr(), 64, 500, a.data_ptr(), 512, out.data_ptr(), 64, _lib.F32,
+                              None, 1, None)
+    assert st != 0
