@@ -12,8 +12,8 @@
 //    rows (fp32). The wave's partial sums meet in a shuffle tree. Rows beyond MR take further
 //    passes over the weight (grid.y).
 //
-// Blocks are 2-byte aligned at best (Q8_0: 34 bytes, Q6_K: 210), so their fields are read with
-// 16-bit buffer loads; the bound is issue rate, not HBM, and is measured as such.
+// Blocks are 2-byte aligned at best (Q8_0: 34 bytes, Q6_K: 210): a run of bytes is read as the
+// dword-aligned window that covers it, in 16-byte loads, and shifted into place per lane.
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -32,12 +32,29 @@ template <> struct GgufGeom<23> { static constexpr int kElems = 256, kBytes = 13
 
 __device__ __forceinline__ uint32_t ld16(rsrc_t r, uint32_t off) { return buffer_load_u16(r, off, 0); }
 
-// Bytes 2 i and 2 i + 1 of the 16 loaded halves of a 32-byte run starting at `off` (2-aligned).
-__device__ __forceinline__ void load_run32(rsrc_t r, uint32_t off, uint32_t (&h)[16]) {
+// W dwords of bytes starting at a 2-aligned `off` (all 4 W of them inside the weight): the dword-aligned window that covers them (W + 1
+// dwords, the first in 16-byte pieces; buffer loads need only dword alignment) shifted into place
+// by the lane's 0- or 2-byte misalignment (v_alignbyte_b32). Every byte read lies in the weight.
+template <int W>
+__device__ __forceinline__ void load_span(rsrc_t r, uint32_t off, uint32_t (&out)[W]) {
+    const uint32_t a0 = off & ~3u, sh = off & 3u;
+    uint32_t win[W + 1];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) h[i] = ld16(r, off + 2 * i);
+    for (int q = 0; q < (W + 1) / 4; ++q) {
+        const u32x4 x = buffer_load16(r, a0 + 16u * q, 0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) win[4 * q + e] = x[e];
+    }
+#pragma unroll
+    for (int e = (W + 1) / 4 * 4; e < W; ++e) win[e] = buffer_load_u32(r, a0 + 4u * e, 0);
+    // Only the low half of the last window dword is ever used (when off is 2 mod 4), and its high
+    // half may lie past the weight, where a dword load would read zero for the whole dword.
+    win[W] = buffer_load_u16(r, a0 + 4u * W, 0);
+#pragma unroll
+    for (int i = 0; i < W; ++i) out[i] = __builtin_amdgcn_alignbyte(win[i + 1], win[i], sh);
 }
-__device__ __forceinline__ uint32_t byte_of(const uint32_t (&h)[16], int e) { return (h[e >> 1] >> (8 * (e & 1))) & 0xFF; }
+template <int W>
+__device__ __forceinline__ uint32_t byte_of(const uint32_t (&w)[W], int e) { return (w[e >> 2] >> (8 * (e & 3))) & 0xFF; }
 
 // Group g of a row whose blocks start at byte `row` (GgufQuant.swift decode, fp32 op order).
 template <int TYPE>
@@ -45,22 +62,20 @@ __device__ __forceinline__ void decode_group(rsrc_t r, uint32_t row, int g, floa
     if constexpr (TYPE == 8) {  // Q8_0 (GgufQuant.swift:172-175)
         const uint32_t b = row + (uint32_t)g * 34u;
         const float d = half_bits_to_f32(ld16(r, b));
-        uint32_t h[16];
-        load_run32(r, b + 2, h);
+        uint32_t h[8];   // the 32 codes
+        load_span<8>(r, b + 2, h);
 #pragma unroll
         for (int e = 0; e < 32; ++e) v[e] = d * (float)(int8_t)byte_of(h, e);
     } else if constexpr (TYPE == 20) {  // IQ4_NL (:179-185)
         const uint32_t b = row + (uint32_t)g * 18u;
         const float d = half_bits_to_f32(ld16(r, b));
+        uint32_t h[4];   // 16 bytes of two codes
+        load_span<4>(r, b + 2, h);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t two = ld16(r, b + 2 + 2 * i);
-#pragma unroll
-            for (int k = 0; k < 2; ++k) {
-                const uint32_t byte = (two >> (8 * k)) & 0xFF;
-                v[2 * i + k] = d * kIq4Table[byte & 15];
-                v[16 + 2 * i + k] = d * kIq4Table[byte >> 4];
-            }
+        for (int e = 0; e < 16; ++e) {
+            const uint32_t byte = byte_of(h, e);
+            v[e] = d * kIq4Table[byte & 15];
+            v[16 + e] = d * kIq4Table[byte >> 4];
         }
     } else if constexpr (TYPE == 14) {  // Q6_K (:218-230): ql[128], qh[64], scales[16], d
         const int j = g & 7, half = j >> 2, quarter = j & 3;
@@ -68,9 +83,9 @@ __device__ __forceinline__ void decode_group(rsrc_t r, uint32_t row, int g, floa
         const float d = half_bits_to_f32(ld16(r, b + 208));
         const uint32_t sc = ld16(r, b + 192 + 2 * j);
         const float ds0 = d * (float)(int8_t)(sc & 0xFF), ds1 = d * (float)(int8_t)(sc >> 8);
-        uint32_t ql[16], qh[16];
-        load_run32(r, b + 64 * half + 32 * (quarter & 1), ql);
-        load_run32(r, b + 128 + 32 * half, qh);
+        uint32_t ql[8], qh[8];
+        load_span<8>(r, b + 64 * half + 32 * (quarter & 1), ql);
+        load_span<8>(r, b + 128 + 32 * half, qh);
         const int lsh = 4 * (quarter >> 1), hsh = 2 * quarter;
 #pragma unroll
         for (int e = 0; e < 32; ++e) {
@@ -87,15 +102,13 @@ __device__ __forceinline__ void decode_group(rsrc_t r, uint32_t row, int g, floa
         const uint32_t low = (lowb >> (8 * ((j >> 1) & 1) + 4 * (j & 1))) & 15;
         const uint32_t scale = low | (((high >> (2 * j)) & 3) << 4);
         const float scaled = d * ((float)scale - 32.0f);
+        const u32x4 q = buffer_load16(r, b + 8 + 16 * j, 0);   // blocks of 136 bytes: 8-aligned runs
+        const uint32_t qs[4] = {q[0], q[1], q[2], q[3]};
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t two = ld16(r, b + 8 + 16 * j + 2 * i);
-#pragma unroll
-            for (int k = 0; k < 2; ++k) {
-                const uint32_t byte = (two >> (8 * k)) & 0xFF;
-                v[2 * i + k] = scaled * kIq4Table[byte & 15];
-                v[16 + 2 * i + k] = scaled * kIq4Table[byte >> 4];
-            }
+        for (int e = 0; e < 16; ++e) {
+            const uint32_t byte = byte_of(qs, e);
+            v[e] = scaled * kIq4Table[byte & 15];
+            v[16 + e] = scaled * kIq4Table[byte >> 4];
         }
     }
 }
