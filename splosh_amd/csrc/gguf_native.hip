@@ -19,9 +19,18 @@
 
 namespace splosh {
 
-// IQ4_NL / IQ4_XS code values (llama.cpp's kvalues_iq4nl; the format's table).
-__constant__ float kIq4Table[16] = {-127.0f, -104.0f, -83.0f, -65.0f, -49.0f, -35.0f, -22.0f, -10.0f,
-                                    1.0f,    13.0f,   25.0f,  38.0f,  53.0f,  69.0f,  89.0f,  113.0f};
+// IQ4_NL / IQ4_XS code values (llama.cpp's kvalues_iq4nl, the format's table: -127, -104, -83,
+// -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113) as int8 bytes, four to a dword.
+constexpr uint32_t kIq4Tab0 = 0xBFAD9881u, kIq4Tab1 = 0xF6EADDCFu, kIq4Tab2 = 0x26190D01u, kIq4Tab3 = 0x71594535u;
+
+// Table values (int8) of the four 4-bit codes in the bytes of `idx`: entries 0..7 and 8..15 by two
+// byte permutes, then per byte the half that bit 3 of the code picks.
+__device__ __forceinline__ uint32_t iq4_lookup4(uint32_t idx) {
+    const uint32_t sel = idx & 0x07070707u;
+    const uint32_t lo = perm_bytes(kIq4Tab1, kIq4Tab0, sel), hi = perm_bytes(kIq4Tab3, kIq4Tab2, sel);
+    const uint32_t mask = ((idx >> 3) & 0x01010101u) * 0xFFu;
+    return (hi & mask) | (lo & ~mask);
+}
 
 template <int TYPE>
 struct GgufGeom;
@@ -72,10 +81,13 @@ __device__ __forceinline__ void decode_group(rsrc_t r, uint32_t row, int g, floa
         uint32_t h[4];   // 16 bytes of two codes
         load_span<4>(r, b + 2, h);
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const uint32_t byte = byte_of(h, e);
-            v[e] = d * kIq4Table[byte & 15];
-            v[16 + e] = d * kIq4Table[byte >> 4];
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t lo = iq4_lookup4(h[q] & 0x0F0F0F0Fu), hi = iq4_lookup4((h[q] >> 4) & 0x0F0F0F0Fu);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v[4 * q + e] = d * (float)(int8_t)((lo >> (8 * e)) & 0xFF);
+                v[16 + 4 * q + e] = d * (float)(int8_t)((hi >> (8 * e)) & 0xFF);
+            }
         }
     } else if constexpr (TYPE == 14) {  // Q6_K (:218-230): ql[128], qh[64], scales[16], d
         const int j = g & 7, half = j >> 2, quarter = j & 3;
@@ -105,10 +117,13 @@ __device__ __forceinline__ void decode_group(rsrc_t r, uint32_t row, int g, floa
         const u32x4 q = buffer_load16(r, b + 8 + 16 * j, 0);   // blocks of 136 bytes: 8-aligned runs
         const uint32_t qs[4] = {q[0], q[1], q[2], q[3]};
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const uint32_t byte = byte_of(qs, e);
-            v[e] = scaled * kIq4Table[byte & 15];
-            v[16 + e] = scaled * kIq4Table[byte >> 4];
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t lo = iq4_lookup4(qs[k] & 0x0F0F0F0Fu), hi = iq4_lookup4((qs[k] >> 4) & 0x0F0F0F0Fu);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v[4 * k + e] = scaled * (float)(int8_t)((lo >> (8 * e)) & 0xFF);
+                v[16 + 4 * k + e] = scaled * (float)(int8_t)((hi >> (8 * e)) & 0xFF);
+            }
         }
     }
 }
