@@ -169,9 +169,9 @@ __global__ void __launch_bounds__(256) gguf_gemv_kernel(GgufNativeArgs args) {
     float acc[MR];
 #pragma unroll
     for (int i = 0; i < MR; ++i) acc[i] = 0.0f;
-    for (int g = lane; g < groups; g += 64) {
-        float v[32];
-        decode_group<TYPE>(r, row, g, v);
+    // Two groups an iteration (the second 64 groups on), both decoded before either is used so
+    // that their loads are in flight together; the groups left over one at a time.
+    auto accumulate = [&](int g, const float (&v)[32]) {
 #pragma unroll
         for (int i = 0; i < MR; ++i) {
             if (m0 + i >= args.m) break;
@@ -188,6 +188,22 @@ __global__ void __launch_bounds__(256) gguf_gemv_kernel(GgufNativeArgs args) {
             }
             acc[i] += s;
         }
+    };
+    int g = lane;
+    // Measured: pairs pay off for Q8_0 (27.8 -> 24.7 us at K17408 -> N5120), not for the formats
+    // whose decode holds more registers.
+    constexpr bool kPairs = TYPE == 8;
+    for (; kPairs && g + 64 < groups; g += 128) {
+        float v0[32], v1[32];
+        decode_group<TYPE>(r, row, g, v0);
+        decode_group<TYPE>(r, row, g + 64, v1);
+        accumulate(g, v0);
+        accumulate(g + 64, v1);
+    }
+    for (; g < groups; g += 64) {
+        float v[32];
+        decode_group<TYPE>(r, row, g, v);
+        accumulate(g, v);
     }
 #pragma unroll
     for (int i = 0; i < MR; ++i) {
