@@ -140,9 +140,10 @@ int splosh_q4_shape_validate(int64_t rows, int64_t columns, int64_t inner, const
  * its scratch (Runtime/Engine.swift:460-486); here the caller does, and the library allocates
  * nothing. Without a workspace (or with a smaller one) the kernels do not split K: the results
  * agree up to the fp32 summation order, with less parallelism. Calls that share one workspace
- * must be ordered on one stream. The workspace must be zero-filled before its first use: it holds
- * per-band arrival counters that the kernels return to zero before they exit, so later calls
- * reuse it as it is (zero it again after a call that failed or was aborted). */
+ * must be ordered on one stream. The workspace must be zero-filled before its first use: its first
+ * 16 KiB hold per-band arrival counters that the kernels return to zero before they exit, and no
+ * call writes anything else there, so later calls of any shape, row count or entry point reuse it
+ * as it is (zero it again after a call that failed or was aborted). */
 size_t splosh_workspace_bytes(int64_t rows, int64_t columns, int64_t inner);
 
 const char *splosh_status_string(int status);

@@ -96,6 +96,14 @@ __device__ __forceinline__ void wait_vmcnt() {
 // outstanding global loads (which __syncthreads' fence would drain), so prefetches stay in flight.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// lds_barrier() at a hand-off where up to OUTSTANDING loads into LDS, the youngest ones issued,
+// are meant to stay in flight. The count is written into the assembly as a comment, where a
+// static check compares it with what the preceding vmcnt wait really leaves outstanding.
+template <int OUTSTANDING>
+__device__ __forceinline__ void lds_barrier_staged() {
+    asm volatile("; splosh-lds-outstanding %0\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(OUTSTANDING) : "memory");
+}
+
 // x sigmoid(x) with the hardware reciprocal (v_rcp_f32, about 1 ulp) instead of a full-precision
 // divide: the result is rounded to bf16 or summed in fp32 afterwards.
 __device__ __forceinline__ float silu(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }

@@ -98,14 +98,15 @@ struct Q4Format {
     static constexpr int kUnitK = kGroup;
     static constexpr int kBandCols = CW * 32;
     static constexpr int kSBuf = kStageSide ? NW * 2 * KW * kBandCols * 2 : 0;
-    static_assert(KW * (kBandCols * 2 / 16) <= 64, "one wave-wide load covers an array's step");
+    static constexpr int kSidePer = kStageSide ? NW * 2 * KW * (kBandCols * 2 / 16) / (CW * KW) : 0;
+    static constexpr int kSideLoads = kStageSide ? 1 : 0;  // staging loads per wave and step
+    static_assert(!kStageSide || (KW * 8) % kSidePer == 0, "a wave's pieces lie in one array");
     static constexpr int piece(int i) { return i; }
 
     rsrc_t q_rsrc[NW], s_rsrc[NW], b_rsrc[NW], side_rsrc;
     int wave, lane, kw, cw, r, h, ga, gb;
     uint32_t G32, q_lane, side_lane, q_group, side_group, side_src;
-    bool side_loader;
-    u32x4 sr;
+    int side_g;      // group (within a step) of this lane's staged sidecar piece
     u32x4 wq[D][NW];
     uint32_t wsc[D][NW], wbi[D][NW];
     MixCoef cf[NW];  // coefficients of the step being dequantized
@@ -123,12 +124,15 @@ struct Q4Format {
             s_rsrc[w] = make_rsrc(args.scales[w], args.sidecar_bytes);
             b_rsrc[w] = make_rsrc(args.biases[w], args.sidecar_bytes);
         }
-        // The sidecar array this wave stages (waves 0 .. 2 NW - 1): weight wave / 2, bias if odd.
-        const int side_w = (wave >> 1) < NW ? (wave >> 1) : 0;
-        side_rsrc = make_rsrc((wave & 1) ? (const void *)args.biases[side_w] : (const void *)args.scales[side_w],
+        // The staged sidecars of a step are NW x 2 arrays x KW groups x 8 pieces of 16 bytes (the
+        // band's 64 columns of one group); wave v stages pieces [v kSidePer, (v + 1) kSidePer), all
+        // of one array: array a = weight a / 2, bias if a is odd.
+        const int piece0 = wave * kSidePer;
+        const int arr = piece0 / (KW * 8);
+        const int side_w = (arr >> 1) < NW ? (arr >> 1) : 0;
+        side_rsrc = make_rsrc((arr & 1) ? (const void *)args.biases[side_w] : (const void *)args.scales[side_w],
                               args.sidecar_bytes);
-        side_loader = kStageSide && wave < 2 * NW && lane < 8 * KW;
-        sr = u32x4{0u, 0u, 0u, 0u};
+        side_g = ((piece0 + lane) / 8) % KW;
         asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic));
     }
     __device__ int steps(int ga_, int gb_) const { return (gb_ - ga_ + KW - 1) / KW; }
@@ -145,7 +149,7 @@ struct Q4Format {
             q_group = 128u * 32u;
             side_group = 128u * 2u;
             const uint32_t n0 = (uint32_t)band * kBandCols;
-            side_src = (((n0 >> 7) * G32 * 128u + (n0 & 127u)) * 2u) + 16u * (lane & 7);
+            side_src = (((n0 >> 7) * G32 * 128u + (n0 & 127u)) * 2u) + 16u * (lane & 7);  // piece (v kSidePer + lane) % 8
         } else {
             q_lane = col * (uint32_t)args.stride_words * 4u + 16u * h;
             side_lane = col * G32 * 2u;
@@ -154,14 +158,16 @@ struct Q4Format {
             side_src = 0;
         }
     }
-    __device__ void load_s(int t) {
-        if (!side_loader) return;
-        int g = ga + t * KW + (lane >> 3);
-        g = g < gb ? g : gb - 1;
-        sr = buffer_load16(side_rsrc, side_src + (uint32_t)g * 256u, 0);
-    }
-    __device__ void store_s(char *sbuf) {
-        if (side_loader) *(u32x4 *)(sbuf + (wave * 8 * KW + lane) * 16) = sr;
+    // Sidecars of step t, straight into LDS (the staging buffer `sbuf`): lane l < kSidePer of
+    // wave v writes piece v kSidePer + l. Groups past the job re-read the last one.
+    __device__ void load_s(int t, char *sbuf) {
+        if constexpr (kStageSide) {
+            if (lane < kSidePer) {
+                int g = ga + t * KW + side_g;
+                g = g < gb ? g : gb - 1;
+                buffer_load_lds16(side_rsrc, sbuf + wave * kSidePer * 16, side_src + (uint32_t)g * 256u);
+            }
+        }
     }
     // Codes (and row-major sidecars) of step t into ring slot `slot`; the group is a wave-uniform
     // offset, clamped into the job so it stays in bounds.
@@ -227,6 +233,8 @@ struct Q5Format {
     static constexpr int kUnitK = 256;
     static constexpr int kBandCols = CW * 32;
     static constexpr int kSBuf = kBandCols * 16;
+    static constexpr int kSidePer = kBandCols / (CW * KW);  // meta records a wave stages per step
+    static constexpr int kSideLoads = 1;
     static_assert(KW == 4, "four waves cover the eight groups of a block");
     static_assert(kBandCols <= 64, "one wave loads the band's meta records");
     static constexpr int piece(int i) { return ((i & 1) << 1) | (i >> 1); }
@@ -236,7 +244,6 @@ struct Q5Format {
     uint32_t blocks, p0_lane, p1_lane, m_lane;
     u32x4 wq[D];
     uint32_t wh[D];
-    u32x4 mr;
     float scaled, offset;  // d sc and -(dmin mn) of the lane's group in the step being dequantized
     uint32_t lo[2], hi[2]; // 5-bit codes of two words, shared by two sub-steps
 
@@ -249,7 +256,6 @@ struct Q5Format {
         p0_rsrc = make_rsrc(args.plane0, args.code_bytes);
         p1_rsrc = make_rsrc(FIFTH ? (const void *)args.plane1 : (const void *)args.plane0, FIFTH ? args.sidecar_bytes : 0u);
         m_rsrc = make_rsrc(args.meta, args.meta_bytes);
-        mr = u32x4{0u, 0u, 0u, 0u};
     }
     __device__ int steps(int ga_, int gb_) const { return gb_ - ga_; }
     __device__ bool active(int) const { return true; }
@@ -264,7 +270,8 @@ struct Q5Format {
         const uint32_t rec0 = ((col >> 7) * blocks * 8u + 2u * kw + h) * 128u + (col & 127u);
         p0_lane = rec0 * 16u;
         p1_lane = rec0 * 4u;
-        const int64_t mcol64 = (int64_t)band * kBandCols + lane;
+        // The meta record this lane stages (lanes < kSidePer): band column v kSidePer + lane.
+        const int64_t mcol64 = (int64_t)band * kBandCols + wave * kSidePer + (lane % kSidePer);
         const uint32_t mcol = (uint32_t)(mcol64 < args.n ? mcol64 : args.n - 1);
         m_lane = ((mcol >> 7) * blocks * 128u + (mcol & 127u)) * 16u;
     }
@@ -272,11 +279,9 @@ struct Q5Format {
         const int b = ga + t < gb ? ga + t : gb - 1;
         return (uint32_t)__builtin_amdgcn_readfirstlane(b);
     }
-    __device__ void load_s(int t) {
-        if (wave == 0) mr = buffer_load16(m_rsrc, m_lane, block(t) * (128u * 16u));
-    }
-    __device__ void store_s(char *sbuf) {
-        if (wave == 0 && lane < kBandCols) *(u32x4 *)(sbuf + lane * 16) = mr;
+    // Meta records of step t's block straight into LDS (`sbuf`, one 16-byte record a column).
+    __device__ void load_s(int t, char *sbuf) {
+        if (lane < kSidePer) buffer_load_lds16(m_rsrc, sbuf + wave * kSidePer * 16, m_lane + block(t) * (128u * 16u));
     }
     __device__ void load_w(int slot, int t) {
         const uint32_t b = block(t);
@@ -341,7 +346,7 @@ struct MmaShape {
     static constexpr int kAPer = kAPieces / kThreads;              // activation loads per wave and step
     static constexpr int kABuf = kAPieces * 16;                    // bytes of one chunk buffer
     static constexpr int kSBuf = SBUF;                             // bytes of one staged-sidecar buffer
-    static constexpr int kNB = 3;                                  // chunk buffers
+    static constexpr int kNB = 4;                                  // stage buffers (chunk + sidecars)
     static constexpr int kAcc = FM * NW * 16;                      // accumulator floats per lane
     static constexpr size_t kRedBytes = (size_t)KW * CW * kAcc * 64 * sizeof(float);
     static constexpr size_t kABytes = (size_t)kNB * (kABuf + kSBuf);
@@ -405,8 +410,14 @@ mma_kernel(MmaArgs args) {
     char *lds_bytes = (char *)lds;
     char *side_lds = lds_bytes + S::kNB * S::kABuf;
 
-    // One job: column band `band`, units [ga, gb); slot < 0 writes the output, else a partial.
-    auto run_job = [&](int band, int ga, int gb, int slot) {
+    // The K-summed results of a job, in the MFMA output layout: wave (kw, cw) owns rows
+    // 32 f + 8 kw + 4 h + i (i < 4) of band column cw 32 + r, for each weight.
+    f32x4 fin[NW][FM];
+
+    // One job: column band `band`, units [ga, gb); leaves its sums in `fin`. `after_prologue`
+    // runs once every wave has passed the prologue's barrier (all of the workgroup's earlier
+    // stores are complete by then).
+    auto run_job = [&](int band, int ga, int gb, auto &&after_prologue) {
         const int T = fmt.steps(ga, gb);
         fmt.begin(args, band, ga, gb);
 
@@ -421,9 +432,16 @@ mma_kernel(MmaArgs args) {
         };
         auto load_a = [&](int t, int buf) { load_a_part(t, buf, 0, S::kAPer); };
         constexpr int kAHalf = (S::kAPer + 1) / 2;
-        auto load_s = [&](int t) { fmt.load_s(t); };
-        auto store_s = [&](int buf) { fmt.store_s(side_lds + buf * S::kSBuf); };
+        // Stage j = the activation chunk of step j and the sidecars (or block metadata) of step
+        // j + 1, both straight into buffer j mod 4 (chunk area and sidecar area).
+        auto load_side = [&](int t, int buf) { fmt.load_s(t, side_lds + buf * S::kSBuf); };
         auto load_w = [&](int slot_, int t) { fmt.load_w(slot_, t); };
+        // Loads a wave issues per stage, and the mid-step wait: at the middle of step t the wave
+        // needs stage t + 1 (issued in step t - 2); after it it has issued the weights of step
+        // t + 2, stage t + 2 and the weights of step t + 3, which may stay in flight.
+        constexpr int kStageLoads = S::kAPer + F::kSideLoads;
+        constexpr int kMidWait = 2 * kWLoads + kStageLoads;
+        static_assert(kMidWait + kWLoads + kStageLoads <= 63, "vmcnt holds 6 bits");
         // Dequantized weights of the current step; operand i is replaced by the next step's as
         // soon as the MFMAs of sub-step i have been issued.
         bf16x8 bw[NW][4];
@@ -443,32 +461,39 @@ mma_kernel(MmaArgs args) {
 #pragma unroll
                 for (int e = 0; e < 16; ++e) acc[w][f][e] = 0.0f;
 
-        // The step count is padded to a multiple of 3: steps past T compute nothing but keep the
-        // load pattern regular (their loads re-read in-bounds data). Each step has its barrier in
-        // the middle, between MFMA sub-steps 1 and 2. There the wave waits for its pieces of the
-        // next step's chunk (loaded a step earlier), stores them to LDS, passes the barrier and
-        // reads the next step's first activation fragments; the loads of chunk t + 2 and of the
-        // weights of step t + 3 are issued around it (see the hooks below). Loads return in
-        // order, so "chunk t + 1 has arrived" is "at most the weight loads issued after it are
-        // outstanding". The chunk buffer written (t + 1 mod 3) last held chunk t - 2, which every
-        // wave finished before the previous barrier. LDS latency and the barrier hide behind
-        // sub-steps 2 and 3.
+        // The step count is padded to a multiple of 3 (the weight ring's depth): steps past T
+        // compute nothing but keep the load pattern regular (their loads re-read in-bounds data).
+        // Each step has its barrier in the middle, between MFMA sub-steps 1 and 2. There the wave
+        // waits for stage t + 1 (loaded two steps earlier), passes the barrier and reads the next
+        // step's first activation fragments; after the barrier it issues stage t + 3 into buffer
+        // t + 3 mod 4, which last held stage t - 1: chunk t - 1 (read in step t - 1) and the
+        // sidecars of step t (read at the start of step t - 1), both finished by every wave before
+        // this barrier. Loads complete in issue order (vmcnt counts down in order, and a load
+        // into LDS counts like any other and has written LDS when it is counted off), so "stage
+        // t + 1 has arrived" is "at most the kMidWait loads issued after it are outstanding":
+        // the weights of steps t + 2 and t + 3 stay in flight across the wait. The compiler does
+        // not track loads into LDS, so these waits, the barriers and the issue order (kept by the
+        // sched_barriers) are the whole of their synchronisation.
         const int Tp = (T + D - 1) / D * D;
-        auto nbuf = [&](int b) { return b == S::kNB - 1 ? 0 : b + 1; };
-        load_a(0, 0);
-        load_s(0);
+        auto nbuf = [&](int b) { return (b + 1) & (S::kNB - 1); };
+        static_assert(S::kNB == 4, "buffer arithmetic mod 4");
+        load_side(0, 3);  // sidecars of step 0: "stage -1"
         load_w(0, 0);
-        wait_vmcnt<kWLoads>();
-        store_s(0);
-        load_s(1);
+        load_a(0, 0);
+        load_side(1, 0);
+        __builtin_amdgcn_sched_barrier(0);
         load_w(1, 1);
-        wait_vmcnt<kWLoads>();
-        store_s(1);
         load_a(1, 1);
-        load_s(2);
+        load_side(2, 1);
+        __builtin_amdgcn_sched_barrier(0);
         load_w(2, 2);
-        lds_barrier();
-        dequant(0, 0, T > 0 && fmt.active(0));
+        load_a(2, 2);
+        load_side(3, 2);
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vmcnt<2 * kWLoads + 2 * kStageLoads>();  // stage -1, stage 0 and the weights of step 0
+        lds_barrier_staged<2 * kStageLoads>();         // stages 1 and 2 may be in flight
+        after_prologue();
+        dequant(0, 3, T > 0 && fmt.active(0));
         auto read_af = [&](bf16x8 *dst, int buf, int i) {
             const char *ap = lds_bytes + buf * S::kABuf;
 #pragma unroll
@@ -486,7 +511,8 @@ mma_kernel(MmaArgs args) {
         auto live = [&](int t) { return t < T && fmt.active(t); };
         auto step = [&](int t, int d, int abuf, auto &&mid, auto &&hook) {
             const int next = (d + 1) % D;
-            fmt.prepare(next, side_lds + nbuf(abuf) * S::kSBuf, live(t + 1));
+            // The sidecars of step t + 1 came with stage t (buffer t mod 4 = abuf).
+            fmt.prepare(next, side_lds + abuf * S::kSBuf, live(t + 1));
             // Fragments of sub-step i + 1 are read as soon as sub-step i's MFMAs are issued, so their
             // LDS latency hides behind the dequantization (two alternating register sets; sub-step 0
             // uses af_pre, read at the previous step's barrier).
@@ -504,44 +530,38 @@ mma_kernel(MmaArgs args) {
 #pragma unroll
                 for (int w = 0; w < NW; ++w) bw[w][i] = fmt.operand(w, i, next);
                 hook(i);
-                __builtin_amdgcn_sched_barrier(0);  // sub-steps stay in order (register pressure)
+                __builtin_amdgcn_sched_barrier(0);  // sub-steps stay in order (register pressure, load order)
             }
         };
 
         // Loads are spread over the step so that the workgroup's waves do not all queue at the
         // texture unit at once: sub-step 0 issues the weights of step t + 3 (their ring slot was
-        // dequantized in step t - 1), sub-steps 2 and 3 the halves of chunk t + 2 and the
-        // sidecars of step t + 3, after `mid` has stored the previous contents of those registers.
-        // So the last loads before "chunk t + 1 and sidecars t + 2" are complete are always the
-        // kWLoads weight loads of the current step. Sidecars run one step ahead of the chunks:
-        // those of step t + 2 are stored at the middle of step t (buffer t + 2 mod 3, last used
-        // for step t - 1's dequantization in step t - 2) and read while step t + 1 dequantizes
-        // step t + 2.
+        // dequantized in step t - 1), sub-steps 2 and 3 the halves of stage t + 3.
         int abuf = 0;  // buffer of step t's chunk
         for (int t0 = 0; t0 < Tp - D; t0 += D) {
 #pragma unroll
             for (int d = 0; d < D; ++d) {
                 const int t = t0 + d;
+                const int sbuf = (abuf + 3) & 3;  // stage t + 3
                 step(t, d, abuf,
                      [&] {
-                         wait_vmcnt<kWLoads>();  // chunk t + 1, sidecars t + 2 have arrived
-                         store_s(nbuf(nbuf(abuf)));
-                         lds_barrier();
+                         wait_vmcnt<kMidWait>();  // stage t + 1 has arrived
+                         lds_barrier_staged<kStageLoads>();  // stage t + 2 may be in flight
                          read_af(af_pre, nbuf(abuf), 0);
                      },
                      [&](int i) {
                          if (i == 0) load_w(d, t + D);
                          if (i == 2) {
-                             load_a_part(t + 2, nbuf(nbuf(abuf)), 0, kAHalf);
-                             load_s(t + 3);
+                             load_a_part(t + 3, sbuf, 0, kAHalf);
+                             load_side(t + 4, sbuf);
                          }
-                         if (i == 3) load_a_part(t + 2, nbuf(nbuf(abuf)), kAHalf, S::kAPer);
+                         if (i == 3) load_a_part(t + 3, sbuf, kAHalf, S::kAPer);
                      });
                 abuf = nbuf(abuf);
             }
         }
-        // The last three steps load only chunk Tp - 1 (in the first of them). Steps past T (at most
-        // the last two; T is uniform over the workgroup) are skipped: they would add nothing.
+        // The last three steps issue no loads (every stage they read was issued already). Steps
+        // past T (at most the last two; T is uniform over the workgroup) are skipped.
 #pragma unroll
         for (int d = 0; d < D; ++d) {
             const int t = Tp - D + d;
@@ -549,196 +569,211 @@ mma_kernel(MmaArgs args) {
             step(t, d, abuf,
                  [&] {
                      wait_vmcnt<0>();
-                     if (d == 0) store_s(nbuf(nbuf(abuf)));
                      lds_barrier();
                      if (d < 2) read_af(af_pre, nbuf(abuf), 0);
                  },
-                 [&](int i) {
-                     if (d == 0 && i == 2) load_a_part(t + 2, nbuf(nbuf(abuf)), 0, kAHalf);
-                     if (d == 0 && i == 3) load_a_part(t + 2, nbuf(nbuf(abuf)), kAHalf, S::kAPer);
-                 });
+                 [&](int) {});
             abuf = nbuf(abuf);
         }
-        lds_barrier();  // every wave is past its last fragment read
-        // No load is in flight now; the last barrier also ended every read of the chunk buffers.
+        wait_vmcnt<0>();  // nothing is in flight any more (the last steps waited); stated for every path
+        lds_barrier();    // every wave is past its last fragment read
+        // The last barrier also ended every read of the chunk buffers.
 
-        // Every wave parks its partial sums in LDS (element e of block f of weight w at
-        // [kw][cw][(w FM + f) 16 + e][lane]); then the whole workgroup sums the KW slices per output
-        // and writes whole rows: thread (m0, c) = (tid / band columns, tid % band columns) takes
-        // rows m0, m0 + kThreads / band columns, ...
+        // Sum the KW K-slices: every wave parks its accumulators in LDS as 16-byte quarters
+        // ([kw][cw][w][f][quarter][lane], conflict-free), and wave kw collects quarter kw of its
+        // column slice from all KW waves, in kw order (the same order whatever the timing).
         {
-            float *red = (float *)lds + (size_t)(kw * CW + cw) * S::kAcc * 64 + lane;
+            char *x = (char *)lds;
+            auto xoff = [&](int s, int w, int f, int q) {
+                return (((((s * CW + cw) * NW + w) * FM + f) * 4 + q) * 64 + lane) * 16;
+            };
 #pragma unroll
             for (int w = 0; w < NW; ++w)
 #pragma unroll
                 for (int f = 0; f < FM; ++f)
 #pragma unroll
-                    for (int e = 0; e < 16; ++e) red[((w * FM + f) * 16 + e) * 64] = acc[w][f][e];
+                    for (int q = 0; q < 4; ++q)
+                        *(f32x4 *)(x + xoff(kw, w, f, q)) =
+                            f32x4{acc[w][f][4 * q], acc[w][f][4 * q + 1], acc[w][f][4 * q + 2], acc[w][f][4 * q + 3]};
+            lds_barrier();
+#pragma unroll
+            for (int w = 0; w < NW; ++w)
+#pragma unroll
+                for (int f = 0; f < FM; ++f) {
+                    f32x4 sum = *(const f32x4 *)(x + xoff(0, w, f, kw));
+#pragma unroll
+                    for (int s2 = 1; s2 < KW; ++s2) sum += *(const f32x4 *)(x + xoff(s2, w, f, kw));
+                    fin[w][f] = sum;
+                }
         }
-        lds_barrier();
-        constexpr int kRowStep = S::kThreads / S::kBandCols;
-        const int c = tid % S::kBandCols;
-        const int64_t ocol = (int64_t)band * S::kBandCols + c;
-        const int rows = (int)args.rows;
-        const float *red = (const float *)lds + (size_t)(c / 32) * S::kAcc * 64 + (c % 32);
-        // With 64-column bands a thread's rows are the same for its whole wave: scalar row
-        // arithmetic (a per-lane 64-bit row offset per iteration would be hoisted and spilled).
-        static_assert(S::kBandCols % 64 == 0, "a wave's threads share their rows");
-        const int m_first = __builtin_amdgcn_readfirstlane(tid / S::kBandCols);
-        auto store_out = [&](int m, const float *v) {
-            float value = v[0];
-            if constexpr (NW == 2) value = silu(v[0]) * v[1];
-            const int64_t index = (int64_t)m * args.ldc + ocol;
-            if (args.out_dtype == SPLOSH_F32) {
-                if (args.residual) value += ((const float *)args.residual)[index];
-                ((float *)args.out)[index] = value;
-            } else {
-                if (args.residual) value += bf16_bits_to_f32(((const uint16_t *)args.residual)[index]);
-                ((uint16_t *)args.out)[index] = f32_to_bf16(value);
-            }
-        };
-        // Partial of slot s, weight w, row m, this thread's column: a byte offset into the workspace.
-        auto part_off = [&](int wg, int sl, int w, int m) {
-            return (uint32_t)((((wg * 2 + sl) * NW + w) * rows + m) * S::kBandCols + c) * 4u;
-        };
-#pragma unroll
-        for (int m = m_first; m < S::kRows; m += kRowStep) {
-            if (m >= rows) break;
-            const int f = m / 32, mm = m % 32;
-            const int e = (mm / 8) * 4 + (mm % 4), lane_h = ((mm / 4) % 2) * 32;
-            float v[NW];
-#pragma unroll
-            for (int w = 0; w < NW; ++w) {
-                float sum = 0.0f;
-#pragma unroll
-                for (int k = 0; k < KW; ++k) sum += red[(size_t)k * CW * S::kAcc * 64 + ((w * FM + f) * 16 + e) * 64 + lane_h];
-                v[w] = sum;
-            }
-            if (slot >= 0) {
-                // Written through to memory (gfx94x cache policy sc0 sc1): the workgroup that sums
-                // the band may run on another XCD, whose L2 is not coherent with this one's.
-#pragma unroll
-                for (int w = 0; w < NW; ++w)
-                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v[w]), p_rsrc, part_off(blockIdx.x, slot, w, m), 0, kDeviceCpol);
-                continue;
-            }
-            if (ocol < args.n) store_out(m, v);
-        }
-        // A shared band's fix-up runs in finish_band(), called by the caller: at once for the last
-        // job of the range, at the end of the range for the first (whose partial then has long
-        // reached memory, so the workgroup does not stall on it between its jobs).
     };
 
-    // The fix-up of a shared band: the last of its workgroups to arrive sums every partial in
-    // workgroup order (so the result does not depend on who is last), applies the epilogue and
-    // returns the band's counter to zero for the next call.
-    auto finish_band = [&](int band) {
-        constexpr int kRowStep = S::kThreads / S::kBandCols;
-        const int c = tid % S::kBandCols;
-        const int64_t ocol = (int64_t)band * S::kBandCols + c;
-        const int rows = (int)args.rows;
-        const int m_first = __builtin_amdgcn_readfirstlane(tid / S::kBandCols);
-        auto store_out = [&](int m, const float *v) {
-            float value = v[0];
-            if constexpr (NW == 2) value = silu(v[0]) * v[1];
-            const int64_t index = (int64_t)m * args.ldc + ocol;
-            if (args.out_dtype == SPLOSH_F32) {
-                if (args.residual) value += ((const float *)args.residual)[index];
-                ((float *)args.out)[index] = value;
-            } else {
-                if (args.residual) value += bf16_bits_to_f32(((const uint16_t *)args.residual)[index]);
-                ((uint16_t *)args.out)[index] = f32_to_bf16(value);
+    const int rows = (int)args.rows;
+    // Row i of this lane's quarter of block f, and the lane's band column.
+    auto own_row = [&](int f, int i) { return 32 * f + 8 * kw + 4 * h + i; };
+    const int bcol = cw * 32 + r;
+    auto store_out = [&](int band, const f32x4 (&v)[NW][FM]) {
+        const int64_t ocol = (int64_t)band * S::kBandCols + bcol;
+        if (ocol >= args.n) return;
+#pragma unroll
+        for (int f = 0; f < FM; ++f)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = own_row(f, i);
+                if (m >= rows) continue;
+                float value = v[0][f][i];
+                if constexpr (NW == 2) value = silu(v[0][f][i]) * v[1][f][i];
+                const int64_t index = (int64_t)m * args.ldc + ocol;
+                if (args.out_dtype == SPLOSH_F32) {
+                    if (args.residual) value += ((const float *)args.residual)[index];
+                    ((float *)args.out)[index] = value;
+                } else {
+                    if (args.residual) value += bf16_bits_to_f32(((const uint16_t *)args.residual)[index]);
+                    ((uint16_t *)args.out)[index] = f32_to_bf16(value);
+                }
             }
-        };
-        auto part_off = [&](int wg, int sl, int w, int m) {
-            return (uint32_t)((((wg * 2 + sl) * NW + w) * rows + m) * S::kBandCols + c) * 4u;
-        };
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this workgroup's partial is in memory
-        __syncthreads();
+    };
+    // Partial of workgroup wg, slot sl, weight w, row m, this lane's band column: a byte offset
+    // into the partial area ([grid][2][NW][rows][band columns] fp32).
+    auto part_off = [&](int wg, int sl, int w, int m) {
+        return (uint32_t)((((wg * 2 + sl) * NW + w) * rows + m) * S::kBandCols + bcol) * 4u;
+    };
+    // Written through to memory (gfx94x cache policy sc0 sc1): the workgroup that sums the band
+    // may run on another XCD, whose L2 is not coherent with this one's.
+    auto write_partial = [&](int sl) {
+#pragma unroll
+        for (int w = 0; w < NW; ++w)
+#pragma unroll
+            for (int f = 0; f < FM; ++f) {
+                const u32x4 bits = __builtin_bit_cast(u32x4, fin[w][f]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int m = own_row(f, i);
+                    if (m < rows) __builtin_amdgcn_raw_buffer_store_b32(bits[i], p_rsrc, part_off(blockIdx.x, sl, w, m), 0, kDeviceCpol);
+                }
+            }
+    };
+    // The contributors of a shared band (workgroups whose non-empty range meets it), in order,
+    // each as 2 wg + the slot it used: 1 if its range began in an earlier band. Thread 0 fills
+    // fix_list; the count is returned to every thread.
+    auto contributors = [&](int band) {
         const int64_t lo = (int64_t)(band - args.dp_bands) * U, hi = lo + U;  // the band's units
         const int i_lo = (int)(((lo + 1) * P - 1) / args.sk_units), i_hi = (int)((hi * P - 1) / args.sk_units);
         if (tid == 0) {
-            // The band's contributors (workgroups with a non-empty range meeting it), in order, and
-            // the slot each one used for it: 1 if its range began in an earlier band.
             int count = 0;
             for (int i = i_lo; i <= i_hi; ++i) {
                 const int64_t st = sk_start(i);
                 if (st == sk_start(i + 1)) continue;
                 fix_list[count++] = (uint16_t)(i * 2 + (st < lo ? 1 : 0));
             }
-            int *counter = args.counters + (band - args.dp_bands);
-            const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-            const bool last = old == count - 1;
-            if (last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-            fix_count = last ? count : 0;
+            fix_count = count;
         }
         __syncthreads();
-        const int count = fix_count;
-        if (count == 0) return;
-        // Partials are read in batches of contributors for every row of the thread at once,
-        // so that their memory latencies overlap; each sum still runs in contributor order.
-        constexpr int kMine = S::kRows / kRowStep;  // rows of this thread (those past `rows` idle)
-        float v[kMine][NW];
-#pragma unroll
-        for (int j = 0; j < kMine; ++j)
-#pragma unroll
-            for (int w = 0; w < NW; ++w) v[j][w] = 0.0f;
-        constexpr int kBatch = kMine * NW >= 32 ? 1 : 32 / (kMine * NW) < 4 ? 32 / (kMine * NW) : 4;
-        for (int c0 = 0; c0 < count; c0 += kBatch) {
-            float x[kBatch][kMine][NW];
-#pragma unroll
-            for (int q = 0; q < kBatch; ++q) {
-                const int entry = fix_list[c0 + q < count ? c0 + q : count - 1];
-#pragma unroll
-                for (int j = 0; j < kMine; ++j) {
-                    const int m = m_first + j * kRowStep;
-                    const int mc = m < rows ? m : rows - 1;
-#pragma unroll
-                    for (int w = 0; w < NW; ++w)
-                        x[q][j][w] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                                                   p_rsrc, part_off(entry >> 1, entry & 1, w, mc), 0, kDeviceCpol));
-                }
-            }
-#pragma unroll
-            for (int q = 0; q < kBatch; ++q)
-                if (c0 + q < count)
-#pragma unroll
-                    for (int j = 0; j < kMine; ++j)
-#pragma unroll
-                        for (int w = 0; w < NW; ++w) v[j][w] += x[q][j][w];
-        }
-        if (ocol < args.n) {
-#pragma unroll
-            for (int j = 0; j < kMine; ++j) {
-                const int m = m_first + j * kRowStep;
-                if (m < rows) store_out(m, v[j]);
-            }
-        }
+        return fix_count;
     };
+    // The sum of a shared band over its contributors in workgroup order (so the result does not
+    // depend on who sums it), then the epilogue. `own` >= 0: this workgroup's contribution is the
+    // one in `fin` (entry `own` of the list), not yet in memory.
+    auto sum_band = [&](int band, int count, int own) {
+        f32x4 v[NW][FM];
+#pragma unroll
+        for (int w = 0; w < NW; ++w)
+#pragma unroll
+            for (int f = 0; f < FM; ++f) v[w][f] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int c = 0; c < count; ++c) {
+            const int entry = fix_list[c];
+            if (entry == own) {
+#pragma unroll
+                for (int w = 0; w < NW; ++w)
+#pragma unroll
+                    for (int f = 0; f < FM; ++f) v[w][f] += fin[w][f];
+                continue;
+            }
+#pragma unroll
+            for (int w = 0; w < NW; ++w)
+#pragma unroll
+                for (int f = 0; f < FM; ++f)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int m = own_row(f, i) < rows ? own_row(f, i) : rows - 1;
+                        v[w][f][i] += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                                    p_rsrc, part_off(entry >> 1, entry & 1, w, m), 0, kDeviceCpol));
+                    }
+        }
+        store_out(band, v);
+    };
+    // Arrival counters, one per shared band, at the start of the workspace; the workgroup that
+    // sums a band returns its counter to zero for the next call.
+    auto counter = [&](int band) { return args.counters + (band - args.dp_bands); };
 
+    auto nothing = [] {};
     for (int band = blockIdx.x; band < args.dp_bands; band += P) {
-        run_job(band, 0, U, -1);
+        run_job(band, 0, U, nothing);
+        store_out(band, fin);
         lds_barrier();  // the next job's loads overwrite the reduction area; stores need not drain
     }
     if (args.sk_units > 0) {
+        // A workgroup's range meets at most two bands partially: its first job (slot 0) and its
+        // last (slot 1). The first job's partial is written at once and announced after the next
+        // job's prologue (its stores have completed by then, and the wait for them hides behind
+        // that prologue's loads); whether that made this workgroup the band's last contributor is
+        // looked at when the range is done. The last job's band is summed at once if every other
+        // contributor has already announced itself (the usual case: they did so long before),
+        // from this workgroup's registers and their partials; otherwise this workgroup writes and
+        // announces its partial too, and the last to arrive sums.
         int64_t u = sk_start(blockIdx.x);
         const int64_t u_end = sk_start(blockIdx.x + 1);
-        int slot = 0, deferred = -1;
+        int slot = 0, pending = -1, pending_old = -1, announce = -1;
+        __shared__ int arrival;
         while (u < u_end) {
             const int band = args.dp_bands + (int)(u / U);
             const int ga = (int)(u % U);
             const int gb = (int)((int64_t)ga + (u_end - u) < U ? ga + (u_end - u) : U);
             const bool whole = ga == 0 && gb == U;
-            run_job(band, ga, gb, whole ? -1 : slot);
-            lds_barrier();
+            run_job(band, ga, gb, [&] {
+                if (announce >= 0 && tid == 0)
+                    pending_old = __hip_atomic_fetch_add(counter(announce), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                announce = -1;  // once: later jobs of the range announce nothing
+            });
             u += gb - ga;
-            if (!whole) {
-                if (slot == 0 && u < u_end) deferred = band;  // more jobs follow: fix up at the end
-                else finish_band(band);
+            if (whole) {
+                store_out(band, fin);
+            } else if (u < u_end) {
+                write_partial(slot);
+                pending = announce = band;
+            } else {
+                const int count = contributors(band);
+                if (tid == 0)
+                    arrival = __hip_atomic_load(counter(band), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                __syncthreads();
+                if (arrival == count - 1) {
+                    if (tid == 0) __hip_atomic_store(counter(band), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                    sum_band(band, count, (int)blockIdx.x * 2 + slot);
+                } else {
+                    write_partial(slot);
+                    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the partial is in memory
+                    __syncthreads();
+                    if (tid == 0) {
+                        const int old = __hip_atomic_fetch_add(counter(band), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                        if (old == count - 1) __hip_atomic_store(counter(band), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                        arrival = old;
+                    }
+                    __syncthreads();
+                    if (arrival == count - 1) sum_band(band, count, -1);
+                }
             }
+            lds_barrier();
             slot = 1;
         }
-        if (deferred >= 0) finish_band(deferred);
+        if (pending >= 0) {
+            if (tid == 0) arrival = pending_old;
+            __syncthreads();
+            const int count = contributors(pending);
+            if (arrival == count - 1) {
+                if (tid == 0) __hip_atomic_store(counter(pending), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                sum_band(pending, count, -1);
+            }
+        }
     }
 }
 
@@ -774,13 +809,16 @@ static int device_cus() {
     return cache[dev];
 }
 
-// Partials [grid][2][nw][rows][band columns] fp32, then one arrival counter per band.
+// Workspace: a fixed region of arrival counters (one per shared band, zero between calls) at the
+// start, then the partials [grid][2][nw][rows][band columns] fp32. The counters sit at the same
+// place for every shape, kernel variant and row count, so calls of different shapes can share one
+// workspace: a call never writes partials where another call keeps counters.
+constexpr size_t kCounterBytes = 16384;
+constexpr int kMaxSkBands = (int)(kCounterBytes / sizeof(int));
 static size_t sk_partial_bytes(int grid, int64_t rows, bool mlp) {
     return ((size_t)grid * 2 * (mlp ? 2 : 1) * rows * (kMmaCW * 32) * sizeof(float) + 255) / 256 * 256;
 }
-static size_t sk_bytes(int grid, int64_t rows, int bands, bool mlp) {
-    return sk_partial_bytes(grid, rows, mlp) + (size_t)bands * sizeof(int);
-}
+static size_t sk_bytes(int grid, int64_t rows, int, bool mlp) { return kCounterBytes + sk_partial_bytes(grid, rows, mlp); }
 
 MmaPlan plan_mma(int64_t rows, int64_t columns, int64_t groups, bool mlp, size_t workspace_bytes, int64_t unit_elems) {
     MmaPlan p;
@@ -804,7 +842,7 @@ MmaPlan plan_mma(int64_t rows, int64_t columns, int64_t groups, bool mlp, size_t
         // Whole bands per workgroup already balance: no partials.
         p.dp_bands = p.bands;
         p.sk_units = 0;
-    } else if (sk_bytes(grid, rows, p.bands, mlp) > workspace_bytes) {
+    } else if (sk_bytes(grid, rows, p.bands, mlp) > workspace_bytes || p.bands > kMaxSkBands) {
         // No room for partials: every band whole, one workgroup each.
         p.grid = p.bands;
         p.dp_bands = p.bands;
@@ -848,9 +886,9 @@ static void set_io(MmaArgs &args, const MmaPlan &plan, const uint16_t *a, int64_
     args.residual = residual;
     args.rows = rows;
     args.out_dtype = out_dtype;
-    args.partial = plan.sk_units > 0 ? (float *)workspace : nullptr;
+    args.counters = plan.sk_units > 0 ? (int *)workspace : nullptr;
+    args.partial = plan.sk_units > 0 ? (float *)((char *)workspace + kCounterBytes) : nullptr;
     args.partial_bytes = plan.sk_units > 0 ? (uint32_t)sk_partial_bytes(plan.grid, rows, mlp) : 0;
-    args.counters = plan.sk_units > 0 ? (int *)((char *)workspace + args.partial_bytes) : nullptr;
     args.dp_bands = plan.dp_bands;
     args.sk_units = plan.sk_units;
     args.a_bytes = (uint32_t)(((rows - 1) * lda + inner) * 2);

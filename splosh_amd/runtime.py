@@ -136,9 +136,17 @@ class Q4KWeight:
         return self.rows * (self.inner // 256) * 144
 
 
-def _out(a, rows, n, out, out_dtype):
+def _on(stream):
+    """The stream a call's kernels run on (the caller's, else torch's current one)."""
+    return stream if stream is not None else torch.cuda.current_stream()
+
+
+def _out(a, rows, n, out, out_dtype, stream=None):
     if out is None:
-        out = torch.empty((rows, n), dtype=out_dtype, device=a.device)
+        # Allocated on the stream the kernel writes it from, so torch's caching allocator orders
+        # any reuse of the block after that kernel.
+        with torch.cuda.stream(_on(stream)):
+            out = torch.empty((rows, n), dtype=out_dtype, device=a.device)
     return out
 
 
@@ -168,9 +176,12 @@ def workspace_bytes(rows, columns, inner):
     return _lib.lib().splosh_workspace_bytes(rows, columns, inner)
 
 
-def _workspace(workspace, rows, n, inner, device):
+def _workspace(workspace, rows, n, inner, device, stream=None):
     """The split-K scratch of the kernels: the caller's tensor (an empty one: none), or a fresh one
-    from torch's stream-ordered allocator sized by splosh_workspace_bytes."""
+    from torch's stream-ordered allocator sized by splosh_workspace_bytes. A fresh one is
+    zero-filled and allocated on the stream the kernel runs on: the fill is ordered before the
+    kernel, and once the tensor is dropped the allocator hands the block out again only to work
+    ordered after that kernel on the same stream."""
     if workspace is not None and workspace.numel() == 0:
         return None, 0
     if workspace is not None:
@@ -178,7 +189,8 @@ def _workspace(workspace, rows, n, inner, device):
     need = _lib.lib().splosh_workspace_bytes(rows, n, inner)
     if need == 0:
         return None, 0
-    buf = torch.zeros(need, dtype=torch.uint8, device=device)  # zero-filled before first use
+    with torch.cuda.stream(_on(stream)):
+        buf = torch.zeros(need, dtype=torch.uint8, device=device)
     return _ptr(buf), need
 
 
@@ -193,7 +205,7 @@ def gemm(w, a, out=None, residual=None, out_dtype=torch.bfloat16, kernel=AUTO, r
         raise SploshError(13, "activations must be bf16")
     if a.stride(-1) != 1:
         raise SploshError(1, "activation rows must be contiguous")
-    out = _out(a, rows, w.rows, out, out_dtype)
+    out = _out(a, rows, w.rows, out, out_dtype, stream)
     _require(a, ((rows - 1) * a.stride(0) + w.inner) * 2, "a")
     _require(out, ((rows - 1) * out.stride(0) + w.rows) * out.element_size(), "output")
     if residual is not None:
@@ -205,7 +217,7 @@ def gemm(w, a, out=None, residual=None, out_dtype=torch.bfloat16, kernel=AUTO, r
                                                rows, _stream(stream)))
         return out
     wc = w.c()
-    ws, ws_bytes = _workspace(workspace, rows, w.rows, w.inner, a.device)
+    ws, ws_bytes = _workspace(workspace, rows, w.rows, w.inner, a.device, stream)
     if isinstance(w, Q4Weight):
         st = _lib.lib().splosh_q4_gemm(ctypes.byref(wc), _ptr(a), a.stride(0), _ptr(out), out.stride(0),
                                        _dtype_code(out.dtype), _ptr(residual), rows, kernel, ws, ws_bytes,
@@ -224,11 +236,11 @@ def mlp_in(gate, up, a, out=None, out_dtype=torch.bfloat16, kernel=AUTO, rows=No
     rows = a.shape[0] if rows is None else rows
     if a.dtype != torch.bfloat16 or a.stride(-1) != 1:
         raise SploshError(13, "activations must be contiguous bf16 rows")
-    out = _out(a, rows, gate.rows, out, out_dtype)
+    out = _out(a, rows, gate.rows, out, out_dtype, stream)
     _require(a, ((rows - 1) * a.stride(0) + gate.inner) * 2, "a")
     _require(out, ((rows - 1) * out.stride(0) + gate.rows) * out.element_size(), "output")
     gc, uc = gate.c(), up.c()
-    ws, ws_bytes = _workspace(workspace, rows, gate.rows, gate.inner, a.device)
+    ws, ws_bytes = _workspace(workspace, rows, gate.rows, gate.inner, a.device, stream)
     st = _lib.lib().splosh_q4_mlp_in(ctypes.byref(gc), ctypes.byref(uc), _ptr(a), a.stride(0), _ptr(out),
                                      out.stride(0), _dtype_code(out.dtype), rows, kernel, ws, ws_bytes,
                                      _stream(stream))

@@ -1,0 +1,165 @@
+"""Static check of the hand-counted vmcnt waits in mma.hip, on the AMD assembly of this build.
+
+The M <= 64 kernel stages activation chunks and sidecars with direct-to-LDS buffer loads, which
+the compiler does not track: the only thing that makes a stage's data visible in LDS before the
+barrier that hands it to the other waves is an `s_waitcnt vmcnt(N)` whose N the source computes
+by hand (kMidWait = 2 kWLoads + kStageLoads in the main loop; 2 kWLoads + 2 kStageLoads in the
+prologue). N is only right if the compiler keeps the loads in the issue order the source assumes.
+vmcnt counts down in issue order, and loads into LDS are never reordered among themselves (they
+all may write LDS), so the condition is: at every barrier, the loads that may still be
+outstanding (the N youngest before the last vmcnt wait, plus any issued after it) include at most
+N - 2 kWLoads loads into LDS -- the stages the design leaves in flight. A compiler change that
+sinks a stage's load below the weight loads it is counted against fails this test.
+
+CPU only: hipcc cross-compiles gfx950 to assembly here (about 10 s)."""
+import re
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HIPCC = "/opt/rocm/bin/hipcc"
+
+VMEM = re.compile(r"^\s*(buffer_load|global_load|buffer_store|global_store|buffer_atomic|global_atomic)")
+
+
+def _kernels(asm):
+    lines = asm.split("\n")
+    starts = [i for i, l in enumerate(lines) if re.match(r"^_ZN6splosh10mma_kernel\S*:", l)]
+    for j, i in enumerate(starts):
+        end = next((k for k in range(i, len(lines)) if lines[k].strip().startswith("s_endpgm")), len(lines))
+        code = []
+        for l in lines[i + 1:end + 1]:
+            m = re.search(r"; splosh-lds-outstanding (\d+)", l)
+            code.append(f"#MARK {m.group(1)}" if m else l.split(";")[0].strip())
+        yield lines[i].split(":")[0], code
+
+
+def _weight_loads(name):
+    """kWLoads of the instantiation, from its mangled template arguments."""
+    m = re.search(r"Q4FormatILi(\d)ELb(\d)", name)
+    if m:
+        nw, tiled = int(m.group(1)), m.group(2) == "1"
+        return nw if tiled else 3 * nw
+    m = re.search(r"Q5FormatILi\d+ELi\d+ELi\d+ELb(\d)", name)
+    assert m, name
+    return 2 if m.group(1) == "1" else 1
+
+
+def _stage_loads(name):
+    """Loads into LDS of one stage: the activation chunk (FM x 32 rows x KW x 8 pieces over CW x
+    KW waves) plus one sidecar/meta load when those are staged (tiled q4, Q4_K/Q5_K)."""
+    m = re.search(r"EELi(\d)ELi(\d)ELi(\d)ELi(\d)EEEvNS_7MmaArgsE", name)
+    assert m, name
+    fm, cw, kw = int(m.group(1)), int(m.group(2)), int(m.group(3))
+    a_per = fm * 32 * kw * 8 // (cw * kw * 64)
+    staged = bool(re.search(r"Q4FormatILi\dELb1", name)) or "Q5Format" in name
+    return a_per + (1 if staged else 0)
+
+
+def _cfg(code):
+    """Basic blocks of a function: instruction lists and predecessor lists."""
+    blocks, labels, cur = [], {}, []
+    for ins in code:
+        if not ins:
+            continue
+        if re.match(r"^\.LBB\d+_\d+:", ins):
+            if cur:
+                blocks.append(cur)
+            cur = []
+            labels[ins[:-1]] = len(blocks)
+            continue
+        cur.append(ins)
+        if ins.startswith(("s_branch", "s_cbranch", "s_endpgm", "s_setpc")):
+            blocks.append(cur)
+            cur = []
+    if cur:
+        blocks.append(cur)
+    # Labels point at the block that starts after them.
+    preds = [[] for _ in blocks]
+    for b, ins_list in enumerate(blocks):
+        last = ins_list[-1] if ins_list else ""
+        tgt = re.match(r"^s_c?branch\S*\s+(\.LBB\d+_\d+)", last)
+        if tgt and tgt.group(1) in labels:
+            preds[labels[tgt.group(1)]].append(b)
+        if not last.startswith(("s_branch", "s_endpgm", "s_setpc")) and b + 1 < len(blocks):
+            preds[b + 1].append(b)
+    return blocks, preds
+
+
+def _windows(blocks, preds, b, idx, want, seen=()):
+    """Every possible sequence of the `want` youngest VMEM instructions issued before instruction
+    idx of block b (youngest first), following predecessors; shorter at the function entry."""
+    got = []
+    for ins in reversed(blocks[b][:idx]):
+        if len(got) == want:
+            return [got]
+        if VMEM.match(ins):
+            got.append(ins)
+    if len(got) == want or not preds[b]:
+        return [got]
+    out = []
+    for p in preds[b]:
+        key = (p, want - len(got))
+        if key in seen:  # a cycle without enough loads: treat as the entry
+            out.append(got)
+            continue
+        for rest in _windows(blocks, preds, p, len(blocks[p]), want - len(got), seen + (key,)):
+            out.append(got + rest)
+    return out
+
+
+def _check_function(name, code):
+    stage = _stage_loads(name)
+    blocks, preds = _cfg(code)
+    checked = 0
+    for b, ins_list in enumerate(blocks):
+        for i, ins in enumerate(ins_list):
+            if not ins.startswith("s_barrier"):
+                continue
+            # The design's statement, if any: "; splosh-lds-outstanding K" (comments are stripped
+            # from `code`, so look in the raw marker list kept beside it).
+            allowed = 0
+            for k in range(i - 1, max(i - 4, -1), -1):
+                m = re.match(r"^#MARK (\d+)$", ins_list[k])
+                if m:
+                    allowed = int(m.group(1))
+                    break
+            # The last vmcnt wait before this barrier in the block, and VMEM issued since.
+            after, n, wait_at = 0, None, None
+            for k in range(i - 1, -1, -1):
+                m = re.search(r"vmcnt\((\d+)\)", ins_list[k]) if ins_list[k].startswith("s_waitcnt") else None
+                if m:
+                    n, wait_at = int(m.group(1)), k
+                    break
+                if VMEM.match(ins_list[k]):
+                    after += 1
+            if n is None:
+                continue
+            for win in _windows(blocks, preds, b, wait_at, n):
+                lds = sum(1 for x in win if x.startswith("buffer_load") and x.endswith(" lds")) + after
+                assert lds <= allowed, (
+                    f"{name}: a barrier's vmcnt({n}) leaves {lds} loads into LDS outstanding, the "
+                    f"design allows {allowed}: {win}")
+            if allowed:
+                assert allowed % stage == 0, (name, allowed, stage)
+                checked += 1
+    return checked
+
+
+@pytest.mark.skipif(not Path(HIPCC).exists(), reason="needs hipcc")
+def test_mma_stage_waits_cover_their_loads(tmp_path):
+    out = tmp_path / "mma.s"
+    cmd = [HIPCC, "-O3", "-std=c++17", "--offload-arch=gfx950", "-Xclang", "-target-feature", "-Xclang",
+           "-packed-fp32-ops", f"-I{ROOT / 'include'}", "--cuda-device-only", "-S",
+           str(ROOT / "splosh_amd" / "csrc" / "mma.hip"), "-o", str(out)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    assert res.returncode == 0, res.stderr[-2000:]
+    kernels = list(_kernels(out.read_text()))
+    assert len(kernels) >= 8
+    for name, code in kernels:
+        # Every instantiation has the prologue barrier and at least three mid-step barriers whose
+        # waits keep loads in flight.
+        assert _check_function(name, code) >= 4, name
