@@ -7,6 +7,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
+#include <mutex>
 #include <string>
 
 #include "../../include/splosh_q4.h"
@@ -218,6 +219,45 @@ int check_q5k_weight(const splosh_q5k_weight *w, bool fifth = true) {
     return SPLOSH_OK;
 }
 
+// ---- the allocation-free entry point's scratch ------------------------------------------------
+//
+// splosh_q4_gemm_noalloc runs the same kernels as splosh_q4_gemm with this file-scope device array
+// as its workspace: the split-K arrival counters (first 16 KiB, as in any workspace) and the
+// partials of the M <= 64 MFMA kernel on one weight (grid x 2 slots x 64 rows x 64 columns fp32 =
+// 8 MiB at the 256 workgroups of an MI355X). Every GPU the library runs on holds its own copy
+// until the process ends. In host code `scratch` names a host-side stand-in, never the device
+// memory: its address on each device comes from hipGetSymbolAddress, once per device.
+constexpr size_t kScratchBytes = (size_t)16384 + ((size_t)8 << 20);
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void *g_scratch_ptr[kMaxDevices] = {nullptr};
+
+// The scratch array's device address on the current device (looked up on the first call there).
+int scratch_on_current_device(void **out) {
+    int dev = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return fail(SPLOSH_ERR_HIP, std::string("hipGetDevice: ") + hipGetErrorString(err));
+    if (dev < 0 || dev >= kMaxDevices) return fail(SPLOSH_ERR_UNSUPPORTED, "device index out of range");
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[dev]) {
+        void *ptr = nullptr;
+        err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (err != hipSuccess || !ptr)
+            return fail(SPLOSH_ERR_HIP, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(err));
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return SPLOSH_OK;
+}
+
+// Zeroes `words` 32-bit words (a fill kernel rather than hipMemsetAsync, so that a caller may
+// capture the call in a HIP graph).
+__global__ void zero_words_kernel(uint32_t *p, int words) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < words; i += gridDim.x * blockDim.x) p[i] = 0u;
+}
+
 }  // namespace
 
 extern "C" {
@@ -374,6 +414,30 @@ int splosh_q4_gemm(const splosh_q4_weight *w, const uint16_t *a, int64_t lda, vo
                    hipStream_t stream) {
     return q4_gemm_impl(w, nullptr, a, lda, out, ldc, out_dtype, residual, rows, kernel, workspace, workspace_bytes,
                         stream);
+}
+
+// splosh_q4_gemm with the library's static device scratch as its workspace: no allocation.
+int splosh_q4_gemm_noalloc(const splosh_q4_weight *w, const uint16_t *a, int64_t lda, void *out, int64_t ldc,
+                           int out_dtype, const void *residual, int64_t rows, int kernel, hipStream_t stream) {
+    int st = check_q4_weight(w, "weight");
+    if (st) return st;
+    if ((st = check_io(a, lda, out, ldc, out_dtype, rows, w->rows, w->inner))) return st;
+    // The scratch the M <= 64 kernel would split K with; other kernels run unsplit when the
+    // scratch cannot hold their partials.
+    const size_t need = rows <= 64 && w->inner % kGroupSize == 0
+                            ? splosh::mma_workspace_bytes(rows, w->rows, w->inner / kGroupSize, false)
+                            : 0;
+    if (need > kScratchBytes)
+        return fail(SPLOSH_ERR_WORKSPACE_TOO_SMALL,
+                    "the call needs " + std::to_string(need) + " bytes of scratch; the static scratch holds " +
+                        std::to_string(kScratchBytes));
+    void *ptr = nullptr;
+    if ((st = scratch_on_current_device(&ptr))) return st;
+    // The arrival counters must start at zero: every call returns them to zero, and this call
+    // clears them first anyway (a call that failed half-way may have left them set).
+    hipLaunchKernelGGL(zero_words_kernel, dim3(4), dim3(256), 0, stream, (uint32_t *)ptr, 16384 / 4);
+    if ((st = hip_status(hipGetLastError(), "scratch clear launch"))) return st;
+    return q4_gemm_impl(w, nullptr, a, lda, out, ldc, out_dtype, residual, rows, kernel, ptr, kScratchBytes, stream);
 }
 
 int splosh_q4_mlp_in(const splosh_q4_weight *gate, const splosh_q4_weight *up, const uint16_t *a, int64_t lda,
