@@ -64,25 +64,19 @@ typedef enum splosh_dtype { SPLOSH_F32 = 0, SPLOSH_BF16 = 1 } splosh_dtype;
 /* Kernel choice (the reference selects kernels through SPLOSH_* environment variables,
  * Runtime/Engine.swift:380-440; here the caller names one, or AUTO picks by rows). */
 typedef enum splosh_kernel {
-    SPLOSH_KERNEL_AUTO = 0,     /* rows <= 2: STREAM; 3..64: DEQUANT (VERIFY for tiled weights with
-                                   SPLOSH_VERIFY=1 in the environment); more: PREFILL for one tiled
+    SPLOSH_KERNEL_AUTO = 0,     /* rows <= 2: STREAM; 3..64: DEQUANT; more: PREFILL for one tiled
                                    weight with lda % 8 == 0 and ldc % 4 == 0, else TILE; SCALAR for
                                    operands no other kernel takes */
     SPLOSH_KERNEL_STREAM = 1,   /* weight streaming on raw codes: the every-CU decode kernel for
-                                   1-2 rows of tiled weights (SPLOSH_DECODE=0 in the environment
-                                   opts out), the lane-per-row kernel for row-major ones, raw-code
-                                   MFMA kernels above */
+                                   1-2 rows of tiled weights, the lane-per-row kernel for row-major
+                                   ones, the raw-code MFMA kernel for more rows */
     SPLOSH_KERNEL_DEQUANT = 2,  /* rows <= 64: stream-K MFMA kernel on weights dequantized to bf16 in
                                    registers; uses the workspace for split bands when given one */
     SPLOSH_KERNEL_TILE = 3,     /* any rows: LDS-tiled dequant-to-bf16 MFMA GEMM (prefill) */
     SPLOSH_KERNEL_SCALAR = 4,   /* one thread per output (gemm_q4.metal semantics) */
-    SPLOSH_KERNEL_PREFILL = 5,  /* one TILED128 weight (not mlp_in): 256 x 256 output tiles, one
+    SPLOSH_KERNEL_PREFILL = 5   /* one TILED128 weight (not mlp_in): 256 x 256 output tiles, one
                                    wave per SIMD, weights dequantized in registers; uses the
                                    workspace to split the last round of tiles over all CUs */
-    SPLOSH_KERNEL_VERIFY = 6    /* TILED128 weights, 2 < rows <= 64, inner % 128 == 0: groups of
-                                   16-column tiles, eight waves splitting K, weights dequantized
-                                   in registers; tiles past a whole number of groups a workgroup
-                                   are split along K through the workspace */
 } splosh_kernel;
 
 /* Q4BufferLayout (Quant/Q4BufferLayout.swift:29-79). */

@@ -26,7 +26,7 @@ STATUS_NAMES = {
 ROWS_BY_K, K_BY_COLUMNS = 0, 1
 ROW_MAJOR, TILED128 = 0, 1
 F32, BF16 = 0, 1
-KERNEL_AUTO, KERNEL_STREAM, KERNEL_DEQUANT, KERNEL_TILE, KERNEL_SCALAR, KERNEL_PREFILL, KERNEL_VERIFY = 0, 1, 2, 3, 4, 5, 6
+KERNEL_AUTO, KERNEL_STREAM, KERNEL_DEQUANT, KERNEL_TILE, KERNEL_SCALAR, KERNEL_PREFILL = 0, 1, 2, 3, 4, 5
 
 
 class SploshLibraryError(RuntimeError):

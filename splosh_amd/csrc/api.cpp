@@ -106,24 +106,13 @@ int q4_gemm_impl(const splosh_q4_weight *w, const splosh_q4_weight *up, const ui
     const bool prefill_ok = wide16 && !up && w->order == SPLOSH_Q4_TILED128 && aligned(out, 16) &&
                             (!residual || aligned(residual, 16)) &&
                             splosh::prefill_fits(rows, w->rows, w->inner, lda, ldc);
-    const char *verify_env = getenv("SPLOSH_VERIFY");
-    splosh::VerifyPlan vplan{};
-    bool verify_ok = wide16 && splosh::verify_fits(rows, w->rows, w->inner, w->order, lda);
-    if (verify_ok) {
-        vplan = splosh::plan_verify(rows, w->rows, w->inner / kGroupSize, up != nullptr);
-        const size_t need = splosh::verify_workspace_bytes(vplan);
-        verify_ok = need == 0 || (workspace && workspace_bytes >= need);
-    }
-    const char *decode_env = getenv("SPLOSH_DECODE");
-    const bool decode_ok = wide16 && !(decode_env && atoi(decode_env) == 0) &&
-                           splosh::decode_fits(rows, w->rows, w->inner, w->order);
+    const bool decode_ok = wide16 && splosh::decode_fits(rows, w->rows, w->inner, w->order);
     int choice = kernel;
     if (choice == SPLOSH_KERNEL_AUTO) {
         if (!eligible) choice = SPLOSH_KERNEL_SCALAR;
         else if (decode_ok) choice = SPLOSH_KERNEL_STREAM;
         else if (wide16 && splosh::lanes_fit(rows, w->rows, w->inner, w->row_stride_words, up != nullptr))
             choice = SPLOSH_KERNEL_STREAM;
-        else if (verify_ok && verify_env && atoi(verify_env) == 1) choice = SPLOSH_KERNEL_VERIFY;
         else if (mma_ok) choice = SPLOSH_KERNEL_DEQUANT;
         else if (prefill_ok) choice = SPLOSH_KERNEL_PREFILL;
         else if (tile_ok) choice = SPLOSH_KERNEL_TILE;
@@ -167,18 +156,6 @@ int q4_gemm_impl(const splosh_q4_weight *w, const splosh_q4_weight *up, const ui
                                                           stream),
                                   "q4 lanes launch");
             }
-            if (wide16 && splosh::gemv_fits(rows, w->inner)) {
-                const splosh::StreamPlan plan = splosh::plan_gemv(rows, w->rows, w->inner / kGroupSize, up != nullptr);
-                return hip_status(splosh::launch_q4_gemv(plan, *w, up, a, lda, out, ldc, out_dtype, residual, rows,
-                                                         stream),
-                                  "q4 gemv launch");
-            }
-            if (rows <= 32 && wide16) {
-                const splosh::StreamPlan plan = splosh::plan_stream32(rows, w->rows, w->inner / kGroupSize, up != nullptr);
-                return hip_status(splosh::launch_q4_stream32(plan, *w, up, a, lda, out, ldc, out_dtype, residual, rows,
-                                                             stream),
-                                  "q4 stream32 launch");
-            }
             const splosh::StreamPlan plan = splosh::plan_stream(rows, w->rows, w->inner / kGroupSize, up != nullptr, 4);
             if (plan.row_chunks > 65535) return fail(SPLOSH_ERR_UNSUPPORTED, "too many rows for one launch");
             return hip_status(splosh::launch_q4_stream(plan, *w, up, a, lda, out, ldc, out_dtype, residual, rows, stream),
@@ -188,14 +165,6 @@ int q4_gemm_impl(const splosh_q4_weight *w, const splosh_q4_weight *up, const ui
             if (rows > 65535) return fail(SPLOSH_ERR_UNSUPPORTED, "scalar kernel takes at most 65535 rows");
             return hip_status(splosh::launch_q4_gemm_scalar(*w, up, a, lda, out, ldc, out_dtype, residual, rows, stream),
                               "q4 scalar launch");
-        case SPLOSH_KERNEL_VERIFY:
-            if (!verify_ok)
-                return fail(SPLOSH_ERR_UNSUPPORTED,
-                            "verify kernel needs a TILED128 weight, 2 < rows <= 64, inner % 128 == 0, lda % 8 == 0, "
-                            "aligned operands and the workspace splosh_workspace_bytes() gives");
-            return hip_status(splosh::launch_q4_verify(vplan, *w, up, a, lda, out, ldc, out_dtype, residual, rows,
-                                                       workspace, stream),
-                              "q4 verify launch");
         case SPLOSH_KERNEL_DEQUANT: {
             if (!mma_ok) return fail(SPLOSH_ERR_UNSUPPORTED, "dequant kernel needs rows <= 64 and aligned operands");
             const splosh::MmaPlan plan =
@@ -384,13 +353,7 @@ size_t splosh_workspace_bytes(int64_t rows, int64_t columns, int64_t inner) {
     const size_t tile = splosh::tile_workspace_bytes(rows, columns, groups, true);
     const size_t mma = rows <= 64 ? splosh::mma_workspace_bytes(rows, columns, groups, true) : 0;
     const size_t prefill = rows > 64 && columns % 128 == 0 ? splosh::prefill_workspace_bytes(rows, columns, groups) : 0;
-    size_t need = tile > mma ? tile : mma;
-    if (rows > 2 && rows <= 64 && columns % 128 == 0 && inner % 128 == 0) {
-        for (bool mlp : {false, true}) {
-            const size_t v = splosh::verify_workspace_bytes(splosh::plan_verify(rows, columns, groups, mlp));
-            need = need > v ? need : v;
-        }
-    }
+    const size_t need = tile > mma ? tile : mma;
     return need > prefill ? need : prefill;
 }
 
@@ -499,9 +462,7 @@ static int gguf_gemm(const splosh_q5k_weight *w_in, bool fifth, const uint16_t *
     const bool eligible = lda % 4 == 0 && aligned(a, 8) && aligned(w->plane0, 16) && (!fifth || aligned(w->plane1, 4)) &&
                           aligned(w->meta, 16);
     const bool mma_ok = eligible && lda % 8 == 0 && aligned(a, 16) && splosh::q5k_mma_fits(rows, w->rows, w->inner, lda);
-    const char *decode_env = getenv("SPLOSH_DECODE");
-    const bool decode_ok = eligible && aligned(a, 16) && !(decode_env && atoi(decode_env) == 0) &&
-                           splosh::q5k_decode_fits(rows, w->rows, w->inner);
+    const bool decode_ok = eligible && aligned(a, 16) && splosh::q5k_decode_fits(rows, w->rows, w->inner);
     int choice = kernel;
     if (kernel == SPLOSH_KERNEL_AUTO) {
         if (!eligible) choice = SPLOSH_KERNEL_SCALAR;

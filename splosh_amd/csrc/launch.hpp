@@ -45,19 +45,6 @@ hipError_t launch_q4_stream(const StreamPlan &plan, const splosh_q4_weight &w, c
                             const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype,
                             const void *residual, int64_t rows, hipStream_t stream);
 
-// The 32x32x16 MFMA streaming kernel for rows <= 32 (stream32.hip).
-StreamPlan plan_stream32(int64_t rows, int64_t columns, int64_t groups, bool mlp);
-hipError_t launch_q4_stream32(const StreamPlan &plan, const splosh_q4_weight &w, const splosh_q4_weight *up,
-                              const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype,
-                              const void *residual, int64_t rows, hipStream_t stream);
-
-// The decode kernel for rows <= 8 with activations staged in LDS (gemv.hip).
-bool gemv_fits(int64_t rows, int64_t inner);
-StreamPlan plan_gemv(int64_t rows, int64_t columns, int64_t groups, bool mlp);
-hipError_t launch_q4_gemv(const StreamPlan &plan, const splosh_q4_weight &w, const splosh_q4_weight *up,
-                          const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype,
-                          const void *residual, int64_t rows, hipStream_t stream);
-
 // The lane-per-row decode kernel for one or two rows (lanes.hip).
 bool lanes_fit(int64_t rows, int64_t columns, int64_t inner, int64_t stride_words, bool mlp);
 StreamPlan plan_lanes(int64_t rows, int64_t columns, int64_t groups, bool mlp);
@@ -90,22 +77,6 @@ size_t mma_workspace_bytes(int64_t rows, int64_t columns, int64_t groups, bool m
 hipError_t launch_q4_mma(const MmaPlan &plan, const splosh_q4_weight &w, const splosh_q4_weight *up,
                          const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype, const void *residual,
                          int64_t rows, void *workspace, hipStream_t stream);
-
-// The M <= 64 verify kernel for tiled q4 weights (verify.hip): groups of 16-column tiles over
-// K, eight waves splitting K; tiles past a whole number of groups a workgroup are split along K
-// and need verify_workspace_bytes() of workspace.
-struct VerifyPlan {
-    int n1, s1;        // phase 1: groups of T tiles, pieces of K each
-    int n2, s2;        // phase 2: single tiles, pieces of K each
-    int units, grid;
-    size_t partial_floats1, partial_floats2;
-};
-bool verify_fits(int64_t rows, int64_t columns, int64_t inner, int order, int64_t lda);
-VerifyPlan plan_verify(int64_t rows, int64_t columns, int64_t groups, bool mlp);
-size_t verify_workspace_bytes(const VerifyPlan &plan);
-hipError_t launch_q4_verify(const VerifyPlan &plan, const splosh_q4_weight &w, const splosh_q4_weight *up,
-                            const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype,
-                            const void *residual, int64_t rows, void *workspace, hipStream_t stream);
 
 // GGUF Q8_0 / Q6_K / IQ4_NL / IQ4_XS in native blocks (gguf_native.hip).
 int gguf_native_block(int type, int *elems, int *bytes);

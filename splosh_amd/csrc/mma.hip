@@ -831,7 +831,9 @@ MmaPlan plan_mma(int64_t rows, int64_t columns, int64_t groups, bool mlp, size_t
     const int64_t min_units = (1280 + unit_elems - 1) / unit_elems;
     const int64_t want = ((int64_t)p.bands * groups + min_units - 1) / min_units;
     if (want < grid) grid = (int)(want > 0 ? want : 1);
-    if (const char *env = getenv("SPLOSH_MMA_GRID")) grid = atoi(env) > 0 ? atoi(env) : grid;
+    // A development override of the grid, read from the environment once per process.
+    static const int grid_override = [] { const char *e = getenv("SPLOSH_MMA_GRID"); return e ? atoi(e) : 0; }();
+    if (grid_override > 0) grid = grid_override;
     grid = grid < kMmaMaxGrid ? grid : kMmaMaxGrid;  // the fix-up's contributor list
     p.grid = grid;
     // Every band's units go into one stream, cut into `grid` equal contiguous ranges: a band is

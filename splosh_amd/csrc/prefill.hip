@@ -452,7 +452,9 @@ static int prefill_grid() {
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
         cus = 256;
-    if (const char *env = getenv("SPLOSH_PREFILL_GRID")) cus = atoi(env) > 0 ? atoi(env) : cus;
+    // A development override of the grid, read from the environment once per process.
+    static const int grid_override = [] { const char *e = getenv("SPLOSH_PREFILL_GRID"); return e ? atoi(e) : 0; }();
+    if (grid_override > 0) cus = grid_override;
     return cus < kPFinishMax ? cus : kPFinishMax;
 }
 

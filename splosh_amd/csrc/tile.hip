@@ -275,7 +275,9 @@ static TileShape tile_shape(int kind) {
 
 static int tile_kind(int64_t rows, bool mlp) {
     int kind = rows <= 64 ? 0 : (rows >= 1024 && !mlp ? 1 : 2);
-    if (const char *env = getenv("SPLOSH_TILE_KIND")) kind = atoi(env);
+    // A development override of the tile shape, read from the environment once per process.
+    static const int kind_override = [] { const char *e = getenv("SPLOSH_TILE_KIND"); return e ? atoi(e) : -1; }();
+    if (kind_override >= 0) kind = kind_override;
     if (mlp && kind == 1) kind = 2;
     return kind;
 }
@@ -296,7 +298,8 @@ TilePlan plan_tile(int64_t rows, int64_t columns, int64_t groups, bool mlp, size
     int splits = 1;
     const int64_t blocks = (int64_t)p.grid_m * p.grid_n;
     while (splits < 8 && blocks * splits < 256 && groups / (splits * 2) >= 8) splits *= 2;
-    if (const char *env = getenv("SPLOSH_TILE_SPLITS")) splits = atoi(env);
+    static const int splits_override = [] { const char *e = getenv("SPLOSH_TILE_SPLITS"); return e ? atoi(e) : 0; }();
+    if (splits_override > 0) splits = splits_override;
     const size_t need = (size_t)splits * (mlp ? 2 : 1) * rows * columns * sizeof(float);
     if (splits > 1 && need > workspace_bytes) splits = 1;
     p.splits = splits;

@@ -25,7 +25,6 @@ DEQUANT = _lib.KERNEL_DEQUANT
 TILE = _lib.KERNEL_TILE
 SCALAR = _lib.KERNEL_SCALAR
 PREFILL = _lib.KERNEL_PREFILL
-VERIFY = _lib.KERNEL_VERIFY
 ROW_MAJOR = _lib.ROW_MAJOR
 TILED128 = _lib.TILED128
 
