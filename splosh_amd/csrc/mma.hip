@@ -351,7 +351,7 @@ struct MmaShape {
     static constexpr size_t kRedBytes = (size_t)KW * CW * kAcc * 64 * sizeof(float);
     static constexpr size_t kABytes = (size_t)kNB * (kABuf + kSBuf);
     static constexpr size_t kLds = kRedBytes > kABytes ? kRedBytes : kABytes;
-    static_assert(D == 3, "the pipeline below is written for weights three steps ahead");
+    static_assert(D >= 3, "the pipeline below keeps weights at least three steps ahead");
 };
 
 // Work split. The N columns form `bands` bands of CW * 32. Bands [0, dp_bands) are computed whole
@@ -490,7 +490,10 @@ mma_kernel(MmaArgs args) {
         load_a(2, 2);
         load_side(3, 2);
         __builtin_amdgcn_sched_barrier(0);
-        wait_vmcnt<2 * kWLoads + 2 * kStageLoads>();  // stage -1, stage 0 and the weights of step 0
+#pragma unroll
+        for (int j = 3; j < D; ++j) load_w(j, j);
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vmcnt<(D - 1) * kWLoads + 2 * kStageLoads>();  // stage -1, stage 0 and the weights of step 0
         lds_barrier_staged<2 * kStageLoads>();         // stages 1 and 2 may be in flight
         after_prologue();
         dequant(0, 3, T > 0 && fmt.active(0));
@@ -560,19 +563,29 @@ mma_kernel(MmaArgs args) {
                 abuf = nbuf(abuf);
             }
         }
-        // The last three steps issue no loads (every stage they read was issued already). Steps
-        // past T (at most the last two; T is uniform over the workgroup) are skipped.
+        // The last D steps load no weights (every step's were issued already) and, but for D - 3 of
+        // them, no stages; they wait for everything. Steps past T (at most D - 1; T is uniform over
+        // the workgroup) are skipped.
 #pragma unroll
         for (int d = 0; d < D; ++d) {
             const int t = Tp - D + d;
             if (t >= T) break;
+            const int sbuf = (abuf + 3) & 3;  // stage t + 3
             step(t, d, abuf,
                  [&] {
                      wait_vmcnt<0>();
                      lds_barrier();
-                     if (d < 2) read_af(af_pre, nbuf(abuf), 0);
+                     if (d < D - 1) read_af(af_pre, nbuf(abuf), 0);
                  },
-                 [&](int) {});
+                 [&](int i) {
+                     if (d + 3 < D) {
+                         if (i == 2) {
+                             load_a_part(t + 3, sbuf, 0, kAHalf);
+                             load_side(t + 4, sbuf);
+                         }
+                         if (i == 3) load_a_part(t + 3, sbuf, kAHalf, S::kAPer);
+                     }
+                 });
             abuf = nbuf(abuf);
         }
         wait_vmcnt<0>();  // nothing is in flight any more (the last steps waited); stated for every path
@@ -730,10 +743,19 @@ mma_kernel(MmaArgs args) {
             const int ga = (int)(u % U);
             const int gb = (int)((int64_t)ga + (u_end - u) < U ? ga + (u_end - u) : U);
             const bool whole = ga == 0 && gb == U;
+            const bool last_partial = !whole && u + (gb - ga) >= u_end;
+            int count = 0, early = -1;
             run_job(band, ga, gb, [&] {
                 if (announce >= 0 && tid == 0)
                     pending_old = __hip_atomic_fetch_add(counter(announce), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
                 announce = -1;  // once: later jobs of the range announce nothing
+                // The last job's band: its contributors, and how many have announced so far (read
+                // now, so that the round trip hides behind the job; once count - 1 have announced,
+                // the count stays there until this workgroup sums).
+                if (last_partial) {
+                    count = contributors(band);
+                    if (tid == 0) early = __hip_atomic_load(counter(band), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                }
             });
             u += gb - ga;
             if (whole) {
@@ -742,9 +764,9 @@ mma_kernel(MmaArgs args) {
                 write_partial(slot);
                 pending = announce = band;
             } else {
-                const int count = contributors(band);
                 if (tid == 0)
-                    arrival = __hip_atomic_load(counter(band), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                    arrival = early == count - 1 ? early
+                                                 : __hip_atomic_load(counter(band), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
                 __syncthreads();
                 if (arrival == count - 1) {
                     if (tid == 0) __hip_atomic_store(counter(band), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
