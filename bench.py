@@ -6,7 +6,7 @@ projection (two K=5120 -> N=17408 weights sharing one activation read, out = sil
 by the down projection (K=17408 -> N=5120) on that output. One "step" is that pair of launches.
 
     python bench.py [--steps K] [--warmup W]
-                    [--workload verify64|decode1|q5k1|q5k16|q5k64|q4k1|q4k64|q6k1|q80_1|iq4nl1|iq4xs1|prefill2048|layerset|lmhead1|lmhead64|operand64]
+                    [--workload verify64|decode1|q5k1|q5k16|q5k64|q4k1|q4k64|q6k1|q80_1|iq4nl1|iq4xs1|q3k1|iq3s1|prefill2048|layerset|lmhead1|lmhead64|operand64]
 
 Inputs are synthetic (seeded, on the device): code words uniform random, scale = bf16(|N(0,0.02)|),
 bias = bf16(N(0,0.01)), activations bf16(N(0,1)). Several copies of the weight set are rotated so
@@ -253,7 +253,8 @@ def build_workload(name, rt, torch, gen, kernel):
                "format": f"gguf {'q5_k' if fifth else 'q4_k'} planes",
                "weight_copies": ncopy}
         return launches, b, 2 * m * n * k, {"q5k": b}, cfg, {"q5k": 2 * m * n * k}
-    native_types = {"q80_": (8, "Q8_0"), "q6k": (14, "Q6_K"), "iq4nl": (20, "IQ4_NL"), "iq4xs": (23, "IQ4_XS")}
+    native_types = {"q80_": (8, "Q8_0"), "q6k": (14, "Q6_K"), "iq4nl": (20, "IQ4_NL"), "iq4xs": (23, "IQ4_XS"),
+                    "q3k": (11, "Q3_K"), "iq3s": (21, "IQ3_S")}
     for prefix, (gtype, label) in native_types.items():
         if not name.startswith(prefix):
             continue
@@ -264,7 +265,7 @@ def build_workload(name, rt, torch, gen, kernel):
         elems, size = rt.GGUF_NATIVE[gtype]
         one = n * (k // elems) * size
         ncopy = copies_for(one)
-        at = 208 if gtype == 14 else 0
+        at = {14: 208, 11: 108}.get(gtype, 0)
         ws = []
         for _ in range(ncopy):
             blocks = n * (k // elems)

@@ -230,7 +230,8 @@ int splosh_q4k_dequant(const splosh_q5k_weight *w, float *out, hipStream_t strea
 
 /* ---- Other GGUF formats, native blocks --------------------------------------------------------
  *
- * Q8_0 (8), Q6_K (14), IQ4_NL (20) and IQ4_XS (23), ggml type ids as in the file, in the blocks a
+ * Q8_0 (8), Q3_K (11), Q6_K (14), IQ4_NL (20), IQ3_S (21) and IQ4_XS (23), ggml type ids as in the
+ * file, in the blocks a
  * GGUF file holds: `rows` rows of `inner` elements, each row inner / block elements native blocks
  * (GgufQuant.swift:13-48), rows back to back. They replace the reference's staged GGUF kernels
  * for these formats (Engine.swift:1673-1694 dispatching sp_gguf_* by format,
@@ -239,6 +240,7 @@ int splosh_q4k_dequant(const splosh_q5k_weight *w, float *out, hipStream_t strea
  * splosh_gguf_gemm: out[m][n] = sum_k a[m][k] w[n][k] (+ residual), rows of activations in
  * passes of four over the weight (a streaming kernel for decode-sized row counts).
  * splosh_gguf_dequant: the weight as fp32 [rows][inner], bit-exact with the reference decoder.
+ * `native` must be 4-byte aligned (GGUF tensor data is 32-byte aligned).
  * Unsupported types return SPLOSH_ERR_UNSUPPORTED. */
 int splosh_gguf_gemm(int gguf_type, const uint8_t *native, int64_t rows, int64_t inner, const uint16_t *a,
                      int64_t lda, void *out, int64_t ldc, int out_dtype, const void *residual, int64_t m,

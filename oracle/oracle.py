@@ -45,6 +45,8 @@ def lib():
         L.or_gguf_decode.argtypes = [ctypes.c_int, _ptr, _i64, _ptr]
         L.or_gguf_block_bytes.restype = ctypes.c_int
         L.or_gguf_block_bytes.argtypes = [ctypes.c_int]
+        L.or_iq3s_grid.restype = None
+        L.or_iq3s_grid.argtypes = [_ptr]
         L.or_untile128.argtypes = [_ptr, _ptr, _i64, _i64, _i64]
         L.or_gemm_a_bf16_w_f32.argtypes = [_ptr, _i64, _ptr, _i64, _i64, _i64, _ptr]
         L.or_gemm_bf16.argtypes = [_ptr, _ptr, _i64, _i64, _i64, _ptr]
@@ -220,7 +222,15 @@ def q45k_decode(blocks, fifth_bit=True):
     return out
 
 
-GGUF_BLOCK = {8: (32, 34), 12: (256, 144), 13: (256, 176), 14: (256, 210), 20: (32, 18), 23: (256, 136)}
+GGUF_BLOCK = {8: (32, 34), 11: (256, 110), 12: (256, 144), 13: (256, 176), 14: (256, 210), 20: (32, 18),
+              21: (256, 110), 23: (256, 136)}
+
+
+def iq3s_grid():
+    """The oracle's IQ3_S codebook, 512 uint32 entries."""
+    out = np.empty(512, dtype=np.uint32)
+    lib().or_iq3s_grid(_p(out))
+    return out
 
 
 def gguf_decode(gguf_type, blocks):
@@ -236,13 +246,13 @@ def gguf_decode(gguf_type, blocks):
 
 def gguf_random_native(gguf_type, n, k, seed):
     """Rows of random native blocks with sane fp16 scales: every byte random, then each fp16
-    field (Q8_0 / IQ4_NL / IQ4_XS: d at 0; Q6_K: d at 208) set to about 1e-3 (sign random in one
+    field (Q8_0 / IQ4_NL / IQ4_XS / IQ3_S: d at 0; Q6_K: d at 208; Q3_K: d at 108) set to about 1e-3 (sign random in one
     block of four)."""
     elems, size = GGUF_BLOCK[gguf_type]
     blocks = n * k // elems
     rng = np.random.default_rng(seed)
     raw = rng.integers(0, 256, size=(blocks, size), dtype=np.uint8)
-    at = 208 if gguf_type == 14 else 0
+    at = {14: 208, 11: 108}.get(gguf_type, 0)
     v = 1e-3 * (1 + 0.25 * rng.uniform(-1, 1, size=blocks))
     v = np.where(rng.integers(0, 4, size=blocks) == 0, -v, v).astype(np.float16)
     raw[:, at:at + 2] = v.view(np.uint8).reshape(blocks, 2)

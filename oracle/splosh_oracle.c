@@ -334,6 +334,56 @@ void or_q45k_decode(const uint8_t *blocks, int64_t nblocks, int fifth_bit, float
  * reference keeps it at GgufQuant.swift:56). */
 static const int8_t kIq4Values[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
 
+/* The IQ3_S codebook (the format's table: llama.cpp's iq3s_grid, which the reference keeps as
+ * GgufTensorType.iq3sGrid, GgufQuant.swift:60). An entry is four magnitudes, each an odd number
+ * 1..15; here entry i is stored as twelve bits, magnitude t = 2 ((code >> 3t) & 7) + 1. The
+ * tests compare the expansion with the 512 entries read from the reference's file. */
+static const uint16_t kIq3sPacked[512] = {
+    0x000, 0x001, 0x002, 0x005, 0x007, 0x008, 0x009, 0x00a, 0x00c, 0x00e, 0x010, 0x011, 0x015, 0x01b, 0x020, 0x022,
+    0x025, 0x027, 0x029, 0x02b, 0x030, 0x032, 0x039, 0x03c, 0x03f, 0x040, 0x041, 0x042, 0x044, 0x048, 0x049, 0x04d,
+    0x050, 0x053, 0x057, 0x059, 0x05d, 0x064, 0x071, 0x075, 0x07a, 0x080, 0x081, 0x085, 0x087, 0x088, 0x08b, 0x08e,
+    0x091, 0x095, 0x098, 0x09c, 0x0a2, 0x0a5, 0x0a7, 0x0a9, 0x0ab, 0x0b8, 0x0bb, 0x0c3, 0x0c9, 0x0cd, 0x0d0, 0x0d2,
+    0x0d9, 0x0db, 0x0de, 0x0e4, 0x0e8, 0x0ea, 0x0f7, 0x0f9, 0x0fd, 0x100, 0x10b, 0x10f, 0x111, 0x114, 0x11a, 0x120,
+    0x123, 0x129, 0x138, 0x142, 0x144, 0x150, 0x152, 0x156, 0x15b, 0x161, 0x165, 0x167, 0x176, 0x17b, 0x186, 0x189,
+    0x18b, 0x199, 0x1aa, 0x1b9, 0x1c0, 0x1c2, 0x1c4, 0x1d0, 0x1d2, 0x1d6, 0x1db, 0x1e8, 0x1ec, 0x200, 0x201, 0x202,
+    0x204, 0x208, 0x209, 0x20b, 0x20d, 0x20f, 0x210, 0x212, 0x219, 0x21c, 0x21e, 0x22c, 0x22e, 0x231, 0x23a, 0x240,
+    0x241, 0x243, 0x246, 0x248, 0x24c, 0x251, 0x258, 0x25b, 0x261, 0x268, 0x26a, 0x278, 0x27e, 0x280, 0x28a, 0x28d,
+    0x28f, 0x290, 0x294, 0x29a, 0x2a0, 0x2a3, 0x2ad, 0x2b0, 0x2ba, 0x2c1, 0x2c4, 0x2c7, 0x2c8, 0x2cb, 0x2d1, 0x2d7,
+    0x2d8, 0x2dc, 0x2e1, 0x2f2, 0x2f8, 0x303, 0x305, 0x30a, 0x30c, 0x319, 0x31b, 0x322, 0x326, 0x328, 0x32c, 0x341,
+    0x348, 0x34b, 0x351, 0x358, 0x35a, 0x369, 0x390, 0x394, 0x397, 0x3a4, 0x3a6, 0x3c1, 0x3c3, 0x3c8, 0x3ca, 0x3d1,
+    0x3dd, 0x3e1, 0x3f2, 0x3f8, 0x400, 0x401, 0x403, 0x405, 0x407, 0x408, 0x40a, 0x40c, 0x40e, 0x411, 0x413, 0x417,
+    0x418, 0x41a, 0x421, 0x423, 0x425, 0x428, 0x42a, 0x437, 0x438, 0x43b, 0x43d, 0x440, 0x442, 0x448, 0x44b, 0x44f,
+    0x452, 0x455, 0x459, 0x45c, 0x462, 0x469, 0x481, 0x484, 0x487, 0x491, 0x493, 0x498, 0x49f, 0x4a1, 0x4ab, 0x4af,
+    0x4b9, 0x4bc, 0x4c0, 0x4c2, 0x4c5, 0x4c9, 0x4d2, 0x4d4, 0x4d9, 0x4db, 0x4e2, 0x4e8, 0x4f6, 0x501, 0x507, 0x510,
+    0x513, 0x51a, 0x51d, 0x521, 0x53a, 0x53d, 0x544, 0x549, 0x552, 0x55f, 0x560, 0x56b, 0x578, 0x580, 0x582, 0x587,
+    0x591, 0x5ad, 0x5b1, 0x5c5, 0x5c9, 0x5d6, 0x5d8, 0x5e3, 0x5e8, 0x602, 0x609, 0x60b, 0x60d, 0x60f, 0x612, 0x619,
+    0x61b, 0x61d, 0x622, 0x624, 0x627, 0x629, 0x633, 0x639, 0x641, 0x643, 0x645, 0x64c, 0x651, 0x653, 0x660, 0x670,
+    0x67a, 0x67e, 0x680, 0x68a, 0x690, 0x69a, 0x69c, 0x6a8, 0x6c1, 0x6c8, 0x6cc, 0x6d1, 0x6d3, 0x6d7, 0x6d8, 0x6e1,
+    0x6e3, 0x6e7, 0x6ed, 0x6fb, 0x703, 0x709, 0x70e, 0x712, 0x719, 0x72a, 0x730, 0x734, 0x741, 0x748, 0x74a, 0x755,
+    0x75a, 0x764, 0x76e, 0x77b, 0x78e, 0x7a1, 0x7c1, 0x7c3, 0x7d0, 0x7d2, 0x7dd, 0x800, 0x804, 0x80a, 0x810, 0x814,
+    0x817, 0x81a, 0x821, 0x828, 0x838, 0x842, 0x847, 0x849, 0x84b, 0x852, 0x858, 0x85d, 0x863, 0x869, 0x86d, 0x881,
+    0x883, 0x888, 0x88d, 0x891, 0x89b, 0x8a0, 0x8af, 0x8b2, 0x8b8, 0x8c4, 0x8c9, 0x8cb, 0x8d0, 0x8d2, 0x8d9, 0x8dd,
+    0x900, 0x902, 0x914, 0x91f, 0x920, 0x939, 0x945, 0x947, 0x951, 0x972, 0x98b, 0x99c, 0x9b0, 0x9c8, 0x9cd, 0x9d8,
+    0x9e3, 0x9e9, 0xa02, 0xa08, 0xa0c, 0xa12, 0xa20, 0xa24, 0xa27, 0xa2a, 0xa36, 0xa3c, 0xa41, 0xa43, 0xa45, 0xa4a,
+    0xa51, 0xa5a, 0xa7a, 0xa80, 0xa89, 0xa93, 0xa98, 0xa9e, 0xaab, 0xac2, 0xac7, 0xac8, 0xad7, 0xae4, 0xae9, 0xaf5,
+    0xafb, 0xb01, 0xb04, 0xb10, 0xb1a, 0xb26, 0xb4a, 0xb56, 0xb69, 0xb6b, 0xba2, 0xbc2, 0xbc4, 0xbd2, 0xc09, 0xc0b,
+    0xc0d, 0xc19, 0xc1b, 0xc30, 0xc40, 0xc50, 0xc57, 0xc74, 0xc8a, 0xc9c, 0xca2, 0xcad, 0xcb2, 0xcb8, 0xcc0, 0xccc,
+    0xcd1, 0xce0, 0xd15, 0xd23, 0xd32, 0xd40, 0xd43, 0xd5c, 0xd70, 0xd85, 0xda0, 0xdc9, 0xdcb, 0xe00, 0xe04, 0xe07,
+    0xe10, 0xe12, 0xe1e, 0xe20, 0xe2c, 0xe32, 0xe42, 0xe49, 0xe54, 0xe63, 0xe65, 0xe81, 0xe84, 0xe88, 0xe8e, 0xe91,
+    0xe98, 0xea9, 0xec2, 0xeda, 0xedd, 0xeeb, 0xf01, 0xf05, 0xf0b, 0xf10, 0xf28, 0xf52, 0xf62, 0xf82, 0xf99, 0xfc0,
+};
+
+static uint32_t iq3s_entry(int code) {
+    const uint32_t c = kIq3sPacked[code];
+    uint32_t e = 0;
+    for (int t = 0; t < 4; ++t) e |= (2u * ((c >> (3 * t)) & 7u) + 1u) << (8 * t);
+    return e;
+}
+
+void or_iq3s_grid(uint32_t *out) {
+    for (int i = 0; i < 512; ++i) out[i] = iq3s_entry(i);
+}
+
 /* One native block of a 32- or 256-element GGUF format to fp32, with the reference decoder's fp32
  * operation order (GgufQuant.swift): Q8_0 :172-175 (d * int8), IQ4_NL :179-185 (d * table, low
  * nibbles first), Q6_K :218-230 ((d * scale) * (code - 32) with the 4 low bits from ql and 2 high
@@ -384,6 +434,43 @@ static int gguf_decode_block(int type, const uint8_t *b, float *out) {
             }
             return 256;
         }
+        case 11: { /* Q3_K: hmask[32], qs[64], scales[12], d (fp16) at 108 (GgufQuant.swift:238-256) */
+            const float d = half_to_f32((uint16_t)(b[108] | (b[109] << 8)));
+            for (int j = 0; j < 8; ++j) {
+                const int half = j / 4, shift = 2 * (j % 4);
+                for (int e = 0; e < 32; ++e) {
+                    const int k = 2 * j + e / 16, word = k / 4, byte = k % 4;
+                    const int slow = (b[96 + 4 * (word % 2) + byte] >> (4 * (word / 2))) & 0xF;
+                    const int shigh = (b[104 + byte] >> (2 * word)) & 3;
+                    const float scale = (float)(slow | (shigh << 4)) - 32.0f;
+                    const int low = (b[32 + 32 * half + e] >> shift) & 3;
+                    const int high = (b[e] >> j) & 1;
+                    const float code = (float)(low | (high << 2)) - 4.0f;
+                    const float ds = d * scale;
+                    out[32 * j + e] = ds * code;
+                }
+            }
+            return 256;
+        }
+        case 21: { /* IQ3_S: d, qs[64], qh[8], signs[32], scales[4] (GgufQuant.swift:283-300) */
+            const float d = half_to_f32((uint16_t)(b[0] | (b[1] << 8)));
+            for (int j = 0; j < 8; ++j) {
+                const int scale = (b[106 + j / 2] >> (4 * (j % 2))) & 15;
+                const float weight = d * (1.0f + 2.0f * (float)scale);
+                const int ninth = b[66 + j];
+                for (int k = 0; k < 8; ++k) {
+                    const uint32_t entry = iq3s_entry(b[2 + 8 * j + k] | (((ninth >> k) & 1) << 8));
+                    for (int t = 0; t < 4; ++t) {
+                        const int e = 4 * k + t;
+                        const float magnitude = (float)((entry >> (8 * t)) & 0xFFu);
+                        const int negative = (b[74 + 4 * j + e / 8] >> (e % 8)) & 1;
+                        const float wm = weight * magnitude;
+                        out[32 * j + e] = wm * (1.0f - 2.0f * (float)negative);
+                    }
+                }
+            }
+            return 256;
+        }
         default:
             return 0;
     }
@@ -395,6 +482,8 @@ int or_gguf_block_bytes(int type) {
         case 20: return 18;
         case 14: return 210;
         case 23: return 136;
+        case 11: return 110;
+        case 21: return 110;
         case 12: return 144;
         case 13: return 176;
         default: return 0;

@@ -90,6 +90,8 @@ void or_q45k_decode(const uint8_t *blocks, int64_t nblocks, int fifth_bit, float
  * for another type. or_gguf_block_bytes: the native block size (0: not handled). */
 int or_gguf_decode(int type, const uint8_t *blocks, int64_t nblocks, float *out);
 int or_gguf_block_bytes(int type);
+/* The IQ3_S codebook's 512 entries as the oracle expands them (byte t = magnitude of element t). */
+void or_iq3s_grid(uint32_t *out);
 
 /* GgufPlanes for Q4_K / Q5_K (GgufPlanes.swift:62-136, 161-194, 221-229, 288-305).
  * plane0 [N/128][K/32][128][16 B], plane1 [N/128][K/32][128][4 B] (Q5_K only),

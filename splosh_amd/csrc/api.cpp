@@ -529,8 +529,11 @@ int splosh_q4k_dequant(const splosh_q5k_weight *w, float *out, hipStream_t strea
 static int check_gguf_native(int type, const uint8_t *native, int64_t rows, int64_t inner) {
     int elems = 0, bytes = 0;
     if (!splosh::gguf_native_block(type, &elems, &bytes))
-        return fail(SPLOSH_ERR_UNSUPPORTED, "ggml type not supported in native blocks (Q8_0, Q6_K, IQ4_NL, IQ4_XS)");
+        return fail(SPLOSH_ERR_UNSUPPORTED, "ggml type not supported in native blocks (Q8_0, Q3_K, Q6_K, IQ4_NL, IQ3_S, IQ4_XS)");
     if (!native) return fail(SPLOSH_ERR_NULL_POINTER, "null weight");
+    // The kernels read the blocks through dword-aligned windows relative to this base (GGUF tensor
+    // data is 32-byte aligned in the file).
+    if (!aligned(native, 4)) return fail(SPLOSH_ERR_LAYOUT_MISMATCH, "native weight must be 4-byte aligned");
     if (rows <= 0 || inner <= 0) return fail(SPLOSH_ERR_INVALID_SHAPE, "rows and inner must be positive");
     if (inner % elems != 0) return fail(SPLOSH_ERR_LAYOUT_MISMATCH, "inner is not a whole number of native blocks");
     if (mul_overflows(rows, inner / elems * bytes) || rows * (inner / elems * bytes) >= ((int64_t)1 << 32))

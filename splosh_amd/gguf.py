@@ -172,12 +172,12 @@ def load_weight(f, name, device="cuda"):
     from . import runtime as rt
     t = f.tensor(name)
     if t.type in rt.GGUF_NATIVE:
-        # Q8_0, Q6_K, IQ4_NL, IQ4_XS stay in their native blocks.
+        # Q8_0, Q3_K, Q6_K, IQ4_NL, IQ3_S, IQ4_XS stay in their native blocks.
         native = torch.from_numpy(np.array(f.bytes(name))).to(device)
         return rt.GgufWeight(native, t.type, t.rows, t.inner)
     if t.type not in (Q4_K, Q5_K):
-        raise GgufError(f"tensor {name} has ggml type {t.type}; the device kernels take Q4_K, Q5_K, Q6_K, "
-                        "Q8_0, IQ4_NL and IQ4_XS")
+        raise GgufError(f"tensor {name} has ggml type {t.type}; the device kernels take Q4_K, Q5_K, Q3_K, "
+                        "Q6_K, Q8_0, IQ4_NL, IQ3_S and IQ4_XS")
     rows, inner = t.rows, t.inner
     stored = -(-rows // 128) * 128
     block = BLOCK[t.type][1]

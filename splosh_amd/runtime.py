@@ -150,8 +150,8 @@ def _out(a, rows, n, out, out_dtype, stream=None):
 
 
 # ggml type id -> (block elements, block bytes) of the formats kept in native blocks
-# (GgufQuant.swift:13-48): Q8_0, Q6_K, IQ4_NL, IQ4_XS.
-GGUF_NATIVE = {8: (32, 34), 14: (256, 210), 20: (32, 18), 23: (256, 136)}
+# (GgufQuant.swift:13-48): Q8_0, Q3_K, Q6_K, IQ4_NL, IQ3_S, IQ4_XS.
+GGUF_NATIVE = {8: (32, 34), 11: (256, 110), 14: (256, 210), 20: (32, 18), 21: (256, 110), 23: (256, 136)}
 
 
 @dataclass

@@ -1,4 +1,4 @@
-"""GGUF Q8_0, Q6_K, IQ4_NL and IQ4_XS in native blocks on the GPU against the oracle: the dequant
+"""GGUF Q8_0, Q3_K, Q6_K, IQ4_NL, IQ3_S and IQ4_XS in native blocks on the GPU against the oracle: the dequant
 is bit-exact (the reference's golden blocks included), the GEMM within one bf16 rounding of the
 fp32-accumulate reference for every pass count of activation rows, the residual and both output
 types, config-0 sizes through sampled columns, and weights read out of a GGUF file."""
@@ -14,7 +14,7 @@ from qcheck import abs_gemm, bf16_tensor, check_close, to_f32
 from splosh_amd import gguf
 
 pytestmark = pytest.mark.gpu
-TYPES = {"q8_0": 8, "q6K": 14, "iq4NL": 20, "iq4XS": 23}
+TYPES = {"q8_0": 8, "q6K": 14, "iq4NL": 20, "iq4XS": 23, "q3K": 11, "iq3S": 21}
 GOLDEN = Path(__file__).resolve().parent / "golden" / "gguf_golden_blocks.json"
 
 
@@ -101,10 +101,14 @@ def test_rejects_other_types_and_bad_shapes(rt):
     out = torch.empty((1, 64), dtype=torch.float32, device="cuda")
     native = torch.zeros(64 * 16 * 34, dtype=torch.uint8, device="cuda")
     lib = _lib.lib()
-    for t in (0, 2, 11, 21):   # f32, Q4_0, Q3_K, IQ3_S: not in native form here
+    for t in (0, 2, 12, 13):   # f32, Q4_0; Q4_K and Q5_K take the plane form, not native blocks
         st = lib.splosh_gguf_gemm(t, native.data_ptr(), 64, 512, a.data_ptr(), 512, out.data_ptr(), 64,
                                   _lib.F32, None, 1, None)
         assert st != 0
     st = lib.splosh_gguf_gemm(8, native.data_ptr(), 64, 500, a.data_ptr(), 512, out.data_ptr(), 64, _lib.F32,
                               None, 1, None)
     assert st != 0
+    # A native pointer that is not 4-byte aligned is refused (the kernels read dword windows).
+    st = lib.splosh_gguf_gemm(8, native.data_ptr() + 2, 64, 512, a.data_ptr(), 512, out.data_ptr(), 64, _lib.F32,
+                              None, 1, None)
+    assert st == 2  # layoutMismatch

@@ -175,7 +175,8 @@ def test_gguf_golden_blocks(oracle, name, fifth):
     assert np.array_equal(got.view(np.uint32), expected.view(np.uint32))
 
 
-@pytest.mark.parametrize("name,gguf_type", [("q6K", 14), ("q8_0", 8), ("iq4NL", 20), ("iq4XS", 23)])
+@pytest.mark.parametrize("name,gguf_type", [("q6K", 14), ("q8_0", 8), ("iq4NL", 20), ("iq4XS", 23), ("q3K", 11),
+                                             ("iq3S", 21)])
 def test_gguf_golden_blocks_other_formats(oracle, name, gguf_type):
     """The other formats' golden blocks (GgufGoldenBlocks.swift, GgufTests.swift:237-247): the
     oracle's decode is bit-exact against the values the reference holds for each real block."""
@@ -219,6 +220,61 @@ def test_gguf_closed_forms(oracle):
     block = _f16(2.0) + [high & 0xFF, high >> 8] + low + [0x88] * 128
     v = oracle.gguf_decode(23, np.array(block, np.uint8)).reshape(8, 32)
     assert np.array_equal(v[:, 0], 2.0 * np.arange(8, dtype=np.float32)) and np.all(v == v[:, :1])
+
+
+def test_iq3s_grid_matches_the_reference_table(oracle):
+    """The oracle's IQ3_S codebook equals the 512 entries read from the reference's file."""
+    want = np.array(json.loads((GOLDEN.parent / "iq3s_grid.json").read_text())["grid"], np.uint32)
+    assert np.array_equal(oracle.iq3s_grid(), want)
+
+
+def test_q3k_closed_forms(oracle):
+    """Q3_K blocks whose values follow from the layout (GgufQuant.swift:232-256): d = 1; scale k
+    built from its low nibble (byte k % 4 of word (k / 4) % 2, nibble k / 8) and its top two bits
+    (bits 2 (k / 4) of byte 104 + k % 4), applied less 32 to 16 elements; group j's code takes bits
+    2 (j % 4) of byte 32 + 32 (j / 4) + e and bit j of byte e, less 4."""
+    b = np.zeros(110, np.uint8)
+    b[108:110] = _f16(1.0)
+    # Every scale = 33 (low nibble 1, top bits 2 = 0b10): byte k%4 of words 0, 1 hold nibbles
+    # 1 | 1 << 4; bytes 104..107 hold 0b10 at every 2-bit field.
+    b[96:104] = 0x11
+    b[104:108] = 0b10101010
+    v = oracle.gguf_decode(11, b).reshape(8, 32)
+    assert np.all(v == (33 - 32) * (0 - 4))  # all codes 0 - 4
+    # Group 5 (half 1, shift 2): low bits 3 at element 7; high bit (bit 5 of byte 7) set -> code
+    # 3 | 4 = 7 - 4 = 3.
+    b[32 + 32 + 7] = 0b11 << 2
+    b[7] = 1 << 5
+    v = oracle.gguf_decode(11, b).reshape(8, 32)
+    assert v[5, 7] == 3.0 and v[5, 6] == -4.0 and v[1, 7] == -4.0
+    # Scale 11 (word 2: high nibble of byte 3 of word 0; top bits at bits 4..5 of byte 107) = 0:
+    # group 5's elements 16..31 get scale 1 | 0 << 4 ... set the nibble to 5 and top bits to 1.
+    b[96 + 3] = (5 << 4) | 1
+    b[104 + 3] = (int(b[104 + 3]) & 0xCF) | (1 << 4)
+    v = oracle.gguf_decode(11, b).reshape(8, 32)
+    assert np.all(v[5, 16:] == ((5 | 16) - 32) * -4.0) and np.all(v[5, 8:16] == 1 * -4.0)
+
+
+def test_iq3s_closed_forms(oracle):
+    """IQ3_S blocks whose values follow from the layout (GgufQuant.swift:277-300): d = 0.5, scale
+    nibble s weighs group j by d (1 + 2 s); grid entry (code byte 8 j + k, ninth bit k of byte 66 + j)
+    gives the magnitudes of elements 4 k .. 4 k + 3; sign bit e of bytes 74 + 4 j .. negates."""
+    grid = oracle.iq3s_grid()
+    b = np.zeros(110, np.uint8)
+    b[0:2] = _f16(0.5)
+    b[106:110] = [0x21, 0x43, 0x65, 0x87]         # scales 1, 2, ..., 8 for groups 0..7
+    b[2:66] = np.arange(64, dtype=np.uint8) * 3   # code bytes
+    b[66:74] = [0, 0xFF, 0x0F, 0xF0, 0x55, 0xAA, 0x01, 0x80]  # ninth bits
+    b[74:106] = np.arange(32, dtype=np.uint8) * 37  # sign bytes
+    v = oracle.gguf_decode(21, b).reshape(8, 32)
+    for j in range(8):
+        weight = 0.5 * (1 + 2 * (j + 1))
+        for e in range(32):
+            k, t = e // 4, e % 4
+            code = int(b[2 + 8 * j + k]) | (((int(b[66 + j]) >> k) & 1) << 8)
+            mag = (int(grid[code]) >> (8 * t)) & 0xFF
+            neg = (int(b[74 + 4 * j + e // 8]) >> (e % 8)) & 1
+            assert v[j, e] == np.float32(weight * mag * (1 - 2 * neg)), (j, e)
 
 
 def test_q4k_group_layout_contract(oracle):
