@@ -247,6 +247,18 @@ int splosh_gguf_gemm(int gguf_type, const uint8_t *native, int64_t rows, int64_t
                      hipStream_t stream);
 int splosh_gguf_dequant(int gguf_type, const uint8_t *native, int64_t rows, int64_t inner, float *out,
                         hipStream_t stream);
+
+/* sp_gguf_embed (Shaders/engine_gguf.metal:302-318, bound at Engine.swift:400 and dispatched at
+ * :1612-1625), the embedding lookup on a GGUF table: out[i][k] = decode(w)[tokens[i]][k] for
+ * i < count, fp32 (bit-identical to GgufTensorType.decode) or bf16 (RNE), row stride ldo. tokens:
+ * count uint32 ids on the device; an id >= rows gives a row of zeros. splosh_q5k_embed /
+ * splosh_q4k_embed take the plane form, splosh_gguf_embed the native blocks of the types above. */
+int splosh_q5k_embed(const splosh_q5k_weight *w, const uint32_t *tokens, int64_t count, void *out, int64_t ldo,
+                     int out_dtype, hipStream_t stream);
+int splosh_q4k_embed(const splosh_q5k_weight *w, const uint32_t *tokens, int64_t count, void *out, int64_t ldo,
+                     int out_dtype, hipStream_t stream);
+int splosh_gguf_embed(int gguf_type, const uint8_t *native, int64_t rows, int64_t inner, const uint32_t *tokens,
+                      int64_t count, void *out, int64_t ldo, int out_dtype, hipStream_t stream);
 int splosh_q4k_repack(const uint8_t *native, int64_t rows, int64_t inner, uint8_t *plane0, uint8_t *meta,
                       hipStream_t stream);
 int splosh_q4k_unpack(const uint8_t *plane0, const uint8_t *meta, int64_t rows, int64_t inner, uint8_t *native,

@@ -564,6 +564,48 @@ int splosh_gguf_dequant(int gguf_type, const uint8_t *native, int64_t rows, int6
                       "gguf native dequant launch");
 }
 
+// Checks shared by the embedding lookups: ids, output and its row stride.
+static int check_embed_io(const uint32_t *tokens, int64_t count, const void *out, int64_t ldo, int64_t inner,
+                          int out_dtype) {
+    if (!tokens || !out) return fail(SPLOSH_ERR_NULL_POINTER, "null tokens or output");
+    if (count <= 0) return fail(SPLOSH_ERR_INVALID_SHAPE, "count must be positive");
+    if (ldo < inner) return fail(SPLOSH_ERR_INVALID_ROW_STRIDE, "ldo is shorter than inner");
+    if (out_dtype != SPLOSH_F32 && out_dtype != SPLOSH_BF16) return fail(SPLOSH_ERR_UNSUPPORTED, "unknown out_dtype");
+    if (mul_overflows(count, ldo) || count * (inner / 32) >= ((int64_t)1 << 40))
+        return fail(SPLOSH_ERR_ARITHMETIC_OVERFLOW, "size overflows");
+    return SPLOSH_OK;
+}
+
+static int gguf_embed_planes(const splosh_q5k_weight *w, bool fifth, const uint32_t *tokens, int64_t count, void *out,
+                             int64_t ldo, int out_dtype, hipStream_t stream) {
+    int st = check_q5k_weight(w, fifth);
+    if (st) return st;
+    if ((st = check_embed_io(tokens, count, out, ldo, w->inner, out_dtype))) return st;
+    splosh_q5k_weight wv = *w;
+    if (!fifth) wv.plane1 = nullptr;
+    return hip_status(splosh::launch_q5k_embed(wv, tokens, count, out, ldo, out_dtype, stream), "gguf embed launch");
+}
+
+int splosh_q5k_embed(const splosh_q5k_weight *w, const uint32_t *tokens, int64_t count, void *out, int64_t ldo,
+                     int out_dtype, hipStream_t stream) {
+    return gguf_embed_planes(w, true, tokens, count, out, ldo, out_dtype, stream);
+}
+
+int splosh_q4k_embed(const splosh_q5k_weight *w, const uint32_t *tokens, int64_t count, void *out, int64_t ldo,
+                     int out_dtype, hipStream_t stream) {
+    return gguf_embed_planes(w, false, tokens, count, out, ldo, out_dtype, stream);
+}
+
+int splosh_gguf_embed(int gguf_type, const uint8_t *native, int64_t rows, int64_t inner, const uint32_t *tokens,
+                      int64_t count, void *out, int64_t ldo, int out_dtype, hipStream_t stream) {
+    int st = check_gguf_native(gguf_type, native, rows, inner);
+    if (st) return st;
+    if ((st = check_embed_io(tokens, count, out, ldo, inner, out_dtype))) return st;
+    return hip_status(splosh::launch_gguf_embed(gguf_type, native, rows, inner, tokens, count, out, ldo, out_dtype,
+                                                stream),
+                      "gguf native embed launch");
+}
+
 int splosh_q5k_repack(const uint8_t *native, int64_t rows, int64_t inner, uint8_t *plane0, uint8_t *plane1,
                       uint8_t *meta, hipStream_t stream) {
     if (!native || !plane0 || !plane1 || !meta) return fail(SPLOSH_ERR_NULL_POINTER, "null buffer");

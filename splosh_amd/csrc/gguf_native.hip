@@ -240,6 +240,36 @@ __global__ void __launch_bounds__(256) gguf_dequant_kernel(GgufNativeArgs args) 
     for (int q = 0; q < 8; ++q) dst[q] = f32x4{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
 }
 
+// sp_gguf_embed (engine_gguf.metal:302-318) on native blocks: one thread a group of 32 of one
+// token's row; an id past the table gives zeros. `dense` receives fp32 (bit-exact) or, with
+// out_dtype bf16, bf16 (RNE); args.m is the token count and args.ldc the output row stride.
+template <int TYPE>
+__global__ void __launch_bounds__(256) gguf_embed_kernel(GgufNativeArgs args, const uint32_t *__restrict__ tokens) {
+    const int64_t groups = args.inner / 32;
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= args.m * groups) return;
+    const int64_t i = t / groups;
+    const int g = (int)(t % groups);
+    const int64_t row = tokens[i];
+    float v[32];
+    if (row >= args.rows) {
+#pragma unroll
+        for (int e = 0; e < 32; ++e) v[e] = 0.0f;
+    } else {
+        const rsrc_t r = make_rsrc(args.w, args.w_bytes);
+        decode_group<TYPE>(r, (uint32_t)(row * args.row_bytes), g, v);
+    }
+    if (args.out_dtype == SPLOSH_F32) {
+        float *dst = (float *)args.out + i * args.ldc + (int64_t)g * 32;
+#pragma unroll
+        for (int e = 0; e < 32; ++e) dst[e] = v[e];
+    } else {
+        uint16_t *dst = (uint16_t *)args.out + i * args.ldc + (int64_t)g * 32;
+#pragma unroll
+        for (int e = 0; e < 32; ++e) dst[e] = f32_to_bf16(v[e]);
+    }
+}
+
 template <int TYPE, int MR>
 __global__ void __launch_bounds__(256) gguf_gemv_kernel(GgufNativeArgs args) {
     const int lane = threadIdx.x & 63;
@@ -345,6 +375,26 @@ hipError_t launch_gguf_dequant(int type, const uint8_t *w, int64_t rows, int64_t
         case 11: hipLaunchKernelGGL(gguf_dequant_kernel<11>, grid, dim3(256), 0, stream, args); break;
         case 21: hipLaunchKernelGGL(gguf_dequant_kernel<21>, grid, dim3(256), 0, stream, args); break;
         default: hipLaunchKernelGGL(gguf_dequant_kernel<23>, grid, dim3(256), 0, stream, args); break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_gguf_embed(int type, const uint8_t *w, int64_t rows, int64_t inner, const uint32_t *tokens,
+                             int64_t count, void *out, int64_t ldo, int out_dtype, hipStream_t stream) {
+    GgufNativeArgs args = {};
+    fill_args(args, type, w, rows, inner);
+    args.m = count;
+    args.out = out;
+    args.ldc = ldo;
+    args.out_dtype = out_dtype;
+    const dim3 grid((unsigned)((count * (inner / 32) + 255) / 256));
+    switch (type) {
+        case 8: hipLaunchKernelGGL(gguf_embed_kernel<8>, grid, dim3(256), 0, stream, args, tokens); break;
+        case 20: hipLaunchKernelGGL(gguf_embed_kernel<20>, grid, dim3(256), 0, stream, args, tokens); break;
+        case 14: hipLaunchKernelGGL(gguf_embed_kernel<14>, grid, dim3(256), 0, stream, args, tokens); break;
+        case 11: hipLaunchKernelGGL(gguf_embed_kernel<11>, grid, dim3(256), 0, stream, args, tokens); break;
+        case 21: hipLaunchKernelGGL(gguf_embed_kernel<21>, grid, dim3(256), 0, stream, args, tokens); break;
+        default: hipLaunchKernelGGL(gguf_embed_kernel<23>, grid, dim3(256), 0, stream, args, tokens); break;
     }
     return hipGetLastError();
 }

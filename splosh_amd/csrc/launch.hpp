@@ -82,6 +82,11 @@ hipError_t launch_q4_mma(const MmaPlan &plan, const splosh_q4_weight &w, const s
 int gguf_native_block(int type, int *elems, int *bytes);
 hipError_t launch_gguf_dequant(int type, const uint8_t *w, int64_t rows, int64_t inner, float *dense,
                                hipStream_t stream);
+hipError_t launch_gguf_embed(int type, const uint8_t *w, int64_t rows, int64_t inner, const uint32_t *tokens,
+                             int64_t count, void *out, int64_t ldo, int out_dtype, hipStream_t stream);
+// The embedding lookup on Q5_K / Q4_K planes (plane1 null: Q4_K).
+hipError_t launch_q5k_embed(const splosh_q5k_weight &w, const uint32_t *tokens, int64_t count, void *out, int64_t ldo,
+                            int out_dtype, hipStream_t stream);
 hipError_t launch_gguf_gemv(int type, const uint8_t *w, int64_t rows, int64_t inner, const uint16_t *a, int64_t lda,
                             void *out, int64_t ldc, int out_dtype, const void *residual, int64_t m,
                             hipStream_t stream);

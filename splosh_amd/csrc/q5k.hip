@@ -148,6 +148,54 @@ q5k_dequant_kernel(splosh_q5k_weight w, float *__restrict__ out) {
     }
 }
 
+// sp_gguf_embed (engine_gguf.metal:302-318) on Q5_K / Q4_K planes: out[i] = decode(row tokens[i]),
+// one thread a group of 32 of one token; fp32 (bit-identical to the decoder) or bf16 (RNE). An id
+// past the table gives zeros.
+__global__ void __launch_bounds__(256)
+q5k_embed_kernel(splosh_q5k_weight w, const uint32_t *__restrict__ tokens, int64_t count, void *__restrict__ out,
+                 int64_t ldo, int out_dtype) {
+    const int64_t groups = w.inner / 32, blocks = w.inner / 256;
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= count * groups) return;
+    const int64_t i = idx / groups, g = idx % groups;
+    const int64_t row = tokens[i];
+    float v[32];
+    if (row >= w.rows) {
+        for (int e = 0; e < 32; ++e) v[e] = 0.0f;
+    } else {
+        const int64_t rec = plane_record(row, g, groups);
+        const u32x4 words = *(const u32x4 *)(w.plane0 + rec * 16);
+        const uint32_t bits = w.plane1 ? *(const uint32_t *)(w.plane1 + rec * 4) : 0u;  // null: Q4_K
+        uint8_t m[16];
+        const int64_t mrec = plane_record(row, g / 8, blocks);
+        for (int k = 0; k < 16; ++k) m[k] = w.meta[mrec * 16 + k];
+        float scaled, offset;
+        q5k_group_coefficients(m, (int)(g % 8), &scaled, &offset);
+        for (int e = 0; e < 32; ++e) {
+            const int slot = gguf_slot(e);
+            const int k = slot & 7;
+            const uint32_t code = ((words[slot >> 3] >> ((k & 1) * 16 + 4 * (k >> 1))) & 15u) | (((bits >> slot) & 1u) << 4);
+            const float p = (float)code * scaled;
+            v[e] = p - offset;
+        }
+    }
+    if (out_dtype == SPLOSH_F32) {
+        float *dst = (float *)out + i * ldo + g * 32;
+        for (int e = 0; e < 32; ++e) dst[e] = v[e];
+    } else {
+        uint16_t *dst = (uint16_t *)out + i * ldo + g * 32;
+        for (int e = 0; e < 32; ++e) dst[e] = f32_to_bf16(v[e]);
+    }
+}
+
+hipError_t launch_q5k_embed(const splosh_q5k_weight &w, const uint32_t *tokens, int64_t count, void *out, int64_t ldo,
+                            int out_dtype, hipStream_t stream) {
+    const int64_t total = count * (w.inner / 32);
+    hipLaunchKernelGGL(q5k_embed_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, w, tokens, count,
+                       out, ldo, out_dtype);
+    return hipGetLastError();
+}
+
 hipError_t launch_q5k_dequant(const splosh_q5k_weight &w, float *out, hipStream_t stream) {
     const int64_t total = w.rows * (w.inner / 32);
     hipLaunchKernelGGL(q5k_dequant_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, w, out);

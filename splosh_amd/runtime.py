@@ -432,7 +432,8 @@ def row_inv(squares, dim, eps, out=None, stream=None):
 
 
 def embed(w, tokens, out=None, out_dtype=torch.float32, stream=None):
-    """sp_embed_q4 (engine.metal:39-57): rows tokens[i] of the dequantized q4 table, [count, inner].
+    """sp_embed_q4 (engine.metal:39-57) for a q4 table, sp_gguf_embed (engine_gguf.metal:302-318)
+    for a GGUF one (planes or native blocks): rows tokens[i] of the decoded table, [count, inner].
     tokens: uint32 ids on the device (int32 tensors are taken as their bits); an id past the table
     gives zeros."""
     if tokens.dtype not in (torch.int32,) or not tokens.is_contiguous():
@@ -441,7 +442,13 @@ def embed(w, tokens, out=None, out_dtype=torch.float32, stream=None):
     if out is None:
         out = torch.empty((count, w.inner), dtype=out_dtype, device=tokens.device)
     _require(out, ((count - 1) * out.stride(0) + w.inner) * out.element_size(), "output")
+    if isinstance(w, GgufWeight):
+        _lib.check(_lib.lib().splosh_gguf_embed(w.gguf_type, _ptr(w.native), w.rows, w.inner, _ptr(tokens), count,
+                                                _ptr(out), out.stride(0), _dtype_code(out.dtype), _stream(stream)))
+        return out
     wc = w.c()
-    _lib.check(_lib.lib().splosh_q4_embed(ctypes.byref(wc), _ptr(tokens), count, _ptr(out), out.stride(0),
-                                          _dtype_code(out.dtype), _stream(stream)))
+    fn = (_lib.lib().splosh_q4_embed if isinstance(w, Q4Weight) else
+          _lib.lib().splosh_q4k_embed if isinstance(w, Q4KWeight) else _lib.lib().splosh_q5k_embed)
+    _lib.check(fn(ctypes.byref(wc), _ptr(tokens), count, _ptr(out), out.stride(0), _dtype_code(out.dtype),
+                  _stream(stream)))
     return out

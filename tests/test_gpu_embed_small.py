@@ -46,6 +46,34 @@ def test_embed_odd_k_and_out_of_range(rt):
     assert np.all(got[[2, 3], :k] == 0) and np.all(got[:, k:] == 7.0)
 
 
+@pytest.mark.parametrize("kind", ["q5k", "q4k", 8, 11, 14, 20, 21, 23])
+def test_gguf_embed_rows_bit_exact(rt, kind):
+    """sp_gguf_embed (engine_gguf.metal:302-318) on Q5_K / Q4_K planes and on every native-block
+    format: the rows of the pinned decoder, bit-exact in fp32 and RNE in bf16; ids past the table
+    give zeros; the output row stride is honoured."""
+    from qcheck import dev_u8
+    n, k = 256, 512
+    if kind in ("q5k", "q4k"):
+        fifth = kind == "q5k"
+        native = oracle.q45k_random_native(n, k, seed=41, fifth_bit=fifth)
+        w = (rt.q5k_repack if fifth else rt.q4k_repack)(dev_u8(native), n, k)
+        dense = oracle.q45k_decode(native, fifth_bit=fifth).reshape(n, k)
+    else:
+        native = oracle.gguf_random_native(kind, n, k, seed=42)
+        w = rt.GgufWeight(dev_u8(native), kind, n, k)
+        dense = oracle.gguf_decode(kind, native).reshape(n, k)
+    ids = np.array([0, 255, 17, 300, 128, 17, 0xFFFFFFFF], np.uint32)
+    tokens = torch.from_numpy(ids.view(np.int32)).cuda()
+    out = torch.full((len(ids), k + 8), 5.0, device="cuda")
+    rt.embed(w, tokens, out=out)
+    got = out.cpu().numpy()
+    inside = ids < n
+    assert np.array_equal(got[inside, :k].view(np.uint32), dense[ids[inside]].view(np.uint32))
+    assert np.all(got[~inside, :k] == 0) and np.all(got[:, k:] == 5.0)
+    got16 = rt.embed(w, tokens, out_dtype=torch.bfloat16).view(torch.int16).cpu().numpy().view(np.uint16)
+    assert np.array_equal(got16[inside], oracle.f32_to_bf16_rne(dense[ids[inside]]).reshape(int(inside.sum()), k))
+
+
 @pytest.mark.parametrize("rows", [1, 2, 16, 64])
 def test_small_projection_48_rows(rt, rows):
     """The gated-delta a and b projections: 48 outputs from 5120, row-major (the engine keeps them
