@@ -6,7 +6,7 @@ projection (two K=5120 -> N=17408 weights sharing one activation read, out = sil
 by the down projection (K=17408 -> N=5120) on that output. One "step" is that pair of launches.
 
     python bench.py [--steps K] [--warmup W]
-                    [--workload verify64|decode1|q5k1|q5k16|q5k64|q4k1|q4k64|q6k1|q80_1|iq4nl1|iq4xs1|q3k1|iq3s1|prefill2048|layerset|lmhead1|lmhead64|operand64]
+                    [--workload verify64|decode1|q5k1|q5k16|q5k64|q4k1|q4k64|q6k1|q80_1|iq4nl1|iq4xs1|q3k1|iq3s1|prefill2048|layerset|lmhead1|lmhead64|operand64|emit64|stream50|stream715]
 
 Inputs are synthetic (seeded, on the device): code words uniform random, scale = bf16(|N(0,0.02)|),
 bias = bf16(N(0,0.01)), activations bf16(N(0,1)). Several copies of the weight set are rotated so
@@ -190,6 +190,58 @@ def build_workload(name, rt, torch, gen, kernel):
         cfg = {"workload": "layer set at M=64: attention q/k/v/o, gated-delta in/out, MLP gate+up and down",
                "rows": m, "format": "mlx affine q4 g64, tiled128", "weight_copies": ncopy}
         return launches, sum(kb.values()), sum(kf.values()), kb, cfg, kf
+    if name.startswith("stream"):
+        # The practical ceiling of one launch: a plain streaming read of as many bytes as the named
+        # decode weight (stream50: config 0's 50,180,096 bytes; stream715: the lm_head's), on 2048
+        # workgroups (the best of 256..4096 measured; SPLOSH_PROBE_GRID overrides), rotated over copies. Not part of the path: the probe kernel
+        # is exported by the library for this measurement only.
+        import ctypes
+        from splosh_amd import _lib
+        lib = _lib.lib()
+        lib.splosh_probe_stream_read.restype = ctypes.c_int
+        lib.splosh_probe_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int,
+                                                 ctypes.c_void_p]
+        b = {"stream50": q4_bytes(17408, 5120), "stream715": q4_bytes(248320, 5120)}[name]
+        ncopy = copies_for(b)
+        bufs = [torch.randint(0, 255, (b,), dtype=torch.uint8, device="cuda", generator=gen) for _ in range(ncopy)]
+        grid = int(os.environ.get("SPLOSH_PROBE_GRID", "2048"))
+        sink = torch.zeros(4 * grid, dtype=torch.int32, device="cuda")
+
+        def launches(i):
+            buf = bufs[i % ncopy]
+            return [("read", lambda: _lib.check(lib.splosh_probe_stream_read(
+                buf.data_ptr(), b, sink.data_ptr(), grid, torch.cuda.current_stream().cuda_stream)))]
+
+        cfg = {"workload": f"streaming read of {b} bytes a launch (probe, not the path)", "rows": 0,
+               "format": "bytes", "weight_copies": ncopy}
+        return launches, b, 0, {"read": b}, cfg, {"read": 0}
+    if name == "emit64":
+        # The MLP's down projection at M=64 as the residual projection that feeds the next RMSNorm:
+        # fp32 hidden state += a w^T, and the next GEMM's operand (bf16 h * norm weight, per-64 sums
+        # and sums of squares). "fused": the emit in the GEMM's epilogue (splosh_q4_gemm_emit);
+        # "separate": the GEMM, then the operand pass over the hidden state.
+        m, h, inter = 64, 5120, 17408
+        ncopy = copies_for(q4_bytes(h, inter))
+        ws = [make_q4(rt, h, inter, gen) for _ in range(ncopy)]
+        x = torch.randn(m, inter, device="cuda", generator=gen).to(torch.bfloat16)
+        hid = torch.randn(m, h, device="cuda", generator=gen)
+        wn = (1 + 0.1 * torch.randn(h, device="cuda", generator=gen)).to(torch.bfloat16)
+        scr = workspace(m, h, inter)
+        be = torch.empty(m, h, dtype=torch.bfloat16, device="cuda")
+        se = torch.empty(m, h // 64, device="cuda")
+        qe = torch.empty_like(se)
+        b = q4_bytes(h, inter) + m * inter * 2 + 2 * m * h * 4 + m * h * 2 + 2 * m * (h // 64) * 4
+
+        def launches(i):
+            w = ws[i % ncopy]
+            return [("fused", lambda: rt.gemm_emit(w, x, wn, out=hid, residual=hid, workspace=scr)),
+                    ("separate", lambda: (rt.gemm(w, x, out=hid, residual=hid, out_dtype=torch.float32, workspace=scr),
+                                          rt.emit_operand(hid, wn, values=be, sums=se, squares=qe)))]
+
+        cfg = {"workload": "down projection K17408->N5120 at M=64 with the next norm's operand emitted", "rows": m,
+               "format": "mlx affine q4 g64, tiled128", "weight_copies": ncopy}
+        return launches, 2 * b, 4 * m * h * inter, {"fused": b, "separate": b}, cfg, \
+            {"fused": 2 * m * h * inter, "separate": 2 * m * h * inter}
     if name.startswith("operand"):
         # The operand producers around the draft-verify MLP at M rows (default 64): the input
         # operand (fp32 -> bf16 + sums, 5120), the down projection's operand (silu(g) u, 17408) and
@@ -287,13 +339,24 @@ def build_workload(name, rt, torch, gen, kernel):
     raise SystemExit(f"unknown workload {name}")
 
 
-def cpu_baseline(workload, seconds=8.0):
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(workload, step_bytes, step_flops, seconds=3.0):
     """The CPU oracle (oracle/: dequantize each weight row to fp32, sequential fp32 dot per
     activation row -- DequantOracle.dequantize + the fp32 GEMM loop) timed on a bounded sample of
-    output columns of the same workload and extrapolated to the whole step."""
+    output columns of the same workload, on one core and on every core of the host, and
+    extrapolated to the whole step. The rate counts the same bytes (or flops) as the GPU's."""
     import numpy as np
     import oracle
-    threads = max(1, min(16, os.cpu_count() or 1))
+    nproc = os.cpu_count() or 1
     if workload == "verify64":
         mats = [(17408, 5120), (17408, 5120), (5120, 17408)]
         m = 64
@@ -305,31 +368,35 @@ def cpu_baseline(workload, seconds=8.0):
         m = 2048
     else:
         return None
-    total_bytes = sum(q4_bytes(n, k) for n, k in mats) + 0
-    # A seeded sample weight per shape; a column's cost does not depend on its values.
-    frac = 1 / 64 if m <= 64 else 1 / 4096
-    elapsed = 0.0
-    while True:
-        t_total = 0.0
-        for idx, (n, k) in enumerate(mats):
-            cols = max(threads, int(n * frac))
-            words, stride, sc, bi = oracle.q4_random_weight(cols, k, seed=idx)
-            a = oracle.bf16_normal((m, k), seed=99)
-            t0 = time.perf_counter()
-            oracle.q4_gemm_rowmajor(a, words, stride, sc, bi, cols, k, threads=threads)
-            t_total += (time.perf_counter() - t0) * n / cols
-            elapsed += time.perf_counter() - t0
-        if elapsed >= 2.0 or frac >= 1.0:
-            break
-        frac = min(1.0, frac * max(2.0, seconds / max(elapsed, 1e-3) / 2))
-    sample = f"{frac * 100:.2f}% of each weight's output columns at M={m}, extrapolated to the full step"
-    if workload == "prefill2048":
-        flops = 2 * m * sum(n * k for n, k in mats)
-        return {"value": flops / t_total / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-                "sample": sample, "step_seconds": t_total}
-    step_bytes = total_bytes + m * 5120 * 2 * (2 if workload == "verify64" else 1)
-    return {"value": step_bytes / t_total / 1e12, "unit": "TB/s", "cores": threads, "kind": "port",
-            "sample": sample, "step_seconds": t_total}
+
+    def step_seconds(threads):
+        # A seeded sample weight per shape; a column's cost does not depend on its values. The
+        # sample grows until it has run for `seconds` or covers every column.
+        frac = 1 / 256 if m <= 64 else 1 / 8192
+        while True:
+            t_total, elapsed = 0.0, 0.0
+            for idx, (n, k) in enumerate(mats):
+                cols = max(threads, int(n * frac))
+                words, stride, sc, bi = oracle.q4_random_weight(cols, k, seed=idx)
+                a = oracle.bf16_normal((m, k), seed=99)
+                t0 = time.perf_counter()
+                oracle.q4_gemm_rowmajor(a, words, stride, sc, bi, cols, k, threads=threads)
+                dt = time.perf_counter() - t0
+                t_total += dt * n / cols
+                elapsed += dt
+            if elapsed >= seconds or frac >= 1.0:
+                return t_total, frac
+            frac = min(1.0, frac * max(2.0, seconds / max(elapsed, 1e-3)))
+
+    t1, f1 = step_seconds(1)
+    tn, fn = step_seconds(nproc)
+    work, unit = (step_flops, "TFLOP/s") if workload == "prefill2048" else (step_bytes, "TB/s")
+    v1, vn = work / t1 / 1e12, work / tn / 1e12
+    return {"value": vn, "unit": unit, "cores": nproc, "kind": "port",
+            "sample": f"{fn * 100:.2f}% (all cores) and {f1 * 100:.2f}% (one core) of each weight's output "
+                      f"columns at M={m}, extrapolated to the full step; same work count as the GPU line",
+            "single_core": v1, "all_cores": vn, "nproc": nproc, "cpu_model": _cpu_model(),
+            "step_seconds": {"single_core": t1, "all_cores": tn}}
 
 
 def main():
@@ -436,7 +503,7 @@ def main():
                     "kernel": dominant, "kernel_us": round(dom_ms * 1e3, 2),
                     "algorithmic_bytes": kernel_bytes[dominant]}
         value, unit = step_bytes / (ms_per_step * 1e-3) / 1e12, "TB/s"
-    cpu = None if args.no_cpu else cpu_baseline(args.workload)
+    cpu = None if args.no_cpu else cpu_baseline(args.workload, step_bytes, step_flops)
     result = {
         "metric": "quant GEMM effective HBM TB/s at M=1/64; TFLOP/s at M=2048 prefill",
         "value": round(value, 4), "unit": unit, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,

@@ -160,6 +160,19 @@ int splosh_q4_gemm(const splosh_q4_weight *w, const uint16_t *a, int64_t lda, vo
                    int out_dtype, const void *residual, int64_t rows, int kernel, void *workspace,
                    size_t workspace_bytes, hipStream_t stream);
 
+/* Engine.gemm with `emit` (Runtime/Engine.swift:1652-1806; kernels sp_gemm_q4_nat_m32n128s4_emit and
+ * sp_gemm_q4_split_tiled_m16n64p4_emit, Shaders/engine_na.metal:322-473, SpNaEmit :26-36): the
+ * residual projection out = residual + a w^T (fp32, residual may be NULL or alias out) that also
+ * writes the next RMSNorm-ed GEMM's operand from the same values: values = bf16(out * norm_weight)
+ * (RNE, [rows][ld_values]), and per row and per 64 columns the sums of those rounded values and of
+ * out * out (fp32 [rows][w->rows / 64]), as splosh_emit_operand computes them. w->rows % 64 == 0.
+ * The M <= 64 kernel (AUTO for 3..64 rows) writes them from its epilogue; other row counts run the
+ * GEMM and then the operand pass. */
+int splosh_q4_gemm_emit(const splosh_q4_weight *w, const uint16_t *a, int64_t lda, float *out, int64_t ldc,
+                        const float *residual, int64_t rows, const uint16_t *norm_weight, uint16_t *values,
+                        int64_t ld_values, float *sums, float *squares, int kernel, void *workspace,
+                        size_t workspace_bytes, hipStream_t stream);
+
 /* No counterpart in the reference: splosh_q4_gemm for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). It takes no
  * workspace and allocates nothing: the kernels use a static scratch array in the library's device

@@ -82,6 +82,8 @@ SIGNATURES = {
     "splosh_q5k_embed": (_int, [ctypes.POINTER(Q5KWeight), _vp, _i64, _vp, _i64, _int, _vp]),
     "splosh_q4k_embed": (_int, [ctypes.POINTER(Q5KWeight), _vp, _i64, _vp, _i64, _int, _vp]),
     "splosh_gguf_embed": (_int, [_int, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _int, _vp]),
+    "splosh_q4_gemm_emit": (_int, [ctypes.POINTER(Q4Weight), _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _vp,
+                                     _vp, _int, _vp, _sz, _vp]),
     "splosh_q4_gemm_noalloc": (_int, [ctypes.POINTER(Q4Weight), _vp, _i64, _vp, _i64, _int, _vp, _i64, _int, _vp]),
     "splosh_q4_mlp_in": (_int, [ctypes.POINTER(Q4Weight), ctypes.POINTER(Q4Weight), _vp, _i64, _vp, _i64, _int,
                                 _i64, _int, _vp, _sz, _vp]),

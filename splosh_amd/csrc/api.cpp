@@ -88,7 +88,8 @@ bool q4_stream_eligible(const splosh_q4_weight &w, const uint16_t *a, int64_t ld
 
 int q4_gemm_impl(const splosh_q4_weight *w, const splosh_q4_weight *up, const uint16_t *a, int64_t lda, void *out,
                  int64_t ldc, int out_dtype, const void *residual, int64_t rows, int kernel, void *workspace,
-                 size_t workspace_bytes, hipStream_t stream) {
+                 size_t workspace_bytes, hipStream_t stream, const splosh::EmitOperand *emit = nullptr,
+                 bool *emitted = nullptr) {
     int st = check_q4_weight(w, up ? "gate" : "weight");
     if (st) return st;
     if (up) {
@@ -169,8 +170,9 @@ int q4_gemm_impl(const splosh_q4_weight *w, const splosh_q4_weight *up, const ui
             if (!mma_ok) return fail(SPLOSH_ERR_UNSUPPORTED, "dequant kernel needs rows <= 64 and aligned operands");
             const splosh::MmaPlan plan =
                 splosh::plan_mma(rows, w->rows, w->inner / kGroupSize, up != nullptr, workspace ? workspace_bytes : 0);
+            if (emitted) *emitted = emit != nullptr;
             return hip_status(splosh::launch_q4_mma(plan, *w, up, a, lda, out, ldc, out_dtype, residual, rows,
-                                                    workspace, stream),
+                                                    workspace, stream, emit),
                               "q4 mma launch");
         }
         default:
@@ -377,6 +379,33 @@ int splosh_q4_gemm(const splosh_q4_weight *w, const uint16_t *a, int64_t lda, vo
                    hipStream_t stream) {
     return q4_gemm_impl(w, nullptr, a, lda, out, ldc, out_dtype, residual, rows, kernel, workspace, workspace_bytes,
                         stream);
+}
+
+// Engine.gemm with emit (engine_na.metal:322-473): the residual projection that also writes the
+// next RMSNorm's operand. The M <= 64 kernel writes it from its epilogue; other kernels are followed
+// by the separate operand pass on the fp32 output.
+int splosh_q4_gemm_emit(const splosh_q4_weight *w, const uint16_t *a, int64_t lda, float *out, int64_t ldc,
+                        const float *residual, int64_t rows, const uint16_t *norm_weight, uint16_t *values,
+                        int64_t ld_values, float *sums, float *squares, int kernel, void *workspace,
+                        size_t workspace_bytes, hipStream_t stream) {
+    int st = check_q4_weight(w, "weight");
+    if (st) return st;
+    if (!norm_weight || !values || !sums || !squares) return fail(SPLOSH_ERR_NULL_POINTER, "null emit buffer");
+    if (w->rows % 64 != 0) return fail(SPLOSH_ERR_INVALID_SHAPE, "emit needs the output width to be a multiple of 64");
+    if (ld_values < w->rows) return fail(SPLOSH_ERR_INVALID_SHAPE, "ld_values is shorter than the output width");
+    if (!aligned(out, 16) || ldc % 4 != 0 || !aligned(values, 8) || ld_values % 4 != 0 || !aligned(norm_weight, 8))
+        return fail(SPLOSH_ERR_UNSUPPORTED,
+                    "emit needs a 16-byte aligned fp32 output with ldc % 4 == 0, 8-byte aligned values with "
+                    "ld_values % 4 == 0 and an 8-byte aligned norm weight");
+    const splosh::EmitOperand emit{norm_weight, values, ld_values, sums, squares};
+    bool emitted = false;
+    if ((st = q4_gemm_impl(w, nullptr, a, lda, out, ldc, SPLOSH_F32, residual, rows, kernel, workspace,
+                           workspace_bytes, stream, &emit, &emitted)))
+        return st;
+    if (emitted) return ok();
+    return hip_status(splosh::launch_emit_operand(out, ldc, norm_weight, rows, w->rows, values, ld_values, sums, squares,
+                                                  stream),
+                      "emit operand launch");
 }
 
 // splosh_q4_gemm with the library's static device scratch as its workspace: no allocation.

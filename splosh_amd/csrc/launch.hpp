@@ -74,9 +74,17 @@ bool mma_fits(int64_t rows, int64_t columns, int64_t inner, int64_t stride_words
 MmaPlan plan_mma(int64_t rows, int64_t columns, int64_t groups, bool mlp, size_t workspace_bytes,
                  int64_t unit_elems = 64);
 size_t mma_workspace_bytes(int64_t rows, int64_t columns, int64_t groups, bool mlp);
+// The next RMSNorm's operand a residual projection emits (SpNaEmit, engine_na.metal:26-36).
+struct EmitOperand {
+    const uint16_t *norm_weight;  // bf16 [n]
+    uint16_t *values;             // bf16 [rows][ldv]
+    int64_t ldv;
+    float *sums, *squares;        // fp32 [rows][n / 64]
+};
+// emit: null, or the operand to write from the epilogue (single weight, fp32 output, n % 64 == 0).
 hipError_t launch_q4_mma(const MmaPlan &plan, const splosh_q4_weight &w, const splosh_q4_weight *up,
                          const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype, const void *residual,
-                         int64_t rows, void *workspace, hipStream_t stream);
+                         int64_t rows, void *workspace, hipStream_t stream, const EmitOperand *emit = nullptr);
 
 // GGUF Q8_0 / Q6_K / IQ4_NL / IQ4_XS in native blocks (gguf_native.hip).
 int gguf_native_block(int type, int *elems, int *bytes);

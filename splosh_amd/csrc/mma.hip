@@ -67,6 +67,13 @@ struct MmaArgs {
     // Buffer extents (the fits checks keep them < 4 GiB): q4 codes and sidecars, or Q5_K plane0,
     // plane1 and meta; activations.
     uint32_t code_bytes, sidecar_bytes, meta_bytes, a_bytes;
+    // The next RMSNorm's operand, emitted from the epilogue (single weight, fp32 output, N a multiple
+    // of 64; null norm_weight: no emit): values = bf16(h norm_weight[col]), and per row and band of
+    // 64 columns the sums of the rounded values and of h * h, h being the value written to `out`.
+    const uint16_t *norm_weight;
+    uint16_t *values;
+    int64_t ldv;
+    float *sums, *squares;   // [rows][n / 64]
 };
 
 __device__ __forceinline__ float cvt_byte(uint32_t x, int j) {
@@ -350,7 +357,8 @@ struct MmaShape {
     static constexpr int kAcc = FM * NW * 16;                      // accumulator floats per lane
     static constexpr size_t kRedBytes = (size_t)KW * CW * kAcc * 64 * sizeof(float);
     static constexpr size_t kABytes = (size_t)kNB * (kABuf + kSBuf);
-    static constexpr size_t kLds = kRedBytes > kABytes ? kRedBytes : kABytes;
+    static constexpr size_t kEmitBytes = (size_t)kRows * 2 * 2 * sizeof(float);  // emit band sums
+    static constexpr size_t kLds = kRedBytes + kEmitBytes > kABytes ? kRedBytes + kEmitBytes : kABytes;
     static_assert(D >= 3, "the pipeline below keeps weights at least three steps ahead");
 };
 
@@ -625,17 +633,19 @@ mma_kernel(MmaArgs args) {
     // Row i of this lane's quarter of block f, and the lane's band column.
     auto own_row = [&](int f, int i) { return 32 * f + 8 * kw + 4 * h + i; };
     const int bcol = cw * 32 + r;
+    // The epilogue of a finished band: every wave calls it (the emit's band sums meet in LDS).
     auto store_out = [&](int band, const f32x4 (&v)[NW][FM]) {
         const int64_t ocol = (int64_t)band * S::kBandCols + bcol;
-        if (ocol >= args.n) return;
+        float hv[FM][4];
 #pragma unroll
         for (int f = 0; f < FM; ++f)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int m = own_row(f, i);
-                if (m >= rows) continue;
                 float value = v[0][f][i];
                 if constexpr (NW == 2) value = silu(v[0][f][i]) * v[1][f][i];
+                hv[f][i] = value;
+                if (m >= rows || ocol >= args.n) continue;
                 const int64_t index = (int64_t)m * args.ldc + ocol;
                 if (args.out_dtype == SPLOSH_F32) {
                     if (args.residual) value += ((const float *)args.residual)[index];
@@ -644,7 +654,49 @@ mma_kernel(MmaArgs args) {
                     if (args.residual) value += bf16_bits_to_f32(((const uint16_t *)args.residual)[index]);
                     ((uint16_t *)args.out)[index] = f32_to_bf16(value);
                 }
+                hv[f][i] = value;
             }
+        if constexpr (NW == 1) {
+            if (args.norm_weight) {
+                // Emit (engine_na.metal:365-411 restated): the rounded operand, then per row the
+                // band's sums: over this wave's 32 columns by a shuffle tree inside the lane half
+                // that holds the row, then the two column waves' halves through LDS.
+                const float wn = bf16_bits_to_f32(args.norm_weight[ocol]);
+                float *part = (float *)((char *)lds + S::kRedBytes);  // [FM * 32 rows][2 cw][2]
+                const int64_t groups = args.n / 64;
+#pragma unroll
+                for (int f = 0; f < FM; ++f)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int m = own_row(f, i);
+                        const uint16_t vb = f32_to_bf16(hv[f][i] * wn);
+                        if (m < rows) args.values[(int64_t)m * args.ldv + ocol] = vb;
+                        float sv = bf16_bits_to_f32(vb), sq = hv[f][i] * hv[f][i];
+#pragma unroll
+                        for (int o = 1; o < 32; o <<= 1) {
+                            sv += __shfl_xor(sv, o, 64);
+                            sq += __shfl_xor(sq, o, 64);
+                        }
+                        if (r == 0) {
+                            part[(m * 2 + cw) * 2] = sv;
+                            part[(m * 2 + cw) * 2 + 1] = sq;
+                        }
+                    }
+                __syncthreads();
+                if (cw == 0 && r == 0) {
+#pragma unroll
+                    for (int f = 0; f < FM; ++f)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const int m = own_row(f, i);
+                            if (m >= rows) continue;
+                            args.sums[(int64_t)m * groups + band] = part[m * 4] + part[m * 4 + 2];
+                            args.squares[(int64_t)m * groups + band] = part[m * 4 + 1] + part[m * 4 + 3];
+                        }
+                }
+                __syncthreads();  // the band sums are read before the next band writes them
+            }
+        }
     };
     // Partial of workgroup wg, slot sl, weight w, row m, this lane's band column: a byte offset
     // into the partial area ([grid][2][NW][rows][band columns] fp32).
@@ -920,8 +972,15 @@ static void set_io(MmaArgs &args, const MmaPlan &plan, const uint16_t *a, int64_
 
 hipError_t launch_q4_mma(const MmaPlan &plan, const splosh_q4_weight &w, const splosh_q4_weight *up,
                          const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype, const void *residual,
-                         int64_t rows, void *workspace, hipStream_t stream) {
+                         int64_t rows, void *workspace, hipStream_t stream, const EmitOperand *emit) {
     MmaArgs args = {};
+    if (emit) {
+        args.norm_weight = emit->norm_weight;
+        args.values = emit->values;
+        args.ldv = emit->ldv;
+        args.sums = emit->sums;
+        args.squares = emit->squares;
+    }
     args.packed[0] = w.packed;
     args.scales[0] = w.scales;
     args.biases[0] = w.biases;

@@ -229,6 +229,32 @@ def gemm(w, a, out=None, residual=None, out_dtype=torch.bfloat16, kernel=AUTO, r
     return out
 
 
+def gemm_emit(w, a, norm_weight, out=None, residual=None, kernel=AUTO, rows=None, stream=None, workspace=None):
+    """Engine.gemm with emit (engine_na.metal:322-473): out = a @ dequant(w)^T (+ residual), fp32,
+    and the next RMSNorm's operand from it: (bf16 out * norm_weight, per-64 sums of those values,
+    per-64 sums of out^2). Returns (out, values, sums, squares)."""
+    rows = a.shape[0] if rows is None else rows
+    if a.dtype != torch.bfloat16 or a.stride(-1) != 1:
+        raise SploshError(13, "activations must be contiguous bf16 rows")
+    out = _out(a, rows, w.rows, out, torch.float32, stream)
+    if out.dtype != torch.float32:
+        raise SploshError(13, "the emitting projection writes fp32")
+    _require(a, ((rows - 1) * a.stride(0) + w.inner) * 2, "a")
+    _require(out, ((rows - 1) * out.stride(0) + w.rows) * 4, "output")
+    if norm_weight.dtype != torch.bfloat16 or norm_weight.numel() < w.rows:
+        raise SploshError(13, "norm_weight must be bf16 with one value a column")
+    with torch.cuda.stream(_on(stream)):
+        values = torch.empty((rows, w.rows), dtype=torch.bfloat16, device=a.device)
+        sums = torch.empty((rows, w.rows // 64), dtype=torch.float32, device=a.device)
+        squares = torch.empty_like(sums)
+    wc = w.c()
+    ws, ws_bytes = _workspace(workspace, rows, w.rows, w.inner, a.device, stream)
+    _lib.check(_lib.lib().splosh_q4_gemm_emit(ctypes.byref(wc), _ptr(a), a.stride(0), _ptr(out), out.stride(0),
+                                              _ptr(residual), rows, _ptr(norm_weight), _ptr(values), values.stride(0),
+                                              _ptr(sums), _ptr(squares), kernel, ws, ws_bytes, _stream(stream)))
+    return out, values, sums, squares
+
+
 def mlp_in(gate, up, a, out=None, out_dtype=torch.bfloat16, kernel=AUTO, rows=None, stream=None, workspace=None):
     """Engine.mlpIn (Runtime/Engine.swift:1911-1966): out = silu(a @ gate^T) * (a @ up^T), one
     pass over the activations for both weights."""

@@ -81,3 +81,27 @@ def test_operand_rejects_bad_arguments(rt):
     x = torch.zeros((2, 100), device="cuda")
     with pytest.raises(rt.SploshError):
         rt.prepare_operand(x)  # dim not a multiple of 64
+
+
+@pytest.mark.parametrize("rows", [1, 5, 33, 64, 100])
+@pytest.mark.parametrize("n,k", [(640, 4352), (5120, 1280)])
+def test_gemm_emit(rt, rows, n, k):
+    """Engine.gemm with emit (engine_na.metal:322-473): the residual projection's fp32 output, and
+    the next norm's operand computed from that output -- fused into the M <= 64 kernel's epilogue
+    (rows 5..64, with and without split bands), a separate pass after the other kernels. The values
+    are bit-exact against the oracle's operand of the kernel's own output; sums and squares agree
+    to fp32 summation order."""
+    from qcheck import Q4Case, abs_gemm, bf16_tensor, check_close
+    case = Q4Case(n, k, seed=rows + n)
+    a_bits = oracle.bf16_normal((rows, k), seed=rows)
+    res = np.random.default_rng(rows).normal(size=(rows, n)).astype(np.float32)
+    wn = torch.from_numpy(np.random.default_rng(7).normal(1.0, 0.1, size=n).astype(np.float32)).to(torch.bfloat16).cuda()
+    out = torch.from_numpy(res.copy()).cuda()
+    got, values, sums, squares = rt.gemm_emit(case.w_tiled, bf16_tensor(a_bits), wn, out=out, residual=out)
+    ref = oracle.gemm_a_bf16_w_f32(a_bits, case.dense) + res
+    h = got.cpu().numpy()
+    check_close(h, ref, bf16_out=False, label=f"emit out rows={rows}")
+    want_v, want_s, want_q = oracle.emit_operand(h, _bits(wn))
+    assert np.array_equal(_bits(values), want_v)
+    np.testing.assert_allclose(sums.cpu().numpy(), want_s, rtol=1e-5, atol=1e-4)
+    np.testing.assert_allclose(squares.cpu().numpy(), want_q, rtol=1e-5)
