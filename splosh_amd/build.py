@@ -15,7 +15,7 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libsplosh_q4.so"
-SOURCES = ["api.cpp", "q4_basic.hip", "stream.hip", "lanes.hip", "decode.hip", "mma.hip", "tile.hip", "prefill.hip", "q5k.hip", "q5k_decode.hip", "operand.hip", "gguf_native.hip", "probe.hip"]
+SOURCES = ["api.cpp", "q4_basic.hip", "stream.hip", "lanes.hip", "decode.hip", "mma.hip", "tile.hip", "prefill.hip", "q5k.hip", "q5k_decode.hip", "operand.hip", "gguf_native.hip", "gguf_tile.hip", "probe.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"

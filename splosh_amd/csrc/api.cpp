@@ -492,15 +492,22 @@ static int gguf_gemm(const splosh_q5k_weight *w_in, bool fifth, const uint16_t *
                           aligned(w->meta, 16);
     const bool mma_ok = eligible && lda % 8 == 0 && aligned(a, 16) && splosh::q5k_mma_fits(rows, w->rows, w->inner, lda);
     const bool decode_ok = eligible && aligned(a, 16) && splosh::q5k_decode_fits(rows, w->rows, w->inner);
+    const bool tile_ok = eligible && lda % 8 == 0 && aligned(a, 16) && splosh::gguf_tile_fits(rows, w->rows, w->inner, lda);
     int choice = kernel;
     if (kernel == SPLOSH_KERNEL_AUTO) {
         if (!eligible) choice = SPLOSH_KERNEL_SCALAR;
         else if (decode_ok)
             return hip_status(splosh::launch_q5k_decode(*w, a, out, out_dtype, residual, stream), "q5k decode launch");
         else if (mma_ok) choice = SPLOSH_KERNEL_DEQUANT;
+        else if (tile_ok) choice = SPLOSH_KERNEL_TILE;
         else choice = SPLOSH_KERNEL_STREAM;
     }
     switch (choice) {
+        case SPLOSH_KERNEL_TILE:
+            if (!tile_ok) return fail(SPLOSH_ERR_UNSUPPORTED, "tile kernel needs lda % 8 == 0 and aligned operands");
+            return hip_status(splosh::launch_gguf_tile(fifth ? 13 : 12, w->plane0, w->plane1, w->meta, w->rows,
+                                                       w->inner, a, lda, out, ldc, out_dtype, residual, rows, stream),
+                              "gguf tile launch");
         case SPLOSH_KERNEL_STREAM: {
             if (!eligible) return fail(SPLOSH_ERR_UNSUPPORTED, "stream kernel needs lda % 4 == 0 and aligned planes");
             const splosh::StreamPlan plan = splosh::plan_stream(rows, w->rows, w->inner / 256, false, 2);
@@ -578,6 +585,12 @@ int splosh_gguf_gemm(int gguf_type, const uint8_t *native, int64_t rows, int64_t
     if ((st = check_io(a, lda, out, ldc, out_dtype, m, rows, inner))) return st;
     if (lda % 8 != 0 || !aligned(a, 16))
         return fail(SPLOSH_ERR_UNSUPPORTED, "GGUF native kernel needs lda % 8 == 0 and 16-byte aligned activations");
+    // Above four rows the tiled kernel decodes each weight group once per 64- or 128-row block
+    // instead of once per pass of four rows.
+    if (m > 4 && splosh::gguf_tile_fits(m, rows, inner, lda))
+        return hip_status(splosh::launch_gguf_tile(gguf_type, native, nullptr, nullptr, rows, inner, a, lda, out, ldc,
+                                                   out_dtype, residual, m, stream),
+                          "gguf tile launch");
     if (m > ((int64_t)65535 * 4)) return fail(SPLOSH_ERR_UNSUPPORTED, "too many activation rows for one launch");
     return hip_status(splosh::launch_gguf_gemv(gguf_type, native, rows, inner, a, lda, out, ldc, out_dtype, residual,
                                                m, stream),

@@ -41,7 +41,7 @@ def test_golden_block_on_device(rt, name):
 
 
 @pytest.mark.parametrize("name", list(TYPES))
-@pytest.mark.parametrize("rows", [1, 3, 4, 9])
+@pytest.mark.parametrize("rows", [1, 3, 4, 9, 65, 200])
 def test_native_gemm(rt, name, rows):
     t = TYPES[name]
     n, k = 200, 1536
@@ -76,6 +76,19 @@ def test_config0_size_sampled(rt, name):
     dense = oracle.gguf_decode(t, rows.reshape(-1)).reshape(len(cols), k)
     check_close(got[:, cols], oracle.gemm_a_bf16_w_f32(a_bits, dense), bf16_out=False, tight=True,
                 absref=abs_gemm(a_bits, dense), label=f"{name} config0")
+
+
+@pytest.mark.parametrize("name", list(TYPES))
+def test_tiled_large_grid(rt, name):
+    """Enough 128 x 128 blocks for the large tile shape, sampled activation rows."""
+    t = TYPES[name]
+    n, k, rows = 2048, 512, 512
+    w, dense = _weight(rt, t, n, k, seed=40 + t)
+    a_bits = oracle.bf16_normal((rows, k), seed=41)
+    got = rt.gemm(w, bf16_tensor(a_bits), out_dtype=torch.float32).cpu().numpy()
+    pick = np.sort(np.random.default_rng(42).choice(rows, 48, replace=False))
+    check_close(got[pick], oracle.gemm_a_bf16_w_f32(a_bits[pick], dense), bf16_out=False, tight=True,
+                absref=abs_gemm(a_bits[pick], dense), label=f"{name} tiled large")
 
 
 def test_from_gguf_file(rt, tmp_path):

@@ -78,7 +78,7 @@ def test_residual(rt):
     check_close(out.cpu().numpy(), ref, bf16_out=False, tight=True, absref=abs_gemm(a_bits, dense))
 
 
-@pytest.mark.parametrize("rows", [1, 16, 64])
+@pytest.mark.parametrize("rows", [1, 16, 64, 200])
 def test_baseline_shape_sampled(rt, rows):
     """Config 3: Q5_K down projection K=17408 -> N=5120 at full size, 256 sampled columns."""
     n, k = 5120, 17408
@@ -112,6 +112,41 @@ def test_dequant_kernel(rt, rows, split):
         got = rt.gemm(w, bf16_tensor(a_bits), out_dtype=out_dtype, kernel=rt.DEQUANT, workspace=ws)
         check_close(to_f32(got), ref, bf16_out=out_dtype == torch.bfloat16, tight=True, absref=absref,
                     label=f"q5k dequant rows={rows} split={split} {out_dtype}")
+
+
+@pytest.mark.parametrize("rows", [1, 65, 130, 300])
+def test_tile_kernel(rt, rows):
+    """The LDS-tiled kernel (AUTO above 64 rows): both tile shapes, ragged row and column blocks,
+    the residual."""
+    n, k = 384, 1280
+    native = oracle.q45k_random_native(n, k, seed=600 + rows)
+    w = rt.q5k_repack(dev_u8(native), n, k)
+    dense = oracle.q45k_decode(native).reshape(n, k)
+    a_bits = oracle.bf16_normal((rows, k), seed=700 + rows)
+    ref = oracle.gemm_a_bf16_w_f32(a_bits, dense)
+    absref = abs_gemm(a_bits, dense)
+    for out_dtype in (torch.bfloat16, torch.float32):
+        got = rt.gemm(w, bf16_tensor(a_bits), out_dtype=out_dtype, kernel=rt.TILE)
+        check_close(to_f32(got), ref, bf16_out=out_dtype == torch.bfloat16, tight=True, absref=absref,
+                    label=f"q5k tile rows={rows} {out_dtype}")
+    base = torch.from_numpy(oracle.bf16_normal((rows, n), seed=7).astype(np.float32)).cuda()
+    out = base.clone()
+    rt.gemm(w, bf16_tensor(a_bits), out=out, residual=out, kernel=rt.TILE)
+    check_close(out.cpu().numpy(), ref + base.cpu().numpy(), bf16_out=False, tight=True, absref=absref,
+                label=f"q5k tile residual rows={rows}")
+
+
+def test_tile_kernel_large_grid(rt):
+    """Enough 128 x 128 blocks for the large tile shape (AUTO at 512 rows), sampled rows."""
+    n, k, rows = 2048, 512, 512
+    native = oracle.q45k_random_native(n, k, seed=801)
+    w = rt.q5k_repack(dev_u8(native), n, k)
+    dense = oracle.q45k_decode(native).reshape(n, k)
+    a_bits = oracle.bf16_normal((rows, k), seed=802)
+    got = rt.gemm(w, bf16_tensor(a_bits), out_dtype=torch.float32).cpu().numpy()
+    pick = np.sort(np.random.default_rng(803).choice(rows, 48, replace=False))
+    check_close(got[pick], oracle.gemm_a_bf16_w_f32(a_bits[pick], dense), bf16_out=False, tight=True,
+                absref=abs_gemm(a_bits[pick], dense), label="q5k tile large")
 
 
 def test_dequant_kernel_remainder_bands_and_residual(rt):
