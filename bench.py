@@ -328,10 +328,11 @@ def build_workload(name, rt, torch, gen, kernel):
         x = torch.randn(m, k, device="cuda", generator=gen).to(torch.bfloat16)
         out = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
         b = one + m * k * 2 + m * n * 2
+        ws_g = workspace(m, n, k)
 
         def launches(i):
             w = ws[i % ncopy]
-            return [("gguf", lambda: rt.gemm(w, x, out=out))]
+            return [("gguf", lambda: rt.gemm(w, x, out=out, workspace=ws_g))]
 
         cfg = {"workload": f"{label} K17408->N5120 (native blocks)", "rows": m, "format": f"gguf {label.lower()}",
                "weight_copies": ncopy}

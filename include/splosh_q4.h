@@ -250,14 +250,18 @@ int splosh_q4k_dequant(const splosh_q5k_weight *w, float *out, hipStream_t strea
  * for these formats (Engine.swift:1673-1694 dispatching sp_gguf_* by format,
  * engine_gguf.metal:332-349) and GgufTensorType.decode (GgufQuant.swift:136-159).
  *
- * splosh_gguf_gemm: out[m][n] = sum_k a[m][k] w[n][k] (+ residual), rows of activations in
- * passes of four over the weight (a streaming kernel for decode-sized row counts).
+ * splosh_gguf_gemm: out[m][n] = sum_k a[m][k] w[n][k] (+ residual). Up to four activation rows
+ * a streaming kernel reads the weight once; more rows (inner % 64 == 0) go to an LDS-tiled MFMA
+ * kernel that decodes each weight group once per 64, 128 or 256 activation rows, and splits K over
+ * workgroups when its tiles are few and a workspace of splosh_workspace_bytes(m, rows, inner) is
+ * given (zero-filled before first use; the kernel leaves its counters zeroed, so one workspace
+ * serves every later call; null: no split).
  * splosh_gguf_dequant: the weight as fp32 [rows][inner], bit-exact with the reference decoder.
  * `native` must be 4-byte aligned (GGUF tensor data is 32-byte aligned).
  * Unsupported types return SPLOSH_ERR_UNSUPPORTED. */
 int splosh_gguf_gemm(int gguf_type, const uint8_t *native, int64_t rows, int64_t inner, const uint16_t *a,
                      int64_t lda, void *out, int64_t ldc, int out_dtype, const void *residual, int64_t m,
-                     hipStream_t stream);
+                     void *workspace, size_t workspace_bytes, hipStream_t stream);
 int splosh_gguf_dequant(int gguf_type, const uint8_t *native, int64_t rows, int64_t inner, float *out,
                         hipStream_t stream);
 

@@ -98,7 +98,7 @@ SIGNATURES = {
     "splosh_q4k_gemm": (_int, [ctypes.POINTER(Q5KWeight), _vp, _i64, _vp, _i64, _int, _vp, _i64, _int, _vp, _sz,
                                _vp]),
     "splosh_q4k_dequant": (_int, [ctypes.POINTER(Q5KWeight), _vp, _vp]),
-    "splosh_gguf_gemm": (_int, [_int, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _int, _vp, _i64, _vp]),
+    "splosh_gguf_gemm": (_int, [_int, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _int, _vp, _i64, _vp, _sz, _vp]),
     "splosh_gguf_dequant": (_int, [_int, _vp, _i64, _i64, _vp, _vp]),
     "splosh_q4k_repack": (_int, [_vp, _i64, _i64, _vp, _vp, _vp]),
     "splosh_q4k_unpack": (_int, [_vp, _vp, _i64, _i64, _vp, _vp]),

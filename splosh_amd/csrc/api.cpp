@@ -355,8 +355,10 @@ size_t splosh_workspace_bytes(int64_t rows, int64_t columns, int64_t inner) {
     const size_t tile = splosh::tile_workspace_bytes(rows, columns, groups, true);
     const size_t mma = rows <= 64 ? splosh::mma_workspace_bytes(rows, columns, groups, true) : 0;
     const size_t prefill = rows > 64 && columns % 128 == 0 ? splosh::prefill_workspace_bytes(rows, columns, groups) : 0;
-    const size_t need = tile > mma ? tile : mma;
-    return need > prefill ? need : prefill;
+    const size_t gguf = inner % 64 == 0 ? splosh::gguf_tile_workspace_bytes(rows, columns, inner) : 0;
+    size_t need = tile > mma ? tile : mma;
+    need = need > prefill ? need : prefill;
+    return need > gguf ? need : gguf;
 }
 
 // Q4GemmRuntime.dispatch (Runtime/Q4Runtime.swift:94-145).
@@ -506,7 +508,8 @@ static int gguf_gemm(const splosh_q5k_weight *w_in, bool fifth, const uint16_t *
         case SPLOSH_KERNEL_TILE:
             if (!tile_ok) return fail(SPLOSH_ERR_UNSUPPORTED, "tile kernel needs lda % 8 == 0 and aligned operands");
             return hip_status(splosh::launch_gguf_tile(fifth ? 13 : 12, w->plane0, w->plane1, w->meta, w->rows,
-                                                       w->inner, a, lda, out, ldc, out_dtype, residual, rows, stream),
+                                                       w->inner, a, lda, out, ldc, out_dtype, residual, rows,
+                                                       workspace, workspace_bytes, stream),
                               "gguf tile launch");
         case SPLOSH_KERNEL_STREAM: {
             if (!eligible) return fail(SPLOSH_ERR_UNSUPPORTED, "stream kernel needs lda % 4 == 0 and aligned planes");
@@ -579,17 +582,17 @@ static int check_gguf_native(int type, const uint8_t *native, int64_t rows, int6
 
 int splosh_gguf_gemm(int gguf_type, const uint8_t *native, int64_t rows, int64_t inner, const uint16_t *a,
                      int64_t lda, void *out, int64_t ldc, int out_dtype, const void *residual, int64_t m,
-                     hipStream_t stream) {
+                     void *workspace, size_t workspace_bytes, hipStream_t stream) {
     int st = check_gguf_native(gguf_type, native, rows, inner);
     if (st) return st;
     if ((st = check_io(a, lda, out, ldc, out_dtype, m, rows, inner))) return st;
     if (lda % 8 != 0 || !aligned(a, 16))
         return fail(SPLOSH_ERR_UNSUPPORTED, "GGUF native kernel needs lda % 8 == 0 and 16-byte aligned activations");
-    // Above four rows the tiled kernel decodes each weight group once per 64- or 128-row block
-    // instead of once per pass of four rows.
-    if (m > 4 && splosh::gguf_tile_fits(m, rows, inner, lda))
+    // Above eight rows the tiled kernel (each weight group decoded once per 64 to 256 rows) is the
+    // faster; up to eight, one or two passes of the streaming kernel.
+    if (m > 8 && splosh::gguf_tile_fits(m, rows, inner, lda))
         return hip_status(splosh::launch_gguf_tile(gguf_type, native, nullptr, nullptr, rows, inner, a, lda, out, ldc,
-                                                   out_dtype, residual, m, stream),
+                                                   out_dtype, residual, m, workspace, workspace_bytes, stream),
                           "gguf tile launch");
     if (m > ((int64_t)65535 * 4)) return fail(SPLOSH_ERR_UNSUPPORTED, "too many activation rows for one launch");
     return hip_status(splosh::launch_gguf_gemv(gguf_type, native, rows, inner, a, lda, out, ldc, out_dtype, residual,

@@ -70,45 +70,147 @@ __constant__ uint16_t kIq3sPacked[512] = {
 
 __device__ __forceinline__ uint32_t ld16(rsrc_t r, uint32_t off) { return buffer_load_u16(r, off, 0); }
 
-// W dwords of bytes starting at a 2-aligned `off` (all 4 W of them inside the weight): the dword-aligned window that covers them (W + 1
-// dwords, the first in 16-byte pieces; buffer loads need only dword alignment) shifted into place
-// by the lane's 0- or 2-byte misalignment (v_alignbyte_b32). Every byte read lies in the weight.
+// W dwords of bytes starting at a 2-aligned `off` (all 4 W of them inside the weight), fetched as
+// the dword-aligned window that covers them (W + 1 dwords, the first in 16-byte pieces; buffer
+// loads need only dword alignment) and, at decode, shifted into place by the 0- or 2-byte
+// misalignment (v_alignbyte_b32). Every byte read lies in the weight.
 template <int W>
-__device__ __forceinline__ void load_span(rsrc_t r, uint32_t off, uint32_t (&out)[W]) {
-    const uint32_t a0 = off & ~3u, sh = off & 3u;
+struct Span {
     uint32_t win[W + 1];
+    uint32_t sh;
+};
+template <int W>
+__device__ __forceinline__ Span<W> fetch_span(rsrc_t r, uint32_t off) {
+    Span<W> s;
+    const uint32_t a0 = off & ~3u;
+    s.sh = off & 3u;
 #pragma unroll
     for (int q = 0; q < (W + 1) / 4; ++q) {
         const u32x4 x = buffer_load16(r, a0 + 16u * q, 0);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) win[4 * q + e] = x[e];
+        for (int e = 0; e < 4; ++e) s.win[4 * q + e] = x[e];
     }
 #pragma unroll
-    for (int e = (W + 1) / 4 * 4; e < W; ++e) win[e] = buffer_load_u32(r, a0 + 4u * e, 0);
+    for (int e = (W + 1) / 4 * 4; e < W; ++e) s.win[e] = buffer_load_u32(r, a0 + 4u * e, 0);
     // Only the low half of the last window dword is ever used (when off is 2 mod 4), and its high
     // half may lie past the weight, where a dword load would read zero for the whole dword.
-    win[W] = buffer_load_u16(r, a0 + 4u * W, 0);
+    s.win[W] = buffer_load_u16(r, a0 + 4u * W, 0);
+    return s;
+}
+template <int W>
+__device__ __forceinline__ void align_span(const Span<W> &s, uint32_t (&out)[W]) {
 #pragma unroll
-    for (int i = 0; i < W; ++i) out[i] = __builtin_amdgcn_alignbyte(win[i + 1], win[i], sh);
+    for (int i = 0; i < W; ++i) out[i] = __builtin_amdgcn_alignbyte(s.win[i + 1], s.win[i], s.sh);
 }
 template <int W>
 __device__ __forceinline__ uint32_t byte_of(const uint32_t (&w)[W], int e) { return (w[e >> 2] >> (8 * (e & 3))) & 0xFF; }
 
-// Group g of a row whose blocks start at byte `row` (GgufQuant.swift decode, fp32 op order).
+// Each native format's group decoder in two halves: gguf_fetch issues every load of group g of a
+// row whose blocks start at byte `row` and returns the raw bytes (GgufRaw<TYPE>); gguf_decode turns
+// them into the 32 values with no memory access, so that a kernel can fetch one step ahead.
+// Values follow GgufQuant.swift's decode in its fp32 operation order.
 template <int TYPE>
-__device__ __forceinline__ void decode_group(rsrc_t r, uint32_t row, int g, float (&v)[32]) {
-    if constexpr (TYPE == 8) {  // Q8_0 (GgufQuant.swift:172-175)
+struct GgufRaw;
+
+template <>
+struct GgufRaw<8> {  // Q8_0 (GgufQuant.swift:172-175): d, 32 int8 codes
+    uint32_t d;
+    Span<8> codes;
+};
+template <>
+struct GgufRaw<20> {  // IQ4_NL (:179-185): d, 16 bytes of two 4-bit codes
+    uint32_t d;
+    Span<4> codes;
+};
+template <>
+struct GgufRaw<14> {  // Q6_K (:218-230): ql[128], qh[64], scales[16], d
+    uint32_t d, sc;
+    Span<8> ql, qh;
+    int j;
+};
+template <>
+struct GgufRaw<11> {  // Q3_K (:238-256): hmask[32], qs[64], scales[12], d
+    uint32_t d, lows, highs;
+    Span<8> hm, qs;
+    int j;
+};
+template <>
+struct GgufRaw<21> {  // IQ3_S (:283-300): d, qs[64], qh[8], signs[32], scales[4]
+    uint32_t d, scale, ninth;
+    Span<2> cb;
+    Span<1> sg;
+    int j;
+};
+template <>
+struct GgufRaw<23> {  // IQ4_XS (:261-275): d, scales_h, scales_l[4], qs[128]
+    uint32_t d, high, lowb;
+    u32x4 q;
+    int j;
+};
+
+template <int TYPE>
+__device__ __forceinline__ GgufRaw<TYPE> gguf_fetch(rsrc_t r, uint32_t row, int g) {
+    GgufRaw<TYPE> w;
+    if constexpr (TYPE == 8) {
         const uint32_t b = row + (uint32_t)g * 34u;
-        const float d = half_bits_to_f32(ld16(r, b));
-        uint32_t h[8];   // the 32 codes
-        load_span<8>(r, b + 2, h);
+        w.d = ld16(r, b);
+        w.codes = fetch_span<8>(r, b + 2);
+    } else if constexpr (TYPE == 20) {
+        const uint32_t b = row + (uint32_t)g * 18u;
+        w.d = ld16(r, b);
+        w.codes = fetch_span<4>(r, b + 2);
+    } else if constexpr (TYPE == 14) {
+        const int j = g & 7, half = j >> 2, quarter = j & 3;
+        const uint32_t b = row + (uint32_t)(g >> 3) * 210u;
+        w.j = j;
+        w.d = ld16(r, b + 208);
+        w.sc = ld16(r, b + 192 + 2 * j);
+        w.ql = fetch_span<8>(r, b + 64 * half + 32 * (quarter & 1));
+        w.qh = fetch_span<8>(r, b + 128 + 32 * half);
+    } else if constexpr (TYPE == 11) {
+        const int j = g & 7, half = j >> 2, word = j >> 1;
+        const uint32_t b = row + (uint32_t)(g >> 3) * 110u;
+        w.j = j;
+        w.d = ld16(r, b + 108);
+        // Scales 2 j and 2 j + 1: bytes 2 (j % 2), 2 (j % 2) + 1 of word j / 2 % 2 (their low or
+        // high nibbles) and of the third word (bits 2 (j / 2)).
+        w.lows = ld16(r, b + 96 + 4 * (word & 1) + 2 * (j & 1));
+        w.highs = ld16(r, b + 104 + 2 * (j & 1));
+        w.hm = fetch_span<8>(r, b);
+        w.qs = fetch_span<8>(r, b + 32 + 32 * half);
+    } else if constexpr (TYPE == 21) {
+        const int j = g & 7;
+        const uint32_t b = row + (uint32_t)(g >> 3) * 110u;
+        w.j = j;
+        w.d = ld16(r, b);
+        w.scale = ld16(r, b + 106 + 2 * (j >> 2));
+        w.ninth = ld16(r, b + 66 + (j & ~1));
+        w.cb = fetch_span<2>(r, b + 2 + 8 * j);
+        w.sg = fetch_span<1>(r, b + 74 + 4 * j);
+    } else {
+        const int j = g & 7;
+        const uint32_t b = row + (uint32_t)(g >> 3) * 136u;
+        w.j = j;
+        w.d = ld16(r, b);
+        w.high = ld16(r, b + 2);
+        w.lowb = ld16(r, b + 4 + 2 * (j >> 2));  // bytes 4 + 2 (j / 4) .. + 1
+        w.q = buffer_load16(r, b + 8 + 16 * j, 0);  // blocks of 136 bytes: 8-aligned runs
+    }
+    return w;
+}
+
+template <int TYPE>
+__device__ __forceinline__ void gguf_decode(const GgufRaw<TYPE> &w, float (&v)[32]) {
+    if constexpr (TYPE == 8) {
+        const float d = half_bits_to_f32(w.d);
+        uint32_t h[8];
+        align_span(w.codes, h);
 #pragma unroll
         for (int e = 0; e < 32; ++e) v[e] = d * (float)(int8_t)byte_of(h, e);
-    } else if constexpr (TYPE == 20) {  // IQ4_NL (:179-185)
-        const uint32_t b = row + (uint32_t)g * 18u;
-        const float d = half_bits_to_f32(ld16(r, b));
-        uint32_t h[4];   // 16 bytes of two codes
-        load_span<4>(r, b + 2, h);
+    } else if constexpr (TYPE == 20) {
+        const float d = half_bits_to_f32(w.d);
+        uint32_t h[4];
+        align_span(w.codes, h);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const uint32_t lo = iq4_lookup4(h[q] & 0x0F0F0F0Fu), hi = iq4_lookup4((h[q] >> 4) & 0x0F0F0F0Fu);
@@ -118,15 +220,13 @@ __device__ __forceinline__ void decode_group(rsrc_t r, uint32_t row, int g, floa
                 v[16 + 4 * q + e] = d * (float)(int8_t)((hi >> (8 * e)) & 0xFF);
             }
         }
-    } else if constexpr (TYPE == 14) {  // Q6_K (:218-230): ql[128], qh[64], scales[16], d
-        const int j = g & 7, half = j >> 2, quarter = j & 3;
-        const uint32_t b = row + (uint32_t)(g >> 3) * 210u;
-        const float d = half_bits_to_f32(ld16(r, b + 208));
-        const uint32_t sc = ld16(r, b + 192 + 2 * j);
-        const float ds0 = d * (float)(int8_t)(sc & 0xFF), ds1 = d * (float)(int8_t)(sc >> 8);
+    } else if constexpr (TYPE == 14) {
+        const int quarter = w.j & 3;
+        const float d = half_bits_to_f32(w.d);
+        const float ds0 = d * (float)(int8_t)(w.sc & 0xFF), ds1 = d * (float)(int8_t)(w.sc >> 8);
         uint32_t ql[8], qh[8];
-        load_span<8>(r, b + 64 * half + 32 * (quarter & 1), ql);
-        load_span<8>(r, b + 128 + 32 * half, qh);
+        align_span(w.ql, ql);
+        align_span(w.qh, qh);
         const int lsh = 4 * (quarter >> 1), hsh = 2 * quarter;
 #pragma unroll
         for (int e = 0; e < 32; ++e) {
@@ -134,36 +234,31 @@ __device__ __forceinline__ void decode_group(rsrc_t r, uint32_t row, int g, floa
             const float code = (float)(low | (high << 4)) - 32.0f;
             v[e] = (e < 16 ? ds0 : ds1) * code;
         }
-    } else if constexpr (TYPE == 11) {  // Q3_K (:238-256): hmask[32], qs[64], scales[12], d
-        const int j = g & 7, half = j >> 2, shift = 2 * (j & 3), word = j >> 1;
-        const uint32_t b = row + (uint32_t)(g >> 3) * 110u;
-        const float d = half_bits_to_f32(ld16(r, b + 108));
-        // Scales 2 j and 2 j + 1: bytes 2 (j % 2), 2 (j % 2) + 1 of word j / 2 % 2 (their low or high
-        // nibbles) and of the third word (bits 2 (j / 2)).
-        const uint32_t lows = ld16(r, b + 96 + 4 * (word & 1) + 2 * (j & 1)) >> (4 * (word >> 1));
-        const uint32_t highs = ld16(r, b + 104 + 2 * (j & 1)) >> (2 * word);
+    } else if constexpr (TYPE == 11) {
+        const int j = w.j, shift = 2 * (j & 3), word = j >> 1;
+        const float d = half_bits_to_f32(w.d);
+        const uint32_t lows = w.lows >> (4 * (word >> 1)), highs = w.highs >> (2 * word);
         const float s0 = (float)((lows & 0xF) | ((highs & 3) << 4)) - 32.0f;
         const float s1 = (float)(((lows >> 8) & 0xF) | (((highs >> 8) & 3) << 4)) - 32.0f;
         const float ds0 = d * s0, ds1 = d * s1;
         uint32_t hm[8], qs[8];
-        load_span<8>(r, b, hm);
-        load_span<8>(r, b + 32 + 32 * half, qs);
+        align_span(w.hm, hm);
+        align_span(w.qs, qs);
 #pragma unroll
         for (int e = 0; e < 32; ++e) {
             const uint32_t low = (byte_of(qs, e) >> shift) & 3, high = (byte_of(hm, e) >> j) & 1;
             const float code = (float)(low | (high << 2)) - 4.0f;
             v[e] = (e < 16 ? ds0 : ds1) * code;
         }
-    } else if constexpr (TYPE == 21) {  // IQ3_S (:283-300): d, qs[64], qh[8], signs[32], scales[4]
-        const int j = g & 7;
-        const uint32_t b = row + (uint32_t)(g >> 3) * 110u;
-        const float d = half_bits_to_f32(ld16(r, b));
-        const uint32_t scale = (ld16(r, b + 106 + 2 * (j >> 2)) >> (8 * ((j >> 1) & 1) + 4 * (j & 1))) & 15;
+    } else if constexpr (TYPE == 21) {
+        const int j = w.j;
+        const float d = half_bits_to_f32(w.d);
+        const uint32_t scale = (w.scale >> (8 * ((j >> 1) & 1) + 4 * (j & 1))) & 15;
         const float weight = d * (1.0f + 2.0f * (float)scale);
-        const uint32_t ninth = (ld16(r, b + 66 + (j & ~1)) >> (8 * (j & 1))) & 0xFF;
+        const uint32_t ninth = (w.ninth >> (8 * (j & 1))) & 0xFF;
         uint32_t cb[2], sg[1];
-        load_span<2>(r, b + 2 + 8 * j, cb);
-        load_span<1>(r, b + 74 + 4 * j, sg);
+        align_span(w.cb, cb);
+        align_span(w.sg, sg);
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             const uint32_t code = ((cb[k >> 2] >> (8 * (k & 3))) & 0xFF) | (((ninth >> k) & 1) << 8);
@@ -176,17 +271,13 @@ __device__ __forceinline__ void decode_group(rsrc_t r, uint32_t row, int g, floa
                 v[e] = (weight * magnitude) * sign;
             }
         }
-    } else {  // IQ4_XS (:261-275): d, scales_h, scales_l[4], qs[128]
-        const int j = g & 7;
-        const uint32_t b = row + (uint32_t)(g >> 3) * 136u;
-        const float d = half_bits_to_f32(ld16(r, b));
-        const uint32_t high = ld16(r, b + 2);
-        const uint32_t lowb = ld16(r, b + 4 + 2 * (j >> 2));   // bytes 4 + 2 (j / 4) .. + 1
-        const uint32_t low = (lowb >> (8 * ((j >> 1) & 1) + 4 * (j & 1))) & 15;
-        const uint32_t scale = low | (((high >> (2 * j)) & 3) << 4);
+    } else {
+        const int j = w.j;
+        const float d = half_bits_to_f32(w.d);
+        const uint32_t low = (w.lowb >> (8 * ((j >> 1) & 1) + 4 * (j & 1))) & 15;
+        const uint32_t scale = low | (((w.high >> (2 * j)) & 3) << 4);
         const float scaled = d * ((float)scale - 32.0f);
-        const u32x4 q = buffer_load16(r, b + 8 + 16 * j, 0);   // blocks of 136 bytes: 8-aligned runs
-        const uint32_t qs[4] = {q[0], q[1], q[2], q[3]};
+        const uint32_t qs[4] = {w.q[0], w.q[1], w.q[2], w.q[3]};
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const uint32_t lo = iq4_lookup4(qs[k] & 0x0F0F0F0Fu), hi = iq4_lookup4((qs[k] >> 4) & 0x0F0F0F0Fu);
@@ -199,23 +290,39 @@ __device__ __forceinline__ void decode_group(rsrc_t r, uint32_t row, int g, floa
     }
 }
 
+// Group g of a row whose blocks start at byte `row`: fetch and decode at once.
+template <int TYPE>
+__device__ __forceinline__ void decode_group(rsrc_t r, uint32_t row, int g, float (&v)[32]) {
+    gguf_decode<TYPE>(gguf_fetch<TYPE>(r, row, g), v);
+}
+
 
 // Group g of row `row` of a Q5_K / Q4_K weight in plane form (GgufPlanes.swift:62-74; plane1 null:
 // Q4_K), as decodeQ45K computes it (GgufQuant.swift:191-212): code (low nibble, fifth bit) times
 // d sc, less dmin mn.
 __device__ __forceinline__ int plane_slot(int e) { return 8 * ((e >> 2) & 3) + 4 * (e >> 4) + (e & 3); }
-__device__ __forceinline__ void decode_plane_group(const uint8_t *plane0, const uint8_t *plane1, const uint8_t *meta,
-                                                   int64_t inner, int64_t row, int64_t g, float (&v)[32]) {
+struct PlaneRaw {
+    u32x4 words, m;  // the group's 16 bytes of low nibbles; its block's 16 bytes of meta
+    uint32_t bits;   // the group's 32 fifth bits (0 for Q4_K)
+    int j;           // the group within its block
+};
+__device__ __forceinline__ PlaneRaw fetch_plane_group(const uint8_t *plane0, const uint8_t *plane1,
+                                                      const uint8_t *meta, int64_t inner, int64_t row, int64_t g) {
+    PlaneRaw w;
     const int64_t groups = inner / 32, blocks = inner / 256;
     const int64_t rec = ((row >> 7) * groups + g) * 128 + (row & 127);
-    const u32x4 words = *(const u32x4 *)(plane0 + rec * 16);
-    const uint32_t bits = plane1 ? *(const uint32_t *)(plane1 + rec * 4) : 0u;
+    w.words = *(const u32x4 *)(plane0 + rec * 16);
+    w.bits = plane1 ? *(const uint32_t *)(plane1 + rec * 4) : 0u;
     const int64_t mrec = ((row >> 7) * blocks + g / 8) * 128 + (row & 127);
-    const u32x4 m = *(const u32x4 *)(meta + mrec * 16);
-    const int j = (int)(g % 8);
-    const float d = half_bits_to_f32(m[0]), dmin = half_bits_to_f32(m[0] >> 16);
+    w.m = *(const u32x4 *)(meta + mrec * 16);
+    w.j = (int)(g % 8);
+    return w;
+}
+__device__ __forceinline__ void decode_plane(const PlaneRaw &w, float (&v)[32]) {
+    const int j = w.j;
+    const float d = half_bits_to_f32(w.m[0]), dmin = half_bits_to_f32(w.m[0] >> 16);
     // Packed 6-bit scale and minimum of group j (bytes 4..15 of the block = m[1..3]).
-    auto pk = [&](int k) { return (m[1 + (k >> 2)] >> (8 * (k & 3))) & 0xFFu; };
+    auto pk = [&](int k) { return (w.m[1 + (k >> 2)] >> (8 * (k & 3))) & 0xFFu; };
     uint32_t sc, mn;
     if (j < 4) {
         sc = pk(j) & 63u;
@@ -228,10 +335,15 @@ __device__ __forceinline__ void decode_plane_group(const uint8_t *plane0, const 
 #pragma unroll
     for (int e = 0; e < 32; ++e) {
         const int slot = plane_slot(e), i = slot & 7;
-        const uint32_t code = ((words[slot >> 3] >> ((i & 1) * 16 + 4 * (i >> 1))) & 15u) | (((bits >> slot) & 1u) << 4);
+        const uint32_t code =
+            ((w.words[slot >> 3] >> ((i & 1) * 16 + 4 * (i >> 1))) & 15u) | (((w.bits >> slot) & 1u) << 4);
         const float p = (float)code * scaled;
         v[e] = p - offset;
     }
+}
+__device__ __forceinline__ void decode_plane_group(const uint8_t *plane0, const uint8_t *plane1, const uint8_t *meta,
+                                                   int64_t inner, int64_t row, int64_t g, float (&v)[32]) {
+    decode_plane(fetch_plane_group(plane0, plane1, meta, inner, row, g), v);
 }
 
 }  // namespace splosh

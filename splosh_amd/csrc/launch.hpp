@@ -96,11 +96,16 @@ hipError_t launch_gguf_embed(int type, const uint8_t *w, int64_t rows, int64_t i
 hipError_t launch_q5k_embed(const splosh_q5k_weight &w, const uint32_t *tokens, int64_t count, void *out, int64_t ldo,
                             int out_dtype, hipStream_t stream);
 // The LDS-tiled MFMA GEMM for GGUF weights (gguf_tile.hip): type a native-block ggml id, or 13 / 12
-// for Q5_K / Q4_K planes (w = plane0). Needs inner % 64 == 0 and lda % 8 == 0.
+// for Q5_K / Q4_K planes (w = plane0). Needs inner % 64 == 0 and lda % 8 == 0. With a workspace
+// (zero-filled before first use, left zeroed) it splits K over workgroups when the tiles are few.
 bool gguf_tile_fits(int64_t rows, int64_t columns, int64_t inner, int64_t lda);
 hipError_t launch_gguf_tile(int type, const uint8_t *w, const uint8_t *plane1, const uint8_t *meta, int64_t rows_w,
                             int64_t inner, const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype,
-                            const void *residual, int64_t m, hipStream_t stream);
+                            const void *residual, int64_t m, void *workspace, size_t workspace_bytes,
+                            hipStream_t stream);
+// Workspace that lets the tiled kernel split K (0: it would not split): arrival counters in the
+// first 16 KiB, fp32 partials after.
+size_t gguf_tile_workspace_bytes(int64_t rows, int64_t n, int64_t inner);
 hipError_t launch_gguf_gemv(int type, const uint8_t *w, int64_t rows, int64_t inner, const uint16_t *a, int64_t lda,
                             void *out, int64_t ldc, int out_dtype, const void *residual, int64_t m,
                             hipStream_t stream);

@@ -210,13 +210,13 @@ def gemm(w, a, out=None, residual=None, out_dtype=torch.bfloat16, kernel=AUTO, r
     if residual is not None:
         if residual.dtype != out.dtype or residual.stride(0) != out.stride(0):
             raise SploshError(13, "residual must match the output's dtype and row stride")
+    ws, ws_bytes = _workspace(workspace, rows, w.rows, w.inner, a.device, stream)
     if isinstance(w, GgufWeight):
         _lib.check(_lib.lib().splosh_gguf_gemm(w.gguf_type, _ptr(w.native), w.rows, w.inner, _ptr(a), a.stride(0),
                                                _ptr(out), out.stride(0), _dtype_code(out.dtype), _ptr(residual),
-                                               rows, _stream(stream)))
+                                               rows, ws, ws_bytes, _stream(stream)))
         return out
     wc = w.c()
-    ws, ws_bytes = _workspace(workspace, rows, w.rows, w.inner, a.device, stream)
     if isinstance(w, Q4Weight):
         st = _lib.lib().splosh_q4_gemm(ctypes.byref(wc), _ptr(a), a.stride(0), _ptr(out), out.stride(0),
                                        _dtype_code(out.dtype), _ptr(residual), rows, kernel, ws, ws_bytes,

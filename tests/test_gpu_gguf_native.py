@@ -91,6 +91,23 @@ def test_tiled_large_grid(rt, name):
                 absref=abs_gemm(a_bits[pick], dense), label=f"{name} tiled large")
 
 
+def test_tiled_workspace_reuse_and_no_split(rt):
+    """One workspace reused across shapes and formats (the split kernel leaves its counters zeroed),
+    and the unsplit kernel (an empty workspace)."""
+    k = 2048
+    ws = torch.zeros(rt.workspace_bytes(64, 512, k), dtype=torch.uint8, device="cuda")
+    for name, n, rows in (("q6K", 512, 64), ("q8_0", 256, 9), ("q6K", 512, 33), ("iq4XS", 384, 64), ("q8_0", 100, 70)):
+        t = TYPES[name]
+        w, dense = _weight(rt, t, n, k, seed=n + rows)
+        a_bits = oracle.bf16_normal((rows, k), seed=rows)
+        ref = oracle.gemm_a_bf16_w_f32(a_bits, dense)
+        for space in (ws, torch.empty(0, dtype=torch.uint8, device="cuda")):
+            got = rt.gemm(w, bf16_tensor(a_bits), out_dtype=torch.float32, workspace=space)
+            check_close(got.cpu().numpy(), ref, bf16_out=False, tight=True, absref=abs_gemm(a_bits, dense),
+                        label=f"{name} n={n} rows={rows} split={space.numel() > 0}")
+    assert not ws[:16384].any(), "arrival counters left nonzero"
+
+
 def test_from_gguf_file(rt, tmp_path):
     n, k = 96, 512
     tensors, dense = [], {}
@@ -116,12 +133,12 @@ def test_rejects_other_types_and_bad_shapes(rt):
     lib = _lib.lib()
     for t in (0, 2, 12, 13):   # f32, Q4_0; Q4_K and Q5_K take the plane form, not native blocks
         st = lib.splosh_gguf_gemm(t, native.data_ptr(), 64, 512, a.data_ptr(), 512, out.data_ptr(), 64,
-                                  _lib.F32, None, 1, None)
+                                  _lib.F32, None, 1, None, 0, None)
         assert st != 0
     st = lib.splosh_gguf_gemm(8, native.data_ptr(), 64, 500, a.data_ptr(), 512, out.data_ptr(), 64, _lib.F32,
-                              None, 1, None)
+                              None, 1, None, 0, None)
     assert st != 0
     # A native pointer that is not 4-byte aligned is refused (the kernels read dword windows).
     st = lib.splosh_gguf_gemm(8, native.data_ptr() + 2, 64, 512, a.data_ptr(), 512, out.data_ptr(), 64, _lib.F32,
-                              None, 1, None)
+                              None, 1, None, 0, None)
     assert st == 2  # layoutMismatch
