@@ -16,9 +16,10 @@
 //    column slice split a step's K by 64-element slices and the CW column slices of a workgroup
 //    share one activation chunk of KW slices, staged in LDS once per step: activations are read
 //    from L2 once per workgroup.
-//  * Weight codes are loaded three steps ahead into a register ring; the activation chunk one step
-//    ahead into registers, then stored to one of three LDS buffers, and so are per-band sidecars
-//    or block metadata. One barrier per step, in its middle.
+//  * Weight codes are loaded three steps ahead into a register ring; the activation chunk and the
+//    per-band sidecars (or block metadata) go straight from memory into one of four LDS buffers
+//    (buffer loads with the LDS modifier), three steps ahead, ordered by counted vmcnt waits. One
+//    barrier per step, in its middle.
 //  * At the end of a job the KW partial sums meet in LDS and the workgroup writes whole output
 //    rows. With a workspace, the (band, unit) pairs of all bands form one stream cut into equal
 //    contiguous ranges, one a workgroup (stream-K); a band shared by several workgroups is summed
