@@ -651,11 +651,20 @@ int splosh_gguf_embed(int gguf_type, const uint8_t *native, int64_t rows, int64_
                       "gguf native embed launch");
 }
 
+// The repack kernels move native blocks in dwords and plane records in 16-byte pieces.
+static int check_plane_alignment(const uint8_t *native, const uint8_t *plane0, const uint8_t *plane1,
+                                 const uint8_t *meta) {
+    if (!aligned(native, 4) || !aligned(plane0, 16) || (plane1 && !aligned(plane1, 4)) || !aligned(meta, 16))
+        return fail(SPLOSH_ERR_LAYOUT_MISMATCH, "native blocks need 4-byte, plane0 and meta 16-byte, plane1 4-byte alignment");
+    return ok();
+}
+
 int splosh_q5k_repack(const uint8_t *native, int64_t rows, int64_t inner, uint8_t *plane0, uint8_t *plane1,
                       uint8_t *meta, hipStream_t stream) {
     if (!native || !plane0 || !plane1 || !meta) return fail(SPLOSH_ERR_NULL_POINTER, "null buffer");
     if (rows <= 0 || inner <= 0 || rows % 128 != 0 || inner % 256 != 0)
         return fail(SPLOSH_ERR_LAYOUT_MISMATCH, "Q5_K planes need rows % 128 == 0 and inner % 256 == 0");
+    if (int st = check_plane_alignment(native, plane0, plane1, meta)) return st;
     return hip_status(splosh::launch_q5k_repack(native, rows, inner, plane0, plane1, meta, false, stream),
                       "q5k repack launch");
 }
@@ -665,6 +674,7 @@ int splosh_q4k_repack(const uint8_t *native, int64_t rows, int64_t inner, uint8_
     if (!native || !plane0 || !meta) return fail(SPLOSH_ERR_NULL_POINTER, "null buffer");
     if (rows <= 0 || inner <= 0 || rows % 128 != 0 || inner % 256 != 0)
         return fail(SPLOSH_ERR_LAYOUT_MISMATCH, "Q4_K planes need rows % 128 == 0 and inner % 256 == 0");
+    if (int st = check_plane_alignment(native, plane0, nullptr, meta)) return st;
     return hip_status(splosh::launch_q5k_repack(native, rows, inner, plane0, nullptr, meta, false, stream, false),
                       "q4k repack launch");
 }
@@ -674,6 +684,7 @@ int splosh_q4k_unpack(const uint8_t *plane0, const uint8_t *meta, int64_t rows, 
     if (!native || !plane0 || !meta) return fail(SPLOSH_ERR_NULL_POINTER, "null buffer");
     if (rows <= 0 || inner <= 0 || rows % 128 != 0 || inner % 256 != 0)
         return fail(SPLOSH_ERR_LAYOUT_MISMATCH, "Q4_K planes need rows % 128 == 0 and inner % 256 == 0");
+    if (int st = check_plane_alignment(native, plane0, nullptr, meta)) return st;
     return hip_status(splosh::launch_q5k_repack(native, rows, inner, const_cast<uint8_t *>(plane0), nullptr,
                                                 const_cast<uint8_t *>(meta), true, stream, false),
                       "q4k unpack launch");
@@ -684,6 +695,7 @@ int splosh_q5k_unpack(const uint8_t *plane0, const uint8_t *plane1, const uint8_
     if (!native || !plane0 || !plane1 || !meta) return fail(SPLOSH_ERR_NULL_POINTER, "null buffer");
     if (rows <= 0 || inner <= 0 || rows % 128 != 0 || inner % 256 != 0)
         return fail(SPLOSH_ERR_LAYOUT_MISMATCH, "Q5_K planes need rows % 128 == 0 and inner % 256 == 0");
+    if (int st = check_plane_alignment(native, plane0, plane1, meta)) return st;
     return hip_status(splosh::launch_q5k_repack(native, rows, inner, const_cast<uint8_t *>(plane0),
                                                 const_cast<uint8_t *>(plane1), const_cast<uint8_t *>(meta), true,
                                                 stream),

@@ -40,67 +40,102 @@ __device__ __forceinline__ void q5k_scale_min(const uint8_t *packed, int j, uint
     }
 }
 
-// ---- repack / unpack: one thread per (row, native block) ------------------------------------
+// ---- repack / unpack: a workgroup per (32 rows, native block) ------------------------------------
+//
+// The 32 rows' blocks are copied between memory and LDS with consecutive lanes on consecutive dwords
+// of a block; thread (j, row) = (tid / 32, tid % 32) then builds (or takes apart) the plane record
+// of group j, so that a wave's plane stores (or loads) are runs of 32 consecutive 16-byte records.
+constexpr int kRepackRows = 32;
 
 __global__ void __launch_bounds__(256)
 q5k_repack_kernel(const uint8_t *__restrict__ native, int64_t rows, int64_t inner, uint8_t *__restrict__ p0,
                   uint8_t *__restrict__ p1, uint8_t *__restrict__ meta, int fifth) {
+    __shared__ uint32_t blk[kRepackRows * kQ5BlockBytes / 4];
     const int64_t blocks = inner / 256, groups = inner / 32;
-    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= rows * blocks) return;
-    const int64_t row = idx / blocks, block = idx % blocks;
-    const int bytes = fifth ? kQ5BlockBytes : kQ4KBlockBytes, qs = fifth ? 48 : 16;
-    const uint8_t *b = native + (row * blocks + block) * bytes;
-    for (int j = 0; j < 8; ++j) {
-        uint32_t words[4] = {0u, 0u, 0u, 0u}, bits = 0u;
-        for (int e = 0; e < 32; ++e) {
-            const int slot = gguf_slot(e);
-            const uint32_t low = (b[qs + 32 * (j / 2) + e] >> (4 * (j % 2))) & 15u;
-            const uint32_t high = fifth ? (b[16 + e] >> j) & 1u : 0u;
-            const int i = slot & 7;
-            words[slot >> 3] |= low << ((i & 1) * 16 + 4 * (i >> 1));
-            bits |= high << slot;
-        }
-        const int64_t rec = plane_record(row, block * 8 + j, groups);
-        *(u32x4 *)(p0 + rec * 16) = u32x4{words[0], words[1], words[2], words[3]};
-        if (fifth) *(uint32_t *)(p1 + rec * 4) = bits;
+    const int64_t r0 = (int64_t)blockIdx.x * kRepackRows, block = blockIdx.y;
+    const int bytes = fifth ? kQ5BlockBytes : kQ4KBlockBytes, qs = fifth ? 48 : 16, words = bytes / 4;
+    const int tid = threadIdx.x;
+    for (int d = tid; d < kRepackRows * words; d += 256) {
+        const int64_t row = r0 + d / words;
+        if (row < rows) blk[d] = *(const uint32_t *)(native + (row * blocks + block) * bytes + 4 * (d % words));
     }
-    const int64_t mrec = plane_record(row, block, blocks);
-    for (int i = 0; i < 16; ++i) meta[mrec * 16 + i] = b[i];
+    __syncthreads();
+    const int j = tid / kRepackRows, lr = tid % kRepackRows;
+    const int64_t row = r0 + lr;
+    if (row >= rows) return;
+    const uint8_t *b = (const uint8_t *)blk + lr * bytes;
+    uint32_t w[4] = {0u, 0u, 0u, 0u}, bits = 0u;
+#pragma unroll
+    for (int e = 0; e < 32; ++e) {
+        const int slot = gguf_slot(e), i = slot & 7;
+        const uint32_t low = (b[qs + 32 * (j / 2) + e] >> (4 * (j % 2))) & 15u;
+        w[slot >> 3] |= low << ((i & 1) * 16 + 4 * (i >> 1));
+        if (fifth) bits |= ((b[16 + e] >> j) & 1u) << slot;
+    }
+    const int64_t rec = plane_record(row, block * 8 + j, groups);
+    *(u32x4 *)(p0 + rec * 16) = u32x4{w[0], w[1], w[2], w[3]};
+    if (fifth) *(uint32_t *)(p1 + rec * 4) = bits;
+    if (j == 0) {
+        const uint32_t *m = blk + lr * words;
+        *(u32x4 *)(meta + plane_record(row, block, blocks) * 16) = u32x4{m[0], m[1], m[2], m[3]};
+    }
 }
 
 __global__ void __launch_bounds__(256)
 q5k_unpack_kernel(const uint8_t *__restrict__ p0, const uint8_t *__restrict__ p1, const uint8_t *__restrict__ meta,
                   int64_t rows, int64_t inner, uint8_t *__restrict__ native, int fifth) {
+    // The 5-bit codes of the 32 rows' blocks ([row][element 0..255]), then the block bytes.
+    __shared__ uint8_t codes[kRepackRows * 256];
+    __shared__ u32x4 metas[kRepackRows];
     const int64_t blocks = inner / 256, groups = inner / 32;
-    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= rows * blocks) return;
-    const int64_t row = idx / blocks, block = idx % blocks;
-    const int bytes = fifth ? kQ5BlockBytes : kQ4KBlockBytes, qs = fifth ? 48 : 16;
-    uint8_t b[kQ5BlockBytes];
-    for (int i = 0; i < kQ5BlockBytes; ++i) b[i] = 0;
-    const int64_t mrec = plane_record(row, block, blocks);
-    for (int i = 0; i < 16; ++i) b[i] = meta[mrec * 16 + i];
-    for (int j = 0; j < 8; ++j) {
-        const int64_t rec = plane_record(row, block * 8 + j, groups);
-        const u32x4 words = *(const u32x4 *)(p0 + rec * 16);
-        const uint32_t bits = fifth ? *(const uint32_t *)(p1 + rec * 4) : 0u;
-        for (int e = 0; e < 32; ++e) {
-            const int slot = gguf_slot(e);
-            const int i = slot & 7;
-            const uint32_t low = (words[slot >> 3] >> ((i & 1) * 16 + 4 * (i >> 1))) & 15u;
-            b[qs + 32 * (j / 2) + e] |= (uint8_t)(low << (4 * (j % 2)));
-            if (fifth) b[16 + e] |= (uint8_t)(((bits >> slot) & 1u) << j);
+    const int64_t r0 = (int64_t)blockIdx.x * kRepackRows, block = blockIdx.y;
+    const int bytes = fifth ? kQ5BlockBytes : kQ4KBlockBytes, qs = fifth ? 48 : 16, words = bytes / 4;
+    const int tid = threadIdx.x;
+    {
+        const int j = tid / kRepackRows, lr = tid % kRepackRows;
+        const int64_t row = r0 + lr;
+        if (row < rows) {
+            const int64_t rec = plane_record(row, block * 8 + j, groups);
+            const u32x4 w = *(const u32x4 *)(p0 + rec * 16);
+            const uint32_t bits = fifth ? *(const uint32_t *)(p1 + rec * 4) : 0u;
+#pragma unroll
+            for (int e = 0; e < 32; ++e) {
+                const int slot = gguf_slot(e), i = slot & 7;
+                const uint32_t low = (w[slot >> 3] >> ((i & 1) * 16 + 4 * (i >> 1))) & 15u;
+                codes[lr * 256 + 32 * j + e] = (uint8_t)(low | (((bits >> slot) & 1u) << 4));
+            }
+            if (j == 0) metas[lr] = *(const u32x4 *)(meta + plane_record(row, block, blocks) * 16);
         }
     }
-    uint8_t *dst = native + (row * blocks + block) * bytes;
-    for (int i = 0; i < bytes; ++i) dst[i] = b[i];
+    __syncthreads();
+    for (int d = tid; d < kRepackRows * words; d += 256) {
+        const int lr = d / words, o = 4 * (d % words);
+        const int64_t row = r0 + lr;
+        if (row >= rows) continue;
+        const uint8_t *c = codes + lr * 256;
+        uint32_t v = 0u;
+        for (int k = 0; k < 4; ++k) {
+            const int at = o + k;
+            uint32_t byte;
+            if (at < 16) {
+                byte = (metas[lr][at >> 2] >> (8 * (at & 3))) & 0xFFu;
+            } else if (at < qs) {  // fifth bits: bit j of byte 16 + e is element e of group j
+                const int e = at - 16;
+                byte = 0u;
+                for (int j = 0; j < 8; ++j) byte |= (uint32_t)(c[32 * j + e] >> 4) << j;
+            } else {  // low nibble: group 2 q, high nibble: group 2 q + 1
+                const int q = (at - qs) / 32, e = (at - qs) % 32;
+                byte = (c[64 * q + e] & 15u) | ((uint32_t)(c[64 * q + 32 + e] & 15u) << 4);
+            }
+            v |= byte << (8 * k);
+        }
+        *(uint32_t *)(native + (row * blocks + block) * bytes + o) = v;
+    }
 }
 
 hipError_t launch_q5k_repack(const uint8_t *native, int64_t rows, int64_t inner, uint8_t *p0, uint8_t *p1,
                              uint8_t *meta, bool inverse, hipStream_t stream, bool fifth) {
-    const int64_t total = rows * (inner / 256);
-    const dim3 grid((unsigned)((total + 255) / 256));
+    const dim3 grid((unsigned)((rows + kRepackRows - 1) / kRepackRows), (unsigned)(inner / 256));
     if (inverse)
         hipLaunchKernelGGL(q5k_unpack_kernel, grid, dim3(256), 0, stream, p0, p1, meta, rows, inner,
                            const_cast<uint8_t *>(native), fifth ? 1 : 0);
