@@ -43,6 +43,13 @@ namespace splosh {
 
 constexpr int kMmaMaxGrid = 1024;  // workgroups of a stream-K launch
 
+// a / b for 0 <= a, 0 < b, in 32 bits when both fit (the stream-K bookkeeping divides wave-uniform
+// values; a 64-bit division is a long VALU sequence, a 32-bit one a short one).
+__device__ __forceinline__ int64_t div_nn(int64_t a, int64_t b) {
+    if ((uint64_t)a <= 0xffffffffull && (uint64_t)b <= 0xffffffffull) return (int64_t)((uint32_t)a / (uint32_t)b);
+    return a / b;
+}
+
 struct MmaArgs {
     // q4: the weight (gate) and, for the fused pair, up.
     const uint32_t *packed[2];
@@ -192,16 +199,20 @@ struct Q4Format {
             }
         }
     }
-    // Sidecars of the step whose codes sit in `slot` and whose staged sidecars sit in `sbuf`
-    // (zeros when the step has no group for this wave).
-    // The sidecars are read whatever `on` says and then scaled by 0 or 1 (exact), so that the
+    // The staged sidecars of the step after next sit in LDS buffer `sbuf` (recorded at the barrier
+    // that makes them visible; read by prepare(), which measured faster for q4 than reading them a
+    // step early into registers, as Q5Format does: the registers are not to spare here).
+    const char *side_buf = nullptr;
+    __device__ void fetch_side(const char *sbuf) { side_buf = sbuf; }
+    // Coefficients of the step whose codes sit in `slot` (zeros when the step has no group for this
+    // wave). The sidecars are read whatever `on` says and then scaled by 0 or 1 (exact), so that the
     // reads of both weights are issued together instead of behind a branch each.
-    __device__ void prepare(int slot, const char *sbuf, bool on) {
+    __device__ void prepare(int slot, bool on) {
         uint32_t sb[NW], bb[NW];
 #pragma unroll
         for (int w = 0; w < NW; ++w) {
             if (kStageSide) {
-                const char *base = sbuf + (((w * 2) * KW + kw) * kBandCols + cw * 32 + r) * 2;
+                const char *base = side_buf + (((w * 2) * KW + kw) * kBandCols + cw * 32 + r) * 2;
                 sb[w] = *(const uint16_t *)base;
                 bb[w] = *(const uint16_t *)(base + KW * kBandCols * 2);
             } else {
@@ -301,8 +312,12 @@ struct Q5Format {
     // 4 + k, so for j < 4 (kw < 2, wave-uniform) sc and mn are the low six bits of meta bytes 4 + j
     // and 8 + j; for j >= 4 they are the nibbles of byte 12 + (j - 4) joined with the top two bits
     // of bytes 4 + (j - 4) and 8 + (j - 4). Either way the byte within its word is 2 (kw & 1) + h.
-    __device__ void prepare(int, const char *sbuf, bool on) {
-        const u32x4 m = *(const u32x4 *)(sbuf + (cw * 32 + r) * 16);
+    // The meta record of the step after next, read from LDS a step before prepare() needs it, so
+    // the LDS latency does not stall the step that uses it.
+    u32x4 rm;
+    __device__ void fetch_side(const char *sbuf) { rm = *(const u32x4 *)(sbuf + (cw * 32 + r) * 16); }
+    __device__ void prepare(int, bool on) {
+        const u32x4 m = rm;
         const float d = half_bits_to_f32(m[0]), dmin = half_bits_to_f32(m[0] >> 16);
         const uint32_t sh = 8u * (2u * (kw & 1) + h);
         uint32_t sc, mn;
@@ -394,7 +409,7 @@ mma_kernel(MmaArgs args) {
     const int P = gridDim.x;
     const rsrc_t p_rsrc = make_rsrc(args.partial, args.partial_bytes);
     // Workgroup i takes stream-K units [sk_start(i), sk_start(i + 1)).
-    auto sk_start = [&](int i) { return args.sk_units * i / P; };
+    auto sk_start = [&](int i) { return div_nn(args.sk_units * i, P); };
     __shared__ int fix_count;
     __shared__ uint16_t fix_list[kMmaMaxGrid];  // contributors of a shared band: 2 wg + slot
     F fmt(args, wave, lane);
@@ -454,8 +469,10 @@ mma_kernel(MmaArgs args) {
         // Dequantized weights of the current step; operand i is replaced by the next step's as
         // soon as the MFMAs of sub-step i have been issued.
         bf16x8 bw[NW][4];
+        auto fetch_side = [&](int sbuf) { fmt.fetch_side(side_lds + sbuf * S::kSBuf); };
         auto dequant = [&](int slot_, int sbuf, bool on) {
-            fmt.prepare(slot_, side_lds + sbuf * S::kSBuf, on);
+            fetch_side(sbuf);
+            fmt.prepare(slot_, on);
 #pragma unroll
             for (int w = 0; w < NW; ++w)
 #pragma unroll
@@ -513,6 +530,7 @@ mma_kernel(MmaArgs args) {
         };
         bf16x8 af_pre[FM];  // sub-step 0 fragments of the current step
         read_af(af_pre, 0, 0);
+        fetch_side(0);  // the sidecars of step 1 came with stage 0
 
         // Step t: MFMA sub-steps with the dequantization of step t + 1 interleaved, `mid` between
         // sub-steps 1 and 2.
@@ -523,8 +541,9 @@ mma_kernel(MmaArgs args) {
         auto live = [&](int t) { return t < T && fmt.active(t); };
         auto step = [&](int t, int d, int abuf, auto &&mid, auto &&hook) {
             const int next = (d + 1) % D;
-            // The sidecars of step t + 1 came with stage t (buffer t mod 4 = abuf).
-            fmt.prepare(next, side_lds + abuf * S::kSBuf, live(t + 1));
+            // The sidecars of step t + 1 came with stage t (buffer t mod 4 = abuf), fetched at the
+            // previous step's barrier.
+            fmt.prepare(next, live(t + 1));
             // Fragments of sub-step i + 1 are read as soon as sub-step i's MFMAs are issued, so their
             // LDS latency hides behind the dequantization (two alternating register sets; sub-step 0
             // uses af_pre, read at the previous step's barrier).
@@ -560,6 +579,7 @@ mma_kernel(MmaArgs args) {
                          wait_vmcnt<kMidWait>();  // stage t + 1 has arrived
                          lds_barrier_staged<kStageLoads>();  // stage t + 2 may be in flight
                          read_af(af_pre, nbuf(abuf), 0);
+                         fetch_side(nbuf(abuf));  // the sidecars of step t + 2 (stage t + 1)
                      },
                      [&](int i) {
                          if (i == 0) load_w(d, t + D);
@@ -584,7 +604,10 @@ mma_kernel(MmaArgs args) {
                  [&] {
                      wait_vmcnt<0>();
                      lds_barrier();
-                     if (d < D - 1) read_af(af_pre, nbuf(abuf), 0);
+                     if (d < D - 1) {
+                         read_af(af_pre, nbuf(abuf), 0);
+                         fetch_side(nbuf(abuf));
+                     }
                  },
                  [&](int i) {
                      if (d + 3 < D) {
@@ -724,7 +747,7 @@ mma_kernel(MmaArgs args) {
     // fix_list; the count is returned to every thread.
     auto contributors = [&](int band) {
         const int64_t lo = (int64_t)(band - args.dp_bands) * U, hi = lo + U;  // the band's units
-        const int i_lo = (int)(((lo + 1) * P - 1) / args.sk_units), i_hi = (int)((hi * P - 1) / args.sk_units);
+        const int i_lo = (int)div_nn((lo + 1) * P - 1, args.sk_units), i_hi = (int)div_nn(hi * P - 1, args.sk_units);
         if (tid == 0) {
             int count = 0;
             for (int i = i_lo; i <= i_hi; ++i) {
@@ -792,8 +815,9 @@ mma_kernel(MmaArgs args) {
         int slot = 0, pending = -1, pending_old = -1, announce = -1;
         __shared__ int arrival;
         while (u < u_end) {
-            const int band = args.dp_bands + (int)(u / U);
-            const int ga = (int)(u % U);
+            const int64_t uq = div_nn(u, U);
+            const int band = args.dp_bands + (int)uq;
+            const int ga = (int)(u - uq * U);
             const int gb = (int)((int64_t)ga + (u_end - u) < U ? ga + (u_end - u) : U);
             const bool whole = ga == 0 && gb == U;
             const bool last_partial = !whole && u + (gb - ga) >= u_end;
