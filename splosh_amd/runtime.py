@@ -175,22 +175,34 @@ def workspace_bytes(rows, columns, inner):
     return _lib.lib().splosh_workspace_bytes(rows, columns, inner)
 
 
+class _Scratch:
+    """The split-K scratch of one call: (pointer, bytes), and the tensor that owns it, held by the
+    caller until the kernel has been launched."""
+
+    def __init__(self, ptr, nbytes, owner=None):
+        self.ptr, self.nbytes, self.owner = ptr, nbytes, owner
+
+    def __iter__(self):
+        return iter((self.ptr, self.nbytes))
+
+
 def _workspace(workspace, rows, n, inner, device, stream=None):
     """The split-K scratch of the kernels: the caller's tensor (an empty one: none), or a fresh one
     from torch's stream-ordered allocator sized by splosh_workspace_bytes. A fresh one is
-    zero-filled and allocated on the stream the kernel runs on: the fill is ordered before the
-    kernel, and once the tensor is dropped the allocator hands the block out again only to work
-    ordered after that kernel on the same stream."""
+    zero-filled and allocated on the stream the kernel runs on, so the fill is ordered before the
+    kernel; the caller keeps the returned object (and with it the tensor) until the kernel has
+    been launched, after which the allocator hands the block out again only to work ordered after
+    that kernel on the same stream."""
     if workspace is not None and workspace.numel() == 0:
-        return None, 0
+        return _Scratch(None, 0)
     if workspace is not None:
-        return _ptr(workspace), workspace.numel() * workspace.element_size()
+        return _Scratch(_ptr(workspace), workspace.numel() * workspace.element_size(), workspace)
     need = _lib.lib().splosh_workspace_bytes(rows, n, inner)
     if need == 0:
-        return None, 0
+        return _Scratch(None, 0)
     with torch.cuda.stream(_on(stream)):
         buf = torch.zeros(need, dtype=torch.uint8, device=device)
-    return _ptr(buf), need
+    return _Scratch(_ptr(buf), need, buf)
 
 
 def gemm(w, a, out=None, residual=None, out_dtype=torch.bfloat16, kernel=AUTO, rows=None, stream=None,
@@ -210,7 +222,8 @@ def gemm(w, a, out=None, residual=None, out_dtype=torch.bfloat16, kernel=AUTO, r
     if residual is not None:
         if residual.dtype != out.dtype or residual.stride(0) != out.stride(0):
             raise SploshError(13, "residual must match the output's dtype and row stride")
-    ws, ws_bytes = _workspace(workspace, rows, w.rows, w.inner, a.device, stream)
+    scratch = _workspace(workspace, rows, w.rows, w.inner, a.device, stream)  # held until the launch
+    ws, ws_bytes = scratch
     if isinstance(w, GgufWeight):
         _lib.check(_lib.lib().splosh_gguf_gemm(w.gguf_type, _ptr(w.native), w.rows, w.inner, _ptr(a), a.stride(0),
                                                _ptr(out), out.stride(0), _dtype_code(out.dtype), _ptr(residual),
@@ -248,7 +261,8 @@ def gemm_emit(w, a, norm_weight, out=None, residual=None, kernel=AUTO, rows=None
         sums = torch.empty((rows, w.rows // 64), dtype=torch.float32, device=a.device)
         squares = torch.empty_like(sums)
     wc = w.c()
-    ws, ws_bytes = _workspace(workspace, rows, w.rows, w.inner, a.device, stream)
+    scratch = _workspace(workspace, rows, w.rows, w.inner, a.device, stream)  # held until the launch
+    ws, ws_bytes = scratch
     _lib.check(_lib.lib().splosh_q4_gemm_emit(ctypes.byref(wc), _ptr(a), a.stride(0), _ptr(out), out.stride(0),
                                               _ptr(residual), rows, _ptr(norm_weight), _ptr(values), values.stride(0),
                                               _ptr(sums), _ptr(squares), kernel, ws, ws_bytes, _stream(stream)))
@@ -265,7 +279,8 @@ def mlp_in(gate, up, a, out=None, out_dtype=torch.bfloat16, kernel=AUTO, rows=No
     _require(a, ((rows - 1) * a.stride(0) + gate.inner) * 2, "a")
     _require(out, ((rows - 1) * out.stride(0) + gate.rows) * out.element_size(), "output")
     gc, uc = gate.c(), up.c()
-    ws, ws_bytes = _workspace(workspace, rows, gate.rows, gate.inner, a.device, stream)
+    scratch = _workspace(workspace, rows, gate.rows, gate.inner, a.device, stream)  # held until the launch
+    ws, ws_bytes = scratch
     st = _lib.lib().splosh_q4_mlp_in(ctypes.byref(gc), ctypes.byref(uc), _ptr(a), a.stride(0), _ptr(out),
                                      out.stride(0), _dtype_code(out.dtype), rows, kernel, ws, ws_bytes,
                                      _stream(stream))
