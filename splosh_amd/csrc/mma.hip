@@ -441,9 +441,20 @@ mma_kernel(MmaArgs args) {
     // One job: column band `band`, units [ga, gb); leaves its sums in `fin`. `after_prologue`
     // runs once every wave has passed the prologue's barrier (all of the workgroup's earlier
     // stores are complete by then).
+    // The emit's norm weight of the lane's column of the job's band, loaded when the job starts
+    // (its latency hides behind the job instead of stalling the epilogue).
+    int wn_band = -1;
+    uint32_t wn_bits = 0;
     auto run_job = [&](int band, int ga, int gb, auto &&after_prologue) {
         const int T = fmt.steps(ga, gb);
         fmt.begin(args, band, ga, gb);
+        if constexpr (NW == 1) {
+            if (args.norm_weight) {
+                const int64_t c = (int64_t)band * S::kBandCols + cw * 32 + r;
+                wn_band = band;
+                wn_bits = args.norm_weight[c < args.n ? c : args.n - 1];
+            }
+        }
 
         // Pieces [j0, j1) of chunk t, straight from memory into LDS buffer `buf` (buffer loads with
         // the LDS modifier: lane l of the wave's piece j lands at ((wave kAPer + j) 64 + l) 16).
@@ -685,7 +696,7 @@ mma_kernel(MmaArgs args) {
                 // Emit (engine_na.metal:365-411 restated): the rounded operand, then per row the
                 // band's sums: over this wave's 32 columns by a shuffle tree inside the lane half
                 // that holds the row, then the two column waves' halves through LDS.
-                const float wn = bf16_bits_to_f32(args.norm_weight[ocol]);
+                const float wn = bf16_bits_to_f32(band == wn_band ? wn_bits : (uint32_t)args.norm_weight[ocol]);
                 float *part = (float *)((char *)lds + S::kRedBytes);  // [FM * 32 rows][2 cw][2]
                 const int64_t groups = args.n / 64;
 #pragma unroll
@@ -769,25 +780,36 @@ mma_kernel(MmaArgs args) {
         for (int w = 0; w < NW; ++w)
 #pragma unroll
             for (int f = 0; f < FM; ++f) v[w][f] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        for (int c = 0; c < count; ++c) {
-            const int entry = fix_list[c];
-            if (entry == own) {
+        // Four contributors' partials are loaded before any is added (one memory round trip per
+        // four, not per contributor); the sum still runs in contributor order.
+        constexpr int kBatch = 4;
+        for (int c0 = 0; c0 < count; c0 += kBatch) {
+            f32x4 part[kBatch][NW][FM];
+#pragma unroll
+            for (int j = 0; j < kBatch; ++j) {
+                // Past the list or this workgroup's own entry: a harmless read of entry 0's partial.
+                int entry = c0 + j < count ? fix_list[c0 + j] : own;
+                if (entry == own) entry = fix_list[0] == own ? fix_list[count > 1 ? 1 : 0] : fix_list[0];
 #pragma unroll
                 for (int w = 0; w < NW; ++w)
 #pragma unroll
-                    for (int f = 0; f < FM; ++f) v[w][f] += fin[w][f];
-                continue;
+                    for (int f = 0; f < FM; ++f)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const int m = own_row(f, i) < rows ? own_row(f, i) : rows - 1;
+                            part[j][w][f][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                                            p_rsrc, part_off(entry >> 1, entry & 1, w, m), 0, kDeviceCpol));
+                        }
             }
 #pragma unroll
-            for (int w = 0; w < NW; ++w)
+            for (int j = 0; j < kBatch; ++j) {
+                if (c0 + j >= count) break;
+                const bool mine = fix_list[c0 + j] == own;
 #pragma unroll
-                for (int f = 0; f < FM; ++f)
+                for (int w = 0; w < NW; ++w)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int m = own_row(f, i) < rows ? own_row(f, i) : rows - 1;
-                        v[w][f][i] += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                                                    p_rsrc, part_off(entry >> 1, entry & 1, w, m), 0, kDeviceCpol));
-                    }
+                    for (int f = 0; f < FM; ++f) v[w][f] += mine ? fin[w][f] : part[j][w][f];
+            }
         }
         store_out(band, v);
     };
