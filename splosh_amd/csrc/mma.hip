@@ -960,6 +960,9 @@ MmaPlan plan_mma(int64_t rows, int64_t columns, int64_t groups, bool mlp, size_t
     // to bands - 1 idle CUs (K=17408 -> N=5120 at M=64: 240 workgroups, 31.5 -> 30.2 us; the
     // 5120 -> 5120 projections 23.4 -> 19.1 us).
     else if (p.bands < grid && grid / p.bands >= 2) grid = p.bands * (grid / p.bands);
+    // Between three quarters of the CUs and all of them: one band a workgroup beats two jobs a
+    // workgroup (5120 -> 12288 at M=64, 192 bands: 23.1 -> 19.9 us with 64 CUs idle).
+    else if (p.bands < grid && 4 * p.bands >= 3 * grid) grid = p.bands;
     grid = grid < kMmaMaxGrid ? grid : kMmaMaxGrid;  // the fix-up's contributor list
     p.grid = grid;
     // Every band's units go into one stream, cut into `grid` equal contiguous ranges: a band is
