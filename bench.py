@@ -34,21 +34,21 @@ BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
 # a plain 256 MiB device copy (FETCH_SIZE reads half the bytes moved, WRITE_SIZE all of them).
 # The readings and commands are in profiles/; calls not listed are unmeasured (None).
 MEASURED_TRAFFIC = {
-    ("verify64", "mlp_in"): 55900.3 * 2 * 1024 + 9871.0 * 1024,  # mma_kernel<Q4Format<2, true, 2, 4, 3>, 2, 2, 4, 3>
-    ("verify64", "down"): 32891.7 * 2 * 1024 + 4746.5 * 1024,  # mma_kernel<Q4Format<1, true, 2, 4, 3>, 2, 2, 4, 3>
+    ("verify64", "mlp_in"): 55942.5 * 2 * 1024 + 9871.0 * 1024,  # mma_kernel<Q4Format<2, true, 2, 4, 3>, 2, 2, 4, 3>
+    ("verify64", "down"): 35292.5 * 2 * 1024 + 4420.5 * 1024,  # mma_kernel<Q4Format<1, true, 2, 4, 3>, 2, 2, 4, 3>
     ("decode1", "gemv"): 27279.7 * 2 * 1024 + 34.0 * 1024,  # q4_decode_kernel<1, 1, 32, 2>
     ("lmhead1", "lm_head"): 388082.2 * 2 * 1024 + 485.0 * 1024,  # q4_decode_kernel<1, 1, 32, 2>
     ("q5k1", "q5k"): 46418.9 * 2 * 1024 + 20.0 * 1024,  # q5k_decode_kernel<8, 2, true>
-    ("q5k64", "q5k"): 38130.2 * 2 * 1024 + 4970.9 * 1024,  # mma_kernel<Q5Format<2, 4, 3, true>, 2, 2, 4, 3>
-    ("q5k16", "q5k"): 32251.7 * 2 * 1024 + 1258.3 * 1024,  # mma_kernel<Q5Format<2, 4, 3, true>, 1, 2, 4, 3>
+    ("q5k64", "q5k"): 41370.6 * 2 * 1024 + 4415.2 * 1024,  # mma_kernel<Q5Format<2, 4, 3, true>, 2, 2, 4, 3>
+    ("q5k16", "q5k"): 32944.4 * 2 * 1024 + 1115.2 * 1024,  # mma_kernel<Q5Format<2, 4, 3, true>, 1, 2, 4, 3>
     ("prefill2048", "prefill_up"): 263306.6 * 2 * 1024 + 118272.0 * 1024,  # q4_prefill_kernel<1>
     ("q5k2048", "q5k"): 374456.7 * 2 * 1024 + 20480.9 * 1024,  # gguf_tile_kernel<13, 2, 2, false>
     ("q6k64", "gguf"): 53827.8 * 2 * 1024 + 21137.9 * 1024,  # gguf_tile_kernel<14, 1, 2, true>
     ("q6k1", "gguf"): 36154.8 * 2 * 1024 + 40.0 * 1024,  # gguf_gemv_kernel<14, 4>
     ("q80_1", "gguf"): 46735.3 * 2 * 1024 + 40.1 * 1024,  # gguf_gemv_kernel<8, 4>
     ("stream50", "read"): 24680.2 * 2 * 1024 + 64.0 * 1024,  # stream_read_kernel
-    ("layerset", "mlp_in"): 55905.5 * 2 * 1024 + 9871.0 * 1024,  # mma_kernel<Q4Format<2, true, 2, 4, 3>, 2, 2, 4, 3>
-    ("emit64", "fused"): 33538.6 * 2 * 1024 + 5807.2 * 1024,  # mma_kernel<Q4Format<1, true, 2, 4, 3>, 2, 2, 4, 3>
+    ("layerset", "mlp_in"): 55934.6 * 2 * 1024 + 9871.0 * 1024,  # mma_kernel<Q4Format<2, true, 2, 4, 3>, 2, 2, 4, 3>
+    ("emit64", "fused"): 35950.1 * 2 * 1024 + 5475.5 * 1024,  # mma_kernel<Q4Format<1, true, 2, 4, 3>, 2, 2, 4, 3>
 }
 
 
