@@ -43,7 +43,7 @@ MEASURED_TRAFFIC = {
     ("q5k16", "q5k"): 32944.4 * 2 * 1024 + 1115.2 * 1024,  # mma_kernel<Q5Format<2, 4, 3, true>, 1, 2, 4, 3>
     ("prefill2048", "prefill_up"): 263306.6 * 2 * 1024 + 118272.0 * 1024,  # q4_prefill_kernel<1>
     ("q5k2048", "q5k"): 374456.7 * 2 * 1024 + 20480.9 * 1024,  # gguf_tile_kernel<13, 2, 2, false>
-    ("q6k64", "gguf"): 53827.8 * 2 * 1024 + 21137.9 * 1024,  # gguf_tile_kernel<14, 1, 2, true>
+    ("q6k64", "gguf"): (50699.6 + 6421.1) * 2 * 1024 + (25600.0 + 644.2) * 1024,  # gguf_tile_kernel<14, 1, 2, true> + gguf_tile_finish<1, 2>
     ("q6k1", "gguf"): 36154.8 * 2 * 1024 + 40.0 * 1024,  # gguf_gemv_kernel<14, 4>
     ("q80_1", "gguf"): 46735.3 * 2 * 1024 + 40.1 * 1024,  # gguf_gemv_kernel<8, 4>
     ("stream50", "read"): 24680.2 * 2 * 1024 + 64.0 * 1024,  # stream_read_kernel

@@ -12,8 +12,8 @@
 //     written to LDS as B[BN][64];
 //   * every wave multiplies its (32 FM) x (32 FN) sub-block from LDS fragments (row stride 144
 //     bytes: the 16-byte operand reads do not conflict).
-// Two barriers a step; no prefetch: several workgroups a CU (small tiles, few registers) hide the
-// decode's load latency behind each other's MFMAs.
+// Two barriers a step; a step's global reads go out one step ahead. With few tiles K is split over
+// workgroups, whose fp32 partials a second pass (gguf_tile_finish) sums in slice order.
 //
 // Numerics: the weight is the decoder's fp32 value rounded to bf16 (RNE), products exact in fp32,
 // fp32 accumulation -- as the q4 MFMA kernels.
@@ -26,9 +26,9 @@
 namespace splosh {
 
 constexpr int kGtStride = 72;       // bf16 elements per LDS row: 64 + 8 padding (144 bytes)
-constexpr int kGtCounterBytes = 16384;  // arrival counters at the start of the workspace
+constexpr int kGtCounterBytes = 16384;  // reserved at the start of the workspace (partials follow)
 constexpr int kGtMaxSplitTiles = kGtCounterBytes / 4;
-constexpr int kGtMaxSplits = 8;         // K slices at most (the summing workgroup reads them all)
+constexpr int kGtMaxSplits = 32;        // K slices at most
 constexpr int kGtCpol = 1 | 16;         // partials written through to memory (sc0 sc1)
 constexpr int kGtSqStride = 36;         // floats a row of a wave's 32 x 32 epilogue square
 
@@ -46,7 +46,6 @@ struct GgufTileArgs {
     int out_dtype;
     int vector_out;            // out / residual 16-byte aligned and ldc % 8 == 0: 16-byte stores
     int splits;                // K slices (gridDim.z); > 1 needs the workspace
-    int *counters;             // [tiles] arrival counts, zero between calls
     char *partial;             // [tiles][splits][256 threads][FM FN 16] fp32
     uint32_t partial_bytes;
 };
@@ -237,8 +236,7 @@ __global__ void __launch_bounds__(256) gguf_tile_kernel(GgufTileArgs args) {
     } else {
 
     // Split K: every slice writes its accumulators (16-byte pieces, [tile][slice][thread] order,
-    // coalesced) and counts itself in; the last to arrive sums all slices from memory in slice
-    // order, one 32 x 32 block at a time, so the result does not depend on the timing.
+    // coalesced); gguf_tile_finish sums them.
     constexpr int kPer = FM * FN * 16;  // floats a thread
     const int tile = blockIdx.y * gridDim.x + blockIdx.x;
     const rsrc_t pr = make_rsrc(args.partial, args.partial_bytes);
@@ -255,43 +253,49 @@ __global__ void __launch_bounds__(256) gguf_tile_kernel(GgufTileArgs args) {
                 __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), pr, off(z, (i * FN + j) * 4 + q),
                                                        0, kGtCpol);
             }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the partial is in memory
-    __syncthreads();
-    __shared__ int arrival;
-    if (tid == 0) {
-        const int old = __hip_atomic_fetch_add(args.counters + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        if (old == S - 1) __hip_atomic_store(args.counters + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        arrival = old;
     }
-    __syncthreads();
-    if (arrival != S - 1) return;
+}
+
+// Split K, second pass: sums the slices' partials of every tile in slice order (so the result does
+// not depend on timing) and writes the outputs. Block (tile, p) takes accumulator quarter p of all
+// 256 threads of the split kernel: thread t's quarter holds rows 8 (e / 4) + 4 h + e % 4 of one
+// column, in the MFMA output layout the split kernel wrote them in.
+template <int FM, int FN>
+__global__ void __launch_bounds__(256) gguf_tile_finish(GgufTileArgs args) {
+    constexpr int kPer = FM * FN * 16;
+    const int tile = blockIdx.x, p = blockIdx.y;  // p: (i FN + j) 4 + q
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1, r = lane & 31, h = lane >> 5;
+    const int S = args.splits;
+    const int tiles_n = (int)((args.n + 64 * FN - 1) / (64 * FN));
+    const int64_t m0 = (int64_t)(tile / tiles_n) * 64 * FM, n0 = (int64_t)(tile % tiles_n) * 64 * FN;
+    const rsrc_t pr = make_rsrc(args.partial, args.partial_bytes);
+    auto off = [&](int slice) { return (uint32_t)((((int64_t)tile * S + slice) * 256 + tid) * kPer + 4 * p) * 4u; };
+    f32x4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s0 = 0; s0 < S; s0 += 4) {
+        f32x4 part[4];
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+        for (int k = 0; k < 4; ++k)
+            part[k] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(pr, off(s0 + k < S ? s0 + k : 0), 0, kGtCpol));
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
-            f32x4 sum[4];
+        for (int k = 0; k < 4; ++k)
+            if (s0 + k < S) sum += part[k];
+    }
+    const int i = p / (FN * 4), j = (p / 4) % FN, q = p % 4;
+    const int64_t n = n0 + wn * FN * 32 + j * 32 + r;
+    if (n >= args.n) return;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) sum[q] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            // Two slices' loads in flight at a time, added in slice order.
-            for (int base = 0; base < S; base += 2) {
-                f32x4 part[2][4];
-#pragma unroll
-                for (int k = 0; k < 2; ++k)
-#pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        if (base + k < S)
-                            part[k][q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                                       pr, off(base + k, (i * FN + j) * 4 + q), 0, kGtCpol));
-#pragma unroll
-                for (int k = 0; k < 2; ++k)
-#pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        if (base + k < S) sum[q] += part[k][q];
-            }
-            f32x16 block;
-#pragma unroll
-            for (int e = 0; e < 16; ++e) block[e] = sum[e >> 2][e & 3];
-            store_block(i, j, block);
+    for (int e = 0; e < 4; ++e) {
+        const int64_t m = m0 + wm * FM * 32 + i * 32 + 8 * q + 4 * h + e;
+        if (m >= args.rows) continue;
+        const int64_t index = m * args.ldc + n;
+        float value = sum[e];
+        if (args.out_dtype == SPLOSH_F32) {
+            if (args.residual) value += ((const float *)args.residual)[index];
+            ((float *)args.out)[index] = value;
+        } else {
+            if (args.residual) value += bf16_bits_to_f32(((const uint16_t *)args.residual)[index]);
+            ((uint16_t *)args.out)[index] = f32_to_bf16(value);
         }
     }
 }
@@ -306,14 +310,20 @@ static int gt_fm(int64_t rows) {
     return rows <= 64 ? 1 : 2;
 }
 
-// K slices: enough workgroups for about two a CU, at least four 64-element steps a slice, and
-// only with room in the workspace.
+// K slices: enough workgroups for about 1.5 a CU (measured best among 1.25, 1.5, 2, 2.5, 4 and 8
+// a CU at K17408 -> N5120, M=16 and 64, for Q8_0, Q6_K, IQ3_S and Q5_K at M=128), at least four
+// 64-element steps a slice, and only with room in the workspace.
 static int gt_splits(int64_t rows, int64_t n, int64_t inner, size_t workspace_bytes) {
     const int fm = gt_fm(rows);
     const int64_t tiles = ((rows + 64 * fm - 1) / (64 * fm)) * ((n + 127) / 128);
     static const int target = [] {
         const char *e = getenv("SPLOSH_GGUF_TILE_WGS");
-        return e && atoi(e) > 0 ? atoi(e) : 512;
+        if (e && atoi(e) > 0) return atoi(e);
+        int dev = 0, cus = 256;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+        return cus * 25 / 16;
     }();
     int64_t s = (target + tiles - 1) / tiles;
     const int64_t most = inner / 64 / 4;
@@ -340,10 +350,14 @@ static hipError_t launch_gt(const GgufTileArgs &args, hipStream_t stream) {
     const dim3 grid((unsigned)((args.n + BN - 1) / BN), (unsigned)((args.rows + BM - 1) / BM), (unsigned)args.splits);
     // The split variant is a kernel of its own: its summing code needs registers that would
     // otherwise cost the unsplit kernel occupancy.
-    if (args.splits > 1)
+    if (args.splits > 1) {
         hipLaunchKernelGGL((gguf_tile_kernel<TYPE, FM, FN, true>), grid, dim3(256), lds, stream, args);
-    else
+        const hipError_t err = hipGetLastError();
+        if (err != hipSuccess) return err;
+        hipLaunchKernelGGL((gguf_tile_finish<FM, FN>), dim3(grid.x * grid.y, FM * FN * 4), dim3(256), 0, stream, args);
+    } else {
         hipLaunchKernelGGL((gguf_tile_kernel<TYPE, FM, FN, false>), grid, dim3(256), lds, stream, args);
+    }
     return hipGetLastError();
 }
 
@@ -381,7 +395,6 @@ hipError_t launch_gguf_tile(int type, const uint8_t *w, const uint8_t *plane1, c
     args.vector_out = ((uintptr_t)out % 16 == 0) && ((uintptr_t)residual % 16 == 0) && ldc % 8 == 0;
     args.splits = workspace ? gt_splits(m, rows_w, inner, workspace_bytes) : 1;
     if (args.splits > 1) {
-        args.counters = (int *)workspace;
         args.partial = (char *)workspace + kGtCounterBytes;
         const size_t room = workspace_bytes - kGtCounterBytes;
         args.partial_bytes = (uint32_t)(room < ((size_t)1 << 31) ? room : ((size_t)1 << 31));
