@@ -36,9 +36,9 @@ BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
 MEASURED_TRAFFIC = {
     ("verify64", "mlp_in"): 55942.5 * 2 * 1024 + 9871.0 * 1024,  # mma_kernel<Q4Format<2, true, 2, 4, 3>, 2, 2, 4, 3>
     ("verify64", "down"): 35292.5 * 2 * 1024 + 4420.5 * 1024,  # mma_kernel<Q4Format<1, true, 2, 4, 3>, 2, 2, 4, 3>
-    ("decode1", "gemv"): 27279.7 * 2 * 1024 + 34.0 * 1024,  # q4_decode_kernel<1, 1, 32, 2>
-    ("lmhead1", "lm_head"): 388082.2 * 2 * 1024 + 485.0 * 1024,  # q4_decode_kernel<1, 1, 32, 2>
-    ("q5k1", "q5k"): 46418.9 * 2 * 1024 + 20.0 * 1024,  # q5k_decode_kernel<8, 2, true>
+    ("decode1", "gemv"): 24559.8 * 2 * 1024 + 34.0 * 1024,  # q4_decode_kernel<1, 1, 32, 2>
+    ("lmhead1", "lm_head"): 349280.3 * 2 * 1024 + 486.2 * 1024,  # q4_decode_kernel<1, 1, 32, 2>
+    ("q5k1", "q5k"): 30096.8 * 2 * 1024 + 10.0 * 1024,  # q5k_decode_kernel<8, 2, true>
     ("q5k64", "q5k"): 41370.6 * 2 * 1024 + 4415.2 * 1024,  # mma_kernel<Q5Format<2, 4, 3, true>, 2, 2, 4, 3>
     ("q5k16", "q5k"): 32944.4 * 2 * 1024 + 1115.2 * 1024,  # mma_kernel<Q5Format<2, 4, 3, true>, 1, 2, 4, 3>
     ("prefill2048", "prefill_up"): 263306.6 * 2 * 1024 + 118272.0 * 1024,  # q4_prefill_kernel<1>

@@ -104,6 +104,15 @@ __device__ __forceinline__ void lds_barrier_staged() {
     asm volatile("; splosh-lds-outstanding %0\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::"n"(OUTSTANDING) : "memory");
 }
 
+// The block a workgroup takes when neighbouring blocks share cache lines: workgroups are handed to
+// the eight XCDs (each with its own L2) round robin by id, so consecutive ids land on different
+// L2s and a line two neighbours share is fetched from memory twice. Block = (id mod 8) (G / 8) +
+// id / 8 gives every XCD a contiguous run of blocks instead (G a multiple of 8; otherwise the id
+// itself). Only the order of the work changes.
+__device__ __forceinline__ int xcd_block(int id, int grid) {
+    return grid % 8 == 0 ? (id & 7) * (grid >> 3) + (id >> 3) : id;
+}
+
 // x sigmoid(x) with the hardware reciprocal (v_rcp_f32, about 1 ulp) instead of a full-precision
 // divide: the result is rounded to bf16 or summed in fp32 afterwards.
 __device__ __forceinline__ float silu(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }

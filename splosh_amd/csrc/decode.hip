@@ -126,7 +126,7 @@ q4_decode_kernel(DecodeArgs args) {
         s_rsrc[w] = make_rsrc(args.scales[w], args.sidecar_bytes);
         b_rsrc[w] = make_rsrc(args.biases[w], args.sidecar_bytes);
     }
-    const int64_t r0 = (int64_t)blockIdx.x * B;
+    const int64_t r0 = (int64_t)xcd_block(blockIdx.x, gridDim.x) * B;
     const uint32_t tile_base = (uint32_t)(r0 >> 7) * (uint32_t)G * 128u + (uint32_t)(r0 & 127) + (uint32_t)row;
     u32x4 cq[D][NW];
     uint32_t cs[D][NW], cb[D][NW];

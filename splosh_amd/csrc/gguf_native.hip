@@ -83,7 +83,7 @@ __global__ void __launch_bounds__(256) gguf_embed_kernel(GgufNativeArgs args, co
 template <int TYPE, int MR>
 __global__ void __launch_bounds__(256) gguf_gemv_kernel(GgufNativeArgs args) {
     const int lane = threadIdx.x & 63;
-    const int64_t n = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t n = (int64_t)xcd_block(blockIdx.x, gridDim.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (n >= args.rows) return;
     const int64_t m0 = (int64_t)blockIdx.y * MR;
     const int groups = (int)(args.inner / 32);

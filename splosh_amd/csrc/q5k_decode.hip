@@ -96,7 +96,7 @@ q5k_decode_kernel(Q5DecodeArgs args) {
     const rsrc_t p0_rsrc = make_rsrc(args.plane0, args.p0_bytes);
     const rsrc_t p1_rsrc = make_rsrc(FIFTH ? args.plane1 : args.plane0, FIFTH ? args.p1_bytes : 0u);
     const rsrc_t m_rsrc = make_rsrc(args.meta, args.meta_bytes);
-    const int64_t r0 = (int64_t)blockIdx.x * B;
+    const int64_t r0 = (int64_t)xcd_block(blockIdx.x, gridDim.x) * B;
     const uint32_t rr = (uint32_t)(r0 & 127) + (uint32_t)row;
     const uint32_t tile = (uint32_t)(r0 >> 7);
     u32x4 c0[D], cm[D];
