@@ -6,7 +6,7 @@ projection (two K=5120 -> N=17408 weights sharing one activation read, out = sil
 by the down projection (K=17408 -> N=5120) on that output. One "step" is that pair of launches.
 
     python bench.py [--steps K] [--warmup W]
-                    [--workload verify64|decode1|q5k1|q5k16|q5k64|q4k1|q4k64|q6k1|q80_1|iq4nl1|iq4xs1|q3k1|iq3s1|prefill2048|layerset|lmhead1|lmhead64|operand64|emit64|stream50|stream715]
+                    [--workload verify64|decode1|q5k1|q5k16|q5k64|q4k1|q4k64|q6k1|q80_1|iq4nl1|iq4xs1|q3k1|iq3s1|prefill2048|layerset|lmhead1|lmhead64|operand64|emit64|stream50|stream715|gemm2048]
 
 Inputs are synthetic (seeded, on the device): code words uniform random, scale = bf16(|N(0,0.02)|),
 bias = bf16(N(0,0.01)), activations bf16(N(0,1)). Several copies of the weight set are rotated so
@@ -41,7 +41,7 @@ MEASURED_TRAFFIC = {
     ("q5k1", "q5k"): 30096.8 * 2 * 1024 + 10.0 * 1024,  # q5k_decode_kernel<8, 2, true>
     ("q5k64", "q5k"): 41370.6 * 2 * 1024 + 4415.2 * 1024,  # mma_kernel<Q5Format<2, 4, 3, true>, 2, 2, 4, 3>
     ("q5k16", "q5k"): 32944.4 * 2 * 1024 + 1115.2 * 1024,  # mma_kernel<Q5Format<2, 4, 3, true>, 1, 2, 4, 3>
-    ("prefill2048", "prefill_up"): 263306.6 * 2 * 1024 + 118272.0 * 1024,  # q4_prefill_kernel<1>
+    ("prefill2048", "prefill_up"): 264479.7 * 2 * 1024 + 114688.0 * 1024,  # q4_prefill_kernel
     ("q5k2048", "q5k"): 374456.7 * 2 * 1024 + 20480.9 * 1024,  # gguf_tile_kernel<13, 2, 2, false>
     ("q6k64", "gguf"): (50699.6 + 6421.1) * 2 * 1024 + (25600.0 + 644.2) * 1024,  # gguf_tile_kernel<14, 1, 2, true> + gguf_tile_finish<1, 2>
     ("q6k1", "gguf"): 36154.8 * 2 * 1024 + 40.0 * 1024,  # gguf_gemv_kernel<14, 4>
@@ -224,6 +224,24 @@ def build_workload(name, rt, torch, gen, kernel):
         cfg = {"workload": f"streaming read of {b} bytes a launch (probe, not the path)", "rows": 0,
                "format": "bytes", "weight_copies": ncopy}
         return launches, b, 0, {"read": b}, cfg, {"read": 0}
+    if name == "gemm2048":
+        # The practical ceiling of the matrix cores on config 2's two shapes: the vendor bf16 GEMM
+        # (torch.matmul, hipBLASLt) with the weights already dequantized to bf16 row-major. Not part
+        # of the path: a reference point for prefill2048, which also dequantizes q4.
+        m = 2048
+        shapes = (("gemm_up", 17408, 5120), ("gemm_down", 5120, 17408))
+        wb = {nm: torch.randn(n, k, device="cuda", generator=gen).to(torch.bfloat16) for nm, n, k in shapes}
+        xs = {nm: torch.randn(m, k, device="cuda", generator=gen).to(torch.bfloat16) for nm, n, k in shapes}
+        outs = {nm: torch.empty(m, n, dtype=torch.bfloat16, device="cuda") for nm, n, k in shapes}
+
+        def launches(i):
+            return [(nm, lambda nm=nm: torch.matmul(xs[nm], wb[nm].t(), out=outs[nm])) for nm, _, _ in shapes]
+
+        kb = {nm: 2 * n * k + m * k * 2 + m * n * 2 for nm, n, k in shapes}
+        kf = {nm: 2 * m * n * k for nm, n, k in shapes}
+        cfg = {"workload": "bf16 GEMM (torch.matmul) on the prefill shapes (reference point, not the path)",
+               "rows": m, "format": "bf16", "weight_copies": 1}
+        return launches, sum(kb.values()), sum(kf.values()), kb, cfg, kf
     if name == "emit64":
         # The MLP's down projection at M=64 as the residual projection that feeds the next RMSNorm:
         # fp32 hidden state += a w^T, and the next GEMM's operand (bf16 h * norm weight, per-64 sums
@@ -495,7 +513,7 @@ def main():
 
     dominant = max(per_kernel, key=per_kernel.get)
     dom_ms = per_kernel[dominant]
-    compute_bound = args.workload == "prefill2048"
+    compute_bound = args.workload in ("prefill2048", "gemm2048")
     traffic = MEASURED_TRAFFIC.get((args.workload, dominant))
     traffic = int(traffic) if traffic is not None else None
     if compute_bound:

@@ -135,8 +135,8 @@ hipError_t launch_q4_tile(const TilePlan &plan, const splosh_q4_weight &w, const
                           const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype, const void *residual,
                           int64_t rows, void *workspace, hipStream_t stream);
 
-// The prefill kernel for one tiled weight (prefill.hip): 256 x 256 tiles, one wave per SIMD,
-// weights dequantized in registers; stream-K over a caller workspace of prefill_workspace_bytes().
+// The prefill kernel for one tiled weight (prefill.hip): 256 x 256 tiles, two waves per SIMD,
+// weights dequantized once a workgroup into LDS; stream-K over a caller workspace of prefill_workspace_bytes().
 struct PrefillPlan {
     int mblocks;       // row blocks of 256
     int tiles;

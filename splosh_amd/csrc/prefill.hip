@@ -1,23 +1,23 @@
 // prefill.hip -- q4 GEMM for prefill (hundreds to thousands of activation rows) on
-// v_mfma_f32_32x32x16_bf16, one wave per SIMD.
+// v_mfma_f32_32x32x16_bf16, two waves per SIMD.
 //
-// A workgroup of four waves computes a 256 x 256 output tile; wave w owns all 256 rows of columns
-// 64 w .. 64 w + 63 (8 x 2 MFMA tiles of 32 x 32: 256 fp32 accumulators a lane, held in AGPRs,
-// which is why the kernel runs one wave per SIMD). Per 64-group of K, one "chunk":
-//  * The chunk's activations A[256][64] (32 KB), codes (256 columns x 32 bytes) and sidecars are
-//    staged global -> registers -> LDS by all threads, one group ahead, into one of three buffers
-//    (row strides 144 and 48 bytes: the operand and code reads do not conflict), with one barrier
-//    per group, in its middle.
-//  * Lane (r, h) of wave w reads the 16 bytes of the record of column 64 w + 32 j + r (j = 0, 1)
-//    that hold words 4 h .. 4 h + 3 -- the B operands of the group's four 16-deep MFMA steps -- and
-//    turns each word into eight bf16 weights in 17 VALU (dequant_word_mix) one MFMA step ahead.
-//    Every weight is dequantized exactly once, in registers.
-//  * MFMA step i uses k = 32 h + 8 i .. + 7 for both operands (the order of the code words), so the
-//    A operand of row r is the 16-byte LDS piece 4 h + i of that row.
-// Per group a wave issues 64 MFMAs (2048 cycles of the matrix core) against about 160 VALU, 32 LDS
-// operand reads and 41 KB of L2 and HBM traffic per workgroup: the kernel is MFMA-bound. Within one
-// wave every VALU instruction placed between MFMAs delays the matrix core by about three cycles
-// (measured), so the VALU count per group matters.
+// A workgroup of eight waves computes a 256 x 256 output tile; wave (wm, wn) = (wave / 4,
+// wave % 4) owns rows 128 wm .. 128 wm + 127 of columns 64 wn .. 64 wn + 63 (4 x 2 MFMA tiles of
+// 32 x 32: 128 fp32 accumulators a lane, in AGPRs). Per 64-group of K:
+//  * the activations A[256][64] go straight into LDS (buffer loads with the LDS modifier), rows of
+//    128 bytes whose 16-byte pieces are swizzled: piece P of row R sits at slot P ^ ((R / 2) mod 8),
+//    so that a wave's writes are contiguous and the operand reads of 16 consecutive rows hit 16
+//    different bank groups;
+//  * every thread loads a 16-byte piece of one column's codes with that column's scale and bias,
+//    dequantizes its four code words into bf16 (dequant_word_mix, 17 VALU per 8 weights) and writes
+//    them into the group's weight buffer ([256 columns][64 k], rows of 144 bytes: the operand reads
+//    of 32 consecutive columns do not conflict). Every weight is dequantized once a workgroup.
+//  * MFMA step i uses k = 32 h + 8 i .. + 7 for both operands, piece 4 h + i of a row or column.
+// Two buffers: in step t the waves multiply out of buffer t mod 2 while group t + 1 fills buffer
+// t + 1 mod 2 (its activations loaded at the start of the step, its codes loaded a step earlier and
+// dequantized during the step) and group t + 2's codes are loaded; one barrier ends the step. With
+// two waves on a SIMD one wave's dequantization and LDS traffic run while the other's MFMAs keep
+// the matrix core busy.
 //
 // Work split. Tiles are numbered row block first (tile t: row block t mod MB, column block t / MB),
 // so that with eight row blocks every XCD (workgroup id mod 8) works on one row block and keeps
@@ -55,28 +55,74 @@ struct PrefillArgs {
 };
 
 constexpr int kPB = 256;                       // tile rows and columns
-constexpr int kPRow = 144;                     // LDS bytes per activation row (128 + 16)
-constexpr int kPABuf = kPB * kPRow;            // one activation buffer
+constexpr int kPRow = 144;                     // LDS bytes per weight column (128 + 16)
+constexpr int kPABuf = kPB * kPRow;            // one weight buffer
 constexpr int kPEpiRow = 68;                   // floats per row of a wave's epilogue staging
 constexpr int kPEpi = 32 * kPEpiRow * 4;       // bytes of a wave's epilogue staging (32 rows)
-constexpr int kPCodeRow = 48;                  // LDS bytes per column of a code chunk (32 + 16)
-constexpr int kPCodeBytes = kPB * kPCodeRow;   // the codes of a chunk
-constexpr int kPBuf = kPABuf + kPCodeBytes + 2 * kPB * 2;  // activations, codes, scales and biases
-constexpr size_t kPLds = 3 * kPBuf;            // the epilogue staging reuses the buffers
-static_assert(8 * kPEpi <= (int)kPLds, "eight waves' epilogue staging fits the activation buffers");
 constexpr int kPFinishMax = 1024;              // contributors q4_prefill_finish can list
 
-// WM waves per SIMD: 4 WM waves, wave (wm, wn) = (wave / 4, wave % 4) owns rows
-// 256 / WM * wm .. of columns 64 wn ..; the WM waves sharing a SIMD (equal wn) dequantize the same
-// weights, each for its own rows. Only WM = 1 is launched: with two waves per SIMD (128
-// accumulators each) the doubled dequantization costs more than the second wave hides.
-template <int WM>
-__global__ void __launch_bounds__(256 * WM) __attribute__((amdgpu_waves_per_eu(WM, WM)))
+// A wave's share of a finished tile: rows tr0 .. tr0 + 32 FM - 1 of columns tc0 .. tc0 + 63, one
+// 32-row block at a time through the wave's own LDS area `epi` (over the operand buffers, once
+// every wave is done with them): lane (r, h) holds row 8 (e / 4) + 4 h + e % 4, column 32 j + r;
+// the rows are then written 16 bytes (4 columns) a lane, to the output (slot < 0) or to this
+// workgroup's partial tile `slot`.
+template <int FM>
+__device__ __forceinline__ void prefill_store_tile(const PrefillArgs &args, const f32x16 (&acc)[FM][2], char *epi,
+                                                   int64_t m0, int64_t n0, int tc0, int tr0, int lane, int slot) {
+    const int r = lane & 31, h = lane >> 5;
+#pragma unroll
+    for (int f = 0; f < FM; ++f) {
+        const int tr = tr0 + 32 * f;  // the block's first row in the tile
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int row = 8 * (e >> 2) + 4 * h + (e & 3);
+                *(float *)(epi + (row * kPEpiRow + 32 * j + r) * 4) = acc[f][j][e];
+            }
+#pragma unroll
+        for (int p = 0; p < 8; ++p) {
+            const int idx = p * 64 + lane, row = idx >> 4, c4 = (idx & 15) * 4;
+            const f32x4 v = *(const f32x4 *)(epi + (row * kPEpiRow + c4) * 4);
+            const int64_t m = m0 + tr + row, n = n0 + tc0 + c4;
+            if (m >= args.rows || n >= args.n) continue;
+            if (slot >= 0) {
+                float *dst = args.partial + ((int64_t)(blockIdx.x * 2 + slot) * kPB + tr + row) * kPB + tc0 + c4;
+                *(f32x4 *)dst = v;
+                continue;
+            }
+            const int64_t index = m * args.ldc + n;
+            if (args.out_dtype == SPLOSH_F32) {
+                f32x4 o = v;
+                if (args.residual) o += *(const f32x4 *)((const float *)args.residual + index);
+                *(f32x4 *)((float *)args.out + index) = o;
+            } else {
+                float o[4] = {v[0], v[1], v[2], v[3]};
+                if (args.residual) {
+                    const u32x2 rb = *(const u32x2 *)((const uint16_t *)args.residual + index);
+                    o[0] += bf16_bits_to_f32(rb[0] & 0xffffu);
+                    o[1] += bf16_bits_to_f32(rb[0] >> 16);
+                    o[2] += bf16_bits_to_f32(rb[1] & 0xffffu);
+                    o[3] += bf16_bits_to_f32(rb[1] >> 16);
+                }
+                const u32x2 pk = {f32x2_to_bf16x2(o[0], o[1]), f32x2_to_bf16x2(o[2], o[3])};
+                *(u32x2 *)((uint16_t *)args.out + index) = pk;
+            }
+        }
+    }
+}
+
+// The kernel's buffers (see the top of the file).
+constexpr int kSA = kPB * 128;                 // swizzled activations of a group
+constexpr int kSBuf = kSA + kPABuf;            // activations and bf16 weights of a group
+constexpr size_t kSLds = 2 * (size_t)kSBuf;
+constexpr int kSALoads = 4;                    // activation loads (into LDS) of a wave and group
+constexpr int kSCodeLoads = 3;                 // code, scale and bias loads of a thread and group
+static_assert(8 * kPEpi <= (int)kSLds, "eight waves' epilogue staging fits the buffers");
+
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 q4_prefill_kernel(PrefillArgs args) {
-    constexpr int kPThreads = 256 * WM;
-    constexpr int FM = 8 / WM;     // 32-row blocks per wave
-    constexpr int kAPer = 8 / WM;  // activation pieces per thread and chunk
-    constexpr int kCPer = 2 / WM;  // code pieces per thread and chunk
+    constexpr int FM = 4, kAPer = 4;
     extern __shared__ __align__(16) char lds[];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -92,104 +138,78 @@ q4_prefill_kernel(PrefillArgs args) {
     uint32_t magic;
     asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic));
     {
-        // An AGPR operand makes the compiler select the AGPR form of the MFMAs even where a wave's
-        // register budget is 256 (two waves per SIMD): the accumulators then live in AGPRs.
-        float agpr_use;
+        float agpr_use;  // accumulators in AGPRs (see q4_prefill_kernel)
         asm volatile("v_accvgpr_write_b32 %0, 0" : "=a"(agpr_use));
         (void)agpr_use;
     }
-    char *epi = lds + wave * kPEpi;  // after the main loop, over the activation buffers
+    char *epi = lds + wave * kPEpi;
+    // The operand slot of piece 4 h + i for this lane's rows (32-row blocks start at multiples of
+    // 16 rows, so the swizzle only depends on r).
+    const int swz = (r >> 1) & 7;
 
-    // Tile `tile`, groups [ga, gb); slot < 0 writes the output, else a partial.
     auto run_job = [&](int tile, int ga, int gb, int slot) {
         const int mb = tile % args.mblocks, nb = tile / args.mblocks;
         const int64_t m0 = (int64_t)mb * kPB, n0 = (int64_t)nb * kPB;
         const int T = gb - ga;
-        // Chunk staging (group g of the tile, global -> registers -> LDS buffer):
-        //  * activation piece p of this thread: c = p * threads + tid, row c / 8, 16-byte piece
-        //    c % 8 of the row's 128 bytes (rows past the last clamped);
-        //  * code piece p: c = p * threads + tid, half c % 2 of column c / 2's 32-byte record
-        //    (columns past the last clamped);
-        //  * sidecars: lanes 0..31 of wave 0 (scales) and wave 1 (biases), 8 columns a lane.
-        uint32_t a_src[kAPer], c_src[kCPer];
+        // Activation load p of this wave writes LDS bytes [8192 p + 1024 wave, + 1024): lane l takes
+        // row 64 p + 8 wave + l / 8, slot l % 8, i.e. piece (l % 8) ^ ((row / 2) mod 8) (rows past
+        // the last clamped).
+        uint32_t a_src[kAPer];
 #pragma unroll
         for (int p = 0; p < kAPer; ++p) {
-            const int c = p * kPThreads + tid;
-            const int64_t m = m0 + (c >> 3);
-            a_src[p] = (uint32_t)(((m < args.rows ? m : args.rows - 1) * args.lda + (c & 7) * 8) * 2);
+            const int row = 64 * p + 8 * wave + (lane >> 3);
+            const int piece = (lane & 7) ^ ((row >> 1) & 7);
+            const int64_t m = m0 + row;
+            a_src[p] = (uint32_t)(((m < args.rows ? m : args.rows - 1) * args.lda + piece * 8) * 2);
         }
-#pragma unroll
-        for (int p = 0; p < kCPer; ++p) {
-            const int c = p * kPThreads + tid;
-            const int64_t nc = n0 + (c >> 1);
-            const uint32_t col = (uint32_t)(nc < args.n ? nc : args.n - 1);
-            c_src[p] = ((col >> 7) * G32 * 128u + (col & 127u)) * 32u + 16u * (c & 1);
-        }
-        const bool side_loader = wave < 2 && lane < 32;
-        uint32_t side_src;
+        // The codes of column tid / 2, half tid % 2 (words 4 (tid % 2) .. + 3), and that column's
+        // scale and bias (columns past the last clamped).
+        const int hh = tid & 1, sc = tid >> 1;
+        uint32_t c_src, s_src;
         {
-            const int64_t nc = n0 + 8 * (lane & 31);
-            const uint32_t col = (uint32_t)(nc < args.n ? nc : args.n - 8);
-            side_src = ((col >> 7) * G32 * 128u + (col & 127u)) * 2u;
+            const int64_t nc = n0 + sc;
+            const uint32_t col = (uint32_t)(nc < args.n ? nc : args.n - 1);
+            const uint32_t rec = (col >> 7) * G32 * 128u + (col & 127u);
+            c_src = rec * 32u + 16u * hh;
+            s_src = rec * 2u;
         }
-        const rsrc_t side_rsrc = wave == 1 ? b_rsrc : s_rsrc;
-        auto a_lds = [&](int p) { return (uint32_t)(((p * kPThreads + tid) >> 3) * kPRow + (tid & 7) * 16); };
-        auto c_lds = [&](int p) {
-            const int c = p * kPThreads + tid;
-            return (uint32_t)(kPABuf + (c >> 1) * kPCodeRow + 16 * (c & 1));
-        };
+        const uint32_t b_dst = (uint32_t)(kSA + sc * kPRow + 64 * hh);
         auto clampg = [&](int t) {
             const int g = ga + t < gb ? ga + t : gb - 1;
             return (uint32_t)__builtin_amdgcn_readfirstlane(g);
         };
-
-        u32x4 ar[kAPer], cr[kCPer], sr = {0u, 0u, 0u, 0u};
-        // Half 0: the first activation pieces and the codes; half 1: the others and the sidecars.
-        constexpr int kHalf = kAPer / 2;
-        auto load_half = [&](int t, int half) {
+        auto load_a = [&](int t, int buf) {
             const uint32_t g = clampg(t);
 #pragma unroll
-            for (int p = kHalf * half; p < kHalf * (half + 1); ++p) ar[p] = buffer_load16(a_rsrc, a_src[p] + g * 128u, 0);
-            if (half == 0) {
-#pragma unroll
-                for (int p = 0; p < kCPer; ++p) cr[p] = buffer_load16_cp<2>(q_rsrc, c_src[p] + g * (128u * 32u), 0);
-            } else if (side_loader) {
-                sr = buffer_load16(side_rsrc, side_src + g * 256u, 0);
-            }
+            for (int p = 0; p < kAPer; ++p)
+                buffer_load_lds16(a_rsrc, lds + buf * kSBuf + 8192 * p + 1024 * wave, a_src[p] + g * 128u);
         };
-        auto store_half = [&](int buf, int half) {
-            char *b = lds + buf * kPBuf;
-#pragma unroll
-            for (int p = kHalf * half; p < kHalf * (half + 1); ++p) *(u32x4 *)(b + a_lds(p)) = ar[p];
-            if (half == 0) {
-#pragma unroll
-                for (int p = 0; p < kCPer; ++p) *(u32x4 *)(b + c_lds(p)) = cr[p];
-            } else if (side_loader) {
-                *(u32x4 *)(b + kPABuf + kPCodeBytes + wave * 512 + lane * 16) = sr;
-            }
+        // Codes and sidecars in two register sets: group t's in set t mod 2.
+        u32x4 cr[2];
+        uint32_t sr[2], br[2];
+        auto load_codes = [&](int t, int set) {
+            const uint32_t g = clampg(t);
+            cr[set] = buffer_load16_cp<2>(q_rsrc, c_src + g * (128u * 32u), 0);
+            sr[set] = buffer_load_u16(s_rsrc, s_src + g * 256u, 0);
+            br[set] = buffer_load_u16(b_rsrc, s_src + g * 256u, 0);
         };
-        // A wave's codes of a chunk (16 bytes of column 64 wn + 32 j + r: words 4 h .. 4 h + 3) and
-        // their coefficients (zero for the padding steps).
-        auto read_codes = [&](u32x4 *dst, int buf) {
-            const char *b = lds + buf * kPBuf + kPABuf + (64 * wn + r) * kPCodeRow + 16 * h;
+        // Group t's weights (words q0, q0 + 1 of this thread's piece) into buffer `buf`; zero
+        // coefficients past the job (the step count is padded to even).
+        auto store_b = [&](int buf, int set, bool on, int q0) {
+            const MixCoef cf =
+                mix_coef(on ? bf16_bits_to_f32(sr[set]) : 0.0f, on ? bf16_bits_to_f32(br[set]) : 0.0f);
+            char *b = lds + buf * kSBuf + b_dst;
 #pragma unroll
-            for (int j = 0; j < 2; ++j) dst[j] = *(const u32x4 *)(b + 32 * j * kPCodeRow);
+            for (int q = q0; q < q0 + 2; ++q) *(bf16x8 *)(b + 16 * q) = dequant_word_mix(cr[set][q], cf, magic);
         };
-        MixCoef cf[2];
-        auto read_coef = [&](int buf, bool on) {
-            const char *b = lds + buf * kPBuf + kPABuf + kPCodeBytes + (64 * wn + r) * 2;
+        // Operands of MFMA step i (k = 32 h + 8 i .. + 7 of the group, piece 4 h + i of a row).
+        auto read_ops = [&](bf16x8 *af, bf16x8 *bw, int buf, int i) {
+            const char *pa = lds + buf * kSBuf + (128 * wm + r) * 128 + (((4 * h + i) ^ swz) << 4);
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const float sc = bf16_bits_to_f32(*(const uint16_t *)(b + 64 * j));
-                const float bi = bf16_bits_to_f32(*(const uint16_t *)(b + 512 + 64 * j));
-                cf[j] = mix_coef(on ? sc : 0.0f, on ? bi : 0.0f);
-            }
-        };
-        // Operand reads: MFMA step i of row block f takes row 32 (FM wm + f) + r, piece 4 h + i.
-        auto read_af = [&](bf16x8 *dst, int buf, int i) {
-            const char *p = lds + buf * kPBuf + (FM * wm * 32 + r) * kPRow + (4 * h + i) * 16;
+            for (int f = 0; f < FM; ++f) af[f] = as_bf16x8(*(const u32x4 *)(pa + f * 32 * 128));
+            const char *pb = lds + buf * kSBuf + kSA + (64 * wn + r) * kPRow + (4 * h + i) * 16;
 #pragma unroll
-            for (int f = 0; f < FM; ++f) dst[f] = as_bf16x8(*(const u32x4 *)(p + f * 32 * kPRow));
+            for (int j = 0; j < 2; ++j) bw[j] = as_bf16x8(*(const u32x4 *)(pb + j * 32 * kPRow));
         };
 
         f32x16 acc[FM][2];
@@ -200,155 +220,53 @@ q4_prefill_kernel(PrefillArgs args) {
 #pragma unroll
                 for (int e = 0; e < 16; ++e) acc[f][j][e] = 0.0f;
 
-        // Prologue, loads in the loop's order (so that the wait counts the compiler derives at the
-        // loop head leave the younger loads in flight).
-        load_half(0, 0);
-        load_half(0, 1);
-        store_half(0, 0);
-        store_half(0, 1);
+        // Prologue: group 0 into buffer 0, group 1's codes in flight.
+        load_a(0, 0);
+        load_codes(0, 0);
+        store_b(0, 0, T > 0, 0);
+        store_b(0, 0, T > 0, 2);
         __builtin_amdgcn_sched_barrier(0);
-        load_half(1, 0);
+        load_codes(1, 1);
         __builtin_amdgcn_sched_barrier(0);
-        load_half(1, 1);
-        __builtin_amdgcn_sched_barrier(0);
-        lds_barrier();
-        u32x4 cq[2];  // codes of the current group
-        read_codes(cq, 0);
-        read_coef(0, T > 0);
-        bf16x8 bw[2];  // B operands of the current MFMA step
-#pragma unroll
-        for (int j = 0; j < 2; ++j) bw[j] = dequant_word_mix(cq[j][0], cf[j], magic);
-        bf16x8 af[FM];
-        if (WM == 1) read_af(af, 0, 0);
+        wait_vmcnt<kSCodeLoads>();  // group 0's activations have landed; group 1's codes may not
+        lds_barrier_staged<0>();
 
-        // Step t (group ga + t), d = t mod 3 = its LDS buffer. Every MFMA step interleaves its
-        // MFMAs with the dequantization of the next MFMA step's operands (with one wave per SIMD
-        // the VALU work only hides under the matrix core when its instructions sit between the
-        // MFMAs), its fragment reads and a share of the chunk traffic, spread so that no step
-        // queues at the texture unit:
-        //  * steps 0 and 1 store chunk t + 1 (loaded in step t - 1) into buffer t + 1 mod 3, half
-        //    each, and steps 1 and 2 load chunk t + 2 into the registers just stored;
-        //  * the barrier before step 2 makes chunk t + 1 readable: step 2 reads its codes and
-        //    coefficients, step 3 dequantizes its first operands (and, with one wave per SIMD,
-        //    prefetches its first fragments). Every wave has then finished step t - 1, so buffer
-        //    t + 2 mod 3 (last read in step t - 1) may be written in step t + 1.
-        // Loads past the job re-read its last group.
+        // Step t: buffer and code set d = t mod 2.
         auto step = [&](int t, int d) {
-            const int next = d == 2 ? 0 : d + 1;
-            u32x4 cn[2];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                if (i == 2) {
-                    lds_barrier();
+                // Group t + 1's activations into the other buffer and group t + 2's codes, a step
+                // ahead of their use (pinned here, or the scheduler sinks them to the end of the
+                // step); group t + 1's weights over MFMA steps 1 and 2.
+                if (i == 0) {
+                    load_a(t + 1, d ^ 1);
+                    load_codes(t + 2, d);
                     __builtin_amdgcn_sched_barrier(0);
                 }
-                // One wave per SIMD prefetches the next MFMA step's fragments; with two, the other
-                // wave covers the read latency and the registers are short.
-                constexpr bool kPrefetch = WM == 1;
-                bf16x8 an[FM];
-                if (kPrefetch)
-                    read_af(an, i < 3 ? d : next, i < 3 ? i + 1 : 0);
-                else
-                    read_af(af, d, i);
-                if (i == 2) read_codes(cn, next);
+                // No operand prefetch: the other wave on the SIMD covers the read latency.
+                bf16x8 af[FM], bw[2];
+                read_ops(af, bw, d, i);
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
 #pragma unroll
                     for (int f = 0; f < FM; ++f)
                         acc[f][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[f], bw[j], acc[f][j], 0, 0, 0);
-                // The next MFMA step's operands: word i + 1 of this group, or word 0 of the next.
-                if (i < 3) {
-#pragma unroll
-                    for (int j = 0; j < 2; ++j) bw[j] = dequant_word_mix(cq[j][i + 1], cf[j], magic);
-                } else {
-                    read_coef(next, t + 1 < T);
-#pragma unroll
-                    for (int j = 0; j < 2; ++j) {
-                        cq[j] = cn[j];
-                        bw[j] = dequant_word_mix(cq[j][0], cf[j], magic);
-                    }
-                }
-                if (i < 2) store_half(next, i);
-                if (i == 1 || i == 2) load_half(t + 2, i - 1);
-                constexpr int kMfma = 2 * FM, kValu = (36 + kMfma - 1) / kMfma;
-#pragma unroll
-                for (int m = 0; m < kMfma; ++m) {
-                    if (m < FM) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);     // one LDS read
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                 // one MFMA
-                    __builtin_amdgcn_sched_group_barrier(0x002, kValu, 0);             // VALU
-                    if (m < 8 / WM && (WM == 2 || m % 2 == 1)) {
-                        if (i < 2) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // LDS write
-                        if (i == 1 || i == 2) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM
-                    }
-                }
-                __builtin_amdgcn_sched_barrier(0);
-                if (kPrefetch) {
-#pragma unroll
-                    for (int f = 0; f < FM; ++f) af[f] = an[f];
-                }
+                if (i == 1 || i == 2) store_b(d ^ 1, d ^ 1, t + 1 < T, 2 * (i - 1));
             }
+            // Group t + 1's activations have landed (only group t + 2's code loads, issued after
+            // them, may be outstanding), and every wave is done with buffer t mod 2.
+            __builtin_amdgcn_sched_barrier(0);
+            wait_vmcnt<kSCodeLoads>();
+            lds_barrier_staged<0>();
         };
-        // The step count is padded to a multiple of three (no early exit, whose extra paths cost
-        // the accumulators register copies); steps past T multiply zero weights.
-        const int Tp = (T + 2) / 3 * 3;
-        for (int t0 = 0; t0 < Tp; t0 += 3) {
+        const int Tp = (T + 1) / 2 * 2;
+        for (int t0 = 0; t0 < Tp; t0 += 2) {
             step(t0, 0);
             step(t0 + 1, 1);
-            step(t0 + 2, 2);
         }
-
-        // Epilogue, one 32-row block at a time through the wave's own LDS area (over the
-        // activation buffers, once every wave is done with them): lane (r, h) holds row
-        // 8 (e / 4) + 4 h + e % 4, column 32 j + r; the rows are then written 16 bytes (4 columns)
-        // a lane.
-        lds_barrier();
-        const int64_t nw0 = n0 + 64 * wn;
-#pragma unroll
-        for (int f = 0; f < FM; ++f) {
-            const int tr0 = 32 * (FM * wm + f);  // the block's first row in the tile
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-#pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int row = 8 * (e >> 2) + 4 * h + (e & 3);
-                    *(float *)(epi + (row * kPEpiRow + 32 * j + r) * 4) = acc[f][j][e];
-                }
-#pragma unroll
-            for (int p = 0; p < 8; ++p) {
-                const int idx = p * 64 + lane, row = idx >> 4, c4 = (idx & 15) * 4;
-                const f32x4 v = *(const f32x4 *)(epi + (row * kPEpiRow + c4) * 4);
-                const int64_t m = m0 + tr0 + row, n = nw0 + c4;
-                if (m >= args.rows || n >= args.n) continue;
-                if (slot >= 0) {
-                    float *dst = args.partial + ((int64_t)(blockIdx.x * 2 + slot) * kPB + tr0 + row) * kPB +
-                                 64 * wn + c4;
-                    *(f32x4 *)dst = v;
-                    continue;
-                }
-                const int64_t index = m * args.ldc + n;
-                if (args.out_dtype == SPLOSH_F32) {
-                    f32x4 o = v;
-                    if (args.residual) o += *(const f32x4 *)((const float *)args.residual + index);
-                    *(f32x4 *)((float *)args.out + index) = o;
-                } else {
-                    float o[4] = {v[0], v[1], v[2], v[3]};
-                    if (args.residual) {
-                        const u32x2 rb = *(const u32x2 *)((const uint16_t *)args.residual + index);
-                        o[0] += bf16_bits_to_f32(rb[0] & 0xffffu);
-                        o[1] += bf16_bits_to_f32(rb[0] >> 16);
-                        o[2] += bf16_bits_to_f32(rb[1] & 0xffffu);
-                        o[3] += bf16_bits_to_f32(rb[1] >> 16);
-                    }
-                    const u32x2 pk = {f32x2_to_bf16x2(o[0], o[1]), f32x2_to_bf16x2(o[2], o[3])};
-                    *(u32x2 *)((uint16_t *)args.out + index) = pk;
-                }
-            }
-        }
+        prefill_store_tile<FM>(args, acc, epi, m0, n0, 64 * wn, 32 * FM * wm, lane, slot);
     };
 
-    // The jobs: whole tiles blockIdx.x, blockIdx.x + P, ... below dp_tiles, then this workgroup's
-    // range of the remaining (tile, group) pairs, cut at tile boundaries. One call site, so that
-    // run_job is inlined.
     const int P = gridDim.x;
     int dp_tile = blockIdx.x;
     int64_t u = args.sk_units * blockIdx.x / P;
@@ -481,17 +399,6 @@ size_t prefill_workspace_bytes(int64_t rows, int64_t columns, int64_t groups) {
     return p.sk_units > 0 ? prefill_sk_bytes(p.grid) : 0;
 }
 
-template <int WM>
-static void launch_prefill_wm(const PrefillPlan &plan, const PrefillArgs &args, hipStream_t stream) {
-    static bool once = [] {
-        (void)hipFuncSetAttribute((const void *)q4_prefill_kernel<WM>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  (int)kPLds);
-        return true;
-    }();
-    (void)once;
-    hipLaunchKernelGGL(q4_prefill_kernel<WM>, dim3((unsigned)plan.grid), dim3(256 * WM), kPLds, stream, args);
-}
-
 hipError_t launch_q4_prefill(const PrefillPlan &plan, const splosh_q4_weight &w, const uint16_t *a, int64_t lda,
                              void *out, int64_t ldc, int out_dtype, const void *residual, int64_t rows,
                              void *workspace, hipStream_t stream) {
@@ -515,7 +422,13 @@ hipError_t launch_q4_prefill(const PrefillPlan &plan, const splosh_q4_weight &w,
     args.code_bytes = (uint32_t)(w.rows * args.groups * 32);
     args.sidecar_bytes = (uint32_t)(w.rows * args.groups * 2);
     args.a_bytes = (uint32_t)(((rows - 1) * lda + w.inner) * 2);
-    launch_prefill_wm<1>(plan, args, stream);
+    static bool once = [] {
+        (void)hipFuncSetAttribute((const void *)q4_prefill_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)kSLds);
+        return true;
+    }();
+    (void)once;
+    hipLaunchKernelGGL(q4_prefill_kernel, dim3((unsigned)plan.grid), dim3(512), kSLds, stream, args);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess || plan.sk_units == 0) return err;
     const int remainder = plan.tiles - plan.dp_tiles;

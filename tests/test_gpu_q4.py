@@ -245,7 +245,7 @@ def test_prefill_shape_sampled(rt):
 @pytest.mark.parametrize("rows,n,k", [(256, 256, 640), (300, 384, 576), (513, 128, 64)])
 @pytest.mark.parametrize("split", [True, False])
 def test_prefill_kernel(rt, rows, n, k, split):
-    """The one-wave-per-SIMD prefill kernel: whole and partial 256 x 256 tiles, with the last round
+    """The prefill kernel (two waves a SIMD): whole and partial 256 x 256 tiles, with the last round
     of tiles split over all workgroups (stream-K, a workspace) and without (every tile whole)."""
     case = Q4Case(n, k, seed=rows + n)
     a_bits = oracle.bf16_normal((rows, k), seed=k)

@@ -27,9 +27,9 @@ HIPCC = "/opt/rocm/bin/hipcc"
 VMEM = re.compile(r"^\s*(buffer_load|global_load|buffer_store|global_store|buffer_atomic|global_atomic)")
 
 
-def _kernels(asm):
+def _kernels(asm, symbol=r"_ZN6splosh10mma_kernel\S*"):
     lines = asm.split("\n")
-    starts = [i for i, l in enumerate(lines) if re.match(r"^_ZN6splosh10mma_kernel\S*:", l)]
+    starts = [i for i, l in enumerate(lines) if re.match(rf"^{symbol}:", l)]
     for j, i in enumerate(starts):
         # The function runs to its end label (it may have more than one s_endpgm).
         end = next((k for k in range(i, len(lines)) if lines[k].startswith(".Lfunc_end")), len(lines))
@@ -123,10 +123,12 @@ def _max_lds(blocks, preds, b, idx, want, memo, stack):
     return lds + best
 
 
-def _check_function(name, code):
-    stage = _stage_loads(name)
+def _check_function(name, code, stage=None):
+    """Checks every barrier after a vmcnt wait; returns (barriers with loads into LDS allowed to
+    stay in flight, barriers checked)."""
+    stage = _stage_loads(name) if stage is None else stage
     blocks, preds = _cfg(code)
-    checked = 0
+    checked = waited = 0
     memo = {}
     for b, ins_list in enumerate(blocks):
         for i, ins in enumerate(ins_list):
@@ -151,6 +153,7 @@ def _check_function(name, code):
                     after += 1
             if n is None:
                 continue
+            waited += 1
             lds = _max_lds(blocks, preds, b, wait_at, n, memo, set()) + after
             assert lds <= allowed, (
                 f"{name}: a barrier's vmcnt({n}) leaves {lds} loads into LDS outstanding, the "
@@ -158,7 +161,7 @@ def _check_function(name, code):
             if allowed:
                 assert allowed % stage == 0, (name, allowed, stage)
                 checked += 1
-    return checked
+    return checked, waited
 
 
 @pytest.mark.skipif(not Path(HIPCC).exists(), reason="needs hipcc")
@@ -174,4 +177,23 @@ def test_mma_stage_waits_cover_their_loads(tmp_path):
     for name, code in kernels:
         # Every instantiation has the prologue barrier and at least three mid-step barriers whose
         # waits keep loads in flight.
-        assert _check_function(name, code) >= 4, name
+        assert _check_function(name, code)[0] >= 4, name
+
+
+@pytest.mark.skipif(not Path(HIPCC).exists(), reason="needs hipcc")
+def test_prefill_stage_waits_cover_their_loads(tmp_path):
+    """The prefill kernel's activations arrive through loads into LDS, four a wave and group; the
+    wait before each step's barrier must leave none of them in flight (only the code loads issued
+    after them)."""
+    out = tmp_path / "prefill.s"
+    cmd = [HIPCC, "-O3", "-std=c++17", "--offload-arch=gfx950", "-Xclang", "-target-feature", "-Xclang",
+           "-packed-fp32-ops", f"-I{ROOT / 'include'}", "--cuda-device-only", "-S",
+           str(ROOT / "splosh_amd" / "csrc" / "prefill.hip"), "-o", str(out)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    assert res.returncode == 0, res.stderr[-2000:]
+    kernels = list(_kernels(out.read_text(), r"_ZN6splosh17q4_prefill_kernel\S*"))
+    assert len(kernels) == 1
+    for name, code in kernels:
+        assert any(_is_lds(ins) for ins in code), name
+        # The prologue's barrier and the two unrolled steps'.
+        assert _check_function(name, code, stage=4)[1] >= 3, name
