@@ -44,8 +44,8 @@ MEASURED_TRAFFIC = {
     ("prefill2048", "prefill_up"): 264479.7 * 2 * 1024 + 114688.0 * 1024,  # q4_prefill_kernel
     ("q5k2048", "q5k"): 374456.7 * 2 * 1024 + 20480.9 * 1024,  # gguf_tile_kernel<13, 2, 2, false>
     ("q6k64", "gguf"): (50699.6 + 6421.1) * 2 * 1024 + (25600.0 + 644.2) * 1024,  # gguf_tile_kernel<14, 1, 2, true> + gguf_tile_finish<1, 2>
-    ("q6k1", "gguf"): 36154.8 * 2 * 1024 + 40.0 * 1024,  # gguf_gemv_kernel<14, 4>
-    ("q80_1", "gguf"): 46735.3 * 2 * 1024 + 40.1 * 1024,  # gguf_gemv_kernel<8, 4>
+    ("q6k1", "gguf"): 36140.2 * 2 * 1024 + 10.0 * 1024,  # gguf_gemv_kernel<14, 4>
+    ("q80_1", "gguf"): 46715.8 * 2 * 1024 + 10.0 * 1024,  # gguf_gemv_kernel<8, 4>
     ("stream50", "read"): 24680.2 * 2 * 1024 + 64.0 * 1024,  # stream_read_kernel
     ("layerset", "mlp_in"): 55934.6 * 2 * 1024 + 9871.0 * 1024,  # mma_kernel<Q4Format<2, true, 2, 4, 3>, 2, 2, 4, 3>
     ("emit64", "fused"): 35950.1 * 2 * 1024 + 5475.5 * 1024,  # mma_kernel<Q4Format<1, true, 2, 4, 3>, 2, 2, 4, 3>
