@@ -263,6 +263,33 @@ def test_prefill_kernel(rt, rows, n, k, split):
                 label=f"prefill residual {rows}x{n}x{k} split={split}")
 
 
+@pytest.mark.parametrize("split", [True, False])
+def test_prefill_strides_and_bounds(rt, split):
+    """The prefill kernel on padded activation rows (lda > K), into a wider output buffer (ldc > N)
+    whose other columns and rows must stay untouched, with a bf16 residual of that stride: ragged
+    rows (300) and N (384) a multiple of 128 but not of the 256-column tile."""
+    n, k, rows = 384, 576, 300
+    case = Q4Case(n, k, seed=31)
+    a_full = oracle.bf16_normal((rows, k + 64), seed=32)
+    a_bits = np.ascontiguousarray(a_full[:, :k])
+    ref = oracle.gemm_a_bf16_w_f32(a_bits, case.dense)
+    absref = abs_gemm(a_bits, case.dense)
+    ws = None if split else torch.empty(0, dtype=torch.uint8, device="cuda")
+    out = torch.full((rows + 3, n + 72), 7.0, dtype=torch.float32, device="cuda")
+    rt.gemm(case.w_tiled, bf16_tensor(a_full), out=out, rows=rows, kernel=rt.PREFILL, workspace=ws)
+    o = out.cpu().numpy()
+    check_close(o[:rows, :n], ref, bf16_out=False, tight=True, absref=absref, label=f"prefill strided split={split}")
+    assert np.all(o[:rows, n:] == 7.0) and np.all(o[rows:] == 7.0)
+    base = np.random.default_rng(33).normal(size=(rows + 3, n + 72)).astype(np.float32)
+    res = torch.from_numpy(base).cuda().to(torch.bfloat16)
+    got = res.clone()
+    rt.gemm(case.w_tiled, bf16_tensor(a_full), out=got, residual=got, rows=rows, kernel=rt.PREFILL, workspace=ws)
+    g = got.float().cpu().numpy()
+    check_close(g[:rows, :n], ref + res.float().cpu().numpy()[:rows, :n], bf16_out=True, tight=True,
+                absref=absref + np.abs(res.float().cpu().numpy()[:rows, :n]), label=f"prefill strided residual split={split}")
+    assert torch.equal(got[:rows, n:], res[:rows, n:]) and torch.equal(got[rows:], res[rows:])
+
+
 def test_prefill_down_shape_sampled(rt):
     """Config 2's second shape (M=2048, K=17408 -> N=5120: 160 tiles, all split over the CUs) at
     full size, 256 sampled columns of 256 sampled rows."""
