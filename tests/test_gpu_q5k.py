@@ -95,6 +95,25 @@ def test_baseline_shape_sampled(rt, rows):
                 label=f"q5k full rows={rows}")
 
 
+def test_baseline_shape_prefill_sampled(rt):
+    """Config 3's weight at prefill size (M=2048, the LDS-tiled MFMA kernel): 256 sampled rows x
+    256 sampled columns against the oracle."""
+    n, k, rows = 5120, 17408, 2048
+    native = oracle.q45k_random_native(n, k, seed=78)
+    w = rt.q5k_repack(dev_u8(native), n, k)
+    a_bits = oracle.bf16_normal((rows, k), seed=79)
+    got = to_f32(rt.gemm(w, bf16_tensor(a_bits)))
+    rng = np.random.default_rng(80)
+    cols = np.sort(rng.choice(n, 256, replace=False))
+    sel = np.sort(rng.choice(rows, 256, replace=False))
+    blk = k // 256 * 176
+    dense = oracle.q45k_decode(native.reshape(n, blk)[cols].reshape(-1)).reshape(len(cols), k)
+    a_sel = np.ascontiguousarray(a_bits[sel])
+    ref = oracle.gemm_a_bf16_w_f32(a_sel, dense)
+    check_close(got[sel][:, cols], ref, bf16_out=True, tight=True, absref=abs_gemm(a_sel, dense),
+                label="q5k full rows=2048")
+
+
 @pytest.mark.parametrize("rows", [1, 2, 3, 16, 33, 64])
 @pytest.mark.parametrize("split", [True, False])
 def test_dequant_kernel(rt, rows, split):
