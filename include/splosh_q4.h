@@ -74,9 +74,10 @@ typedef enum splosh_kernel {
                                    registers; uses the workspace for split bands when given one */
     SPLOSH_KERNEL_TILE = 3,     /* any rows: LDS-tiled dequant-to-bf16 MFMA GEMM (prefill) */
     SPLOSH_KERNEL_SCALAR = 4,   /* one thread per output (gemm_q4.metal semantics) */
-    SPLOSH_KERNEL_PREFILL = 5   /* one TILED128 weight (not mlp_in): 256 x 256 output tiles, one
-                                   wave per SIMD, weights dequantized in registers; uses the
-                                   workspace to split the last round of tiles over all CUs */
+    SPLOSH_KERNEL_PREFILL = 5   /* one TILED128 q4 weight (not mlp_in) or Q5_K / Q4_K planes:
+                                   256 x 256 output tiles, two waves per SIMD, every weight
+                                   dequantized once a tile into LDS; uses the workspace to split
+                                   the last round of tiles over all CUs */
 } splosh_kernel;
 
 /* Q4BufferLayout (Quant/Q4BufferLayout.swift:29-79). */
@@ -212,10 +213,12 @@ int splosh_untile128(const void *src, void *dst, int64_t rows, int64_t groups, i
 /* ---- GGUF Q5_K ---------------------------------------------------------------------------- */
 
 /* Engine.gemm on a GGUF weight (Runtime/Engine.swift:1671-1697, kernels
- * Shaders/engine_gguf.metal:82-221 instantiated _q5k at :332-349). AUTO: 1..64 rows take the
- * dequant-to-bf16 MFMA kernel (DEQUANT; lda % 8 == 0 and 16-byte aligned activations), which uses
- * a workspace of splosh_workspace_bytes(rows, w->rows, w->inner) to split K; other row counts take
- * the streaming kernel (STREAM). Odd alignments fall back to SCALAR. */
+ * Shaders/engine_gguf.metal:82-221 instantiated _q5k at :332-349). AUTO: one row takes the
+ * every-CU decode kernel; 2..64 rows the dequant-to-bf16 MFMA kernel (DEQUANT; lda % 8 == 0 and
+ * 16-byte aligned activations); more rows the 256 x 256 prefill kernel (PREFILL; also ldc % 4 == 0
+ * and 16-byte aligned outputs), else the LDS-tiled kernel (TILE), else the streaming kernel
+ * (STREAM). DEQUANT and PREFILL use a workspace of splosh_workspace_bytes(rows, w->rows, w->inner)
+ * to split K. Odd alignments fall back to SCALAR. */
 int splosh_q5k_gemm(const splosh_q5k_weight *w, const uint16_t *a, int64_t lda, void *out, int64_t ldc,
                     int out_dtype, const void *residual, int64_t rows, int kernel, void *workspace,
                     size_t workspace_bytes, hipStream_t stream);

@@ -495,16 +495,33 @@ static int gguf_gemm(const splosh_q5k_weight *w_in, bool fifth, const uint16_t *
     const bool mma_ok = eligible && lda % 8 == 0 && aligned(a, 16) && splosh::q5k_mma_fits(rows, w->rows, w->inner, lda);
     const bool decode_ok = eligible && aligned(a, 16) && splosh::q5k_decode_fits(rows, w->rows, w->inner);
     const bool tile_ok = eligible && lda % 8 == 0 && aligned(a, 16) && splosh::gguf_tile_fits(rows, w->rows, w->inner, lda);
+    const bool prefill_ok = eligible && lda % 8 == 0 && aligned(a, 16) && aligned(out, 16) &&
+                            (!residual || aligned(residual, 16)) &&
+                            splosh::q5k_prefill_fits(rows, w->rows, w->inner, lda, ldc);
     int choice = kernel;
     if (kernel == SPLOSH_KERNEL_AUTO) {
         if (!eligible) choice = SPLOSH_KERNEL_SCALAR;
         else if (decode_ok)
             return hip_status(splosh::launch_q5k_decode(*w, a, out, out_dtype, residual, stream), "q5k decode launch");
         else if (mma_ok) choice = SPLOSH_KERNEL_DEQUANT;
+        // Above 64 rows the 256 x 256 prefill kernel (K17408 -> N5120: 75 us at 128 rows against the
+        // tile kernel's 86, 381 against 627 at 2048).
+        else if (prefill_ok) choice = SPLOSH_KERNEL_PREFILL;
         else if (tile_ok) choice = SPLOSH_KERNEL_TILE;
         else choice = SPLOSH_KERNEL_STREAM;
     }
     switch (choice) {
+        case SPLOSH_KERNEL_PREFILL: {
+            if (!prefill_ok)
+                return fail(SPLOSH_ERR_UNSUPPORTED,
+                            "prefill kernel needs K % 256 == 0, N % 128 == 0, lda % 8 == 0, ldc % 4 == 0 and 16-byte "
+                            "aligned operands");
+            const splosh::PrefillPlan plan =
+                splosh::plan_prefill(rows, w->rows, w->inner / kGroupSize, workspace ? workspace_bytes : 0);
+            return hip_status(splosh::launch_q5k_prefill(plan, *w, fifth, a, lda, out, ldc, out_dtype, residual, rows,
+                                                         workspace, stream),
+                              "q5k prefill launch");
+        }
         case SPLOSH_KERNEL_TILE:
             if (!tile_ok) return fail(SPLOSH_ERR_UNSUPPORTED, "tile kernel needs lda % 8 == 0 and aligned operands");
             return hip_status(splosh::launch_gguf_tile(fifth ? 13 : 12, w->plane0, w->plane1, w->meta, w->rows,

@@ -113,6 +113,18 @@ __device__ __forceinline__ int xcd_block(int id, int grid) {
     return grid % 8 == 0 ? (id & 7) * (grid >> 3) + (id >> 3) : id;
 }
 
+// Byte j of x as an fp32 number (v_cvt_f32_ubyteN, exact).
+__device__ __forceinline__ float cvt_byte(uint32_t x, int j) {
+    float r;
+    switch (j) {
+        case 0: asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(x)); break;
+        case 1: asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(x)); break;
+        case 2: asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(x)); break;
+        default: asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(x)); break;
+    }
+    return r;
+}
+
 // x sigmoid(x) with the hardware reciprocal (v_rcp_f32, about 1 ulp) instead of a full-precision
 // divide: the result is rounded to bf16 or summed in fp32 afterwards.
 __device__ __forceinline__ float silu(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }

@@ -84,17 +84,6 @@ struct MmaArgs {
     float *sums, *squares;   // [rows][n / 64]
 };
 
-__device__ __forceinline__ float cvt_byte(uint32_t x, int j) {
-    float r;
-    switch (j) {
-        case 0: asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(x)); break;
-        case 1: asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(x)); break;
-        case 2: asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(x)); break;
-        default: asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(x)); break;
-    }
-    return r;
-}
-
 // q4 (MLX affine): a step is KW groups of 64; wave kw takes group ga + t KW + kw and lane (r, h)
 // feeds column r from words 4 h .. 4 h + 3 of the group's 32-byte record (one 16-byte load; a
 // wave reads 32 consecutive records, a contiguous kilobyte of the tiled layout). A word becomes

@@ -23,7 +23,7 @@
 // so that with eight row blocks every XCD (workgroup id mod 8) works on one row block and keeps
 // its activations in its L2. As in mma.hip, whole tiles go round-robin over the grid and the
 // remaining tiles' (tile, group) pairs are split evenly over all workgroups (stream-K); a tile
-// covered in part is summed by q4_prefill_finish from fp32 partials in the caller's workspace.
+// covered in part is summed by prefill_finish from fp32 partials in the caller's workspace.
 //
 // Numerics as mma.hip: fp32 dequantized weight rounded to bf16, exact products, fp32 sums.
 #include "common.hpp"
@@ -35,11 +35,11 @@
 namespace splosh {
 
 struct PrefillArgs {
-    const uint32_t *packed;
-    const uint16_t *scales;
-    const uint16_t *biases;
+    // q4: codes, scales, biases; Q5_K / Q4_K: plane0, plane1 (none for Q4_K), meta.
+    const void *w[3];
+    uint32_t w_bytes[3];
     int64_t n;          // weight rows = output columns
-    int64_t groups;
+    int64_t groups;     // 64-element groups of K
     const uint16_t *a;
     int64_t lda;
     void *out;
@@ -51,7 +51,7 @@ struct PrefillArgs {
     float *partial;     // stream-K partial tiles [gridDim.x][2][256][256]
     int dp_tiles;       // tiles computed whole (a multiple of gridDim.x)
     int64_t sk_units;   // (tile, group) pairs of the remaining tiles
-    uint32_t code_bytes, sidecar_bytes, a_bytes;
+    uint32_t a_bytes;
 };
 
 constexpr int kPB = 256;                       // tile rows and columns
@@ -59,7 +59,7 @@ constexpr int kPRow = 144;                     // LDS bytes per weight column (1
 constexpr int kPABuf = kPB * kPRow;            // one weight buffer
 constexpr int kPEpiRow = 68;                   // floats per row of a wave's epilogue staging
 constexpr int kPEpi = 32 * kPEpiRow * 4;       // bytes of a wave's epilogue staging (32 rows)
-constexpr int kPFinishMax = 1024;              // contributors q4_prefill_finish can list
+constexpr int kPFinishMax = 1024;              // contributors prefill_finish can list
 
 // A wave's share of a finished tile: rows tr0 .. tr0 + 32 FM - 1 of columns tc0 .. tc0 + 63, one
 // 32-row block at a time through the wave's own LDS area `epi` (over the operand buffers, once
@@ -112,16 +112,139 @@ __device__ __forceinline__ void prefill_store_tile(const PrefillArgs &args, cons
     }
 }
 
+// The weights of one 64-element group of K for the tile's 256 columns: thread t loads the part
+// of column t / 2 that covers k = 32 (t % 2) .. + 31 of the group, dequantizes it and writes the
+// 64 bytes of bf16 weights into the weight buffer (four 16-byte pieces, `dst` = the first). Loads
+// go to one of two register sets; kLoads loads a thread and group.
+
+// MLX affine q4, TILED128: the thread's 16 bytes of the column's record (words 4 (t % 2) .. + 3)
+// and the column's scale and bias (Retile.swift:135-153), dequantized by dequant_word_mix.
+struct Q4Stage {
+    static constexpr int kLoads = 3;
+    rsrc_t q_rsrc, s_rsrc, b_rsrc;
+    uint32_t magic, c_src, s_src;
+    u32x4 cr[2];
+    uint32_t sr[2], br[2];
+    __device__ Q4Stage(const PrefillArgs &args) {
+        q_rsrc = make_rsrc(args.w[0], args.w_bytes[0]);
+        s_rsrc = make_rsrc(args.w[1], args.w_bytes[1]);
+        b_rsrc = make_rsrc(args.w[2], args.w_bytes[2]);
+        asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic));
+    }
+    __device__ void begin(const PrefillArgs &args, uint32_t col, int hh) {
+        const uint32_t rec = (col >> 7) * (uint32_t)args.groups * 128u + (col & 127u);
+        c_src = rec * 32u + 16u * hh;
+        s_src = rec * 2u;
+    }
+    __device__ void load(uint32_t g, int set) {
+        cr[set] = buffer_load16_cp<2>(q_rsrc, c_src + g * (128u * 32u), 0);
+        sr[set] = buffer_load_u16(s_rsrc, s_src + g * 256u, 0);
+        br[set] = buffer_load_u16(b_rsrc, s_src + g * 256u, 0);
+    }
+    // Words q0 and q0 + 1, pieces q0 and q0 + 1.
+    __device__ void store(char *dst, int set, uint32_t, bool on, int q0) {
+        const MixCoef cf =
+            mix_coef(on ? bf16_bits_to_f32(sr[set]) : 0.0f, on ? bf16_bits_to_f32(br[set]) : 0.0f);
+#pragma unroll
+        for (int q = q0; q < q0 + 2; ++q) *(bf16x8 *)(dst + 16 * q) = dequant_word_mix(cr[set][q], cf, magic);
+    }
+};
+
+// GGUF Q5_K / Q4_K planes (GgufPlanes.swift:8-20, 62-74): the thread's 32-element group j of its
+// 256-element block is one 16-byte plane0 record (nibbles in chunk order), one 4-byte plane1
+// record (fifth bits; none for Q4_K) and the block's 16-byte meta record (fp16 d, dmin, packed
+// 6-bit scales and minimums). In chunk order (gguf_formats.h:17-21) word c of the plane0 record
+// holds elements 4c .. 4c + 3 and 16 + 4c .. 16 + 4c + 3: w & 0x0F0F0F0F has the codes of elements
+// (4c, 16+4c, 4c+1, 16+4c+1) in its bytes and (w >> 4) & 0x0F0F0F0F those of (4c+2, 16+4c+2, 4c+3,
+// 16+4c+3); the fifth bits reach bit 4 of those bytes by one multiply ((x & 0x33) * 0x880110 moves
+// bits 0, 4, 1, 5 of plane1 byte c to bits 4, 12, 20, 28). Words 0 and 1 so give elements 0..7
+// (bytes 0 and 2) and 16..23 (bytes 1 and 3), words 2 and 3 elements 8..15 and 24..31. The weight
+// is code * (d sc) - dmin mn in one fma (both products exact in fp32, GgufQuant.swift:191-212),
+// then RNE to bf16.
+template <bool FIFTH>
+struct Q5Stage {
+    static constexpr int kLoads = FIFTH ? 3 : 2;
+    rsrc_t p0_rsrc, p1_rsrc, m_rsrc;
+    uint32_t p0_src, p1_src, m_src;
+    int hh;
+    u32x4 p0[2], mr[2];
+    uint32_t p1[2];
+    __device__ Q5Stage(const PrefillArgs &args) {
+        p0_rsrc = make_rsrc(args.w[0], args.w_bytes[0]);
+        p1_rsrc = make_rsrc(FIFTH ? args.w[1] : args.w[0], FIFTH ? args.w_bytes[1] : 0u);
+        m_rsrc = make_rsrc(args.w[2], args.w_bytes[2]);
+    }
+    __device__ void begin(const PrefillArgs &args, uint32_t col, int hh_) {
+        hh = hh_;
+        const uint32_t g32 = 2u * (uint32_t)args.groups, blocks = (uint32_t)args.groups / 4u;
+        const uint32_t rec = ((col >> 7) * g32 + (uint32_t)hh) * 128u + (col & 127u);  // 32-group hh of group 0
+        p0_src = rec * 16u;
+        p1_src = rec * 4u;
+        m_src = ((col >> 7) * blocks * 128u + (col & 127u)) * 16u;
+    }
+    // 64-group g: 32-groups 2 g and 2 g + 1, block g / 4.
+    __device__ void load(uint32_t g, int set) {
+        p0[set] = buffer_load16_cp<2>(p0_rsrc, p0_src + g * (2u * 128u * 16u), 0);
+        if constexpr (FIFTH) p1[set] = buffer_load_u32(p1_rsrc, p1_src + g * (2u * 128u * 4u), 0);
+        else p1[set] = 0u;
+        mr[set] = buffer_load16(m_rsrc, m_src + (g >> 2) * (128u * 16u), 0);
+    }
+    // Words q0 and q0 + 1: pieces q0 / 2 (elements 8 (q0 / 2) .. + 7) and 2 + q0 / 2.
+    __device__ void store(char *dst, int set, uint32_t g, bool on, int q0) {
+        // Scale and minimum of 32-group j = (2 g + hh) mod 8 (GgufQuant.swift:196-203): packed byte
+        // k is meta byte 4 + k; for j < 4 the low six bits of bytes 4 + j and 8 + j, else the
+        // nibbles of byte 12 + (j - 4) joined with the top two bits of bytes 4 + (j - 4) and
+        // 8 + (j - 4). j >= 4 is uniform (g & 2); the byte within its word is 2 (g & 1) + hh.
+        const u32x4 m = mr[set];
+        const uint32_t sh = 8u * (2u * (g & 1u) + (uint32_t)hh);
+        uint32_t sc, mn;
+        if ((g & 2u) == 0u) {
+            sc = __builtin_amdgcn_ubfe(m[1], sh, 6);
+            mn = __builtin_amdgcn_ubfe(m[2], sh, 6);
+        } else {
+            sc = __builtin_amdgcn_ubfe(m[3], sh, 4) | (__builtin_amdgcn_ubfe(m[1], sh + 6, 2) << 4);
+            mn = __builtin_amdgcn_ubfe(m[3], sh + 4, 4) | (__builtin_amdgcn_ubfe(m[2], sh + 6, 2) << 4);
+        }
+        const float d = half_bits_to_f32(m[0]), dmin = half_bits_to_f32(m[0] >> 16);
+        const float scaled = on ? d * (float)sc : 0.0f, offset = on ? -(dmin * (float)mn) : 0.0f;
+        uint32_t lo[2], hi[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int c = q0 + e;
+            const uint32_t w = p0[set][c];
+            lo[e] = w & 0x0F0F0F0Fu;
+            hi[e] = (w >> 4) & 0x0F0F0F0Fu;
+            if constexpr (FIFTH) {
+                const uint32_t x = __builtin_amdgcn_ubfe(p1[set], 8 * c, 8);
+                lo[e] |= ((x & 0x33u) * 0x880110u) & 0x10101010u;
+                hi[e] |= (((x >> 2) & 0x33u) * 0x880110u) & 0x10101010u;
+            }
+        }
+        auto wt = [&](uint32_t codes, int j) { return __builtin_fmaf(cvt_byte(codes, j), scaled, offset); };
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {  // bytes b and b + 2 of each word: the lower or upper elements
+            u32x4 v;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                v[2 * e] = f32x2_to_bf16x2(wt(lo[e], b), wt(lo[e], b + 2));
+                v[2 * e + 1] = f32x2_to_bf16x2(wt(hi[e], b), wt(hi[e], b + 2));
+            }
+            *(u32x4 *)(dst + 16 * (2 * b + q0 / 2)) = v;
+        }
+    }
+};
+
 // The kernel's buffers (see the top of the file).
 constexpr int kSA = kPB * 128;                 // swizzled activations of a group
 constexpr int kSBuf = kSA + kPABuf;            // activations and bf16 weights of a group
 constexpr size_t kSLds = 2 * (size_t)kSBuf;
 constexpr int kSALoads = 4;                    // activation loads (into LDS) of a wave and group
-constexpr int kSCodeLoads = 3;                 // code, scale and bias loads of a thread and group
 static_assert(8 * kPEpi <= (int)kSLds, "eight waves' epilogue staging fits the buffers");
 
+template <class W>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
-q4_prefill_kernel(PrefillArgs args) {
+prefill_kernel(PrefillArgs args) {
+    constexpr int kSCodeLoads = W::kLoads;
     constexpr int FM = 4, kAPer = 4;
     extern __shared__ __align__(16) char lds[];
     const int tid = threadIdx.x;
@@ -130,15 +253,12 @@ q4_prefill_kernel(PrefillArgs args) {
     const int wm = wave / 4, wn = wave % 4;
     const int r = lane & 31, h = lane >> 5;
     const int G = (int)args.groups;
-    const uint32_t G32 = (uint32_t)G;
     const rsrc_t a_rsrc = make_rsrc(args.a, args.a_bytes);
-    const rsrc_t q_rsrc = make_rsrc(args.packed, args.code_bytes);
-    const rsrc_t s_rsrc = make_rsrc(args.scales, args.sidecar_bytes);
-    const rsrc_t b_rsrc = make_rsrc(args.biases, args.sidecar_bytes);
-    uint32_t magic;
-    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic));
+    W wst(args);
     {
-        float agpr_use;  // accumulators in AGPRs (see q4_prefill_kernel)
+        // An AGPR operand makes the compiler select the AGPR form of the MFMAs: the accumulators
+        // then live in AGPRs, beside a full set of 128 VGPRs.
+        float agpr_use;
         asm volatile("v_accvgpr_write_b32 %0, 0" : "=a"(agpr_use));
         (void)agpr_use;
     }
@@ -162,16 +282,12 @@ q4_prefill_kernel(PrefillArgs args) {
             const int64_t m = m0 + row;
             a_src[p] = (uint32_t)(((m < args.rows ? m : args.rows - 1) * args.lda + piece * 8) * 2);
         }
-        // The codes of column tid / 2, half tid % 2 (words 4 (tid % 2) .. + 3), and that column's
-        // scale and bias (columns past the last clamped).
+        // The weights of column tid / 2, k = 32 (tid % 2) .. + 31 of each group (columns past the
+        // last clamped).
         const int hh = tid & 1, sc = tid >> 1;
-        uint32_t c_src, s_src;
         {
             const int64_t nc = n0 + sc;
-            const uint32_t col = (uint32_t)(nc < args.n ? nc : args.n - 1);
-            const uint32_t rec = (col >> 7) * G32 * 128u + (col & 127u);
-            c_src = rec * 32u + 16u * hh;
-            s_src = rec * 2u;
+            wst.begin(args, (uint32_t)(nc < args.n ? nc : args.n - 1), hh);
         }
         const uint32_t b_dst = (uint32_t)(kSA + sc * kPRow + 64 * hh);
         auto clampg = [&](int t) {
@@ -184,23 +300,12 @@ q4_prefill_kernel(PrefillArgs args) {
             for (int p = 0; p < kAPer; ++p)
                 buffer_load_lds16(a_rsrc, lds + buf * kSBuf + 8192 * p + 1024 * wave, a_src[p] + g * 128u);
         };
-        // Codes and sidecars in two register sets: group t's in set t mod 2.
-        u32x4 cr[2];
-        uint32_t sr[2], br[2];
-        auto load_codes = [&](int t, int set) {
-            const uint32_t g = clampg(t);
-            cr[set] = buffer_load16_cp<2>(q_rsrc, c_src + g * (128u * 32u), 0);
-            sr[set] = buffer_load_u16(s_rsrc, s_src + g * 256u, 0);
-            br[set] = buffer_load_u16(b_rsrc, s_src + g * 256u, 0);
-        };
-        // Group t's weights (words q0, q0 + 1 of this thread's piece) into buffer `buf`; zero
-        // coefficients past the job (the step count is padded to even).
-        auto store_b = [&](int buf, int set, bool on, int q0) {
-            const MixCoef cf =
-                mix_coef(on ? bf16_bits_to_f32(sr[set]) : 0.0f, on ? bf16_bits_to_f32(br[set]) : 0.0f);
-            char *b = lds + buf * kSBuf + b_dst;
-#pragma unroll
-            for (int q = q0; q < q0 + 2; ++q) *(bf16x8 *)(b + 16 * q) = dequant_word_mix(cr[set][q], cf, magic);
+        // Group t's weights in register set t mod 2.
+        auto load_codes = [&](int t, int set) { wst.load(clampg(t), set); };
+        // Group t's weights (half q0 / 2 of this thread's part) into buffer `buf`; zero weights
+        // past the job (the step count is padded to even).
+        auto store_b = [&](int buf, int set, int t, int q0) {
+            wst.store(lds + buf * kSBuf + b_dst, set, clampg(t), t < T, q0);
         };
         // Operands of MFMA step i (k = 32 h + 8 i .. + 7 of the group, piece 4 h + i of a row).
         auto read_ops = [&](bf16x8 *af, bf16x8 *bw, int buf, int i) {
@@ -223,8 +328,8 @@ q4_prefill_kernel(PrefillArgs args) {
         // Prologue: group 0 into buffer 0, group 1's codes in flight.
         load_a(0, 0);
         load_codes(0, 0);
-        store_b(0, 0, T > 0, 0);
-        store_b(0, 0, T > 0, 2);
+        store_b(0, 0, 0, 0);
+        store_b(0, 0, 0, 2);
         __builtin_amdgcn_sched_barrier(0);
         load_codes(1, 1);
         __builtin_amdgcn_sched_barrier(0);
@@ -251,7 +356,7 @@ q4_prefill_kernel(PrefillArgs args) {
 #pragma unroll
                     for (int f = 0; f < FM; ++f)
                         acc[f][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[f], bw[j], acc[f][j], 0, 0, 0);
-                if (i == 1 || i == 2) store_b(d ^ 1, d ^ 1, t + 1 < T, 2 * (i - 1));
+                if (i == 1 || i == 2) store_b(d ^ 1, d ^ 1, t + 1, 2 * (i - 1));
             }
             // Group t + 1's activations have landed (only group t + 2's code loads, issued after
             // them, may be outstanding), and every wave is done with buffer t mod 2.
@@ -299,7 +404,7 @@ q4_prefill_kernel(PrefillArgs args) {
 // Block (rt, y) covers elements [1024 y, 1024 y + 1024) of remainder tile rt, four a thread; its
 // first thread lists the tile's contributing workgroups once (see q4_mma_finish).
 __global__ void __launch_bounds__(256)
-q4_prefill_finish(const float *__restrict__ partial, int dp_tiles, int64_t sk_units, int P, int64_t groups,
+prefill_finish(const float *__restrict__ partial, int dp_tiles, int64_t sk_units, int P, int64_t groups,
                   int mblocks, int64_t rows, int64_t n, void *out, int64_t ldc, int out_dtype, const void *residual) {
     __shared__ int wg[kPFinishMax];
     __shared__ int slot_of[kPFinishMax];
@@ -399,15 +504,12 @@ size_t prefill_workspace_bytes(int64_t rows, int64_t columns, int64_t groups) {
     return p.sk_units > 0 ? prefill_sk_bytes(p.grid) : 0;
 }
 
-hipError_t launch_q4_prefill(const PrefillPlan &plan, const splosh_q4_weight &w, const uint16_t *a, int64_t lda,
-                             void *out, int64_t ldc, int out_dtype, const void *residual, int64_t rows,
-                             void *workspace, hipStream_t stream) {
-    PrefillArgs args = {};
-    args.packed = w.packed;
-    args.scales = w.scales;
-    args.biases = w.biases;
-    args.n = w.rows;
-    args.groups = w.inner / kGroup;
+template <class W>
+static hipError_t launch_prefill(const PrefillPlan &plan, PrefillArgs &args, int64_t n, int64_t inner,
+                                 const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype,
+                                 const void *residual, int64_t rows, void *workspace, hipStream_t stream) {
+    args.n = n;
+    args.groups = inner / kGroup;
     args.a = a;
     args.lda = lda;
     args.out = out;
@@ -419,23 +521,57 @@ hipError_t launch_q4_prefill(const PrefillPlan &plan, const splosh_q4_weight &w,
     args.partial = plan.sk_units > 0 ? (float *)workspace : nullptr;
     args.dp_tiles = plan.dp_tiles;
     args.sk_units = plan.sk_units;
-    args.code_bytes = (uint32_t)(w.rows * args.groups * 32);
-    args.sidecar_bytes = (uint32_t)(w.rows * args.groups * 2);
-    args.a_bytes = (uint32_t)(((rows - 1) * lda + w.inner) * 2);
+    args.a_bytes = (uint32_t)(((rows - 1) * lda + inner) * 2);
     static bool once = [] {
-        (void)hipFuncSetAttribute((const void *)q4_prefill_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+        (void)hipFuncSetAttribute((const void *)prefill_kernel<W>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                   (int)kSLds);
         return true;
     }();
     (void)once;
-    hipLaunchKernelGGL(q4_prefill_kernel, dim3((unsigned)plan.grid), dim3(512), kSLds, stream, args);
+    hipLaunchKernelGGL(prefill_kernel<W>, dim3((unsigned)plan.grid), dim3(512), kSLds, stream, args);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess || plan.sk_units == 0) return err;
     const int remainder = plan.tiles - plan.dp_tiles;
-    hipLaunchKernelGGL(q4_prefill_finish, dim3((unsigned)remainder, kPB * kPB / 1024), dim3(256), 0, stream,
+    hipLaunchKernelGGL(prefill_finish, dim3((unsigned)remainder, kPB * kPB / 1024), dim3(256), 0, stream,
                        (const float *)workspace, plan.dp_tiles, plan.sk_units, plan.grid, args.groups, plan.mblocks,
-                       rows, w.rows, out, ldc, out_dtype, residual);
+                       rows, n, out, ldc, out_dtype, residual);
     return hipGetLastError();
+}
+
+hipError_t launch_q4_prefill(const PrefillPlan &plan, const splosh_q4_weight &w, const uint16_t *a, int64_t lda,
+                             void *out, int64_t ldc, int out_dtype, const void *residual, int64_t rows,
+                             void *workspace, hipStream_t stream) {
+    PrefillArgs args = {};
+    const int64_t groups = w.inner / kGroup;
+    args.w[0] = w.packed;
+    args.w[1] = w.scales;
+    args.w[2] = w.biases;
+    args.w_bytes[0] = (uint32_t)(w.rows * groups * 32);
+    args.w_bytes[1] = args.w_bytes[2] = (uint32_t)(w.rows * groups * 2);
+    return launch_prefill<Q4Stage>(plan, args, w.rows, w.inner, a, lda, out, ldc, out_dtype, residual, rows,
+                                   workspace, stream);
+}
+
+bool q5k_prefill_fits(int64_t rows, int64_t columns, int64_t inner, int64_t lda, int64_t ldc) {
+    const int64_t limit = ((int64_t)1 << 32) - 256;
+    return inner % 256 == 0 && prefill_fits(rows, columns, inner, lda, ldc) && columns * (inner / 32) * 16 < limit;
+}
+
+hipError_t launch_q5k_prefill(const PrefillPlan &plan, const splosh_q5k_weight &w, bool fifth, const uint16_t *a,
+                              int64_t lda, void *out, int64_t ldc, int out_dtype, const void *residual, int64_t rows,
+                              void *workspace, hipStream_t stream) {
+    PrefillArgs args = {};
+    args.w[0] = w.plane0;
+    args.w[1] = fifth ? (const void *)w.plane1 : nullptr;
+    args.w[2] = w.meta;
+    args.w_bytes[0] = (uint32_t)(w.rows * (w.inner / 32) * 16);
+    args.w_bytes[1] = fifth ? (uint32_t)(w.rows * (w.inner / 32) * 4) : 0u;
+    args.w_bytes[2] = (uint32_t)(w.rows * (w.inner / 256) * 16);
+    if (fifth)
+        return launch_prefill<Q5Stage<true>>(plan, args, w.rows, w.inner, a, lda, out, ldc, out_dtype, residual,
+                                             rows, workspace, stream);
+    return launch_prefill<Q5Stage<false>>(plan, args, w.rows, w.inner, a, lda, out, ldc, out_dtype, residual, rows,
+                                          workspace, stream);
 }
 
 }  // namespace splosh

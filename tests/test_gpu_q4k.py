@@ -46,7 +46,7 @@ def test_repack_unpack_and_dequant_bit_exact(rt):
     assert np.array_equal(got[3, 256:512].view(np.uint32), values.view(np.uint32))
 
 
-@pytest.mark.parametrize("rows", [1, 2, 16, 64, 100, 200])
+@pytest.mark.parametrize("rows", [1, 2, 16, 64, 100, 200, 300])
 def test_gemm_paths(rt, rows):
     n, k = 384, 2048
     native, _ = _native(n, k, seed=10 + rows)
@@ -66,7 +66,7 @@ def test_gemm_paths(rt, rows):
         check_close(out.cpu().numpy(), ref + base, bf16_out=False, tight=True, absref=absref, label="q4k residual")
 
 
-@pytest.mark.parametrize("kernel", ["STREAM", "SCALAR", "DEQUANT", "TILE"])
+@pytest.mark.parametrize("kernel", ["STREAM", "SCALAR", "DEQUANT", "TILE", "PREFILL"])
 def test_gemm_explicit_kernels(rt, kernel):
     n, k, rows = 256, 1280, 5
     native, _ = _native(n, k, seed=30)

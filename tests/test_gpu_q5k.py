@@ -135,7 +135,7 @@ def test_dequant_kernel(rt, rows, split):
 
 @pytest.mark.parametrize("rows", [1, 65, 130, 300])
 def test_tile_kernel(rt, rows):
-    """The LDS-tiled kernel (AUTO above 64 rows): both tile shapes, ragged row and column blocks,
+    """The LDS-tiled kernel (explicit for planes; AUTO for the native formats): both tile shapes, ragged row and column blocks,
     the residual."""
     n, k = 384, 1280
     native = oracle.q45k_random_native(n, k, seed=600 + rows)
@@ -155,14 +155,38 @@ def test_tile_kernel(rt, rows):
                 label=f"q5k tile residual rows={rows}")
 
 
+@pytest.mark.parametrize("rows,n,k", [(65, 384, 1280), (300, 256, 512), (513, 128, 256)])
+@pytest.mark.parametrize("split", [True, False])
+def test_prefill_kernel(rt, rows, n, k, split):
+    """The 256 x 256 prefill kernel over planes (AUTO above 64 rows): whole and partial tiles, the
+    last round split over all workgroups (stream-K) and not, K of one block, both output types,
+    the residual."""
+    native = oracle.q45k_random_native(n, k, seed=900 + rows)
+    w = rt.q5k_repack(dev_u8(native), n, k)
+    dense = oracle.q45k_decode(native).reshape(n, k)
+    a_bits = oracle.bf16_normal((rows, k), seed=950 + rows)
+    ref = oracle.gemm_a_bf16_w_f32(a_bits, dense)
+    absref = abs_gemm(a_bits, dense)
+    ws = None if split else torch.empty(0, dtype=torch.uint8, device="cuda")
+    for out_dtype in (torch.bfloat16, torch.float32):
+        got = rt.gemm(w, bf16_tensor(a_bits), out_dtype=out_dtype, kernel=rt.PREFILL, workspace=ws)
+        check_close(to_f32(got), ref, bf16_out=out_dtype == torch.bfloat16, tight=True, absref=absref,
+                    label=f"q5k prefill {rows}x{n}x{k} split={split} {out_dtype}")
+    base = torch.from_numpy(oracle.bf16_normal((rows, n), seed=8).astype(np.float32)).cuda()
+    out = base.clone()
+    rt.gemm(w, bf16_tensor(a_bits), out=out, residual=out, kernel=rt.PREFILL, workspace=ws)
+    check_close(out.cpu().numpy(), ref + base.cpu().numpy(), bf16_out=False, tight=True, absref=absref,
+                label=f"q5k prefill residual {rows}x{n}x{k} split={split}")
+
+
 def test_tile_kernel_large_grid(rt):
-    """Enough 128 x 128 blocks for the large tile shape (AUTO at 512 rows), sampled rows."""
+    """Enough 128 x 128 blocks for the large tile shape (512 rows), sampled rows."""
     n, k, rows = 2048, 512, 512
     native = oracle.q45k_random_native(n, k, seed=801)
     w = rt.q5k_repack(dev_u8(native), n, k)
     dense = oracle.q45k_decode(native).reshape(n, k)
     a_bits = oracle.bf16_normal((rows, k), seed=802)
-    got = rt.gemm(w, bf16_tensor(a_bits), out_dtype=torch.float32).cpu().numpy()
+    got = rt.gemm(w, bf16_tensor(a_bits), out_dtype=torch.float32, kernel=rt.TILE).cpu().numpy()
     pick = np.sort(np.random.default_rng(803).choice(rows, 48, replace=False))
     check_close(got[pick], oracle.gemm_a_bf16_w_f32(a_bits[pick], dense), bf16_out=False, tight=True,
                 absref=abs_gemm(a_bits[pick], dense), label="q5k tile large")

@@ -183,16 +183,16 @@ def test_mma_stage_waits_cover_their_loads(tmp_path):
 @pytest.mark.skipif(not Path(HIPCC).exists(), reason="needs hipcc")
 def test_prefill_stage_waits_cover_their_loads(tmp_path):
     """The prefill kernel's activations arrive through loads into LDS, four a wave and group; the
-    wait before each step's barrier must leave none of them in flight (only the code loads issued
-    after them)."""
+    wait before each step's barrier must leave none of them in flight (only the weight loads issued
+    after them), for every weight format it stages."""
     out = tmp_path / "prefill.s"
     cmd = [HIPCC, "-O3", "-std=c++17", "--offload-arch=gfx950", "-Xclang", "-target-feature", "-Xclang",
            "-packed-fp32-ops", f"-I{ROOT / 'include'}", "--cuda-device-only", "-S",
            str(ROOT / "splosh_amd" / "csrc" / "prefill.hip"), "-o", str(out)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     assert res.returncode == 0, res.stderr[-2000:]
-    kernels = list(_kernels(out.read_text(), r"_ZN6splosh17q4_prefill_kernel\S*"))
-    assert len(kernels) == 1
+    kernels = list(_kernels(out.read_text(), r"_ZN6splosh14prefill_kernel\S*"))
+    assert len(kernels) == 3  # q4, Q5_K and Q4_K staging
     for name, code in kernels:
         assert any(_is_lds(ins) for ins in code), name
         # The prologue's barrier and the two unrolled steps'.
