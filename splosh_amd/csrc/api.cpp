@@ -597,6 +597,8 @@ static int check_gguf_native(int type, const uint8_t *native, int64_t rows, int6
     return ok();
 }
 
+constexpr int64_t kGgufPrefillRows = 256;  // measured: the tile kernel is as fast or faster up to 128 rows
+
 int splosh_gguf_gemm(int gguf_type, const uint8_t *native, int64_t rows, int64_t inner, const uint16_t *a,
                      int64_t lda, void *out, int64_t ldc, int out_dtype, const void *residual, int64_t m,
                      void *workspace, size_t workspace_bytes, hipStream_t stream) {
@@ -605,8 +607,20 @@ int splosh_gguf_gemm(int gguf_type, const uint8_t *native, int64_t rows, int64_t
     if ((st = check_io(a, lda, out, ldc, out_dtype, m, rows, inner))) return st;
     if (lda % 8 != 0 || !aligned(a, 16))
         return fail(SPLOSH_ERR_UNSUPPORTED, "GGUF native kernel needs lda % 8 == 0 and 16-byte aligned activations");
-    // Above eight rows the tiled kernel (each weight group decoded once per 64 to 256 rows) is the
-    // faster; up to eight, one or two passes of the streaming kernel.
+    // From kGgufPrefillRows rows the 256 x 256 prefill kernel (each weight group decoded once per
+    // 256 rows); above eight the tiled kernel (once per 64 or 128 rows); up to eight, one or two
+    // passes of the streaming kernel. (A development override of the threshold, read once.)
+    static const int64_t prefill_rows = [] {
+        const char *e = getenv("SPLOSH_GGUF_PREFILL_ROWS");
+        return e ? (int64_t)atoll(e) : kGgufPrefillRows;
+    }();
+    if (m >= prefill_rows && aligned(out, 16) && (!residual || aligned(residual, 16)) &&
+        splosh::gguf_prefill_fits(gguf_type, m, rows, inner, lda, ldc)) {
+        const splosh::PrefillPlan plan = splosh::plan_prefill(m, rows, inner / kGroupSize, workspace ? workspace_bytes : 0);
+        return hip_status(splosh::launch_gguf_prefill(plan, gguf_type, native, rows, inner, a, lda, out, ldc, out_dtype,
+                                                      residual, m, workspace, stream),
+                          "gguf prefill launch");
+    }
     if (m > 8 && splosh::gguf_tile_fits(m, rows, inner, lda))
         return hip_status(splosh::launch_gguf_tile(gguf_type, native, nullptr, nullptr, rows, inner, a, lda, out, ldc,
                                                    out_dtype, residual, m, workspace, workspace_bytes, stream),

@@ -155,6 +155,12 @@ bool q5k_prefill_fits(int64_t rows, int64_t columns, int64_t inner, int64_t lda,
 hipError_t launch_q5k_prefill(const PrefillPlan &plan, const splosh_q5k_weight &w, bool fifth, const uint16_t *a,
                               int64_t lda, void *out, int64_t ldc, int out_dtype, const void *residual, int64_t rows,
                               void *workspace, hipStream_t stream);
+// And over the GGUF native blocks (ggml type ids 8, 11, 14, 20, 21, 23): K a multiple of 64 and of
+// the block.
+bool gguf_prefill_fits(int type, int64_t rows, int64_t columns, int64_t inner, int64_t lda, int64_t ldc);
+hipError_t launch_gguf_prefill(const PrefillPlan &plan, int type, const uint8_t *native, int64_t rows_w,
+                               int64_t inner, const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype,
+                               const void *residual, int64_t rows, void *workspace, hipStream_t stream);
 
 // The decode kernel for one activation row of Q5_K planes (q5k_decode.hip).
 bool q5k_decode_fits(int64_t rows, int64_t columns, int64_t inner);

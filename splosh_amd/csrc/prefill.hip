@@ -28,6 +28,7 @@
 // Numerics as mma.hip: fp32 dequantized weight rounded to bf16, exact products, fp32 sums.
 #include "common.hpp"
 #include "launch.hpp"
+#include "gguf_decode.hpp"
 #include "mix.hpp"
 
 #include <cstdlib>
@@ -230,6 +231,40 @@ struct Q5Stage {
                 v[2 * e + 1] = f32x2_to_bf16x2(wt(hi[e], b), wt(hi[e], b + 2));
             }
             *(u32x4 *)(dst + 16 * (2 * b + q0 / 2)) = v;
+        }
+    }
+};
+
+// GGUF native blocks (Q8_0, Q3_K, Q6_K, IQ4_NL, IQ3_S, IQ4_XS; rows back to back): the thread's
+// 32-element group 2 g + t % 2 of its column, fetched by gguf_fetch and decoded by gguf_decode in
+// the reference's fp32 order (GgufQuant.swift), then rounded to bf16. The number of loads a group
+// takes differs by format, so kLoads = 0: the step's wait takes every load.
+template <int TYPE>
+struct GgufStage {
+    static constexpr int kLoads = 0;
+    rsrc_t r;
+    uint32_t row;
+    int hh;
+    GgufRaw<TYPE> raw[2];
+    __device__ GgufStage(const PrefillArgs &args) { r = make_rsrc(args.w[0], args.w_bytes[0]); }
+    __device__ void begin(const PrefillArgs &args, uint32_t col, int hh_) {
+        hh = hh_;
+        const uint32_t row_bytes = (uint32_t)(args.groups * 64 / GgufGeom<TYPE>::kElems * GgufGeom<TYPE>::kBytes);
+        row = col * row_bytes;
+    }
+    __device__ void load(uint32_t g, int set) { raw[set] = gguf_fetch<TYPE>(r, row, (int)(2u * g) + hh); }
+    // The whole part at q0 = 0 (the decoders produce all 32 values at once), nothing at q0 = 2.
+    __device__ void store(char *dst, int set, uint32_t, bool on, int q0) {
+        if (q0 != 0) return;
+        float v[32];
+        gguf_decode<TYPE>(raw[set], v);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            u32x4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                o[e] = on ? f32x2_to_bf16x2(v[8 * q + 2 * e], v[8 * q + 2 * e + 1]) : 0u;
+            *(u32x4 *)(dst + 16 * q) = o;
         }
     }
 };
@@ -572,6 +607,34 @@ hipError_t launch_q5k_prefill(const PrefillPlan &plan, const splosh_q5k_weight &
                                              rows, workspace, stream);
     return launch_prefill<Q5Stage<false>>(plan, args, w.rows, w.inner, a, lda, out, ldc, out_dtype, residual, rows,
                                           workspace, stream);
+}
+
+bool gguf_prefill_fits(int type, int64_t rows, int64_t columns, int64_t inner, int64_t lda, int64_t ldc) {
+    int elems = 0, bytes = 0;
+    if (!gguf_native_block(type, &elems, &bytes)) return false;
+    return inner % 64 == 0 && inner % elems == 0 && prefill_fits(rows, columns, inner, lda, ldc) &&
+           columns * (inner / elems) * bytes < ((int64_t)1 << 32) - 256;
+}
+
+hipError_t launch_gguf_prefill(const PrefillPlan &plan, int type, const uint8_t *native, int64_t rows_w,
+                               int64_t inner, const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype,
+                               const void *residual, int64_t rows, void *workspace, hipStream_t stream) {
+    int elems = 0, bytes = 0;
+    if (!gguf_native_block(type, &elems, &bytes)) return hipErrorInvalidValue;
+    PrefillArgs args = {};
+    args.w[0] = native;
+    args.w_bytes[0] = (uint32_t)(rows_w * (inner / elems) * bytes);
+#define SPLOSH_GGUF_PREFILL(T) \
+    launch_prefill<GgufStage<T>>(plan, args, rows_w, inner, a, lda, out, ldc, out_dtype, residual, rows, workspace, stream)
+    switch (type) {
+        case 8: return SPLOSH_GGUF_PREFILL(8);
+        case 11: return SPLOSH_GGUF_PREFILL(11);
+        case 14: return SPLOSH_GGUF_PREFILL(14);
+        case 20: return SPLOSH_GGUF_PREFILL(20);
+        case 21: return SPLOSH_GGUF_PREFILL(21);
+        default: return SPLOSH_GGUF_PREFILL(23);
+    }
+#undef SPLOSH_GGUF_PREFILL
 }
 
 }  // namespace splosh

@@ -79,6 +79,31 @@ def test_config0_size_sampled(rt, name):
 
 
 @pytest.mark.parametrize("name", list(TYPES))
+@pytest.mark.parametrize("rows", [256, 513])
+@pytest.mark.parametrize("split", [True, False])
+def test_prefill_kernel(rt, name, rows, split):
+    """The 256 x 256 prefill kernel over native blocks (AUTO from 256 rows for N % 128 == 0):
+    partial tiles, the last round split over all workgroups (stream-K) and not, both output
+    types, the residual."""
+    t = TYPES[name]
+    n, k = 384, 1536
+    w, dense = _weight(rt, t, n, k, seed=rows + 7 * t)
+    a_bits = oracle.bf16_normal((rows, k), seed=rows + 1)
+    ref = oracle.gemm_a_bf16_w_f32(a_bits, dense)
+    absref = abs_gemm(a_bits, dense)
+    ws = None if split else torch.empty(0, dtype=torch.uint8, device="cuda")
+    a = bf16_tensor(a_bits)
+    for out_dtype in (torch.bfloat16, torch.float32):
+        got = rt.gemm(w, a, out_dtype=out_dtype, workspace=ws)
+        check_close(to_f32(got), ref, bf16_out=out_dtype == torch.bfloat16, tight=True, absref=absref,
+                    label=f"{name} prefill rows={rows} split={split} {out_dtype}")
+    res = torch.from_numpy(oracle.bf16_normal((rows, n), seed=6).astype(np.float32)).cuda()
+    got = rt.gemm(w, a, out=res.clone(), out_dtype=torch.float32, residual=res, workspace=ws)
+    check_close(got.cpu().numpy(), ref + res.cpu().numpy(), bf16_out=False, tight=True, absref=absref,
+                label=f"{name} prefill residual rows={rows} split={split}")
+
+
+@pytest.mark.parametrize("name", list(TYPES))
 def test_tiled_large_grid(rt, name):
     """Enough 128 x 128 blocks for the large tile shape, sampled activation rows."""
     t = TYPES[name]
