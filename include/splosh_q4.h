@@ -74,7 +74,8 @@ typedef enum splosh_kernel {
                                    registers; uses the workspace for split bands when given one */
     SPLOSH_KERNEL_TILE = 3,     /* any rows: LDS-tiled dequant-to-bf16 MFMA GEMM (prefill) */
     SPLOSH_KERNEL_SCALAR = 4,   /* one thread per output (gemm_q4.metal semantics) */
-    SPLOSH_KERNEL_PREFILL = 5   /* one TILED128 q4 weight (not mlp_in) or Q5_K / Q4_K planes:
+    SPLOSH_KERNEL_PREFILL = 5   /* TILED128 q4 weights (mlp_in: 128 columns of each a tile,
+                                   silu(g) * u in the epilogue) or Q5_K / Q4_K planes:
                                    256 x 256 output tiles, two waves per SIMD, every weight
                                    dequantized once a tile into LDS; uses the workspace to split
                                    the last round of tiles over all CUs */
@@ -186,7 +187,8 @@ int splosh_q4_gemm_noalloc(const splosh_q4_weight *w, const uint16_t *a, int64_t
 
 /* Engine.mlpIn(gate:up:input:output:scratch:rows:) (Runtime/Engine.swift:1911-1966) with the
  * fused lane form sp_mlp_in_tiled_* (Shaders/engine.metal:1987-2055): out = silu(gate(a)) * up(a),
- * both weights read in one pass over a. */
+ * both weights read in one pass over a. AUTO as splosh_q4_gemm: above 64 rows, tiled weights take
+ * the prefill kernel with both weights in each tile. */
 int splosh_q4_mlp_in(const splosh_q4_weight *gate, const splosh_q4_weight *up, const uint16_t *a,
                      int64_t lda, void *out, int64_t ldc, int out_dtype, int64_t rows, int kernel,
                      void *workspace, size_t workspace_bytes, hipStream_t stream);

@@ -107,6 +107,8 @@ int q4_gemm_impl(const splosh_q4_weight *w, const splosh_q4_weight *up, const ui
     const bool prefill_ok = wide16 && !up && w->order == SPLOSH_Q4_TILED128 && aligned(out, 16) &&
                             (!residual || aligned(residual, 16)) &&
                             splosh::prefill_fits(rows, w->rows, w->inner, lda, ldc);
+    const bool prefill_mlp_ok = wide16 && up && w->order == SPLOSH_Q4_TILED128 && up->order == SPLOSH_Q4_TILED128 &&
+                                aligned(out, 16) && splosh::prefill_fits(rows, w->rows, w->inner, lda, ldc);
     const bool decode_ok = wide16 && splosh::decode_fits(rows, w->rows, w->inner, w->order);
     int choice = kernel;
     if (choice == SPLOSH_KERNEL_AUTO) {
@@ -115,12 +117,19 @@ int q4_gemm_impl(const splosh_q4_weight *w, const splosh_q4_weight *up, const ui
         else if (wide16 && splosh::lanes_fit(rows, w->rows, w->inner, w->row_stride_words, up != nullptr))
             choice = SPLOSH_KERNEL_STREAM;
         else if (mma_ok) choice = SPLOSH_KERNEL_DEQUANT;
-        else if (prefill_ok) choice = SPLOSH_KERNEL_PREFILL;
+        else if (prefill_ok || prefill_mlp_ok) choice = SPLOSH_KERNEL_PREFILL;
         else if (tile_ok) choice = SPLOSH_KERNEL_TILE;
         else choice = SPLOSH_KERNEL_STREAM;
     }
     switch (choice) {
         case SPLOSH_KERNEL_PREFILL: {
+            if (prefill_mlp_ok) {
+                const splosh::PrefillPlan plan =
+                    splosh::plan_prefill(rows, 2 * w->rows, w->inner / kGroupSize, workspace ? workspace_bytes : 0);
+                return hip_status(splosh::launch_q4_prefill_mlp(plan, *w, *up, a, lda, out, ldc, out_dtype, rows,
+                                                                workspace, stream),
+                                  "q4 prefill gate+up launch");
+            }
             if (!prefill_ok)
                 return fail(SPLOSH_ERR_UNSUPPORTED,
                             "prefill kernel needs one TILED128 weight, lda % 8 == 0, ldc % 4 == 0 and 16-byte "
@@ -354,7 +363,8 @@ size_t splosh_workspace_bytes(int64_t rows, int64_t columns, int64_t inner) {
     const int64_t groups = inner / kGroupSize;
     const size_t tile = splosh::tile_workspace_bytes(rows, columns, groups, true);
     const size_t mma = rows <= 64 ? splosh::mma_workspace_bytes(rows, columns, groups, true) : 0;
-    const size_t prefill = rows > 64 && columns % 128 == 0 ? splosh::prefill_workspace_bytes(rows, columns, groups) : 0;
+    // (2 columns: the fused gate+up plans its tiles over both weights' columns.)
+    const size_t prefill = rows > 64 && columns % 128 == 0 ? splosh::prefill_workspace_bytes(rows, 2 * columns, groups) : 0;
     const size_t gguf = inner % 64 == 0 ? splosh::gguf_tile_workspace_bytes(rows, columns, inner) : 0;
     size_t need = tile > mma ? tile : mma;
     need = need > prefill ? need : prefill;

@@ -150,6 +150,11 @@ size_t prefill_workspace_bytes(int64_t rows, int64_t columns, int64_t groups);
 hipError_t launch_q4_prefill(const PrefillPlan &plan, const splosh_q4_weight &w, const uint16_t *a, int64_t lda,
                              void *out, int64_t ldc, int out_dtype, const void *residual, int64_t rows,
                              void *workspace, hipStream_t stream);
+// Fused gate+up (silu(g) * u) over two TILED128 weights of one geometry: tiles of 128 columns of
+// each; plan with plan_prefill(rows, 2 * columns, groups, ...).
+hipError_t launch_q4_prefill_mlp(const PrefillPlan &plan, const splosh_q4_weight &gate, const splosh_q4_weight &up,
+                                 const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype, int64_t rows,
+                                 void *workspace, hipStream_t stream);
 // The same kernel over Q5_K (fifth) or Q4_K planes: K a multiple of 256.
 bool q5k_prefill_fits(int64_t rows, int64_t columns, int64_t inner, int64_t lda, int64_t ldc);
 hipError_t launch_q5k_prefill(const PrefillPlan &plan, const splosh_q5k_weight &w, bool fifth, const uint16_t *a,

@@ -38,6 +38,7 @@ namespace splosh {
 struct PrefillArgs {
     // q4: codes, scales, biases; Q5_K / Q4_K: plane0, plane1 (none for Q4_K), meta.
     const void *w[3];
+    const void *u[3];   // fused gate+up: the up weight (same geometry as w)
     uint32_t w_bytes[3];
     int64_t n;          // weight rows = output columns
     int64_t groups;     // 64-element groups of K
@@ -69,7 +70,7 @@ constexpr int kPFinishMax = 1024;              // contributors prefill_finish ca
 // workgroup's partial tile `slot`.
 template <int FM>
 __device__ __forceinline__ void prefill_store_tile(const PrefillArgs &args, const f32x16 (&acc)[FM][2], char *epi,
-                                                   int64_t m0, int64_t n0, int tc0, int tr0, int lane, int slot) {
+                                                   int64_t m0, int64_t ncol, int tc0, int tr0, int lane, int slot) {
     const int r = lane & 31, h = lane >> 5;
 #pragma unroll
     for (int f = 0; f < FM; ++f) {
@@ -85,7 +86,7 @@ __device__ __forceinline__ void prefill_store_tile(const PrefillArgs &args, cons
         for (int p = 0; p < 8; ++p) {
             const int idx = p * 64 + lane, row = idx >> 4, c4 = (idx & 15) * 4;
             const f32x4 v = *(const f32x4 *)(epi + (row * kPEpiRow + c4) * 4);
-            const int64_t m = m0 + tr + row, n = n0 + tc0 + c4;
+            const int64_t m = m0 + tr + row, n = ncol + c4;
             if (m >= args.rows || n >= args.n) continue;
             if (slot >= 0) {
                 float *dst = args.partial + ((int64_t)(blockIdx.x * 2 + slot) * kPB + tr + row) * kPB + tc0 + c4;
@@ -113,6 +114,51 @@ __device__ __forceinline__ void prefill_store_tile(const PrefillArgs &args, cons
     }
 }
 
+// The fused gate+up epilogue of a whole tile: the waves with wn = 0, 1 hold the gate's columns
+// 64 wn .. + 63 of the tile, the waves with wn = 2, 3 the up weight's same columns. One 32-row
+// block at a time every wave parks its block in its LDS area; then the gate waves read their own
+// and their partner's (wave + 2) and write silu(g) * u. Every wave passes the same barriers.
+template <int FM>
+__device__ __forceinline__ void prefill_store_mlp(const PrefillArgs &args, const f32x16 (&acc)[FM][2], char *lds,
+                                                  int wave, int64_t m0, int64_t ncol, int tr0, int lane) {
+    const int r = lane & 31, h = lane >> 5;
+    char *epi = lds + wave * kPEpi;
+    const char *partner = lds + (wave + 2) * kPEpi;
+    const bool gate = (wave & 3) < 2;
+#pragma unroll
+    for (int f = 0; f < FM; ++f) {
+        const int tr = tr0 + 32 * f;
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int row = 8 * (e >> 2) + 4 * h + (e & 3);
+                *(float *)(epi + (row * kPEpiRow + 32 * j + r) * 4) = acc[f][j][e];
+            }
+        lds_barrier();
+        if (gate) {
+#pragma unroll
+            for (int p = 0; p < 8; ++p) {
+                const int idx = p * 64 + lane, row = idx >> 4, c4 = (idx & 15) * 4;
+                const f32x4 g = *(const f32x4 *)(epi + (row * kPEpiRow + c4) * 4);
+                const f32x4 u = *(const f32x4 *)(partner + (row * kPEpiRow + c4) * 4);
+                const int64_t m = m0 + tr + row, n = ncol + c4;
+                if (m >= args.rows || n >= args.n) continue;
+                const float o[4] = {silu(g[0]) * u[0], silu(g[1]) * u[1], silu(g[2]) * u[2], silu(g[3]) * u[3]};
+                const int64_t index = m * args.ldc + n;
+                if (args.out_dtype == SPLOSH_F32) {
+                    const f32x4 v = {o[0], o[1], o[2], o[3]};
+                    *(f32x4 *)((float *)args.out + index) = v;
+                } else {
+                    const u32x2 pk = {f32x2_to_bf16x2(o[0], o[1]), f32x2_to_bf16x2(o[2], o[3])};
+                    *(u32x2 *)((uint16_t *)args.out + index) = pk;
+                }
+            }
+        }
+        lds_barrier();
+    }
+}
+
 // The weights of one 64-element group of K for the tile's 256 columns: thread t loads the part
 // of column t / 2 that covers k = 32 (t % 2) .. + 31 of the group, dequantizes it and writes the
 // 64 bytes of bf16 weights into the weight buffer (four 16-byte pieces, `dst` = the first). Loads
@@ -121,15 +167,16 @@ __device__ __forceinline__ void prefill_store_tile(const PrefillArgs &args, cons
 // MLX affine q4, TILED128: the thread's 16 bytes of the column's record (words 4 (t % 2) .. + 3)
 // and the column's scale and bias (Retile.swift:135-153), dequantized by dequant_word_mix.
 struct Q4Stage {
-    static constexpr int kLoads = 3;
+    static constexpr int kLoads = 3, kNW = 1;
     rsrc_t q_rsrc, s_rsrc, b_rsrc;
     uint32_t magic, c_src, s_src;
     u32x4 cr[2];
     uint32_t sr[2], br[2];
-    __device__ Q4Stage(const PrefillArgs &args) {
-        q_rsrc = make_rsrc(args.w[0], args.w_bytes[0]);
-        s_rsrc = make_rsrc(args.w[1], args.w_bytes[1]);
-        b_rsrc = make_rsrc(args.w[2], args.w_bytes[2]);
+    __device__ Q4Stage(const PrefillArgs &args, bool up = false) {
+        const void *const *w = up ? args.u : args.w;
+        q_rsrc = make_rsrc(w[0], args.w_bytes[0]);
+        s_rsrc = make_rsrc(w[1], args.w_bytes[1]);
+        b_rsrc = make_rsrc(w[2], args.w_bytes[2]);
         asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic));
     }
     __device__ void begin(const PrefillArgs &args, uint32_t col, int hh) {
@@ -151,6 +198,14 @@ struct Q4Stage {
     }
 };
 
+// Fused gate+up over two tiled q4 weights: the tile's 256 columns are 128 of the gate (threads
+// 0 .. 255) and the same 128 of the up weight (threads 256 .. 511).
+struct Q4PairStage : Q4Stage {
+    static constexpr int kNW = 2;
+    __device__ Q4PairStage(const PrefillArgs &args)
+        : Q4Stage(args, __builtin_amdgcn_readfirstlane(threadIdx.x >> 8) != 0) {}
+};
+
 // GGUF Q5_K / Q4_K planes (GgufPlanes.swift:8-20, 62-74): the thread's 32-element group j of its
 // 256-element block is one 16-byte plane0 record (nibbles in chunk order), one 4-byte plane1
 // record (fifth bits; none for Q4_K) and the block's 16-byte meta record (fp16 d, dmin, packed
@@ -164,7 +219,7 @@ struct Q4Stage {
 // then RNE to bf16.
 template <bool FIFTH>
 struct Q5Stage {
-    static constexpr int kLoads = FIFTH ? 3 : 2;
+    static constexpr int kLoads = FIFTH ? 3 : 2, kNW = 1;
     rsrc_t p0_rsrc, p1_rsrc, m_rsrc;
     uint32_t p0_src, p1_src, m_src;
     int hh;
@@ -241,7 +296,7 @@ struct Q5Stage {
 // takes differs by format, so kLoads = 0: the step's wait takes every load.
 template <int TYPE>
 struct GgufStage {
-    static constexpr int kLoads = 0;
+    static constexpr int kLoads = 0, kNW = 1;
     rsrc_t r;
     uint32_t row;
     int hh;
@@ -280,6 +335,8 @@ template <class W>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 prefill_kernel(PrefillArgs args) {
     constexpr int kSCodeLoads = W::kLoads;
+    constexpr int NW = W::kNW;          // 2: fused gate+up, 128 columns of each weight a tile
+    constexpr int kTileCols = kPB / NW; // output columns a tile
     constexpr int FM = 4, kAPer = 4;
     extern __shared__ __align__(16) char lds[];
     const int tid = threadIdx.x;
@@ -304,7 +361,7 @@ prefill_kernel(PrefillArgs args) {
 
     auto run_job = [&](int tile, int ga, int gb, int slot) {
         const int mb = tile % args.mblocks, nb = tile / args.mblocks;
-        const int64_t m0 = (int64_t)mb * kPB, n0 = (int64_t)nb * kPB;
+        const int64_t m0 = (int64_t)mb * kPB, n0 = (int64_t)nb * kTileCols;
         const int T = gb - ga;
         // Activation load p of this wave writes LDS bytes [8192 p + 1024 wave, + 1024): lane l takes
         // row 64 p + 8 wave + l / 8, slot l % 8, i.e. piece (l % 8) ^ ((row / 2) mod 8) (rows past
@@ -321,7 +378,7 @@ prefill_kernel(PrefillArgs args) {
         // last clamped).
         const int hh = tid & 1, sc = tid >> 1;
         {
-            const int64_t nc = n0 + sc;
+            const int64_t nc = n0 + (sc & (kTileCols - 1));
             wst.begin(args, (uint32_t)(nc < args.n ? nc : args.n - 1), hh);
         }
         const uint32_t b_dst = (uint32_t)(kSA + sc * kPRow + 64 * hh);
@@ -404,7 +461,11 @@ prefill_kernel(PrefillArgs args) {
             step(t0, 0);
             step(t0 + 1, 1);
         }
-        prefill_store_tile<FM>(args, acc, epi, m0, n0, 64 * wn, 32 * FM * wm, lane, slot);
+        const int64_t ncol = n0 + ((64 * wn) & (kTileCols - 1));  // the wave's first output column
+        if (NW == 2 && slot < 0)
+            prefill_store_mlp<FM>(args, acc, lds, wave, m0, ncol, 32 * FM * wm, lane);
+        else
+            prefill_store_tile<FM>(args, acc, epi, m0, ncol, 64 * wn, 32 * FM * wm, lane, slot);
     };
 
     const int P = gridDim.x;
@@ -440,7 +501,8 @@ prefill_kernel(PrefillArgs args) {
 // first thread lists the tile's contributing workgroups once (see q4_mma_finish).
 __global__ void __launch_bounds__(256)
 prefill_finish(const float *__restrict__ partial, int dp_tiles, int64_t sk_units, int P, int64_t groups,
-                  int mblocks, int64_t rows, int64_t n, void *out, int64_t ldc, int out_dtype, const void *residual) {
+                  int mblocks, int64_t rows, int64_t n, void *out, int64_t ldc, int out_dtype, const void *residual,
+                  int nw) {
     __shared__ int wg[kPFinishMax];
     __shared__ int slot_of[kPFinishMax];
     __shared__ int count;
@@ -462,22 +524,32 @@ prefill_finish(const float *__restrict__ partial, int dp_tiles, int64_t sk_units
     const int contributors = count;
     if (contributors <= 1) return;  // one workgroup covered the tile and wrote it
     const int tile = dp_tiles + (int)rt;
-    const int64_t m0 = (int64_t)(tile % mblocks) * kPB, n0 = (int64_t)(tile / mblocks) * kPB;
+    const int cols = kPB / nw;  // output columns a tile (nw = 2: gate at tc, up at tc + 128)
+    const int64_t m0 = (int64_t)(tile % mblocks) * kPB, n0 = (int64_t)(tile / mblocks) * cols;
     const int e0 = (blockIdx.y * 256 + threadIdx.x) * 4;  // element of the tile
-    const int tr = e0 / kPB, tc = e0 % kPB;
+    const int tr = e0 / cols, tc = e0 % cols;
     const int64_t m = m0 + tr, col = n0 + tc;
     if (m >= rows || col >= n) return;
-    f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int j0 = 0; j0 < contributors; j0 += 8) {
-        f32x4 x[8];
+    auto sum_at = [&](int c) {
+        f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int j0 = 0; j0 < contributors; j0 += 8) {
+            f32x4 x[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int jj = j0 + j < contributors ? j0 + j : contributors - 1;
-            x[j] = *(const f32x4 *)(partial + ((int64_t)(wg[jj] * 2 + slot_of[jj]) * kPB + tr) * kPB + tc);
+            for (int j = 0; j < 8; ++j) {
+                const int jj = j0 + j < contributors ? j0 + j : contributors - 1;
+                x[j] = *(const f32x4 *)(partial + ((int64_t)(wg[jj] * 2 + slot_of[jj]) * kPB + tr) * kPB + c);
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (j0 + j < contributors) v += x[j];
         }
+        return v;
+    };
+    f32x4 v = sum_at(tc);
+    if (nw == 2) {
+        const f32x4 u = sum_at(tc + cols);
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-            if (j0 + j < contributors) v += x[j];
+        for (int e = 0; e < 4; ++e) v[e] = silu(v[e]) * u[e];
     }
     const int64_t index = m * ldc + col;
     if (out_dtype == SPLOSH_F32) {
@@ -567,9 +639,9 @@ static hipError_t launch_prefill(const PrefillPlan &plan, PrefillArgs &args, int
     hipError_t err = hipGetLastError();
     if (err != hipSuccess || plan.sk_units == 0) return err;
     const int remainder = plan.tiles - plan.dp_tiles;
-    hipLaunchKernelGGL(prefill_finish, dim3((unsigned)remainder, kPB * kPB / 1024), dim3(256), 0, stream,
+    hipLaunchKernelGGL(prefill_finish, dim3((unsigned)remainder, kPB * kPB / 1024 / W::kNW), dim3(256), 0, stream,
                        (const float *)workspace, plan.dp_tiles, plan.sk_units, plan.grid, args.groups, plan.mblocks,
-                       rows, n, out, ldc, out_dtype, residual);
+                       rows, n, out, ldc, out_dtype, residual, W::kNW);
     return hipGetLastError();
 }
 
@@ -585,6 +657,23 @@ hipError_t launch_q4_prefill(const PrefillPlan &plan, const splosh_q4_weight &w,
     args.w_bytes[1] = args.w_bytes[2] = (uint32_t)(w.rows * groups * 2);
     return launch_prefill<Q4Stage>(plan, args, w.rows, w.inner, a, lda, out, ldc, out_dtype, residual, rows,
                                    workspace, stream);
+}
+
+hipError_t launch_q4_prefill_mlp(const PrefillPlan &plan, const splosh_q4_weight &gate, const splosh_q4_weight &up,
+                                 const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype, int64_t rows,
+                                 void *workspace, hipStream_t stream) {
+    PrefillArgs args = {};
+    const int64_t groups = gate.inner / kGroup;
+    args.w[0] = gate.packed;
+    args.w[1] = gate.scales;
+    args.w[2] = gate.biases;
+    args.u[0] = up.packed;
+    args.u[1] = up.scales;
+    args.u[2] = up.biases;
+    args.w_bytes[0] = (uint32_t)(gate.rows * groups * 32);
+    args.w_bytes[1] = args.w_bytes[2] = (uint32_t)(gate.rows * groups * 2);
+    return launch_prefill<Q4PairStage>(plan, args, gate.rows, gate.inner, a, lda, out, ldc, out_dtype, nullptr, rows,
+                                       workspace, stream);
 }
 
 bool q5k_prefill_fits(int64_t rows, int64_t columns, int64_t inner, int64_t lda, int64_t ldc) {

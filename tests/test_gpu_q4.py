@@ -190,6 +190,26 @@ def test_mlp_in_fused(rt, kernel, rows):
         check_close(to_f32(got), ref, bf16_out=True, label=f"mlp bf16 rows={rows}")
 
 
+@pytest.mark.parametrize("rows,n,k", [(65, 384, 576), (300, 256, 640), (513, 128, 64)])
+@pytest.mark.parametrize("split", [True, False])
+def test_mlp_in_prefill(rt, rows, n, k, split):
+    """Fused gate+up through the prefill kernel (AUTO above 64 rows for tiled weights): tiles of 128
+    columns of each weight, silu(g) * u in the epilogue and in the stream-K finish pass, ragged rows."""
+    gate, up = Q4Case(n, k, seed=60 + rows), Q4Case(n, k, seed=61 + rows)
+    a_bits = oracle.bf16_normal((rows, k), seed=62 + rows)
+    g = oracle.gemm_a_bf16_w_f32(a_bits, gate.dense)
+    u = oracle.gemm_a_bf16_w_f32(a_bits, up.dense)
+    ref = oracle.silu_mul(g, u)
+    ws = None if split else torch.empty(0, dtype=torch.uint8, device="cuda")
+    for out_dtype in (torch.float32, torch.bfloat16):
+        got = rt.mlp_in(gate.w_tiled, up.w_tiled, bf16_tensor(a_bits), out_dtype=out_dtype, kernel=rt.PREFILL,
+                        workspace=ws)
+        check_close(to_f32(got), ref, bf16_out=out_dtype == torch.bfloat16,
+                    label=f"mlp prefill {rows}x{n}x{k} split={split} {out_dtype}")
+        auto = rt.mlp_in(gate.w_tiled, up.w_tiled, bf16_tensor(a_bits), out_dtype=out_dtype, workspace=ws)
+        assert torch.equal(auto, got), "AUTO takes the prefill kernel above 64 rows"
+
+
 def _full_size_weight(rt, n, k, seed):
     """A BASELINE-size tiled q4 weight generated on the device (uniform code words,
     scale = bf16(|N(0, 0.02)|), bias = bf16(N(0, 0.01)))."""

@@ -192,7 +192,7 @@ def test_prefill_stage_waits_cover_their_loads(tmp_path):
     res = subprocess.run(cmd, capture_output=True, text=True)
     assert res.returncode == 0, res.stderr[-2000:]
     kernels = list(_kernels(out.read_text(), r"_ZN6splosh14prefill_kernel\S*"))
-    assert len(kernels) == 9  # q4, Q5_K, Q4_K and the six native GGUF formats
+    assert len(kernels) == 10  # q4, fused q4 gate+up, Q5_K, Q4_K and the six native GGUF formats
     for name, code in kernels:
         assert any(_is_lds(ins) for ins in code), name
         # The prologue's barrier and the two unrolled steps'.
