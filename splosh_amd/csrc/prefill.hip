@@ -588,7 +588,10 @@ static int prefill_grid() {
     return cus < kPFinishMax ? cus : kPFinishMax;
 }
 
-static size_t prefill_sk_bytes(int grid) { return (size_t)grid * 2 * kPB * kPB * sizeof(float); }
+// The workspace's first 16 KiB hold the other kernels' arrival counters (left at zero between
+// calls); the partial tiles follow them.
+constexpr size_t kPCounterBytes = 16384;
+static size_t prefill_sk_bytes(int grid) { return kPCounterBytes + (size_t)grid * 2 * kPB * kPB * sizeof(float); }
 
 PrefillPlan plan_prefill(int64_t rows, int64_t columns, int64_t groups, size_t workspace_bytes) {
     PrefillPlan p;
@@ -625,7 +628,7 @@ static hipError_t launch_prefill(const PrefillPlan &plan, PrefillArgs &args, int
     args.rows = rows;
     args.out_dtype = out_dtype;
     args.mblocks = plan.mblocks;
-    args.partial = plan.sk_units > 0 ? (float *)workspace : nullptr;
+    args.partial = plan.sk_units > 0 ? (float *)((char *)workspace + kPCounterBytes) : nullptr;
     args.dp_tiles = plan.dp_tiles;
     args.sk_units = plan.sk_units;
     args.a_bytes = (uint32_t)(((rows - 1) * lda + inner) * 2);
@@ -640,7 +643,7 @@ static hipError_t launch_prefill(const PrefillPlan &plan, PrefillArgs &args, int
     if (err != hipSuccess || plan.sk_units == 0) return err;
     const int remainder = plan.tiles - plan.dp_tiles;
     hipLaunchKernelGGL(prefill_finish, dim3((unsigned)remainder, kPB * kPB / 1024 / W::kNW), dim3(256), 0, stream,
-                       (const float *)workspace, plan.dp_tiles, plan.sk_units, plan.grid, args.groups, plan.mblocks,
+                       (const float *)args.partial, plan.dp_tiles, plan.sk_units, plan.grid, args.groups, plan.mblocks,
                        rows, n, out, ldc, out_dtype, residual, W::kNW);
     return hipGetLastError();
 }

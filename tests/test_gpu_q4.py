@@ -210,6 +210,25 @@ def test_mlp_in_prefill(rt, rows, n, k, split):
         assert torch.equal(auto, got), "AUTO takes the prefill kernel above 64 rows"
 
 
+def test_workspace_shared_by_prefill_and_split_k(rt):
+    """One workspace for a split prefill call and then split M <= 64 calls (gemm and mlp_in): the
+    prefill's partial tiles must not touch the arrival counters at the workspace's start."""
+    n, k = 512, 2048
+    gate, up = Q4Case(n, k, seed=70), Q4Case(n, k, seed=71)
+    ws = torch.zeros(max(rt.workspace_bytes(300, n, k), rt.workspace_bytes(64, n, k)), dtype=torch.uint8,
+                     device="cuda")
+    for rows in (300, 64, 33, 300, 64):
+        a_bits = oracle.bf16_normal((rows, k), seed=72 + rows)
+        g = oracle.gemm_a_bf16_w_f32(a_bits, gate.dense)
+        got = rt.gemm(gate.w_tiled, bf16_tensor(a_bits), out_dtype=torch.float32, workspace=ws)
+        check_close(got.cpu().numpy(), g, bf16_out=False, tight=True, absref=abs_gemm(a_bits, gate.dense),
+                    label=f"shared workspace gemm rows={rows}")
+        got = rt.mlp_in(gate.w_tiled, up.w_tiled, bf16_tensor(a_bits), out_dtype=torch.float32, workspace=ws)
+        check_close(got.cpu().numpy(), oracle.silu_mul(g, oracle.gemm_a_bf16_w_f32(a_bits, up.dense)),
+                    bf16_out=False, label=f"shared workspace mlp rows={rows}")
+        assert not ws[:16384].any(), f"arrival counters left nonzero after rows={rows}"
+
+
 def _full_size_weight(rt, n, k, seed):
     """A BASELINE-size tiled q4 weight generated on the device (uniform code words,
     scale = bf16(|N(0, 0.02)|), bias = bf16(N(0, 0.01)))."""
