@@ -54,3 +54,44 @@ def test_graph_replays_match_eager(rt):
         for got, want in zip((act, out, out1), ref):
             assert torch.equal(got.view(torch.int16), want.view(torch.int16)), f"replay {k} differs"
         del junk
+
+
+def test_prefill_graph_replays_match_eager(rt):
+    """The prefill kernel and its stream-K finish pass under capture: q4 (single weight and fused
+    gate+up) and Q5_K planes at 300 rows, replayed with eager work between replays."""
+    rows, h, inter = 300, 512, 1024
+    gate, up = Q4Case(inter, h, seed=70), Q4Case(inter, h, seed=71)
+    native = oracle.q45k_random_native(h, inter, seed=72)
+    wq5 = rt.q5k_repack(torch.from_numpy(native).cuda(), h, inter)
+    x = bf16_tensor(oracle.bf16_normal((rows, h), seed=73))
+    xi = bf16_tensor(oracle.bf16_normal((rows, inter), seed=74))
+    act = torch.empty(rows, inter, dtype=torch.bfloat16, device="cuda")
+    g1 = torch.empty(rows, inter, dtype=torch.float32, device="cuda")
+    o5 = torch.empty(rows, h, dtype=torch.bfloat16, device="cuda")
+    ws = torch.zeros(max(rt.workspace_bytes(rows, inter, h), rt.workspace_bytes(rows, h, inter)), dtype=torch.uint8,
+                     device="cuda")
+
+    def step():
+        rt.mlp_in(gate.w_tiled, up.w_tiled, x, out=act, workspace=ws)
+        rt.gemm(gate.w_tiled, x, out=g1, workspace=ws)
+        rt.gemm(wq5, xi, out=o5, workspace=ws)
+
+    step()
+    torch.cuda.synchronize()
+    ref = (act.clone(), g1.clone(), o5.clone())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    for k in range(4):
+        act.zero_()
+        g1.fill_(float("nan"))
+        o5.zero_()
+        junk = torch.randn(1 << 20, device="cuda").sum()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for got, want in zip((act, g1, o5), ref):
+            assert torch.equal(got.view(torch.int16) if got.dtype == torch.bfloat16 else got.view(torch.int32),
+                               want.view(torch.int16) if want.dtype == torch.bfloat16 else want.view(torch.int32)), \
+                f"replay {k} differs"
+        del junk
