@@ -117,6 +117,10 @@ int q4_gemm_impl(const splosh_q4_weight *w, const splosh_q4_weight *up, const ui
         else if (wide16 && splosh::lanes_fit(rows, w->rows, w->inner, w->row_stride_words, up != nullptr))
             choice = SPLOSH_KERNEL_STREAM;
         else if (mma_ok) choice = SPLOSH_KERNEL_DEQUANT;
+        // One weight at 65..128 rows: the tile kernel where the prefill kernel's 256-row tiles are
+        // mostly padding and its tiles few (measured at M=64..128: K17408 -> N5120 tile 51-56 us,
+        // prefill 59-65; K5120 -> N17408 tile better at 65 rows, prefill from 96).
+        else if (tile_ok && !up && rows <= 128 && (rows <= 80 || w->rows <= 8192)) choice = SPLOSH_KERNEL_TILE;
         else if (prefill_ok || prefill_mlp_ok) choice = SPLOSH_KERNEL_PREFILL;
         else if (tile_ok) choice = SPLOSH_KERNEL_TILE;
         else choice = SPLOSH_KERNEL_STREAM;
