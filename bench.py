@@ -514,7 +514,8 @@ def main():
 
     dominant = max(per_kernel, key=per_kernel.get)
     dom_ms = per_kernel[dominant]
-    compute_bound = args.workload in ("prefill2048", "gemm2048")
+    # Prefill-sized workloads (512 rows or more) are bound by the matrix cores, the others by HBM.
+    compute_bound = cfg.get("rows", 0) >= 512 and kernel_flops.get(dominant, 0) > 0
     traffic = MEASURED_TRAFFIC.get((args.workload, dominant))
     traffic = int(traffic) if traffic is not None else None
     if compute_bound:
