@@ -228,11 +228,14 @@ __device__ __forceinline__ void gguf_decode(const GgufRaw<TYPE> &w, float (&v)[3
         align_span(w.ql, ql);
         align_span(w.qh, qh);
         const int lsh = 4 * (quarter >> 1), hsh = 2 * quarter;
+        // Four codes a word: the 6-bit (low | high << 4) of each byte, then ds (code - 32) in the
+        // reference's order (the subtraction is exact).
 #pragma unroll
-        for (int e = 0; e < 32; ++e) {
-            const uint32_t low = (byte_of(ql, e) >> lsh) & 15, high = (byte_of(qh, e) >> hsh) & 3;
-            const float code = (float)(low | (high << 4)) - 32.0f;
-            v[e] = (e < 16 ? ds0 : ds1) * code;
+        for (int q = 0; q < 8; ++q) {
+            const uint32_t codes = ((ql[q] >> lsh) & 0x0F0F0F0Fu) | (((qh[q] >> hsh) & 0x03030303u) << 4);
+            const float ds = q < 4 ? ds0 : ds1;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) v[4 * q + t] = ds * (cvt_byte(codes, t) - 32.0f);
         }
     } else if constexpr (TYPE == 11) {
         const int j = w.j, shift = 2 * (j & 3), word = j >> 1;
@@ -244,11 +247,13 @@ __device__ __forceinline__ void gguf_decode(const GgufRaw<TYPE> &w, float (&v)[3
         uint32_t hm[8], qs[8];
         align_span(w.hm, hm);
         align_span(w.qs, qs);
+        // Four codes a word, then ds (code - 4) in the reference's order.
 #pragma unroll
-        for (int e = 0; e < 32; ++e) {
-            const uint32_t low = (byte_of(qs, e) >> shift) & 3, high = (byte_of(hm, e) >> j) & 1;
-            const float code = (float)(low | (high << 2)) - 4.0f;
-            v[e] = (e < 16 ? ds0 : ds1) * code;
+        for (int q = 0; q < 8; ++q) {
+            const uint32_t codes = ((qs[q] >> shift) & 0x03030303u) | (((hm[q] >> j) & 0x01010101u) << 2);
+            const float ds = q < 4 ? ds0 : ds1;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) v[4 * q + t] = ds * (cvt_byte(codes, t) - 4.0f);
         }
     } else if constexpr (TYPE == 21) {
         const int j = w.j;
