@@ -51,16 +51,19 @@ struct GgufTileArgs {
 };
 
 // TYPE: a ggml type id; 13 / 12 = Q5_K / Q4_K planes.
-template <int TYPE, int FM, int FN, bool SPLIT>
-__global__ void __launch_bounds__(256) gguf_tile_kernel(GgufTileArgs args) {
+template <int TYPE, int FM, int FN, bool SPLIT, int KH>
+__global__ void __launch_bounds__(256 * KH) gguf_tile_kernel(GgufTileArgs args) {
     constexpr int BM = 64 * FM, BN = 64 * FN;
     constexpr int kAChunks = BM * 8;        // 16-byte chunks of the A tile
     constexpr int kAPer = kAChunks / 256;
     static_assert(BN == 128, "one 32-element weight group a thread");
     extern __shared__ __align__(16) uint16_t lds[];
-    uint16_t *sA = lds, *sB = lds + BM * kGtStride;
+    // KH K-halves: half kh (threads 256 kh ..) takes the 64-element steps s with s % KH == kh of
+    // the slice into operand tiles of its own; the halves' sums meet in LDS at the end.
+    const int kh = KH > 1 ? __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 8) : 0;
+    uint16_t *sA = lds + kh * (BM + BN) * kGtStride, *sB = sA + BM * kGtStride;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x & 255, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int r = lane & 31, h = lane >> 5;
     const int64_t m0 = (int64_t)blockIdx.y * BM, n0 = (int64_t)blockIdx.x * BN;
@@ -142,14 +145,40 @@ __global__ void __launch_bounds__(256) gguf_tile_kernel(GgufTileArgs args) {
     };
 
     Stage cur, nxt;
-    if (s_lo < s_hi) fetch(cur, s_lo);
-    for (int s = s_lo; s < s_hi; ++s) {
-        if (s + 1 < s_hi) fetch(nxt, s + 1);
-        commit(cur);
+    if (s_lo + kh < s_hi) fetch(cur, s_lo + kh);
+    for (int s = s_lo + kh; s - kh < s_hi; s += KH) {
+        const bool on = s < s_hi;  // wave-uniform: a half whose last step is past the slice idles
+        if (s + KH < s_hi) fetch(nxt, s + KH);
+        if (on) commit(cur);
         __syncthreads();
-        multiply();
+        if (on) multiply();
         __syncthreads();
         cur = nxt;
+    }
+    if constexpr (KH > 1) {
+        // Half 1 hands its sums to half 0 (thread for thread) through LDS; half 0 goes on alone.
+        float *sx = (float *)lds;
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    if (kh == 1)
+                        *(f32x4 *)(sx + (((i * FN + j) * 4 + q) * 256 + tid) * 4) =
+                            f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+        __syncthreads();
+        if (kh == 1) return;
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const f32x4 t = *(const f32x4 *)(sx + (((i * FN + j) * 4 + q) * 256 + tid) * 4);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[i][j][4 * q + e] += t[e];
+                }
     }
 
     // The epilogue takes one 32 x 32 block of a wave at a time through a wave-private LDS
@@ -157,7 +186,7 @@ __global__ void __launch_bounds__(256) gguf_tile_kernel(GgufTileArgs args) {
     // 8 (e / 4) + 4 h + e % 4, column r -- goes in, and lane l takes out row l / 2, columns
     // 16 (l % 2) .. + 16, so that the stores to the output (and the residual loads) are 64 or 32
     // contiguous bytes a lane.
-    float *sq = (float *)lds + wave * 32 * kGtSqStride;
+    float *sq = (float *)lds + (KH > 1 ? FM * FN * 4 * 256 * 4 : 0) + wave * 32 * kGtSqStride;
     auto store_block = [&](int i, int j, const f32x16 &v) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) sq[(8 * (e >> 2) + 4 * h + (e & 3)) * kGtSqStride + r] = v[e];
@@ -301,6 +330,15 @@ __global__ void __launch_bounds__(256) gguf_tile_finish(GgufTileArgs args) {
 }
 
 // Tile shapes (BM x 128 columns): 64 rows up to 64 activation rows, 128 up to 128, 256 above.
+// K-halves a workgroup at 64-row tiles (two: eight waves, two a SIMD instead of about one).
+static int gt_kh() {
+    static const int kh = [] {
+        const char *e = getenv("SPLOSH_GGUF_TILE_KH");
+        return e && atoi(e) == 1 ? 1 : 2;
+    }();
+    return kh;
+}
+
 static int gt_fm(int64_t rows) {
     static const int forced = [] {
         const char *e = getenv("SPLOSH_GGUF_TILE_FM");
@@ -343,20 +381,30 @@ size_t gguf_tile_workspace_bytes(int64_t rows, int64_t n, int64_t inner) {
     return (size_t)kGtCounterBytes + (size_t)tiles * s * 256 * fm * 2 * 16 * 4;
 }
 
-template <int TYPE, int FM, int FN>
+// LDS of one launch: KH pairs of operand tiles; with two K-halves also the hand-over of half 1's
+// sums followed by the epilogue squares (which must not overlap it).
+template <int FM, int FN, int KH>
+constexpr size_t gt_lds_bytes() {
+    const size_t tiles = (size_t)KH * (64 * FM + 64 * FN) * kGtStride * 2;
+    const size_t tail = KH > 1 ? (size_t)FM * FN * 16 * 256 * 4 + 4 * 32 * kGtSqStride * 4 : 0;
+    return tiles > tail ? tiles : tail;
+}
+
+template <int TYPE, int FM, int FN, int KH = 1>
 static hipError_t launch_gt(const GgufTileArgs &args, hipStream_t stream) {
     constexpr int BM = 64 * FM, BN = 64 * FN;
-    const size_t lds = (size_t)(BM + BN) * kGtStride * sizeof(uint16_t);
+    constexpr size_t lds = gt_lds_bytes<FM, FN, KH>();
+    static_assert(lds <= 160 * 1024, "LDS of one workgroup");
     const dim3 grid((unsigned)((args.n + BN - 1) / BN), (unsigned)((args.rows + BM - 1) / BM), (unsigned)args.splits);
     // The split variant is a kernel of its own: its summing code needs registers that would
     // otherwise cost the unsplit kernel occupancy.
     if (args.splits > 1) {
-        hipLaunchKernelGGL((gguf_tile_kernel<TYPE, FM, FN, true>), grid, dim3(256), lds, stream, args);
+        hipLaunchKernelGGL((gguf_tile_kernel<TYPE, FM, FN, true, KH>), grid, dim3(256 * KH), lds, stream, args);
         const hipError_t err = hipGetLastError();
         if (err != hipSuccess) return err;
         hipLaunchKernelGGL((gguf_tile_finish<FM, FN>), dim3(grid.x * grid.y, FM * FN * 4), dim3(256), 0, stream, args);
     } else {
-        hipLaunchKernelGGL((gguf_tile_kernel<TYPE, FM, FN, false>), grid, dim3(256), lds, stream, args);
+        hipLaunchKernelGGL((gguf_tile_kernel<TYPE, FM, FN, false, KH>), grid, dim3(256 * KH), lds, stream, args);
     }
     return hipGetLastError();
 }
@@ -364,7 +412,7 @@ static hipError_t launch_gt(const GgufTileArgs &args, hipStream_t stream) {
 template <int TYPE>
 static hipError_t launch_gt_rows(const GgufTileArgs &args, hipStream_t stream) {
     switch (gt_fm(args.rows)) {
-        case 1: return launch_gt<TYPE, 1, 2>(args, stream);
+        case 1: return gt_kh() > 1 ? launch_gt<TYPE, 1, 2, 2>(args, stream) : launch_gt<TYPE, 1, 2>(args, stream);
         default: return launch_gt<TYPE, 2, 2>(args, stream);
     }
 }
