@@ -80,6 +80,52 @@ __global__ void __launch_bounds__(256) gguf_embed_kernel(GgufNativeArgs args, co
     }
 }
 
+typedef __bf16 bf16x2_g __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float gdot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_g, a), __builtin_bit_cast(bf16x2_g, b), c, false);
+}
+
+// Q6_K group g (GgufQuant.swift:218-230) against up to MR activation rows, on the raw codes: the
+// bf16 0x4300 | c is exactly 128 + c for a 6-bit code c, so with x the activations of one
+// 16-element sub-block, sum x w = ds (sum x (128 + c) - 160 sum x), ds = d sc as the reference
+// forms it. Both sums are v_dot2 on bf16 pairs (exact products, fp32 sums): about three VALU an
+// element in place of six for decoding to fp32 and multiplying there.
+template <int MR>
+__device__ __forceinline__ void q6k_dot(const GgufRaw<14> &w, const GgufNativeArgs &args, int64_t m0, int g,
+                                        float (&acc)[MR]) {
+    const int quarter = w.j & 3;
+    const float d = half_bits_to_f32(w.d);
+    const float ds0 = d * (float)(int8_t)(w.sc & 0xFF), ds1 = d * (float)(int8_t)(w.sc >> 8);
+    uint32_t ql[8], qh[8];
+    align_span(w.ql, ql);
+    align_span(w.qh, qh);
+    const int lsh = 4 * (quarter >> 1), hsh = 2 * quarter;
+    uint32_t p[16];  // bf16 pairs (128 + c) of elements 2 i, 2 i + 1
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        const uint32_t codes = ((ql[q] >> lsh) & 0x0F0F0F0Fu) | (((qh[q] >> hsh) & 0x03030303u) << 4);
+        p[2 * q] = __builtin_amdgcn_perm(0x43434343u, codes, 0x04010400u);
+        p[2 * q + 1] = __builtin_amdgcn_perm(0x43434343u, codes, 0x04030402u);
+    }
+#pragma unroll
+    for (int i = 0; i < MR; ++i) {
+        if (m0 + i >= args.m) break;
+        const u32x4 *ap = (const u32x4 *)(args.a + (m0 + i) * args.lda + (int64_t)g * 32);
+        float s[2] = {0.0f, 0.0f}, t[2] = {0.0f, 0.0f};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const u32x4 x = ap[q];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                s[q >> 1] = gdot2(x[e], p[4 * q + e], s[q >> 1]);
+                t[q >> 1] = gdot2(x[e], 0x3F803F80u, t[q >> 1]);
+            }
+        }
+        acc[i] = __builtin_fmaf(ds0, __builtin_fmaf(-160.0f, t[0], s[0]), acc[i]);
+        acc[i] = __builtin_fmaf(ds1, __builtin_fmaf(-160.0f, t[1], s[1]), acc[i]);
+    }
+}
+
 template <int TYPE, int MR>
 __global__ void __launch_bounds__(256) gguf_gemv_kernel(GgufNativeArgs args) {
     const int lane = threadIdx.x & 63;
@@ -124,9 +170,13 @@ __global__ void __launch_bounds__(256) gguf_gemv_kernel(GgufNativeArgs args) {
         accumulate(g + 64, v1);
     }
     for (; g < groups; g += 64) {
-        float v[32];
-        decode_group<TYPE>(r, row, g, v);
-        accumulate(g, v);
+        if constexpr (TYPE == 14) {
+            q6k_dot<MR>(gguf_fetch<14>(r, row, g), args, m0, g, acc);
+        } else {
+            float v[32];
+            decode_group<TYPE>(r, row, g, v);
+            accumulate(g, v);
+        }
     }
 #pragma unroll
     for (int i = 0; i < MR; ++i) {
