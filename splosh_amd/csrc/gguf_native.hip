@@ -10,8 +10,9 @@
 //  * gguf_gemv_kernel: out[m][n] = sum_k a[m][k] w[n][k] for a few rows of activations. A wave
 //    owns one weight row; its lanes take the row's 32-element groups in turn, decode each into
 //    registers exactly as the dequant kernel does and accumulate it against up to MR activation
-//    rows (fp32). The wave's partial sums meet in a shuffle tree. Rows beyond MR take further
-//    passes over the weight (grid.y).
+//    rows (fp32); Q6_K and Q3_K instead multiply their raw codes as bf16 and apply the scales
+//    per sub-block (raw_code_dot). The wave's partial sums meet in a shuffle tree. Rows beyond
+//    MR take further passes over the weight (grid.y).
 //
 // Blocks are 2-byte aligned at best (Q8_0: 34 bytes, Q6_K: 210): a run of bytes is read as the
 // dword-aligned window that covers it, in 16-byte loads, and shifted into place per lane.
@@ -85,27 +86,20 @@ __device__ __forceinline__ float gdot2(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_g, a), __builtin_bit_cast(bf16x2_g, b), c, false);
 }
 
-// Q6_K group g (GgufQuant.swift:218-230) against up to MR activation rows, on the raw codes: the
-// bf16 0x4300 | c is exactly 128 + c for a 6-bit code c, so with x the activations of one
-// 16-element sub-block, sum x w = ds (sum x (128 + c) - 160 sum x), ds = d sc as the reference
-// forms it. Both sums are v_dot2 on bf16 pairs (exact products, fp32 sums): about three VALU an
-// element in place of six for decoding to fp32 and multiplying there.
+// A K-quant group on its raw codes (Q6_K, GgufQuant.swift:218-230; Q3_K, :238-256): the bf16
+// 0x4300 | c is exactly 128 + c for a code c < 128, so with x the activations of one 16-element
+// sub-block, sum x w = ds (sum x (128 + c) - (128 + o) sum x) for w = ds (c - o), ds as the
+// reference forms it (o = 32 for Q6_K, 4 for Q3_K). Both sums are v_dot2 on bf16 pairs (exact
+// products, fp32 sums): about three VALU an element in place of six for decoding to fp32 and
+// multiplying there. `codes[q]` holds the codes of elements 4 q .. 4 q + 3, a byte each.
 template <int MR>
-__device__ __forceinline__ void q6k_dot(const GgufRaw<14> &w, const GgufNativeArgs &args, int64_t m0, int g,
-                                        float (&acc)[MR]) {
-    const int quarter = w.j & 3;
-    const float d = half_bits_to_f32(w.d);
-    const float ds0 = d * (float)(int8_t)(w.sc & 0xFF), ds1 = d * (float)(int8_t)(w.sc >> 8);
-    uint32_t ql[8], qh[8];
-    align_span(w.ql, ql);
-    align_span(w.qh, qh);
-    const int lsh = 4 * (quarter >> 1), hsh = 2 * quarter;
+__device__ __forceinline__ void raw_code_dot(const uint32_t (&codes)[8], float ds0, float ds1, float bias,
+                                             const GgufNativeArgs &args, int64_t m0, int g, float (&acc)[MR]) {
     uint32_t p[16];  // bf16 pairs (128 + c) of elements 2 i, 2 i + 1
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
-        const uint32_t codes = ((ql[q] >> lsh) & 0x0F0F0F0Fu) | (((qh[q] >> hsh) & 0x03030303u) << 4);
-        p[2 * q] = __builtin_amdgcn_perm(0x43434343u, codes, 0x04010400u);
-        p[2 * q + 1] = __builtin_amdgcn_perm(0x43434343u, codes, 0x04030402u);
+        p[2 * q] = __builtin_amdgcn_perm(0x43434343u, codes[q], 0x04010400u);
+        p[2 * q + 1] = __builtin_amdgcn_perm(0x43434343u, codes[q], 0x04030402u);
     }
 #pragma unroll
     for (int i = 0; i < MR; ++i) {
@@ -121,9 +115,40 @@ __device__ __forceinline__ void q6k_dot(const GgufRaw<14> &w, const GgufNativeAr
                 t[q >> 1] = gdot2(x[e], 0x3F803F80u, t[q >> 1]);
             }
         }
-        acc[i] = __builtin_fmaf(ds0, __builtin_fmaf(-160.0f, t[0], s[0]), acc[i]);
-        acc[i] = __builtin_fmaf(ds1, __builtin_fmaf(-160.0f, t[1], s[1]), acc[i]);
+        acc[i] = __builtin_fmaf(ds0, __builtin_fmaf(-bias, t[0], s[0]), acc[i]);
+        acc[i] = __builtin_fmaf(ds1, __builtin_fmaf(-bias, t[1], s[1]), acc[i]);
     }
+}
+
+template <int MR>
+__device__ __forceinline__ void q6k_dot(const GgufRaw<14> &w, const GgufNativeArgs &args, int64_t m0, int g,
+                                        float (&acc)[MR]) {
+    const int quarter = w.j & 3;
+    const float d = half_bits_to_f32(w.d);
+    const float ds0 = d * (float)(int8_t)(w.sc & 0xFF), ds1 = d * (float)(int8_t)(w.sc >> 8);
+    uint32_t ql[8], qh[8], codes[8];
+    align_span(w.ql, ql);
+    align_span(w.qh, qh);
+    const int lsh = 4 * (quarter >> 1), hsh = 2 * quarter;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) codes[q] = ((ql[q] >> lsh) & 0x0F0F0F0Fu) | (((qh[q] >> hsh) & 0x03030303u) << 4);
+    raw_code_dot<MR>(codes, ds0, ds1, 160.0f, args, m0, g, acc);
+}
+
+template <int MR>
+__device__ __forceinline__ void q3k_dot(const GgufRaw<11> &w, const GgufNativeArgs &args, int64_t m0, int g,
+                                        float (&acc)[MR]) {
+    const int j = w.j, shift = 2 * (j & 3), word = j >> 1;
+    const float d = half_bits_to_f32(w.d);
+    const uint32_t lows = w.lows >> (4 * (word >> 1)), highs = w.highs >> (2 * word);
+    const float s0 = (float)((lows & 0xF) | ((highs & 3) << 4)) - 32.0f;
+    const float s1 = (float)(((lows >> 8) & 0xF) | (((highs >> 8) & 3) << 4)) - 32.0f;
+    uint32_t hm[8], qs[8], codes[8];
+    align_span(w.hm, hm);
+    align_span(w.qs, qs);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) codes[q] = ((qs[q] >> shift) & 0x03030303u) | (((hm[q] >> j) & 0x01010101u) << 2);
+    raw_code_dot<MR>(codes, d * s0, d * s1, 132.0f, args, m0, g, acc);
 }
 
 template <int TYPE, int MR>
@@ -172,6 +197,8 @@ __global__ void __launch_bounds__(256) gguf_gemv_kernel(GgufNativeArgs args) {
     for (; g < groups; g += 64) {
         if constexpr (TYPE == 14) {
             q6k_dot<MR>(gguf_fetch<14>(r, row, g), args, m0, g, acc);
+        } else if constexpr (TYPE == 11) {
+            q3k_dot<MR>(gguf_fetch<11>(r, row, g), args, m0, g, acc);
         } else {
             float v[32];
             decode_group<TYPE>(r, row, g, v);
