@@ -11,7 +11,7 @@
 //    owns one weight row; its lanes take the row's 32-element groups in turn, decode each into
 //    registers exactly as the dequant kernel does and accumulate it against up to MR activation
 //    rows (fp32); Q6_K and Q3_K instead multiply their raw codes as bf16 and apply the scales
-//    per sub-block (raw_code_dot). The wave's partial sums meet in a shuffle tree. Rows beyond
+//    per sub-block (raw_code_dot), IQ3_S its signed codebook magnitudes (iq3s_dot). The wave's partial sums meet in a shuffle tree. Rows beyond
 //    MR take further passes over the weight (grid.y).
 //
 // Blocks are 2-byte aligned at best (Q8_0: 34 bytes, Q6_K: 210): a run of bytes is read as the
@@ -151,8 +151,60 @@ __device__ __forceinline__ void q3k_dot(const GgufRaw<11> &w, const GgufNativeAr
     raw_code_dot<MR>(codes, d * s0, d * s1, 132.0f, args, m0, g, acc);
 }
 
+// IQ3_S group g (GgufQuant.swift:283-300) on bf16 weights formed without fp32 arithmetic: `tab`
+// holds each codebook entry's four magnitudes (odd, 1..15: exact in bf16) as two bf16 pairs, the
+// sign bits are spread to bits 15 and 31 of each pair by one multiply and two byte permutes, and
+// the group's d (1 + 2 scale) multiplies the v_dot2 sum once.
+template <int MR>
+__device__ __forceinline__ void iq3s_dot(const GgufRaw<21> &w, const uint2 *tab, const GgufNativeArgs &args,
+                                         int64_t m0, int g, float (&acc)[MR]) {
+    const int j = w.j;
+    const float d = half_bits_to_f32(w.d);
+    const uint32_t scale = (w.scale >> (8 * ((j >> 1) & 1) + 4 * (j & 1))) & 15;
+    const float weight = d * (1.0f + 2.0f * (float)scale);
+    const uint32_t ninth = (w.ninth >> (8 * (j & 1))) & 0xFF;
+    uint32_t cb[2], sg[1], p[16];
+    align_span(w.cb, cb);
+    align_span(w.sg, sg);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const uint32_t code = ((cb[k >> 2] >> (8 * (k & 3))) & 0xFF) | (((ninth >> k) & 1) << 8);
+        const uint2 m = tab[code];
+        // Sign bit t of elements 4 k + t to bit 7 of byte t, then to bits 15 and 31 of the pairs.
+        const uint32_t spread = ((((sg[0] >> (4 * k)) & 0xFu) * 0x00204081u) & 0x01010101u) << 7;
+        p[2 * k] = m.x ^ __builtin_amdgcn_perm(0u, spread, 0x010C000Cu);
+        p[2 * k + 1] = m.y ^ __builtin_amdgcn_perm(0u, spread, 0x030C020Cu);
+    }
+#pragma unroll
+    for (int i = 0; i < MR; ++i) {
+        if (m0 + i >= args.m) break;
+        const u32x4 *ap = (const u32x4 *)(args.a + (m0 + i) * args.lda + (int64_t)g * 32);
+        float s = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const u32x4 x = ap[q];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) s = gdot2(x[e], p[4 * q + e], s);
+        }
+        acc[i] = __builtin_fmaf(weight, s, acc[i]);
+    }
+}
+
 template <int TYPE, int MR>
 __global__ void __launch_bounds__(256) gguf_gemv_kernel(GgufNativeArgs args) {
+    // IQ3_S: the codebook as bf16 magnitude pairs in LDS, built before any wave leaves.
+    __shared__ uint2 iq3s_tab[TYPE == 21 ? 512 : 1];
+    if constexpr (TYPE == 21) {
+        for (int c = threadIdx.x; c < 512; c += blockDim.x) {
+            const uint32_t packed = kIq3sPacked[c];
+            uint32_t h[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                h[t] = __builtin_bit_cast(uint32_t, (float)(2u * ((packed >> (3 * t)) & 7u) + 1u)) >> 16;
+            iq3s_tab[c] = uint2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+        }
+        __syncthreads();
+    }
     const int lane = threadIdx.x & 63;
     const int64_t n = (int64_t)xcd_block(blockIdx.x, gridDim.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (n >= args.rows) return;
@@ -199,6 +251,8 @@ __global__ void __launch_bounds__(256) gguf_gemv_kernel(GgufNativeArgs args) {
             q6k_dot<MR>(gguf_fetch<14>(r, row, g), args, m0, g, acc);
         } else if constexpr (TYPE == 11) {
             q3k_dot<MR>(gguf_fetch<11>(r, row, g), args, m0, g, acc);
+        } else if constexpr (TYPE == 21) {
+            iq3s_dot<MR>(gguf_fetch<21>(r, row, g), iq3s_tab, args, m0, g, acc);
         } else {
             float v[32];
             decode_group<TYPE>(r, row, g, v);
