@@ -11,7 +11,8 @@
 //    owns one weight row; its lanes take the row's 32-element groups in turn, decode each into
 //    registers exactly as the dequant kernel does and accumulate it against up to MR activation
 //    rows (fp32); Q6_K and Q3_K instead multiply their raw codes as bf16 and apply the scales
-//    per sub-block (raw_code_dot), IQ3_S its signed codebook magnitudes (iq3s_dot). The wave's partial sums meet in a shuffle tree. Rows beyond
+//    per sub-block (raw_code_dot), IQ3_S its signed codebook magnitudes (iq3s_dot), IQ4_NL and
+//    IQ4_XS their table values (iq4_dot), all as bf16 pairs into v_dot2. The wave's partial sums meet in a shuffle tree. Rows beyond
 //    MR take further passes over the weight (grid.y).
 //
 // Blocks are 2-byte aligned at best (Q8_0: 34 bytes, Q6_K: 210): a run of bytes is read as the
@@ -190,10 +191,60 @@ __device__ __forceinline__ void iq3s_dot(const GgufRaw<21> &w, const uint2 *tab,
     }
 }
 
+// IQ4_NL / IQ4_XS group (GgufQuant.swift:179-185, 261-275): `tab[b]` holds the table values of
+// both nibbles of a code byte b as a bf16 pair (the values are integers below 128 in magnitude:
+// exact), for elements 4 q + e (low nibble) and 16 + 4 q + e (high nibble) of byte e of word q;
+// one byte permute pairs the activations the same way, and the group's scale multiplies the
+// v_dot2 sum once.
+template <int MR>
+__device__ __forceinline__ void iq4_dot(const uint32_t (&h)[4], float scale, const uint32_t *tab,
+                                        const GgufNativeArgs &args, int64_t m0, int g, float (&acc)[MR]) {
+    uint32_t w[16];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[4 * q + e] = tab[(h[q] >> (8 * e)) & 0xFFu];
+#pragma unroll
+    for (int i = 0; i < MR; ++i) {
+        if (m0 + i >= args.m) break;
+        const u32x4 *ap = (const u32x4 *)(args.a + (m0 + i) * args.lda + (int64_t)g * 32);
+        uint32_t x[16];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const u32x4 v = ap[q];
+            x[4 * q] = v[0], x[4 * q + 1] = v[1], x[4 * q + 2] = v[2], x[4 * q + 3] = v[3];
+        }
+        float s = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                // Elements 4 q + e and 16 + 4 q + e: the low (e even) or high halves of activation
+                // dwords 2 q + e / 2 and 8 + 2 q + e / 2.
+                const int dw = 2 * q + (e >> 1);
+                const uint32_t pair =
+                    __builtin_amdgcn_perm(x[8 + dw], x[dw], (e & 1) ? 0x07060302u : 0x05040100u);
+                s = gdot2(pair, w[4 * q + e], s);
+            }
+        acc[i] = __builtin_fmaf(scale, s, acc[i]);
+    }
+}
+
 template <int TYPE, int MR>
 __global__ void __launch_bounds__(256) gguf_gemv_kernel(GgufNativeArgs args) {
-    // IQ3_S: the codebook as bf16 magnitude pairs in LDS, built before any wave leaves.
-    __shared__ uint2 iq3s_tab[TYPE == 21 ? 512 : 1];
+    // Lookup tables in LDS, built before any wave leaves: IQ3_S's codebook as bf16 magnitude
+    // pairs (512 x 8 bytes), the IQ4 values of both nibbles of a byte as a bf16 pair (256 x 4).
+    constexpr bool kIq4 = TYPE == 20 || TYPE == 23;
+    __shared__ __align__(8) uint32_t lut[TYPE == 21 ? 1024 : kIq4 ? 256 : 1];
+    uint2 *iq3s_tab = (uint2 *)lut;
+    if constexpr (kIq4) {
+        const uint32_t kv[4] = {kIq4Tab0, kIq4Tab1, kIq4Tab2, kIq4Tab3};
+        auto bf = [&](uint32_t i) {
+            return __builtin_bit_cast(uint32_t, (float)(int8_t)((kv[i >> 2] >> (8 * (i & 3))) & 0xFFu)) >> 16;
+        };
+        for (int c = threadIdx.x; c < 256; c += blockDim.x) lut[c] = bf(c & 15) | (bf(c >> 4) << 16);
+        __syncthreads();
+    }
     if constexpr (TYPE == 21) {
         for (int c = threadIdx.x; c < 512; c += blockDim.x) {
             const uint32_t packed = kIq3sPacked[c];
@@ -253,6 +304,18 @@ __global__ void __launch_bounds__(256) gguf_gemv_kernel(GgufNativeArgs args) {
             q3k_dot<MR>(gguf_fetch<11>(r, row, g), args, m0, g, acc);
         } else if constexpr (TYPE == 21) {
             iq3s_dot<MR>(gguf_fetch<21>(r, row, g), iq3s_tab, args, m0, g, acc);
+        } else if constexpr (TYPE == 20) {
+            const GgufRaw<20> w = gguf_fetch<20>(r, row, g);
+            uint32_t h[4];
+            align_span(w.codes, h);
+            iq4_dot<MR>(h, half_bits_to_f32(w.d), lut, args, m0, g, acc);
+        } else if constexpr (TYPE == 23) {
+            const GgufRaw<23> w = gguf_fetch<23>(r, row, g);
+            const int j = w.j;
+            const uint32_t low = (w.lowb >> (8 * ((j >> 1) & 1) + 4 * (j & 1))) & 15;
+            const uint32_t scale = low | (((w.high >> (2 * j)) & 3) << 4);
+            const uint32_t h[4] = {w.q[0], w.q[1], w.q[2], w.q[3]};
+            iq4_dot<MR>(h, half_bits_to_f32(w.d) * ((float)scale - 32.0f), lut, args, m0, g, acc);
         } else {
             float v[32];
             decode_group<TYPE>(r, row, g, v);
