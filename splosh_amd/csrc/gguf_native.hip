@@ -13,7 +13,7 @@
 //    rows (fp32); Q6_K and Q3_K instead multiply their raw codes as bf16 and apply the scales
 //    per sub-block (raw_code_dot), IQ3_S its signed codebook magnitudes (iq3s_dot), IQ4_NL and
 //    IQ4_XS their table values (iq4_dot), all as bf16 pairs into v_dot2. The wave's partial sums meet in a shuffle tree. Rows beyond
-//    MR take further passes over the weight (grid.y).
+//    MR (4, or 8 above four rows) take further passes over the weight (grid.y).
 //
 // Blocks are 2-byte aligned at best (Q8_0: 34 bytes, Q6_K: 210): a run of bytes is read as the
 // dword-aligned window that covers it, in 16-byte loads, and shifted into place per lane.
@@ -403,8 +403,21 @@ hipError_t launch_gguf_embed(int type, const uint8_t *w, int64_t rows, int64_t i
     return hipGetLastError();
 }
 
-constexpr int kGgufMR = 4;
+template <int MR>
+static void launch_gemv_mr(int type, const GgufNativeArgs &args, hipStream_t stream) {
+    const dim3 grid((unsigned)((args.rows + 3) / 4), (unsigned)((args.m + MR - 1) / MR));
+    switch (type) {
+        case 8: hipLaunchKernelGGL((gguf_gemv_kernel<8, MR>), grid, dim3(256), 0, stream, args); break;
+        case 20: hipLaunchKernelGGL((gguf_gemv_kernel<20, MR>), grid, dim3(256), 0, stream, args); break;
+        case 14: hipLaunchKernelGGL((gguf_gemv_kernel<14, MR>), grid, dim3(256), 0, stream, args); break;
+        case 11: hipLaunchKernelGGL((gguf_gemv_kernel<11, MR>), grid, dim3(256), 0, stream, args); break;
+        case 21: hipLaunchKernelGGL((gguf_gemv_kernel<21, MR>), grid, dim3(256), 0, stream, args); break;
+        default: hipLaunchKernelGGL((gguf_gemv_kernel<23, MR>), grid, dim3(256), 0, stream, args); break;
+    }
+}
 
+// Activation rows a pass over the weight: four up to four rows, eight above (one pass up to
+// eight rows instead of two).
 hipError_t launch_gguf_gemv(int type, const uint8_t *w, int64_t rows, int64_t inner, const uint16_t *a, int64_t lda,
                             void *out, int64_t ldc, int out_dtype, const void *residual, int64_t m,
                             hipStream_t stream) {
@@ -417,15 +430,10 @@ hipError_t launch_gguf_gemv(int type, const uint8_t *w, int64_t rows, int64_t in
     args.out_dtype = out_dtype;
     args.residual = residual;
     args.m = m;
-    const dim3 grid((unsigned)((rows + 3) / 4), (unsigned)((m + kGgufMR - 1) / kGgufMR));
-    switch (type) {
-        case 8: hipLaunchKernelGGL((gguf_gemv_kernel<8, kGgufMR>), grid, dim3(256), 0, stream, args); break;
-        case 20: hipLaunchKernelGGL((gguf_gemv_kernel<20, kGgufMR>), grid, dim3(256), 0, stream, args); break;
-        case 14: hipLaunchKernelGGL((gguf_gemv_kernel<14, kGgufMR>), grid, dim3(256), 0, stream, args); break;
-        case 11: hipLaunchKernelGGL((gguf_gemv_kernel<11, kGgufMR>), grid, dim3(256), 0, stream, args); break;
-        case 21: hipLaunchKernelGGL((gguf_gemv_kernel<21, kGgufMR>), grid, dim3(256), 0, stream, args); break;
-        default: hipLaunchKernelGGL((gguf_gemv_kernel<23, kGgufMR>), grid, dim3(256), 0, stream, args); break;
-    }
+    if (m > 4)
+        launch_gemv_mr<8>(type, args, stream);
+    else
+        launch_gemv_mr<4>(type, args, stream);
     return hipGetLastError();
 }
 

@@ -60,6 +60,24 @@ def test_native_gemm(rt, name, rows):
     check_close(got.cpu().numpy(), ref + res.cpu().numpy(), bf16_out=False, label=f"{name} residual rows={rows}")
 
 
+@pytest.mark.parametrize("name", list(TYPES))
+@pytest.mark.parametrize("rows", [5, 8])
+def test_five_to_eight_rows_both_routes(rt, name, rows):
+    """5-8 activation rows: the split tiled kernel with a workspace, one eight-row pass of the
+    streaming kernel without one; both against the oracle."""
+    t = TYPES[name]
+    n, k = 200, 1536
+    w, dense = _weight(rt, t, n, k, seed=rows + 3 * t)
+    a_bits = oracle.bf16_normal((rows, k), seed=rows + 11)
+    ref = oracle.gemm_a_bf16_w_f32(a_bits, dense)
+    absref = abs_gemm(a_bits, dense)
+    a = bf16_tensor(a_bits)
+    for ws in (None, torch.empty(0, dtype=torch.uint8, device="cuda")):
+        got = rt.gemm(w, a, out_dtype=torch.float32, workspace=ws)
+        check_close(got.cpu().numpy(), ref, bf16_out=False, tight=True, absref=absref,
+                    label=f"{name} rows={rows} workspace={'none' if ws is not None else 'fresh'}")
+
+
 @pytest.mark.parametrize("name", ["q6K", "q8_0"])
 def test_config0_size_sampled(rt, name):
     """K=5120 -> N=17408 at one row, 256 sampled output columns against the oracle."""
