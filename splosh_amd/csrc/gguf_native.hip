@@ -7,13 +7,13 @@
 //
 //  * gguf_dequant_kernel: one thread a 32-element group, the reference decoder's fp32 operations
 //    in its order (bit-exact).
-//  * gguf_gemv_kernel: out[m][n] = sum_k a[m][k] w[n][k] for a few rows of activations. A wave
-//    owns one weight row; its lanes take the row's 32-element groups in turn, decode each into
-//    registers exactly as the dequant kernel does and accumulate it against up to MR activation
-//    rows (fp32); Q6_K and Q3_K instead multiply their raw codes as bf16 and apply the scales
-//    per sub-block (raw_code_dot), IQ3_S its signed codebook magnitudes (iq3s_dot), IQ4_NL and
-//    IQ4_XS their table values (iq4_dot), all as bf16 pairs into v_dot2. The wave's partial sums meet in a shuffle tree. Rows beyond
-//    MR (4, or 8 above four rows) take further passes over the weight (grid.y).
+//  * gguf_gemv_kernel (Q8_0) and gguf_pairs_kernel (the others): out[m][n] = sum_k a[m][k] w[n][k]
+//    for a few rows of activations. A wave owns one weight row (gguf_pairs_kernel: two); its lanes
+//    take the rows' 32-element groups in turn. Q8_0 decodes each group into registers exactly as
+//    the dequant kernel does and accumulates it in fp32; the other formats form exact bf16 weight
+//    pairs without fp32 arithmetic (group_pairs) and sum with v_dot2. Up to MR activation rows
+//    (4, or 8 above four rows) a pass; the partial sums meet in a shuffle tree; further rows take
+//    further passes over the weight (grid.y).
 //
 // Blocks are 2-byte aligned at best (Q8_0: 34 bytes, Q6_K: 210): a run of bytes is read as the
 // dword-aligned window that covers it, in 16-byte loads, and shifted into place per lane.
@@ -87,156 +87,113 @@ __device__ __forceinline__ float gdot2(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_g, a), __builtin_bit_cast(bf16x2_g, b), c, false);
 }
 
-// A K-quant group on its raw codes (Q6_K, GgufQuant.swift:218-230; Q3_K, :238-256): the bf16
-// 0x4300 | c is exactly 128 + c for a code c < 128, so with x the activations of one 16-element
-// sub-block, sum x w = ds (sum x (128 + c) - (128 + o) sum x) for w = ds (c - o), ds as the
-// reference forms it (o = 32 for Q6_K, 4 for Q3_K). Both sums are v_dot2 on bf16 pairs (exact
-// products, fp32 sums): about three VALU an element in place of six for decoding to fp32 and
-// multiplying there. `codes[q]` holds the codes of elements 4 q .. 4 q + 3, a byte each.
-template <int MR>
-__device__ __forceinline__ void raw_code_dot(const uint32_t (&codes)[8], float ds0, float ds1, float bias,
-                                             const GgufNativeArgs &args, int64_t m0, int g, float (&acc)[MR]) {
-    uint32_t p[16];  // bf16 pairs (128 + c) of elements 2 i, 2 i + 1
+// One group of a weight row as 16 bf16 pairs for v_dot2, with the scales of its two 16-element
+// sub-blocks (equal where the format has one scale a group). Pair d holds elements 2 d and 2 d + 1,
+// except for IQ4 (elements 4 q + e and 16 + 4 q + e at pair 4 q + e; the activations are paired
+// the same way). No fp32 arithmetic touches a weight:
+//  * Q6_K, Q3_K (GgufQuant.swift:218-230, 238-256): the raw codes. The bf16 0x4300 | c is exactly
+//    128 + c for a code c < 128, so for a sub-block with scale ds and offset o (32, 4),
+//    sum x w = ds (sum x (128 + c) - (128 + o) sum x), ds as the reference forms it;
+//  * IQ3_S (:283-300): the codebook magnitudes (odd, 1..15) from an LDS table of bf16 pairs, the
+//    sign bits moved to bits 15 and 31 of each pair by one multiply and two byte permutes;
+//  * IQ4_NL, IQ4_XS (:179-185, 261-275): a code byte's two table values (integers below 128 in
+//    magnitude) as one bf16 pair from an LDS table.
+// Exact weights and fp32 sums: about three VALU an element where decoding to fp32 and multiplying
+// there took six.
+struct GroupPairs {
+    uint32_t p[16];
+    float ds0, ds1;
+};
+
+__device__ __forceinline__ void code_pairs(const uint32_t (&codes)[8], GroupPairs &gp) {
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
-        p[2 * q] = __builtin_amdgcn_perm(0x43434343u, codes[q], 0x04010400u);
-        p[2 * q + 1] = __builtin_amdgcn_perm(0x43434343u, codes[q], 0x04030402u);
+        gp.p[2 * q] = __builtin_amdgcn_perm(0x43434343u, codes[q], 0x04010400u);
+        gp.p[2 * q + 1] = __builtin_amdgcn_perm(0x43434343u, codes[q], 0x04030402u);
     }
+}
+
+template <int TYPE>
+__device__ __forceinline__ GroupPairs group_pairs(rsrc_t r, uint32_t row, int g, const uint32_t *lut) {
+    GroupPairs gp;
+    if constexpr (TYPE == 14) {
+        const GgufRaw<14> w = gguf_fetch<14>(r, row, g);
+        const int quarter = w.j & 3;
+        const float d = half_bits_to_f32(w.d);
+        gp.ds0 = d * (float)(int8_t)(w.sc & 0xFF);
+        gp.ds1 = d * (float)(int8_t)(w.sc >> 8);
+        uint32_t ql[8], qh[8], codes[8];
+        align_span(w.ql, ql);
+        align_span(w.qh, qh);
+        const int lsh = 4 * (quarter >> 1), hsh = 2 * quarter;
 #pragma unroll
-    for (int i = 0; i < MR; ++i) {
-        if (m0 + i >= args.m) break;
-        const u32x4 *ap = (const u32x4 *)(args.a + (m0 + i) * args.lda + (int64_t)g * 32);
-        float s[2] = {0.0f, 0.0f}, t[2] = {0.0f, 0.0f};
+        for (int q = 0; q < 8; ++q) codes[q] = ((ql[q] >> lsh) & 0x0F0F0F0Fu) | (((qh[q] >> hsh) & 0x03030303u) << 4);
+        code_pairs(codes, gp);
+    } else if constexpr (TYPE == 11) {
+        const GgufRaw<11> w = gguf_fetch<11>(r, row, g);
+        const int j = w.j, shift = 2 * (j & 3), word = j >> 1;
+        const float d = half_bits_to_f32(w.d);
+        const uint32_t lows = w.lows >> (4 * (word >> 1)), highs = w.highs >> (2 * word);
+        gp.ds0 = d * ((float)((lows & 0xF) | ((highs & 3) << 4)) - 32.0f);
+        gp.ds1 = d * ((float)(((lows >> 8) & 0xF) | (((highs >> 8) & 3) << 4)) - 32.0f);
+        uint32_t hm[8], qs[8], codes[8];
+        align_span(w.hm, hm);
+        align_span(w.qs, qs);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const u32x4 x = ap[q];
+        for (int q = 0; q < 8; ++q) codes[q] = ((qs[q] >> shift) & 0x03030303u) | (((hm[q] >> j) & 0x01010101u) << 2);
+        code_pairs(codes, gp);
+    } else if constexpr (TYPE == 21) {
+        const GgufRaw<21> w = gguf_fetch<21>(r, row, g);
+        const int j = w.j;
+        const float d = half_bits_to_f32(w.d);
+        const uint32_t scale = (w.scale >> (8 * ((j >> 1) & 1) + 4 * (j & 1))) & 15;
+        gp.ds0 = gp.ds1 = d * (1.0f + 2.0f * (float)scale);
+        const uint32_t ninth = (w.ninth >> (8 * (j & 1))) & 0xFF;
+        uint32_t cb[2], sg[1];
+        align_span(w.cb, cb);
+        align_span(w.sg, sg);
+        const uint2 *tab = (const uint2 *)lut;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                s[q >> 1] = gdot2(x[e], p[4 * q + e], s[q >> 1]);
-                t[q >> 1] = gdot2(x[e], 0x3F803F80u, t[q >> 1]);
-            }
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t code = ((cb[k >> 2] >> (8 * (k & 3))) & 0xFF) | (((ninth >> k) & 1) << 8);
+            const uint2 m = tab[code];
+            // Sign bit t of elements 4 k + t to bit 7 of byte t, then to bits 15 and 31 of the pairs.
+            const uint32_t spread = ((((sg[0] >> (4 * k)) & 0xFu) * 0x00204081u) & 0x01010101u) << 7;
+            gp.p[2 * k] = m.x ^ __builtin_amdgcn_perm(0u, spread, 0x010C000Cu);
+            gp.p[2 * k + 1] = m.y ^ __builtin_amdgcn_perm(0u, spread, 0x030C020Cu);
         }
-        acc[i] = __builtin_fmaf(ds0, __builtin_fmaf(-bias, t[0], s[0]), acc[i]);
-        acc[i] = __builtin_fmaf(ds1, __builtin_fmaf(-bias, t[1], s[1]), acc[i]);
-    }
-}
-
-template <int MR>
-__device__ __forceinline__ void q6k_dot(const GgufRaw<14> &w, const GgufNativeArgs &args, int64_t m0, int g,
-                                        float (&acc)[MR]) {
-    const int quarter = w.j & 3;
-    const float d = half_bits_to_f32(w.d);
-    const float ds0 = d * (float)(int8_t)(w.sc & 0xFF), ds1 = d * (float)(int8_t)(w.sc >> 8);
-    uint32_t ql[8], qh[8], codes[8];
-    align_span(w.ql, ql);
-    align_span(w.qh, qh);
-    const int lsh = 4 * (quarter >> 1), hsh = 2 * quarter;
-#pragma unroll
-    for (int q = 0; q < 8; ++q) codes[q] = ((ql[q] >> lsh) & 0x0F0F0F0Fu) | (((qh[q] >> hsh) & 0x03030303u) << 4);
-    raw_code_dot<MR>(codes, ds0, ds1, 160.0f, args, m0, g, acc);
-}
-
-template <int MR>
-__device__ __forceinline__ void q3k_dot(const GgufRaw<11> &w, const GgufNativeArgs &args, int64_t m0, int g,
-                                        float (&acc)[MR]) {
-    const int j = w.j, shift = 2 * (j & 3), word = j >> 1;
-    const float d = half_bits_to_f32(w.d);
-    const uint32_t lows = w.lows >> (4 * (word >> 1)), highs = w.highs >> (2 * word);
-    const float s0 = (float)((lows & 0xF) | ((highs & 3) << 4)) - 32.0f;
-    const float s1 = (float)(((lows >> 8) & 0xF) | (((highs >> 8) & 3) << 4)) - 32.0f;
-    uint32_t hm[8], qs[8], codes[8];
-    align_span(w.hm, hm);
-    align_span(w.qs, qs);
-#pragma unroll
-    for (int q = 0; q < 8; ++q) codes[q] = ((qs[q] >> shift) & 0x03030303u) | (((hm[q] >> j) & 0x01010101u) << 2);
-    raw_code_dot<MR>(codes, d * s0, d * s1, 132.0f, args, m0, g, acc);
-}
-
-// IQ3_S group g (GgufQuant.swift:283-300) on bf16 weights formed without fp32 arithmetic: `tab`
-// holds each codebook entry's four magnitudes (odd, 1..15: exact in bf16) as two bf16 pairs, the
-// sign bits are spread to bits 15 and 31 of each pair by one multiply and two byte permutes, and
-// the group's d (1 + 2 scale) multiplies the v_dot2 sum once.
-template <int MR>
-__device__ __forceinline__ void iq3s_dot(const GgufRaw<21> &w, const uint2 *tab, const GgufNativeArgs &args,
-                                         int64_t m0, int g, float (&acc)[MR]) {
-    const int j = w.j;
-    const float d = half_bits_to_f32(w.d);
-    const uint32_t scale = (w.scale >> (8 * ((j >> 1) & 1) + 4 * (j & 1))) & 15;
-    const float weight = d * (1.0f + 2.0f * (float)scale);
-    const uint32_t ninth = (w.ninth >> (8 * (j & 1))) & 0xFF;
-    uint32_t cb[2], sg[1], p[16];
-    align_span(w.cb, cb);
-    align_span(w.sg, sg);
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const uint32_t code = ((cb[k >> 2] >> (8 * (k & 3))) & 0xFF) | (((ninth >> k) & 1) << 8);
-        const uint2 m = tab[code];
-        // Sign bit t of elements 4 k + t to bit 7 of byte t, then to bits 15 and 31 of the pairs.
-        const uint32_t spread = ((((sg[0] >> (4 * k)) & 0xFu) * 0x00204081u) & 0x01010101u) << 7;
-        p[2 * k] = m.x ^ __builtin_amdgcn_perm(0u, spread, 0x010C000Cu);
-        p[2 * k + 1] = m.y ^ __builtin_amdgcn_perm(0u, spread, 0x030C020Cu);
-    }
-#pragma unroll
-    for (int i = 0; i < MR; ++i) {
-        if (m0 + i >= args.m) break;
-        const u32x4 *ap = (const u32x4 *)(args.a + (m0 + i) * args.lda + (int64_t)g * 32);
-        float s = 0.0f;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const u32x4 x = ap[q];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) s = gdot2(x[e], p[4 * q + e], s);
+    } else {
+        uint32_t h[4];
+        if constexpr (TYPE == 20) {
+            const GgufRaw<20> w = gguf_fetch<20>(r, row, g);
+            align_span(w.codes, h);
+            gp.ds0 = gp.ds1 = half_bits_to_f32(w.d);
+        } else {
+            const GgufRaw<23> w = gguf_fetch<23>(r, row, g);
+            const int j = w.j;
+            const uint32_t low = (w.lowb >> (8 * ((j >> 1) & 1) + 4 * (j & 1))) & 15;
+            const uint32_t scale = low | (((w.high >> (2 * j)) & 3) << 4);
+            h[0] = w.q[0], h[1] = w.q[1], h[2] = w.q[2], h[3] = w.q[3];
+            gp.ds0 = gp.ds1 = half_bits_to_f32(w.d) * ((float)scale - 32.0f);
         }
-        acc[i] = __builtin_fmaf(weight, s, acc[i]);
-    }
-}
-
-// IQ4_NL / IQ4_XS group (GgufQuant.swift:179-185, 261-275): `tab[b]` holds the table values of
-// both nibbles of a code byte b as a bf16 pair (the values are integers below 128 in magnitude:
-// exact), for elements 4 q + e (low nibble) and 16 + 4 q + e (high nibble) of byte e of word q;
-// one byte permute pairs the activations the same way, and the group's scale multiplies the
-// v_dot2 sum once.
-template <int MR>
-__device__ __forceinline__ void iq4_dot(const uint32_t (&h)[4], float scale, const uint32_t *tab,
-                                        const GgufNativeArgs &args, int64_t m0, int g, float (&acc)[MR]) {
-    uint32_t w[16];
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) w[4 * q + e] = tab[(h[q] >> (8 * e)) & 0xFFu];
-#pragma unroll
-    for (int i = 0; i < MR; ++i) {
-        if (m0 + i >= args.m) break;
-        const u32x4 *ap = (const u32x4 *)(args.a + (m0 + i) * args.lda + (int64_t)g * 32);
-        uint32_t x[16];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const u32x4 v = ap[q];
-            x[4 * q] = v[0], x[4 * q + 1] = v[1], x[4 * q + 2] = v[2], x[4 * q + 3] = v[3];
-        }
-        float s = 0.0f;
 #pragma unroll
         for (int q = 0; q < 4; ++q)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                // Elements 4 q + e and 16 + 4 q + e: the low (e even) or high halves of activation
-                // dwords 2 q + e / 2 and 8 + 2 q + e / 2.
-                const int dw = 2 * q + (e >> 1);
-                const uint32_t pair =
-                    __builtin_amdgcn_perm(x[8 + dw], x[dw], (e & 1) ? 0x07060302u : 0x05040100u);
-                s = gdot2(pair, w[4 * q + e], s);
-            }
-        acc[i] = __builtin_fmaf(scale, s, acc[i]);
+            for (int e = 0; e < 4; ++e) gp.p[4 * q + e] = lut[(h[q] >> (8 * e)) & 0xFFu];
     }
+    return gp;
 }
 
-template <int TYPE, int MR>
-__global__ void __launch_bounds__(256) gguf_gemv_kernel(GgufNativeArgs args) {
+// The formats above: R weight rows a wave (a workgroup's four waves take 4 R consecutive rows), so
+// each activation row is loaded, paired and summed once for R weight rows; its lanes take the
+// rows' 32-element groups in turn.
+template <int TYPE, int MR, int R>
+__global__ void __launch_bounds__(256) gguf_pairs_kernel(GgufNativeArgs args) {
+    constexpr bool kIq4 = TYPE == 20 || TYPE == 23;
+    constexpr float kBias = TYPE == 14 ? 160.0f : TYPE == 11 ? 132.0f : 0.0f;
     // Lookup tables in LDS, built before any wave leaves: IQ3_S's codebook as bf16 magnitude
     // pairs (512 x 8 bytes), the IQ4 values of both nibbles of a byte as a bf16 pair (256 x 4).
-    constexpr bool kIq4 = TYPE == 20 || TYPE == 23;
     __shared__ __align__(8) uint32_t lut[TYPE == 21 ? 1024 : kIq4 ? 256 : 1];
-    uint2 *iq3s_tab = (uint2 *)lut;
     if constexpr (kIq4) {
         const uint32_t kv[4] = {kIq4Tab0, kIq4Tab1, kIq4Tab2, kIq4Tab3};
         auto bf = [&](uint32_t i) {
@@ -252,10 +209,107 @@ __global__ void __launch_bounds__(256) gguf_gemv_kernel(GgufNativeArgs args) {
 #pragma unroll
             for (int t = 0; t < 4; ++t)
                 h[t] = __builtin_bit_cast(uint32_t, (float)(2u * ((packed >> (3 * t)) & 7u) + 1u)) >> 16;
-            iq3s_tab[c] = uint2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
+            lut[2 * c] = h[0] | (h[1] << 16);
+            lut[2 * c + 1] = h[2] | (h[3] << 16);
         }
         __syncthreads();
     }
+    const int lane = threadIdx.x & 63;
+    const int64_t n0 =
+        ((int64_t)xcd_block(blockIdx.x, gridDim.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * R;
+    if (n0 >= args.rows) return;
+    const int64_t m0 = (int64_t)blockIdx.y * MR;
+    const int groups = (int)(args.inner / 32);
+    const rsrc_t rs = make_rsrc(args.w, args.w_bytes);
+    uint32_t row[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) row[r] = (uint32_t)((n0 + r < args.rows ? n0 + r : args.rows - 1) * args.row_bytes);
+    float acc[R][MR];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int i = 0; i < MR; ++i) acc[r][i] = 0.0f;
+    for (int g = lane; g < groups; g += 64) {
+        GroupPairs gp[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) gp[r] = group_pairs<TYPE>(rs, row[r], g, lut);
+#pragma unroll
+        for (int i = 0; i < MR; ++i) {
+            if (m0 + i >= args.m) break;
+            const u32x4 *ap = (const u32x4 *)(args.a + (m0 + i) * args.lda + (int64_t)g * 32);
+            uint32_t x[16];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const u32x4 v = ap[q];
+                x[4 * q] = v[0], x[4 * q + 1] = v[1], x[4 * q + 2] = v[2], x[4 * q + 3] = v[3];
+            }
+            if constexpr (kIq4) {
+                // Elements 4 q + e and 16 + 4 q + e: the low (e even) or high halves of dwords
+                // 2 q + e / 2 and 8 + 2 q + e / 2.
+                uint32_t y[16];
+#pragma unroll
+                for (int d = 0; d < 16; ++d) {
+                    const int dw = 2 * (d >> 2) + ((d & 3) >> 1);
+                    y[d] = __builtin_amdgcn_perm(x[8 + dw], x[dw], (d & 1) ? 0x07060302u : 0x05040100u);
+                }
+#pragma unroll
+                for (int d = 0; d < 16; ++d) x[d] = y[d];
+            }
+            float t0 = 0.0f, t1 = 0.0f;
+            if constexpr (kBias != 0.0f) {
+#pragma unroll
+                for (int d = 0; d < 8; ++d) {
+                    t0 = gdot2(x[d], 0x3F803F80u, t0);
+                    t1 = gdot2(x[8 + d], 0x3F803F80u, t1);
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+                for (int d = 0; d < 8; ++d) {
+                    s0 = gdot2(x[d], gp[r].p[d], s0);
+                    s1 = gdot2(x[8 + d], gp[r].p[8 + d], s1);
+                }
+                if constexpr (kBias != 0.0f) {
+                    s0 = __builtin_fmaf(-kBias, t0, s0);
+                    s1 = __builtin_fmaf(-kBias, t1, s1);
+                }
+                acc[r][i] = __builtin_fmaf(gp[r].ds0, s0, acc[r][i]);
+                acc[r][i] = __builtin_fmaf(gp[r].ds1, s1, acc[r][i]);
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int i = 0; i < MR; ++i) {
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) acc[r][i] += __shfl_xor(acc[r][i], o, 64);
+        }
+    if (lane != 0) return;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        if (n0 + r >= args.rows) break;
+#pragma unroll
+        for (int i = 0; i < MR; ++i) {
+            if (m0 + i >= args.m) break;
+            const int64_t index = (m0 + i) * args.ldc + n0 + r;
+            float value = acc[r][i];
+            if (args.out_dtype == SPLOSH_F32) {
+                if (args.residual) value += ((const float *)args.residual)[index];
+                ((float *)args.out)[index] = value;
+            } else {
+                if (args.residual) value += bf16_bits_to_f32(((const uint16_t *)args.residual)[index]);
+                ((uint16_t *)args.out)[index] = f32_to_bf16(value);
+            }
+        }
+    }
+}
+
+// Q8_0: the group decoded to fp32 in the reference's order, dotted in fp32.
+template <int TYPE, int MR>
+__global__ void __launch_bounds__(256) gguf_gemv_kernel(GgufNativeArgs args) {
     const int lane = threadIdx.x & 63;
     const int64_t n = (int64_t)xcd_block(blockIdx.x, gridDim.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (n >= args.rows) return;
@@ -298,25 +352,7 @@ __global__ void __launch_bounds__(256) gguf_gemv_kernel(GgufNativeArgs args) {
         accumulate(g + 64, v1);
     }
     for (; g < groups; g += 64) {
-        if constexpr (TYPE == 14) {
-            q6k_dot<MR>(gguf_fetch<14>(r, row, g), args, m0, g, acc);
-        } else if constexpr (TYPE == 11) {
-            q3k_dot<MR>(gguf_fetch<11>(r, row, g), args, m0, g, acc);
-        } else if constexpr (TYPE == 21) {
-            iq3s_dot<MR>(gguf_fetch<21>(r, row, g), iq3s_tab, args, m0, g, acc);
-        } else if constexpr (TYPE == 20) {
-            const GgufRaw<20> w = gguf_fetch<20>(r, row, g);
-            uint32_t h[4];
-            align_span(w.codes, h);
-            iq4_dot<MR>(h, half_bits_to_f32(w.d), lut, args, m0, g, acc);
-        } else if constexpr (TYPE == 23) {
-            const GgufRaw<23> w = gguf_fetch<23>(r, row, g);
-            const int j = w.j;
-            const uint32_t low = (w.lowb >> (8 * ((j >> 1) & 1) + 4 * (j & 1))) & 15;
-            const uint32_t scale = low | (((w.high >> (2 * j)) & 3) << 4);
-            const uint32_t h[4] = {w.q[0], w.q[1], w.q[2], w.q[3]};
-            iq4_dot<MR>(h, half_bits_to_f32(w.d) * ((float)scale - 32.0f), lut, args, m0, g, acc);
-        } else {
+        {
             float v[32];
             decode_group<TYPE>(r, row, g, v);
             accumulate(g, v);
@@ -403,16 +439,25 @@ hipError_t launch_gguf_embed(int type, const uint8_t *w, int64_t rows, int64_t i
     return hipGetLastError();
 }
 
+#ifndef GGUF_PAIRS_R
+#define GGUF_PAIRS_R 2
+#endif
+constexpr int kPairsRows = GGUF_PAIRS_R;  // weight rows a wave of gguf_pairs_kernel
+
 template <int MR>
 static void launch_gemv_mr(int type, const GgufNativeArgs &args, hipStream_t stream) {
-    const dim3 grid((unsigned)((args.rows + 3) / 4), (unsigned)((args.m + MR - 1) / MR));
+    constexpr int R = kPairsRows;
+    const dim3 grid((unsigned)((args.rows + 4 * R - 1) / (4 * R)), (unsigned)((args.m + MR - 1) / MR));
     switch (type) {
-        case 8: hipLaunchKernelGGL((gguf_gemv_kernel<8, MR>), grid, dim3(256), 0, stream, args); break;
-        case 20: hipLaunchKernelGGL((gguf_gemv_kernel<20, MR>), grid, dim3(256), 0, stream, args); break;
-        case 14: hipLaunchKernelGGL((gguf_gemv_kernel<14, MR>), grid, dim3(256), 0, stream, args); break;
-        case 11: hipLaunchKernelGGL((gguf_gemv_kernel<11, MR>), grid, dim3(256), 0, stream, args); break;
-        case 21: hipLaunchKernelGGL((gguf_gemv_kernel<21, MR>), grid, dim3(256), 0, stream, args); break;
-        default: hipLaunchKernelGGL((gguf_gemv_kernel<23, MR>), grid, dim3(256), 0, stream, args); break;
+        case 8:
+            hipLaunchKernelGGL((gguf_gemv_kernel<8, MR>), dim3((unsigned)((args.rows + 3) / 4), grid.y), dim3(256), 0,
+                               stream, args);
+            break;
+        case 20: hipLaunchKernelGGL((gguf_pairs_kernel<20, MR, R>), grid, dim3(256), 0, stream, args); break;
+        case 14: hipLaunchKernelGGL((gguf_pairs_kernel<14, MR, R>), grid, dim3(256), 0, stream, args); break;
+        case 11: hipLaunchKernelGGL((gguf_pairs_kernel<11, MR, R>), grid, dim3(256), 0, stream, args); break;
+        case 21: hipLaunchKernelGGL((gguf_pairs_kernel<21, MR, R>), grid, dim3(256), 0, stream, args); break;
+        default: hipLaunchKernelGGL((gguf_pairs_kernel<23, MR, R>), grid, dim3(256), 0, stream, args); break;
     }
 }
 
