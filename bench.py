@@ -45,9 +45,9 @@ MEASURED_TRAFFIC = {
     ("q5k2048", "q5k"): 347729.4 * 2 * 1024 + 98304.0 * 1024,  # prefill_kernel<Q5Stage<true>>
     ("q6k2048", "gguf"): 366940.1 * 2 * 1024 + 110080.0 * 1024,  # prefill_kernel<GgufStage<14>>
     ("q6k64", "gguf"): (51389.6 + 6413.1) * 2 * 1024 + (25600.0 + 643.4) * 1024,  # gguf_tile_kernel<14, 1, 2, true, 2> + gguf_tile_finish<1, 2>
-    ("q6k1", "gguf"): 36127.0 * 2 * 1024 + 10.0 * 1024,  # gguf_gemv_kernel<14, 4>
-    ("q3k1", "gguf"): 18885.1 * 2 * 1024 + 10.0 * 1024,  # gguf_gemv_kernel<11, 4>
-    ("iq3s1", "gguf"): 18881.6 * 2 * 1024 + 10.0 * 1024,  # gguf_gemv_kernel<21, 4>
+    ("q6k1", "gguf"): 36191.3 * 2 * 1024 + 10.0 * 1024,  # gguf_pairs_kernel<14, 4, 2>
+    ("q3k1", "gguf"): 19009.8 * 2 * 1024 + 10.0 * 1024,  # gguf_pairs_kernel<11, 4, 2>
+    ("iq3s1", "gguf"): 19068.8 * 2 * 1024 + 10.0 * 1024,  # gguf_pairs_kernel<21, 4, 2>
     ("q80_1", "gguf"): 46715.8 * 2 * 1024 + 10.0 * 1024,  # gguf_gemv_kernel<8, 4>
     ("stream50", "read"): 24680.2 * 2 * 1024 + 64.0 * 1024,  # stream_read_kernel
     ("layerset", "mlp_in"): 55934.6 * 2 * 1024 + 9871.0 * 1024,  # mma_kernel<Q4Format<2, true, 2, 4, 3>, 2, 2, 4, 3>
