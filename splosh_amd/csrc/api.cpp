@@ -622,11 +622,13 @@ int splosh_gguf_gemm(int gguf_type, const uint8_t *native, int64_t rows, int64_t
     if (lda % 8 != 0 || !aligned(a, 16))
         return fail(SPLOSH_ERR_UNSUPPORTED, "GGUF native kernel needs lda % 8 == 0 and 16-byte aligned activations");
     // From kGgufPrefillRows rows the 256 x 256 prefill kernel (each weight group decoded once per
-    // 256 rows); above eight rows, or above four with a workspace for its K split, the tiled kernel
-    // (once per 64 or 128 rows); otherwise one pass of the streaming kernel (a second above eight).
-    // Measured at K17408 -> N5120: the streaming kernel's time grows by 8-10 us an activation row
-    // (45-58 us at four rows, 56-70 at five), the split tiled kernel's is flat at 47-63 us up to
-    // 16 rows. (A development override of the prefill threshold, read once.)
+    // 256 rows); above eight rows, or above the format's streaming limit with a workspace for its K
+    // split, the tiled kernel (once per 64 or 128 rows); otherwise one pass of the streaming
+    // kernel (a second above eight). Measured at K17408 -> N5120: the split tiled kernel's time is
+    // flat up to 16 rows (Q8_0, Q6_K, Q3_K 55-58 us, IQ4 46-48, IQ3_S 76), the streaming kernel's
+    // grows with the rows (at five and six: Q8_0 70 / 79, Q6_K 47 / 52, Q3_K 48 / 54, IQ4_NL
+    // 44 / 48, IQ4_XS 43 / 48, IQ3_S 48 / 54, 64 at eight). (A development override of the
+    // prefill threshold, read once.)
     static const int64_t prefill_rows = [] {
         const char *e = getenv("SPLOSH_GGUF_PREFILL_ROWS");
         return e ? (int64_t)atoll(e) : kGgufPrefillRows;
@@ -638,9 +640,10 @@ int splosh_gguf_gemm(int gguf_type, const uint8_t *native, int64_t rows, int64_t
                                                       residual, m, workspace, stream),
                           "gguf prefill launch");
     }
+    const int64_t stream_rows = gguf_type == 8 ? 4 : gguf_type == 21 ? 8 : (gguf_type == 20 || gguf_type == 23) ? 5 : 6;
     const bool split_room = workspace && workspace_bytes >= splosh::gguf_tile_workspace_bytes(m, rows, inner) &&
                             splosh::gguf_tile_workspace_bytes(m, rows, inner) > 0;
-    if ((m > 8 || (m > 4 && split_room)) && splosh::gguf_tile_fits(m, rows, inner, lda))
+    if ((m > 8 || (m > stream_rows && split_room)) && splosh::gguf_tile_fits(m, rows, inner, lda))
         return hip_status(splosh::launch_gguf_tile(gguf_type, native, nullptr, nullptr, rows, inner, a, lda, out, ldc,
                                                    out_dtype, residual, m, workspace, workspace_bytes, stream),
                           "gguf tile launch");

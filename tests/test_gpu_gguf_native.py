@@ -61,10 +61,11 @@ def test_native_gemm(rt, name, rows):
 
 
 @pytest.mark.parametrize("name", list(TYPES))
-@pytest.mark.parametrize("rows", [5, 8])
+@pytest.mark.parametrize("rows", [5, 7, 8])
 def test_five_to_eight_rows_both_routes(rt, name, rows):
-    """5-8 activation rows: the split tiled kernel with a workspace, one eight-row pass of the
-    streaming kernel without one; both against the oracle."""
+    """5-8 activation rows: with a workspace AUTO's choice (the split tiled kernel above the
+    format's streaming limit, Q8_0 4 .. IQ3_S 8), without one a single eight-row pass of the
+    streaming kernel; both against the oracle."""
     t = TYPES[name]
     n, k = 200, 1536
     w, dense = _weight(rt, t, n, k, seed=rows + 3 * t)
