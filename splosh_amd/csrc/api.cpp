@@ -626,7 +626,7 @@ int splosh_gguf_gemm(int gguf_type, const uint8_t *native, int64_t rows, int64_t
     // split, the tiled kernel (once per 64 or 128 rows); otherwise one pass of the streaming
     // kernel (a second above eight). Measured at K17408 -> N5120: the split tiled kernel's time is
     // flat up to 16 rows (Q8_0, Q6_K, Q3_K 55-58 us, IQ4 46-48, IQ3_S 76), the streaming kernel's
-    // grows with the rows (at five and six: Q8_0 70 / 79, Q6_K 47 / 52, Q3_K 48 / 54, IQ4_NL
+    // grows with the rows (at five and six: Q8_0 51 / -, Q6_K 47 / 52, Q3_K 48 / 54, IQ4_NL
     // 44 / 48, IQ4_XS 43 / 48, IQ3_S 48 / 54, 64 at eight). (A development override of the
     // prefill threshold, read once.)
     static const int64_t prefill_rows = [] {
@@ -640,7 +640,7 @@ int splosh_gguf_gemm(int gguf_type, const uint8_t *native, int64_t rows, int64_t
                                                       residual, m, workspace, stream),
                           "gguf prefill launch");
     }
-    const int64_t stream_rows = gguf_type == 8 ? 4 : gguf_type == 21 ? 8 : (gguf_type == 20 || gguf_type == 23) ? 5 : 6;
+    const int64_t stream_rows = gguf_type == 21 ? 8 : (gguf_type == 14 || gguf_type == 11) ? 6 : 5;
     const bool split_room = workspace && workspace_bytes >= splosh::gguf_tile_workspace_bytes(m, rows, inner) &&
                             splosh::gguf_tile_workspace_bytes(m, rows, inner) > 0;
     if ((m > 8 || (m > stream_rows && split_room)) && splosh::gguf_tile_fits(m, rows, inner, lda))

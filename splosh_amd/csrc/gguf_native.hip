@@ -7,7 +7,7 @@
 //
 //  * gguf_dequant_kernel: one thread a 32-element group, the reference decoder's fp32 operations
 //    in its order (bit-exact).
-//  * gguf_gemv_kernel (Q8_0) and gguf_pairs_kernel (the others): out[m][n] = sum_k a[m][k] w[n][k]
+//  * gguf_gemv_kernel (Q8_0 at one row) and gguf_pairs_kernel (the rest): out[m][n] = sum_k a[m][k] w[n][k]
 //    for a few rows of activations. A wave owns one weight row (gguf_pairs_kernel: two); its lanes
 //    take the rows' 32-element groups in turn. Q8_0 decodes each group into registers exactly as
 //    the dequant kernel does and accumulates it in fp32; the other formats form exact bf16 weight
@@ -116,7 +116,15 @@ __device__ __forceinline__ void code_pairs(const uint32_t (&codes)[8], GroupPair
 template <int TYPE>
 __device__ __forceinline__ GroupPairs group_pairs(rsrc_t r, uint32_t row, int g, const uint32_t *lut) {
     GroupPairs gp;
-    if constexpr (TYPE == 14) {
+    if constexpr (TYPE == 8) {
+        const GgufRaw<8> w = gguf_fetch<8>(r, row, g);
+        uint32_t h[8];
+        align_span(w.codes, h);
+        gp.ds0 = gp.ds1 = half_bits_to_f32(w.d);
+#pragma unroll
+        for (int d = 0; d < 16; ++d)
+            gp.p[d] = f32x2_to_bf16x2((float)(int8_t)byte_of(h, 2 * d), (float)(int8_t)byte_of(h, 2 * d + 1));
+    } else if constexpr (TYPE == 14) {
         const GgufRaw<14> w = gguf_fetch<14>(r, row, g);
         const int quarter = w.j & 3;
         const float d = half_bits_to_f32(w.d);
@@ -450,8 +458,16 @@ static void launch_gemv_mr(int type, const GgufNativeArgs &args, hipStream_t str
     const dim3 grid((unsigned)((args.rows + 4 * R - 1) / (4 * R)), (unsigned)((args.m + MR - 1) / MR));
     switch (type) {
         case 8:
-            hipLaunchKernelGGL((gguf_gemv_kernel<8, MR>), dim3((unsigned)((args.rows + 3) / 4), grid.y), dim3(256), 0,
-                               stream, args);
+            // One activation row: the fp32 decode measured 1-2 us faster (23.7 against 25.3 at
+            // K17408 -> N5120); from two rows the pairs share the activations (four: 56 -> 43 us).
+            if constexpr (MR == 4) {
+                if (args.m == 1) {
+                    hipLaunchKernelGGL((gguf_gemv_kernel<8, MR>), dim3((unsigned)((args.rows + 3) / 4), grid.y),
+                                       dim3(256), 0, stream, args);
+                    break;
+                }
+            }
+            hipLaunchKernelGGL((gguf_pairs_kernel<8, MR, R>), grid, dim3(256), 0, stream, args);
             break;
         case 20: hipLaunchKernelGGL((gguf_pairs_kernel<20, MR, R>), grid, dim3(256), 0, stream, args); break;
         case 14: hipLaunchKernelGGL((gguf_pairs_kernel<14, MR, R>), grid, dim3(256), 0, stream, args); break;
