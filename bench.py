@@ -204,28 +204,36 @@ def build_workload(name, rt, torch, gen, kernel):
         return launches, sum(kb.values()), sum(kf.values()), kb, cfg, kf
     if name.startswith("stream"):
         # The practical ceiling of one launch: a plain streaming read of as many bytes as the named
-        # decode weight (stream50: config 0's 50,180,096 bytes; stream715: the lm_head's), on 2048
-        # workgroups (the best of 256..4096 measured; SPLOSH_PROBE_GRID overrides), rotated over copies. Not part of the path: the probe kernel
-        # is exported by the library for this measurement only.
+        # decode weight (stream50: config 0's 50,180,096 bytes; stream715: the lm_head's), rotated
+        # over copies. Not part of the path: the probes live in libsplosh_probe.so, built beside the
+        # product library and loaded only here. SPLOSH_PROBE_SHAPE picks the probe: 0 = contiguous
+        # slices on SPLOSH_PROBE_GRID workgroups of 256 (default 2048, the best of 256..4096), 1 / 2 =
+        # persistent workgroups of 1024 (default two a CU) with 8 / 16 loads in flight a thread,
+        # 3 = a device-to-device copy of the buffer (hipMemcpyAsync through torch; reads and writes).
         import ctypes
         from splosh_amd import _lib
-        lib = _lib.lib()
+        lib = ctypes.CDLL(str(Path(_lib.PKG) / "libsplosh_probe.so"))
         lib.splosh_probe_stream_read.restype = ctypes.c_int
         lib.splosh_probe_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int,
-                                                 ctypes.c_void_p]
+                                                 ctypes.c_int, ctypes.c_void_p]
         b = {"stream50": q4_bytes(17408, 5120), "stream715": q4_bytes(248320, 5120)}[name]
         ncopy = copies_for(b)
         bufs = [torch.randint(0, 255, (b,), dtype=torch.uint8, device="cuda", generator=gen) for _ in range(ncopy)]
-        grid = int(os.environ.get("SPLOSH_PROBE_GRID", "2048"))
-        sink = torch.zeros(4 * grid, dtype=torch.int32, device="cuda")
+        shape = int(os.environ.get("SPLOSH_PROBE_SHAPE", "0"))
+        cus = torch.cuda.get_device_properties(0).multi_processor_count
+        grid = int(os.environ.get("SPLOSH_PROBE_GRID", "2048" if shape == 0 else str(2 * cus)))
+        sink = torch.zeros(16 * grid, dtype=torch.int32, device="cuda")
+        dst = torch.empty(b, dtype=torch.uint8, device="cuda") if shape == 3 else None
 
         def launches(i):
             buf = bufs[i % ncopy]
+            if shape == 3:
+                return [("read", lambda: dst.copy_(buf))]
             return [("read", lambda: _lib.check(lib.splosh_probe_stream_read(
-                buf.data_ptr(), b, sink.data_ptr(), grid, torch.cuda.current_stream().cuda_stream)))]
+                buf.data_ptr(), b, sink.data_ptr(), grid, shape, torch.cuda.current_stream().cuda_stream)))]
 
-        cfg = {"workload": f"streaming read of {b} bytes a launch (probe, not the path)", "rows": 0,
-               "format": "bytes", "weight_copies": ncopy}
+        cfg = {"workload": f"streaming read of {b} bytes a launch (probe {shape}, grid {grid}, not the path)",
+               "rows": 0, "format": "bytes", "weight_copies": ncopy}
         return launches, b, 0, {"read": b}, cfg, {"read": 0}
     if name == "gemm2048":
         # The practical ceiling of the matrix cores on config 2's two shapes: the vendor bf16 GEMM
@@ -500,18 +508,32 @@ def main():
                             fn()
             return g
 
-        def replay_ms(g):
-            g.replay()  # warm replay
+        def replay_ms(kinds):
+            # Two captures of the same K steps: the warm one and the timed one are enqueued back to
+            # back with no host sync between them, so the timed graph is submitted while the GPU
+            # still runs the warm one (a second launch of the same graph would wait on the host for
+            # the first to finish, and its submission would land in the timed region), and the start
+            # event is reached only when the GPU is done with the warm steps: the timed region holds
+            # the K steps' GPU time, whatever K is.
+            # The warm replays also cover about 30 ms, so that the timed steps run at the clock the
+            # part settles at under this load, not during its ramp after the idle capture.
+            g_warm, g_timed = capture(kinds), capture(kinds)
             torch.cuda.synchronize()
-            start, end = timer.event(), None
-            g.replay()
+            t0 = timer.event()
+            g_warm.replay()
+            t1 = timer.event()
+            torch.cuda.synchronize()
+            reps = max(1, min(1000, int(30.0 / max(t0.elapsed_time(t1), 1e-3)) + 1))
+            for _ in range(reps):
+                g_warm.replay()
+            start = timer.event()
+            g_timed.replay()
             end = timer.event()
             torch.cuda.synchronize()
             return start.elapsed_time(end)
 
-        g_all = capture(set(names))
-        total_ms = replay_ms(g_all)
-        per_kernel = {nm: replay_ms(capture({nm})) / args.steps for nm in names}
+        total_ms = replay_ms(set(names))
+        per_kernel = {nm: replay_ms({nm}) / args.steps for nm in names}
     ms_per_step = total_ms / args.steps
 
     dominant = max(per_kernel, key=per_kernel.get)

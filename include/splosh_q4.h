@@ -180,9 +180,10 @@ int splosh_q4_gemm_emit(const splosh_q4_weight *w, const uint16_t *a, int64_t ld
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). It takes no
  * workspace and allocates nothing: the kernels use a static scratch array in the library's device
  * memory (8 MiB + 16 KiB per GPU, held until the process ends), enough for the M <= 64 kernel's
- * split-K partials on one weight; a call that would need more returns
- * SPLOSH_ERR_WORKSPACE_TOO_SMALL. All calls on one GPU share that scratch: calls that overlap on
- * one GPU (different streams, or host threads without ordering) race and give wrong results. */
+ * split-K partials on one weight; a call whose split partials would need more runs unsplit (the
+ * same results, one workgroup a column band). All calls on one GPU share that scratch: calls that
+ * overlap on one GPU (different streams, or host threads without ordering) race and give wrong
+ * results. */
 int splosh_q4_gemm_noalloc(const splosh_q4_weight *w, const uint16_t *a, int64_t lda, void *out, int64_t ldc,
                            int out_dtype, const void *residual, int64_t rows, int kernel, hipStream_t stream);
 

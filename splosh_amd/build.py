@@ -2,7 +2,9 @@
 
     python -m splosh_amd.build          # or splosh_amd.build.build()
 
-Objects go to splosh_amd/_build/, the library to splosh_amd/libsplosh_q4.so.
+Objects go to splosh_amd/_build/, the library to splosh_amd/libsplosh_q4.so. The measurement
+probes of csrc/bench/ (not part of the path) go into a library of their own,
+splosh_amd/libsplosh_probe.so, which only bench.py loads.
 """
 import os
 import subprocess
@@ -15,7 +17,9 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libsplosh_q4.so"
-SOURCES = ["api.cpp", "q4_basic.hip", "stream.hip", "lanes.hip", "decode.hip", "mma.hip", "tile.hip", "prefill.hip", "q5k.hip", "q5k_decode.hip", "operand.hip", "gguf_native.hip", "gguf_tile.hip", "probe.hip"]
+SOURCES = ["api.cpp", "q4_basic.hip", "stream.hip", "lanes.hip", "decode.hip", "mma.hip", "tile.hip", "prefill.hip", "q5k.hip", "q5k_decode.hip", "operand.hip", "gguf_native.hip", "gguf_tile.hip"]
+PROBE_LIB = PKG / "libsplosh_probe.so"
+PROBE_SOURCES = ["bench/probe.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -26,7 +30,7 @@ COMMON = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Wall", "-Wno
 
 
 def _compile(src):
-    obj = BUILD / (src.replace(".", "_") + ".o")
+    obj = BUILD / (src.replace(".", "_").replace("/", "_") + ".o")
     cmd = [HIPCC, *COMMON, *DEVICE_FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
     if src.endswith(".cpp"):
         cmd[1:1] = ["-x", "hip"]
@@ -36,17 +40,22 @@ def _compile(src):
     return obj
 
 
-def build(verbose=True):
-    BUILD.mkdir(exist_ok=True)
-    jobs = min(len(SOURCES), max(1, os.cpu_count() or 1))
-    with ThreadPoolExecutor(jobs) as pool:
-        objs = list(pool.map(_compile, SOURCES))
-    cmd = [HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *map(str, objs), "-o", str(LIB)]
+def _link(objs, lib):
+    cmd = [HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *map(str, objs), "-o", str(lib)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
-        raise RuntimeError(f"link failed:\n{res.stderr}")
+        raise RuntimeError(f"link failed for {lib.name}:\n{res.stderr}")
+
+
+def build(verbose=True):
+    BUILD.mkdir(exist_ok=True)
+    jobs = min(len(SOURCES) + len(PROBE_SOURCES), max(1, os.cpu_count() or 1))
+    with ThreadPoolExecutor(jobs) as pool:
+        objs = list(pool.map(_compile, SOURCES + PROBE_SOURCES))
+    _link(objs[: len(SOURCES)], LIB)
+    _link(objs[len(SOURCES):], PROBE_LIB)
     if verbose:
-        print(f"built {LIB}")
+        print(f"built {LIB} and {PROBE_LIB.name}")
     return LIB
 
 

@@ -430,15 +430,8 @@ int splosh_q4_gemm_noalloc(const splosh_q4_weight *w, const uint16_t *a, int64_t
     int st = check_q4_weight(w, "weight");
     if (st) return st;
     if ((st = check_io(a, lda, out, ldc, out_dtype, rows, w->rows, w->inner))) return st;
-    // The scratch the M <= 64 kernel would split K with; other kernels run unsplit when the
-    // scratch cannot hold their partials.
-    const size_t need = rows <= 64 && w->inner % kGroupSize == 0
-                            ? splosh::mma_workspace_bytes(rows, w->rows, w->inner / kGroupSize, false)
-                            : 0;
-    if (need > kScratchBytes)
-        return fail(SPLOSH_ERR_WORKSPACE_TOO_SMALL,
-                    "the call needs " + std::to_string(need) + " bytes of scratch; the static scratch holds " +
-                        std::to_string(kScratchBytes));
+    // Every kernel plans against the scratch's size: one whose partials do not fit runs unsplit
+    // (the M <= 64 kernel one workgroup a band, the split-K kernels with one slice).
     void *ptr = nullptr;
     if ((st = scratch_on_current_device(&ptr))) return st;
     // The arrival counters must start at zero: every call returns them to zero, and this call

@@ -288,6 +288,9 @@ bool tile_fits(int64_t rows, int64_t columns, int64_t lda, int64_t stride_words)
     return rows > 0 && columns > 0 && rows * lda < limit && columns * stride_words < limit && rows <= 65535 * 64LL;
 }
 
+// Arrival counters of the other kernels sit in the first 16 KiB of a shared workspace.
+constexpr size_t kTileCounterBytes = 16384;
+
 TilePlan plan_tile(int64_t rows, int64_t columns, int64_t groups, bool mlp, size_t workspace_bytes) {
     TilePlan p;
     p.kind = tile_kind(rows, mlp);
@@ -300,7 +303,7 @@ TilePlan plan_tile(int64_t rows, int64_t columns, int64_t groups, bool mlp, size
     while (splits < 8 && blocks * splits < 256 && groups / (splits * 2) >= 8) splits *= 2;
     static const int splits_override = [] { const char *e = getenv("SPLOSH_TILE_SPLITS"); return e ? atoi(e) : 0; }();
     if (splits_override > 0) splits = splits_override;
-    const size_t need = (size_t)splits * (mlp ? 2 : 1) * rows * columns * sizeof(float);
+    const size_t need = kTileCounterBytes + (size_t)splits * (mlp ? 2 : 1) * rows * columns * sizeof(float);
     if (splits > 1 && need > workspace_bytes) splits = 1;
     p.splits = splits;
     return p;
@@ -308,7 +311,7 @@ TilePlan plan_tile(int64_t rows, int64_t columns, int64_t groups, bool mlp, size
 
 size_t tile_workspace_bytes(int64_t rows, int64_t columns, int64_t groups, bool mlp) {
     const TilePlan p = plan_tile(rows, columns, groups, mlp, (size_t)-1);
-    return p.splits > 1 ? (size_t)p.splits * (mlp ? 2 : 1) * rows * columns * sizeof(float) : 0;
+    return p.splits > 1 ? kTileCounterBytes + (size_t)p.splits * (mlp ? 2 : 1) * rows * columns * sizeof(float) : 0;
 }
 
 template <int WM, int WN, int FM, int FN, int NW>
@@ -368,11 +371,14 @@ hipError_t launch_q4_tile(const TilePlan &plan, const splosh_q4_weight &w, const
     args.residual = residual;
     args.rows = rows;
     args.out_dtype = out_dtype;
-    args.partial = plan.splits > 1 ? (float *)workspace : nullptr;
+    // The partials follow the 16 KiB of arrival counters the other kernels keep at the start of the
+    // workspace (zero between calls), which this kernel never touches.
+    float *partial = plan.splits > 1 ? (float *)((char *)workspace + kTileCounterBytes) : nullptr;
+    args.partial = partial;
     const bool tiled = w.order == SPLOSH_Q4_TILED128;
     hipError_t err = up ? launch_tile_nw<2>(plan, tiled, args, stream) : launch_tile_nw<1>(plan, tiled, args, stream);
     if (err != hipSuccess || plan.splits == 1) return err;
-    return launch_splitk_finish((const float *)workspace, plan.splits, up ? 2 : 1, rows, w.rows, out, ldc, out_dtype,
+    return launch_splitk_finish(partial, plan.splits, up ? 2 : 1, rows, w.rows, out, ldc, out_dtype,
                                 residual, stream);
 }
 

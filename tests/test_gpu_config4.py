@@ -74,17 +74,23 @@ def test_workspace_shared_across_shapes(rt):
     from qcheck import dev_u8
     w5 = rt.q5k_repack(dev_u8(native), 640, 4352)
     dense5 = oracle.q45k_decode(native).reshape(640, 4352)
-    need = max(rt.workspace_bytes(r, n, k) for r in (8, 64) for n, k in ((2176, 5120), (640, 4352)))
+    need = max(rt.workspace_bytes(r, n, k) for r in (8, 64, 96) for n, k in ((2176, 5120), (640, 4352)))
     assert need > 0
     ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
-    seq = [("mlp", 8), ("gemm", 64), ("q5k", 64), ("mlp", 64), ("gemm", 8), ("q5k", 16), ("mlp", 8)]
+    # 96 rows: one tiled weight and a row-major pair go to the split-K tile kernel, whose partials
+    # must stay clear of the counters the M <= 64 calls after it rely on.
+    seq = [("mlp", 8), ("gemm", 64), ("q5k", 64), ("gemm", 96), ("mlp", 64), ("mlp_rm", 96), ("gemm", 8),
+           ("q5k", 16), ("mlp", 8), ("gemm", 64)]
     for kind, rows in seq:
-        k = 5120 if kind == "mlp" else 4352
+        k = 5120 if kind.startswith("mlp") else 4352
         a_bits = oracle.bf16_normal((rows, k), seed=rows + len(kind))
         a = bf16_tensor(a_bits)
         if kind == "mlp":
             ref = oracle.silu_mul(oracle.gemm_a_bf16_w_f32(a_bits, gate.dense), oracle.gemm_a_bf16_w_f32(a_bits, up.dense))
             run = lambda: rt.mlp_in(gate.w_tiled, up.w_tiled, a, out_dtype=torch.float32, workspace=ws)
+        elif kind == "mlp_rm":
+            ref = oracle.silu_mul(oracle.gemm_a_bf16_w_f32(a_bits, gate.dense), oracle.gemm_a_bf16_w_f32(a_bits, up.dense))
+            run = lambda: rt.mlp_in(gate.w_rm, up.w_rm, a, out_dtype=torch.float32, workspace=ws)
         elif kind == "gemm":
             ref = oracle.gemm_a_bf16_w_f32(a_bits, single.dense)
             run = lambda: rt.gemm(single.w_tiled, a, out_dtype=torch.float32, workspace=ws)
