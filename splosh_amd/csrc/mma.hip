@@ -87,7 +87,7 @@ struct MmaArgs {
 // q4 (MLX affine): a step is KW groups of 64; wave kw takes group ga + t KW + kw and lane (r, h)
 // feeds column r from words 4 h .. 4 h + 3 of the group's 32-byte record (one 16-byte load; a
 // wave reads 32 consecutive records, a contiguous kilobyte of the tiled layout). A word becomes
-// eight bf16 weights RNE(s q + b) in 17 VALU (dequant_word_mix).
+// eight bf16 weights RNE(s q + b) in 19 instructions (dequant_word_fp8).
 //
 // Tiled weights stage a step's sidecars for the band (NW weights x {scale, bias} x KW groups x
 // band columns of bf16) through LDS: waves 0 .. 2 NW - 1 each load one array of one weight, lane
@@ -113,8 +113,7 @@ struct Q4Format {
     int side_g;      // group (within a step) of this lane's staged sidecar piece
     u32x4 wq[D][NW];
     uint32_t wsc[D][NW], wbi[D][NW];
-    MixCoef cf[NW];  // coefficients of the step being dequantized
-    uint32_t magic;  // 0x64006400 (binary16 1024 in both halves), kept in a VGPR
+    float cs[NW], cb[NW];  // scale and bias of the step being dequantized
 
     __device__ Q4Format(const MmaArgs &args, int wave_, int lane_) : wave(wave_), lane(lane_) {
         kw = wave / CW;
@@ -137,7 +136,6 @@ struct Q4Format {
         side_rsrc = make_rsrc((arr & 1) ? (const void *)args.biases[side_w] : (const void *)args.scales[side_w],
                               args.sidecar_bytes);
         side_g = ((piece0 + lane) / 8) % KW;
-        asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic));
     }
     __device__ int steps(int ga_, int gb_) const { return (gb_ - ga_ + KW - 1) / KW; }
     __device__ bool active(int t) const { return ga + t * KW + kw < gb; }
@@ -211,9 +209,12 @@ struct Q4Format {
         }
         const float one = on ? 1.0f : 0.0f;
 #pragma unroll
-        for (int w = 0; w < NW; ++w) cf[w] = mix_coef(bf16_bits_to_f32(sb[w]) * one, bf16_bits_to_f32(bb[w]) * one);
+        for (int w = 0; w < NW; ++w) {
+            cs[w] = bf16_bits_to_f32(sb[w]) * one;
+            cb[w] = bf16_bits_to_f32(bb[w]) * one;
+        }
     }
-    __device__ bf16x8 operand(int w, int i, int slot) { return dequant_word_mix(wq[slot][w][i], cf[w], magic); }
+    __device__ bf16x8 operand(int w, int i, int slot) { return dequant_word_fp8(wq[slot][w][i], cs[w], cb[w]); }
 };
 
 // GGUF Q5_K in plane form (GgufPlanes.swift:8-20): a step is one 256-element block; wave kw takes
@@ -377,7 +378,7 @@ struct MmaShape {
 // Pipeline of a job (units [ga, gb) of one band), in steps of KW x 64 elements of K, D steps deep:
 // weight codes go to a D-slot register ring, the activation chunk of a step (rows x KW x 64) and
 // its sidecars via registers to LDS buffer t mod 3, the chunk XOR-swizzled (16-byte piece kc of
-// row m at position kc ^ (m & 7)) so the MFMA operand reads do not conflict. Barriers wait for LDS
+// row m at position kc ^ (m & 15)) so the MFMA operand reads do not conflict. Barriers wait for LDS
 // traffic only, never for global stores.
 template <class F, int FM, int CW, int KW, int D>
 __global__ void __launch_bounds__(CW * KW * 64)
@@ -403,7 +404,7 @@ mma_kernel(MmaArgs args) {
     __shared__ uint16_t fix_list[kMmaMaxGrid];  // contributors of a shared band: 2 wg + slot
     F fmt(args, wave, lane);
     // Activation staging: this thread's piece j of a chunk sits at buffer position
-    // (wave * kAPer + j) * 64 + lane, i.e. row m = pos / kKc, holding piece kc = (pos % kKc) ^ (m & 7)
+    // (wave * kAPer + j) * 64 + lane, i.e. row m = pos / kKc, holding piece kc = (pos % kKc) ^ (m & 15)
     // of the row (an XOR swizzle, so the MFMA operand reads do not conflict), read from byte
     // (m lda + k0 + 8 kc) * 2. Rows past the last are clamped (their outputs are not stored);
     // K past the job belongs to inactive waves; reads past the buffer return zero.
@@ -411,7 +412,7 @@ mma_kernel(MmaArgs args) {
 #pragma unroll
     for (int j = 0; j < S::kAPer; ++j) {
         const int pos = (wave * S::kAPer + j) * 64 + lane;
-        const int row = pos / S::kKc, kc = (pos % S::kKc) ^ (row & 7);
+        const int row = pos / S::kKc, kc = (pos % S::kKc) ^ (row & 15);
         const int64_t rc = row < args.rows ? row : args.rows - 1;
         a_src[j] = (uint32_t)((rc * args.lda + kc * 8) * 2);
     }
@@ -419,7 +420,7 @@ mma_kernel(MmaArgs args) {
     uint32_t a_rd[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-        a_rd[i] = (uint32_t)((r * S::kKc + ((kw * 8 + 4 * h + F::piece(i)) ^ (r & 7))) * 16);
+        a_rd[i] = (uint32_t)((r * S::kKc + ((kw * 8 + 4 * h + F::piece(i)) ^ (r & 15))) * 16);
     char *lds_bytes = (char *)lds;
     char *side_lds = lds_bytes + S::kNB * S::kABuf;
 

@@ -9,7 +9,7 @@
 //    so that a wave's writes are contiguous and the operand reads of 16 consecutive rows hit 16
 //    different bank groups;
 //  * every thread loads a 16-byte piece of one column's codes with that column's scale and bias,
-//    dequantizes its four code words into bf16 (dequant_word_mix, 17 VALU per 8 weights) and writes
+//    dequantizes its four code words into bf16 (dequant_word_fp8, 19 instructions per 8 weights) and writes
 //    them into the group's weight buffer ([256 columns][64 k], rows of 144 bytes: the operand reads
 //    of 32 consecutive columns do not conflict). Every weight is dequantized once a workgroup.
 //  * MFMA step i uses k = 32 h + 8 i .. + 7 for both operands, piece 4 h + i of a row or column.
@@ -165,11 +165,11 @@ __device__ __forceinline__ void prefill_store_mlp(const PrefillArgs &args, const
 // go to one of two register sets; kLoads loads a thread and group.
 
 // MLX affine q4, TILED128: the thread's 16 bytes of the column's record (words 4 (t % 2) .. + 3)
-// and the column's scale and bias (Retile.swift:135-153), dequantized by dequant_word_mix.
+// and the column's scale and bias (Retile.swift:135-153), dequantized by dequant_word_fp8.
 struct Q4Stage {
     static constexpr int kLoads = 3, kNW = 1;
     rsrc_t q_rsrc, s_rsrc, b_rsrc;
-    uint32_t magic, c_src, s_src;
+    uint32_t c_src, s_src;
     u32x4 cr[2];
     uint32_t sr[2], br[2];
     __device__ Q4Stage(const PrefillArgs &args, bool up = false) {
@@ -177,7 +177,6 @@ struct Q4Stage {
         q_rsrc = make_rsrc(w[0], args.w_bytes[0]);
         s_rsrc = make_rsrc(w[1], args.w_bytes[1]);
         b_rsrc = make_rsrc(w[2], args.w_bytes[2]);
-        asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(magic));
     }
     __device__ void begin(const PrefillArgs &args, uint32_t col, int hh) {
         const uint32_t rec = (col >> 7) * (uint32_t)args.groups * 128u + (col & 127u);
@@ -191,10 +190,9 @@ struct Q4Stage {
     }
     // Words q0 and q0 + 1, pieces q0 and q0 + 1.
     __device__ void store(char *dst, int set, uint32_t, bool on, int q0) {
-        const MixCoef cf =
-            mix_coef(on ? bf16_bits_to_f32(sr[set]) : 0.0f, on ? bf16_bits_to_f32(br[set]) : 0.0f);
+        const float s = on ? bf16_bits_to_f32(sr[set]) : 0.0f, b = on ? bf16_bits_to_f32(br[set]) : 0.0f;
 #pragma unroll
-        for (int q = q0; q < q0 + 2; ++q) *(bf16x8 *)(dst + 16 * q) = dequant_word_mix(cr[set][q], cf, magic);
+        for (int q = q0; q < q0 + 2; ++q) *(bf16x8 *)(dst + 16 * q) = dequant_word_fp8(cr[set][q], s, b);
     }
 };
 
