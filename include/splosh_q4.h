@@ -227,6 +227,27 @@ int splosh_q5k_gemm(const splosh_q5k_weight *w, const uint16_t *a, int64_t lda, 
                     int out_dtype, const void *residual, int64_t rows, int kernel, void *workspace,
                     size_t workspace_bytes, hipStream_t stream);
 
+/* The `heads` forms of the GGUF GEMM kernels (Shaders/engine_gguf.metal:55-72,336-338; chosen by
+ * Runtime/Engine.swift:765-779 for the weights in ggufHeadOrder): for the gated-delta out
+ * projection, whose inner columns a GGUF file keeps in its own order of the value heads (128
+ * columns each; GgufConvert.swift:17-23 leaves them so, since moving columns would re-quantise every
+ * block). File head h meets the activations of engine head (heads / key_heads) (h mod key_heads) +
+ * h / key_heads (GgufNames.mlxValueHead: 3 (h % 16) + h / 16 for Qwen's 48 heads and 16 key
+ * heads). key_heads: a power of two dividing inner / 128. Rows the decode or streaming kernel takes
+ * read the activations in that order directly; above that the call first writes a permuted copy of
+ * the activations to the end of the workspace, which must then hold
+ * splosh_heads_workspace_bytes(rows, w->rows, w->inner) (SPLOSH_ERR_WORKSPACE_TOO_SMALL otherwise).
+ * splosh_q4k_gemm_heads is the Q4_K form (plane1 not read). */
+int splosh_q5k_gemm_heads(const splosh_q5k_weight *w, int key_heads, const uint16_t *a, int64_t lda, void *out,
+                          int64_t ldc, int out_dtype, const void *residual, int64_t rows, int kernel, void *workspace,
+                          size_t workspace_bytes, hipStream_t stream);
+int splosh_q4k_gemm_heads(const splosh_q5k_weight *w, int key_heads, const uint16_t *a, int64_t lda, void *out,
+                          int64_t ldc, int out_dtype, const void *residual, int64_t rows, int kernel, void *workspace,
+                          size_t workspace_bytes, hipStream_t stream);
+/* The workspace a head-ordered call of any form needs: splosh_workspace_bytes plus the permuted
+ * activations (rows x inner bf16) and alignment. */
+size_t splosh_heads_workspace_bytes(int64_t rows, int64_t columns, int64_t inner);
+
 /* GgufTensorType.decode for Q5_K (Model/GgufQuant.swift:191-212) read from the planes: out fp32
  * [rows][inner], bit-identical to the CPU reference. */
 int splosh_q5k_dequant(const splosh_q5k_weight *w, float *out, hipStream_t stream);
@@ -271,6 +292,11 @@ int splosh_q4k_dequant(const splosh_q5k_weight *w, float *out, hipStream_t strea
 int splosh_gguf_gemm(int gguf_type, const uint8_t *native, int64_t rows, int64_t inner, const uint16_t *a,
                      int64_t lda, void *out, int64_t ldc, int out_dtype, const void *residual, int64_t m,
                      void *workspace, size_t workspace_bytes, hipStream_t stream);
+/* splosh_gguf_gemm with the weight's inner columns in a GGUF file's value-head order: the `heads`
+ * form described at splosh_q5k_gemm_heads. */
+int splosh_gguf_gemm_heads(int gguf_type, const uint8_t *native, int64_t rows, int64_t inner, int key_heads,
+                           const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype, const void *residual,
+                           int64_t m, void *workspace, size_t workspace_bytes, hipStream_t stream);
 int splosh_gguf_dequant(int gguf_type, const uint8_t *native, int64_t rows, int64_t inner, float *out,
                         hipStream_t stream);
 

@@ -377,3 +377,54 @@ def q45k_random_native_splitmix(N, K, seed, fifth_bit=True):
                 value = -value
             raw[b, field:field + 2] = np.array([value], dtype=np.float16).view(np.uint8)
     return raw.reshape(-1)
+
+
+# ---- GGUF conversion: value-head order and Q8_0 requantisation (GgufNames.swift, GgufConvert.swift)
+
+def mlx_value_head(i, key_heads=16, value_heads=48):
+    return lib().or_mlx_value_head(int(i), key_heads, value_heads)
+
+
+def head_destination(unit, first, span, key_heads=16, value_heads=48):
+    lib().or_head_destination.restype = _i64
+    lib().or_head_destination.argtypes = [_i64, _i64, _i64, ctypes.c_int, ctypes.c_int]
+    return lib().or_head_destination(unit, first, span, key_heads, value_heads)
+
+
+def order_rows(native, rows, row_bytes, first=0, span=0, stored=None, key_heads=16, value_heads=48):
+    """GgufConvert's row order: file row r at row head_destination(r); span 0: rows unchanged."""
+    native = _c(native, np.uint8)
+    stored = rows if stored is None else stored
+    out = np.empty(stored * row_bytes, np.uint8)
+    f = lib().or_order_rows
+    f.argtypes = [_ptr, _i64, _i64, _i64, _i64, ctypes.c_int, ctypes.c_int, _i64, _ptr]
+    f(_p(native), rows, row_bytes, first, span, key_heads, value_heads, stored, _p(out))
+    return out
+
+
+def f32_to_f16_rne(values):
+    v = np.ascontiguousarray(np.asarray(values, np.float32).reshape(-1))
+    f = lib().or_f32_to_f16_rne
+    f.restype = ctypes.c_uint16
+    f.argtypes = [ctypes.c_float]
+    return np.array([f(float(x)) for x in v], np.uint16)
+
+
+def q8_0_blocks(values):
+    v = _c(np.asarray(values, np.float32).reshape(-1), np.float32)
+    out = np.empty(v.size // 32 * 34, np.uint8)
+    f = lib().or_q8_0_blocks
+    f.argtypes = [_ptr, _i64, _ptr]
+    f(_p(v), v.size // 32, _p(out))
+    return out
+
+
+def head_gather(a_bits, key_heads=16):
+    """out[m][k] = a[m][mlx_value_head(k / 128) 128 + k % 128]: the activations a head-ordered weight meets."""
+    a = _c(a_bits, np.uint16)
+    m, inner = a.shape
+    out = np.empty_like(a)
+    f = lib().or_head_gather
+    f.argtypes = [_ptr, _i64, _i64, _i64, ctypes.c_int, _ptr]
+    f(_p(a), inner, m, inner, key_heads, _p(out))
+    return out

@@ -624,3 +624,96 @@ void or_q45k_gemm_native(const uint16_t *a, int64_t lda, const uint8_t *native, 
     }
     (void)threads;
 }
+
+/* ---- GGUF conversion: the gated-delta value heads and the float -> Q8_0 requantisation -------- */
+
+/* GgufNames.mlxValueHead (GgufNames.swift:104): the engine's index of file value head i,
+ * (value_heads / key_heads) (i % key_heads) + i / key_heads -- 3 (i % 16) + i / 16 for Qwen. */
+int or_mlx_value_head(int i, int key_heads, int value_heads) {
+    return (value_heads / key_heads) * (i % key_heads) + i / key_heads;
+}
+
+/* GgufConvert.HeadOrder.destination (GgufConvert.swift:62-69). */
+int64_t or_head_destination(int64_t unit, int64_t first, int64_t span, int key_heads, int value_heads) {
+    if (unit < first || (unit - first) / span >= value_heads) return unit;
+    const int64_t h = (unit - first) / span;
+    return first + (int64_t)or_mlx_value_head((int)h, key_heads, value_heads) * span + (unit - first) % span;
+}
+
+/* GgufConvert.ggufPlanes' `order` (GgufConvert.swift:381-395): file row r to row destination(r),
+ * rows [rows, stored) zero. span <= 0: no reordering. */
+void or_order_rows(const uint8_t *native, int64_t rows, int64_t row_bytes, int64_t first, int64_t span,
+                   int key_heads, int value_heads, int64_t stored, uint8_t *out) {
+    memset(out, 0, (size_t)(stored * row_bytes));
+    for (int64_t r = 0; r < rows; ++r) {
+        const int64_t to = span > 0 ? or_head_destination(r, first, span, key_heads, value_heads) : r;
+        memcpy(out + to * row_bytes, native + r * row_bytes, (size_t)row_bytes);
+    }
+}
+
+/* IEEE binary32 -> binary16 bits, round to nearest even (Swift's Float16(Float)): normals,
+ * subnormals, overflow to infinity, NaN kept quiet. */
+uint16_t or_f32_to_f16_rne(float value) {
+    uint32_t x;
+    memcpy(&x, &value, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const uint32_t exp = (x >> 23) & 0xFFu, mant = x & 0x7FFFFFu;
+    if (exp == 0xFFu) return (uint16_t)(sign | 0x7C00u | (mant ? 0x200u : 0u));
+    const int e = (int)exp - 127 + 15;  /* binary16 biased exponent */
+    if (e >= 31) return (uint16_t)(sign | 0x7C00u);
+    uint32_t m = mant | (exp ? 0x800000u : 0u);  /* 24-bit significand */
+    int shift;                                    /* bits of m dropped */
+    uint32_t he;                                  /* binary16 exponent field of the result */
+    if (e >= 1) {
+        shift = 13;
+        he = (uint32_t)e;
+    } else {
+        shift = 14 - e;  /* subnormal: value = m 2^(exp-150) = q 2^-24 */
+        he = 0;
+        if (exp == 0) shift = 24;  /* binary32 subnormals are far below binary16's range */
+        if (shift > 25) return (uint16_t)sign;
+    }
+    const uint32_t q = m >> shift, rem = m & ((1u << shift) - 1u), half = 1u << (shift - 1);
+    uint32_t r = q + ((rem > half || (rem == half && (q & 1u))) ? 1u : 0u);
+    if (e >= 1) {
+        /* q holds the implicit bit at 2^10; a carry out of the significand moves the exponent */
+        r = (he << 10) + (r - 0x400u);
+        if (r >= 0x7C00u) return (uint16_t)(sign | 0x7C00u);
+        return (uint16_t)(sign | r);
+    }
+    return (uint16_t)(sign | r);  /* a subnormal that rounds up to 0x400 is the smallest normal */
+}
+
+/* GgufConvert.q8_0Blocks (GgufConvert.swift:236-257), block by block as written there: the largest
+ * magnitude, scale = largest / 127 and inverse = 1 / scale in fp32 (0 for a zero scale), the scale
+ * stored as fp16, each code (value * inverse) rounded half away from zero and clamped to int8. */
+void or_q8_0_blocks(const float *values, int64_t blocks, uint8_t *out) {
+    for (int64_t b = 0; b < blocks; ++b) {
+        float largest = 0.0f;
+        for (int e = 0; e < 32; ++e) {
+            const float a = fabsf(values[32 * b + e]);
+            largest = a > largest ? a : largest;
+        }
+        const float scale = largest / 127.0f;
+        const float inverse = scale > 0.0f ? 1.0f / scale : 0.0f;
+        const uint16_t stored = or_f32_to_f16_rne(scale);
+        out[34 * b] = (uint8_t)(stored & 0xFFu);
+        out[34 * b + 1] = (uint8_t)(stored >> 8);
+        for (int e = 0; e < 32; ++e) {
+            float code = roundf(values[32 * b + e] * inverse);
+            code = code < -128.0f ? -128.0f : code > 127.0f ? 127.0f : code;
+            out[34 * b + 2 + e] = (uint8_t)(int8_t)code;
+        }
+    }
+}
+
+/* The activations a head-ordered weight meets (engine_gguf.metal:55-72): out[m][k] = a[m][col(k)],
+ * col(k) = mlxValueHead(k / 128) 128 + k % 128 -- the weight's inner column k is file head k / 128. */
+void or_head_gather(const uint16_t *a, int64_t lda, int64_t m, int64_t inner, int key_heads, uint16_t *out) {
+    const int heads = (int)(inner / 128);
+    for (int64_t r = 0; r < m; ++r)
+        for (int64_t k = 0; k < inner; ++k) {
+            const int64_t col = (int64_t)or_mlx_value_head((int)(k / 128), key_heads, heads) * 128 + k % 128;
+            out[r * inner + k] = a[r * lda + col];
+        }
+}

@@ -110,6 +110,15 @@ void or_q45k_gemm_native(const uint16_t *a, int64_t lda, const uint8_t *native, 
                          int64_t M, int64_t N, int64_t K, int64_t n0, int64_t n1, float *out,
                          int threads);
 
+/* GGUF conversion (GgufNames.swift, GgufConvert.swift): value-head order and Q8_0 requantisation. */
+int or_mlx_value_head(int i, int key_heads, int value_heads);
+int64_t or_head_destination(int64_t unit, int64_t first, int64_t span, int key_heads, int value_heads);
+void or_order_rows(const uint8_t *native, int64_t rows, int64_t row_bytes, int64_t first, int64_t span,
+                   int key_heads, int value_heads, int64_t stored, uint8_t *out);
+uint16_t or_f32_to_f16_rne(float value);
+void or_q8_0_blocks(const float *values, int64_t blocks, uint8_t *out);
+void or_head_gather(const uint16_t *a, int64_t lda, int64_t m, int64_t inner, int key_heads, uint16_t *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -100,6 +100,13 @@ SIGNATURES = {
     "splosh_q4k_dequant": (_int, [ctypes.POINTER(Q5KWeight), _vp, _vp]),
     "splosh_gguf_gemm": (_int, [_int, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _int, _vp, _i64, _vp, _sz, _vp]),
     "splosh_gguf_dequant": (_int, [_int, _vp, _i64, _i64, _vp, _vp]),
+    "splosh_q5k_gemm_heads": (_int, [ctypes.POINTER(Q5KWeight), _int, _vp, _i64, _vp, _i64, _int, _vp, _i64, _int,
+                                     _vp, _sz, _vp]),
+    "splosh_q4k_gemm_heads": (_int, [ctypes.POINTER(Q5KWeight), _int, _vp, _i64, _vp, _i64, _int, _vp, _i64, _int,
+                                     _vp, _sz, _vp]),
+    "splosh_gguf_gemm_heads": (_int, [_int, _vp, _i64, _i64, _int, _vp, _i64, _vp, _i64, _int, _vp, _i64, _vp, _sz,
+                                      _vp]),
+    "splosh_heads_workspace_bytes": (_sz, [_i64, _i64, _i64]),
     "splosh_q4k_repack": (_int, [_vp, _i64, _i64, _vp, _vp, _vp]),
     "splosh_q4k_unpack": (_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
     "splosh_q4_embed": (_int, [ctypes.POINTER(Q4Weight), _vp, _i64, _vp, _i64, _int, _vp]),

@@ -488,19 +488,71 @@ int splosh_untile128(const void *src, void *dst, int64_t rows, int64_t groups, i
     return tile_common(src, dst, rows, groups, element_bytes, true, stream);
 }
 
+// The value-head order of a head-ordered weight's inner columns (engine_gguf.metal:55-72): 128
+// columns a head, file head h read from engine head vph (h mod kh) + h / kh. key_heads = 0: none.
+struct HeadOrder {
+    int hs = -1, vph = 0;
+    bool on() const { return hs >= 0; }
+};
+static int head_order(int key_heads, int64_t inner, HeadOrder *out) {
+    *out = HeadOrder{};
+    if (key_heads == 0) return ok();
+    if (key_heads < 0 || (key_heads & (key_heads - 1)) != 0)
+        return fail(SPLOSH_ERR_INVALID_SHAPE, "key_heads must be a power of two");
+    if (inner % 128 != 0 || (inner / 128) % key_heads != 0)
+        return fail(SPLOSH_ERR_INVALID_SHAPE, "inner must be whole 128-column value heads, a multiple of key_heads of them");
+    int hs = 0;
+    while ((1 << hs) < key_heads) ++hs;
+    out->hs = hs;
+    out->vph = (int)(inner / 128 / key_heads);
+    return ok();
+}
+
+// A head-ordered call on a kernel that reads the activations in place: the permuted copy goes to
+// the end of the workspace (256-byte aligned), and the kernel gets the rest.
+static size_t head_copy_bytes(int64_t m, int64_t inner) { return ((size_t)m * inner * 2 + 255) / 256 * 256; }
+static int head_copy(const HeadOrder &ho, const uint16_t **a, int64_t *lda, int64_t m, int64_t inner, void *workspace,
+                     size_t *workspace_bytes, hipStream_t stream) {
+    const size_t need = head_copy_bytes(m, inner);
+    if (!workspace || *workspace_bytes < need)
+        return fail(SPLOSH_ERR_WORKSPACE_TOO_SMALL,
+                    "a head-ordered weight at this row count needs a workspace of splosh_heads_workspace_bytes()");
+    const size_t rest = (*workspace_bytes - need) / 256 * 256;
+    uint16_t *dst = (uint16_t *)((char *)workspace + rest);
+    int st = hip_status(splosh::launch_head_gather(*a, *lda, m, inner, ho.hs, ho.vph, dst, stream), "head gather launch");
+    if (st) return st;
+    *a = dst;
+    *lda = inner;
+    *workspace_bytes = rest;
+    return ok();
+}
+
 static int gguf_gemm(const splosh_q5k_weight *w_in, bool fifth, const uint16_t *a, int64_t lda, void *out, int64_t ldc,
                      int out_dtype, const void *residual, int64_t rows, int kernel, void *workspace,
-                     size_t workspace_bytes, hipStream_t stream) {
+                     size_t workspace_bytes, hipStream_t stream, int key_heads = 0) {
     int st = check_q5k_weight(w_in, fifth);
     if (st) return st;
+    HeadOrder ho;
+    if ((st = head_order(key_heads, w_in->inner, &ho))) return st;
     splosh_q5k_weight wv = *w_in;
     if (!fifth) wv.plane1 = nullptr;  // the kernels read no fifth bits
     const splosh_q5k_weight *w = &wv;
     if ((st = check_io(a, lda, out, ldc, out_dtype, rows, w->rows, w->inner))) return st;
-    const bool eligible = lda % 4 == 0 && aligned(a, 8) && aligned(w->plane0, 16) && (!fifth || aligned(w->plane1, 4)) &&
-                          aligned(w->meta, 16);
+    const bool planes_ok = aligned(w->plane0, 16) && (!fifth || aligned(w->plane1, 4)) && aligned(w->meta, 16);
+    if (kernel == SPLOSH_KERNEL_AUTO && planes_ok && lda % 4 == 0 && aligned(a, 16) &&
+        splosh::q5k_decode_fits(rows, w->rows, w->inner))
+        return hip_status(splosh::launch_q5k_decode(*w, a, out, out_dtype, residual, stream, ho.hs, ho.vph),
+                          "q5k decode launch");
+    // Every other kernel reads the activations in place: a head-ordered call gives it a permuted
+    // copy (dense rows of `inner`, 256-byte aligned, at the end of the workspace).
+    if (ho.on()) {
+        if (lda % 8 != 0 || !aligned(a, 16))
+            return fail(SPLOSH_ERR_UNSUPPORTED, "head-ordered GEMM needs lda % 8 == 0 and 16-byte aligned activations");
+        if ((st = head_copy(ho, &a, &lda, rows, w->inner, workspace, &workspace_bytes, stream))) return st;
+        if (workspace_bytes == 0) workspace = nullptr;
+    }
+    const bool eligible = lda % 4 == 0 && aligned(a, 8) && planes_ok;
     const bool mma_ok = eligible && lda % 8 == 0 && aligned(a, 16) && splosh::q5k_mma_fits(rows, w->rows, w->inner, lda);
-    const bool decode_ok = eligible && aligned(a, 16) && splosh::q5k_decode_fits(rows, w->rows, w->inner);
     const bool tile_ok = eligible && lda % 8 == 0 && aligned(a, 16) && splosh::gguf_tile_fits(rows, w->rows, w->inner, lda);
     const bool prefill_ok = eligible && lda % 8 == 0 && aligned(a, 16) && aligned(out, 16) &&
                             (!residual || aligned(residual, 16)) &&
@@ -508,8 +560,6 @@ static int gguf_gemm(const splosh_q5k_weight *w_in, bool fifth, const uint16_t *
     int choice = kernel;
     if (kernel == SPLOSH_KERNEL_AUTO) {
         if (!eligible) choice = SPLOSH_KERNEL_SCALAR;
-        else if (decode_ok)
-            return hip_status(splosh::launch_q5k_decode(*w, a, out, out_dtype, residual, stream), "q5k decode launch");
         else if (mma_ok) choice = SPLOSH_KERNEL_DEQUANT;
         // Above 64 rows the 256 x 256 prefill kernel (K17408 -> N5120: 75 us at 128 rows against the
         // tile kernel's 86, 381 against 627 at 2048).
@@ -580,6 +630,28 @@ int splosh_q4k_gemm(const splosh_q5k_weight *w, const uint16_t *a, int64_t lda, 
     return gguf_gemm(w, false, a, lda, out, ldc, out_dtype, residual, rows, kernel, workspace, workspace_bytes, stream);
 }
 
+// The `heads` kernels of engine_gguf.metal:336-338 (Engine.swift:765-779, ggufHeadOrder).
+int splosh_q5k_gemm_heads(const splosh_q5k_weight *w, int key_heads, const uint16_t *a, int64_t lda, void *out,
+                          int64_t ldc, int out_dtype, const void *residual, int64_t rows, int kernel, void *workspace,
+                          size_t workspace_bytes, hipStream_t stream) {
+    if (key_heads <= 0) return fail(SPLOSH_ERR_INVALID_SHAPE, "key_heads must be positive");
+    return gguf_gemm(w, true, a, lda, out, ldc, out_dtype, residual, rows, kernel, workspace, workspace_bytes, stream,
+                     key_heads);
+}
+
+int splosh_q4k_gemm_heads(const splosh_q5k_weight *w, int key_heads, const uint16_t *a, int64_t lda, void *out,
+                          int64_t ldc, int out_dtype, const void *residual, int64_t rows, int kernel, void *workspace,
+                          size_t workspace_bytes, hipStream_t stream) {
+    if (key_heads <= 0) return fail(SPLOSH_ERR_INVALID_SHAPE, "key_heads must be positive");
+    return gguf_gemm(w, false, a, lda, out, ldc, out_dtype, residual, rows, kernel, workspace, workspace_bytes, stream,
+                     key_heads);
+}
+
+size_t splosh_heads_workspace_bytes(int64_t rows, int64_t columns, int64_t inner) {
+    if (rows <= 0 || columns <= 0 || inner <= 0) return 0;
+    return splosh_workspace_bytes(rows, columns, inner) + 256 + head_copy_bytes(rows, inner);
+}
+
 int splosh_q5k_dequant(const splosh_q5k_weight *w, float *out, hipStream_t stream) {
     return gguf_dequant(w, true, out, stream);
 }
@@ -606,14 +678,16 @@ static int check_gguf_native(int type, const uint8_t *native, int64_t rows, int6
 
 constexpr int64_t kGgufPrefillRows = 256;  // measured: the tile kernel is as fast or faster up to 128 rows
 
-int splosh_gguf_gemm(int gguf_type, const uint8_t *native, int64_t rows, int64_t inner, const uint16_t *a,
-                     int64_t lda, void *out, int64_t ldc, int out_dtype, const void *residual, int64_t m,
-                     void *workspace, size_t workspace_bytes, hipStream_t stream) {
+static int gguf_native_gemm(int gguf_type, const uint8_t *native, int64_t rows, int64_t inner, const uint16_t *a,
+                            int64_t lda, void *out, int64_t ldc, int out_dtype, const void *residual, int64_t m,
+                            void *workspace, size_t workspace_bytes, hipStream_t stream, int key_heads) {
     int st = check_gguf_native(gguf_type, native, rows, inner);
     if (st) return st;
     if ((st = check_io(a, lda, out, ldc, out_dtype, m, rows, inner))) return st;
     if (lda % 8 != 0 || !aligned(a, 16))
         return fail(SPLOSH_ERR_UNSUPPORTED, "GGUF native kernel needs lda % 8 == 0 and 16-byte aligned activations");
+    HeadOrder ho;
+    if ((st = head_order(key_heads, inner, &ho))) return st;
     // From kGgufPrefillRows rows the 256 x 256 prefill kernel (each weight group decoded once per
     // 256 rows); above eight rows, or above the format's streaming limit with a workspace for its K
     // split, the tiled kernel (once per 64 or 128 rows); otherwise one pass of the streaming
@@ -626,24 +700,47 @@ int splosh_gguf_gemm(int gguf_type, const uint8_t *native, int64_t rows, int64_t
         const char *e = getenv("SPLOSH_GGUF_PREFILL_ROWS");
         return e ? (int64_t)atoll(e) : kGgufPrefillRows;
     }();
-    if (m >= prefill_rows && aligned(out, 16) && (!residual || aligned(residual, 16)) &&
-        splosh::gguf_prefill_fits(gguf_type, m, rows, inner, lda, ldc)) {
+    const int64_t stream_rows = gguf_type == 21 ? 8 : (gguf_type == 14 || gguf_type == 11) ? 6 : 5;
+    const bool split_room = workspace && workspace_bytes >= splosh::gguf_tile_workspace_bytes(m, rows, inner) &&
+                            splosh::gguf_tile_workspace_bytes(m, rows, inner) > 0;
+    const bool prefill = m >= prefill_rows && aligned(out, 16) && (!residual || aligned(residual, 16)) &&
+                         splosh::gguf_prefill_fits(gguf_type, m, rows, inner, lda, ldc);
+    const bool tile = !prefill && (m > 8 || (m > stream_rows && split_room)) && splosh::gguf_tile_fits(m, rows, inner, lda);
+    // The streaming kernels read the activations through head_group(); the tiled and prefill
+    // kernels get a permuted copy.
+    if (ho.on() && (prefill || tile)) {
+        if ((st = head_copy(ho, &a, &lda, m, inner, workspace, &workspace_bytes, stream))) return st;
+        if (workspace_bytes == 0) workspace = nullptr;
+    }
+    if (prefill) {
         const splosh::PrefillPlan plan = splosh::plan_prefill(m, rows, inner / kGroupSize, workspace ? workspace_bytes : 0);
         return hip_status(splosh::launch_gguf_prefill(plan, gguf_type, native, rows, inner, a, lda, out, ldc, out_dtype,
                                                       residual, m, workspace, stream),
                           "gguf prefill launch");
     }
-    const int64_t stream_rows = gguf_type == 21 ? 8 : (gguf_type == 14 || gguf_type == 11) ? 6 : 5;
-    const bool split_room = workspace && workspace_bytes >= splosh::gguf_tile_workspace_bytes(m, rows, inner) &&
-                            splosh::gguf_tile_workspace_bytes(m, rows, inner) > 0;
-    if ((m > 8 || (m > stream_rows && split_room)) && splosh::gguf_tile_fits(m, rows, inner, lda))
+    if (tile)
         return hip_status(splosh::launch_gguf_tile(gguf_type, native, nullptr, nullptr, rows, inner, a, lda, out, ldc,
                                                    out_dtype, residual, m, workspace, workspace_bytes, stream),
                           "gguf tile launch");
     if (m > ((int64_t)65535 * 4)) return fail(SPLOSH_ERR_UNSUPPORTED, "too many activation rows for one launch");
     return hip_status(splosh::launch_gguf_gemv(gguf_type, native, rows, inner, a, lda, out, ldc, out_dtype, residual,
-                                               m, stream),
+                                               m, stream, ho.hs, ho.vph),
                       "gguf native gemm launch");
+}
+
+int splosh_gguf_gemm(int gguf_type, const uint8_t *native, int64_t rows, int64_t inner, const uint16_t *a,
+                     int64_t lda, void *out, int64_t ldc, int out_dtype, const void *residual, int64_t m,
+                     void *workspace, size_t workspace_bytes, hipStream_t stream) {
+    return gguf_native_gemm(gguf_type, native, rows, inner, a, lda, out, ldc, out_dtype, residual, m, workspace,
+                            workspace_bytes, stream, 0);
+}
+
+int splosh_gguf_gemm_heads(int gguf_type, const uint8_t *native, int64_t rows, int64_t inner, int key_heads,
+                           const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype, const void *residual,
+                           int64_t m, void *workspace, size_t workspace_bytes, hipStream_t stream) {
+    if (key_heads <= 0) return fail(SPLOSH_ERR_INVALID_SHAPE, "key_heads must be positive");
+    return gguf_native_gemm(gguf_type, native, rows, inner, a, lda, out, ldc, out_dtype, residual, m, workspace,
+                            workspace_bytes, stream, key_heads);
 }
 
 int splosh_gguf_dequant(int gguf_type, const uint8_t *native, int64_t rows, int64_t inner, float *out,

@@ -113,6 +113,17 @@ __device__ __forceinline__ int xcd_block(int id, int grid) {
     return grid % 8 == 0 ? (id & 7) * (grid >> 3) + (id >> 3) : id;
 }
 
+// The activation group (32 elements) that weight group g meets when the weight's inner columns keep
+// a GGUF file's order of the gated-delta value heads (128 columns, four groups, each) and the
+// activations the engine's (engine_gguf.metal:55-72, GgufNames.swift mlxValueHead): file head h is
+// engine head vph (h mod kh) + h / kh, kh = 2^hs key heads, vph value heads each. hs < 0: no
+// reordering.
+__device__ __forceinline__ int head_group(int g, int hs, int vph) {
+    if (hs < 0) return g;
+    const int head = g >> 2;
+    return ((vph * (head & ((1 << hs) - 1)) + (head >> hs)) << 2) | (g & 3);
+}
+
 // Byte j of x as an fp32 number (v_cvt_f32_ubyteN, exact).
 __device__ __forceinline__ float cvt_byte(uint32_t x, int j) {
     float r;

@@ -35,6 +35,7 @@ struct GgufNativeArgs {
     int64_t m;
     int out_dtype;
     float *dense;
+    int hs, vph;  // value-head order of the activations (head_group); hs < 0: none
 };
 
 template <int TYPE>
@@ -244,7 +245,8 @@ __global__ void __launch_bounds__(256) gguf_pairs_kernel(GgufNativeArgs args) {
 #pragma unroll
         for (int i = 0; i < MR; ++i) {
             if (m0 + i >= args.m) break;
-            const u32x4 *ap = (const u32x4 *)(args.a + (m0 + i) * args.lda + (int64_t)g * 32);
+            const u32x4 *ap =
+                (const u32x4 *)(args.a + (m0 + i) * args.lda + (int64_t)head_group(g, args.hs, args.vph) * 32);
             uint32_t x[16];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
@@ -334,7 +336,8 @@ __global__ void __launch_bounds__(256) gguf_gemv_kernel(GgufNativeArgs args) {
 #pragma unroll
         for (int i = 0; i < MR; ++i) {
             if (m0 + i >= args.m) break;
-            const u32x4 *ap = (const u32x4 *)(args.a + (m0 + i) * args.lda + (int64_t)g * 32);
+            const u32x4 *ap =
+                (const u32x4 *)(args.a + (m0 + i) * args.lda + (int64_t)head_group(g, args.hs, args.vph) * 32);
             float s = 0.0f;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
@@ -477,13 +480,35 @@ static void launch_gemv_mr(int type, const GgufNativeArgs &args, hipStream_t str
     }
 }
 
+// One 16-byte piece (8 activations) a thread: piece p of row m comes from group head_group(p / 4).
+__global__ void __launch_bounds__(256) head_gather_kernel(const uint16_t *__restrict__ a, int64_t lda, int64_t m,
+                                                          int64_t inner, int hs, int vph, uint16_t *__restrict__ dst) {
+    const int64_t pieces = inner / 8;
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= m * pieces) return;
+    const int64_t row = t / pieces, p = t - row * pieces;
+    const int g = (int)(p >> 2);
+    const int64_t src = row * lda + (int64_t)head_group(g, hs, vph) * 32 + (p & 3) * 8;
+    *(u32x4 *)(dst + row * inner + p * 8) = *(const u32x4 *)(a + src);
+}
+
+hipError_t launch_head_gather(const uint16_t *a, int64_t lda, int64_t m, int64_t inner, int hs, int vph,
+                              uint16_t *dst, hipStream_t stream) {
+    const int64_t total = m * (inner / 8);
+    hipLaunchKernelGGL(head_gather_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, a, lda, m,
+                       inner, hs, vph, dst);
+    return hipGetLastError();
+}
+
 // Activation rows a pass over the weight: four up to four rows, eight above (one pass up to
 // eight rows instead of two).
 hipError_t launch_gguf_gemv(int type, const uint8_t *w, int64_t rows, int64_t inner, const uint16_t *a, int64_t lda,
                             void *out, int64_t ldc, int out_dtype, const void *residual, int64_t m,
-                            hipStream_t stream) {
+                            hipStream_t stream, int hs, int vph) {
     GgufNativeArgs args = {};
     fill_args(args, type, w, rows, inner);
+    args.hs = hs;
+    args.vph = vph;
     args.a = a;
     args.lda = lda;
     args.out = out;

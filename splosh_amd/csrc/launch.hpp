@@ -106,9 +106,13 @@ hipError_t launch_gguf_tile(int type, const uint8_t *w, const uint8_t *plane1, c
 // Workspace that lets the tiled kernel split K (0: it would not split): arrival counters in the
 // first 16 KiB, fp32 partials after.
 size_t gguf_tile_workspace_bytes(int64_t rows, int64_t n, int64_t inner);
+// dst[m][k] = a[m][column of k in the engine's value-head order] (head_group), m rows of `inner`
+// elements: the activations of a head-ordered weight for the kernels that read them unpermuted.
+hipError_t launch_head_gather(const uint16_t *a, int64_t lda, int64_t m, int64_t inner, int hs, int vph,
+                              uint16_t *dst, hipStream_t stream);
 hipError_t launch_gguf_gemv(int type, const uint8_t *w, int64_t rows, int64_t inner, const uint16_t *a, int64_t lda,
                             void *out, int64_t ldc, int out_dtype, const void *residual, int64_t m,
-                            hipStream_t stream);
+                            hipStream_t stream, int hs = -1, int vph = 0);
 
 // The same kernel over Q5_K planes; the plan's units are 256-element blocks.
 bool q5k_mma_fits(int64_t rows, int64_t columns, int64_t inner, int64_t lda);
@@ -170,7 +174,7 @@ hipError_t launch_gguf_prefill(const PrefillPlan &plan, int type, const uint8_t 
 // The decode kernel for one activation row of Q5_K planes (q5k_decode.hip).
 bool q5k_decode_fits(int64_t rows, int64_t columns, int64_t inner);
 hipError_t launch_q5k_decode(const splosh_q5k_weight &w, const uint16_t *a, void *out, int out_dtype,
-                             const void *residual, hipStream_t stream);
+                             const void *residual, hipStream_t stream, int hs = -1, int vph = 0);
 
 // Operand producers (operand.hip).
 hipError_t launch_prepare_operand(const float *x, int64_t ldx, int64_t rows, int64_t dim, uint16_t *out, int64_t ldo,

@@ -34,6 +34,7 @@ struct Q5DecodeArgs {
     const void *residual;
     int out_dtype;
     uint32_t p0_bytes, p1_bytes, meta_bytes;
+    int hs, vph;  // value-head order of the activations (head_group); hs < 0: none
 };
 
 constexpr int kQ5DecodeDepth = 2;  // steps in flight a wave
@@ -74,7 +75,7 @@ q5k_decode_kernel(Q5DecodeArgs args) {
 #pragma unroll
     for (int t = 0; t < kStage; ++t) {
         const int e = threadIdx.x + t * kQ5DecodeWg;
-        const u32x4 *src = (const u32x4 *)(args.a + (e < G ? e : 0) * 32);
+        const u32x4 *src = (const u32x4 *)(args.a + head_group(e < G ? e : 0, args.hs, args.vph) * 32);
 #pragma unroll
         for (int j = 0; j < 4; ++j) xin[t][j] = src[j];
     }
@@ -123,7 +124,7 @@ q5k_decode_kernel(Q5DecodeArgs args) {
     for (int t = 0; t < kStage; ++t)
         if (threadIdx.x + t * kQ5DecodeWg < G) stage(threadIdx.x + t * kQ5DecodeWg, xin[t]);
     for (int e = threadIdx.x + kStage * kQ5DecodeWg; e < G; e += kQ5DecodeWg) {
-        const u32x4 *src = (const u32x4 *)(args.a + e * 32);
+        const u32x4 *src = (const u32x4 *)(args.a + head_group(e, args.hs, args.vph) * 32);
         u32x4 v[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) v[j] = src[j];
@@ -229,8 +230,10 @@ static hipError_t launch_q5k_decode_b(const Q5DecodeArgs &args, hipStream_t stre
 }
 
 hipError_t launch_q5k_decode(const splosh_q5k_weight &w, const uint16_t *a, void *out, int out_dtype,
-                             const void *residual, hipStream_t stream) {
+                             const void *residual, hipStream_t stream, int hs, int vph) {
     Q5DecodeArgs args;
+    args.hs = hs;
+    args.vph = vph;
     args.plane0 = w.plane0;
     args.plane1 = w.plane1;
     args.meta = w.meta;

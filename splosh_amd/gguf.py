@@ -13,8 +13,13 @@ skipped, as there (:292-325).
 `load_weight` turns a Q4_K / Q5_K tensor into a runtime.Q5KWeight / Q4KWeight through the device
 repack (GgufPlanes.repack), with the rows rounded up to whole 128-row tiles by zero blocks
 (GgufConvert.storedRows, GgufConvert.swift:259-262), and a Q8_0 / Q6_K / IQ4_NL / IQ4_XS tensor into
-a runtime.GgufWeight of its native blocks. `write_gguf` writes the same form (the tests'
-fixtures).
+a runtime.GgufWeight of its native blocks. A weight the file holds in a float type (f32, f16, bf16)
+is quantised to Q8_0 first (GgufConvert.storedType / q8_0Blocks, GgufConvert.swift:229-257). The rows
+of a gated-delta layer's head-ordered weights are moved into the engine's order of the value heads
+(GgufConvert.swift:56-70, 326-345, 381-395: `block_head_order`); the out projection keeps its
+columns in the file's order and is multiplied with runtime.gemm(..., key_heads=16). `dense_bf16`
+converts the dense tensors the same way (GgufConvert.ggufDense, :432-457). `write_gguf` writes the
+file form (the tests' fixtures).
 """
 import struct
 from dataclasses import dataclass
@@ -28,6 +33,8 @@ MAGIC = 0x46554747
 BLOCK = {0: (1, 4), 1: (1, 2), 2: (32, 18), 8: (32, 34), 11: (256, 110), 12: (256, 144), 13: (256, 176),
          14: (256, 210), 20: (32, 18), 21: (256, 110), 23: (256, 136), 30: (1, 2)}
 Q4_K, Q5_K = 12, 13
+Q8_0 = 8
+FLOAT_TYPES = (0, 1, 30)  # f32, f16, bf16: kept as Q8_0 (GgufConvert.storedType, GgufConvert.swift:229-234)
 _MAX_KEPT_ARRAY = 4096
 _WIDTH = {0: 1, 1: 1, 7: 1, 2: 2, 3: 2, 4: 4, 5: 4, 6: 4, 10: 8, 11: 8, 12: 8}
 _FMT = {0: "<B", 1: "<b", 2: "<H", 3: "<h", 4: "<I", 5: "<i", 6: "<f", 7: "<B", 10: "<Q", 11: "<q", 12: "<d"}
@@ -165,24 +172,176 @@ class GgufFile:
         return self._map[t.offset:t.offset + t.byte_length]
 
 
-def load_weight(f, name, device="cuda"):
-    """A Q4_K or Q5_K matrix [rows, inner] as planes on the device (GgufPlanes.repack on the GPU),
-    rows rounded up to whole tiles by zero blocks (GgufConvert.swift:259-262)."""
+# ---- the gated-delta value heads (GgufNames.swift, GgufConvert.swift) -------------------------
+
+GDN_KEY_HEADS, GDN_VALUE_HEADS, GDN_HEAD_DIM = 16, 48, 128   # ModelGeometry (ModelWeights.swift:78-82)
+GDN_CHANNELS, GDN_VALUE_DIM = 10240, 6144
+CONV_TAPS = 4
+
+
+def mlx_value_head(i, key_heads=GDN_KEY_HEADS, value_heads=GDN_VALUE_HEADS):
+    """GgufNames.mlxValueHead: the engine's index of the value head a GGUF file stores as head i,
+    3 (i % 16) + i / 16 for 48 heads over 16 key heads."""
+    return (value_heads // key_heads) * (i % key_heads) + i // key_heads
+
+
+@dataclass(frozen=True)
+class HeadOrder:
+    """GgufConvert.HeadOrder: a tensor's value heads are `span` units each from unit `first` (a unit
+    being a row of a weight, a channel of the convolution or an element of a per-head vector)."""
+
+    first: int
+    span: int
+
+    def destination(self, unit, heads=GDN_VALUE_HEADS):
+        """The engine-order place of the file's unit `unit` (units outside the heads stay)."""
+        h = (unit - self.first) // self.span
+        if unit < self.first or h >= heads:
+            return unit
+        return self.first + mlx_value_head(h, value_heads=heads) * self.span + (unit - self.first) % self.span
+
+
+_VALUE_CHANNELS = HeadOrder(GDN_CHANNELS - GDN_VALUE_DIM, GDN_HEAD_DIM)
+# GgufConvert.ggufRole(ofBlockTensor:) for a gated-delta layer (GgufConvert.swift:340-352): the
+# weights whose rows, and the dense tensors whose units, are by value head.
+WEIGHT_HEAD_ORDER = {
+    "attn_qkv.weight": _VALUE_CHANNELS,
+    "attn_gate.weight": HeadOrder(0, GDN_HEAD_DIM),
+    "ssm_alpha.weight": HeadOrder(0, 1),
+    "ssm_beta.weight": HeadOrder(0, 1),
+}
+DENSE_HEAD_ORDER = {  # tail: (unit, head order, negated log)
+    "ssm_conv1d.weight": (CONV_TAPS, _VALUE_CHANNELS, False),
+    "ssm_a": (1, HeadOrder(0, 1), True),
+    "ssm_dt.bias": (1, HeadOrder(0, 1), False),
+}
+# The out projection has the heads as its inner columns, left in the file's order: its GEMM reads
+# the activations in that order instead (runtime.gemm(..., key_heads=GDN_KEY_HEADS)).
+COLUMN_HEAD_ORDER = ("ssm_out.weight",)
+
+
+def block_tail(name):
+    """The tensor's name below `blk.<n>.`, or None outside the blocks."""
+    if not name.startswith("blk."):
+        return None
+    rest = name[4:]
+    digits = len(rest) - len(rest.lstrip("0123456789"))
+    if digits == 0 or rest[digits:digits + 1] != ".":
+        return None
+    return rest[digits + 1:]
+
+
+def block_head_order(name, full_attention=False):
+    """The HeadOrder of a gated-delta layer's weight rows, or None (a full-attention layer has none)."""
+    tail = block_tail(name)
+    return None if full_attention or tail is None else WEIGHT_HEAD_ORDER.get(tail)
+
+
+def order_rows(native, rows, row_bytes, head_order, stored_rows=None, heads=GDN_VALUE_HEADS):
+    """GgufConvert.ggufPlanes' `order` (GgufConvert.swift:381-395): row r of the file goes to row
+    head_order.destination(r), whole rows of native blocks (lossless); rows past `rows` up to
+    `stored_rows` are zero blocks."""
+    native = np.asarray(native, np.uint8).reshape(rows, row_bytes)
+    stored = rows if stored_rows is None else stored_rows
+    out = np.zeros((stored, row_bytes), np.uint8)
+    if head_order is None:
+        out[:rows] = native
+    else:
+        dest = np.array([head_order.destination(r, heads) for r in range(rows)], np.int64)
+        out[dest] = native
+    return out.reshape(-1)
+
+
+def q8_0_blocks(values):
+    """GgufConvert.q8_0Blocks (GgufConvert.swift:236-257): fp32 values, 32 a block, as Q8_0 blocks
+    the way llama.cpp quantises: scale = largest magnitude / 127 (fp32), kept as fp16 (RNE); each
+    code = value x (1 / scale), rounded half away from zero, clamped to int8 (0 for a zero block)."""
+    v = np.asarray(values, np.float32).reshape(-1, 32)
+    largest = np.abs(v).max(axis=1)
+    scale = (largest / np.float32(127)).astype(np.float32)
+    with np.errstate(divide="ignore"):
+        inverse = np.where(scale > 0, np.float32(1) / scale, np.float32(0)).astype(np.float32)
+    x = (v * inverse[:, None]).astype(np.float32).astype(np.float64)
+    code = np.where(x >= 0, np.floor(x + 0.5), np.ceil(x - 0.5))
+    code = np.clip(code, -128, 127).astype(np.int8)
+    out = np.empty((v.shape[0], 34), np.uint8)
+    out[:, 0:2] = scale.astype(np.float16).view(np.uint8).reshape(-1, 2)
+    out[:, 2:] = code.view(np.uint8)
+    return out.reshape(-1)
+
+
+def float_values(f, name):
+    """A float-typed tensor's values as fp32 (f32, f16, bf16)."""
+    t = f.tensor(name)
+    raw = np.array(f.bytes(name))
+    if t.type == 0:
+        return raw.view(np.float32).copy()
+    if t.type == 1:
+        return raw.view(np.float16).astype(np.float32)
+    if t.type == 30:
+        return (raw.view(np.uint16).astype(np.uint32) << 16).view(np.float32)
+    raise GgufError(f"tensor {name} has ggml type {t.type}, not a float type")
+
+
+def bf16_rne(values):
+    """GgufConvert.bf16Bits(roundingToEven:) (GgufConvert.swift:264-268) for each value."""
+    bits = np.asarray(values, np.float32).view(np.uint32).astype(np.uint64)
+    return ((bits + 0x7FFF + ((bits >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def dense_bf16(values, unit=1, head_order=None, negated_log=False, heads=GDN_VALUE_HEADS):
+    """GgufConvert.ggufDense (GgufConvert.swift:432-457): fp32 values -> bf16 (RNE), the decay
+    turned back into A_log (the file holds -exp(A_log)), each unit of `unit` values moved to its
+    engine-order place."""
+    v = np.asarray(values, np.float32).reshape(-1)
+    if negated_log:
+        if not (v < 0).all():
+            raise GgufError("the decay holds a value that is not negative, so is not -exp of anything")
+        v = np.log(-v).astype(np.float32)
+    if not np.isfinite(v).all():
+        raise GgufError("a dense tensor holds a value that is not finite")
+    bits = bf16_rne(v)
+    out = np.empty_like(bits)
+    idx = np.arange(v.size)
+    dest_unit = idx // unit if head_order is None else np.array(
+        [head_order.destination(u, heads) for u in range(v.size // unit)], np.int64)[idx // unit]
+    out[dest_unit * unit + idx % unit] = bits
+    return out
+
+
+def load_weight(f, name, device="cuda", full_attention=False):
+    """A packed matrix [rows, inner] on the device in the form its kernels read: Q4_K / Q5_K as planes
+    (GgufPlanes.repack on the GPU), the other formats in their native blocks, a float type as Q8_0
+    blocks; a gated-delta layer's head-ordered rows in the engine's order (GgufConvert.ggufPlanes,
+    GgufConvert.swift:370-430). Planes round the rows up to whole tiles by zero blocks
+    (GgufConvert.swift:259-262)."""
     import torch
     from . import runtime as rt
     t = f.tensor(name)
-    if t.type in rt.GGUF_NATIVE:
+    order = block_head_order(name, full_attention)
+    if t.type in FLOAT_TYPES:
+        if len(t.dims) != 2 or t.inner % 32:
+            raise GgufError(f"tensor {name} is a dense float tensor (dims {t.dims}); the device kernels take packed "
+                            "matrices (a float matrix is requantised to Q8_0, whole 32-element blocks a row); "
+                            "dense tensors convert with dense_bf16")
+        native = q8_0_blocks(float_values(f, name))
+        gtype = Q8_0
+    else:
+        native = np.array(f.bytes(name))
+        gtype = t.type
+    if gtype in rt.GGUF_NATIVE:
         # Q8_0, Q3_K, Q6_K, IQ4_NL, IQ3_S, IQ4_XS stay in their native blocks.
-        native = torch.from_numpy(np.array(f.bytes(name))).to(device)
-        return rt.GgufWeight(native, t.type, t.rows, t.inner)
+        elems, size = rt.GGUF_NATIVE[gtype]
+        if order is not None:
+            native = order_rows(native, t.rows, t.inner // elems * size, order)
+        return rt.GgufWeight(torch.from_numpy(np.ascontiguousarray(native)).to(device), gtype, t.rows, t.inner)
     if t.type not in (Q4_K, Q5_K):
         raise GgufError(f"tensor {name} has ggml type {t.type}; the device kernels take Q4_K, Q5_K, Q3_K, "
                         "Q6_K, Q8_0, IQ4_NL, IQ3_S and IQ4_XS")
     rows, inner = t.rows, t.inner
     stored = -(-rows // 128) * 128
     block = BLOCK[t.type][1]
-    native = np.zeros(stored * (inner // 256) * block, np.uint8)
-    native[: t.byte_length] = f.bytes(name)
+    native = order_rows(native, rows, inner // 256 * block, order, stored_rows=stored)
     dev = torch.from_numpy(native).to(device)
     if t.type == Q5_K:
         return rt.q5k_repack(dev, stored, inner)

@@ -175,6 +175,11 @@ def workspace_bytes(rows, columns, inner):
     return _lib.lib().splosh_workspace_bytes(rows, columns, inner)
 
 
+def heads_workspace_bytes(rows, columns, inner):
+    """splosh_heads_workspace_bytes: the workspace a head-ordered GGUF GEMM needs."""
+    return _lib.lib().splosh_heads_workspace_bytes(rows, columns, inner)
+
+
 class _Scratch:
     """The split-K scratch of one call: (pointer, bytes), and the tensor that owns it, held by the
     caller until the kernel has been launched."""
@@ -186,7 +191,7 @@ class _Scratch:
         return iter((self.ptr, self.nbytes))
 
 
-def _workspace(workspace, rows, n, inner, device, stream=None):
+def _workspace(workspace, rows, n, inner, device, stream=None, heads=False):
     """The split-K scratch of the kernels: the caller's tensor (an empty one: none), or a fresh one
     from torch's stream-ordered allocator sized by splosh_workspace_bytes. A fresh one is
     zero-filled and allocated on the stream the kernel runs on, so the fill is ordered before the
@@ -197,7 +202,7 @@ def _workspace(workspace, rows, n, inner, device, stream=None):
         return _Scratch(None, 0)
     if workspace is not None:
         return _Scratch(_ptr(workspace), workspace.numel() * workspace.element_size(), workspace)
-    need = _lib.lib().splosh_workspace_bytes(rows, n, inner)
+    need = (_lib.lib().splosh_heads_workspace_bytes if heads else _lib.lib().splosh_workspace_bytes)(rows, n, inner)
     if need == 0:
         return _Scratch(None, 0)
     with torch.cuda.stream(_on(stream)):
@@ -206,11 +211,13 @@ def _workspace(workspace, rows, n, inner, device, stream=None):
 
 
 def gemm(w, a, out=None, residual=None, out_dtype=torch.bfloat16, kernel=AUTO, rows=None, stream=None,
-         workspace=None):
+         workspace=None, key_heads=0):
     """Engine.gemm (Runtime/Engine.swift:1652-1806): out = a @ dequant(w)^T (+ residual).
 
     ``a`` is bf16 [rows, inner] (row stride a.stride(0)); ``out`` [rows, w.rows] in fp32 or bf16;
-    ``residual`` may be ``out`` itself."""
+    ``residual`` may be ``out`` itself. ``key_heads`` > 0 (GGUF weights only): the weight's inner
+    columns are in a GGUF file's value-head order and the activations in the engine's (the `heads`
+    kernels, engine_gguf.metal:55-72)."""
     rows = a.shape[0] if rows is None else rows
     if a.dtype != torch.bfloat16:
         raise SploshError(13, "activations must be bf16")
@@ -222,14 +229,27 @@ def gemm(w, a, out=None, residual=None, out_dtype=torch.bfloat16, kernel=AUTO, r
     if residual is not None:
         if residual.dtype != out.dtype or residual.stride(0) != out.stride(0):
             raise SploshError(13, "residual must match the output's dtype and row stride")
-    scratch = _workspace(workspace, rows, w.rows, w.inner, a.device, stream)  # held until the launch
+    if key_heads and isinstance(w, Q4Weight):
+        raise SploshError(13, "the value-head order applies to GGUF weights only")
+    scratch = _workspace(workspace, rows, w.rows, w.inner, a.device, stream, heads=bool(key_heads))  # held until the launch
     ws, ws_bytes = scratch
     if isinstance(w, GgufWeight):
-        _lib.check(_lib.lib().splosh_gguf_gemm(w.gguf_type, _ptr(w.native), w.rows, w.inner, _ptr(a), a.stride(0),
-                                               _ptr(out), out.stride(0), _dtype_code(out.dtype), _ptr(residual),
-                                               rows, ws, ws_bytes, _stream(stream)))
+        if key_heads:
+            st = _lib.lib().splosh_gguf_gemm_heads(w.gguf_type, _ptr(w.native), w.rows, w.inner, key_heads, _ptr(a),
+                                                   a.stride(0), _ptr(out), out.stride(0), _dtype_code(out.dtype),
+                                                   _ptr(residual), rows, ws, ws_bytes, _stream(stream))
+        else:
+            st = _lib.lib().splosh_gguf_gemm(w.gguf_type, _ptr(w.native), w.rows, w.inner, _ptr(a), a.stride(0),
+                                             _ptr(out), out.stride(0), _dtype_code(out.dtype), _ptr(residual),
+                                             rows, ws, ws_bytes, _stream(stream))
+        _lib.check(st)
         return out
     wc = w.c()
+    if key_heads:
+        fn = _lib.lib().splosh_q4k_gemm_heads if isinstance(w, Q4KWeight) else _lib.lib().splosh_q5k_gemm_heads
+        _lib.check(fn(ctypes.byref(wc), key_heads, _ptr(a), a.stride(0), _ptr(out), out.stride(0),
+                      _dtype_code(out.dtype), _ptr(residual), rows, kernel, ws, ws_bytes, _stream(stream)))
+        return out
     if isinstance(w, Q4Weight):
         st = _lib.lib().splosh_q4_gemm(ctypes.byref(wc), _ptr(a), a.stride(0), _ptr(out), out.stride(0),
                                        _dtype_code(out.dtype), _ptr(residual), rows, kernel, ws, ws_bytes,
