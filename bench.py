@@ -174,7 +174,9 @@ def build_workload(name, rt, torch, gen, kernel):
     if name == "layerset":
         # Config 4: every linear projection of one hybrid layer set at M=64 (shapes as BASELINE.json
         # states them): attention q, k, v, o; gated-delta input (qkv+z+b/a, 12288 outputs) and
-        # output (6144 -> 5120); the MLP's fused gate+up and down. One step is all nine launches.
+        # output (6144 -> 5120); the MLP's fused gate+up and down. The attention layer's q, k and v
+        # read one activation and go as one grouped launch (splosh_q4_gemm_group, the reference's
+        # concurrent encoder); one step is six launches over the nine weights.
         m, h = 64, 5120
         shapes = [("attn_q", 5120, h), ("attn_k", 1024, h), ("attn_v", 1024, h), ("attn_o", 5120, h),
                   ("gdn_in", 12288, h), ("gdn_out", 5120, 6144), ("mlp_gate", 17408, h), ("mlp_up", 17408, h),
@@ -185,21 +187,27 @@ def build_workload(name, rt, torch, gen, kernel):
         xs = {k: torch.randn(m, k, device="cuda", generator=gen).to(torch.bfloat16) for k in (h, 6144, 17408)}
         outs = {nm: torch.empty(m, n, dtype=torch.bfloat16, device="cuda") for nm, n, _ in shapes}
         scratch = {nm: workspace(m, n, k) for nm, n, k in shapes}
-        calls = [(nm, n, k) for nm, n, k in shapes if nm not in ("mlp_gate", "mlp_up")]
+        scratch["attn_qkv"] = workspace(m, 7168, h)
+        qkv = ("attn_q", "attn_k", "attn_v")
+        calls = [(nm, n, k) for nm, n, k in shapes if nm not in ("mlp_gate", "mlp_up") + qkv]
 
         def launches(i):
             ws_ = sets[i % ncopy]
-            out = [(nm, lambda nm=nm, k=k: rt.gemm(ws_[nm], xs[k], out=outs[nm], kernel=kernel, workspace=scratch[nm]))
-                   for nm, n, k in calls]
+            out = [("attn_qkv", lambda: rt.gemm_group([ws_[nm] for nm in qkv], xs[h], outs=[outs[nm] for nm in qkv],
+                                                      kernel=kernel, workspace=scratch["attn_qkv"]))]
+            out += [(nm, lambda nm=nm, k=k: rt.gemm(ws_[nm], xs[k], out=outs[nm], kernel=kernel, workspace=scratch[nm]))
+                    for nm, n, k in calls]
             out.append(("mlp_in", lambda: rt.mlp_in(ws_["mlp_gate"], ws_["mlp_up"], xs[h], out=outs["mlp_gate"],
                                                     kernel=kernel, workspace=scratch["mlp_gate"])))
             return out
 
         kb = {nm: q4_bytes(n, k) + m * k * 2 + m * n * 2 for nm, n, k in calls}
+        kb["attn_qkv"] = q4_bytes(7168, h) + m * h * 2 + m * 7168 * 2
         kb["mlp_in"] = 2 * q4_bytes(17408, h) + m * h * 2 + m * 17408 * 2
         kf = {nm: 2 * m * n * k for nm, n, k in calls}
+        kf["attn_qkv"] = 2 * m * 7168 * h
         kf["mlp_in"] = 4 * m * 17408 * h
-        cfg = {"workload": "layer set at M=64: attention q/k/v/o, gated-delta in/out, MLP gate+up and down",
+        cfg = {"workload": "layer set at M=64: attention q/k/v (grouped) and o, gated-delta in/out, MLP gate+up and down",
                "rows": m, "format": "mlx affine q4 g64, tiled128", "weight_copies": ncopy}
         return launches, sum(kb.values()), sum(kf.values()), kb, cfg, kf
     if name.startswith("stream"):

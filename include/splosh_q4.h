@@ -187,6 +187,20 @@ int splosh_q4_gemm_emit(const splosh_q4_weight *w, const uint16_t *a, int64_t ld
 int splosh_q4_gemm_noalloc(const splosh_q4_weight *w, const uint16_t *a, int64_t lda, void *out, int64_t ldc,
                            int out_dtype, const void *residual, int64_t rows, int kernel, hipStream_t stream);
 
+/* Several projections of one activation in one launch: the reference encodes a layer's independent
+ * projections (q, k and v of an attention layer; qkv and z of a gated-delta layer) into one
+ * concurrent encoder so that they overlap (Runtime/Engine.swift:1402, SploshCore/CommandGraph.swift:
+ * 57-62; the GEMMs at Engine.swift:1131-1140). out_i = a @ dequant(w_i)^T for i < count
+ * (count <= SPLOSH_MAX_GROUP), each into its own output (row stride ldcs[i], out_dtype), no
+ * residual. All weights share inner. Up to 64 rows with TILED128 weights (rows % 64 == 0) the
+ * group is one launch of the M <= 64 kernel over the weights' joined column bands, split over the
+ * CUs as one call (workspace: splosh_workspace_bytes(rows, sum of the weights' rows, inner));
+ * otherwise each weight is its own splosh_q4_gemm call, same results to the path's tolerance. */
+#define SPLOSH_MAX_GROUP 8
+int splosh_q4_gemm_group(const splosh_q4_weight *weights, int count, const uint16_t *a, int64_t lda,
+                         void *const *outs, const int64_t *ldcs, int out_dtype, int64_t rows, int kernel,
+                         void *workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* Engine.mlpIn(gate:up:input:output:scratch:rows:) (Runtime/Engine.swift:1911-1966) with the
  * fused lane form sp_mlp_in_tiled_* (Shaders/engine.metal:1987-2055): out = silu(gate(a)) * up(a),
  * both weights read in one pass over a. AUTO as splosh_q4_gemm: above 64 rows, tiled weights take

@@ -88,6 +88,8 @@ SIGNATURES = {
     "splosh_q4_mlp_in": (_int, [ctypes.POINTER(Q4Weight), ctypes.POINTER(Q4Weight), _vp, _i64, _vp, _i64, _int,
                                 _i64, _int, _vp, _sz, _vp]),
     "splosh_q4_dequant": (_int, [ctypes.POINTER(Q4Weight), _vp, _vp]),
+    "splosh_q4_gemm_group": (_int, [ctypes.POINTER(Q4Weight), _int, _vp, _i64, ctypes.POINTER(_vp),
+                                    ctypes.POINTER(_i64), _int, _i64, _int, _vp, _sz, _vp]),
     "splosh_tile128": (_int, [_vp, _vp, _i64, _i64, _i64, _vp]),
     "splosh_untile128": (_int, [_vp, _vp, _i64, _i64, _i64, _vp]),
     "splosh_q5k_gemm": (_int, [ctypes.POINTER(Q5KWeight), _vp, _i64, _vp, _i64, _int, _vp, _i64, _int, _vp, _sz,

@@ -441,6 +441,41 @@ int splosh_q4_gemm_noalloc(const splosh_q4_weight *w, const uint16_t *a, int64_t
     return q4_gemm_impl(w, nullptr, a, lda, out, ldc, out_dtype, residual, rows, kernel, ptr, kScratchBytes, stream);
 }
 
+int splosh_q4_gemm_group(const splosh_q4_weight *weights, int count, const uint16_t *a, int64_t lda,
+                         void *const *outs, const int64_t *ldcs, int out_dtype, int64_t rows, int kernel,
+                         void *workspace, size_t workspace_bytes, hipStream_t stream) {
+    if (!weights || !outs || !ldcs) return fail(SPLOSH_ERR_NULL_POINTER, "null weight, output or ldc list");
+    if (count < 1 || count > SPLOSH_MAX_GROUP)
+        return fail(SPLOSH_ERR_INVALID_SHAPE, "count must be 1.." + std::to_string(SPLOSH_MAX_GROUP));
+    int st;
+    int64_t columns = 0;
+    bool joined = rows <= 64 && (kernel == SPLOSH_KERNEL_AUTO || kernel == SPLOSH_KERNEL_DEQUANT) && lda % 8 == 0 &&
+                  aligned(a, 16);
+    for (int i = 0; i < count; ++i) {
+        const splosh_q4_weight *w = &weights[i];
+        if ((st = check_q4_weight(w, "weight"))) return st;
+        if (w->inner != weights[0].inner) return fail(SPLOSH_ERR_INVALID_SHAPE, "grouped weights must share inner");
+        if ((st = check_io(a, lda, outs[i], ldcs[i], out_dtype, rows, w->rows, w->inner))) return st;
+        joined = joined && w->order == SPLOSH_Q4_TILED128 && aligned(w->packed, 16) &&
+                 splosh::mma_fits(rows, w->rows, w->inner, w->row_stride_words, lda);
+        columns += w->rows;
+    }
+    joined = joined && splosh::mma_fits(rows, columns, weights[0].inner, 0, lda) &&
+             columns * (weights[0].inner / kGroupSize) * 32 < ((int64_t)1 << 32) - 256;
+    if (!joined) {
+        for (int i = 0; i < count; ++i)
+            if ((st = q4_gemm_impl(&weights[i], nullptr, a, lda, outs[i], ldcs[i], out_dtype, nullptr, rows, kernel,
+                                   workspace, workspace_bytes, stream)))
+                return st;
+        return ok();
+    }
+    const splosh::MmaPlan plan =
+        splosh::plan_mma(rows, columns, weights[0].inner / kGroupSize, false, workspace ? workspace_bytes : 0);
+    return hip_status(splosh::launch_q4_mma_group(plan, weights, count, outs, ldcs, a, lda, out_dtype, rows, workspace,
+                                                  stream),
+                      "q4 grouped mma launch");
+}
+
 int splosh_q4_mlp_in(const splosh_q4_weight *gate, const splosh_q4_weight *up, const uint16_t *a, int64_t lda,
                      void *out, int64_t ldc, int out_dtype, int64_t rows, int kernel, void *workspace,
                      size_t workspace_bytes, hipStream_t stream) {

@@ -74,6 +74,10 @@ bool mma_fits(int64_t rows, int64_t columns, int64_t inner, int64_t stride_words
 MmaPlan plan_mma(int64_t rows, int64_t columns, int64_t groups, bool mlp, size_t workspace_bytes,
                  int64_t unit_elems = 64);
 size_t mma_workspace_bytes(int64_t rows, int64_t columns, int64_t groups, bool mlp);
+hipError_t launch_q4_mma_group(const MmaPlan &plan, const splosh_q4_weight *w, int count, void *const *outs,
+                               const int64_t *ldcs, const uint16_t *a, int64_t lda, int out_dtype, int64_t rows,
+                               void *workspace, hipStream_t stream);
+
 // The next RMSNorm's operand a residual projection emits (SpNaEmit, engine_na.metal:26-36).
 struct EmitOperand {
     const uint16_t *norm_weight;  // bf16 [n]

@@ -42,6 +42,7 @@ constexpr int kDeviceCpol = 1 | 16;
 namespace splosh {
 
 constexpr int kMmaMaxGrid = 1024;  // workgroups of a stream-K launch
+constexpr int kMmaMaxGroup = SPLOSH_MAX_GROUP;  // weights of a grouped call
 
 // a / b for 0 <= a, 0 < b, in 32 bits when both fit (the stream-K bookkeeping divides wave-uniform
 // values; a 64-bit division is a long VALU sequence, a 32-bit one a short one).
@@ -82,6 +83,21 @@ struct MmaArgs {
     uint16_t *values;
     int64_t ldv;
     float *sums, *squares;   // [rows][n / 64]
+    // A grouped call (several tiled weights on one activation, one launch): weight i owns bands
+    // [gband[i], gband[i + 1]) of the band space and writes its own output; n, out, ldc and the
+    // weight pointers above are unused.
+    int ngroup;
+    int gband[kMmaMaxGroup + 1];
+    const uint32_t *gpacked[kMmaMaxGroup];
+    const uint16_t *gscales[kMmaMaxGroup], *gbiases[kMmaMaxGroup];
+    void *gout[kMmaMaxGroup];
+    int64_t gn[kMmaMaxGroup], gldc[kMmaMaxGroup];
+    // The weight of a grouped call that owns `band` (wave-uniform; a short scalar loop).
+    __device__ int group_of(int band) const {
+        int gi = 0;
+        for (int i = 1; i < ngroup; ++i) gi = band >= gband[i] ? i : gi;
+        return gi;
+    }
 };
 
 // q4 (MLX affine): a step is KW groups of 64; wave kw takes group ga + t KW + kw and lane (r, h)
@@ -94,8 +110,13 @@ struct MmaArgs {
 // l < 8 KW bytes 16 (l & 7) .. of group l >> 3's 128-byte run (groups past the job re-read the
 // last one). LDS layout per buffer: [weight][array][group][column]. Row-major weights load the
 // sidecars per lane with the codes.
-template <int NW_, bool TILED, int CW, int KW, int D>
+//
+// GROUPED (one tiled weight a band, of a grouped call): each job takes its band's weight, buffer
+// resources and column offset from the group table.
+template <int NW_, bool TILED, int CW, int KW, int D, bool GROUPED = false>
 struct Q4Format {
+    static_assert(!GROUPED || (NW_ == 1 && TILED), "grouped calls take single tiled weights");
+    static constexpr bool kGrouped = GROUPED;
     static constexpr int NW = NW_;
     static constexpr bool kStageSide = TILED;
     static constexpr int kWLoads = kStageSide ? NW : NW * 3;  // weight loads per wave and step
@@ -111,6 +132,7 @@ struct Q4Format {
     int wave, lane, kw, cw, r, h, ga, gb;
     uint32_t G32, q_lane, side_lane, q_group, side_group, side_src;
     int side_g;      // group (within a step) of this lane's staged sidecar piece
+    bool side_bias;  // the array this wave stages: biases (else scales)
     u32x4 wq[D][NW];
     uint32_t wsc[D][NW], wbi[D][NW];
     float cs[NW], cb[NW];  // scale and bias of the step being dequantized
@@ -133,7 +155,8 @@ struct Q4Format {
         const int piece0 = wave * kSidePer;
         const int arr = piece0 / (KW * 8);
         const int side_w = (arr >> 1) < NW ? (arr >> 1) : 0;
-        side_rsrc = make_rsrc((arr & 1) ? (const void *)args.biases[side_w] : (const void *)args.scales[side_w],
+        side_bias = (arr & 1) != 0;
+        side_rsrc = make_rsrc(side_bias ? (const void *)args.biases[side_w] : (const void *)args.scales[side_w],
                               args.sidecar_bytes);
         side_g = ((piece0 + lane) / 8) % KW;
     }
@@ -142,8 +165,17 @@ struct Q4Format {
     __device__ void begin(const MmaArgs &args, int band, int ga_, int gb_) {
         ga = ga_;
         gb = gb_;
+        int64_t n = args.n;
+        if constexpr (GROUPED) {
+            const int gi = args.group_of(band);
+            band -= args.gband[gi];
+            n = args.gn[gi];
+            q_rsrc[0] = make_rsrc(args.gpacked[gi], (uint32_t)n * G32 * 32u);
+            side_rsrc = make_rsrc(side_bias ? (const void *)args.gbiases[gi] : (const void *)args.gscales[gi],
+                                  (uint32_t)n * G32 * 2u);
+        }
         const int64_t ncol = (int64_t)band * kBandCols + cw * 32 + r;
-        const uint32_t col = (uint32_t)(ncol < args.n ? ncol : args.n - 1);
+        const uint32_t col = (uint32_t)(ncol < n ? ncol : n - 1);
         if (TILED) {
             const uint32_t rec0 = (col >> 7) * G32 * 128u + (col & 127u);  // record of group 0
             q_lane = rec0 * 32u + 16u * h;
@@ -237,6 +269,7 @@ struct Q4Format {
 // FIFTH = false: Q4_K (no plane1; the codes are the nibbles).
 template <int CW, int KW, int D, bool FIFTH = true>
 struct Q5Format {
+    static constexpr bool kGrouped = false;
     static constexpr int NW = 1;
     static constexpr int kWLoads = FIFTH ? 2 : 1;  // loads per wave and step: the mid-step wait counts them
     static constexpr int kUnitK = 256;
@@ -660,6 +693,15 @@ mma_kernel(MmaArgs args) {
     const int bcol = cw * 32 + r;
     // The epilogue of a finished band: every wave calls it (the emit's band sums meet in LDS).
     auto store_out = [&](int band, const f32x4 (&v)[NW][FM]) {
+        void *out = args.out;
+        int64_t ldc = args.ldc, n = args.n;
+        if constexpr (F::kGrouped) {
+            const int gi = args.group_of(band);
+            out = args.gout[gi];
+            ldc = args.gldc[gi];
+            n = args.gn[gi];
+            band -= args.gband[gi];
+        }
         const int64_t ocol = (int64_t)band * S::kBandCols + bcol;
         float hv[FM][4];
 #pragma unroll
@@ -670,14 +712,14 @@ mma_kernel(MmaArgs args) {
                 float value = v[0][f][i];
                 if constexpr (NW == 2) value = silu(v[0][f][i]) * v[1][f][i];
                 hv[f][i] = value;
-                if (m >= rows || ocol >= args.n) continue;
-                const int64_t index = (int64_t)m * args.ldc + ocol;
+                if (m >= rows || ocol >= n) continue;
+                const int64_t index = (int64_t)m * ldc + ocol;
                 if (args.out_dtype == SPLOSH_F32) {
                     if (args.residual) value += ((const float *)args.residual)[index];
-                    ((float *)args.out)[index] = value;
+                    ((float *)out)[index] = value;
                 } else {
                     if (args.residual) value += bf16_bits_to_f32(((const uint16_t *)args.residual)[index]);
-                    ((uint16_t *)args.out)[index] = f32_to_bf16(value);
+                    ((uint16_t *)out)[index] = f32_to_bf16(value);
                 }
                 hv[f][i] = value;
             }
@@ -995,8 +1037,8 @@ static hipError_t launch_mma_fm(const MmaPlan &p, const MmaArgs &args, hipStream
     return p.fm == 1 ? launch_mma_v<F, 1>(p, args, stream) : launch_mma_v<F, 2>(p, args, stream);
 }
 
-template <int NW, bool TILED>
-using Q4F = Q4Format<NW, TILED, kMmaCW, kMmaKW, kMmaDepth>;
+template <int NW, bool TILED, bool GROUPED = false>
+using Q4F = Q4Format<NW, TILED, kMmaCW, kMmaKW, kMmaDepth, GROUPED>;
 
 static void set_io(MmaArgs &args, const MmaPlan &plan, const uint16_t *a, int64_t lda, void *out, int64_t ldc,
                    int out_dtype, const void *residual, int64_t rows, int64_t inner, void *workspace, bool mlp) {
@@ -1046,6 +1088,39 @@ hipError_t launch_q4_mma(const MmaPlan &plan, const splosh_q4_weight &w, const s
     else
         err = tiled ? launch_mma_fm<Q4F<1, true>>(plan, args, stream) : launch_mma_fm<Q4F<1, false>>(plan, args, stream);
     return err;
+}
+
+// Several tiled weights of one inner size on one activation (the reference's concurrent encoder of
+// independent projections, Engine.swift:1402): their bands form one band space, split as one call.
+hipError_t launch_q4_mma_group(const MmaPlan &plan, const splosh_q4_weight *w, int count, void *const *outs,
+                               const int64_t *ldcs, const uint16_t *a, int64_t lda, int out_dtype, int64_t rows,
+                               void *workspace, hipStream_t stream) {
+    MmaArgs args = {};
+    const int64_t groups = w[0].inner / kGroup;
+    args.units = groups;
+    args.ngroup = count;
+    int band = 0;
+    for (int i = 0; i < count; ++i) {
+        args.gband[i] = band;
+        args.gpacked[i] = w[i].packed;
+        args.gscales[i] = w[i].scales;
+        args.gbiases[i] = w[i].biases;
+        args.gout[i] = outs[i];
+        args.gn[i] = w[i].rows;
+        args.gldc[i] = ldcs[i];
+        band += (int)(w[i].rows / (kMmaCW * 32));
+    }
+    args.gband[count] = band;
+    // The first weight's pointers stand in for the single-weight fields (never read for codes).
+    args.packed[0] = args.packed[1] = w[0].packed;
+    args.scales[0] = args.scales[1] = w[0].scales;
+    args.biases[0] = args.biases[1] = w[0].biases;
+    args.n = w[0].rows;
+    args.stride_words = w[0].row_stride_words;
+    set_io(args, plan, a, lda, outs[0], ldcs[0], out_dtype, nullptr, rows, w[0].inner, workspace, false);
+    args.code_bytes = (uint32_t)(w[0].rows * groups * 32);
+    args.sidecar_bytes = (uint32_t)(w[0].rows * groups * 2);
+    return launch_mma_fm<Q4F<1, true, true>>(plan, args, stream);
 }
 
 hipError_t launch_q5k_mma(const MmaPlan &plan, const splosh_q5k_weight &w, const uint16_t *a, int64_t lda, void *out,

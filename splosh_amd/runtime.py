@@ -39,7 +39,9 @@ def _stream(stream=None):
 
 
 def _require(t, nbytes, name):
-    have = t.numel() * t.element_size()
+    # The bytes the pointer may address: to the end of the tensor's storage (a strided view of a
+    # larger buffer reaches past its own elements).
+    have = t.untyped_storage().nbytes() - t.storage_offset() * t.element_size()
     if have < nbytes:
         raise GemmQ4Error(8, f"bufferTooSmall(name: {name}, expected: {nbytes}, observed: {have})")
     if not t.is_cuda:
@@ -260,6 +262,34 @@ def gemm(w, a, out=None, residual=None, out_dtype=torch.bfloat16, kernel=AUTO, r
                 _ptr(residual), rows, kernel, ws, ws_bytes, _stream(stream))
     _lib.check(st)
     return out
+
+
+def gemm_group(weights, a, outs=None, out_dtype=torch.bfloat16, kernel=AUTO, rows=None, stream=None,
+               workspace=None):
+    """Several projections of one activation in one launch (the reference's concurrent encoder of a
+    layer's independent projections, Engine.swift:1402, 1131-1140): [a @ dequant(w)^T for w in
+    weights], each in its own output. Returns the outputs."""
+    rows = a.shape[0] if rows is None else rows
+    if a.dtype != torch.bfloat16 or a.stride(-1) != 1:
+        raise SploshError(13, "activations must be bf16 with contiguous rows")
+    weights = list(weights)
+    if outs is None:
+        outs = [None] * len(weights)
+    outs = [_out(a, rows, w.rows, o, out_dtype, stream) for w, o in zip(weights, outs)]
+    _require(a, ((rows - 1) * a.stride(0) + weights[0].inner) * 2, "a")
+    for w, o in zip(weights, outs):
+        _require(o, ((rows - 1) * o.stride(0) + w.rows) * o.element_size(), "output")
+        if o.dtype != outs[0].dtype:
+            raise SploshError(13, "grouped outputs must share one dtype")
+    scratch = _workspace(workspace, rows, sum(w.rows for w in weights), weights[0].inner, a.device, stream)
+    ws, ws_bytes = scratch
+    wcs = (_lib.Q4Weight * len(weights))(*[w.c() for w in weights])
+    out_ptrs = (ctypes.c_void_p * len(outs))(*[_ptr(o) for o in outs])
+    ldcs = (ctypes.c_int64 * len(outs))(*[o.stride(0) for o in outs])
+    _lib.check(_lib.lib().splosh_q4_gemm_group(wcs, len(weights), _ptr(a), a.stride(0), out_ptrs, ldcs,
+                                               _dtype_code(outs[0].dtype), rows, kernel, ws, ws_bytes,
+                                               _stream(stream)))
+    return outs
 
 
 def gemm_emit(w, a, norm_weight, out=None, residual=None, kernel=AUTO, rows=None, stream=None, workspace=None):

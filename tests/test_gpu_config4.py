@@ -103,3 +103,57 @@ def test_workspace_shared_across_shapes(rt):
         assert np.array_equal(first, again), f"{kind} rows={rows}: second call differs"
     # Every counter is back at zero.
     assert int(ws[:16384].view(torch.int32).abs().sum().item()) == 0
+
+
+@pytest.mark.parametrize("rows", [1, 8, 33, 64, 100])
+def test_gemm_group_attention_qkv(rt, rows):
+    """Config 4's attention inputs, q (5120 x 5120), k and v (5120 -> 1024), as one grouped call:
+    one launch of the M <= 64 kernel over their joined bands (rows <= 64), three calls above; each
+    output against the oracle on sampled columns (bf16 out)."""
+    k = 5120
+    shapes = (5120, 1024, 1024)
+    ws = [_full_size_weight(rt, n, k, seed=300 + i) for i, n in enumerate(shapes)]
+    a_bits = oracle.bf16_normal((rows, k), seed=310 + rows)
+    outs = rt.gemm_group(ws, bf16_tensor(a_bits))
+    for i, (w, out, n) in enumerate(zip(ws, outs, shapes)):
+        assert tuple(out.shape) == (rows, n)
+        cols = np.sort(np.random.default_rng(320 + i).choice(n, 192, replace=False))
+        ref, absref = _sampled_reference(w, a_bits, cols)
+        check_close(to_f32(out)[:, cols], ref, bf16_out=True, tight=True, absref=absref,
+                    label=f"group weight {i} rows={rows}")
+
+
+def test_gemm_group_small_shapes_and_workspace(rt):
+    """Four small tiled weights of different widths into strided fp32 outputs of one buffer, twice
+    on one shared workspace (same results; every counter back at zero), against the oracle on
+    every column; and the argument checks."""
+    k = 1024
+    cases = [Q4Case(n, k, seed=330 + n) for n in (128, 384, 256, 640)]
+    ws = [c.w_tiled for c in cases]
+    total = sum(c.n for c in cases)
+    rows = 40
+    a_bits = oracle.bf16_normal((rows, k), seed=341)
+    buf = torch.zeros(rows, total + 16, dtype=torch.float32, device="cuda")
+    views, c0 = [], 0
+    for c in cases:
+        views.append(buf[:, c0:c0 + c.n])
+        c0 += c.n
+    need = rt.workspace_bytes(rows, total, k)
+    scratch = torch.zeros(max(need, 16384), dtype=torch.uint8, device="cuda")
+    rt.gemm_group(ws, bf16_tensor(a_bits), outs=views, workspace=scratch)
+    first = buf.cpu().numpy().copy()
+    c0 = 0
+    for c in cases:
+        ref = oracle.gemm_a_bf16_w_f32(a_bits, c.dense)
+        check_close(first[:, c0:c0 + c.n], ref, bf16_out=False, tight=True, absref=abs_gemm(a_bits, c.dense),
+                    label=f"group n={c.n}")
+        c0 += c.n
+    assert not first[:, total:].any()  # columns past the views untouched
+    rt.gemm_group(ws, bf16_tensor(a_bits), outs=views, workspace=scratch)
+    assert np.array_equal(first, buf.cpu().numpy())
+    assert int(scratch[:16384].view(torch.int32).abs().sum().item()) == 0
+    from splosh_amd._lib import SploshError
+    with pytest.raises(SploshError):
+        rt.gemm_group(ws + [Q4Case(128, 512, seed=1).w_tiled], bf16_tensor(a_bits))  # inner differs
+    with pytest.raises(SploshError):
+        rt.gemm_group(ws * 3, bf16_tensor(a_bits))  # more than SPLOSH_MAX_GROUP
