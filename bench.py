@@ -264,8 +264,9 @@ def build_workload(name, rt, torch, gen, kernel):
     if name == "emit64":
         # The MLP's down projection at M=64 as the residual projection that feeds the next RMSNorm:
         # fp32 hidden state += a w^T, and the next GEMM's operand (bf16 h * norm weight, per-64 sums
-        # and sums of squares). "fused": the emit in the GEMM's epilogue (splosh_q4_gemm_emit);
-        # "separate": the GEMM, then the operand pass over the hidden state.
+        # and sums of squares). "fused": the emit in the GEMM's epilogue (splosh_q4_gemm_emit with
+        # the DEQUANT kernel); "separate": the GEMM, then the operand pass over the hidden state (what
+        # splosh_q4_gemm_emit runs under AUTO).
         m, h, inter = 64, 5120, 17408
         ncopy = copies_for(q4_bytes(h, inter))
         ws = [make_q4(rt, h, inter, gen) for _ in range(ncopy)]
@@ -280,7 +281,7 @@ def build_workload(name, rt, torch, gen, kernel):
 
         def launches(i):
             w = ws[i % ncopy]
-            return [("fused", lambda: rt.gemm_emit(w, x, wn, out=hid, residual=hid, workspace=scr)),
+            return [("fused", lambda: rt.gemm_emit(w, x, wn, out=hid, residual=hid, kernel=rt.DEQUANT, workspace=scr)),
                     ("separate", lambda: (rt.gemm(w, x, out=hid, residual=hid, out_dtype=torch.float32, workspace=scr),
                                           rt.emit_operand(hid, wn, values=be, sums=se, squares=qe)))]
 

@@ -169,8 +169,8 @@ int splosh_q4_gemm(const splosh_q4_weight *w, const uint16_t *a, int64_t lda, vo
  * writes the next RMSNorm-ed GEMM's operand from the same values: values = bf16(out * norm_weight)
  * (RNE, [rows][ld_values]), and per row and per 64 columns the sums of those rounded values and of
  * out * out (fp32 [rows][w->rows / 64]), as splosh_emit_operand computes them. w->rows % 64 == 0.
- * The M <= 64 kernel (AUTO for 3..64 rows) writes them from its epilogue; other row counts run the
- * GEMM and then the operand pass. */
+ * With SPLOSH_KERNEL_DEQUANT (rows <= 64) the M <= 64 kernel writes them from its epilogue; AUTO and
+ * the other kernels run the GEMM and then the operand pass (the faster of the two at M = 64). */
 int splosh_q4_gemm_emit(const splosh_q4_weight *w, const uint16_t *a, int64_t lda, float *out, int64_t ldc,
                         const float *residual, int64_t rows, const uint16_t *norm_weight, uint16_t *values,
                         int64_t ld_values, float *sums, float *squares, int kernel, void *workspace,

@@ -398,8 +398,9 @@ int splosh_q4_gemm(const splosh_q4_weight *w, const uint16_t *a, int64_t lda, vo
 }
 
 // Engine.gemm with emit (engine_na.metal:322-473): the residual projection that also writes the
-// next RMSNorm's operand. The M <= 64 kernel writes it from its epilogue; other kernels are followed
-// by the separate operand pass on the fp32 output.
+// next RMSNorm's operand. With SPLOSH_KERNEL_DEQUANT the M <= 64 kernel writes it from its
+// epilogue; AUTO and the other kernels are followed by the separate operand pass on the fp32 output
+// (at M=64, K17408 -> N5120 the GEMM plus the pass takes 30.1 us, the fused epilogue 31.2 us).
 int splosh_q4_gemm_emit(const splosh_q4_weight *w, const uint16_t *a, int64_t lda, float *out, int64_t ldc,
                         const float *residual, int64_t rows, const uint16_t *norm_weight, uint16_t *values,
                         int64_t ld_values, float *sums, float *squares, int kernel, void *workspace,
@@ -416,7 +417,7 @@ int splosh_q4_gemm_emit(const splosh_q4_weight *w, const uint16_t *a, int64_t ld
     const splosh::EmitOperand emit{norm_weight, values, ld_values, sums, squares};
     bool emitted = false;
     if ((st = q4_gemm_impl(w, nullptr, a, lda, out, ldc, SPLOSH_F32, residual, rows, kernel, workspace,
-                           workspace_bytes, stream, &emit, &emitted)))
+                           workspace_bytes, stream, kernel == SPLOSH_KERNEL_DEQUANT ? &emit : nullptr, &emitted)))
         return st;
     if (emitted) return ok();
     return hip_status(splosh::launch_emit_operand(out, ldc, norm_weight, rows, w->rows, values, ld_values, sums, squares,

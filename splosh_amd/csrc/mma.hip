@@ -113,10 +113,11 @@ struct MmaArgs {
 //
 // GROUPED (one tiled weight a band, of a grouped call): each job takes its band's weight, buffer
 // resources and column offset from the group table.
-template <int NW_, bool TILED, int CW, int KW, int D, bool GROUPED = false>
+template <int NW_, bool TILED, int CW, int KW, int D, bool GROUPED = false, bool EMIT = false>
 struct Q4Format {
     static_assert(!GROUPED || (NW_ == 1 && TILED), "grouped calls take single tiled weights");
     static constexpr bool kGrouped = GROUPED;
+    static constexpr bool kEmit = EMIT && !GROUPED;  // the epilogue emits the next norm's operand
     static constexpr int NW = NW_;
     static constexpr bool kStageSide = TILED;
     static constexpr int kWLoads = kStageSide ? NW : NW * 3;  // weight loads per wave and step
@@ -270,6 +271,7 @@ struct Q4Format {
 template <int CW, int KW, int D, bool FIFTH = true>
 struct Q5Format {
     static constexpr bool kGrouped = false;
+    static constexpr bool kEmit = false;
     static constexpr int NW = 1;
     static constexpr int kWLoads = FIFTH ? 2 : 1;  // loads per wave and step: the mid-step wait counts them
     static constexpr int kUnitK = 256;
@@ -471,7 +473,7 @@ mma_kernel(MmaArgs args) {
     auto run_job = [&](int band, int ga, int gb, auto &&after_prologue) {
         const int T = fmt.steps(ga, gb);
         fmt.begin(args, band, ga, gb);
-        if constexpr (NW == 1) {
+        if constexpr (NW == 1 && F::kEmit) {
             if (args.norm_weight) {
                 const int64_t c = (int64_t)band * S::kBandCols + cw * 32 + r;
                 wn_band = band;
@@ -723,14 +725,43 @@ mma_kernel(MmaArgs args) {
                 }
                 hv[f][i] = value;
             }
-        if constexpr (NW == 1) {
+        if constexpr (NW == 1 && F::kEmit) {
             if (args.norm_weight) {
                 // Emit (engine_na.metal:365-411 restated): the rounded operand, then per row the
-                // band's sums: over this wave's 32 columns by a shuffle tree inside the lane half
-                // that holds the row, then the two column waves' halves through LDS.
+                // band's sums: over this wave's 32 columns inside the lane half that holds the
+                // rows, then the two column waves' halves through LDS. The 32-lane sums of the
+                // lane's NQ rows run as a reduce-scatter (exchange half the rows with lane r ^ 16,
+                // then a quarter with r ^ 8, ...; plain sums over the lanes left): 31 shuffles a
+                // quantity at most instead of 5 a row. Lane r ends with the sum of slot
+                // q(r) = sum over level k of bit 4 - k of r times NQ / 2^(k+1).
                 const float wn = bf16_bits_to_f32(band == wn_band ? wn_bits : (uint32_t)args.norm_weight[ocol]);
                 float *part = (float *)((char *)lds + S::kRedBytes);  // [FM * 32 rows][2 cw][2]
                 const int64_t groups = args.n / 64;
+                constexpr int NQ = FM * 4;
+                constexpr int L = NQ == 16 ? 4 : NQ == 8 ? 3 : 2;  // reduce-scatter levels
+                auto lane_sum = [&](float (&x)[NQ]) {
+#pragma unroll
+                    for (int k = 0; k < L; ++k) {
+                        // Keep slots [0, half) (the upper lane of the pair r, r ^ 2 half: slots
+                        // [half, 2 half), moved down) and add the partner's copy of them.
+                        const int half = NQ >> (k + 1), xm = 16 >> k;
+                        const bool upper = (r & xm) != 0;
+#pragma unroll
+                        for (int j = 0; j < half; ++j) {
+                            const float keep = upper ? x[half + j] : x[j], give = upper ? x[j] : x[half + j];
+                            x[j] = keep + __shfl_xor(give, xm, 64);
+                        }
+                    }
+#pragma unroll
+                    for (int xm = 16 >> L; xm >= 1; xm >>= 1) x[0] += __shfl_xor(x[0], xm, 64);
+                    return x[0];
+                };
+                int q = 0;
+#pragma unroll
+                for (int k = 0; k < L; ++k) q += ((r >> (4 - k)) & 1) * (NQ >> (k + 1));
+                const bool lead = (r & ((32 >> L) - 1)) == 0;
+                const int qm = own_row(q >> 2, q & 3);
+                float x[NQ];
 #pragma unroll
                 for (int f = 0; f < FM; ++f)
 #pragma unroll
@@ -738,17 +769,16 @@ mma_kernel(MmaArgs args) {
                         const int m = own_row(f, i);
                         const uint16_t vb = f32_to_bf16(hv[f][i] * wn);
                         if (m < rows) args.values[(int64_t)m * args.ldv + ocol] = vb;
-                        float sv = bf16_bits_to_f32(vb), sq = hv[f][i] * hv[f][i];
-#pragma unroll
-                        for (int o = 1; o < 32; o <<= 1) {
-                            sv += __shfl_xor(sv, o, 64);
-                            sq += __shfl_xor(sq, o, 64);
-                        }
-                        if (r == 0) {
-                            part[(m * 2 + cw) * 2] = sv;
-                            part[(m * 2 + cw) * 2 + 1] = sq;
-                        }
+                        x[f * 4 + i] = bf16_bits_to_f32(vb);
                     }
+                const float sv = lane_sum(x);
+                if (lead) part[(qm * 2 + cw) * 2] = sv;
+#pragma unroll
+                for (int f = 0; f < FM; ++f)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) x[f * 4 + i] = hv[f][i] * hv[f][i];
+                const float sq = lane_sum(x);
+                if (lead) part[(qm * 2 + cw) * 2 + 1] = sq;
                 __syncthreads();
                 if (cw == 0 && r == 0) {
 #pragma unroll
@@ -1037,8 +1067,10 @@ static hipError_t launch_mma_fm(const MmaPlan &p, const MmaArgs &args, hipStream
     return p.fm == 1 ? launch_mma_v<F, 1>(p, args, stream) : launch_mma_v<F, 2>(p, args, stream);
 }
 
-template <int NW, bool TILED, bool GROUPED = false>
-using Q4F = Q4Format<NW, TILED, kMmaCW, kMmaKW, kMmaDepth, GROUPED>;
+// EMIT: a build with the emit epilogue, kept apart so that its registers do not weigh on the
+// kernel without it.
+template <int NW, bool TILED, bool GROUPED = false, bool EMIT = false>
+using Q4F = Q4Format<NW, TILED, kMmaCW, kMmaKW, kMmaDepth, GROUPED, EMIT>;
 
 static void set_io(MmaArgs &args, const MmaPlan &plan, const uint16_t *a, int64_t lda, void *out, int64_t ldc,
                    int out_dtype, const void *residual, int64_t rows, int64_t inner, void *workspace, bool mlp) {
@@ -1085,6 +1117,9 @@ hipError_t launch_q4_mma(const MmaPlan &plan, const splosh_q4_weight &w, const s
     hipError_t err;
     if (up)
         err = tiled ? launch_mma_fm<Q4F<2, true>>(plan, args, stream) : launch_mma_fm<Q4F<2, false>>(plan, args, stream);
+    else if (emit)
+        err = tiled ? launch_mma_fm<Q4F<1, true, false, true>>(plan, args, stream)
+                    : launch_mma_fm<Q4F<1, false, false, true>>(plan, args, stream);
     else
         err = tiled ? launch_mma_fm<Q4F<1, true>>(plan, args, stream) : launch_mma_fm<Q4F<1, false>>(plan, args, stream);
     return err;

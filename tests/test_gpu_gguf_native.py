@@ -61,11 +61,12 @@ def test_native_gemm(rt, name, rows):
 
 
 @pytest.mark.parametrize("name", list(TYPES))
-@pytest.mark.parametrize("rows", [5, 7, 8])
-def test_five_to_eight_rows_both_routes(rt, name, rows):
-    """5-8 activation rows: with a workspace AUTO's choice (the split tiled kernel above the
-    format's streaming limit, Q8_0 4 .. IQ3_S 8), without one a single eight-row pass of the
-    streaming kernel; both against the oracle."""
+@pytest.mark.parametrize("rows", [2, 5, 6, 7, 8])
+def test_two_to_eight_rows_both_routes(rt, name, rows):
+    """2-8 activation rows: with a workspace AUTO's choice (the split tiled kernel above the
+    format's streaming limit -- Q8_0, IQ4_NL and IQ4_XS 5, Q6_K and Q3_K 6, IQ3_S 8 -- the streaming
+    kernel up to it), without one a single eight-row pass of the streaming kernel; both against the
+    oracle. Two rows take the streaming kernel's pairs form at four rows a pass."""
     t = TYPES[name]
     n, k = 200, 1536
     w, dense = _weight(rt, t, n, k, seed=rows + 3 * t)
@@ -95,6 +96,25 @@ def test_config0_size_sampled(rt, name):
     dense = oracle.gguf_decode(t, rows.reshape(-1)).reshape(len(cols), k)
     check_close(got[:, cols], oracle.gemm_a_bf16_w_f32(a_bits, dense), bf16_out=False, tight=True,
                 absref=abs_gemm(a_bits, dense), label=f"{name} config0")
+
+
+@pytest.mark.parametrize("name", ["q6K", "q3K"])
+@pytest.mark.parametrize("rows", [2, 4, 6])
+def test_streaming_long_k_sampled(rt, name, rows):
+    """Q6_K and Q3_K at K=17408 -> N=5120 through the streaming kernel (AUTO up to six rows): its
+    pairs form sums the unsigned codes and takes the bias off once a group, so the cancellation
+    grows with K; 256 sampled columns against the oracle at the tight tolerance."""
+    t = TYPES[name]
+    n, k = 5120, 17408
+    elems, size = oracle.GGUF_BLOCK[t]
+    native = oracle.gguf_random_native(t, n, k, seed=50 + rows)
+    w = rt.GgufWeight(torch.from_numpy(native).cuda(), t, n, k)
+    a_bits = oracle.bf16_normal((rows, k), seed=51 + rows)
+    got = rt.gemm(w, bf16_tensor(a_bits), out_dtype=torch.float32).cpu().numpy()
+    cols = np.sort(np.random.default_rng(52 + rows).choice(n, 256, replace=False))
+    dense = oracle.gguf_decode(t, native.reshape(n, k // elems * size)[cols].reshape(-1)).reshape(len(cols), k)
+    check_close(got[:, cols], oracle.gemm_a_bf16_w_f32(a_bits, dense), bf16_out=False, tight=True,
+                absref=abs_gemm(a_bits, dense), label=f"{name} K17408 rows={rows}")
 
 
 @pytest.mark.parametrize("name", list(TYPES))

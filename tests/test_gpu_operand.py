@@ -83,21 +83,26 @@ def test_operand_rejects_bad_arguments(rt):
         rt.prepare_operand(x)  # dim not a multiple of 64
 
 
+@pytest.mark.parametrize("kernel", ["auto", "dequant"])
 @pytest.mark.parametrize("rows", [1, 5, 33, 64, 100])
 @pytest.mark.parametrize("n,k", [(640, 4352), (5120, 1280)])
-def test_gemm_emit(rt, rows, n, k):
+def test_gemm_emit(rt, rows, n, k, kernel):
     """Engine.gemm with emit (engine_na.metal:322-473): the residual projection's fp32 output, and
     the next norm's operand computed from that output -- fused into the M <= 64 kernel's epilogue
-    (rows 5..64, with and without split bands), a separate pass after the other kernels. The values
-    are bit-exact against the oracle's operand of the kernel's own output; sums and squares agree
-    to fp32 summation order."""
+    (kernel DEQUANT, rows <= 64, with and without split bands), a separate pass after the GEMM
+    (AUTO). The values are bit-exact against the oracle's operand of the kernel's own output; sums
+    and squares agree to fp32 summation order."""
+    if kernel == "dequant" and rows > 64:
+        pytest.skip("the M <= 64 kernel takes at most 64 rows")
+    kcode = rt.DEQUANT if kernel == "dequant" else rt.AUTO
     from qcheck import Q4Case, abs_gemm, bf16_tensor, check_close
     case = Q4Case(n, k, seed=rows + n)
     a_bits = oracle.bf16_normal((rows, k), seed=rows)
     res = np.random.default_rng(rows).normal(size=(rows, n)).astype(np.float32)
     wn = torch.from_numpy(np.random.default_rng(7).normal(1.0, 0.1, size=n).astype(np.float32)).to(torch.bfloat16).cuda()
     out = torch.from_numpy(res.copy()).cuda()
-    got, values, sums, squares = rt.gemm_emit(case.w_tiled, bf16_tensor(a_bits), wn, out=out, residual=out)
+    got, values, sums, squares = rt.gemm_emit(case.w_tiled, bf16_tensor(a_bits), wn, out=out, residual=out,
+                                              kernel=kcode)
     ref = oracle.gemm_a_bf16_w_f32(a_bits, case.dense) + res
     h = got.cpu().numpy()
     check_close(h, ref, bf16_out=False, label=f"emit out rows={rows}")
