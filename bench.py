@@ -34,13 +34,13 @@ BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
 # a plain 256 MiB device copy (FETCH_SIZE reads half the bytes moved, WRITE_SIZE all of them).
 # The readings and commands are in profiles/; calls not listed are unmeasured (None).
 MEASURED_TRAFFIC = {
-    ("verify64", "mlp_in"): 55942.5 * 2 * 1024 + 9871.0 * 1024,  # mma_kernel<Q4Format<2, true, 2, 4, 3>, 2, 2, 4, 3>
-    ("verify64", "down"): 35292.5 * 2 * 1024 + 4420.5 * 1024,  # mma_kernel<Q4Format<1, true, 2, 4, 3>, 2, 2, 4, 3>
-    ("decode1", "gemv"): 24559.8 * 2 * 1024 + 34.0 * 1024,  # q4_decode_kernel<1, 1, 32, 2>
+    ("verify64", "mlp_in"): 55912.9 * 2 * 1024 + 9871.0 * 1024,  # mma_kernel<Q4Format<2, true, 2, 4, 3, false, false>, 2, 2, 4, 3>
+    ("verify64", "down"): 35308.5 * 2 * 1024 + 4444.6 * 1024,  # mma_kernel<Q4Format<1, true, 2, 4, 3, false, false>, 2, 2, 4, 3>
+    ("decode1", "gemv"): 24560.9 * 2 * 1024 + 34.0 * 1024,  # q4_decode_kernel<1, 1, 32, 2>
     ("lmhead1", "lm_head"): 349280.3 * 2 * 1024 + 486.2 * 1024,  # q4_decode_kernel<1, 1, 32, 2>
     ("q5k1", "q5k"): 30096.8 * 2 * 1024 + 10.0 * 1024,  # q5k_decode_kernel<8, 2, true>
-    ("q5k64", "q5k"): 41370.6 * 2 * 1024 + 4415.2 * 1024,  # mma_kernel<Q5Format<2, 4, 3, true>, 2, 2, 4, 3>
-    ("q5k16", "q5k"): 32944.4 * 2 * 1024 + 1115.2 * 1024,  # mma_kernel<Q5Format<2, 4, 3, true>, 1, 2, 4, 3>
+    ("q5k64", "q5k"): 41344.6 * 2 * 1024 + 4364.4 * 1024,  # mma_kernel<Q5Format<2, 4, 3, true>, 2, 2, 4, 3>
+    ("q5k16", "q5k"): 32946.8 * 2 * 1024 + 1095.7 * 1024,  # mma_kernel<Q5Format<2, 4, 3, true>, 1, 2, 4, 3>
     ("prefill2048", "prefill_up"): 266967.5 * 2 * 1024 + 114688.0 * 1024,  # prefill_kernel<Q4Stage>
     ("q5k2048", "q5k"): 347729.4 * 2 * 1024 + 98304.0 * 1024,  # prefill_kernel<Q5Stage<true>>
     ("q6k2048", "gguf"): 366940.1 * 2 * 1024 + 110080.0 * 1024,  # prefill_kernel<GgufStage<14>>
@@ -49,9 +49,10 @@ MEASURED_TRAFFIC = {
     ("q3k1", "gguf"): 19009.8 * 2 * 1024 + 10.0 * 1024,  # gguf_pairs_kernel<11, 4, 2>
     ("iq3s1", "gguf"): 19068.8 * 2 * 1024 + 10.0 * 1024,  # gguf_pairs_kernel<21, 4, 2>
     ("q80_1", "gguf"): 46715.8 * 2 * 1024 + 10.0 * 1024,  # gguf_gemv_kernel<8, 4>
-    ("stream50", "read"): 24680.2 * 2 * 1024 + 64.0 * 1024,  # stream_read_kernel
-    ("layerset", "mlp_in"): 55934.6 * 2 * 1024 + 9871.0 * 1024,  # mma_kernel<Q4Format<2, true, 2, 4, 3>, 2, 2, 4, 3>
-    ("emit64", "fused"): 35950.1 * 2 * 1024 + 5475.5 * 1024,  # mma_kernel<Q4Format<1, true, 2, 4, 3>, 2, 2, 4, 3>
+    ("stream50", "read"): 24684.0 * 2 * 1024 + 64.0 * 1024,  # stream_read_kernel (shape 0, the default)
+    ("layerset", "mlp_in"): 55924.8 * 2 * 1024 + 9871.0 * 1024,  # mma_kernel<Q4Format<2, true, 2, 4, 3, false, false>, 2, 2, 4, 3>
+    ("lmhead64", "lm_head"): 355049.4 * 2 * 1024 + 35023.5 * 1024,  # mma_kernel<Q4Format<1, true, 2, 4, 3, false, false>, 2, 2, 4, 3>
+    ("emit64", "fused"): 35951.5 * 2 * 1024 + 5507.6 * 1024,  # mma_kernel<Q4Format<1, true, 2, 4, 3, false, true>, 2, 2, 4, 3>
 }
 
 
