@@ -6,7 +6,7 @@ projection (two K=5120 -> N=17408 weights sharing one activation read, out = sil
 by the down projection (K=17408 -> N=5120) on that output. One "step" is that pair of launches.
 
     python bench.py [--steps K] [--warmup W]
-                    [--workload verify64|decode1|q5k1|q5k16|q5k64|q4k1|q4k64|q6k1|q80_1|iq4nl1|iq4xs1|q3k1|iq3s1|prefill2048|layerset|lmhead1|lmhead64|operand64|emit64|stream50|stream715|gemm2048]
+                    [--workload verify64|decode1|q5k1|q5k16|q5k64|q4k1|q4k64|q6k1|q80_1|iq4nl1|iq4xs1|q3k1|iq3s1|prefill2048|layerset|lmhead1|lmhead64|operand64|emit64|emit2048|stream50|stream715|gemm2048]
 
 Inputs are synthetic (seeded, on the device): code words uniform random, scale = bf16(|N(0,0.02)|),
 bias = bf16(N(0,0.01)), activations bf16(N(0,1)). Several copies of the weight set are rotated so
@@ -135,7 +135,7 @@ def build_workload(name, rt, torch, gen, kernel):
                "format": "mlx affine q4 g64, tiled128", "weight_copies": {nm: len(v) for nm, v in mats.items()}}
         return launches, sum(kb.values()), sum(kf.values()), kb, cfg, kf
     if name == "verify64":
-        m, h, inter = 64, 5120, 17408
+        m, h, inter = int(name[4:] or 64), 5120, 17408
         one = 2 * q4_bytes(inter, h) + q4_bytes(h, inter)
         ncopy = copies_for(one)
         sets = [(make_q4(rt, inter, h, gen), make_q4(rt, inter, h, gen), make_q4(rt, h, inter, gen))
@@ -262,13 +262,13 @@ def build_workload(name, rt, torch, gen, kernel):
         cfg = {"workload": "bf16 GEMM (torch.matmul) on the prefill shapes (reference point, not the path)",
                "rows": m, "format": "bf16", "weight_copies": 1}
         return launches, sum(kb.values()), sum(kf.values()), kb, cfg, kf
-    if name == "emit64":
-        # The MLP's down projection at M=64 as the residual projection that feeds the next RMSNorm:
-        # fp32 hidden state += a w^T, and the next GEMM's operand (bf16 h * norm weight, per-64 sums
-        # and sums of squares). "fused": the emit in the GEMM's epilogue (splosh_q4_gemm_emit with
-        # the DEQUANT kernel); "separate": the GEMM, then the operand pass over the hidden state (what
-        # splosh_q4_gemm_emit runs under AUTO).
-        m, h, inter = 64, 5120, 17408
+    if name.startswith("emit"):
+        # The MLP's down projection at M rows (emit64, emit2048) as the residual projection that
+        # feeds the next RMSNorm: fp32 hidden state += a w^T, and the next GEMM's operand (bf16
+        # h * norm weight, per-64 sums and sums of squares). "fused": the emit in the GEMM's
+        # epilogue (splosh_q4_gemm_emit); "separate": the GEMM, then the operand pass over the
+        # hidden state.
+        m, h, inter = int(name[4:] or 64), 5120, 17408
         ncopy = copies_for(q4_bytes(h, inter))
         ws = [make_q4(rt, h, inter, gen) for _ in range(ncopy)]
         x = torch.randn(m, inter, device="cuda", generator=gen).to(torch.bfloat16)
@@ -282,11 +282,14 @@ def build_workload(name, rt, torch, gen, kernel):
 
         def launches(i):
             w = ws[i % ncopy]
-            return [("fused", lambda: rt.gemm_emit(w, x, wn, out=hid, residual=hid, kernel=rt.DEQUANT, workspace=scr)),
+            # At most 64 rows the fused epilogue is the M <= 64 kernel's, asked for by name (AUTO takes
+            # the separate pass there); above that AUTO's prefill or tile kernel.
+            fk = rt.DEQUANT if m <= 64 else rt.AUTO
+            return [("fused", lambda: rt.gemm_emit(w, x, wn, out=hid, residual=hid, kernel=fk, workspace=scr)),
                     ("separate", lambda: (rt.gemm(w, x, out=hid, residual=hid, out_dtype=torch.float32, workspace=scr),
                                           rt.emit_operand(hid, wn, values=be, sums=se, squares=qe)))]
 
-        cfg = {"workload": "down projection K17408->N5120 at M=64 with the next norm's operand emitted", "rows": m,
+        cfg = {"workload": f"down projection K17408->N5120 at M={m} with the next norm's operand emitted", "rows": m,
                "format": "mlx affine q4 g64, tiled128", "weight_copies": ncopy}
         return launches, 2 * b, 4 * m * h * inter, {"fused": b, "separate": b}, cfg, \
             {"fused": 2 * m * h * inter, "separate": 2 * m * h * inter}

@@ -169,8 +169,9 @@ int splosh_q4_gemm(const splosh_q4_weight *w, const uint16_t *a, int64_t lda, vo
  * writes the next RMSNorm-ed GEMM's operand from the same values: values = bf16(out * norm_weight)
  * (RNE, [rows][ld_values]), and per row and per 64 columns the sums of those rounded values and of
  * out * out (fp32 [rows][w->rows / 64]), as splosh_emit_operand computes them. w->rows % 64 == 0.
- * With SPLOSH_KERNEL_DEQUANT (rows <= 64) the M <= 64 kernel writes them from its epilogue; AUTO and
- * the other kernels run the GEMM and then the operand pass (the faster of the two at M = 64). */
+ * The prefill kernel (AUTO for most shapes from 256 rows, or SPLOSH_KERNEL_PREFILL) writes them from
+ * its epilogue, and so does the M <= 64 kernel when SPLOSH_KERNEL_DEQUANT is asked for (rows <= 64);
+ * otherwise the GEMM is followed by the operand pass (under AUTO at M <= 64 the faster of the two). */
 int splosh_q4_gemm_emit(const splosh_q4_weight *w, const uint16_t *a, int64_t lda, float *out, int64_t ldc,
                         const float *residual, int64_t rows, const uint16_t *norm_weight, uint16_t *values,
                         int64_t ld_values, float *sums, float *squares, int kernel, void *workspace,

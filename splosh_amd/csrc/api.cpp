@@ -140,8 +140,9 @@ int q4_gemm_impl(const splosh_q4_weight *w, const splosh_q4_weight *up, const ui
                             "aligned operands");
             const splosh::PrefillPlan plan =
                 splosh::plan_prefill(rows, w->rows, w->inner / kGroupSize, workspace ? workspace_bytes : 0);
+            if (emitted) *emitted = emit != nullptr;
             return hip_status(splosh::launch_q4_prefill(plan, *w, a, lda, out, ldc, out_dtype, residual, rows,
-                                                        workspace, stream),
+                                                        workspace, stream, emit),
                               "q4 prefill launch");
         }
         case SPLOSH_KERNEL_TILE: {
@@ -183,9 +184,12 @@ int q4_gemm_impl(const splosh_q4_weight *w, const splosh_q4_weight *up, const ui
             if (!mma_ok) return fail(SPLOSH_ERR_UNSUPPORTED, "dequant kernel needs rows <= 64 and aligned operands");
             const splosh::MmaPlan plan =
                 splosh::plan_mma(rows, w->rows, w->inner / kGroupSize, up != nullptr, workspace ? workspace_bytes : 0);
-            if (emitted) *emitted = emit != nullptr;
+            // The emit epilogue only when asked for by name: under AUTO the GEMM plus the separate
+            // pass is the faster of the two at these row counts.
+            const splosh::EmitOperand *mma_emit = kernel == SPLOSH_KERNEL_DEQUANT ? emit : nullptr;
+            if (emitted) *emitted = mma_emit != nullptr;
             return hip_status(splosh::launch_q4_mma(plan, *w, up, a, lda, out, ldc, out_dtype, residual, rows,
-                                                    workspace, stream, emit),
+                                                    workspace, stream, mma_emit),
                               "q4 mma launch");
         }
         default:
@@ -398,9 +402,10 @@ int splosh_q4_gemm(const splosh_q4_weight *w, const uint16_t *a, int64_t lda, vo
 }
 
 // Engine.gemm with emit (engine_na.metal:322-473): the residual projection that also writes the
-// next RMSNorm's operand. With SPLOSH_KERNEL_DEQUANT the M <= 64 kernel writes it from its
-// epilogue; AUTO and the other kernels are followed by the separate operand pass on the fp32 output
-// (at M=64, K17408 -> N5120 the GEMM plus the pass takes 30.1 us, the fused epilogue 31.2 us).
+// next RMSNorm's operand. The prefill kernel (AUTO from 256 rows for most shapes) writes it from its
+// epilogue, and so does the M <= 64 kernel when SPLOSH_KERNEL_DEQUANT is asked for; otherwise the
+// GEMM is followed by the separate operand pass on the fp32 output (at M=64, K17408 -> N5120 the
+// GEMM plus the pass takes 30.1 us, the fused M <= 64 epilogue 31.2 us).
 int splosh_q4_gemm_emit(const splosh_q4_weight *w, const uint16_t *a, int64_t lda, float *out, int64_t ldc,
                         const float *residual, int64_t rows, const uint16_t *norm_weight, uint16_t *values,
                         int64_t ld_values, float *sums, float *squares, int kernel, void *workspace,
@@ -417,7 +422,7 @@ int splosh_q4_gemm_emit(const splosh_q4_weight *w, const uint16_t *a, int64_t ld
     const splosh::EmitOperand emit{norm_weight, values, ld_values, sums, squares};
     bool emitted = false;
     if ((st = q4_gemm_impl(w, nullptr, a, lda, out, ldc, SPLOSH_F32, residual, rows, kernel, workspace,
-                           workspace_bytes, stream, kernel == SPLOSH_KERNEL_DEQUANT ? &emit : nullptr, &emitted)))
+                           workspace_bytes, stream, &emit, &emitted)))
         return st;
     if (emitted) return ok();
     return hip_status(splosh::launch_emit_operand(out, ldc, norm_weight, rows, w->rows, values, ld_values, sums, squares,

@@ -155,9 +155,10 @@ struct PrefillPlan {
 bool prefill_fits(int64_t rows, int64_t columns, int64_t inner, int64_t lda, int64_t ldc);
 PrefillPlan plan_prefill(int64_t rows, int64_t columns, int64_t groups, size_t workspace_bytes);
 size_t prefill_workspace_bytes(int64_t rows, int64_t columns, int64_t groups);
+// emit: null, or the operand to write from the epilogue (fp32 output, n % 64 == 0).
 hipError_t launch_q4_prefill(const PrefillPlan &plan, const splosh_q4_weight &w, const uint16_t *a, int64_t lda,
                              void *out, int64_t ldc, int out_dtype, const void *residual, int64_t rows,
-                             void *workspace, hipStream_t stream);
+                             void *workspace, hipStream_t stream, const EmitOperand *emit = nullptr);
 // Fused gate+up (silu(g) * u) over two TILED128 weights of one geometry: tiles of 128 columns of
 // each; plan with plan_prefill(rows, 2 * columns, groups, ...).
 hipError_t launch_q4_prefill_mlp(const PrefillPlan &plan, const splosh_q4_weight &gate, const splosh_q4_weight &up,

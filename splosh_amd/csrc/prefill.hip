@@ -54,6 +54,9 @@ struct PrefillArgs {
     int dp_tiles;       // tiles computed whole (a multiple of gridDim.x)
     int64_t sk_units;   // (tile, group) pairs of the remaining tiles
     uint32_t a_bytes;
+    // The next RMSNorm's operand, written from the epilogue (one weight, fp32 output, N % 64 == 0;
+    // null norm_weight: none).
+    EmitOperand emit;
 };
 
 constexpr int kPB = 256;                       // tile rows and columns
@@ -63,12 +66,68 @@ constexpr int kPEpiRow = 68;                   // floats per row of a wave's epi
 constexpr int kPEpi = 32 * kPEpiRow * 4;       // bytes of a wave's epilogue staging (32 rows)
 constexpr int kPFinishMax = 1024;              // contributors prefill_finish can list
 
+// Four output elements of row m, columns n .. n + 3, with the residual added; returns the values
+// before the output's rounding.
+__device__ __forceinline__ f32x4 prefill_out4(void *out, int64_t ldc, int out_dtype, const void *residual, int64_t m,
+                                              int64_t n, f32x4 v) {
+    const int64_t index = m * ldc + n;
+    if (out_dtype == SPLOSH_F32) {
+        if (residual) v += *(const f32x4 *)((const float *)residual + index);
+        *(f32x4 *)((float *)out + index) = v;
+    } else {
+        if (residual) {
+            const u32x2 rb = *(const u32x2 *)((const uint16_t *)residual + index);
+            v[0] += bf16_bits_to_f32(rb[0] & 0xffffu);
+            v[1] += bf16_bits_to_f32(rb[0] >> 16);
+            v[2] += bf16_bits_to_f32(rb[1] & 0xffffu);
+            v[3] += bf16_bits_to_f32(rb[1] >> 16);
+        }
+        const u32x2 pk = {f32x2_to_bf16x2(v[0], v[1]), f32x2_to_bf16x2(v[2], v[3])};
+        *(u32x2 *)((uint16_t *)out + index) = pk;
+    }
+    return v;
+}
+
+// Emit (engine_na.metal:365-411 restated) for four fp32 outputs h of row m, columns n .. n + 3:
+// values bf16(h w_norm) (RNE), and the row's sums over its 64-column band n / 64 of those rounded
+// values and of h^2. The band's 64 columns are the four-column pieces of 16 consecutive lanes
+// (lane % 16 = piece), summed by a shuffle tree; every lane of the wave calls it (`live` false
+// past the rows or columns).
+__device__ __forceinline__ void prefill_emit_band(const EmitOperand &e, int64_t n_total, int64_t m, int64_t n, f32x4 h,
+                                                  bool live, int lane) {
+    float sv = 0.0f, sq = 0.0f;
+    if (live) {
+        const u32x2 wb = *(const u32x2 *)(e.norm_weight + n);
+        const float wn[4] = {bf16_bits_to_f32(wb[0] & 0xffffu), bf16_bits_to_f32(wb[0] >> 16),
+                             bf16_bits_to_f32(wb[1] & 0xffffu), bf16_bits_to_f32(wb[1] >> 16)};
+        uint32_t vb[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            vb[i] = f32_to_bf16(h[i] * wn[i]);
+            sv += bf16_bits_to_f32(vb[i]);
+            sq += h[i] * h[i];
+        }
+        const u32x2 pk = {vb[0] | (vb[1] << 16), vb[2] | (vb[3] << 16)};
+        *(u32x2 *)(e.values + m * e.ldv + n) = pk;
+    }
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) {
+        sv += __shfl_xor(sv, o, 64);
+        sq += __shfl_xor(sq, o, 64);
+    }
+    if (live && (lane & 15) == 0) {
+        const int64_t at = m * (n_total / 64) + n / 64;
+        e.sums[at] = sv;
+        e.squares[at] = sq;
+    }
+}
+
 // A wave's share of a finished tile: rows tr0 .. tr0 + 32 FM - 1 of columns tc0 .. tc0 + 63, one
 // 32-row block at a time through the wave's own LDS area `epi` (over the operand buffers, once
 // every wave is done with them): lane (r, h) holds row 8 (e / 4) + 4 h + e % 4, column 32 j + r;
 // the rows are then written 16 bytes (4 columns) a lane, to the output (slot < 0) or to this
 // workgroup's partial tile `slot`.
-template <int FM>
+template <int FM, bool EMIT>
 __device__ __forceinline__ void prefill_store_tile(const PrefillArgs &args, const f32x16 (&acc)[FM][2], char *epi,
                                                    int64_t m0, int64_t ncol, int tc0, int tr0, int lane, int slot) {
     const int r = lane & 31, h = lane >> 5;
@@ -87,29 +146,19 @@ __device__ __forceinline__ void prefill_store_tile(const PrefillArgs &args, cons
             const int idx = p * 64 + lane, row = idx >> 4, c4 = (idx & 15) * 4;
             const f32x4 v = *(const f32x4 *)(epi + (row * kPEpiRow + c4) * 4);
             const int64_t m = m0 + tr + row, n = ncol + c4;
-            if (m >= args.rows || n >= args.n) continue;
+            const bool live = m < args.rows && n < args.n;
+            if (EMIT && slot < 0 && args.emit.norm_weight) {  // fp32 output, whole 64-column bands
+                const f32x4 h = live ? prefill_out4(args.out, args.ldc, SPLOSH_F32, args.residual, m, n, v) : v;
+                prefill_emit_band(args.emit, args.n, m, n, h, live, lane);
+                continue;
+            }
+            if (!live) continue;
             if (slot >= 0) {
                 float *dst = args.partial + ((int64_t)(blockIdx.x * 2 + slot) * kPB + tr + row) * kPB + tc0 + c4;
                 *(f32x4 *)dst = v;
                 continue;
             }
-            const int64_t index = m * args.ldc + n;
-            if (args.out_dtype == SPLOSH_F32) {
-                f32x4 o = v;
-                if (args.residual) o += *(const f32x4 *)((const float *)args.residual + index);
-                *(f32x4 *)((float *)args.out + index) = o;
-            } else {
-                float o[4] = {v[0], v[1], v[2], v[3]};
-                if (args.residual) {
-                    const u32x2 rb = *(const u32x2 *)((const uint16_t *)args.residual + index);
-                    o[0] += bf16_bits_to_f32(rb[0] & 0xffffu);
-                    o[1] += bf16_bits_to_f32(rb[0] >> 16);
-                    o[2] += bf16_bits_to_f32(rb[1] & 0xffffu);
-                    o[3] += bf16_bits_to_f32(rb[1] >> 16);
-                }
-                const u32x2 pk = {f32x2_to_bf16x2(o[0], o[1]), f32x2_to_bf16x2(o[2], o[3])};
-                *(u32x2 *)((uint16_t *)args.out + index) = pk;
-            }
+            prefill_out4(args.out, args.ldc, args.out_dtype, args.residual, m, n, v);
         }
     }
 }
@@ -168,6 +217,7 @@ __device__ __forceinline__ void prefill_store_mlp(const PrefillArgs &args, const
 // and the column's scale and bias (Retile.swift:135-153), dequantized by dequant_word_fp8.
 struct Q4Stage {
     static constexpr int kLoads = 3, kNW = 1;
+    static constexpr bool kEmit = true;  // the epilogue can write the next norm's operand
     rsrc_t q_rsrc, s_rsrc, b_rsrc;
     uint32_t c_src, s_src;
     u32x4 cr[2];
@@ -200,6 +250,7 @@ struct Q4Stage {
 // 0 .. 255) and the same 128 of the up weight (threads 256 .. 511).
 struct Q4PairStage : Q4Stage {
     static constexpr int kNW = 2;
+    static constexpr bool kEmit = false;
     __device__ Q4PairStage(const PrefillArgs &args)
         : Q4Stage(args, __builtin_amdgcn_readfirstlane(threadIdx.x >> 8) != 0) {}
 };
@@ -218,6 +269,7 @@ struct Q4PairStage : Q4Stage {
 template <bool FIFTH>
 struct Q5Stage {
     static constexpr int kLoads = FIFTH ? 3 : 2, kNW = 1;
+    static constexpr bool kEmit = false;
     rsrc_t p0_rsrc, p1_rsrc, m_rsrc;
     uint32_t p0_src, p1_src, m_src;
     int hh;
@@ -295,6 +347,7 @@ struct Q5Stage {
 template <int TYPE>
 struct GgufStage {
     static constexpr int kLoads = 0, kNW = 1;
+    static constexpr bool kEmit = false;
     rsrc_t r;
     uint32_t row;
     int hh;
@@ -463,7 +516,7 @@ prefill_kernel(PrefillArgs args) {
         if (NW == 2 && slot < 0)
             prefill_store_mlp<FM>(args, acc, lds, wave, m0, ncol, 32 * FM * wm, lane);
         else
-            prefill_store_tile<FM>(args, acc, epi, m0, ncol, 64 * wn, 32 * FM * wm, lane, slot);
+            prefill_store_tile<FM, W::kEmit>(args, acc, epi, m0, ncol, 64 * wn, 32 * FM * wm, lane, slot);
     };
 
     const int P = gridDim.x;
@@ -500,7 +553,7 @@ prefill_kernel(PrefillArgs args) {
 __global__ void __launch_bounds__(256)
 prefill_finish(const float *__restrict__ partial, int dp_tiles, int64_t sk_units, int P, int64_t groups,
                   int mblocks, int64_t rows, int64_t n, void *out, int64_t ldc, int out_dtype, const void *residual,
-                  int nw) {
+                  int nw, EmitOperand emit) {
     __shared__ int wg[kPFinishMax];
     __shared__ int slot_of[kPFinishMax];
     __shared__ int count;
@@ -527,7 +580,8 @@ prefill_finish(const float *__restrict__ partial, int dp_tiles, int64_t sk_units
     const int e0 = (blockIdx.y * 256 + threadIdx.x) * 4;  // element of the tile
     const int tr = e0 / cols, tc = e0 % cols;
     const int64_t m = m0 + tr, col = n0 + tc;
-    if (m >= rows || col >= n) return;
+    const bool live = m < rows && col < n;
+    if (!live && !emit.norm_weight) return;
     auto sum_at = [&](int c) {
         f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
         for (int j0 = 0; j0 < contributors; j0 += 8) {
@@ -549,22 +603,14 @@ prefill_finish(const float *__restrict__ partial, int dp_tiles, int64_t sk_units
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = silu(v[e]) * u[e];
     }
-    const int64_t index = m * ldc + col;
-    if (out_dtype == SPLOSH_F32) {
-        if (residual) v += *(const f32x4 *)((const float *)residual + index);
-        *(f32x4 *)((float *)out + index) = v;
-    } else {
-        float o[4] = {v[0], v[1], v[2], v[3]};
-        if (residual) {
-            const u32x2 rb = *(const u32x2 *)((const uint16_t *)residual + index);
-            o[0] += bf16_bits_to_f32(rb[0] & 0xffffu);
-            o[1] += bf16_bits_to_f32(rb[0] >> 16);
-            o[2] += bf16_bits_to_f32(rb[1] & 0xffffu);
-            o[3] += bf16_bits_to_f32(rb[1] >> 16);
-        }
-        const u32x2 pk = {f32x2_to_bf16x2(o[0], o[1]), f32x2_to_bf16x2(o[2], o[3])};
-        *(u32x2 *)((uint16_t *)out + index) = pk;
+    if (emit.norm_weight) {
+        // One weight, fp32 output: a row's 256 columns are the 64 lanes of one wave, a 64-column
+        // band 16 consecutive lanes.
+        const f32x4 h = live ? prefill_out4(out, ldc, SPLOSH_F32, residual, m, col, v) : v;
+        prefill_emit_band(emit, n, m, col, h, live, (int)threadIdx.x & 63);
+        return;
     }
+    prefill_out4(out, ldc, out_dtype, residual, m, col, v);
 }
 
 // One tiled weight, 16-byte aligned rows of activations and outputs (vector epilogue), 32-bit
@@ -642,14 +688,15 @@ static hipError_t launch_prefill(const PrefillPlan &plan, PrefillArgs &args, int
     const int remainder = plan.tiles - plan.dp_tiles;
     hipLaunchKernelGGL(prefill_finish, dim3((unsigned)remainder, kPB * kPB / 1024 / W::kNW), dim3(256), 0, stream,
                        (const float *)args.partial, plan.dp_tiles, plan.sk_units, plan.grid, args.groups, plan.mblocks,
-                       rows, n, out, ldc, out_dtype, residual, W::kNW);
+                       rows, n, out, ldc, out_dtype, residual, W::kNW, args.emit);
     return hipGetLastError();
 }
 
 hipError_t launch_q4_prefill(const PrefillPlan &plan, const splosh_q4_weight &w, const uint16_t *a, int64_t lda,
                              void *out, int64_t ldc, int out_dtype, const void *residual, int64_t rows,
-                             void *workspace, hipStream_t stream) {
+                             void *workspace, hipStream_t stream, const EmitOperand *emit) {
     PrefillArgs args = {};
+    if (emit) args.emit = *emit;
     const int64_t groups = w.inner / kGroup;
     args.w[0] = w.packed;
     args.w[1] = w.scales;

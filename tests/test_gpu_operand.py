@@ -110,3 +110,28 @@ def test_gemm_emit(rt, rows, n, k, kernel):
     assert np.array_equal(_bits(values), want_v)
     np.testing.assert_allclose(sums.cpu().numpy(), want_s, rtol=1e-5, atol=1e-4)
     np.testing.assert_allclose(squares.cpu().numpy(), want_q, rtol=1e-5)
+
+
+@pytest.mark.parametrize("split", [True, False])
+@pytest.mark.parametrize("rows", [256, 300, 600])
+@pytest.mark.parametrize("n,k", [(640, 4352), (5120, 1280)])
+def test_gemm_emit_prefill(rt, rows, n, k, split):
+    """The emit from the prefill kernel's epilogue (AUTO from 256 rows): whole tiles write it from
+    the accumulators, tiles split over workgroups from prefill_finish (split=True: the default
+    workspace; False: an empty one, every tile whole). Same bar as test_gemm_emit."""
+    from qcheck import Q4Case, bf16_tensor, check_close
+    case = Q4Case(n, k, seed=rows + 2 * n)
+    a_bits = oracle.bf16_normal((rows, k), seed=rows + 1)
+    res = np.random.default_rng(rows + 1).normal(size=(rows, n)).astype(np.float32)
+    wn = torch.from_numpy(np.random.default_rng(8).normal(1.0, 0.1, size=n).astype(np.float32)).to(torch.bfloat16).cuda()
+    out = torch.from_numpy(res.copy()).cuda()
+    ws = None if split else torch.empty(0, dtype=torch.uint8, device="cuda")
+    got, values, sums, squares = rt.gemm_emit(case.w_tiled, bf16_tensor(a_bits), wn, out=out, residual=out,
+                                              workspace=ws)
+    ref = oracle.gemm_a_bf16_w_f32(a_bits, case.dense) + res
+    h = got.cpu().numpy()
+    check_close(h, ref, bf16_out=False, label=f"emit prefill out rows={rows} split={split}")
+    want_v, want_s, want_q = oracle.emit_operand(h, _bits(wn))
+    assert np.array_equal(_bits(values), want_v)
+    np.testing.assert_allclose(sums.cpu().numpy(), want_s, rtol=1e-5, atol=1e-4)
+    np.testing.assert_allclose(squares.cpu().numpy(), want_q, rtol=1e-5)
