@@ -86,6 +86,16 @@ __device__ __forceinline__ void buffer_load_lds16(rsrc_t r, void *lds_dst, uint3
 #endif
 }
 
+// 4 bytes a lane straight into LDS: lane l writes bytes [4 l, 4 l + 4) after `lds_dst`
+// (wave-uniform), as buffer_load_lds16.
+__device__ __forceinline__ void buffer_load_lds4(rsrc_t r, void *lds_dst, uint32_t voffset) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void *)lds_dst, 4, (int)voffset, 0, 0, 0);
+#else
+    (void)r, (void)lds_dst, (void)voffset;
+#endif
+}
+
 // s_waitcnt with only vmcnt bounded (expcnt and lgkmcnt left at their maxima), gfx9 encoding.
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {

@@ -123,17 +123,23 @@ struct Q4Format {
     static constexpr int kWLoads = kStageSide ? NW : NW * 3;  // weight loads per wave and step
     static constexpr int kUnitK = kGroup;
     static constexpr int kBandCols = CW * 32;
-    static constexpr int kSBuf = kStageSide ? NW * 2 * KW * kBandCols * 2 : 0;
-    static constexpr int kSidePer = kStageSide ? NW * 2 * KW * (kBandCols * 2 / 16) / (CW * KW) : 0;
+    // The staged sidecars of a step: NW x 2 arrays x KW groups x the band's 64 columns (bf16), in
+    // that order; wave v stages bytes [256 v, 256 v + 256), 4 a lane, with every lane's load
+    // issued (waves past the NW * 4 that hold data read out of range into the rest of the buffer):
+    // a branch there would split the step's schedule region and keep the compiler from
+    // interleaving the MFMAs with the dequantization.
+    static constexpr int kSBuf = kStageSide ? CW * KW * 256 : 0;
     static constexpr int kSideLoads = kStageSide ? 1 : 0;  // staging loads per wave and step
-    static_assert(!kStageSide || (KW * 8) % kSidePer == 0, "a wave's pieces lie in one array");
+    static_assert(!kStageSide || (KW == 4 && kBandCols == 64 && CW * KW >= NW * 4),
+                  "a wave's 256 bytes are two groups of one array");
     static constexpr int piece(int i) { return i; }
 
     rsrc_t q_rsrc[NW], s_rsrc[NW], b_rsrc[NW], side_rsrc;
     int wave, lane, kw, cw, r, h, ga, gb;
     uint32_t G32, q_lane, side_lane, q_group, side_group, side_src;
-    int side_g;      // group (within a step) of this lane's staged sidecar piece
+    int side_g;      // group (within a step) of this lane's staged sidecar dword
     bool side_bias;  // the array this wave stages: biases (else scales)
+    bool side_on;    // this wave stages data (else it reads out of range)
     u32x4 wq[D][NW];
     uint32_t wsc[D][NW], wbi[D][NW];
     float cs[NW], cb[NW];  // scale and bias of the step being dequantized
@@ -150,16 +156,15 @@ struct Q4Format {
             s_rsrc[w] = make_rsrc(args.scales[w], args.sidecar_bytes);
             b_rsrc[w] = make_rsrc(args.biases[w], args.sidecar_bytes);
         }
-        // The staged sidecars of a step are NW x 2 arrays x KW groups x 8 pieces of 16 bytes (the
-        // band's 64 columns of one group); wave v stages pieces [v kSidePer, (v + 1) kSidePer), all
-        // of one array: array a = weight a / 2, bias if a is odd.
-        const int piece0 = wave * kSidePer;
-        const int arr = piece0 / (KW * 8);
-        const int side_w = (arr >> 1) < NW ? (arr >> 1) : 0;
+        // Wave v stages array a = v / 2 (weight a / 2, biases if a is odd), groups 2 (v % 2) and
+        // 2 (v % 2) + 1 of the step: lane l the column pair l % 32 of group 2 (v % 2) + l / 32.
+        const int arr = wave >> 1;
+        side_on = (arr >> 1) < NW;
+        const int side_w = side_on ? (arr >> 1) : 0;
         side_bias = (arr & 1) != 0;
         side_rsrc = make_rsrc(side_bias ? (const void *)args.biases[side_w] : (const void *)args.scales[side_w],
                               args.sidecar_bytes);
-        side_g = ((piece0 + lane) / 8) % KW;
+        side_g = 2 * (wave & 1) + (lane >> 5);
     }
     __device__ int steps(int ga_, int gb_) const { return (gb_ - ga_ + KW - 1) / KW; }
     __device__ bool active(int t) const { return ga + t * KW + kw < gb; }
@@ -184,7 +189,7 @@ struct Q4Format {
             q_group = 128u * 32u;
             side_group = 128u * 2u;
             const uint32_t n0 = (uint32_t)band * kBandCols;
-            side_src = (((n0 >> 7) * G32 * 128u + (n0 & 127u)) * 2u) + 16u * (lane & 7);  // piece (v kSidePer + lane) % 8
+            side_src = (((n0 >> 7) * G32 * 128u + (n0 & 127u)) * 2u) + 4u * (lane & 31);  // column pair lane % 32
         } else {
             q_lane = col * (uint32_t)args.stride_words * 4u + 16u * h;
             side_lane = col * G32 * 2u;
@@ -193,15 +198,13 @@ struct Q4Format {
             side_src = 0;
         }
     }
-    // Sidecars of step t, straight into LDS (the staging buffer `sbuf`): lane l < kSidePer of
-    // wave v writes piece v kSidePer + l. Groups past the job re-read the last one.
+    // Sidecars of step t, straight into LDS (the staging buffer `sbuf`): wave v writes bytes
+    // [256 v, 256 v + 256). Groups past the job re-read the last one.
     __device__ void load_s(int t, char *sbuf) {
         if constexpr (kStageSide) {
-            if (lane < kSidePer) {
-                int g = ga + t * KW + side_g;
-                g = g < gb ? g : gb - 1;
-                buffer_load_lds16(side_rsrc, sbuf + wave * kSidePer * 16, side_src + (uint32_t)g * 256u);
-            }
+            int g = ga + t * KW + side_g;
+            g = g < gb ? g : gb - 1;
+            buffer_load_lds4(side_rsrc, sbuf + wave * 256, side_on ? side_src + (uint32_t)g * 256u : 0xFFFFFFF0u);
         }
     }
     // Codes (and row-major sidecars) of step t into ring slot `slot`; the group is a wave-uniform
@@ -254,7 +257,7 @@ struct Q4Format {
 // its 32-element groups 2 kw and 2 kw + 1, lane (r, h) group j = 2 kw + h of column r: a 16-byte
 // plane0 record of low nibbles and a 4-byte plane1 record of fifth bits. The block's 16-byte meta
 // record (fp16 d and dmin, twelve bytes of packed 6-bit scales and minimums) of each band column
-// is staged through LDS by wave 0, a step ahead, like the q4 sidecars.
+// is staged through LDS by waves 0 .. 3, a step ahead, like the q4 sidecars.
 //
 // Chunk order (gguf_formats.h:17-21): word c of a plane0 record holds elements 4c..4c+3 in its
 // nibbles at bits 0, 16, 4, 20 and 16+4c..16+4c+3 at bits 8, 24, 12, 28; the fifth bit of the
@@ -276,8 +279,11 @@ struct Q5Format {
     static constexpr int kWLoads = FIFTH ? 2 : 1;  // loads per wave and step: the mid-step wait counts them
     static constexpr int kUnitK = 256;
     static constexpr int kBandCols = CW * 32;
-    static constexpr int kSBuf = kBandCols * 16;
-    static constexpr int kSidePer = kBandCols / (CW * KW);  // meta records a wave stages per step
+    // The band's 64 meta records of a step (1 KB); wave v stages bytes [256 v, 256 v + 256), 4 a
+    // lane, every lane's load issued (waves 4 .. 7 read out of range into the rest of the buffer),
+    // as the q4 sidecars.
+    static constexpr int kSBuf = CW * KW * 256;
+    static_assert(kBandCols * 16 <= 4 * 256 && CW * KW >= 4, "four waves stage the meta records");
     static constexpr int kSideLoads = 1;
     static_assert(KW == 4, "four waves cover the eight groups of a block");
     static_assert(kBandCols <= 64, "one wave loads the band's meta records");
@@ -314,10 +320,10 @@ struct Q5Format {
         const uint32_t rec0 = ((col >> 7) * blocks * 8u + 2u * kw + h) * 128u + (col & 127u);
         p0_lane = rec0 * 16u;
         p1_lane = rec0 * 4u;
-        // The meta record this lane stages (lanes < kSidePer): band column v kSidePer + lane.
-        const int64_t mcol64 = (int64_t)band * kBandCols + wave * kSidePer + (lane % kSidePer);
+        // The meta record word this lane stages: word l % 4 of band column 16 v + l / 4.
+        const int64_t mcol64 = (int64_t)band * kBandCols + 16 * (wave & 3) + (lane >> 2);
         const uint32_t mcol = (uint32_t)(mcol64 < args.n ? mcol64 : args.n - 1);
-        m_lane = ((mcol >> 7) * blocks * 128u + (mcol & 127u)) * 16u;
+        m_lane = ((mcol >> 7) * blocks * 128u + (mcol & 127u)) * 16u + 4u * (lane & 3);
     }
     __device__ uint32_t block(int t) const {
         const int b = ga + t < gb ? ga + t : gb - 1;
@@ -325,7 +331,7 @@ struct Q5Format {
     }
     // Meta records of step t's block straight into LDS (`sbuf`, one 16-byte record a column).
     __device__ void load_s(int t, char *sbuf) {
-        if (lane < kSidePer) buffer_load_lds16(m_rsrc, sbuf + wave * kSidePer * 16, m_lane + block(t) * (128u * 16u));
+        buffer_load_lds4(m_rsrc, sbuf + wave * 256, wave < 4 ? m_lane + block(t) * (128u * 16u) : 0xFFFFFFF0u);
     }
     __device__ void load_w(int slot, int t) {
         const uint32_t b = block(t);
@@ -401,6 +407,7 @@ struct MmaShape {
     static constexpr size_t kEmitBytes = (size_t)kRows * 2 * 2 * sizeof(float);  // emit band sums
     static constexpr size_t kLds = kRedBytes + kEmitBytes > kABytes ? kRedBytes + kEmitBytes : kABytes;
     static_assert(D >= 3, "the pipeline below keeps weights at least three steps ahead");
+    static_assert(kLds <= 160 * 1024, "the workgroup's LDS fits a CU");
 };
 
 // Work split. The N columns form `bands` bands of CW * 32. Bands [0, dp_bands) are computed whole
