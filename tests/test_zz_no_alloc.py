@@ -49,6 +49,34 @@ def test_noalloc_matches_workspace_entry_point():
         assert torch.equal(out, want + res)
 
 
+# The scratch the entry point plans against: 16 KiB of counters and 8 MiB of partials.
+SCRATCH_BYTES = 16384 + (8 << 20)
+
+
+@pytest.mark.parametrize("rows,n,k", [(100, 1024, 4352), (300, 640, 2048)])
+def test_noalloc_above_64_rows(rows, n, k):
+    """Above 64 rows (the split-K tile kernel at 100 rows, the prefill kernel at 300) the kernels
+    plan against the scratch's size: their partials fit it or the call runs unsplit. The same call
+    through splosh_q4_gemm with a zero-filled workspace of that size gives the same bits; both
+    against the oracle. Run twice, so that the second call sees the scratch the first left."""
+    from splosh_amd import _lib
+    from splosh_amd import runtime as rt
+    lib = _lib.lib()
+    case = Q4Case(n, k, seed=rows)
+    a_bits = oracle.bf16_normal((rows, k), seed=rows + 1)
+    a = bf16_tensor(a_bits)
+    ws = torch.zeros(SCRATCH_BYTES, dtype=torch.uint8, device="cuda")
+    want = rt.gemm(case.w_tiled, a, out_dtype=torch.float32, workspace=ws)
+    check_close(want.cpu().numpy(), oracle.gemm_a_bf16_w_f32(a_bits, case.dense), bf16_out=False,
+                label=f"workspace rows={rows}")
+    for _ in range(2):
+        got = torch.full((rows, n), float("nan"), device="cuda")
+        st = _noalloc(lib, case.w_tiled, a, got)
+        assert st == 0, lib.splosh_last_error().decode()
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"rows={rows}: differs from splosh_q4_gemm"
+
+
 def test_noalloc_rejects_bad_arguments():
     from splosh_amd import _lib
     lib = _lib.lib()
