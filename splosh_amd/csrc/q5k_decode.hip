@@ -13,9 +13,11 @@
 // Arithmetic. In chunk order (gguf_formats.h:17-21) pair p of plane0 word c, (w >> 4p) & 0x000F000F,
 // holds two consecutive elements e0, e0 + 1 (e0 = 16 (p >> 1) + 4 c + 2 (p & 1)) in its 16-bit
 // halves, so the activations need no permutation: the pair meets the bf16 pair (x_e0, x_e0+1) as
-// staged. Their fifth bits are plane1 bits 8 c + 2 p and 8 c + 2 p + 1; with f those two bits,
-// (f * 0x80010) & 0x00100010 puts them at bits 4 and 20, so one more v_and_or_b32 gives
-// the bf16 pair (128 + code_e0, 128 + code_e0+1), code = nibble + 16 bit. With P = sum x (128 + code)
+// staged. Their fifth bits are plane1 bits 8 c + 2 p and 8 c + 2 p + 1: a 256-entry LDS table,
+// indexed by plane1 byte c, holds for each of the word's four pairs those two bits at bits 4 and 20
+// over the bf16 exponent of 128, so one v_and_or_b32 of the shifted word into table word p gives
+// the bf16 pair (128 + code_e0, 128 + code_e0+1), code = nibble + 16 bit (one 16-byte LDS read a
+// word instead of three VALU a pair). With P = sum x (128 + code)
 // and S = sum x over the group, sum x w = ds P - (128 ds + dm) S for w = code ds - dm, ds = d sc,
 // dm = dmin mn (GgufQuant.swift:191-212).
 #include "common.hpp"
@@ -40,6 +42,7 @@ struct Q5DecodeArgs {
 constexpr int kQ5DecodeDepth = 2;  // steps in flight a wave
 constexpr int kQ5DecodeWg = 256;
 constexpr int kQ5DecodeWaves = kQ5DecodeWg / 64;
+static_assert(kQ5DecodeWg == 256, "one thread builds each of the 256 fifth-bit table entries");
 
 __device__ __forceinline__ float qdot2(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_q, a), __builtin_bit_cast(bf16x2_q, b), c, false);
@@ -64,8 +67,10 @@ q5k_decode_kernel(Q5DecodeArgs args) {
     const uint32_t blocks = (uint32_t)G / 8u;
     const int steps = (G + GPS - 1) / GPS;
 
-    // LDS: xa[K / 8] (16 bytes: 8 activations as staged), xs[G] (group sums), red[waves][GPS][B].
-    u32x4 *xa = (u32x4 *)lds;
+    // LDS: fifth[256] (the fifth-bit table), xa[K / 8] (16 bytes: 8 activations as staged), xs[G]
+    // (group sums), red[waves][GPS][B].
+    u32x4 *fifth = (u32x4 *)lds;
+    u32x4 *xa = fifth + 256;
     float *xs = (float *)(xa + K / 8);
     float *red = xs + G;
 
@@ -119,7 +124,15 @@ q5k_decode_kernel(Q5DecodeArgs args) {
         __builtin_amdgcn_sched_barrier(0);  // the same load order as the loop's refills
     }
 
-    // 3. Stage the activations (the rest, for long K, after the weight loads went out).
+    // 3. The fifth-bit table (entry x, word p: bits 2p and 2p + 1 of x at bits 4 and 20, over
+    // 0x43004300), and the activations (the rest, for long K, after the weight loads went out).
+    if constexpr (FIFTH) {
+        const uint32_t x = threadIdx.x;  // kQ5DecodeWg == 256 entries
+        u32x4 e;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) e[p] = 0x43004300u | (((x >> (2 * p)) & 1u) << 4) | (((x >> (2 * p + 1)) & 1u) << 20);
+        fifth[x] = e;
+    }
 #pragma unroll
     for (int t = 0; t < kStage; ++t)
         if (threadIdx.x + t * kQ5DecodeWg < G) stage(threadIdx.x + t * kQ5DecodeWg, xin[t]);
@@ -132,7 +145,7 @@ q5k_decode_kernel(Q5DecodeArgs args) {
     }
     lds_barrier();  // LDS only: the weight loads stay in flight
 
-    const uint32_t kMask = 0x000F000Fu, kFifth = 0x00100010u;
+    const uint32_t kMask = 0x000F000Fu;
     uint32_t magic;  // the bf16 exponent of 128 in both halves
     asm("v_mov_b32 %0, 0x43004300" : "=v"(magic));
 
@@ -162,15 +175,11 @@ q5k_decode_kernel(Q5DecodeArgs args) {
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
                 const uint32_t w = c0[k][c];
+                u32x4 hi = {};  // the pairs' fifth bits over the exponent of 128
+                if constexpr (FIFTH) hi = fifth[__builtin_amdgcn_ubfe(c1[k], 8 * c, 8)];
 #pragma unroll
                 for (int p = 0; p < 4; ++p) {
-                    const uint32_t nib = qand_or(p ? w >> (4 * p) : w, kMask, magic);
-                    uint32_t pair = nib;
-                    if constexpr (FIFTH) {
-                        // Exactly the two fifth bits (wider input would carry into bit 20).
-                        const uint32_t fb = __builtin_amdgcn_ubfe(c1[k], 8 * c + 2 * p, 2);
-                        pair = qand_or(fb * 0x80010u, kFifth, nib);
-                    }
+                    const uint32_t pair = qand_or(p ? w >> (4 * p) : w, kMask, FIFTH ? hi[p] : magic);
                     const uint32_t xw = xq[(p >> 1) * 2 + (c >> 1)][(c & 1) * 2 + (p & 1)];  // x u32 8(p>>1) + 2c + (p&1)
                     if (p & 1) pb = qdot2(pair, xw, pb);
                     else pa = qdot2(pair, xw, pa);
@@ -206,7 +215,8 @@ q5k_decode_kernel(Q5DecodeArgs args) {
 }
 
 static size_t q5k_decode_lds(int64_t inner, int block) {
-    return (size_t)inner * 2 + (size_t)(inner / 32) * 4 + (size_t)kQ5DecodeWaves * (64 / block) * block * 4;
+    return (size_t)256 * 16 + (size_t)inner * 2 + (size_t)(inner / 32) * 4 +
+           (size_t)kQ5DecodeWaves * (64 / block) * block * 4;
 }
 
 bool q5k_decode_fits(int64_t rows, int64_t columns, int64_t inner) {
