@@ -118,6 +118,8 @@ struct Q4Format {
     static_assert(!GROUPED || (NW_ == 1 && TILED), "grouped calls take single tiled weights");
     static constexpr bool kGrouped = GROUPED;
     static constexpr bool kEmit = EMIT && !GROUPED;  // the epilogue emits the next norm's operand
+    static constexpr int kTblBytes = 0;
+    __device__ void build_table(char *, int) {}
     static constexpr int NW = NW_;
     static constexpr bool kStageSide = TILED;
     static constexpr int kWLoads = kStageSide ? NW : NW * 3;  // weight loads per wave and step
@@ -266,7 +268,8 @@ struct Q4Format {
 // (4c+2, 16+4c+2, 4c+3, 16+4c+3), and the fifth bits reach bit 4 of those bytes by one multiply:
 // byte x = plane1 >> 8c, ((x & 0x33) * 0x880110) & 0x10101010 moves bits 0, 4, 1, 5 to bits 4, 12,
 // 20, 28 (the other partial products and their carries stay below or between them), and x >> 2
-// does the same for the second set. Words 0 and 1 thus give elements 0..7 (bytes 0 and 2) and
+// does the same for the second set; both patterns come from a 256-entry LDS table built once a
+// workgroup. Words 0 and 1 thus give elements 0..7 (bytes 0 and 2) and
 // 16..23 (bytes 1 and 3) of the group, words 2 and 3 elements 8..15 and 24..31: sub-step i takes
 // activation piece ((i & 1) << 1) | (i >> 1). w = code d sc - dmin mn as one fma (d sc, code d sc
 // and dmin mn are exact in fp32), then RNE to bf16.
@@ -276,6 +279,19 @@ struct Q5Format {
     static constexpr bool kGrouped = false;
     static constexpr bool kEmit = false;
     static constexpr int NW = 1;
+    // The fifth bits of a plane1 byte x (four codes' worth for each of the two code words it
+    // serves) at bit 4 of each byte: entry x = {((x & 0x33) * 0x880110) & 0x10101010, the same
+    // of x >> 2}; one 8-byte LDS read instead of eight VALU a word.
+    static constexpr int kTblBytes = FIFTH ? 256 * 8 : 0;
+    const u32x2 *tbl = nullptr;
+    __device__ void build_table(char *t, int tid) {
+        tbl = (const u32x2 *)t;
+        if (tid < 256) {
+            const uint32_t x = (uint32_t)tid;
+            const u32x2 e = {((x & 0x33u) * 0x880110u) & 0x10101010u, (((x >> 2) & 0x33u) * 0x880110u) & 0x10101010u};
+            ((u32x2 *)t)[tid] = e;
+        }
+    }
     static constexpr int kWLoads = FIFTH ? 2 : 1;  // loads per wave and step: the mid-step wait counts them
     static constexpr int kUnitK = 256;
     static constexpr int kBandCols = CW * 32;
@@ -372,9 +388,9 @@ struct Q5Format {
                 lo[e] = w & 0x0F0F0F0Fu;
                 hi[e] = (w >> 4) & 0x0F0F0F0Fu;
                 if constexpr (FIFTH) {
-                    const uint32_t x = __builtin_amdgcn_ubfe(wh[slot], 8 * c, 8);
-                    lo[e] |= ((x & 0x33u) * 0x880110u) & 0x10101010u;
-                    hi[e] |= (((x >> 2) & 0x33u) * 0x880110u) & 0x10101010u;
+                    const u32x2 f = tbl[__builtin_amdgcn_ubfe(wh[slot], 8 * c, 8)];
+                    lo[e] |= f[0];
+                    hi[e] |= f[1];
                 }
             }
         }
@@ -389,7 +405,7 @@ struct Q5Format {
     }
 };
 
-template <int FM, int NW, int CW, int KW, int D, int SBUF>
+template <int FM, int NW, int CW, int KW, int D, int SBUF, int TBL = 0>
 struct MmaShape {
     static constexpr int kThreads = CW * KW * 64;
     static constexpr int kRows = FM * 32;
@@ -405,7 +421,9 @@ struct MmaShape {
     static constexpr size_t kRedBytes = (size_t)KW * CW * kAcc * 64 * sizeof(float);
     static constexpr size_t kABytes = (size_t)kNB * (kABuf + kSBuf);
     static constexpr size_t kEmitBytes = (size_t)kRows * 2 * 2 * sizeof(float);  // emit band sums
-    static constexpr size_t kLds = kRedBytes + kEmitBytes > kABytes ? kRedBytes + kEmitBytes : kABytes;
+    // The format's lookup table (TBL bytes, kept for the whole kernel) after the rest.
+    static constexpr size_t kTblAt = kRedBytes + kEmitBytes > kABytes ? kRedBytes + kEmitBytes : kABytes;
+    static constexpr size_t kLds = kTblAt + TBL;
     static_assert(D >= 3, "the pipeline below keeps weights at least three steps ahead");
     static_assert(kLds <= 160 * 1024, "the workgroup's LDS fits a CU");
 };
@@ -426,7 +444,7 @@ template <class F, int FM, int CW, int KW, int D>
 __global__ void __launch_bounds__(CW * KW * 64)
 mma_kernel(MmaArgs args) {
     constexpr int NW = F::NW;
-    using S = MmaShape<FM, NW, CW, KW, D, F::kSBuf>;
+    using S = MmaShape<FM, NW, CW, KW, D, F::kSBuf, F::kTblBytes>;
     static_assert(F::kBandCols == S::kBandCols, "one band geometry");
     constexpr int kWLoads = F::kWLoads;
     extern __shared__ __align__(16) uint16_t lds[];
@@ -445,6 +463,8 @@ mma_kernel(MmaArgs args) {
     __shared__ int fix_count;
     __shared__ uint16_t fix_list[kMmaMaxGrid];  // contributors of a shared band: 2 wg + slot
     F fmt(args, wave, lane);
+    // The format's lookup table, written here and first read after the job prologue's barrier.
+    if constexpr (F::kTblBytes > 0) fmt.build_table((char *)lds + S::kTblAt, tid);
     // Activation staging: this thread's piece j of a chunk sits at buffer position
     // (wave * kAPer + j) * 64 + lane, i.e. row m = pos / kKc, holding piece kc = (pos % kKc) ^ (m & 15)
     // of the row (an XOR swizzle, so the MFMA operand reads do not conflict), read from byte
@@ -1058,7 +1078,7 @@ size_t mma_workspace_bytes(int64_t rows, int64_t columns, int64_t groups, bool m
 
 template <class F, int FM>
 static hipError_t launch_mma_v(const MmaPlan &p, const MmaArgs &args, hipStream_t stream) {
-    using S = MmaShape<FM, F::NW, kMmaCW, kMmaKW, kMmaDepth, F::kSBuf>;
+    using S = MmaShape<FM, F::NW, kMmaCW, kMmaKW, kMmaDepth, F::kSBuf, F::kTblBytes>;
     auto kernel = mma_kernel<F, FM, kMmaCW, kMmaKW, kMmaDepth>;
     static bool once = [&] {
         (void)hipFuncSetAttribute((const void *)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)S::kLds);
