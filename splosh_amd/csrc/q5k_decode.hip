@@ -177,12 +177,16 @@ q5k_decode_kernel(Q5DecodeArgs args) {
                 const uint32_t w = c0[k][c];
                 u32x4 hi = {};  // the pairs' fifth bits over the exponent of 128
                 if constexpr (FIFTH) hi = fifth[__builtin_amdgcn_ubfe(c1[k], 8 * c, 8)];
+                // The word's four pairs first, then their dot products (a pair consumed by the very
+                // next instruction costs a wait state).
+                uint32_t pair[4];
+#pragma unroll
+                for (int p = 0; p < 4; ++p) pair[p] = qand_or(p ? w >> (4 * p) : w, kMask, FIFTH ? hi[p] : magic);
 #pragma unroll
                 for (int p = 0; p < 4; ++p) {
-                    const uint32_t pair = qand_or(p ? w >> (4 * p) : w, kMask, FIFTH ? hi[p] : magic);
                     const uint32_t xw = xq[(p >> 1) * 2 + (c >> 1)][(c & 1) * 2 + (p & 1)];  // x u32 8(p>>1) + 2c + (p&1)
-                    if (p & 1) pb = qdot2(pair, xw, pb);
-                    else pa = qdot2(pair, xw, pa);
+                    if (p & 1) pb = qdot2(pair[p], xw, pb);
+                    else pa = qdot2(pair[p], xw, pa);
                 }
             }
             const float live = g0 < G ? 1.0f : 0.0f;
