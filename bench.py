@@ -135,7 +135,7 @@ def build_workload(name, rt, torch, gen, kernel):
                "format": "mlx affine q4 g64, tiled128", "weight_copies": {nm: len(v) for nm, v in mats.items()}}
         return launches, sum(kb.values()), sum(kf.values()), kb, cfg, kf
     if name == "verify64":
-        m, h, inter = int(name[4:] or 64), 5120, 17408
+        m, h, inter = 64, 5120, 17408
         one = 2 * q4_bytes(inter, h) + q4_bytes(h, inter)
         ncopy = copies_for(one)
         sets = [(make_q4(rt, inter, h, gen), make_q4(rt, inter, h, gen), make_q4(rt, h, inter, gen))
