@@ -38,9 +38,9 @@ MEASURED_TRAFFIC = {
     ("verify64", "down"): 35308.5 * 2 * 1024 + 4444.6 * 1024,  # mma_kernel<Q4Format<1, true, 2, 4, 3, false, false>, 2, 2, 4, 3>
     ("decode1", "gemv"): 24560.9 * 2 * 1024 + 34.0 * 1024,  # q4_decode_kernel<1, 1, 32, 2>
     ("lmhead1", "lm_head"): 349280.3 * 2 * 1024 + 486.2 * 1024,  # q4_decode_kernel<1, 1, 32, 2>
-    ("q5k1", "q5k"): 30096.8 * 2 * 1024 + 10.0 * 1024,  # q5k_decode_kernel<8, 2, true>
-    ("q5k64", "q5k"): 41344.6 * 2 * 1024 + 4364.4 * 1024,  # mma_kernel<Q5Format<2, 4, 3, true>, 2, 2, 4, 3>
-    ("q5k16", "q5k"): 32946.8 * 2 * 1024 + 1095.7 * 1024,  # mma_kernel<Q5Format<2, 4, 3, true>, 1, 2, 4, 3>
+    ("q5k1", "q5k"): 30096.1 * 2 * 1024 + 10.0 * 1024,  # q5k_decode_kernel<8, 2, true>
+    ("q5k64", "q5k"): 41324.4 * 2 * 1024 + 4383.1 * 1024,  # mma_kernel<Q5Format<2, 4, 3, true>, 2, 2, 4, 3>
+    ("q5k16", "q5k"): 32873.8 * 2 * 1024 + 1082.3 * 1024,  # mma_kernel<Q5Format<2, 4, 3, true>, 1, 2, 4, 3>
     ("prefill2048", "prefill_up"): 266967.5 * 2 * 1024 + 114688.0 * 1024,  # prefill_kernel<Q4Stage>
     ("q5k2048", "q5k"): 347729.4 * 2 * 1024 + 98304.0 * 1024,  # prefill_kernel<Q5Stage<true>>
     ("q6k2048", "gguf"): 366940.1 * 2 * 1024 + 110080.0 * 1024,  # prefill_kernel<GgufStage<14>>
