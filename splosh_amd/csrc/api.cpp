@@ -162,7 +162,7 @@ int q4_gemm_impl(const splosh_q4_weight *w, const splosh_q4_weight *up, const ui
                             "stream kernel needs inner % 64 == 0, lda % 8 == 0 and aligned operands");
             if (wide16 && decode_ok) {
                 return hip_status(splosh::launch_q4_decode(*w, up, a, lda, out, ldc, out_dtype, residual, rows,
-                                                           stream),
+                                                           workspace, workspace ? workspace_bytes : 0, stream),
                                   "q4 decode launch");
             }
             if (wide16 && splosh::lanes_fit(rows, w->rows, w->inner, w->row_stride_words, up != nullptr)) {
@@ -374,7 +374,9 @@ size_t splosh_workspace_bytes(int64_t rows, int64_t columns, int64_t inner) {
     // (2 columns: the fused gate+up plans its tiles over both weights' columns.)
     const size_t prefill = rows > 64 && columns % 128 == 0 ? splosh::prefill_workspace_bytes(rows, 2 * columns, groups) : 0;
     const size_t gguf = inner % 64 == 0 ? splosh::gguf_tile_workspace_bytes(rows, columns, inner) : 0;
+    const size_t decode = splosh::decode_workspace_bytes(rows, columns, inner, 2);
     size_t need = tile > mma ? tile : mma;
+    need = need > decode ? need : decode;
     need = need > prefill ? need : prefill;
     return need > gguf ? need : gguf;
 }

@@ -28,6 +28,15 @@
 //
 // Reduction. The two half lanes of a row meet in a DPP swap, then the waves (and the groups of a
 // step) in LDS, and the workgroup writes its B rows (silu(g) * u for the fused gate+up).
+//
+// Balance. A CU that holds one block more than the others sets the time of the call (at
+// K=5120: 512 blocks 10.3 us, 516 blocks 11.6). With a workspace, when the blocks do not divide
+// evenly over the CUs, the whole rounds stay whole and each block of the last round is cut into S
+// slices of K, one a CU: every CU then holds its whole blocks and one slice. A slice writes its
+// rows' fp32 sums to the workspace and counts itself in on the block's arrival counter; the last
+// to arrive adds the S partials in slice order (so the result does not depend on who arrives
+// last) and writes the rows. Workgroup i goes to XCD i mod 8, and each XCD gets the same share of
+// whole blocks and of slices.
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -51,7 +60,18 @@ struct DecodeArgs {
     int rows;
     int out_dtype;
     uint32_t code_bytes, sidecar_bytes;
+    // Balance split (slices > 1): blocks [0, nwhole) whole, blocks nwhole + [0, tail) in `slices`
+    // slices of K each; partials [tail][slices][NW][rows][B] fp32 after the counters.
+    int nwhole, tail, slices;
+    float *partial;
+    int *counters;
+    uint32_t partial_bytes;
 };
+
+// Partials are summed on another CU, possibly of another XCD (whose L2 is not coherent with this
+// one's): written and read through to memory (gfx94x cache policy sc0 sc1).
+constexpr int kDecodeDeviceCpol = 1 | 16;
+constexpr int kDecodeMaxSlices = 16;  // slices of one block at most
 
 constexpr int kDecodeDepth = 2;  // steps in flight a wave (measured: 2 beats 1, 3, 4, 6 and 8)
 constexpr int kDecodeWg = 256;   // threads a workgroup
@@ -80,7 +100,26 @@ q4_decode_kernel(DecodeArgs args) {
     const int h = lane & 1, row = (lane >> 1) % B, gsub = (lane >> 1) / B;
     const int G = args.groups;
     const int K = G * kGroup;
-    const int steps = (G + GPS - 1) / GPS;
+    // This workgroup's block and its groups [ga, gb): all of K, or slice sl of tail block tb.
+    int blk, ga = 0, gb = G, tb = -1, sl = 0;
+    if (args.slices > 1) {
+        const int x = blockIdx.x & 7, j = blockIdx.x >> 3;
+        const int wpx = args.nwhole >> 3;  // whole blocks an XCD
+        if (j < wpx) {
+            blk = x * wpx + j;
+        } else {
+            const int q = x * ((args.tail * args.slices) >> 3) + (j - wpx);
+            tb = q / args.slices;
+            sl = q - tb * args.slices;
+            blk = args.nwhole + tb;
+            ga = (int)((int64_t)G * sl / args.slices);
+            gb = (int)((int64_t)G * (sl + 1) / args.slices);
+        }
+    } else {
+        blk = xcd_block(blockIdx.x, gridDim.x);
+    }
+    const int GS = gb - ga;  // groups of this workgroup
+    const int steps = (GS + GPS - 1) / GPS;
 
     // LDS: xp[R][K / 8] (16 bytes: the four activation pairs of a code word), xs[R][K / 32]
     // (half-group sums), red[waves][GPS][NW][R][B] (the partial sums).
@@ -88,19 +127,22 @@ q4_decode_kernel(DecodeArgs args) {
     float *xs = (float *)(xp + R * (K / 8));
     float *red = xs + R * (K / 32);
 
-    // 1. This thread's first activation slices (a half group: 32 values, four 16-byte loads).
-    const int items = R * (K / 32);
+    // 1. This thread's first activation slices (a half group: 32 values, four 16-byte loads). Item
+    // e is half group 2 ga + e mod 2 GS of row e / 2 GS, staged at index m (K / 32) + hg.
+    const int items = R * 2 * GS;
+    auto item_row = [&](int e) { return e / (2 * GS); };
+    auto item_hg = [&](int e) { return 2 * ga + e % (2 * GS); };
     constexpr int kStage = 2;
     u32x4 xin[kStage][4];
 #pragma unroll
     for (int t = 0; t < kStage; ++t) {
         const int e = threadIdx.x + t * kDecodeWg;
-        const int m = e < items ? e / (K / 32) : 0, hg = e < items ? e % (K / 32) : 0;
+        const int m = e < items ? item_row(e) : 0, hg = e < items ? item_hg(e) : 2 * ga;
         const u32x4 *src = (const u32x4 *)(args.a + (int64_t)(m < args.rows ? m : 0) * args.lda + hg * 32);
 #pragma unroll
         for (int j = 0; j < 4; ++j) xin[t][j] = src[j];
     }
-    auto stage = [&](int e, const u32x4 (&v)[4]) {
+    auto stage = [&](int e, const u32x4 (&v)[4]) {  // e: the staging index m (K / 32) + hg
         float s0 = 0.0f, s1 = 0.0f;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -126,14 +168,14 @@ q4_decode_kernel(DecodeArgs args) {
         s_rsrc[w] = make_rsrc(args.scales[w], args.sidecar_bytes);
         b_rsrc[w] = make_rsrc(args.biases[w], args.sidecar_bytes);
     }
-    const int64_t r0 = (int64_t)xcd_block(blockIdx.x, gridDim.x) * B;
+    const int64_t r0 = (int64_t)blk * B;
     const uint32_t tile_base = (uint32_t)(r0 >> 7) * (uint32_t)G * 128u + (uint32_t)(r0 & 127) + (uint32_t)row;
     u32x4 cq[D][NW];
     uint32_t cs[D][NW], cb[D][NW];
     auto issue = [&](int slot, int t) {
-        // Step t of this wave: groups (wave + 4 t) GPS + gsub.
-        const int g = (wave + kDecodeWaves * t) * GPS + gsub;
-        const bool live = g < G;
+        // Step t of this wave: groups ga + (wave + 4 t) GPS + gsub.
+        const int g = ga + (wave + kDecodeWaves * t) * GPS + gsub;
+        const bool live = g < gb;
         const uint32_t rec = tile_base + (uint32_t)(live ? g : 0) * 128u;
         // Out of range: zero, no memory traffic. (Every load is unconditional: a load under a branch
         // makes the compiler's wait counts conservative, which stalls the ring.)
@@ -157,15 +199,17 @@ q4_decode_kernel(DecodeArgs args) {
 
     // 3. Stage the activations (the rest of them, for long K, after the weight loads went out).
 #pragma unroll
-    for (int t = 0; t < kStage; ++t)
-        if (threadIdx.x + t * kDecodeWg < items) stage(threadIdx.x + t * kDecodeWg, xin[t]);
+    for (int t = 0; t < kStage; ++t) {
+        const int e = threadIdx.x + t * kDecodeWg;
+        if (e < items) stage(item_row(e) * (K / 32) + item_hg(e), xin[t]);
+    }
     for (int e = threadIdx.x + kStage * kDecodeWg; e < items; e += kDecodeWg) {
-        const int m = e / (K / 32), hg = e % (K / 32);
+        const int m = item_row(e), hg = item_hg(e);
         const u32x4 *src = (const u32x4 *)(args.a + (int64_t)(m < args.rows ? m : 0) * args.lda + hg * 32);
         u32x4 v[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) v[j] = src[j];
-        stage(e, v);
+        stage(m * (K / 32) + hg, v);
     }
     lds_barrier();  // LDS only: the weight loads stay in flight
 
@@ -184,8 +228,8 @@ q4_decode_kernel(DecodeArgs args) {
         for (int k = 0; k < D; ++k) {
             const int t = t0 + k;
             {
-                const int g = (wave + kDecodeWaves * t) * GPS + gsub;
-                const int hg = 2 * (g < G ? g : G - 1) + h;  // the lane's half group
+                const int g = ga + (wave + kDecodeWaves * t) * GPS + gsub;
+                const int hg = 2 * (g < gb ? g : gb - 1) + h;  // the lane's half group
                 u32x4 xq[R][4];
                 float sx[R];
 #pragma unroll
@@ -242,18 +286,22 @@ q4_decode_kernel(DecodeArgs args) {
             for (int m = 0; m < R; ++m) red[(((wave * GPS + gsub) * NW + w) * R + m) * B + row] = acc[w][m];
     }
     __syncthreads();
-    if ((int)threadIdx.x < R * B) {
-        const int m = threadIdx.x / B, rr = threadIdx.x % B;
-        const int64_t nn = r0 + rr;
-        float v[NW];
+    const int tid = threadIdx.x;
+    constexpr int RB = R * B;
+    const int m = tid / B, rr = tid % B;
+    const int64_t nn = r0 + rr;
+    float v[NW];
 #pragma unroll
-        for (int w = 0; w < NW; ++w) {
-            float sum = 0.0f;
+    for (int w = 0; w < NW; ++w) {
+        float sum = 0.0f;
+        if (tid < RB) {
 #pragma unroll
             for (int p = 0; p < kDecodeWaves * GPS; ++p) sum += red[((p * NW + w) * R + m) * B + rr];
-            v[w] = sum;
         }
-        if (m < args.rows && nn < args.n) {
+        v[w] = sum;
+    }
+    auto write_rows = [&] {
+        if (tid < RB && m < args.rows && nn < args.n) {
             float value = v[0];
             if constexpr (NW == 2) value = silu(v[0]) * v[1];
             const int64_t index = m * args.ldc + nn;
@@ -265,7 +313,49 @@ q4_decode_kernel(DecodeArgs args) {
                 ((uint16_t *)args.out)[index] = f32_to_bf16(value);
             }
         }
+    };
+    if (tb < 0) {
+        write_rows();
+        return;
     }
+    // A slice: its partial sums, the arrival, and, for the last slice to arrive, the sum of all.
+    const int S = args.slices;
+    const rsrc_t p_rsrc = make_rsrc(args.partial, args.partial_bytes);
+    auto part_off = [&](int slice, int w) { return (uint32_t)((((tb * S + slice) * NW + w) * RB + tid) * 4); };
+    if (tid < RB) {
+#pragma unroll
+        for (int w = 0; w < NW; ++w)
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v[w]), p_rsrc, part_off(sl, w), 0,
+                                                  kDecodeDeviceCpol);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial is in memory
+    __syncthreads();
+    __shared__ int arrival;
+    if (tid == 0) {
+        const int old = __hip_atomic_fetch_add(args.counters + tb, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        if (old == S - 1) __hip_atomic_store(args.counters + tb, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        arrival = old;
+    }
+    __syncthreads();
+    if (arrival != S - 1) return;
+    if (tid < RB) {
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            // Every slice's partial loaded first (one round trip), then added in slice order.
+            float part[kDecodeMaxSlices];
+#pragma unroll
+            for (int q = 0; q < kDecodeMaxSlices; ++q)
+                part[q] = q < S ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(p_rsrc, part_off(q, w), 0,
+                                                                                                 kDecodeDeviceCpol))
+                                : 0.0f;
+            float sum = 0.0f;
+#pragma unroll
+            for (int q = 0; q < kDecodeMaxSlices; ++q)
+                if (q < S) sum += part[q];
+            v[w] = sum;
+        }
+    }
+    write_rows();
 }
 
 static int decode_cus() {
@@ -290,11 +380,43 @@ bool decode_fits(int64_t rows, int64_t columns, int64_t inner, int order) {
     return decode_lds(rows, inner, 2, 16) <= 64 * 1024 && columns * (inner / kGroup) * 32 < ((int64_t)1 << 32) - 4096;
 }
 
+// The balance split of a call: blocks [0, nwhole) whole and `tail` blocks in `slices` slices of K
+// (slices = 1: every block whole). It applies when the blocks do not divide evenly over the CUs
+// and each CU can take one slice of the last round; the XCD interleave of the kernel needs the
+// whole blocks and the slices to divide by 8.
+struct DecodeSplit {
+    int nwhole, tail, slices;
+};
+static DecodeSplit plan_decode_split(int64_t columns, int groups) {
+    const int block = decode_block(columns), cus = decode_cus();
+    const int64_t blocks = columns / block, base = blocks / cus * cus, tail = blocks - base;
+    DecodeSplit p{(int)blocks, 0, 1};
+    // Only where each CU already holds two whole blocks or more (at 320 blocks of 16 rows on 256
+    // CUs, one whole block and a slice took 7.07 us against 6.85 unsplit).
+    if (base < 2 * cus || tail == 0 || base % 8 != 0) return p;
+    int slices = (int)(cus / tail);
+    slices = slices < groups ? slices : groups;
+    slices = slices < kDecodeMaxSlices ? slices : kDecodeMaxSlices;
+    while (slices >= 2 && (tail * slices) % 8 != 0) --slices;
+    if (slices >= 2) p = DecodeSplit{(int)base, (int)tail, slices};
+    return p;
+}
+
+// The workspace's first 16 KiB hold the arrival counters (zero between calls, shared with the other
+// kernels); the partials follow.
+constexpr size_t kDecodeCounterBytes = 16384;
+size_t decode_workspace_bytes(int64_t rows, int64_t columns, int64_t inner, int nw) {
+    if (rows < 1 || rows > 2 || inner % kGroup != 0 || columns % 128 != 0) return 0;
+    const DecodeSplit p = plan_decode_split(columns, (int)(inner / kGroup));
+    if (p.slices < 2) return 0;
+    return kDecodeCounterBytes + (size_t)p.tail * p.slices * nw * rows * decode_block(columns) * sizeof(float);
+}
+
 template <int R, int NW, int B>
 static hipError_t launch_decode_v(const DecodeArgs &args, hipStream_t stream) {
     const size_t lds = decode_lds(R, (int64_t)args.groups * kGroup, NW, B);
-    hipLaunchKernelGGL((q4_decode_kernel<R, NW, B, kDecodeDepth>), dim3((unsigned)(args.n / B)), dim3(kDecodeWg), lds,
-                       stream, args);
+    const unsigned grid = args.slices > 1 ? (unsigned)(args.nwhole + args.tail * args.slices) : (unsigned)(args.n / B);
+    hipLaunchKernelGGL((q4_decode_kernel<R, NW, B, kDecodeDepth>), dim3(grid), dim3(kDecodeWg), lds, stream, args);
     return hipGetLastError();
 }
 
@@ -305,8 +427,8 @@ static hipError_t launch_decode_rn(const DecodeArgs &args, hipStream_t stream) {
 
 hipError_t launch_q4_decode(const splosh_q4_weight &w, const splosh_q4_weight *up, const uint16_t *a, int64_t lda,
                             void *out, int64_t ldc, int out_dtype, const void *residual, int64_t rows,
-                            hipStream_t stream) {
-    DecodeArgs args;
+                            void *workspace, size_t workspace_bytes, hipStream_t stream) {
+    DecodeArgs args = {};
     args.packed[0] = w.packed;
     args.scales[0] = w.scales;
     args.biases[0] = w.biases;
@@ -324,6 +446,22 @@ hipError_t launch_q4_decode(const splosh_q4_weight &w, const splosh_q4_weight *u
     args.out_dtype = out_dtype;
     args.code_bytes = (uint32_t)(w.rows * args.groups * 32);
     args.sidecar_bytes = (uint32_t)(w.rows * args.groups * 2);
+    // The balance split when the workspace holds its partials (else every block whole).
+    const int nw = up ? 2 : 1;
+    const DecodeSplit split = plan_decode_split(w.rows, args.groups);
+    const size_t need = split.slices > 1 ? kDecodeCounterBytes + (size_t)split.tail * split.slices * nw * rows *
+                                                                     decode_block(w.rows) * sizeof(float)
+                                         : 0;
+    if (need > 0 && workspace && workspace_bytes >= need) {
+        args.nwhole = split.nwhole;
+        args.tail = split.tail;
+        args.slices = split.slices;
+        args.counters = (int *)workspace;
+        args.partial = (float *)((char *)workspace + kDecodeCounterBytes);
+        args.partial_bytes = (uint32_t)(need - kDecodeCounterBytes);
+    } else {
+        args.slices = 1;
+    }
     if (rows == 1)
         return up ? launch_decode_rn<1, 2>(args, stream) : launch_decode_rn<1, 1>(args, stream);
     return up ? launch_decode_rn<2, 2>(args, stream) : launch_decode_rn<2, 1>(args, stream);

@@ -53,11 +53,14 @@ hipError_t launch_q4_lanes(const StreamPlan &plan, const splosh_q4_weight &w, co
                            const void *residual, int64_t rows, hipStream_t stream);
 
 // The decode kernel on every CU for one or two rows of tiled weights (decode.hip): a workgroup a
-// block of 16 or 32 output rows over the whole of K, no workspace.
+// block of 16 or 32 output rows over the whole of K. With a workspace of decode_workspace_bytes
+// (zero: not needed) the last round of blocks is split over K so that every CU gets the same work;
+// without one every block is whole.
 bool decode_fits(int64_t rows, int64_t columns, int64_t inner, int order);
+size_t decode_workspace_bytes(int64_t rows, int64_t columns, int64_t inner, int nw);
 hipError_t launch_q4_decode(const splosh_q4_weight &w, const splosh_q4_weight *up, const uint16_t *a, int64_t lda,
                             void *out, int64_t ldc, int out_dtype, const void *residual, int64_t rows,
-                            hipStream_t stream);
+                            void *workspace, size_t workspace_bytes, hipStream_t stream);
 
 // The dequant-to-bf16 weight-streaming MFMA kernel for up to 64 rows (mma.hip). Split K over
 // workgroups (stream-K) uses a caller workspace of mma_workspace_bytes(); without one every band

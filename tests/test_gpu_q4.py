@@ -373,3 +373,35 @@ def test_decode_kernel(rt, rows, mlp, n, k):
         out = torch.from_numpy(base.copy()).cuda()
         rt.gemm(g.w_tiled, bf16_tensor(a_bits), out=out, residual=out, kernel=rt.STREAM, workspace=ws)
         check_close(out.cpu().numpy(), ref + base, bf16_out=False, tight=True, label="decode residual")
+
+
+@pytest.mark.parametrize("rows", [1, 2])
+@pytest.mark.parametrize("mlp", [False, True])
+@pytest.mark.parametrize("n,k", [(17408, 5120), (17408, 320), (16896, 1024), (5120, 1024)])
+def test_decode_balance_split(rt, rows, mlp, n, k):
+    """The decode kernel with a workspace: when the row blocks do not divide evenly over the CUs
+    (and every CU holds two whole blocks or more) the last round's blocks are cut into slices of K
+    (on 256 CUs: 544 blocks = 512 whole + 32 in 8 slices; K=320, 5 groups: 5 slices; 528 blocks:
+    16 slices of one group; 320 blocks of 16 rows: no split). Against the oracle, the same bits on
+    a second call, every arrival counter back at zero, and within rounding of the unsplit kernel
+    (an empty workspace)."""
+    g, u = Q4Case(n, k, seed=730 + rows), Q4Case(n, k, seed=740 + rows)
+    a_bits = oracle.bf16_normal((rows, k), seed=750 + rows)
+    need = rt.workspace_bytes(rows, n, k)
+    ws = torch.zeros(max(need, 16384), dtype=torch.uint8, device="cuda")
+    empty = torch.empty(0, dtype=torch.uint8, device="cuda")
+    if mlp:
+        ref = oracle.silu_mul(oracle.gemm_a_bf16_w_f32(a_bits, g.dense), oracle.gemm_a_bf16_w_f32(a_bits, u.dense))
+        run = lambda w: rt.mlp_in(g.w_tiled, u.w_tiled, bf16_tensor(a_bits), out_dtype=torch.float32,
+                                  kernel=rt.STREAM, workspace=w)
+    else:
+        ref = oracle.gemm_a_bf16_w_f32(a_bits, g.dense)
+        run = lambda w: rt.gemm(g.w_tiled, bf16_tensor(a_bits), out_dtype=torch.float32, kernel=rt.STREAM,
+                                workspace=w)
+    first = run(ws).cpu().numpy()
+    second = run(ws).cpu().numpy()
+    assert np.array_equal(first, second), "calls differ"
+    assert int(ws[:16384].view(torch.int32).abs().sum().item()) == 0, "arrival counters left set"
+    check_close(first, ref, bf16_out=False, tight=not mlp, label=f"decode split {n}x{k} rows={rows} mlp={mlp}")
+    whole = run(empty).cpu().numpy()
+    check_close(first, whole, bf16_out=False, tight=True, label=f"split vs whole {n}x{k}")
