@@ -69,8 +69,10 @@ typedef enum splosh_kernel {
                                    rows: TILE up to 80 rows or 8192 columns), else TILE; SCALAR for
                                    operands no other kernel takes */
     SPLOSH_KERNEL_STREAM = 1,   /* weight streaming on raw codes: the every-CU decode kernel for
-                                   1-2 rows of tiled weights, the lane-per-row kernel for row-major
-                                   ones, the raw-code MFMA kernel for more rows */
+                                   1-2 rows of tiled weights (with a workspace it splits the last
+                                   round of row blocks over K, so every CU gets the same share),
+                                   the lane-per-row kernel for row-major ones, the raw-code MFMA
+                                   kernel for more rows */
     SPLOSH_KERNEL_DEQUANT = 2,  /* rows <= 64: stream-K MFMA kernel on weights dequantized to bf16 in
                                    registers; uses the workspace for split bands when given one */
     SPLOSH_KERNEL_TILE = 3,     /* any rows: LDS-tiled dequant-to-bf16 MFMA GEMM (prefill) */
