@@ -375,8 +375,10 @@ size_t splosh_workspace_bytes(int64_t rows, int64_t columns, int64_t inner) {
     const size_t prefill = rows > 64 && columns % 128 == 0 ? splosh::prefill_workspace_bytes(rows, 2 * columns, groups) : 0;
     const size_t gguf = inner % 64 == 0 ? splosh::gguf_tile_workspace_bytes(rows, columns, inner) : 0;
     const size_t decode = splosh::decode_workspace_bytes(rows, columns, inner, 2);
+    const size_t q5k_decode = splosh::q5k_decode_workspace_bytes(rows, columns, inner);
     size_t need = tile > mma ? tile : mma;
     need = need > decode ? need : decode;
+    need = need > q5k_decode ? need : q5k_decode;
     need = need > prefill ? need : prefill;
     return need > gguf ? need : gguf;
 }
@@ -584,7 +586,8 @@ static int gguf_gemm(const splosh_q5k_weight *w_in, bool fifth, const uint16_t *
     const bool planes_ok = aligned(w->plane0, 16) && (!fifth || aligned(w->plane1, 4)) && aligned(w->meta, 16);
     if (kernel == SPLOSH_KERNEL_AUTO && planes_ok && lda % 4 == 0 && aligned(a, 16) &&
         splosh::q5k_decode_fits(rows, w->rows, w->inner))
-        return hip_status(splosh::launch_q5k_decode(*w, a, out, out_dtype, residual, stream, ho.hs, ho.vph),
+        return hip_status(splosh::launch_q5k_decode(*w, a, out, out_dtype, residual, workspace,
+                                                    workspace ? workspace_bytes : 0, stream, ho.hs, ho.vph),
                           "q5k decode launch");
     // Every other kernel reads the activations in place: a head-ordered call gives it a permuted
     // copy (dense rows of `inner`, 256-byte aligned, at the end of the workspace).

@@ -150,4 +150,109 @@ __device__ __forceinline__ float cvt_byte(uint32_t x, int j) {
 // divide: the result is rounded to bf16 or summed in fp32 afterwards.
 __device__ __forceinline__ float silu(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 
+// ---- Balance split of a streaming kernel's last round -----------------------------------------
+//
+// A kernel whose workgroups each own a block of output rows over all of K runs as long as the CUs
+// that hold one block more than the others. When the blocks do not divide evenly over the CUs,
+// the whole rounds stay whole and each block of the last round is cut into `slices` ranges of K
+// units, one workgroup a slice, so that every CU holds its whole blocks and one slice. A slice
+// writes its fp32 sums to a workspace and counts itself in on the block's arrival counter; the
+// last to arrive adds the partials in slice order (the result does not depend on who arrives
+// last) and writes the rows.
+
+struct BalanceSplit {
+    int nwhole, tail, slices;  // slices < 2: every block whole
+};
+constexpr int kBalanceMaxSlices = 16;
+// The workspace's first 16 KiB hold the arrival counters (zero between calls, the region every
+// kernel's counters share); the partials follow.
+constexpr size_t kBalanceCounterBytes = 16384;
+
+// The split for `blocks` row blocks of `units` units of K on `cus` CUs: only where every CU
+// already holds two whole blocks or more, and the whole blocks and the slices divide by 8 (the
+// XCD interleave of balance_block).
+inline BalanceSplit plan_balance(int64_t blocks, int cus, int units) {
+    const int64_t base = blocks / cus * cus, tail = blocks - base;
+    BalanceSplit p{(int)blocks, 0, 1};
+    if (base < 2 * (int64_t)cus || tail == 0 || base % 8 != 0) return p;
+    int slices = (int)(cus / tail);
+    slices = slices < units ? slices : units;
+    slices = slices < kBalanceMaxSlices ? slices : kBalanceMaxSlices;
+    while (slices >= 2 && (tail * slices) % 8 != 0) --slices;
+    if (slices >= 2) p = BalanceSplit{(int)base, (int)tail, slices};
+    return p;
+}
+
+// Workgroup `id` of the split grid: its block and units [ua, ub); tb >= 0 (and its slice sl) for a
+// slice of tail block tb. Workgroup i goes to XCD i mod 8, and each XCD takes the same share of
+// whole blocks (contiguous, as xcd_block) and of slices. Without a split, xcd_block's order.
+__device__ __forceinline__ void balance_block(int id, int grid, int nwhole, int tail, int slices, int units, int &blk,
+                                              int &ua, int &ub, int &tb, int &sl) {
+    ua = 0;
+    ub = units;
+    tb = -1;
+    sl = 0;
+    if (slices < 2) {
+        blk = xcd_block(id, grid);
+        return;
+    }
+    const int x = id & 7, j = id >> 3;
+    const int wpx = nwhole >> 3;  // whole blocks an XCD
+    if (j < wpx) {
+        blk = x * wpx + j;
+        return;
+    }
+    const int q = x * ((tail * slices) >> 3) + (j - wpx);
+    tb = q / slices;
+    sl = q - tb * slices;
+    blk = nwhole + tb;
+    ua = (int)((int64_t)units * sl / slices);
+    ub = (int)((int64_t)units * (sl + 1) / slices);
+}
+
+// The merge of a slice's NV values a thread (threads [0, nact) hold values): written through to
+// memory (gfx94x cache policy sc0 sc1: the summing workgroup may run on another XCD, whose L2 is
+// not coherent with this one's), then the arrival. Returns true for the last slice to arrive,
+// with `v` replaced by the sums over all slices in slice order. Every thread of the workgroup
+// calls it.
+template <int NV>
+__device__ __forceinline__ bool balance_merge(float (&v)[NV], int tid, int nact, int tb, int sl, int slices,
+                                              float *partial, uint32_t partial_bytes, int *counters) {
+    constexpr int kCpol = 1 | 16;
+    const rsrc_t p_rsrc = make_rsrc(partial, partial_bytes);
+    auto off = [&](int slice, int j) { return (uint32_t)((((tb * slices + slice) * NV + j) * nact + tid) * 4); };
+    if (tid < nact) {
+#pragma unroll
+        for (int j = 0; j < NV; ++j)
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v[j]), p_rsrc, off(sl, j), 0, kCpol);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial is in memory
+    __syncthreads();
+    __shared__ int arrival;
+    if (tid == 0) {
+        const int old = __hip_atomic_fetch_add(counters + tb, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        if (old == slices - 1) __hip_atomic_store(counters + tb, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        arrival = old;
+    }
+    __syncthreads();
+    if (arrival != slices - 1) return false;
+    if (tid < nact) {
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            // Every slice's partial loaded first (one round trip), then added in slice order.
+            float part[kBalanceMaxSlices];
+#pragma unroll
+            for (int q = 0; q < kBalanceMaxSlices; ++q)
+                part[q] = q < slices ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(p_rsrc, off(q, j), 0, kCpol))
+                                     : 0.0f;
+            float sum = 0.0f;
+#pragma unroll
+            for (int q = 0; q < kBalanceMaxSlices; ++q)
+                if (q < slices) sum += part[q];
+            v[j] = sum;
+        }
+    }
+    return true;
+}
+
 }  // namespace splosh

@@ -30,13 +30,8 @@
 // step) in LDS, and the workgroup writes its B rows (silu(g) * u for the fused gate+up).
 //
 // Balance. A CU that holds one block more than the others sets the time of the call (at
-// K=5120: 512 blocks 10.3 us, 516 blocks 11.6). With a workspace, when the blocks do not divide
-// evenly over the CUs, the whole rounds stay whole and each block of the last round is cut into S
-// slices of K, one a CU: every CU then holds its whole blocks and one slice. A slice writes its
-// rows' fp32 sums to the workspace and counts itself in on the block's arrival counter; the last
-// to arrive adds the S partials in slice order (so the result does not depend on who arrives
-// last) and writes the rows. Workgroup i goes to XCD i mod 8, and each XCD gets the same share of
-// whole blocks and of slices.
+// K=5120: 512 blocks 10.3 us, 516 blocks 11.6). With a workspace the last round of blocks is
+// split over K (plan_balance / balance_block / balance_merge in common.hpp), one slice a CU.
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -68,10 +63,7 @@ struct DecodeArgs {
     uint32_t partial_bytes;
 };
 
-// Partials are summed on another CU, possibly of another XCD (whose L2 is not coherent with this
-// one's): written and read through to memory (gfx94x cache policy sc0 sc1).
-constexpr int kDecodeDeviceCpol = 1 | 16;
-constexpr int kDecodeMaxSlices = 16;  // slices of one block at most
+
 
 constexpr int kDecodeDepth = 2;  // steps in flight a wave (measured: 2 beats 1, 3, 4, 6 and 8)
 constexpr int kDecodeWg = 256;   // threads a workgroup
@@ -101,23 +93,8 @@ q4_decode_kernel(DecodeArgs args) {
     const int G = args.groups;
     const int K = G * kGroup;
     // This workgroup's block and its groups [ga, gb): all of K, or slice sl of tail block tb.
-    int blk, ga = 0, gb = G, tb = -1, sl = 0;
-    if (args.slices > 1) {
-        const int x = blockIdx.x & 7, j = blockIdx.x >> 3;
-        const int wpx = args.nwhole >> 3;  // whole blocks an XCD
-        if (j < wpx) {
-            blk = x * wpx + j;
-        } else {
-            const int q = x * ((args.tail * args.slices) >> 3) + (j - wpx);
-            tb = q / args.slices;
-            sl = q - tb * args.slices;
-            blk = args.nwhole + tb;
-            ga = (int)((int64_t)G * sl / args.slices);
-            gb = (int)((int64_t)G * (sl + 1) / args.slices);
-        }
-    } else {
-        blk = xcd_block(blockIdx.x, gridDim.x);
-    }
+    int blk, ga, gb, tb, sl;
+    balance_block(blockIdx.x, gridDim.x, args.nwhole, args.tail, args.slices, G, blk, ga, gb, tb, sl);
     const int GS = gb - ga;  // groups of this workgroup
     const int steps = (GS + GPS - 1) / GPS;
 
@@ -314,47 +291,8 @@ q4_decode_kernel(DecodeArgs args) {
             }
         }
     };
-    if (tb < 0) {
-        write_rows();
-        return;
-    }
-    // A slice: its partial sums, the arrival, and, for the last slice to arrive, the sum of all.
-    const int S = args.slices;
-    const rsrc_t p_rsrc = make_rsrc(args.partial, args.partial_bytes);
-    auto part_off = [&](int slice, int w) { return (uint32_t)((((tb * S + slice) * NW + w) * RB + tid) * 4); };
-    if (tid < RB) {
-#pragma unroll
-        for (int w = 0; w < NW; ++w)
-            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v[w]), p_rsrc, part_off(sl, w), 0,
-                                                  kDecodeDeviceCpol);
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial is in memory
-    __syncthreads();
-    __shared__ int arrival;
-    if (tid == 0) {
-        const int old = __hip_atomic_fetch_add(args.counters + tb, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        if (old == S - 1) __hip_atomic_store(args.counters + tb, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        arrival = old;
-    }
-    __syncthreads();
-    if (arrival != S - 1) return;
-    if (tid < RB) {
-#pragma unroll
-        for (int w = 0; w < NW; ++w) {
-            // Every slice's partial loaded first (one round trip), then added in slice order.
-            float part[kDecodeMaxSlices];
-#pragma unroll
-            for (int q = 0; q < kDecodeMaxSlices; ++q)
-                part[q] = q < S ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(p_rsrc, part_off(q, w), 0,
-                                                                                                 kDecodeDeviceCpol))
-                                : 0.0f;
-            float sum = 0.0f;
-#pragma unroll
-            for (int q = 0; q < kDecodeMaxSlices; ++q)
-                if (q < S) sum += part[q];
-            v[w] = sum;
-        }
-    }
+    if (tb >= 0 && !balance_merge<NW>(v, tid, RB, tb, sl, args.slices, args.partial, args.partial_bytes, args.counters))
+        return;  // a slice whose block another slice finishes
     write_rows();
 }
 
@@ -380,36 +318,15 @@ bool decode_fits(int64_t rows, int64_t columns, int64_t inner, int order) {
     return decode_lds(rows, inner, 2, 16) <= 64 * 1024 && columns * (inner / kGroup) * 32 < ((int64_t)1 << 32) - 4096;
 }
 
-// The balance split of a call: blocks [0, nwhole) whole and `tail` blocks in `slices` slices of K
-// (slices = 1: every block whole). It applies when the blocks do not divide evenly over the CUs
-// and each CU can take one slice of the last round; the XCD interleave of the kernel needs the
-// whole blocks and the slices to divide by 8.
-struct DecodeSplit {
-    int nwhole, tail, slices;
-};
-static DecodeSplit plan_decode_split(int64_t columns, int groups) {
-    const int block = decode_block(columns), cus = decode_cus();
-    const int64_t blocks = columns / block, base = blocks / cus * cus, tail = blocks - base;
-    DecodeSplit p{(int)blocks, 0, 1};
-    // Only where each CU already holds two whole blocks or more (at 320 blocks of 16 rows on 256
-    // CUs, one whole block and a slice took 7.07 us against 6.85 unsplit).
-    if (base < 2 * cus || tail == 0 || base % 8 != 0) return p;
-    int slices = (int)(cus / tail);
-    slices = slices < groups ? slices : groups;
-    slices = slices < kDecodeMaxSlices ? slices : kDecodeMaxSlices;
-    while (slices >= 2 && (tail * slices) % 8 != 0) --slices;
-    if (slices >= 2) p = DecodeSplit{(int)base, (int)tail, slices};
-    return p;
+static BalanceSplit plan_decode_split(int64_t columns, int groups) {
+    return plan_balance(columns / decode_block(columns), decode_cus(), groups);
 }
 
-// The workspace's first 16 KiB hold the arrival counters (zero between calls, shared with the other
-// kernels); the partials follow.
-constexpr size_t kDecodeCounterBytes = 16384;
 size_t decode_workspace_bytes(int64_t rows, int64_t columns, int64_t inner, int nw) {
     if (rows < 1 || rows > 2 || inner % kGroup != 0 || columns % 128 != 0) return 0;
-    const DecodeSplit p = plan_decode_split(columns, (int)(inner / kGroup));
+    const BalanceSplit p = plan_decode_split(columns, (int)(inner / kGroup));
     if (p.slices < 2) return 0;
-    return kDecodeCounterBytes + (size_t)p.tail * p.slices * nw * rows * decode_block(columns) * sizeof(float);
+    return kBalanceCounterBytes + (size_t)p.tail * p.slices * nw * rows * decode_block(columns) * sizeof(float);
 }
 
 template <int R, int NW, int B>
@@ -448,17 +365,15 @@ hipError_t launch_q4_decode(const splosh_q4_weight &w, const splosh_q4_weight *u
     args.sidecar_bytes = (uint32_t)(w.rows * args.groups * 2);
     // The balance split when the workspace holds its partials (else every block whole).
     const int nw = up ? 2 : 1;
-    const DecodeSplit split = plan_decode_split(w.rows, args.groups);
-    const size_t need = split.slices > 1 ? kDecodeCounterBytes + (size_t)split.tail * split.slices * nw * rows *
-                                                                     decode_block(w.rows) * sizeof(float)
-                                         : 0;
+    const BalanceSplit split = plan_decode_split(w.rows, args.groups);
+    const size_t need = decode_workspace_bytes(rows, w.rows, w.inner, nw);
     if (need > 0 && workspace && workspace_bytes >= need) {
         args.nwhole = split.nwhole;
         args.tail = split.tail;
         args.slices = split.slices;
         args.counters = (int *)workspace;
-        args.partial = (float *)((char *)workspace + kDecodeCounterBytes);
-        args.partial_bytes = (uint32_t)(need - kDecodeCounterBytes);
+        args.partial = (float *)((char *)workspace + kBalanceCounterBytes);
+        args.partial_bytes = (uint32_t)(need - kBalanceCounterBytes);
     } else {
         args.slices = 1;
     }

@@ -181,8 +181,10 @@ hipError_t launch_gguf_prefill(const PrefillPlan &plan, int type, const uint8_t 
 
 // The decode kernel for one activation row of Q5_K planes (q5k_decode.hip).
 bool q5k_decode_fits(int64_t rows, int64_t columns, int64_t inner);
+size_t q5k_decode_workspace_bytes(int64_t rows, int64_t columns, int64_t inner);
 hipError_t launch_q5k_decode(const splosh_q5k_weight &w, const uint16_t *a, void *out, int out_dtype,
-                             const void *residual, hipStream_t stream, int hs = -1, int vph = 0);
+                             const void *residual, void *workspace, size_t workspace_bytes, hipStream_t stream,
+                             int hs = -1, int vph = 0);
 
 // Operand producers (operand.hip).
 hipError_t launch_prepare_operand(const float *x, int64_t ldx, int64_t rows, int64_t dim, uint16_t *out, int64_t ldo,

@@ -37,6 +37,12 @@ struct Q5DecodeArgs {
     int out_dtype;
     uint32_t p0_bytes, p1_bytes, meta_bytes;
     int hs, vph;  // value-head order of the activations (head_group); hs < 0: none
+    // Balance split of the last round of blocks (slices > 1; common.hpp): partials
+    // [tail][slices][B] fp32 after the counters.
+    int nwhole, tail, slices;
+    float *partial;
+    int *counters;
+    uint32_t partial_bytes;
 };
 
 constexpr int kQ5DecodeDepth = 2;  // steps in flight a wave
@@ -65,7 +71,11 @@ q5k_decode_kernel(Q5DecodeArgs args) {
     const int G = args.groups;
     const int K = G * 32;
     const uint32_t blocks = (uint32_t)G / 8u;
-    const int steps = (G + GPS - 1) / GPS;
+    // This workgroup's block and its groups [ga, gb): all of K, or slice sl of tail block tb.
+    int blk, ga, gb, tb, sl;
+    balance_block(blockIdx.x, gridDim.x, args.nwhole, args.tail, args.slices, G, blk, ga, gb, tb, sl);
+    const int GS = gb - ga;
+    const int steps = (GS + GPS - 1) / GPS;
 
     // LDS: fifth[256] (the fifth-bit table), xa[K / 8] (16 bytes: 8 activations as staged), xs[G]
     // (group sums), red[waves][GPS][B].
@@ -74,13 +84,14 @@ q5k_decode_kernel(Q5DecodeArgs args) {
     float *xs = (float *)(xa + K / 8);
     float *red = xs + G;
 
-    // 1. This thread's first activation groups (32 values, four 16-byte loads each).
+    // 1. This thread's first activation groups (32 values, four 16-byte loads each): groups
+    // ga + e of this workgroup's range.
     constexpr int kStage = 2;
     u32x4 xin[kStage][4];
 #pragma unroll
     for (int t = 0; t < kStage; ++t) {
         const int e = threadIdx.x + t * kQ5DecodeWg;
-        const u32x4 *src = (const u32x4 *)(args.a + head_group(e < G ? e : 0, args.hs, args.vph) * 32);
+        const u32x4 *src = (const u32x4 *)(args.a + head_group(ga + (e < GS ? e : 0), args.hs, args.vph) * 32);
 #pragma unroll
         for (int j = 0; j < 4; ++j) xin[t][j] = src[j];
     }
@@ -102,14 +113,14 @@ q5k_decode_kernel(Q5DecodeArgs args) {
     const rsrc_t p0_rsrc = make_rsrc(args.plane0, args.p0_bytes);
     const rsrc_t p1_rsrc = make_rsrc(FIFTH ? args.plane1 : args.plane0, FIFTH ? args.p1_bytes : 0u);
     const rsrc_t m_rsrc = make_rsrc(args.meta, args.meta_bytes);
-    const int64_t r0 = (int64_t)xcd_block(blockIdx.x, gridDim.x) * B;
+    const int64_t r0 = (int64_t)blk * B;
     const uint32_t rr = (uint32_t)(r0 & 127) + (uint32_t)row;
     const uint32_t tile = (uint32_t)(r0 >> 7);
     u32x4 c0[D], cm[D];
     uint32_t c1[D] = {};
     auto issue = [&](int slot, int t) {
-        const int g = (wave + kQ5DecodeWaves * t) * GPS + gsub;
-        const bool live = g < G;
+        const int g = ga + (wave + kQ5DecodeWaves * t) * GPS + gsub;
+        const bool live = g < gb;
         const uint32_t gg = live ? (uint32_t)g : 0u;
         const uint32_t rec = (tile * (uint32_t)G + gg) * 128u + rr;
         const uint32_t mrec = (tile * blocks + gg / 8u) * 128u + rr;
@@ -135,13 +146,13 @@ q5k_decode_kernel(Q5DecodeArgs args) {
     }
 #pragma unroll
     for (int t = 0; t < kStage; ++t)
-        if (threadIdx.x + t * kQ5DecodeWg < G) stage(threadIdx.x + t * kQ5DecodeWg, xin[t]);
-    for (int e = threadIdx.x + kStage * kQ5DecodeWg; e < G; e += kQ5DecodeWg) {
-        const u32x4 *src = (const u32x4 *)(args.a + head_group(e, args.hs, args.vph) * 32);
+        if (threadIdx.x + t * kQ5DecodeWg < GS) stage(ga + threadIdx.x + t * kQ5DecodeWg, xin[t]);
+    for (int e = threadIdx.x + kStage * kQ5DecodeWg; e < GS; e += kQ5DecodeWg) {
+        const u32x4 *src = (const u32x4 *)(args.a + head_group(ga + e, args.hs, args.vph) * 32);
         u32x4 v[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) v[j] = src[j];
-        stage(e, v);
+        stage(ga + e, v);
     }
     lds_barrier();  // LDS only: the weight loads stay in flight
 
@@ -154,8 +165,8 @@ q5k_decode_kernel(Q5DecodeArgs args) {
 #pragma unroll
         for (int k = 0; k < D; ++k) {
             const int t = t0 + k;
-            const int g0 = (wave + kQ5DecodeWaves * t) * GPS + gsub;
-            const int g = g0 < G ? g0 : G - 1;  // past K: zero scales, no contribution
+            const int g0 = ga + (wave + kQ5DecodeWaves * t) * GPS + gsub;
+            const int g = g0 < gb ? g0 : gb - 1;  // past the range: zero scales, no contribution
             u32x4 xq[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) xq[j] = xa[g * 4 + j];
@@ -189,7 +200,7 @@ q5k_decode_kernel(Q5DecodeArgs args) {
                     else pa = qdot2(pair[p], xw, pa);
                 }
             }
-            const float live = g0 < G ? 1.0f : 0.0f;
+            const float live = g0 < gb ? 1.0f : 0.0f;
             acc = __builtin_fmaf(ds * live, pa + pb, __builtin_fmaf(-__builtin_fmaf(128.0f, ds, dm) * live, sx, acc));
             issue(k, t + D);
             // Keep the refill here, in the prologue's order (else the scheduler sinks the refills
@@ -201,11 +212,17 @@ q5k_decode_kernel(Q5DecodeArgs args) {
     // 4. The groups of a step and the waves meet in LDS; the workgroup writes its B rows.
     red[(wave * GPS + gsub) * B + row] = acc;
     __syncthreads();
-    if ((int)threadIdx.x < B) {
-        const int64_t nn = r0 + threadIdx.x;
-        float value = 0.0f;
+    const int tid = threadIdx.x;
+    float v[1] = {0.0f};
+    if (tid < B) {
 #pragma unroll
-        for (int p = 0; p < kQ5DecodeWaves * GPS; ++p) value += red[p * B + threadIdx.x];
+        for (int p = 0; p < kQ5DecodeWaves * GPS; ++p) v[0] += red[p * B + tid];
+    }
+    if (tb >= 0 && !balance_merge<1>(v, tid, B, tb, sl, args.slices, args.partial, args.partial_bytes, args.counters))
+        return;  // a slice whose block another slice finishes
+    if (tid < B) {
+        const int64_t nn = r0 + tid;
+        float value = v[0];
         if (nn < args.n) {
             if (args.out_dtype == SPLOSH_F32) {
                 if (args.residual) value += ((const float *)args.residual)[nn];
@@ -236,16 +253,31 @@ static int q5k_decode_cus() {
     return cus;
 }
 
+// Row block: the largest of 32, 16 and 8 that gives at least two workgroups a CU.
+static int q5k_decode_block(int64_t columns) {
+    const int64_t cus = q5k_decode_cus();
+    return columns / 32 >= 2 * cus ? 32 : columns / 16 >= 2 * cus ? 16 : 8;
+}
+
+size_t q5k_decode_workspace_bytes(int64_t rows, int64_t columns, int64_t inner) {
+    if (rows != 1 || columns % 128 != 0 || inner % 256 != 0) return 0;
+    const int block = q5k_decode_block(columns);
+    const BalanceSplit p = plan_balance(columns / block, q5k_decode_cus(), (int)(inner / 32));
+    return p.slices < 2 ? 0 : kBalanceCounterBytes + (size_t)p.tail * p.slices * block * sizeof(float);
+}
+
 template <int B, bool FIFTH>
 static hipError_t launch_q5k_decode_b(const Q5DecodeArgs &args, hipStream_t stream) {
-    hipLaunchKernelGGL((q5k_decode_kernel<B, kQ5DecodeDepth, FIFTH>), dim3((unsigned)(args.n / B)), dim3(kQ5DecodeWg),
+    const unsigned grid = args.slices > 1 ? (unsigned)(args.nwhole + args.tail * args.slices) : (unsigned)(args.n / B);
+    hipLaunchKernelGGL((q5k_decode_kernel<B, kQ5DecodeDepth, FIFTH>), dim3(grid), dim3(kQ5DecodeWg),
                        q5k_decode_lds((int64_t)args.groups * 32, B), stream, args);
     return hipGetLastError();
 }
 
 hipError_t launch_q5k_decode(const splosh_q5k_weight &w, const uint16_t *a, void *out, int out_dtype,
-                             const void *residual, hipStream_t stream, int hs, int vph) {
-    Q5DecodeArgs args;
+                             const void *residual, void *workspace, size_t workspace_bytes, hipStream_t stream, int hs,
+                             int vph) {
+    Q5DecodeArgs args = {};
     args.hs = hs;
     args.vph = vph;
     args.plane0 = w.plane0;
@@ -260,12 +292,23 @@ hipError_t launch_q5k_decode(const splosh_q5k_weight &w, const uint16_t *a, void
     args.p0_bytes = (uint32_t)(w.rows * args.groups * 16);
     args.p1_bytes = w.plane1 ? (uint32_t)(w.rows * args.groups * 4) : 0u;
     args.meta_bytes = (uint32_t)(w.rows * (args.groups / 8) * 16);
-    // Row block: the largest of 32, 16 and 8 that gives at least two workgroups a CU.
-    const int64_t cus = q5k_decode_cus();
+    const int block = q5k_decode_block(w.rows);
+    // The balance split when the workspace holds its partials (else every block whole).
+    const size_t need = q5k_decode_workspace_bytes(1, w.rows, w.inner);
+    args.slices = 1;
+    if (need > 0 && workspace && workspace_bytes >= need) {
+        const BalanceSplit p = plan_balance(w.rows / block, q5k_decode_cus(), args.groups);
+        args.nwhole = p.nwhole;
+        args.tail = p.tail;
+        args.slices = p.slices;
+        args.counters = (int *)workspace;
+        args.partial = (float *)((char *)workspace + kBalanceCounterBytes);
+        args.partial_bytes = (uint32_t)(need - kBalanceCounterBytes);
+    }
     const bool fifth = w.plane1 != nullptr;  // null: Q4_K
-    if (w.rows / 32 >= 2 * cus)
+    if (block == 32)
         return fifth ? launch_q5k_decode_b<32, true>(args, stream) : launch_q5k_decode_b<32, false>(args, stream);
-    if (w.rows / 16 >= 2 * cus)
+    if (block == 16)
         return fifth ? launch_q5k_decode_b<16, true>(args, stream) : launch_q5k_decode_b<16, false>(args, stream);
     return fifth ? launch_q5k_decode_b<8, true>(args, stream) : launch_q5k_decode_b<8, false>(args, stream);
 }

@@ -232,3 +232,26 @@ def test_decode_kernel(rt, n, k):
     out = torch.from_numpy(base.copy()).cuda()
     rt.gemm(w, bf16_tensor(a_bits), out=out, residual=out)
     check_close(out.cpu().numpy(), ref + base, bf16_out=False, tight=True, absref=absref, label="q5k decode residual")
+
+
+@pytest.mark.parametrize("n,k", [(5120, 2048), (5120, 17408), (5248, 1024)])
+def test_decode_balance_split(rt, n, k):
+    """The Q5_K decode kernel with a workspace: on 256 CUs 640 blocks of 8 rows are 512 whole + 128
+    in 2 slices of K, 656 blocks 512 + 144 unsplit (one slice each does not fit the CUs: no
+    split), the partials summed by the last slice in slice order. Against the oracle (K=2048), the same bits on a second call, every
+    arrival counter back at zero, and within rounding of the unsplit kernel (no workspace)."""
+    native = oracle.q45k_random_native(n, k, seed=950 + n + k)
+    w = rt.q5k_repack(dev_u8(native), n, k)
+    a_bits = oracle.bf16_normal((1, k), seed=951)
+    ws = torch.zeros(max(rt.workspace_bytes(1, n, k), 16384), dtype=torch.uint8, device="cuda")
+    empty = torch.empty(0, dtype=torch.uint8, device="cuda")
+    first = rt.gemm(w, bf16_tensor(a_bits), out_dtype=torch.float32, workspace=ws).cpu().numpy()
+    second = rt.gemm(w, bf16_tensor(a_bits), out_dtype=torch.float32, workspace=ws).cpu().numpy()
+    assert np.array_equal(first, second), "calls differ"
+    assert int(ws[:16384].view(torch.int32).abs().sum().item()) == 0, "arrival counters left set"
+    whole = rt.gemm(w, bf16_tensor(a_bits), out_dtype=torch.float32, workspace=empty).cpu().numpy()
+    check_close(first, whole, bf16_out=False, tight=True, label=f"q5k split vs whole {n}x{k}")
+    if k <= 2048:
+        dense = oracle.q45k_decode(native).reshape(n, k)
+        check_close(first, oracle.gemm_a_bf16_w_f32(a_bits, dense), bf16_out=False, tight=True,
+                    absref=abs_gemm(a_bits, dense), label=f"q5k split {n}x{k}")
