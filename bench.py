@@ -34,14 +34,14 @@ BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
 # a plain 256 MiB device copy (FETCH_SIZE reads half the bytes moved, WRITE_SIZE all of them).
 # The readings and commands are in profiles/; calls not listed are unmeasured (None).
 MEASURED_TRAFFIC = {
-    ("verify64", "mlp_in"): 55912.9 * 2 * 1024 + 9871.0 * 1024,  # mma_kernel<Q4Format<2, true, 2, 4, 3, false, false>, 2, 2, 4, 3>
-    ("verify64", "down"): 35308.5 * 2 * 1024 + 4444.6 * 1024,  # mma_kernel<Q4Format<1, true, 2, 4, 3, false, false>, 2, 2, 4, 3>
-    ("decode1", "gemv"): 24603.8 * 2 * 1024 + 75.0 * 1024,  # q4_decode_kernel<1, 1, 32, 2>
-    ("lmhead1", "lm_head"): 349280.3 * 2 * 1024 + 486.2 * 1024,  # q4_decode_kernel<1, 1, 32, 2>
-    ("q5k1", "q5k"): 30124.4 * 2 * 1024 + 30.0 * 1024,  # q5k_decode_kernel<8, 2, true>
-    ("q5k64", "q5k"): 41324.4 * 2 * 1024 + 4383.1 * 1024,  # mma_kernel<Q5Format<2, 4, 3, true>, 2, 2, 4, 3>
-    ("q5k16", "q5k"): 32873.8 * 2 * 1024 + 1082.3 * 1024,  # mma_kernel<Q5Format<2, 4, 3, true>, 1, 2, 4, 3>
-    ("prefill2048", "prefill_up"): 266967.5 * 2 * 1024 + 114688.0 * 1024,  # prefill_kernel<Q4Stage>
+    ("verify64", "mlp_in"): 55922.4 * 2 * 1024 + 9871.0 * 1024,  # mma_kernel<Q4Format<2, true, 2, 4, 3, false, false>, 2, 2, 4, 3>
+    ("verify64", "down"): 35307.0 * 2 * 1024 + 4460.6 * 1024,  # mma_kernel<Q4Format<1, true, 2, 4, 3, false, false>, 2, 2, 4, 3>
+    ("decode1", "gemv"): 24604.2 * 2 * 1024 + 75.0 * 1024,  # q4_decode_kernel<1, 1, 32, 2>
+    ("lmhead1", "lm_head"): 349322.0 * 2 * 1024 + 525.9 * 1024,  # q4_decode_kernel<1, 1, 32, 2>
+    ("q5k1", "q5k"): 30124.5 * 2 * 1024 + 30.0 * 1024,  # q5k_decode_kernel<8, 2, true>
+    ("q5k64", "q5k"): 41299.7 * 2 * 1024 + 4303.0 * 1024,  # mma_kernel<Q5Format<2, 4, 3, true>, 2, 2, 4, 3>
+    ("q5k16", "q5k"): 32869.4 * 2 * 1024 + 1050.0 * 1024,  # mma_kernel<Q5Format<2, 4, 3, true>, 1, 2, 4, 3>
+    ("prefill2048", "prefill_up"): 264791.5 * 2 * 1024 + 114688.0 * 1024,  # prefill_kernel<Q4Stage>
     ("q5k2048", "q5k"): 347729.4 * 2 * 1024 + 98304.0 * 1024,  # prefill_kernel<Q5Stage<true>>
     ("q6k2048", "gguf"): 366940.1 * 2 * 1024 + 110080.0 * 1024,  # prefill_kernel<GgufStage<14>>
     ("q6k64", "gguf"): (51389.6 + 6413.1) * 2 * 1024 + (25600.0 + 643.4) * 1024,  # gguf_tile_kernel<14, 1, 2, true, 2> + gguf_tile_finish<1, 2>
@@ -50,9 +50,9 @@ MEASURED_TRAFFIC = {
     ("iq3s1", "gguf"): 19068.8 * 2 * 1024 + 10.0 * 1024,  # gguf_pairs_kernel<21, 4, 2>
     ("q80_1", "gguf"): 46715.8 * 2 * 1024 + 10.0 * 1024,  # gguf_gemv_kernel<8, 4>
     ("stream50", "read"): 24684.0 * 2 * 1024 + 64.0 * 1024,  # stream_read_kernel (shape 0, the default)
-    ("layerset", "mlp_in"): 55924.8 * 2 * 1024 + 9871.0 * 1024,  # mma_kernel<Q4Format<2, true, 2, 4, 3, false, false>, 2, 2, 4, 3>
-    ("lmhead64", "lm_head"): 355049.4 * 2 * 1024 + 35023.5 * 1024,  # mma_kernel<Q4Format<1, true, 2, 4, 3, false, false>, 2, 2, 4, 3>
-    ("emit64", "fused"): 35951.5 * 2 * 1024 + 5507.6 * 1024,  # mma_kernel<Q4Format<1, true, 2, 4, 3, false, true>, 2, 2, 4, 3>
+    ("layerset", "mlp_in"): 55918.2 * 2 * 1024 + 9871.0 * 1024,  # mma_kernel<Q4Format<2, true, 2, 4, 3, false, false>, 2, 2, 4, 3>
+    ("lmhead64", "lm_head"): 354944.8 * 2 * 1024 + 35023.5 * 1024,  # mma_kernel<Q4Format<1, true, 2, 4, 3, false, false>, 2, 2, 4, 3>
+    ("emit64", "fused"): 35993.7 * 2 * 1024 + 5883.2 * 1024,  # mma_kernel<Q4Format<1, true, 2, 4, 3, false, true>, 2, 2, 4, 3>
 }
 
 
