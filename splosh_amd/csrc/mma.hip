@@ -120,6 +120,7 @@ struct Q4Format {
     static constexpr bool kEmit = EMIT && !GROUPED;  // the epilogue emits the next norm's operand
     static constexpr int kTblBytes = 0;
     __device__ void build_table(char *, int) {}
+    static constexpr bool kPrefetchSide = true;  // single weight: sidecars read at the barrier before
     static constexpr int NW = NW_;
     static constexpr bool kStageSide = TILED;
     static constexpr int kWLoads = kStageSide ? NW : NW * 3;  // weight loads per wave and step
@@ -228,7 +229,18 @@ struct Q4Format {
     // that makes them visible; read by prepare(), which measured faster for q4 than reading them a
     // step early into registers, as Q5Format does: the registers are not to spare here).
     const char *side_buf = nullptr;
-    __device__ void fetch_side(const char *sbuf) { side_buf = sbuf; }
+    // One weight: the lane's scale and bias are read from LDS here, at the barrier a step before
+    // prepare() needs them, so that the LDS latency does not stall the step (as Q5Format does with
+    // its meta records; two weights would need more registers than the gate+up kernel has).
+    uint32_t sb_pre = 0, bb_pre = 0;
+    __device__ void fetch_side(const char *sbuf) {
+        side_buf = sbuf;
+        if constexpr (NW == 1 && kStageSide && kPrefetchSide) {
+            const char *base = sbuf + ((kw * kBandCols + cw * 32 + r) * 2);
+            sb_pre = *(const uint16_t *)base;
+            bb_pre = *(const uint16_t *)(base + KW * kBandCols * 2);
+        }
+    }
     // Coefficients of the step whose codes sit in `slot` (zeros when the step has no group for this
     // wave). The sidecars are read whatever `on` says and then scaled by 0 or 1 (exact), so that the
     // reads of both weights are issued together instead of behind a branch each.
@@ -236,7 +248,10 @@ struct Q4Format {
         uint32_t sb[NW], bb[NW];
 #pragma unroll
         for (int w = 0; w < NW; ++w) {
-            if (kStageSide) {
+            if (NW == 1 && kStageSide && kPrefetchSide) {
+                sb[w] = sb_pre;
+                bb[w] = bb_pre;
+            } else if (kStageSide) {
                 const char *base = side_buf + (((w * 2) * KW + kw) * kBandCols + cw * 32 + r) * 2;
                 sb[w] = *(const uint16_t *)base;
                 bb[w] = *(const uint16_t *)(base + KW * kBandCols * 2);
