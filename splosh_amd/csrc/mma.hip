@@ -120,7 +120,6 @@ struct Q4Format {
     static constexpr bool kEmit = EMIT && !GROUPED;  // the epilogue emits the next norm's operand
     static constexpr int kTblBytes = 0;
     __device__ void build_table(char *, int) {}
-    static constexpr bool kPrefetchSide = true;  // single weight: sidecars read at the barrier before
     static constexpr int NW = NW_;
     static constexpr bool kStageSide = TILED;
     static constexpr int kWLoads = kStageSide ? NW : NW * 3;  // weight loads per wave and step
@@ -235,7 +234,7 @@ struct Q4Format {
     uint32_t sb_pre = 0, bb_pre = 0;
     __device__ void fetch_side(const char *sbuf) {
         side_buf = sbuf;
-        if constexpr (NW == 1 && kStageSide && kPrefetchSide) {
+        if constexpr (NW == 1 && kStageSide) {
             const char *base = sbuf + ((kw * kBandCols + cw * 32 + r) * 2);
             sb_pre = *(const uint16_t *)base;
             bb_pre = *(const uint16_t *)(base + KW * kBandCols * 2);
@@ -248,7 +247,7 @@ struct Q4Format {
         uint32_t sb[NW], bb[NW];
 #pragma unroll
         for (int w = 0; w < NW; ++w) {
-            if (NW == 1 && kStageSide && kPrefetchSide) {
+            if (NW == 1 && kStageSide) {
                 sb[w] = sb_pre;
                 bb[w] = bb_pre;
             } else if (kStageSide) {
