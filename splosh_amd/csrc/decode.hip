@@ -65,7 +65,11 @@ struct DecodeArgs {
 
 
 
-constexpr int kDecodeDepth = 2;  // steps in flight a wave (measured: 2 beats 1, 3, 4, 6 and 8)
+// Steps in flight a wave: 3 for one weight when each CU holds a few blocks (a long, latency-bound
+// loop: K5120 -> N17408 11.0 -> 10.5 us, K17408 -> N5120 16.7 -> 15.3), else 2 (the fused gate+up
+// 18.2 -> 19.6 us and the lm_head, 30 blocks a CU, 101.6 -> 102.5 us at 3; 4 is slower everywhere).
+constexpr int kDecodeDepth = 2, kDecodeDeepDepth = 3;
+constexpr int kDecodeDeepBlocksPerCu = 4;  // the most blocks a CU for the deeper ring
 constexpr int kDecodeWg = 256;   // threads a workgroup
 constexpr int kDecodeWaves = kDecodeWg / 64;
 
@@ -333,7 +337,11 @@ template <int R, int NW, int B>
 static hipError_t launch_decode_v(const DecodeArgs &args, hipStream_t stream) {
     const size_t lds = decode_lds(R, (int64_t)args.groups * kGroup, NW, B);
     const unsigned grid = args.slices > 1 ? (unsigned)(args.nwhole + args.tail * args.slices) : (unsigned)(args.n / B);
-    hipLaunchKernelGGL((q4_decode_kernel<R, NW, B, kDecodeDepth>), dim3(grid), dim3(kDecodeWg), lds, stream, args);
+    if (NW == 1 && args.n / B <= (int64_t)kDecodeDeepBlocksPerCu * decode_cus())
+        hipLaunchKernelGGL((q4_decode_kernel<R, NW, B, kDecodeDeepDepth>), dim3(grid), dim3(kDecodeWg), lds, stream,
+                           args);
+    else
+        hipLaunchKernelGGL((q4_decode_kernel<R, NW, B, kDecodeDepth>), dim3(grid), dim3(kDecodeWg), lds, stream, args);
     return hipGetLastError();
 }
 
