@@ -4,7 +4,7 @@
 // workgroups, keeps it in flight while the arithmetic of the groups already loaded runs, and needs
 // no reduction across workgroups.
 //
-// Mapping. A workgroup owns a block of B output rows (B = 16 or 32, inside one 128-row tile) over
+// Mapping. A workgroup owns a block of B output rows (B = 8, 16 or 32, inside one 128-row tile) over
 // the whole of K: N / B workgroups, several a CU, so the read is spread evenly. In the tiled layout
 // (Model/Retile.swift:135-153) the block's records of one group are B * 32 contiguous bytes. Lane l
 // of a wave takes half h = l & 1 of row (l >> 1) % B of the group (l >> 1) / B of a step of
@@ -308,8 +308,15 @@ static int decode_cus() {
     return cus;
 }
 
-// Row block: 32 rows when that gives at least two workgroups a CU, else 16 (more workgroups).
-static int decode_block(int64_t columns) { return columns / 32 >= 2 * decode_cus() ? 32 : 16; }
+// Row block: 32 rows when that gives at least two workgroups a CU; else 8 for long K (at least 128
+// groups), where 16-row blocks would leave a CU one or two workgroups for a long loop (K17408 ->
+// N5120: 640 blocks of 8 rows with the balance split 13.3 us, 320 of 16 rows 15.4 us); else 16
+// (K5120 -> N5120: 6.5 us at 16 rows, 7.1 at 8).
+static int decode_block(int64_t columns, int64_t groups) {
+    const int64_t cus = decode_cus();
+    if (columns / 32 >= 2 * cus) return 32;
+    return groups >= 128 && columns / 16 < 2 * cus ? 8 : 16;
+}
 
 static size_t decode_lds(int64_t rows, int64_t inner, int nw, int block) {
     return (size_t)rows * inner * 2 + (size_t)rows * (inner / 32) * 4 +
@@ -323,14 +330,15 @@ bool decode_fits(int64_t rows, int64_t columns, int64_t inner, int order) {
 }
 
 static BalanceSplit plan_decode_split(int64_t columns, int groups) {
-    return plan_balance(columns / decode_block(columns), decode_cus(), groups);
+    return plan_balance(columns / decode_block(columns, groups), decode_cus(), groups);
 }
 
 size_t decode_workspace_bytes(int64_t rows, int64_t columns, int64_t inner, int nw) {
     if (rows < 1 || rows > 2 || inner % kGroup != 0 || columns % 128 != 0) return 0;
     const BalanceSplit p = plan_decode_split(columns, (int)(inner / kGroup));
     if (p.slices < 2) return 0;
-    return kBalanceCounterBytes + (size_t)p.tail * p.slices * nw * rows * decode_block(columns) * sizeof(float);
+    return kBalanceCounterBytes +
+           (size_t)p.tail * p.slices * nw * rows * decode_block(columns, inner / kGroup) * sizeof(float);
 }
 
 template <int R, int NW, int B>
@@ -347,7 +355,11 @@ static hipError_t launch_decode_v(const DecodeArgs &args, hipStream_t stream) {
 
 template <int R, int NW>
 static hipError_t launch_decode_rn(const DecodeArgs &args, hipStream_t stream) {
-    return decode_block(args.n) == 32 ? launch_decode_v<R, NW, 32>(args, stream) : launch_decode_v<R, NW, 16>(args, stream);
+    switch (decode_block(args.n, args.groups)) {
+        case 32: return launch_decode_v<R, NW, 32>(args, stream);
+        case 16: return launch_decode_v<R, NW, 16>(args, stream);
+        default: return launch_decode_v<R, NW, 8>(args, stream);
+    }
 }
 
 hipError_t launch_q4_decode(const splosh_q4_weight &w, const splosh_q4_weight *up, const uint16_t *a, int64_t lda,

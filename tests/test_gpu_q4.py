@@ -377,14 +377,15 @@ def test_decode_kernel(rt, rows, mlp, n, k):
 
 @pytest.mark.parametrize("rows", [1, 2])
 @pytest.mark.parametrize("mlp", [False, True])
-@pytest.mark.parametrize("n,k", [(17408, 5120), (17408, 320), (16896, 1024), (5120, 1024)])
+@pytest.mark.parametrize("n,k", [(17408, 5120), (17408, 320), (16896, 1024), (5120, 1024), (5120, 8192)])
 def test_decode_balance_split(rt, rows, mlp, n, k):
     """The decode kernel with a workspace: when the row blocks do not divide evenly over the CUs
     (and every CU holds two whole blocks or more) the last round's blocks are cut into slices of K
     (on 256 CUs: 544 blocks = 512 whole + 32 in 8 slices; K=320, 5 groups: 5 slices; 528 blocks:
-    16 slices of one group; 320 blocks of 16 rows: no split). Against the oracle, the same bits on
-    a second call, every arrival counter back at zero, and within rounding of the unsplit kernel
-    (an empty workspace)."""
+    16 slices of one group; 320 blocks of 16 rows: no split; K=8192 -> N=5120: 640 blocks of 8
+    rows, 512 whole + 128 in 2 slices). Against the oracle, the same bits on a second call, every
+    arrival counter back at zero, and within rounding of the unsplit kernel (an empty
+    workspace)."""
     g, u = Q4Case(n, k, seed=730 + rows), Q4Case(n, k, seed=740 + rows)
     a_bits = oracle.bf16_normal((rows, k), seed=750 + rows)
     need = rt.workspace_bytes(rows, n, k)
