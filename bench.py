@@ -36,9 +36,9 @@ BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
 MEASURED_TRAFFIC = {
     ("verify64", "mlp_in"): 55922.4 * 2 * 1024 + 9871.0 * 1024,  # mma_kernel<Q4Format<2, true, 2, 4, 3, false, false>, 2, 2, 4, 3>
     ("verify64", "down"): 35307.0 * 2 * 1024 + 4460.6 * 1024,  # mma_kernel<Q4Format<1, true, 2, 4, 3, false, false>, 2, 2, 4, 3>
-    ("decode1", "gemv"): 24604.2 * 2 * 1024 + 75.0 * 1024,  # q4_decode_kernel<1, 1, 32, 2>
-    ("lmhead1", "lm_head"): 349322.0 * 2 * 1024 + 525.9 * 1024,  # q4_decode_kernel<1, 1, 32, 2>
-    ("q5k1", "q5k"): 30124.5 * 2 * 1024 + 30.0 * 1024,  # q5k_decode_kernel<8, 2, true>
+    ("decode1", "gemv"): 24607.9 * 2 * 1024 + 75.0 * 1024,  # q4_decode_kernel<1, 1, 32, 3>
+    ("lmhead1", "lm_head"): 349321.9 * 2 * 1024 + 526.2 * 1024,  # q4_decode_kernel<1, 1, 32, 2>
+    ("q5k1", "q5k"): 30124.4 * 2 * 1024 + 30.0 * 1024,  # q5k_decode_kernel<8, 2, true>
     ("q5k64", "q5k"): 41299.7 * 2 * 1024 + 4303.0 * 1024,  # mma_kernel<Q5Format<2, 4, 3, true>, 2, 2, 4, 3>
     ("q5k16", "q5k"): 32869.4 * 2 * 1024 + 1050.0 * 1024,  # mma_kernel<Q5Format<2, 4, 3, true>, 1, 2, 4, 3>
     ("prefill2048", "prefill_up"): 264791.5 * 2 * 1024 + 114688.0 * 1024,  # prefill_kernel<Q4Stage>
