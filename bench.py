@@ -476,7 +476,8 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU's share of the path; --gpus {args.gpus} is not supported "
-              "(the multi-GPU design is sharding along N, described in DESIGN.md)", file=sys.stderr)
+              "(the multi-GPU design shards the weights along N: every GPU streams N / G columns of each "
+              "projection and the outputs are gathered)", file=sys.stderr)
         sys.exit(2)
 
     import torch

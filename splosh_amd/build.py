@@ -23,7 +23,9 @@ PROBE_SOURCES = ["bench/probe.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
-# Packed fp32 instructions are disabled for every device pass (see the build notes in DESIGN.md).
+# Packed fp32 instructions (v_pk_fma_f32 and the like) are disabled for every device pass: the
+# compiler would otherwise form them from ordinary float code, and some of their forms have given
+# wrong results on this hardware without an error.
 DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 COMMON = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Wall", "-Wno-unused-result",
           f"-I{ROOT / 'include'}"]
