@@ -53,12 +53,14 @@ def test_noalloc_matches_workspace_entry_point():
 SCRATCH_BYTES = 16384 + (8 << 20)
 
 
-@pytest.mark.parametrize("rows,n,k", [(100, 1024, 4352), (300, 640, 2048)])
-def test_noalloc_above_64_rows(rows, n, k):
-    """Above 64 rows (the split-K tile kernel at 100 rows, the prefill kernel at 300) the kernels
-    plan against the scratch's size: their partials fit it or the call runs unsplit. The same call
-    through splosh_q4_gemm with a zero-filled workspace of that size gives the same bits; both
-    against the oracle. Run twice, so that the second call sees the scratch the first left."""
+@pytest.mark.parametrize("rows,n,k", [(100, 1024, 4352), (300, 640, 2048), (1, 17408, 1024), (2, 16896, 512)])
+def test_noalloc_planned_against_scratch(rows, n, k):
+    """Every kernel plans against the scratch's size: above 64 rows the split-K tile kernel (100
+    rows) and the prefill kernel (300), whose partials fit it or run unsplit; at one or two rows
+    the decode kernel, whose last round of row blocks is split over K in the scratch (544 and 528
+    blocks on 256 CUs). The same call through splosh_q4_gemm with a zero-filled workspace of that
+    size gives the same bits; both against the oracle. Run twice, so that the second call sees the
+    scratch the first left."""
     from splosh_amd import _lib
     from splosh_amd import runtime as rt
     lib = _lib.lib()
