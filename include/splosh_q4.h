@@ -64,12 +64,14 @@ typedef enum splosh_dtype { SPLOSH_F32 = 0, SPLOSH_BF16 = 1 } splosh_dtype;
 /* Kernel choice (the reference selects kernels through SPLOSH_* environment variables,
  * Runtime/Engine.swift:380-440; here the caller names one, or AUTO picks by rows). */
 typedef enum splosh_kernel {
-    SPLOSH_KERNEL_AUTO = 0,     /* rows <= 2: STREAM; 3..64: DEQUANT; more: PREFILL for tiled
+    SPLOSH_KERNEL_AUTO = 0,     /* rows <= 2 (and 3..4 of tiled weights whose four staged activation
+                                   rows fit 64 KB: K up to about 7600): STREAM; else up to 64:
+                                   DEQUANT; more: PREFILL for tiled
                                    weights with lda % 8 == 0 and ldc % 4 == 0 (one weight at 65..128
                                    rows: TILE up to 80 rows or 8192 columns), else TILE; SCALAR for
                                    operands no other kernel takes */
     SPLOSH_KERNEL_STREAM = 1,   /* weight streaming on raw codes: the every-CU decode kernel for
-                                   1-2 rows of tiled weights (with a workspace it splits the last
+                                   1-4 rows of tiled weights (with a workspace it splits the last
                                    round of row blocks over K, so every CU gets the same share),
                                    the lane-per-row kernel for row-major ones, the raw-code MFMA
                                    kernel for more rows */

@@ -52,7 +52,7 @@ hipError_t launch_q4_lanes(const StreamPlan &plan, const splosh_q4_weight &w, co
                            const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype,
                            const void *residual, int64_t rows, hipStream_t stream);
 
-// The decode kernel on every CU for one or two rows of tiled weights (decode.hip): a workgroup a
+// The decode kernel on every CU for one to four rows of tiled weights (decode.hip): a workgroup a
 // block of 16 or 32 output rows over the whole of K. With a workspace of decode_workspace_bytes
 // (zero: not needed) the last round of blocks is split over K so that every CU gets the same work;
 // without one every block is whole.

@@ -346,13 +346,15 @@ def test_prefill_down_shape_sampled(rt):
 DECODE_SHAPES = [(4096, 4096), (1024, 17408), (17408, 320), (256, 64), (2048, 5120), (16384, 1024)]
 
 
-@pytest.mark.parametrize("rows", [1, 2])
+@pytest.mark.parametrize("rows", [1, 2, 3, 4])
 @pytest.mark.parametrize("mlp", [False, True])
 @pytest.mark.parametrize("n,k", DECODE_SHAPES)
 def test_decode_kernel(rt, rows, mlp, n, k):
-    """The every-CU decode kernel (AUTO for rows <= 2 of tiled weights): a workgroup a block of 16
-    or 32 rows over the whole of K, so two calls give the same bits. The shapes cover both block
-    sizes, a K of one group, K not a multiple of the workgroup's 4 waves x steps, and long K."""
+    """The every-CU decode kernel (AUTO for rows <= 2 of tiled weights, and 3..4 when four staged
+    activation rows fit its LDS; else kernel STREAM falls back to the streaming kernels): a
+    workgroup a block of 8, 16 or 32 rows over the whole of K, so two calls give the same bits.
+    The shapes cover every block size, a K of one group, K not a multiple of the workgroup's 4
+    waves x steps, and long K."""
     g, u = Q4Case(n, k, seed=700 + rows), Q4Case(n, k, seed=710 + rows)
     a_bits = oracle.bf16_normal((rows, k), seed=720 + rows)
     ws = torch.empty(0, dtype=torch.uint8, device="cuda")  # the kernel takes no workspace
@@ -375,7 +377,7 @@ def test_decode_kernel(rt, rows, mlp, n, k):
         check_close(out.cpu().numpy(), ref + base, bf16_out=False, tight=True, label="decode residual")
 
 
-@pytest.mark.parametrize("rows", [1, 2])
+@pytest.mark.parametrize("rows", [1, 2, 3])
 @pytest.mark.parametrize("mlp", [False, True])
 @pytest.mark.parametrize("n,k", [(17408, 5120), (17408, 320), (16896, 1024), (5120, 1024), (5120, 8192)])
 def test_decode_balance_split(rt, rows, mlp, n, k):
