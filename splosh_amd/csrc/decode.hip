@@ -328,10 +328,13 @@ static size_t decode_lds(int64_t rows, int64_t inner, int nw, int block) {
 // 30.0 on the M <= 64 MFMA kernel.
 static int decode_rows(int64_t rows) { return rows <= 2 ? (int)rows : 4; }
 
-// Shapes the kernel takes: tiled weights, 32-bit offsets, staged activations within 64 KB of LDS.
+// LDS a workgroup may take: two workgroups a CU still fit (two rows of K17408: 73 KB).
+constexpr size_t kDecodeMaxLds = 80 * 1024;
+
+// Shapes the kernel takes: tiled weights, 32-bit offsets, staged activations within kDecodeMaxLds.
 bool decode_fits(int64_t rows, int64_t columns, int64_t inner, int order) {
     if (order != SPLOSH_Q4_TILED128 || rows < 1 || rows > 4 || inner % kGroup != 0 || columns % 128 != 0) return false;
-    return decode_lds(decode_rows(rows), inner, 2, 16) <= 64 * 1024 &&
+    return decode_lds(decode_rows(rows), inner, 2, 16) <= kDecodeMaxLds &&
            columns * (inner / kGroup) * 32 < ((int64_t)1 << 32) - 4096;
 }
 
@@ -347,9 +350,24 @@ size_t decode_workspace_bytes(int64_t rows, int64_t columns, int64_t inner, int 
            (size_t)p.tail * p.slices * nw * decode_rows(rows) * decode_block(columns, inner / kGroup) * sizeof(float);
 }
 
+// Raises a kernel's dynamic LDS limit to kDecodeMaxLds once (the default is 64 KB).
+template <int R, int NW, int B, int D>
+static void decode_lds_attribute() {
+    static const bool done = [] {
+        (void)hipFuncSetAttribute((const void *)q4_decode_kernel<R, NW, B, D>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)kDecodeMaxLds);
+        return true;
+    }();
+    (void)done;
+}
+
 template <int R, int NW, int B>
 static hipError_t launch_decode_v(const DecodeArgs &args, hipStream_t stream) {
     const size_t lds = decode_lds(R, (int64_t)args.groups * kGroup, NW, B);
+    if (lds > 64 * 1024) {
+        decode_lds_attribute<R, NW, B, kDecodeDepth>();
+        decode_lds_attribute<R, NW, B, kDecodeDeepDepth>();
+    }
     const unsigned grid = args.slices > 1 ? (unsigned)(args.nwhole + args.tail * args.slices) : (unsigned)(args.n / B);
     if (NW == 1 && args.n / B <= (int64_t)kDecodeDeepBlocksPerCu * decode_cus())
         hipLaunchKernelGGL((q4_decode_kernel<R, NW, B, kDecodeDeepDepth>), dim3(grid), dim3(kDecodeWg), lds, stream,

@@ -350,8 +350,8 @@ DECODE_SHAPES = [(4096, 4096), (1024, 17408), (17408, 320), (256, 64), (2048, 51
 @pytest.mark.parametrize("mlp", [False, True])
 @pytest.mark.parametrize("n,k", DECODE_SHAPES)
 def test_decode_kernel(rt, rows, mlp, n, k):
-    """The every-CU decode kernel (AUTO for rows <= 2 of tiled weights, and 3..4 when four staged
-    activation rows fit its LDS; else kernel STREAM falls back to the streaming kernels): a
+    """The every-CU decode kernel (AUTO for 1..4 rows of tiled weights when the staged activation
+    rows fit its LDS; else kernel STREAM falls back to the streaming kernels): a
     workgroup a block of 8, 16 or 32 rows over the whole of K, so two calls give the same bits.
     The shapes cover every block size, a K of one group, K not a multiple of the workgroup's 4
     waves x steps, and long K."""
