@@ -65,7 +65,7 @@ typedef enum splosh_dtype { SPLOSH_F32 = 0, SPLOSH_BF16 = 1 } splosh_dtype;
  * Runtime/Engine.swift:380-440; here the caller names one, or AUTO picks by rows). */
 typedef enum splosh_kernel {
     SPLOSH_KERNEL_AUTO = 0,     /* 1..4 rows of tiled weights whose staged activation rows fit 80 KB
-                                   (one or two rows up to K of about 18000, four up to about 9600):
+                                   (one or two rows up to K of about 18700, four up to about 9100):
                                    STREAM; else up to 64:
                                    DEQUANT; more: PREFILL for tiled
                                    weights with lda % 8 == 0 and ldc % 4 == 0 (one weight at 65..128
