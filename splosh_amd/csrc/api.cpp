@@ -735,23 +735,18 @@ static int gguf_native_gemm(int gguf_type, const uint8_t *native, int64_t rows, 
     HeadOrder ho;
     if ((st = head_order(key_heads, inner, &ho))) return st;
     // From kGgufPrefillRows rows the 256 x 256 prefill kernel (each weight group decoded once per
-    // 256 rows); above eight rows, or above the format's streaming limit with a workspace for its K
-    // split, the tiled kernel (once per 64 or 128 rows); otherwise one pass of the streaming
-    // kernel (a second above eight). Measured at K17408 -> N5120: the split tiled kernel's time is
-    // flat up to 16 rows (Q8_0, Q6_K, Q3_K 55-58 us, IQ4 46-48, IQ3_S 76), the streaming kernel's
-    // grows with the rows (at five and six: Q8_0 51 / -, Q6_K 47 / 52, Q3_K 48 / 54, IQ4_NL
-    // 44 / 48, IQ4_XS 43 / 48, IQ3_S 48 / 54, 64 at eight). (A development override of the
-    // prefill threshold, read once.)
+    // 256 rows); above eight rows the tiled kernel (once per 64 or 128 rows); otherwise one pass of
+    // the streaming kernel. Measured at K17408 -> N5120 with a workspace, five to eight rows, the
+    // streaming kernel (activations staged in LDS) against the split tiled kernel: Q8_0 38-47 us
+    // against 57, Q6_K 44-56 against 70, Q3_K 43-54 against 64, IQ4_NL 43-53 against 53, IQ4_XS
+    // 42-52 against 57. (A development override of the prefill threshold, read once.)
     static const int64_t prefill_rows = [] {
         const char *e = getenv("SPLOSH_GGUF_PREFILL_ROWS");
         return e ? (int64_t)atoll(e) : kGgufPrefillRows;
     }();
-    const int64_t stream_rows = gguf_type == 21 ? 8 : (gguf_type == 14 || gguf_type == 11) ? 6 : 5;
-    const bool split_room = workspace && workspace_bytes >= splosh::gguf_tile_workspace_bytes(m, rows, inner) &&
-                            splosh::gguf_tile_workspace_bytes(m, rows, inner) > 0;
     const bool prefill = m >= prefill_rows && aligned(out, 16) && (!residual || aligned(residual, 16)) &&
                          splosh::gguf_prefill_fits(gguf_type, m, rows, inner, lda, ldc);
-    const bool tile = !prefill && (m > 8 || (m > stream_rows && split_room)) && splosh::gguf_tile_fits(m, rows, inner, lda);
+    const bool tile = !prefill && m > 8 && splosh::gguf_tile_fits(m, rows, inner, lda);
     // The streaming kernels read the activations through head_group(); the tiled and prefill
     // kernels get a permuted copy.
     if (ho.on() && (prefill || tile)) {

@@ -195,8 +195,12 @@ __device__ __forceinline__ GroupPairs group_pairs(rsrc_t r, uint32_t row, int g,
 
 // The formats above: R weight rows a wave (a workgroup's four waves take 4 R consecutive rows), so
 // each activation row is loaded, paired and summed once for R weight rows; its lanes take the
-// rows' 32-element groups in turn.
-template <int TYPE, int MR, int R>
+// rows' 32-element groups in turn, 64 groups a round.
+// SA (from two activation rows): a round's activations are staged in LDS once for the
+// workgroup's four waves instead of each wave reading them through the texture path (at K17408 ->
+// N5120 and four rows: Q8_0 47.7 -> 35.3 us, Q6_K 50.3 -> 38.2, IQ4_NL 41.3 -> 33.1; at one row
+// the barrier a round cost more than it saved, 0.3 - 3 us).
+template <int TYPE, int MR, int R, bool SA>
 __global__ void __launch_bounds__(256) gguf_pairs_kernel(GgufNativeArgs args) {
     constexpr bool kIq4 = TYPE == 20 || TYPE == 23;
     constexpr float kBias = TYPE == 14 ? 160.0f : TYPE == 11 ? 132.0f : 0.0f;
@@ -224,10 +228,14 @@ __global__ void __launch_bounds__(256) gguf_pairs_kernel(GgufNativeArgs args) {
         __syncthreads();
     }
     const int lane = threadIdx.x & 63;
-    const int64_t n0 =
-        ((int64_t)xcd_block(blockIdx.x, gridDim.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * R;
-    if (n0 >= args.rows) return;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t n0 = ((int64_t)xcd_block(blockIdx.x, gridDim.x) * 4 + wave) * R;
+    // A wave past the last weight row leaves, or with SA stages its share of the activations and
+    // meets the barriers.
+    const bool live = n0 < args.rows;
+    if (!SA && !live) return;
     const int64_t m0 = (int64_t)blockIdx.y * MR;
+    const int mr = (int)(args.m - m0 < MR ? args.m - m0 : MR);  // activation rows of this pass
     const int groups = (int)(args.inner / 32);
     const rsrc_t rs = make_rsrc(args.w, args.w_bytes);
     uint32_t row[R];
@@ -238,20 +246,59 @@ __global__ void __launch_bounds__(256) gguf_pairs_kernel(GgufNativeArgs args) {
     for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int i = 0; i < MR; ++i) acc[r][i] = 0.0f;
-    for (int g = lane; g < groups; g += 64) {
+    // SA: round c's activations, 64 groups of each row (4 KB a row) in buffer c % 2. Wave w loads
+    // groups 16 w .. 16 w + 15 of every row, one 16-byte LDS-DMA a lane (lane l: piece l % 4 of
+    // the 16 w + l / 4th group, as head_group orders them). Piece p of slot j sits at
+    // 4 j + (p ^ (j / 4 % 4)), so that the lanes' 16-byte reads of their own slot, 64 bytes apart,
+    // spread over all banks.
+    __shared__ __align__(16) u32x4 act_lds[SA ? 2 : 1][SA ? MR : 1][SA ? 256 : 1];
+    const int aslot = 16 * wave + (lane >> 2);
+    const uint32_t apiece = (uint32_t)((lane & 3) ^ ((aslot >> 2) & 3));
+    const rsrc_t ars =
+        make_rsrc(args.a + m0 * args.lda, SA ? (uint32_t)(((int64_t)(mr - 1) * args.lda + args.inner) * 2) : 0u);
+    auto stage_act = [&](int c) {
+        const int g = c * 64 + aslot < groups ? c * 64 + aslot : groups - 1;
+        const uint32_t off = (uint32_t)(head_group(g, args.hs, args.vph) * 32 + 8 * apiece) * 2u;
+#pragma unroll
+        for (int i = 0; i < MR; ++i)
+            if (i < mr) buffer_load_lds16(ars, &act_lds[c & 1][i][64 * wave], off + (uint32_t)(i * args.lda * 2));
+    };
+    const int rounds = (groups + 63) / 64;
+    if constexpr (SA) stage_act(0);
+    for (int c = 0; c < rounds; ++c) {
+        if constexpr (SA) {
+            // This wave's loads of round c have landed; past the barrier every wave's have, and
+            // every wave is done with round c - 1, whose buffer round c + 1 then takes.
+            wait_vmcnt<0>();
+            __syncthreads();
+            if (c + 1 < rounds) stage_act(c + 1);
+            asm volatile("" ::: "memory");
+        }
+        const int g = c * 64 + lane;
+        if (!live || g >= groups) continue;
         GroupPairs gp[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) gp[r] = group_pairs<TYPE>(rs, row[r], g, lut);
 #pragma unroll
         for (int i = 0; i < MR; ++i) {
-            if (m0 + i >= args.m) break;
-            const u32x4 *ap =
-                (const u32x4 *)(args.a + (m0 + i) * args.lda + (int64_t)head_group(g, args.hs, args.vph) * 32);
+            if (i >= mr) break;
             uint32_t x[16];
+            if constexpr (SA) {
+                const u32x4 *ap = &act_lds[c & 1][i][4 * lane];
+                const int sw = (lane >> 2) & 3;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const u32x4 v = ap[q];
-                x[4 * q] = v[0], x[4 * q + 1] = v[1], x[4 * q + 2] = v[2], x[4 * q + 3] = v[3];
+                for (int q = 0; q < 4; ++q) {
+                    const u32x4 v = ap[q ^ sw];
+                    x[4 * q] = v[0], x[4 * q + 1] = v[1], x[4 * q + 2] = v[2], x[4 * q + 3] = v[3];
+                }
+            } else {
+                const u32x4 *ap =
+                    (const u32x4 *)(args.a + (m0 + i) * args.lda + (int64_t)head_group(g, args.hs, args.vph) * 32);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const u32x4 v = ap[q];
+                    x[4 * q] = v[0], x[4 * q + 1] = v[1], x[4 * q + 2] = v[2], x[4 * q + 3] = v[3];
+                }
             }
             if constexpr (kIq4) {
                 // Elements 4 q + e and 16 + 4 q + e: the low (e even) or high halves of dwords
@@ -297,7 +344,7 @@ __global__ void __launch_bounds__(256) gguf_pairs_kernel(GgufNativeArgs args) {
 #pragma unroll
             for (int o = 32; o >= 1; o >>= 1) acc[r][i] += __shfl_xor(acc[r][i], o, 64);
         }
-    if (lane != 0) return;
+    if (!live || lane != 0) return;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         if (n0 + r >= args.rows) break;
@@ -455,29 +502,36 @@ hipError_t launch_gguf_embed(int type, const uint8_t *w, int64_t rows, int64_t i
 #endif
 constexpr int kPairsRows = GGUF_PAIRS_R;  // weight rows a wave of gguf_pairs_kernel
 
+template <int MR, bool SA>
+static void launch_pairs(int type, const GgufNativeArgs &args, dim3 grid, hipStream_t stream) {
+    constexpr int R = kPairsRows;
+    switch (type) {
+        case 8: hipLaunchKernelGGL((gguf_pairs_kernel<8, MR, R, SA>), grid, dim3(256), 0, stream, args); break;
+        case 20: hipLaunchKernelGGL((gguf_pairs_kernel<20, MR, R, SA>), grid, dim3(256), 0, stream, args); break;
+        case 14: hipLaunchKernelGGL((gguf_pairs_kernel<14, MR, R, SA>), grid, dim3(256), 0, stream, args); break;
+        case 11: hipLaunchKernelGGL((gguf_pairs_kernel<11, MR, R, SA>), grid, dim3(256), 0, stream, args); break;
+        case 21: hipLaunchKernelGGL((gguf_pairs_kernel<21, MR, R, SA>), grid, dim3(256), 0, stream, args); break;
+        default: hipLaunchKernelGGL((gguf_pairs_kernel<23, MR, R, SA>), grid, dim3(256), 0, stream, args); break;
+    }
+}
+
 template <int MR>
 static void launch_gemv_mr(int type, const GgufNativeArgs &args, hipStream_t stream) {
     constexpr int R = kPairsRows;
     const dim3 grid((unsigned)((args.rows + 4 * R - 1) / (4 * R)), (unsigned)((args.m + MR - 1) / MR));
-    switch (type) {
-        case 8:
-            // One activation row: the fp32 decode measured 1-2 us faster (23.7 against 25.3 at
-            // K17408 -> N5120); from two rows the pairs share the activations (four: 56 -> 43 us).
-            if constexpr (MR == 4) {
-                if (args.m == 1) {
-                    hipLaunchKernelGGL((gguf_gemv_kernel<8, MR>), dim3((unsigned)((args.rows + 3) / 4), grid.y),
-                                       dim3(256), 0, stream, args);
-                    break;
-                }
-            }
-            hipLaunchKernelGGL((gguf_pairs_kernel<8, MR, R>), grid, dim3(256), 0, stream, args);
-            break;
-        case 20: hipLaunchKernelGGL((gguf_pairs_kernel<20, MR, R>), grid, dim3(256), 0, stream, args); break;
-        case 14: hipLaunchKernelGGL((gguf_pairs_kernel<14, MR, R>), grid, dim3(256), 0, stream, args); break;
-        case 11: hipLaunchKernelGGL((gguf_pairs_kernel<11, MR, R>), grid, dim3(256), 0, stream, args); break;
-        case 21: hipLaunchKernelGGL((gguf_pairs_kernel<21, MR, R>), grid, dim3(256), 0, stream, args); break;
-        default: hipLaunchKernelGGL((gguf_pairs_kernel<23, MR, R>), grid, dim3(256), 0, stream, args); break;
+    if constexpr (MR == 4) {
+        if (args.m == 1) {
+            // One activation row: for Q8_0 the fp32 decode measured 1-2 us faster (23.7 against
+            // 25.3 at K17408 -> N5120); from two rows the pairs share the activations.
+            if (type == 8)
+                hipLaunchKernelGGL((gguf_gemv_kernel<8, MR>), dim3((unsigned)((args.rows + 3) / 4), grid.y),
+                                   dim3(256), 0, stream, args);
+            else
+                launch_pairs<MR, false>(type, args, grid, stream);
+            return;
+        }
     }
+    launch_pairs<MR, true>(type, args, grid, stream);
 }
 
 // One 16-byte piece (8 activations) a thread: piece p of row m comes from group head_group(p / 4).

@@ -65,7 +65,7 @@ def test_heads_gemm_planes(m, fifth):
     assert np.abs(got - plain).max() > 1e-3 * np.abs(plain).max()
 
 
-@pytest.mark.parametrize("gtype,m", [(14, 1), (14, 4), (8, 1), (8, 5), (14, 16), (8, 16), (14, 256)])
+@pytest.mark.parametrize("gtype,m", [(14, 1), (14, 4), (8, 1), (8, 5), (11, 7), (21, 2), (14, 16), (8, 16), (14, 256)])
 def test_heads_gemm_native(gtype, m):
     """The same for native blocks: the streaming kernels read the activations in head order
     directly, the tiled (16 rows) and prefill (256 rows) kernels get the permuted copy."""

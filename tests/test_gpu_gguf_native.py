@@ -62,14 +62,15 @@ def test_native_gemm(rt, name, rows):
 
 @pytest.mark.parametrize("name", list(TYPES))
 @pytest.mark.parametrize("rows", [2, 5, 6, 7, 8])
-def test_two_to_eight_rows_both_routes(rt, name, rows):
-    """2-8 activation rows: with a workspace AUTO's choice (the split tiled kernel above the
-    format's streaming limit -- Q8_0, IQ4_NL and IQ4_XS 5, Q6_K and Q3_K 6, IQ3_S 8 -- the streaming
-    kernel up to it), without one a single eight-row pass of the streaming kernel; both against the
-    oracle. Two rows take the streaming kernel's pairs form at four rows a pass."""
+@pytest.mark.parametrize("n,k", [(200, 1536), (203, 4352)])
+def test_two_to_eight_rows_streaming(rt, name, rows, n, k):
+    """2-8 activation rows take one pass of the streaming kernel (four rows a pass up to four,
+    eight above), its activations staged in LDS for a workgroup's four waves, with and without a
+    workspace, against the oracle. 203 weight rows leave waves past the last row, which still
+    stage their share and meet the barriers; K4352 gives three rounds of 64 groups, the last
+    partial."""
     t = TYPES[name]
-    n, k = 200, 1536
-    w, dense = _weight(rt, t, n, k, seed=rows + 3 * t)
+    w, dense = _weight(rt, t, n, k, seed=rows + 3 * t + n)
     a_bits = oracle.bf16_normal((rows, k), seed=rows + 11)
     ref = oracle.gemm_a_bf16_w_f32(a_bits, dense)
     absref = abs_gemm(a_bits, dense)
@@ -77,7 +78,7 @@ def test_two_to_eight_rows_both_routes(rt, name, rows):
     for ws in (None, torch.empty(0, dtype=torch.uint8, device="cuda")):
         got = rt.gemm(w, a, out_dtype=torch.float32, workspace=ws)
         check_close(got.cpu().numpy(), ref, bf16_out=False, tight=True, absref=absref,
-                    label=f"{name} rows={rows} workspace={'none' if ws is not None else 'fresh'}")
+                    label=f"{name} rows={rows} n={n} k={k} workspace={'none' if ws is not None else 'fresh'}")
 
 
 @pytest.mark.parametrize("name", ["q6K", "q8_0"])
@@ -99,9 +100,9 @@ def test_config0_size_sampled(rt, name):
 
 
 @pytest.mark.parametrize("name", ["q6K", "q3K"])
-@pytest.mark.parametrize("rows", [2, 4, 6])
+@pytest.mark.parametrize("rows", [2, 4, 6, 8])
 def test_streaming_long_k_sampled(rt, name, rows):
-    """Q6_K and Q3_K at K=17408 -> N=5120 through the streaming kernel (AUTO up to six rows): its
+    """Q6_K and Q3_K at K=17408 -> N=5120 through the streaming kernel (AUTO up to eight rows): its
     pairs form sums the unsigned codes and takes the bias off once a group, so the cancellation
     grows with K; 256 sampled columns against the oracle at the tight tolerance."""
     t = TYPES[name]
