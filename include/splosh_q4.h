@@ -298,9 +298,8 @@ int splosh_q4k_dequant(const splosh_q5k_weight *w, float *out, hipStream_t strea
  * for these formats (Engine.swift:1673-1694 dispatching sp_gguf_* by format,
  * engine_gguf.metal:332-349) and GgufTensorType.decode (GgufQuant.swift:136-159).
  *
- * splosh_gguf_gemm: out[m][n] = sum_k a[m][k] w[n][k] (+ residual). Up to a few activation rows
- * (Q8_0 and IQ4 5, Q6_K and Q3_K 6, IQ3_S 8; 8 without a workspace) a streaming kernel reads the
- * weight once; more rows (inner % 64 == 0) go to an LDS-tiled MFMA kernel that decodes each
+ * splosh_gguf_gemm: out[m][n] = sum_k a[m][k] w[n][k] (+ residual). Up to eight activation rows
+ * a streaming kernel reads the weight once; more rows (inner % 64 == 0) go to an LDS-tiled MFMA kernel that decodes each
  * weight group once per 64 or 128 activation rows, and from 256 rows (rows % 128 == 0,
  * ldc % 4 == 0, 16-byte aligned outputs) to the 256 x 256 prefill
  * kernel, once per 256. Both split K over workgroups when their tiles are few and a workspace of
