@@ -7,13 +7,16 @@
 //
 //  * gguf_dequant_kernel: one thread a 32-element group, the reference decoder's fp32 operations
 //    in its order (bit-exact).
-//  * gguf_gemv_kernel (Q8_0 at one row) and gguf_pairs_kernel (the rest): out[m][n] = sum_k a[m][k] w[n][k]
-//    for a few rows of activations. A wave owns one weight row (gguf_pairs_kernel: two); its lanes
-//    take the rows' 32-element groups in turn. Q8_0 decodes each group into registers exactly as
-//    the dequant kernel does and accumulates it in fp32; the other formats form exact bf16 weight
-//    pairs without fp32 arithmetic (group_pairs) and sum with v_dot2. Up to MR activation rows
-//    (4, or 8 above four rows) a pass; the partial sums meet in a shuffle tree; further rows take
-//    further passes over the weight (grid.y).
+//  * gguf_pairs_kernel: out[m][n] = sum_k a[m][k] w[n][k] for a few rows of activations. A wave
+//    owns two weight rows; its lanes take the rows' 32-element groups in turn, 64 a round. Each
+//    format forms exact bf16 weight pairs without fp32 arithmetic (group_pairs) and sums with
+//    v_dot2. The activations come from LDS, staged once per workgroup (a round at a time from two
+//    rows, the whole row for Q8_0 at one), or, for the other formats at one row, from memory. Up
+//    to MR activation rows (4, or 8 above four rows) a pass; the partial sums meet in a shuffle
+//    tree; further rows take further passes over the weight (grid.y).
+//  * gguf_gemv_kernel: Q8_0 at one row when the row does not fit the LDS (K > 32768): a wave
+//    owns one weight row, decodes each group into registers exactly as the dequant kernel does
+//    and accumulates it in fp32.
 //
 // Blocks are 2-byte aligned at best (Q8_0: 34 bytes, Q6_K: 210): a run of bytes is read as the
 // dword-aligned window that covers it, in 16-byte loads, and shifted into place per lane.
@@ -196,11 +199,12 @@ __device__ __forceinline__ GroupPairs group_pairs(rsrc_t r, uint32_t row, int g,
 // The formats above: R weight rows a wave (a workgroup's four waves take 4 R consecutive rows), so
 // each activation row is loaded, paired and summed once for R weight rows; its lanes take the
 // rows' 32-element groups in turn, 64 groups a round.
-// SA (from two activation rows): a round's activations are staged in LDS once for the
+// SA = 1 (from two activation rows): a round's activations are staged in LDS once for the
 // workgroup's four waves instead of each wave reading them through the texture path (at K17408 ->
 // N5120 and four rows: Q8_0 47.7 -> 35.3 us, Q6_K 50.3 -> 38.2, IQ4_NL 41.3 -> 33.1; at one row
-// the barrier a round cost more than it saved, 0.3 - 3 us).
-template <int TYPE, int MR, int R, bool SA>
+// the barrier a round cost more than it saved, 0.3 - 3 us). SA = 2 (Q8_0 at one row): the whole
+// activation row staged once. SA = 0: each lane reads its group's activations from memory.
+template <int TYPE, int MR, int R, int SA>
 __global__ void __launch_bounds__(256) gguf_pairs_kernel(GgufNativeArgs args) {
     constexpr bool kIq4 = TYPE == 20 || TYPE == 23;
     constexpr float kBias = TYPE == 14 ? 160.0f : TYPE == 11 ? 132.0f : 0.0f;
@@ -233,7 +237,7 @@ __global__ void __launch_bounds__(256) gguf_pairs_kernel(GgufNativeArgs args) {
     // A wave past the last weight row leaves, or with SA stages its share of the activations and
     // meets the barriers.
     const bool live = n0 < args.rows;
-    if (!SA && !live) return;
+    if (SA == 0 && !live) return;
     const int64_t m0 = (int64_t)blockIdx.y * MR;
     const int mr = (int)(args.m - m0 < MR ? args.m - m0 : MR);  // activation rows of this pass
     const int groups = (int)(args.inner / 32);
@@ -251,11 +255,14 @@ __global__ void __launch_bounds__(256) gguf_pairs_kernel(GgufNativeArgs args) {
     // the 16 w + l / 4th group, as head_group orders them). Piece p of slot j sits at
     // 4 j + (p ^ (j / 4 % 4)), so that the lanes' 16-byte reads of their own slot, 64 bytes apart,
     // spread over all banks.
-    __shared__ __align__(16) u32x4 act_lds[SA ? 2 : 1][SA ? MR : 1][SA ? 256 : 1];
+    __shared__ __align__(16) u32x4 act_lds[SA == 1 ? 2 : 1][SA == 1 ? MR : 1][SA == 1 ? 256 : 1];
+    // SA == 2: every activation row whole, in the same swizzled form (group j of row i at
+    // 4 (i groups + j)), staged once before the first round: one barrier for the call.
+    extern __shared__ __align__(16) u32x4 act_all[];
     const int aslot = 16 * wave + (lane >> 2);
     const uint32_t apiece = (uint32_t)((lane & 3) ^ ((aslot >> 2) & 3));
     const rsrc_t ars =
-        make_rsrc(args.a + m0 * args.lda, SA ? (uint32_t)(((int64_t)(mr - 1) * args.lda + args.inner) * 2) : 0u);
+        make_rsrc(args.a + m0 * args.lda, SA != 0 ? (uint32_t)(((int64_t)(mr - 1) * args.lda + args.inner) * 2) : 0u);
     auto stage_act = [&](int c) {
         const int g = c * 64 + aslot < groups ? c * 64 + aslot : groups - 1;
         const uint32_t off = (uint32_t)(head_group(g, args.hs, args.vph) * 32 + 8 * apiece) * 2u;
@@ -264,9 +271,22 @@ __global__ void __launch_bounds__(256) gguf_pairs_kernel(GgufNativeArgs args) {
             if (i < mr) buffer_load_lds16(ars, &act_lds[c & 1][i][64 * wave], off + (uint32_t)(i * args.lda * 2));
     };
     const int rounds = (groups + 63) / 64;
-    if constexpr (SA) stage_act(0);
+    if constexpr (SA == 1) stage_act(0);
+    if constexpr (SA == 2) {
+        const int total = mr * groups * 4;  // 16-byte pieces; the buffer is rounded up to 256 of them
+        for (int base = 64 * wave; base < total; base += 256) {
+            const int l = base + lane < total ? base + lane : total - 1;
+            const int i = l / (groups * 4), j = (l >> 2) - i * groups;
+            const uint32_t p = (uint32_t)((l & 3) ^ ((j >> 2) & 3));
+            const uint32_t off = (uint32_t)((int64_t)i * args.lda + head_group(j, args.hs, args.vph) * 32 + 8 * p) * 2u;
+            buffer_load_lds16(ars, &act_all[base], off);
+        }
+        wait_vmcnt<0>();
+        __syncthreads();
+        if (!live) return;
+    }
     for (int c = 0; c < rounds; ++c) {
-        if constexpr (SA) {
+        if constexpr (SA == 1) {
             // This wave's loads of round c have landed; past the barrier every wave's have, and
             // every wave is done with round c - 1, whose buffer round c + 1 then takes.
             wait_vmcnt<0>();
@@ -283,8 +303,8 @@ __global__ void __launch_bounds__(256) gguf_pairs_kernel(GgufNativeArgs args) {
         for (int i = 0; i < MR; ++i) {
             if (i >= mr) break;
             uint32_t x[16];
-            if constexpr (SA) {
-                const u32x4 *ap = &act_lds[c & 1][i][4 * lane];
+            if constexpr (SA != 0) {
+                const u32x4 *ap = SA == 1 ? &act_lds[c & 1][i][4 * lane] : &act_all[4 * (i * groups + g)];
                 const int sw = (lane >> 2) & 3;
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
@@ -502,16 +522,16 @@ hipError_t launch_gguf_embed(int type, const uint8_t *w, int64_t rows, int64_t i
 #endif
 constexpr int kPairsRows = GGUF_PAIRS_R;  // weight rows a wave of gguf_pairs_kernel
 
-template <int MR, bool SA>
-static void launch_pairs(int type, const GgufNativeArgs &args, dim3 grid, hipStream_t stream) {
+template <int MR, int SA>
+static void launch_pairs(int type, const GgufNativeArgs &args, dim3 grid, size_t lds, hipStream_t stream) {
     constexpr int R = kPairsRows;
     switch (type) {
-        case 8: hipLaunchKernelGGL((gguf_pairs_kernel<8, MR, R, SA>), grid, dim3(256), 0, stream, args); break;
-        case 20: hipLaunchKernelGGL((gguf_pairs_kernel<20, MR, R, SA>), grid, dim3(256), 0, stream, args); break;
-        case 14: hipLaunchKernelGGL((gguf_pairs_kernel<14, MR, R, SA>), grid, dim3(256), 0, stream, args); break;
-        case 11: hipLaunchKernelGGL((gguf_pairs_kernel<11, MR, R, SA>), grid, dim3(256), 0, stream, args); break;
-        case 21: hipLaunchKernelGGL((gguf_pairs_kernel<21, MR, R, SA>), grid, dim3(256), 0, stream, args); break;
-        default: hipLaunchKernelGGL((gguf_pairs_kernel<23, MR, R, SA>), grid, dim3(256), 0, stream, args); break;
+        case 8: hipLaunchKernelGGL((gguf_pairs_kernel<8, MR, R, SA>), grid, dim3(256), lds, stream, args); break;
+        case 20: hipLaunchKernelGGL((gguf_pairs_kernel<20, MR, R, SA>), grid, dim3(256), lds, stream, args); break;
+        case 14: hipLaunchKernelGGL((gguf_pairs_kernel<14, MR, R, SA>), grid, dim3(256), lds, stream, args); break;
+        case 11: hipLaunchKernelGGL((gguf_pairs_kernel<11, MR, R, SA>), grid, dim3(256), lds, stream, args); break;
+        case 21: hipLaunchKernelGGL((gguf_pairs_kernel<21, MR, R, SA>), grid, dim3(256), lds, stream, args); break;
+        default: hipLaunchKernelGGL((gguf_pairs_kernel<23, MR, R, SA>), grid, dim3(256), lds, stream, args); break;
     }
 }
 
@@ -521,17 +541,23 @@ static void launch_gemv_mr(int type, const GgufNativeArgs &args, hipStream_t str
     const dim3 grid((unsigned)((args.rows + 4 * R - 1) / (4 * R)), (unsigned)((args.m + MR - 1) / MR));
     if constexpr (MR == 4) {
         if (args.m == 1) {
-            // One activation row: for Q8_0 the fp32 decode measured 1-2 us faster (23.7 against
-            // 25.3 at K17408 -> N5120); from two rows the pairs share the activations.
-            if (type == 8)
+            // One activation row. Q8_0 stages the whole row in LDS (up to 64 KB: K <= 32768) and
+            // takes the pairs form: 26.3 -> 22.9 us at K17408 -> N5120, 30.3 -> 24.9 at K5120 ->
+            // N17408, against its fp32 decode reading the activations from memory (which still
+            // serves longer rows). For the other formats the whole-row staging measured slower
+            // (IQ4_XS 17.3 -> 20.3 us, Q3_K 21.7 -> 23.5), and they read the activations directly.
+            const size_t whole = (size_t)((args.inner / 32 * 4 + 255) / 256 * 256) * 16;
+            if (type == 8 && whole <= 65536)
+                hipLaunchKernelGGL((gguf_pairs_kernel<8, MR, R, 2>), grid, dim3(256), whole, stream, args);
+            else if (type == 8)
                 hipLaunchKernelGGL((gguf_gemv_kernel<8, MR>), dim3((unsigned)((args.rows + 3) / 4), grid.y),
                                    dim3(256), 0, stream, args);
             else
-                launch_pairs<MR, false>(type, args, grid, stream);
+                launch_pairs<MR, 0>(type, args, grid, 0, stream);
             return;
         }
     }
-    launch_pairs<MR, true>(type, args, grid, stream);
+    launch_pairs<MR, 1>(type, args, grid, 0, stream);
 }
 
 // One 16-byte piece (8 activations) a thread: piece p of row m comes from group head_group(p / 4).

@@ -81,6 +81,18 @@ def test_two_to_eight_rows_streaming(rt, name, rows, n, k):
                     label=f"{name} rows={rows} n={n} k={k} workspace={'none' if ws is not None else 'fresh'}")
 
 
+def test_q8_0_one_row_long_k(rt):
+    """Q8_0 at one row with K = 33792, past the 32768 whose activation row fits the LDS: the fp32
+    decode kernel reading the activations from memory, against the oracle."""
+    t = TYPES["q8_0"]
+    n, k = 72, 33792
+    w, dense = _weight(rt, t, n, k, seed=71)
+    a_bits = oracle.bf16_normal((1, k), seed=72)
+    got = rt.gemm(w, bf16_tensor(a_bits), out_dtype=torch.float32).cpu().numpy()
+    check_close(got, oracle.gemm_a_bf16_w_f32(a_bits, dense), bf16_out=False, tight=True,
+                absref=abs_gemm(a_bits, dense), label="q8_0 K33792 one row")
+
+
 @pytest.mark.parametrize("name", ["q6K", "q8_0"])
 def test_config0_size_sampled(rt, name):
     """K=5120 -> N=17408 at one row, 256 sampled output columns against the oracle."""
