@@ -48,7 +48,9 @@ MEASURED_TRAFFIC = {
     ("q6k1", "gguf"): 36191.3 * 2 * 1024 + 10.0 * 1024,  # gguf_pairs_kernel<14, 4, 2>
     ("q3k1", "gguf"): 19009.8 * 2 * 1024 + 10.0 * 1024,  # gguf_pairs_kernel<11, 4, 2>
     ("iq3s1", "gguf"): 19068.8 * 2 * 1024 + 10.0 * 1024,  # gguf_pairs_kernel<21, 4, 2>
-    ("q80_1", "gguf"): 46715.8 * 2 * 1024 + 10.0 * 1024,  # gguf_gemv_kernel<8, 4>
+    ("q80_1", "gguf"): 46754.4 * 2 * 1024 + 10.0 * 1024,  # gguf_pairs_kernel<8, 4, 2, 2>
+    ("q80_4", "gguf"): 47196.6 * 2 * 1024 + 40.0 * 1024,  # gguf_pairs_kernel<8, 4, 2, 1>
+    ("q6k4", "gguf"): 36625.1 * 2 * 1024 + 40.0 * 1024,  # gguf_pairs_kernel<14, 4, 2, 1>
     ("stream50", "read"): 24684.0 * 2 * 1024 + 64.0 * 1024,  # stream_read_kernel (shape 0, the default)
     ("layerset", "mlp_in"): 55918.2 * 2 * 1024 + 9871.0 * 1024,  # mma_kernel<Q4Format<2, true, 2, 4, 3, false, false>, 2, 2, 4, 3>
     ("lmhead64", "lm_head"): 354944.8 * 2 * 1024 + 35023.5 * 1024,  # mma_kernel<Q4Format<1, true, 2, 4, 3, false, false>, 2, 2, 4, 3>
