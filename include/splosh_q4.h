@@ -298,13 +298,16 @@ int splosh_q4k_dequant(const splosh_q5k_weight *w, float *out, hipStream_t strea
  * for these formats (Engine.swift:1673-1694 dispatching sp_gguf_* by format,
  * engine_gguf.metal:332-349) and GgufTensorType.decode (GgufQuant.swift:136-159).
  *
- * splosh_gguf_gemm: out[m][n] = sum_k a[m][k] w[n][k] (+ residual). Up to eight activation rows
- * a streaming kernel reads the weight once; more rows (inner % 64 == 0) go to an LDS-tiled MFMA kernel that decodes each
- * weight group once per 64 or 128 activation rows, and from 256 rows (rows % 128 == 0,
- * ldc % 4 == 0, 16-byte aligned outputs) to the 256 x 256 prefill
- * kernel, once per 256. Both split K over workgroups when their tiles are few and a workspace of
- * splosh_workspace_bytes(m, rows, inner) is given (zero-filled before first use; the kernels leave
- * their counters zeroed, so one workspace serves every later call; null: no split).
+ * splosh_gguf_gemm: out[m][n] = sum_k a[m][k] w[n][k] (+ residual). Up to a few activation rows
+ * (IQ4_NL 3, Q3_K 6, the others 4) a streaming kernel reads the weight once. Up to 64 rows
+ * (inner % 256 == 0) the stream-K MFMA kernel of splosh_q4_gemm decodes each weight group once
+ * (where it does not fit, the streaming kernel serves up to eight rows). Above that an LDS-tiled
+ * MFMA kernel (inner % 64 == 0) decodes each weight group once per 64 or 128 activation rows. From 256
+ * rows (rows % 128 == 0, ldc % 4 == 0, 16-byte aligned outputs) the 256 x 256 prefill kernel
+ * decodes each group once per 256 rows. The MFMA kernels split K over workgroups when their work
+ * is uneven or their tiles few and a workspace of splosh_workspace_bytes(m, rows, inner) is given
+ * (zero-filled before first use; the kernels leave their counters zeroed, so one workspace serves
+ * every later call; null: no split).
  * splosh_gguf_dequant: the weight as fp32 [rows][inner], bit-exact with the reference decoder.
  * `native` must be 4-byte aligned (GGUF tensor data is 32-byte aligned).
  * Unsupported types return SPLOSH_ERR_UNSUPPORTED. */

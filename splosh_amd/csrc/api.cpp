@@ -735,21 +735,26 @@ static int gguf_native_gemm(int gguf_type, const uint8_t *native, int64_t rows, 
     HeadOrder ho;
     if ((st = head_order(key_heads, inner, &ho))) return st;
     // From kGgufPrefillRows rows the 256 x 256 prefill kernel (each weight group decoded once per
-    // 256 rows); above eight rows the tiled kernel (once per 64 or 128 rows); otherwise one pass of
-    // the streaming kernel. Measured at K17408 -> N5120 with a workspace, five to eight rows, the
-    // streaming kernel (activations staged in LDS) against the split tiled kernel: Q8_0 38-47 us
-    // against 57, Q6_K 44-56 against 70, Q3_K 43-54 against 64, IQ4_NL 43-53 against 53, IQ4_XS
-    // 42-52 against 57. (A development override of the prefill threshold, read once.)
+    // 256 rows). Up to 64 rows the stream-K MFMA kernel (each weight group decoded once), above
+    // the format's streaming limit; up to it one pass of the streaming kernel. Measured at K17408
+    // -> N5120 with a workspace (us): the MFMA kernel is flat up to 32 rows (Q8_0 33, Q6_K 44, Q3_K
+    // 47, IQ3_S 42, IQ4_NL 27, IQ4_XS 30); the streaming kernel at four rows Q8_0 31, Q6_K 35, Q3_K
+    // 32, IQ3_S 31, IQ4_NL 29, IQ4_XS 29, at five Q6_K 45, Q3_K 43, IQ3_S 43, at six Q3_K 47, at
+    // three IQ4_NL 26. Where the MFMA kernel does not fit (K % 256 != 0), the streaming kernel
+    // serves up to eight rows and the LDS-tiled kernel above. (A development override of the
+    // prefill threshold, read once.)
     static const int64_t prefill_rows = [] {
         const char *e = getenv("SPLOSH_GGUF_PREFILL_ROWS");
         return e ? (int64_t)atoll(e) : kGgufPrefillRows;
     }();
     const bool prefill = m >= prefill_rows && aligned(out, 16) && (!residual || aligned(residual, 16)) &&
                          splosh::gguf_prefill_fits(gguf_type, m, rows, inner, lda, ldc);
-    const bool tile = !prefill && m > 8 && splosh::gguf_tile_fits(m, rows, inner, lda);
-    // The streaming kernels read the activations through head_group(); the tiled and prefill
-    // kernels get a permuted copy.
-    if (ho.on() && (prefill || tile)) {
+    const int64_t stream_max = gguf_type == 11 ? 6 : gguf_type == 20 ? 3 : 4;
+    const bool mma = !prefill && m > stream_max && splosh::gguf_mma_fits(gguf_type, m, rows, inner, lda);
+    const bool tile = !prefill && !mma && m > 8 && splosh::gguf_tile_fits(m, rows, inner, lda);
+    // The streaming kernels read the activations through head_group(); the other kernels get a
+    // permuted copy.
+    if (ho.on() && (prefill || mma || tile)) {
         if ((st = head_copy(ho, &a, &lda, m, inner, workspace, &workspace_bytes, stream))) return st;
         if (workspace_bytes == 0) workspace = nullptr;
     }
@@ -758,6 +763,13 @@ static int gguf_native_gemm(int gguf_type, const uint8_t *native, int64_t rows, 
         return hip_status(splosh::launch_gguf_prefill(plan, gguf_type, native, rows, inner, a, lda, out, ldc, out_dtype,
                                                       residual, m, workspace, stream),
                           "gguf prefill launch");
+    }
+    if (mma) {
+        const splosh::MmaPlan plan =
+            splosh::plan_mma(m, rows, inner / 256, false, workspace ? workspace_bytes : 0, 256);
+        return hip_status(splosh::launch_gguf_mma(plan, gguf_type, native, rows, inner, a, lda, out, ldc, out_dtype,
+                                                  residual, m, workspace, stream),
+                          "gguf mma launch");
     }
     if (tile)
         return hip_status(splosh::launch_gguf_tile(gguf_type, native, nullptr, nullptr, rows, inner, a, lda, out, ldc,

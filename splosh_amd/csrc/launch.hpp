@@ -127,6 +127,13 @@ hipError_t launch_q5k_mma(const MmaPlan &plan, const splosh_q5k_weight &w, const
                           int64_t ldc, int out_dtype, const void *residual, int64_t rows, void *workspace,
                           hipStream_t stream);
 
+// The same kernel over GGUF native blocks (Q8_0, IQ4_NL, Q6_K, Q3_K, IQ3_S, IQ4_XS); the plan's
+// units are 256 elements of K.
+bool gguf_mma_fits(int type, int64_t rows, int64_t columns, int64_t inner, int64_t lda);
+hipError_t launch_gguf_mma(const MmaPlan &plan, int type, const uint8_t *native, int64_t columns, int64_t inner,
+                           const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype, const void *residual,
+                           int64_t rows, void *workspace, hipStream_t stream);
+
 // Sums split-K partials [splits][nw][rows][n] in slice order and applies the epilogue
 // (silu(g) * u for nw = 2, then the optional residual, then the output conversion).
 hipError_t launch_splitk_finish(const float *partial, int splits, int nw, int64_t rows, int64_t n, void *out,

@@ -29,6 +29,7 @@
 // GgufQuant.swift:205-210 for Q5_K) rounded to bf16 (RNE), products exact in fp32, fp32
 // accumulation.
 #include "common.hpp"
+#include "gguf_decode.hpp"
 #include "launch.hpp"
 #include "mix.hpp"
 
@@ -76,6 +77,7 @@ struct MmaArgs {
     // Buffer extents (the fits checks keep them < 4 GiB): q4 codes and sidecars, or Q5_K plane0,
     // plane1 and meta; activations.
     uint32_t code_bytes, sidecar_bytes, meta_bytes, a_bytes;
+    uint32_t row_bytes;  // GGUF native blocks: bytes of a weight row
     // The next RMSNorm's operand, emitted from the epilogue (single weight, fp32 output, N a multiple
     // of 64; null norm_weight: no emit): values = bf16(h norm_weight[col]), and per row and band of
     // 64 columns the sums of the rounded values and of h * h, h being the value written to `out`.
@@ -415,6 +417,179 @@ struct Q5Format {
             d[2 * e] = f32x2_to_bf16x2(weight(lo[e], b), weight(lo[e], b + 2));
             d[2 * e + 1] = f32x2_to_bf16x2(weight(hi[e], b), weight(hi[e], b + 2));
         }
+        return as_bf16x8(d);
+    }
+};
+
+// GGUF native blocks (Q8_0, IQ4_NL, Q6_K, Q3_K, IQ3_S, IQ4_XS; GgufQuant.swift:136-300), rows of
+// blocks back to back as the file holds them: a step is 256 elements of K (one super-block, or
+// eight 32-element blocks); wave kw takes its 32-element groups 2 kw and 2 kw + 1, lane (r, h)
+// group j = 2 kw + h of column r, fetched by gguf_fetch (every load per lane, the blocks being
+// 2-byte aligned at best) D steps ahead like the q4 codes. prepare() takes the group's scales and
+// aligned words from the ring slot; operand(i) decodes elements 8 i .. 8 i + 7 in the reference
+// decoder's fp32 operation order (gguf_decode) and rounds them to bf16 (RNE), the MFMA's B operand
+// -- the same weights as the tiled and prefill kernels use.
+template <int TYPE, int CW, int KW, int D>
+struct GgufFormat {
+    static constexpr bool kGrouped = false;
+    static constexpr bool kEmit = false;
+    static constexpr int NW = 1;
+    // IQ3_S: the codebook's four magnitudes of each of its 512 entries as bytes, in LDS.
+    static constexpr int kTblBytes = TYPE == 21 ? 512 * 4 : 0;
+    const uint32_t *tbl = nullptr;
+    __device__ void build_table(char *t, int tid) {
+        if constexpr (TYPE == 21) {
+            tbl = (const uint32_t *)t;
+            if (tid < 512) {
+                const uint32_t packed = kIq3sPacked[tid];
+                uint32_t m = 0;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) m |= (2u * ((packed >> (3 * q)) & 7u) + 1u) << (8 * q);
+                ((uint32_t *)t)[tid] = m;
+            }
+        }
+    }
+    // Buffer loads of gguf_fetch<TYPE> as issued (the mid-step wait counts them; IQ3_S's two
+    // dword loads of codebook indices merge into one); the assembly check in the tests fails if
+    // the code issues fewer.
+    static constexpr int kWLoads = TYPE == 8 ? 4 : TYPE == 20 ? 3 : TYPE == 14 ? 8 : TYPE == 11 ? 9 : TYPE == 21 ? 7 : 4;
+    static constexpr int kUnitK = 256;
+    static constexpr int kBandCols = CW * 32;
+    static constexpr int kSBuf = 0;
+    static constexpr int kSideLoads = 0;
+    static_assert(KW == 4, "four waves cover the eight groups of a step");
+    static constexpr int piece(int i) { return i; }
+
+    rsrc_t rs;
+    int kw, cw, r, h, ga, gb;
+    uint32_t row_off;
+    GgufRaw<TYPE> raw[D];
+    // The group being dequantized: its scales (zero when the step has no group for this wave) and
+    // its code words in place.
+    float s0, s1;
+    uint32_t wd[8];
+    uint32_t extra;  // IQ3_S: the group's ninth bits
+
+    __device__ GgufFormat(const MmaArgs &args, int wave, int lane) {
+        kw = wave / CW;
+        cw = wave % CW;
+        r = lane & 31;
+        h = lane >> 5;
+        rs = make_rsrc(args.plane0, args.code_bytes);
+    }
+    __device__ int steps(int ga_, int gb_) const { return gb_ - ga_; }
+    __device__ bool active(int) const { return true; }
+    __device__ void begin(const MmaArgs &args, int band, int ga_, int gb_) {
+        ga = ga_;
+        gb = gb_;
+        const int64_t ncol = (int64_t)band * kBandCols + cw * 32 + r;
+        row_off = (uint32_t)(ncol < args.n ? ncol : args.n - 1) * args.row_bytes;
+    }
+    __device__ void load_s(int, char *) {}
+    __device__ void fetch_side(const char *) {}
+    __device__ void load_w(int slot, int t) {
+        const int b = ga + t < gb ? ga + t : gb - 1;
+        const int ub = __builtin_amdgcn_readfirstlane(b);
+        raw[slot] = gguf_fetch<TYPE>(rs, row_off, 8 * ub + 2 * kw + h);
+    }
+    __device__ void prepare(int slot, bool on) {
+        const GgufRaw<TYPE> &w = raw[slot];
+        const float one = on ? 1.0f : 0.0f;
+        if constexpr (TYPE == 8) {
+            s0 = half_bits_to_f32(w.d) * one;
+            uint32_t t[8];
+            align_span(w.codes, t);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) wd[q] = t[q];
+        } else if constexpr (TYPE == 20) {
+            s0 = half_bits_to_f32(w.d) * one;
+            uint32_t t[4];
+            align_span(w.codes, t);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) wd[q] = t[q];
+        } else if constexpr (TYPE == 23) {
+            const int j = w.j;
+            const uint32_t low = (w.lowb >> (8 * ((j >> 1) & 1) + 4 * (j & 1))) & 15;
+            const uint32_t scale = low | (((w.high >> (2 * j)) & 3) << 4);
+            s0 = half_bits_to_f32(w.d) * ((float)scale - 32.0f) * one;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) wd[q] = w.q[q];
+        } else if constexpr (TYPE == 14) {
+            const int quarter = w.j & 3;
+            const float d = half_bits_to_f32(w.d);
+            s0 = d * (float)(int8_t)(w.sc & 0xFF) * one;
+            s1 = d * (float)(int8_t)(w.sc >> 8) * one;
+            uint32_t ql[8], qh[8];
+            align_span(w.ql, ql);
+            align_span(w.qh, qh);
+            const int lsh = 4 * (quarter >> 1), hsh = 2 * quarter;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) wd[q] = ((ql[q] >> lsh) & 0x0F0F0F0Fu) | (((qh[q] >> hsh) & 0x03030303u) << 4);
+        } else if constexpr (TYPE == 11) {
+            const int j = w.j, shift = 2 * (j & 3), word = j >> 1;
+            const float d = half_bits_to_f32(w.d);
+            const uint32_t lows = w.lows >> (4 * (word >> 1)), highs = w.highs >> (2 * word);
+            s0 = d * ((float)((lows & 0xF) | ((highs & 3) << 4)) - 32.0f) * one;
+            s1 = d * ((float)(((lows >> 8) & 0xF) | (((highs >> 8) & 3) << 4)) - 32.0f) * one;
+            uint32_t hm[8], qs[8];
+            align_span(w.hm, hm);
+            align_span(w.qs, qs);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) wd[q] = ((qs[q] >> shift) & 0x03030303u) | (((hm[q] >> j) & 0x01010101u) << 2);
+        } else {
+            const int j = w.j;
+            const uint32_t scale = (w.scale >> (8 * ((j >> 1) & 1) + 4 * (j & 1))) & 15;
+            s0 = half_bits_to_f32(w.d) * (1.0f + 2.0f * (float)scale) * one;
+            extra = (w.ninth >> (8 * (j & 1))) & 0xFF;
+            uint32_t cb[2], sg[1];
+            align_span(w.cb, cb);
+            align_span(w.sg, sg);
+            wd[0] = cb[0];
+            wd[1] = cb[1];
+            wd[2] = sg[0];
+        }
+    }
+    // Elements 8 i .. 8 i + 7 of the group as bf16 (RNE) in k order, each the decoder's value
+    // (gguf_decode, same fp32 operations).
+    __device__ bf16x8 operand(int, int i, int) {
+        float v[8];
+        if constexpr (TYPE == 8) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = s0 * (float)(int8_t)((wd[2 * i + (e >> 2)] >> (8 * (e & 3))) & 0xFF);
+        } else if constexpr (TYPE == 20 || TYPE == 23) {
+            // Element e < 16: the low nibble of byte e; e >= 16: the high nibble of byte e - 16.
+            const int hi = i >> 1;
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const uint32_t x = wd[2 * (i & 1) + q];
+                const uint32_t vals = iq4_lookup4(hi ? (x >> 4) & 0x0F0F0F0Fu : x & 0x0F0F0F0Fu);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[4 * q + e] = s0 * (float)(int8_t)((vals >> (8 * e)) & 0xFF);
+            }
+        } else if constexpr (TYPE == 14 || TYPE == 11) {
+            constexpr float kOff = TYPE == 14 ? 32.0f : 4.0f;
+            const float ds = i < 2 ? s0 : s1;
+#pragma unroll
+            for (int q = 0; q < 2; ++q)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[4 * q + e] = ds * (cvt_byte(wd[2 * i + q], e) - kOff);
+        } else {
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                const int k = 2 * i + q;
+                const uint32_t code = ((wd[k >> 2] >> (8 * (k & 3))) & 0xFF) | (((extra >> k) & 1) << 8);
+                const uint32_t m = tbl[code];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float x = s0 * cvt_byte(m, e);
+                    const uint32_t sign = ((wd[2] >> (4 * k + e)) & 1u) << 31;
+                    v[4 * q + e] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, x) ^ sign);
+                }
+            }
+        }
+        u32x4 d;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) d[p] = f32x2_to_bf16x2(v[2 * p], v[2 * p + 1]);
         return as_bf16x8(d);
     }
 };
@@ -1215,6 +1390,36 @@ hipError_t launch_q5k_mma(const MmaPlan &plan, const splosh_q5k_weight &w, const
     args.meta_bytes = (uint32_t)(w.rows * blocks * 16);
     if (!w.plane1) return launch_mma_fm<Q5Format<kMmaCW, kMmaKW, kMmaDepth, false>>(plan, args, stream);  // Q4_K
     return launch_mma_fm<Q5Format<kMmaCW, kMmaKW, kMmaDepth>>(plan, args, stream);
+}
+
+bool gguf_mma_fits(int type, int64_t rows, int64_t columns, int64_t inner, int64_t lda) {
+    int elems = 0, bytes = 0;
+    if (!gguf_native_block(type, &elems, &bytes)) return false;
+    const int64_t limit = ((int64_t)1 << 32) - 256;
+    return rows >= 1 && rows <= 64 && columns > 0 && inner >= 256 && inner % 256 == 0 &&
+           (rows * lda + inner) * 2 < limit && columns * (inner / elems) * bytes < limit;
+}
+
+hipError_t launch_gguf_mma(const MmaPlan &plan, int type, const uint8_t *native, int64_t columns, int64_t inner,
+                           const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype, const void *residual,
+                           int64_t rows, void *workspace, hipStream_t stream) {
+    int elems = 0, bytes = 0;
+    gguf_native_block(type, &elems, &bytes);
+    MmaArgs args = {};
+    args.plane0 = native;
+    args.n = columns;
+    args.units = inner / 256;
+    set_io(args, plan, a, lda, out, ldc, out_dtype, residual, rows, inner, workspace, false);
+    args.row_bytes = (uint32_t)(inner / elems * bytes);
+    args.code_bytes = (uint32_t)(columns * args.row_bytes);
+    switch (type) {
+        case 8: return launch_mma_fm<GgufFormat<8, kMmaCW, kMmaKW, kMmaDepth>>(plan, args, stream);
+        case 20: return launch_mma_fm<GgufFormat<20, kMmaCW, kMmaKW, kMmaDepth>>(plan, args, stream);
+        case 14: return launch_mma_fm<GgufFormat<14, kMmaCW, kMmaKW, kMmaDepth>>(plan, args, stream);
+        case 11: return launch_mma_fm<GgufFormat<11, kMmaCW, kMmaKW, kMmaDepth>>(plan, args, stream);
+        case 21: return launch_mma_fm<GgufFormat<21, kMmaCW, kMmaKW, kMmaDepth>>(plan, args, stream);
+        default: return launch_mma_fm<GgufFormat<23, kMmaCW, kMmaKW, kMmaDepth>>(plan, args, stream);
+    }
 }
 
 }  // namespace splosh

@@ -63,12 +63,12 @@ def test_native_gemm(rt, name, rows):
 @pytest.mark.parametrize("name", list(TYPES))
 @pytest.mark.parametrize("rows", [2, 5, 6, 7, 8])
 @pytest.mark.parametrize("n,k", [(200, 1536), (203, 4352)])
-def test_two_to_eight_rows_streaming(rt, name, rows, n, k):
-    """2-8 activation rows take one pass of the streaming kernel (four rows a pass up to four,
-    eight above), its activations staged in LDS for a workgroup's four waves, with and without a
-    workspace, against the oracle. 203 weight rows leave waves past the last row, which still
-    stage their share and meet the barriers; K4352 gives three rounds of 64 groups, the last
-    partial."""
+def test_two_to_eight_rows_auto(rt, name, rows, n, k):
+    """2-8 activation rows through AUTO, with and without a workspace, against the oracle: the
+    streaming kernel up to the format's limit (four rows a pass, activations staged in LDS for a
+    workgroup's four waves), the stream-K MFMA kernel above it. 203 weight rows leave streaming
+    waves past the last row, which still stage their share and meet the barriers, and a partial
+    MFMA band; K4352 gives three streaming rounds of 64 groups, the last partial."""
     t = TYPES[name]
     w, dense = _weight(rt, t, n, k, seed=rows + 3 * t + n)
     a_bits = oracle.bf16_normal((rows, k), seed=rows + 11)
@@ -79,6 +79,45 @@ def test_two_to_eight_rows_streaming(rt, name, rows, n, k):
         got = rt.gemm(w, a, out_dtype=torch.float32, workspace=ws)
         check_close(got.cpu().numpy(), ref, bf16_out=False, tight=True, absref=absref,
                     label=f"{name} rows={rows} n={n} k={k} workspace={'none' if ws is not None else 'fresh'}")
+
+
+@pytest.mark.parametrize("name,rows", [("q8_0", 5), ("q8_0", 8), ("iq4NL", 4), ("iq4NL", 7), ("q3K", 5), ("q3K", 6)])
+def test_streaming_eight_rows(rt, name, rows):
+    """The streaming kernel's eight-row pass: Q8_0 and IQ4_NL with K % 256 != 0 (the MFMA kernel
+    takes 256 elements a step, so AUTO streams up to eight rows), Q3_K up to its limit of six."""
+    t = TYPES[name]
+    n, k = 203, 1568 if name != "q3K" else 4352
+    w, dense = _weight(rt, t, n, k, seed=rows + 5 * t)
+    a_bits = oracle.bf16_normal((rows, k), seed=rows + 13)
+    ref = oracle.gemm_a_bf16_w_f32(a_bits, dense)
+    got = rt.gemm(w, bf16_tensor(a_bits), out_dtype=torch.float32)
+    check_close(got.cpu().numpy(), ref, bf16_out=False, tight=True, absref=abs_gemm(a_bits, dense),
+                label=f"{name} streaming rows={rows} k={k}")
+
+
+@pytest.mark.parametrize("name", list(TYPES))
+@pytest.mark.parametrize("rows", [9, 33, 64])
+def test_mma_kernel(rt, name, rows):
+    """The stream-K MFMA kernel over native blocks (AUTO above the streaming limit, up to 64 rows):
+    a partial band (N = 203), 17 steps of K, split over workgroups (workspace) and whole bands (an
+    empty one), bf16 and fp32 out, the residual; against the oracle."""
+    t = TYPES[name]
+    n, k = 203, 4352
+    w, dense = _weight(rt, t, n, k, seed=rows + 17 * t)
+    a_bits = oracle.bf16_normal((rows, k), seed=rows + 19)
+    ref = oracle.gemm_a_bf16_w_f32(a_bits, dense)
+    absref = abs_gemm(a_bits, dense)
+    a = bf16_tensor(a_bits)
+    for ws in (None, torch.empty(0, dtype=torch.uint8, device="cuda")):
+        split = ws is None
+        got = rt.gemm(w, a, out_dtype=torch.float32, workspace=ws)
+        check_close(got.cpu().numpy(), ref, bf16_out=False, tight=True, absref=absref,
+                    label=f"{name} mma rows={rows} split={split}")
+        got = rt.gemm(w, a, workspace=ws)
+        check_close(to_f32(got), ref, bf16_out=True, tight=True, absref=absref, label=f"{name} mma bf16 rows={rows}")
+    res = torch.from_numpy(oracle.bf16_normal((rows, n), seed=7).astype(np.float32)).cuda()
+    got = rt.gemm(w, a, out=res.clone(), out_dtype=torch.float32, residual=res)
+    check_close(got.cpu().numpy(), ref + res.cpu().numpy(), bf16_out=False, label=f"{name} mma residual rows={rows}")
 
 
 def test_q8_0_one_row_long_k(rt):
@@ -114,9 +153,10 @@ def test_config0_size_sampled(rt, name):
 @pytest.mark.parametrize("name", ["q6K", "q3K"])
 @pytest.mark.parametrize("rows", [2, 4, 6, 8])
 def test_streaming_long_k_sampled(rt, name, rows):
-    """Q6_K and Q3_K at K=17408 -> N=5120 through the streaming kernel (AUTO up to eight rows): its
-    pairs form sums the unsigned codes and takes the bias off once a group, so the cancellation
-    grows with K; 256 sampled columns against the oracle at the tight tolerance."""
+    """Q6_K and Q3_K at K=17408 -> N=5120 through AUTO: the streaming kernel up to the format's
+    limit (its pairs form sums the unsigned codes and takes the bias off once a group, so the
+    cancellation grows with K), the MFMA kernel above; 256 sampled columns against the oracle at
+    the tight tolerance."""
     t = TYPES[name]
     n, k = 5120, 17408
     elems, size = oracle.GGUF_BLOCK[t]

@@ -46,6 +46,10 @@ def _weight_loads(name):
     if m:
         nw, tiled = int(m.group(1)), m.group(2) == "1"
         return nw if tiled else 3 * nw
+    m = re.search(r"GgufFormatILi(\d+)E", name)
+    if m:
+        # gguf_fetch's buffer loads per format: fp16 fields and the dword windows of its spans.
+        return {8: 4, 20: 3, 14: 8, 11: 9, 21: 7, 23: 4}[int(m.group(1))]
     m = re.search(r"Q5FormatILi\d+ELi\d+ELi\d+ELb(\d)", name)
     assert m, name
     return 2 if m.group(1) == "1" else 1
