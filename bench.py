@@ -44,7 +44,8 @@ MEASURED_TRAFFIC = {
     ("prefill2048", "prefill_up"): 264791.5 * 2 * 1024 + 114688.0 * 1024,  # prefill_kernel<Q4Stage>
     ("q5k2048", "q5k"): 347729.4 * 2 * 1024 + 98304.0 * 1024,  # prefill_kernel<Q5Stage<true>>
     ("q6k2048", "gguf"): 366940.1 * 2 * 1024 + 110080.0 * 1024,  # prefill_kernel<GgufStage<14>>
-    ("q6k64", "gguf"): (51389.6 + 6413.1) * 2 * 1024 + (25600.0 + 643.4) * 1024,  # gguf_tile_kernel<14, 1, 2, true, 2> + gguf_tile_finish<1, 2>
+    ("q6k64", "gguf"): 47875.7 * 2 * 1024 + 4212.1 * 1024,  # mma_kernel<GgufFormat<14, 2, 4, 3>, 2, 2, 4, 3>
+    ("iq3s64", "gguf"): 30858.2 * 2 * 1024 + 4174.7 * 1024,  # mma_kernel<GgufFormat<21, 2, 4, 3>, 2, 2, 4, 3>
     ("q6k1", "gguf"): 36191.3 * 2 * 1024 + 10.0 * 1024,  # gguf_pairs_kernel<14, 4, 2>
     ("q3k1", "gguf"): 19009.8 * 2 * 1024 + 10.0 * 1024,  # gguf_pairs_kernel<11, 4, 2>
     ("iq3s1", "gguf"): 19068.8 * 2 * 1024 + 10.0 * 1024,  # gguf_pairs_kernel<21, 4, 2>
