@@ -567,12 +567,15 @@ struct GgufFormat {
                 for (int e = 0; e < 4; ++e) v[4 * q + e] = s0 * (float)(int8_t)((vals >> (8 * e)) & 0xFF);
             }
         } else if constexpr (TYPE == 14 || TYPE == 11) {
+            // ds (c - o) as fma(c, ds, -o ds): o is a power of two, so -o ds is exact, the fma's
+            // sum is ds (c - o) exactly and its one rounding is the product's.
             constexpr float kOff = TYPE == 14 ? 32.0f : 4.0f;
             const float ds = i < 2 ? s0 : s1;
+            const float nd = -kOff * ds;
 #pragma unroll
             for (int q = 0; q < 2; ++q)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) v[4 * q + e] = ds * (cvt_byte(wd[2 * i + q], e) - kOff);
+                for (int e = 0; e < 4; ++e) v[4 * q + e] = __builtin_fmaf(cvt_byte(wd[2 * i + q], e), ds, nd);
         } else {
 #pragma unroll
             for (int q = 0; q < 2; ++q) {
