@@ -46,6 +46,8 @@ MEASURED_TRAFFIC = {
     ("q6k2048", "gguf"): 366940.1 * 2 * 1024 + 110080.0 * 1024,  # prefill_kernel<GgufStage<14>>
     ("q6k64", "gguf"): 47875.7 * 2 * 1024 + 4212.1 * 1024,  # mma_kernel<GgufFormat<14, 2, 4, 3>, 2, 2, 4, 3>
     ("iq3s64", "gguf"): 30858.2 * 2 * 1024 + 4174.7 * 1024,  # mma_kernel<GgufFormat<21, 2, 4, 3>, 2, 2, 4, 3>
+    ("q6k64r", "gguf"): 47010.9 * 2 * 1024 + 4340.4 * 1024,  # the same, Q6_K in the ROWS32 order
+    ("q80_64r", "gguf"): 57538.1 * 2 * 1024 + 4337.7 * 1024,  # mma_kernel<GgufFormat<8, 2, 4, 3>, 2, 2, 4, 3>, ROWS32
     ("q6k1", "gguf"): 36191.3 * 2 * 1024 + 10.0 * 1024,  # gguf_pairs_kernel<14, 4, 2>
     ("q3k1", "gguf"): 19009.8 * 2 * 1024 + 10.0 * 1024,  # gguf_pairs_kernel<11, 4, 2>
     ("iq3s1", "gguf"): 19068.8 * 2 * 1024 + 10.0 * 1024,  # gguf_pairs_kernel<21, 4, 2>
@@ -365,8 +367,10 @@ def build_workload(name, rt, torch, gen, kernel):
         if not name.startswith(prefix):
             continue
         # Config 3's shape (K=17408 -> N=5120) with the weight in the native blocks of another GGUF
-        # format (random bytes, fp16 scale fields of about 1e-3).
-        m = int(name[len(prefix):] or 1)
+        # format (random bytes, fp16 scale fields of about 1e-3); a trailing "r": in the ROWS32
+        # order (splosh_gguf_repack_rows32).
+        rows32 = name.endswith("r")
+        m = int(name[len(prefix):len(name) - (1 if rows32 else 0)] or 1)
         k, n = 17408, 5120
         elems, size = rt.GGUF_NATIVE[gtype]
         one = n * (k // elems) * size
@@ -378,7 +382,9 @@ def build_workload(name, rt, torch, gen, kernel):
             native = torch.randint(0, 256, (blocks, size), dtype=torch.uint8, device="cuda", generator=gen)
             d = (1e-3 * (1 + 0.25 * (torch.rand(blocks, device="cuda", generator=gen) * 2 - 1))).to(torch.float16)
             native[:, at:at + 2] = d.view(torch.uint8).view(blocks, 2)
-            ws.append(rt.GgufWeight(native.view(-1), gtype, n, k))
+            w = rt.GgufWeight(native.view(-1), gtype, n, k)
+            ws.append(rt.gguf_repack_rows32(w) if rows32 else w)
+            del native
         x = torch.randn(m, k, device="cuda", generator=gen).to(torch.bfloat16)
         out = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
         b = one + m * k * 2 + m * n * 2
@@ -388,7 +394,8 @@ def build_workload(name, rt, torch, gen, kernel):
             w = ws[i % ncopy]
             return [("gguf", lambda: rt.gemm(w, x, out=out, workspace=ws_g))]
 
-        cfg = {"workload": f"{label} K17408->N5120 (native blocks)", "rows": m, "format": f"gguf {label.lower()}",
+        order = "ROWS32 order" if rows32 else "native blocks"
+        cfg = {"workload": f"{label} K17408->N5120 ({order})", "rows": m, "format": f"gguf {label.lower()}",
                "weight_copies": ncopy}
         return launches, b, 2 * m * n * k, {"gguf": b}, cfg, {"gguf": 2 * m * n * k}
     raise SystemExit(f"unknown workload {name}")

@@ -298,6 +298,15 @@ int splosh_q4k_dequant(const splosh_q5k_weight *w, float *out, hipStream_t strea
  * for these formats (Engine.swift:1673-1694 dispatching sp_gguf_* by format,
  * engine_gguf.metal:332-349) and GgufTensorType.decode (GgufQuant.swift:136-159).
  *
+ * Layout. `gguf_type | SPLOSH_GGUF_ROWS32` (every entry point below) names the same blocks in
+ * the ROWS32 order that splosh_gguf_repack_rows32 writes: the 256-element units (one super-block,
+ * or eight 32-element blocks) of 32 consecutive rows interleaved -- unit u of row n at byte
+ * ((n / 32) (inner / 256) 32 + u 32 + n % 32) x unit bytes -- rows padded to a multiple of 32,
+ * inner % 256 == 0. The bytes of every block are the file's; only their order differs. It has no
+ * counterpart in the reference (whose GgufPlanes repack serves Q5_K only): the 32 lanes of a
+ * wave that read one unit of 32 weight rows read one contiguous run, which the row-major file
+ * order scatters over 32 rows (at K17408 -> N5120, M=64: Q8_0 44 -> 33 us, IQ4_XS 39 -> 31).
+ *
  * splosh_gguf_gemm: out[m][n] = sum_k a[m][k] w[n][k] (+ residual). Up to a few activation rows
  * (IQ4_NL 3, Q3_K 6, the others 4) a streaming kernel reads the weight once. Up to 64 rows
  * (inner % 256 == 0) the stream-K MFMA kernel of splosh_q4_gemm decodes each weight group once
@@ -311,6 +320,15 @@ int splosh_q4k_dequant(const splosh_q5k_weight *w, float *out, hipStream_t strea
  * splosh_gguf_dequant: the weight as fp32 [rows][inner], bit-exact with the reference decoder.
  * `native` must be 4-byte aligned (GGUF tensor data is 32-byte aligned).
  * Unsupported types return SPLOSH_ERR_UNSUPPORTED. */
+#define SPLOSH_GGUF_ROWS32 0x100
+
+/* The ROWS32 order of a native-block weight (layout above): out holds
+ * splosh_gguf_rows32_bytes(gguf_type, rows, inner) bytes (the padding rows zero); 0 when the type
+ * or shape has no ROWS32 form (inner % 256 != 0). */
+size_t splosh_gguf_rows32_bytes(int gguf_type, int64_t rows, int64_t inner);
+int splosh_gguf_repack_rows32(int gguf_type, const uint8_t *native, int64_t rows, int64_t inner, uint8_t *out,
+                              hipStream_t stream);
+
 int splosh_gguf_gemm(int gguf_type, const uint8_t *native, int64_t rows, int64_t inner, const uint16_t *a,
                      int64_t lda, void *out, int64_t ldc, int out_dtype, const void *residual, int64_t m,
                      void *workspace, size_t workspace_bytes, hipStream_t stream);

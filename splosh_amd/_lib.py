@@ -102,6 +102,8 @@ SIGNATURES = {
     "splosh_q4k_dequant": (_int, [ctypes.POINTER(Q5KWeight), _vp, _vp]),
     "splosh_gguf_gemm": (_int, [_int, _vp, _i64, _i64, _vp, _i64, _vp, _i64, _int, _vp, _i64, _vp, _sz, _vp]),
     "splosh_gguf_dequant": (_int, [_int, _vp, _i64, _i64, _vp, _vp]),
+    "splosh_gguf_rows32_bytes": (_sz, [_int, _i64, _i64]),
+    "splosh_gguf_repack_rows32": (_int, [_int, _vp, _i64, _i64, _vp, _vp]),
     "splosh_q5k_gemm_heads": (_int, [ctypes.POINTER(Q5KWeight), _int, _vp, _i64, _vp, _i64, _int, _vp, _i64, _int,
                                      _vp, _sz, _vp]),
     "splosh_q4k_gemm_heads": (_int, [ctypes.POINTER(Q5KWeight), _int, _vp, _i64, _vp, _i64, _int, _vp, _i64, _int,

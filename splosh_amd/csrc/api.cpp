@@ -709,15 +709,19 @@ int splosh_q4k_dequant(const splosh_q5k_weight *w, float *out, hipStream_t strea
 // Shape and geometry checks shared by the native-block GGUF entry points.
 static int check_gguf_native(int type, const uint8_t *native, int64_t rows, int64_t inner) {
     int elems = 0, bytes = 0;
-    if (!splosh::gguf_native_block(type, &elems, &bytes))
+    if ((type & ~(0xFF | SPLOSH_GGUF_ROWS32)) != 0 || !splosh::gguf_native_block(type, &elems, &bytes))
         return fail(SPLOSH_ERR_UNSUPPORTED, "ggml type not supported in native blocks (Q8_0, Q3_K, Q6_K, IQ4_NL, IQ3_S, IQ4_XS)");
+    const bool rows32 = (type & SPLOSH_GGUF_ROWS32) != 0;
+    if (rows32 && (inner <= 0 || inner % 256 != 0))
+        return fail(SPLOSH_ERR_LAYOUT_MISMATCH, "the ROWS32 layout needs inner % 256 == 0");
     if (!native) return fail(SPLOSH_ERR_NULL_POINTER, "null weight");
     // The kernels read the blocks through dword-aligned windows relative to this base (GGUF tensor
     // data is 32-byte aligned in the file).
     if (!aligned(native, 4)) return fail(SPLOSH_ERR_LAYOUT_MISMATCH, "native weight must be 4-byte aligned");
     if (rows <= 0 || inner <= 0) return fail(SPLOSH_ERR_INVALID_SHAPE, "rows and inner must be positive");
     if (inner % elems != 0) return fail(SPLOSH_ERR_LAYOUT_MISMATCH, "inner is not a whole number of native blocks");
-    if (mul_overflows(rows, inner / elems * bytes) || rows * (inner / elems * bytes) >= ((int64_t)1 << 32))
+    const int64_t stored = rows32 ? (rows + 31) / 32 * 32 : rows;  // ROWS32 pads to whole groups of 32 rows
+    if (mul_overflows(stored, inner / elems * bytes) || stored * (inner / elems * bytes) >= ((int64_t)1 << 32))
         return fail(SPLOSH_ERR_ARITHMETIC_OVERFLOW, "weight larger than 4 GiB");
     return ok();
 }
@@ -749,7 +753,8 @@ static int gguf_native_gemm(int gguf_type, const uint8_t *native, int64_t rows, 
     }();
     const bool prefill = m >= prefill_rows && aligned(out, 16) && (!residual || aligned(residual, 16)) &&
                          splosh::gguf_prefill_fits(gguf_type, m, rows, inner, lda, ldc);
-    const int64_t stream_max = gguf_type == 11 ? 6 : gguf_type == 20 ? 3 : 4;
+    const int base_type = gguf_type & 0xFF;
+    const int64_t stream_max = base_type == 11 ? 6 : base_type == 20 ? 3 : 4;
     const bool mma = !prefill && m > stream_max && splosh::gguf_mma_fits(gguf_type, m, rows, inner, lda);
     const bool tile = !prefill && !mma && m > 8 && splosh::gguf_tile_fits(m, rows, inner, lda);
     // The streaming kernels read the activations through head_group(); the other kernels get a
@@ -779,6 +784,25 @@ static int gguf_native_gemm(int gguf_type, const uint8_t *native, int64_t rows, 
     return hip_status(splosh::launch_gguf_gemv(gguf_type, native, rows, inner, a, lda, out, ldc, out_dtype, residual,
                                                m, stream, ho.hs, ho.vph),
                       "gguf native gemm launch");
+}
+
+size_t splosh_gguf_rows32_bytes(int gguf_type, int64_t rows, int64_t inner) {
+    int elems = 0, bytes = 0;
+    if ((gguf_type & ~0xFF) != 0 || !splosh::gguf_native_block(gguf_type, &elems, &bytes) || rows <= 0 ||
+        inner <= 0 || inner % 256 != 0)
+        return 0;
+    return (size_t)((rows + 31) / 32 * 32) * (size_t)(inner / elems * bytes);
+}
+
+int splosh_gguf_repack_rows32(int gguf_type, const uint8_t *native, int64_t rows, int64_t inner, uint8_t *out,
+                              hipStream_t stream) {
+    if (gguf_type & SPLOSH_GGUF_ROWS32) return fail(SPLOSH_ERR_LAYOUT_MISMATCH, "the source must be in the file's order");
+    int st = check_gguf_native(gguf_type | SPLOSH_GGUF_ROWS32, native, rows, inner);
+    if (st) return st;
+    if (!out) return fail(SPLOSH_ERR_NULL_POINTER, "null output");
+    if (!aligned(out, 4)) return fail(SPLOSH_ERR_LAYOUT_MISMATCH, "output must be 4-byte aligned");
+    return hip_status(splosh::launch_gguf_repack_rows32(gguf_type, native, rows, inner, out, stream),
+                      "gguf rows32 repack launch");
 }
 
 int splosh_gguf_gemm(int gguf_type, const uint8_t *native, int64_t rows, int64_t inner, const uint16_t *a,

@@ -30,6 +30,26 @@ template <> struct GgufGeom<23> { static constexpr int kElems = 256, kBytes = 13
 template <> struct GgufGeom<11> { static constexpr int kElems = 256, kBytes = 110; }; // Q3_K
 template <> struct GgufGeom<21> { static constexpr int kElems = 256, kBytes = 110; }; // IQ3_S
 
+// Bytes of 256 elements of a row (one super-block, or eight 32-element blocks): the unit of the
+// ROWS32 layout.
+template <int TYPE>
+constexpr uint32_t gguf_unit_bytes() { return 256 / GgufGeom<TYPE>::kElems * GgufGeom<TYPE>::kBytes; }
+
+// Where row n's 256-element units lie: unit u at base + u ustride.
+//  * NATIVE (the file's order, rows back to back): base n row_bytes, ustride one unit.
+//  * ROWS32 (inner % 256 == 0, rows padded to a multiple of 32): the units of 32 consecutive rows
+//    interleaved -- unit u of row n at ((n / 32) units 32 + u 32 + n % 32) unit bytes -- so the 32
+//    lanes that read one unit of 32 rows each read one contiguous run.
+struct GgufRow {
+    uint32_t base, ustride;
+};
+template <int TYPE>
+__device__ __forceinline__ GgufRow gguf_row(uint32_t n, uint32_t row_bytes, bool rows32) {
+    constexpr uint32_t UB = gguf_unit_bytes<TYPE>();
+    if (rows32) return GgufRow{((n >> 5) * (row_bytes / UB) * 32u + (n & 31u)) * UB, 32u * UB};
+    return GgufRow{n * row_bytes, UB};
+}
+
 // The IQ3_S codebook (the format's table, llama.cpp's iq3s_grid, kept by the reference as
 // GgufTensorType.iq3sGrid, GgufQuant.swift:60): entry i holds four magnitudes, each 1..15 and odd,
 // stored as twelve bits: magnitude t = 2 ((code >> 3t) & 7) + 1.
@@ -106,7 +126,7 @@ template <int W>
 __device__ __forceinline__ uint32_t byte_of(const uint32_t (&w)[W], int e) { return (w[e >> 2] >> (8 * (e & 3))) & 0xFF; }
 
 // Each native format's group decoder in two halves: gguf_fetch issues every load of group g of a
-// row whose blocks start at byte `row` and returns the raw bytes (GgufRaw<TYPE>); gguf_decode turns
+// row (where its units lie: gguf_row) and returns the raw bytes (GgufRaw<TYPE>); gguf_decode turns
 // them into the 32 values with no memory access, so that a kernel can fetch one step ahead.
 // Values follow GgufQuant.swift's decode in its fp32 operation order.
 template <int TYPE>
@@ -149,19 +169,21 @@ struct GgufRaw<23> {  // IQ4_XS (:261-275): d, scales_h, scales_l[4], qs[128]
 };
 
 template <int TYPE>
-__device__ __forceinline__ GgufRaw<TYPE> gguf_fetch(rsrc_t r, uint32_t row, int g) {
+__device__ __forceinline__ GgufRaw<TYPE> gguf_fetch(rsrc_t r, GgufRow row_, int g) {
     GgufRaw<TYPE> w;
+    // The group's unit (8 groups of 32), then its block within the unit for 32-element blocks.
+    const uint32_t row = row_.base + (uint32_t)(g >> 3) * row_.ustride;
     if constexpr (TYPE == 8) {
-        const uint32_t b = row + (uint32_t)g * 34u;
+        const uint32_t b = row + (uint32_t)(g & 7) * 34u;
         w.d = ld16(r, b);
         w.codes = fetch_span<8>(r, b + 2);
     } else if constexpr (TYPE == 20) {
-        const uint32_t b = row + (uint32_t)g * 18u;
+        const uint32_t b = row + (uint32_t)(g & 7) * 18u;
         w.d = ld16(r, b);
         w.codes = fetch_span<4>(r, b + 2);
     } else if constexpr (TYPE == 14) {
         const int j = g & 7, half = j >> 2, quarter = j & 3;
-        const uint32_t b = row + (uint32_t)(g >> 3) * 210u;
+        const uint32_t b = row;
         w.j = j;
         w.d = ld16(r, b + 208);
         w.sc = ld16(r, b + 192 + 2 * j);
@@ -169,7 +191,7 @@ __device__ __forceinline__ GgufRaw<TYPE> gguf_fetch(rsrc_t r, uint32_t row, int 
         w.qh = fetch_span<8>(r, b + 128 + 32 * half);
     } else if constexpr (TYPE == 11) {
         const int j = g & 7, half = j >> 2, word = j >> 1;
-        const uint32_t b = row + (uint32_t)(g >> 3) * 110u;
+        const uint32_t b = row;
         w.j = j;
         w.d = ld16(r, b + 108);
         // Scales 2 j and 2 j + 1: bytes 2 (j % 2), 2 (j % 2) + 1 of word j / 2 % 2 (their low or
@@ -180,7 +202,7 @@ __device__ __forceinline__ GgufRaw<TYPE> gguf_fetch(rsrc_t r, uint32_t row, int 
         w.qs = fetch_span<8>(r, b + 32 + 32 * half);
     } else if constexpr (TYPE == 21) {
         const int j = g & 7;
-        const uint32_t b = row + (uint32_t)(g >> 3) * 110u;
+        const uint32_t b = row;
         w.j = j;
         w.d = ld16(r, b);
         w.scale = ld16(r, b + 106 + 2 * (j >> 2));
@@ -189,7 +211,7 @@ __device__ __forceinline__ GgufRaw<TYPE> gguf_fetch(rsrc_t r, uint32_t row, int 
         w.sg = fetch_span<1>(r, b + 74 + 4 * j);
     } else {
         const int j = g & 7;
-        const uint32_t b = row + (uint32_t)(g >> 3) * 136u;
+        const uint32_t b = row;
         w.j = j;
         w.d = ld16(r, b);
         w.high = ld16(r, b + 2);
@@ -295,9 +317,9 @@ __device__ __forceinline__ void gguf_decode(const GgufRaw<TYPE> &w, float (&v)[3
     }
 }
 
-// Group g of a row whose blocks start at byte `row`: fetch and decode at once.
+// Group g of a row (gguf_row): fetch and decode at once.
 template <int TYPE>
-__device__ __forceinline__ void decode_group(rsrc_t r, uint32_t row, int g, float (&v)[32]) {
+__device__ __forceinline__ void decode_group(rsrc_t r, GgufRow row, int g, float (&v)[32]) {
     gguf_decode<TYPE>(gguf_fetch<TYPE>(r, row, g), v);
 }
 

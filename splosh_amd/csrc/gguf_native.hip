@@ -39,6 +39,7 @@ struct GgufNativeArgs {
     int out_dtype;
     float *dense;
     int hs, vph;  // value-head order of the activations (head_group); hs < 0: none
+    int rows32;   // the weight in the ROWS32 order (gguf_row)
 };
 
 template <int TYPE>
@@ -50,7 +51,7 @@ __global__ void __launch_bounds__(256) gguf_dequant_kernel(GgufNativeArgs args) 
     const int g = (int)(t % groups);
     const rsrc_t r = make_rsrc(args.w, args.w_bytes);
     float v[32];
-    decode_group<TYPE>(r, (uint32_t)(n * args.row_bytes), g, v);
+    decode_group<TYPE>(r, gguf_row<TYPE>((uint32_t)n, args.row_bytes, args.rows32), g, v);
     f32x4 *dst = (f32x4 *)(args.dense + n * args.inner + (int64_t)g * 32);
 #pragma unroll
     for (int q = 0; q < 8; ++q) dst[q] = f32x4{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
@@ -73,7 +74,7 @@ __global__ void __launch_bounds__(256) gguf_embed_kernel(GgufNativeArgs args, co
         for (int e = 0; e < 32; ++e) v[e] = 0.0f;
     } else {
         const rsrc_t r = make_rsrc(args.w, args.w_bytes);
-        decode_group<TYPE>(r, (uint32_t)(row * args.row_bytes), g, v);
+        decode_group<TYPE>(r, gguf_row<TYPE>((uint32_t)row, args.row_bytes, args.rows32), g, v);
     }
     if (args.out_dtype == SPLOSH_F32) {
         float *dst = (float *)args.out + i * args.ldc + (int64_t)g * 32;
@@ -118,7 +119,7 @@ __device__ __forceinline__ void code_pairs(const uint32_t (&codes)[8], GroupPair
 }
 
 template <int TYPE>
-__device__ __forceinline__ GroupPairs group_pairs(rsrc_t r, uint32_t row, int g, const uint32_t *lut) {
+__device__ __forceinline__ GroupPairs group_pairs(rsrc_t r, GgufRow row, int g, const uint32_t *lut) {
     GroupPairs gp;
     if constexpr (TYPE == 8) {
         const GgufRaw<8> w = gguf_fetch<8>(r, row, g);
@@ -242,9 +243,10 @@ __global__ void __launch_bounds__(256) gguf_pairs_kernel(GgufNativeArgs args) {
     const int mr = (int)(args.m - m0 < MR ? args.m - m0 : MR);  // activation rows of this pass
     const int groups = (int)(args.inner / 32);
     const rsrc_t rs = make_rsrc(args.w, args.w_bytes);
-    uint32_t row[R];
+    GgufRow row[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) row[r] = (uint32_t)((n0 + r < args.rows ? n0 + r : args.rows - 1) * args.row_bytes);
+    for (int r = 0; r < R; ++r)
+        row[r] = gguf_row<TYPE>((uint32_t)(n0 + r < args.rows ? n0 + r : args.rows - 1), args.row_bytes, args.rows32);
     float acc[R][MR];
 #pragma unroll
     for (int r = 0; r < R; ++r)
@@ -393,7 +395,7 @@ __global__ void __launch_bounds__(256) gguf_gemv_kernel(GgufNativeArgs args) {
     const int64_t m0 = (int64_t)blockIdx.y * MR;
     const int groups = (int)(args.inner / 32);
     const rsrc_t r = make_rsrc(args.w, args.w_bytes);
-    const uint32_t row = (uint32_t)(n * args.row_bytes);
+    const GgufRow row = gguf_row<TYPE>((uint32_t)n, args.row_bytes, args.rows32);
     float acc[MR];
 #pragma unroll
     for (int i = 0; i < MR; ++i) acc[i] = 0.0f;
@@ -458,7 +460,7 @@ __global__ void __launch_bounds__(256) gguf_gemv_kernel(GgufNativeArgs args) {
 }
 
 int gguf_native_block(int type, int *elems, int *bytes) {
-    switch (type) {
+    switch (type & 0xFF) {
         case 8: *elems = 32; *bytes = 34; return 1;
         case 20: *elems = 32; *bytes = 18; return 1;
         case 14: *elems = 256; *bytes = 210; return 1;
@@ -469,20 +471,50 @@ int gguf_native_block(int type, int *elems, int *bytes) {
     }
 }
 
-static void fill_args(GgufNativeArgs &args, int type, const uint8_t *w, int64_t rows, int64_t inner) {
+// Fills the weight fields; returns the type id without its layout flag.
+static int fill_args(GgufNativeArgs &args, int type, const uint8_t *w, int64_t rows, int64_t inner) {
+    args.rows32 = gguf_layout(type);
     int elems = 0, bytes = 0;
     gguf_native_block(type, &elems, &bytes);
     args.w = w;
     args.rows = rows;
     args.inner = inner;
     args.row_bytes = (uint32_t)(inner / elems * bytes);
-    args.w_bytes = (uint32_t)(rows * (int64_t)args.row_bytes);
+    const int64_t stored = args.rows32 ? (rows + 31) / 32 * 32 : rows;
+    args.w_bytes = (uint32_t)(stored * (int64_t)args.row_bytes);
+    return type;
+}
+
+// One thread a 2-byte word of the ROWS32 weight: its unit (row n, unit u) and the word's place in
+// it, copied from the native order (zero for the padding rows). Every block is an even number of
+// bytes, so words never straddle a unit.
+__global__ void __launch_bounds__(256) gguf_rows32_kernel(const uint16_t *__restrict__ native, int64_t rows,
+                                                          int64_t units, int unit_words, uint16_t *__restrict__ out,
+                                                          int64_t total) {
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= total) return;
+    const int64_t slot = t / unit_words, wd = t - slot * unit_words;  // slot: unit position in ROWS32
+    const int64_t grp = slot / (units * 32), rem = slot - grp * units * 32;
+    const int64_t u = rem / 32, n = grp * 32 + rem % 32;
+    out[t] = n < rows ? native[(n * units + u) * unit_words + wd] : (uint16_t)0;
+}
+
+hipError_t launch_gguf_repack_rows32(int type, const uint8_t *native, int64_t rows, int64_t inner, uint8_t *out,
+                                     hipStream_t stream) {
+    type &= 0xFF;
+    int elems = 0, bytes = 0;
+    gguf_native_block(type, &elems, &bytes);
+    const int unit_words = 256 / elems * bytes / 2;
+    const int64_t units = inner / 256, total = (rows + 31) / 32 * 32 * units * unit_words;
+    hipLaunchKernelGGL(gguf_rows32_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream,
+                       (const uint16_t *)native, rows, units, unit_words, (uint16_t *)out, total);
+    return hipGetLastError();
 }
 
 hipError_t launch_gguf_dequant(int type, const uint8_t *w, int64_t rows, int64_t inner, float *dense,
                                hipStream_t stream) {
     GgufNativeArgs args = {};
-    fill_args(args, type, w, rows, inner);
+    type = fill_args(args, type, w, rows, inner);
     args.dense = dense;
     const int64_t threads = rows * (inner / 32);
     const dim3 grid((unsigned)((threads + 255) / 256));
@@ -500,7 +532,7 @@ hipError_t launch_gguf_dequant(int type, const uint8_t *w, int64_t rows, int64_t
 hipError_t launch_gguf_embed(int type, const uint8_t *w, int64_t rows, int64_t inner, const uint32_t *tokens,
                              int64_t count, void *out, int64_t ldo, int out_dtype, hipStream_t stream) {
     GgufNativeArgs args = {};
-    fill_args(args, type, w, rows, inner);
+    type = fill_args(args, type, w, rows, inner);
     args.m = count;
     args.out = out;
     args.ldc = ldo;
@@ -586,7 +618,7 @@ hipError_t launch_gguf_gemv(int type, const uint8_t *w, int64_t rows, int64_t in
                             void *out, int64_t ldc, int out_dtype, const void *residual, int64_t m,
                             hipStream_t stream, int hs, int vph) {
     GgufNativeArgs args = {};
-    fill_args(args, type, w, rows, inner);
+    type = fill_args(args, type, w, rows, inner);
     args.hs = hs;
     args.vph = vph;
     args.a = a;

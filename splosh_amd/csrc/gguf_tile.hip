@@ -36,6 +36,7 @@ struct GgufTileArgs {
     const uint8_t *w;          // native blocks (rows back to back), or plane0 for Q5_K / Q4_K
     const uint8_t *plane1, *meta;
     uint32_t w_bytes, row_bytes;
+    int rows32;                // native blocks in the ROWS32 order (gguf_row)
     int64_t n, inner;
     const uint16_t *a;
     int64_t lda;
@@ -104,7 +105,7 @@ __global__ void __launch_bounds__(256 * KH) gguf_tile_kernel(GgufTileArgs args) 
         if constexpr (kPlanes)
             st.w = fetch_plane_group(args.w, TYPE == 13 ? args.plane1 : nullptr, args.meta, args.inner, wcol, g);
         else
-            st.w = gguf_fetch<TYPE>(wr, (uint32_t)(wcol * args.row_bytes), (int)g);
+            st.w = gguf_fetch<TYPE>(wr, gguf_row<TYPE>((uint32_t)wcol, args.row_bytes, args.rows32), (int)g);
     };
     auto commit = [&](const Stage &st) {
 #pragma unroll
@@ -447,11 +448,12 @@ hipError_t launch_gguf_tile(int type, const uint8_t *w, const uint8_t *plane1, c
         const size_t room = workspace_bytes - kGtCounterBytes;
         args.partial_bytes = (uint32_t)(room < ((size_t)1 << 31) ? room : ((size_t)1 << 31));
     }
+    args.rows32 = gguf_layout(type);
     if (type != 13 && type != 12) {
         int elems = 0, bytes = 0;
         gguf_native_block(type, &elems, &bytes);
         args.row_bytes = (uint32_t)(inner / elems * bytes);
-        args.w_bytes = (uint32_t)(rows_w * (int64_t)args.row_bytes);
+        args.w_bytes = (uint32_t)((args.rows32 ? (rows_w + 31) / 32 * 32 : rows_w) * (int64_t)args.row_bytes);
     }
     switch (type) {
         case 8: return launch_gt_rows<8>(args, stream);

@@ -93,8 +93,16 @@ hipError_t launch_q4_mma(const MmaPlan &plan, const splosh_q4_weight &w, const s
                          const uint16_t *a, int64_t lda, void *out, int64_t ldc, int out_dtype, const void *residual,
                          int64_t rows, void *workspace, hipStream_t stream, const EmitOperand *emit = nullptr);
 
-// GGUF Q8_0 / Q6_K / IQ4_NL / IQ4_XS in native blocks (gguf_native.hip).
+// GGUF Q8_0 / Q6_K / IQ4_NL / IQ4_XS in native blocks (gguf_native.hip). The launchers below
+// take the type id with the layout flag (SPLOSH_GGUF_ROWS32) and split it with gguf_layout.
 int gguf_native_block(int type, int *elems, int *bytes);
+inline bool gguf_layout(int &type) {
+    const bool rows32 = (type & SPLOSH_GGUF_ROWS32) != 0;
+    type &= 0xFF;
+    return rows32;
+}
+hipError_t launch_gguf_repack_rows32(int type, const uint8_t *native, int64_t rows, int64_t inner, uint8_t *out,
+                                     hipStream_t stream);
 hipError_t launch_gguf_dequant(int type, const uint8_t *w, int64_t rows, int64_t inner, float *dense,
                                hipStream_t stream);
 hipError_t launch_gguf_embed(int type, const uint8_t *w, int64_t rows, int64_t inner, const uint32_t *tokens,

@@ -78,6 +78,7 @@ struct MmaArgs {
     // plane1 and meta; activations.
     uint32_t code_bytes, sidecar_bytes, meta_bytes, a_bytes;
     uint32_t row_bytes;  // GGUF native blocks: bytes of a weight row
+    int rows32;          // GGUF native blocks in the ROWS32 order (gguf_row)
     // The next RMSNorm's operand, emitted from the epilogue (single weight, fp32 output, N a multiple
     // of 64; null norm_weight: no emit): values = bf16(h norm_weight[col]), and per row and band of
     // 64 columns the sums of the rounded values and of h * h, h being the value written to `out`.
@@ -462,7 +463,7 @@ struct GgufFormat {
 
     rsrc_t rs;
     int kw, cw, r, h, ga, gb;
-    uint32_t row_off;
+    GgufRow row;
     GgufRaw<TYPE> raw[D];
     // The group being dequantized: its scales (zero when the step has no group for this wave) and
     // its code words in place.
@@ -483,14 +484,14 @@ struct GgufFormat {
         ga = ga_;
         gb = gb_;
         const int64_t ncol = (int64_t)band * kBandCols + cw * 32 + r;
-        row_off = (uint32_t)(ncol < args.n ? ncol : args.n - 1) * args.row_bytes;
+        row = gguf_row<TYPE>((uint32_t)(ncol < args.n ? ncol : args.n - 1), args.row_bytes, args.rows32);
     }
     __device__ void load_s(int, char *) {}
     __device__ void fetch_side(const char *) {}
     __device__ void load_w(int slot, int t) {
         const int b = ga + t < gb ? ga + t : gb - 1;
         const int ub = __builtin_amdgcn_readfirstlane(b);
-        raw[slot] = gguf_fetch<TYPE>(rs, row_off, 8 * ub + 2 * kw + h);
+        raw[slot] = gguf_fetch<TYPE>(rs, row, 8 * ub + 2 * kw + h);
     }
     __device__ void prepare(int slot, bool on) {
         const GgufRaw<TYPE> &w = raw[slot];
@@ -1400,7 +1401,7 @@ bool gguf_mma_fits(int type, int64_t rows, int64_t columns, int64_t inner, int64
     if (!gguf_native_block(type, &elems, &bytes)) return false;
     const int64_t limit = ((int64_t)1 << 32) - 256;
     return rows >= 1 && rows <= 64 && columns > 0 && inner >= 256 && inner % 256 == 0 &&
-           (rows * lda + inner) * 2 < limit && columns * (inner / elems) * bytes < limit;
+           (rows * lda + inner) * 2 < limit && (columns + 31) * (inner / elems) * bytes < limit;
 }
 
 hipError_t launch_gguf_mma(const MmaPlan &plan, int type, const uint8_t *native, int64_t columns, int64_t inner,
@@ -1409,12 +1410,13 @@ hipError_t launch_gguf_mma(const MmaPlan &plan, int type, const uint8_t *native,
     int elems = 0, bytes = 0;
     gguf_native_block(type, &elems, &bytes);
     MmaArgs args = {};
+    args.rows32 = gguf_layout(type);
     args.plane0 = native;
     args.n = columns;
     args.units = inner / 256;
     set_io(args, plan, a, lda, out, ldc, out_dtype, residual, rows, inner, workspace, false);
     args.row_bytes = (uint32_t)(inner / elems * bytes);
-    args.code_bytes = (uint32_t)(columns * args.row_bytes);
+    args.code_bytes = (uint32_t)((args.rows32 ? (columns + 31) / 32 * 32 : columns) * args.row_bytes);
     switch (type) {
         case 8: return launch_mma_fm<GgufFormat<8, kMmaCW, kMmaKW, kMmaDepth>>(plan, args, stream);
         case 20: return launch_mma_fm<GgufFormat<20, kMmaCW, kMmaKW, kMmaDepth>>(plan, args, stream);

@@ -40,6 +40,7 @@ struct PrefillArgs {
     const void *w[3];
     const void *u[3];   // fused gate+up: the up weight (same geometry as w)
     uint32_t w_bytes[3];
+    int rows32;         // GGUF native blocks in the ROWS32 order (gguf_row)
     int64_t n;          // weight rows = output columns
     int64_t groups;     // 64-element groups of K
     const uint16_t *a;
@@ -349,14 +350,14 @@ struct GgufStage {
     static constexpr int kLoads = 0, kNW = 1;
     static constexpr bool kEmit = false;
     rsrc_t r;
-    uint32_t row;
+    GgufRow row;
     int hh;
     GgufRaw<TYPE> raw[2];
     __device__ GgufStage(const PrefillArgs &args) { r = make_rsrc(args.w[0], args.w_bytes[0]); }
     __device__ void begin(const PrefillArgs &args, uint32_t col, int hh_) {
         hh = hh_;
         const uint32_t row_bytes = (uint32_t)(args.groups * 64 / GgufGeom<TYPE>::kElems * GgufGeom<TYPE>::kBytes);
-        row = col * row_bytes;
+        row = gguf_row<TYPE>(col, row_bytes, args.rows32);
     }
     __device__ void load(uint32_t g, int set) { raw[set] = gguf_fetch<TYPE>(r, row, (int)(2u * g) + hh); }
     // The whole part at q0 = 0 (the decoders produce all 32 values at once), nothing at q0 = 2.
@@ -750,7 +751,7 @@ bool gguf_prefill_fits(int type, int64_t rows, int64_t columns, int64_t inner, i
     int elems = 0, bytes = 0;
     if (!gguf_native_block(type, &elems, &bytes)) return false;
     return inner % 64 == 0 && inner % elems == 0 && prefill_fits(rows, columns, inner, lda, ldc) &&
-           columns * (inner / elems) * bytes < ((int64_t)1 << 32) - 256;
+           (columns + 31) * (inner / elems) * bytes < ((int64_t)1 << 32) - 256;
 }
 
 hipError_t launch_gguf_prefill(const PrefillPlan &plan, int type, const uint8_t *native, int64_t rows_w,
@@ -759,8 +760,9 @@ hipError_t launch_gguf_prefill(const PrefillPlan &plan, int type, const uint8_t 
     int elems = 0, bytes = 0;
     if (!gguf_native_block(type, &elems, &bytes)) return hipErrorInvalidValue;
     PrefillArgs args = {};
+    args.rows32 = gguf_layout(type);
     args.w[0] = native;
-    args.w_bytes[0] = (uint32_t)(rows_w * (inner / elems) * bytes);
+    args.w_bytes[0] = (uint32_t)((args.rows32 ? (rows_w + 31) / 32 * 32 : rows_w) * (inner / elems) * bytes);
 #define SPLOSH_GGUF_PREFILL(T) \
     launch_prefill<GgufStage<T>>(plan, args, rows_w, inner, a, lda, out, ldc, out_dtype, residual, rows, workspace, stream)
     switch (type) {

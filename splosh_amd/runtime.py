@@ -156,20 +156,46 @@ def _out(a, rows, n, out, out_dtype, stream=None):
 GGUF_NATIVE = {8: (32, 34), 11: (256, 110), 14: (256, 210), 20: (32, 18), 21: (256, 110), 23: (256, 136)}
 
 
+# splosh_gguf_gemm's layout flag: the ROWS32 order of the native blocks (splosh_gguf_repack_rows32).
+GGUF_ROWS32 = 0x100
+
+
 @dataclass
 class GgufWeight:
-    """A GGUF weight in the native blocks its file holds (rows x inner, rows back to back)."""
+    """A GGUF weight in native blocks (rows x inner): in the order its file holds them (rows back to
+    back), or with rows32=True in the ROWS32 order of gguf_repack_rows32 (the units of 256
+    elements of 32 consecutive rows interleaved, rows padded to a multiple of 32)."""
 
     native: torch.Tensor
     gguf_type: int
     rows: int
     inner: int
+    rows32: bool = False
 
     def __post_init__(self):
         if self.gguf_type not in GGUF_NATIVE:
             raise SploshError(13, f"ggml type {self.gguf_type} is not kept in native blocks")
         elems, size = GGUF_NATIVE[self.gguf_type]
-        _require(self.native, self.rows * (self.inner // elems) * size, "native")
+        stored = (self.rows + 31) // 32 * 32 if self.rows32 else self.rows
+        _require(self.native, stored * (self.inner // elems) * size, "native")
+
+    @property
+    def type_id(self):
+        """The type id the entry points take: the ggml id, with the layout flag for ROWS32."""
+        return self.gguf_type | (GGUF_ROWS32 if self.rows32 else 0)
+
+
+def gguf_repack_rows32(w, stream=None):
+    """splosh_gguf_repack_rows32: the same weight in the ROWS32 order (a new device tensor)."""
+    if w.rows32:
+        raise SploshError(2, "the weight is already in the ROWS32 order")
+    nbytes = _lib.lib().splosh_gguf_rows32_bytes(w.gguf_type, w.rows, w.inner)
+    if nbytes == 0:
+        raise SploshError(2, "no ROWS32 form for this type or shape (inner % 256 != 0)")
+    out = torch.empty(nbytes, dtype=torch.uint8, device=w.native.device)
+    _lib.check(_lib.lib().splosh_gguf_repack_rows32(w.gguf_type, _ptr(w.native), w.rows, w.inner, _ptr(out),
+                                                    _stream(stream)))
+    return GgufWeight(out, w.gguf_type, w.rows, w.inner, rows32=True)
 
 
 def workspace_bytes(rows, columns, inner):
@@ -237,11 +263,11 @@ def gemm(w, a, out=None, residual=None, out_dtype=torch.bfloat16, kernel=AUTO, r
     ws, ws_bytes = scratch
     if isinstance(w, GgufWeight):
         if key_heads:
-            st = _lib.lib().splosh_gguf_gemm_heads(w.gguf_type, _ptr(w.native), w.rows, w.inner, key_heads, _ptr(a),
+            st = _lib.lib().splosh_gguf_gemm_heads(w.type_id, _ptr(w.native), w.rows, w.inner, key_heads, _ptr(a),
                                                    a.stride(0), _ptr(out), out.stride(0), _dtype_code(out.dtype),
                                                    _ptr(residual), rows, ws, ws_bytes, _stream(stream))
         else:
-            st = _lib.lib().splosh_gguf_gemm(w.gguf_type, _ptr(w.native), w.rows, w.inner, _ptr(a), a.stride(0),
+            st = _lib.lib().splosh_gguf_gemm(w.type_id, _ptr(w.native), w.rows, w.inner, _ptr(a), a.stride(0),
                                              _ptr(out), out.stride(0), _dtype_code(out.dtype), _ptr(residual),
                                              rows, ws, ws_bytes, _stream(stream))
         _lib.check(st)
@@ -346,7 +372,7 @@ def dequant(w, out=None, stream=None):
         out = torch.empty((w.rows, w.inner), dtype=torch.float32, device=dev)
     _require(out, w.rows * w.inner * 4, "output")
     if isinstance(w, GgufWeight):
-        _lib.check(_lib.lib().splosh_gguf_dequant(w.gguf_type, _ptr(w.native), w.rows, w.inner, _ptr(out),
+        _lib.check(_lib.lib().splosh_gguf_dequant(w.type_id, _ptr(w.native), w.rows, w.inner, _ptr(out),
                                                   _stream(stream)))
         return out
     wc = w.c()
@@ -534,7 +560,7 @@ def embed(w, tokens, out=None, out_dtype=torch.float32, stream=None):
         out = torch.empty((count, w.inner), dtype=out_dtype, device=tokens.device)
     _require(out, ((count - 1) * out.stride(0) + w.inner) * out.element_size(), "output")
     if isinstance(w, GgufWeight):
-        _lib.check(_lib.lib().splosh_gguf_embed(w.gguf_type, _ptr(w.native), w.rows, w.inner, _ptr(tokens), count,
+        _lib.check(_lib.lib().splosh_gguf_embed(w.type_id, _ptr(w.native), w.rows, w.inner, _ptr(tokens), count,
                                                 _ptr(out), out.stride(0), _dtype_code(out.dtype), _stream(stream)))
         return out
     wc = w.c()

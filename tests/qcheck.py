@@ -84,3 +84,15 @@ def check_close(got, ref, *, bf16_out, tight=False, absref=None, label=""):
         worst = (diff - bound).max()
         assert worst <= 0, f"{label}: beyond the tight bound by {worst} (max rel {max_rel})"
     return max_rel, cos
+
+
+def rows32_order(native, gguf_type, rows, inner):
+    """The ROWS32 order of a native-block weight (numpy, host): the 256-element units of 32
+    consecutive rows interleaved, unit u of row n at ((n // 32) * units * 32 + u * 32 + n % 32) unit
+    bytes, rows padded with zeros to a multiple of 32."""
+    elems, size = oracle.GGUF_BLOCK[gguf_type]
+    ub, units = 256 // elems * size, inner // 256
+    r32 = (rows + 31) // 32 * 32
+    x = np.zeros((r32, units, ub), np.uint8)
+    x[:rows] = np.asarray(native, np.uint8).reshape(rows, units, ub)
+    return x.reshape(r32 // 32, 32, units, ub).transpose(0, 2, 1, 3).reshape(-1).copy()

@@ -79,6 +79,10 @@ def test_heads_gemm_native(gtype, m):
     got = to_f32(rt.gemm(w, bf16_tensor(a_bits), out_dtype=torch.float32, key_heads=16, workspace=ws))
     check_close(got, oracle.gemm_a_bf16_w_f32(a_file, dense), bf16_out=False, tight=True,
                 absref=abs_gemm(a_file, dense), label=f"heads type={gtype} m={m}")
+    # The same weight in the ROWS32 order: the same result, bit for bit.
+    got32 = to_f32(rt.gemm(rt.gguf_repack_rows32(w), bf16_tensor(a_bits), out_dtype=torch.float32, key_heads=16,
+                           workspace=ws))
+    assert np.array_equal(got, got32)
 
 
 @pytest.mark.parametrize("m", [1, 64])

@@ -120,6 +120,54 @@ def test_mma_kernel(rt, name, rows):
     check_close(got.cpu().numpy(), ref + res.cpu().numpy(), bf16_out=False, label=f"{name} mma residual rows={rows}")
 
 
+@pytest.mark.parametrize("name", list(TYPES))
+def test_rows32_repack_on_device(rt, name):
+    """splosh_gguf_repack_rows32 against the host restatement of the order, byte for byte (the
+    padding rows zero)."""
+    from qcheck import rows32_order
+    t = TYPES[name]
+    n, k = 203, 768
+    native = oracle.gguf_random_native(t, n, k, seed=81 + t)
+    w = rt.GgufWeight(torch.from_numpy(native).cuda(), t, n, k)
+    w32 = rt.gguf_repack_rows32(w)
+    assert w32.rows32 and w32.native.numel() == 224 * native.size // n
+    assert np.array_equal(w32.native.cpu().numpy(), rows32_order(native, t, n, k))
+
+
+@pytest.mark.parametrize("name", list(TYPES))
+def test_rows32_kernels_match_native(rt, name):
+    """Every kernel on the ROWS32 order gives what it gives on the file's order, bit for bit (the
+    same blocks decoded in the same order): the streaming kernel (1-8 rows), the stream-K MFMA
+    kernel (to 64), the tiled kernel (100), the prefill kernel (256), the dequant and the embedding
+    lookup; and the native results match the oracle."""
+    t = TYPES[name]
+    n, k = 256, 768
+    native = oracle.gguf_random_native(t, n - 53, k, seed=91 + t)
+    rows_w = n - 53  # 203 weight rows: a partial group of 32
+    w = rt.GgufWeight(torch.from_numpy(native).cuda(), t, rows_w, k)
+    w32 = rt.gguf_repack_rows32(w)
+    dense = oracle.gguf_decode(t, native).reshape(rows_w, k)
+    for rows in (1, 2, 4, 6, 8, 33, 64, 100):
+        a_bits = oracle.bf16_normal((rows, k), seed=rows + 97)
+        a = bf16_tensor(a_bits)
+        got = rt.gemm(w, a, out_dtype=torch.float32).cpu().numpy()
+        got32 = rt.gemm(w32, a, out_dtype=torch.float32).cpu().numpy()
+        assert np.array_equal(got, got32), f"{name} rows={rows}"
+        if rows in (2, 33):
+            check_close(got, oracle.gemm_a_bf16_w_f32(a_bits, dense), bf16_out=False, tight=True,
+                        absref=abs_gemm(a_bits, dense), label=f"{name} rows={rows}")
+    # The prefill kernel takes whole 128-column tiles: 256 weight rows.
+    native_p = oracle.gguf_random_native(t, n, k, seed=93 + t)
+    wp = rt.GgufWeight(torch.from_numpy(native_p).cuda(), t, n, k)
+    a = bf16_tensor(oracle.bf16_normal((256, k), seed=98))
+    assert np.array_equal(rt.gemm(wp, a, out_dtype=torch.float32).cpu().numpy(),
+                          rt.gemm(rt.gguf_repack_rows32(wp), a, out_dtype=torch.float32).cpu().numpy())
+    assert np.array_equal(rt.dequant(w32).cpu().numpy().view(np.uint32), dense.view(np.uint32))
+    tokens = torch.tensor([0, 31, 32, 202, 77, 203], dtype=torch.int32, device="cuda")  # 203: past the table
+    assert np.array_equal(rt.embed(w, tokens, out_dtype=torch.float32).cpu().numpy(),
+                          rt.embed(w32, tokens, out_dtype=torch.float32).cpu().numpy())
+
+
 def test_q8_0_one_row_long_k(rt):
     """Q8_0 at one row with K = 33792, past the 32768 whose activation row fits the LDS: the fp32
     decode kernel reading the activations from memory, against the oracle."""
