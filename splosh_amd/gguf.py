@@ -309,12 +309,13 @@ def dense_bf16(values, unit=1, head_order=None, negated_log=False, heads=GDN_VAL
     return out
 
 
-def load_weight(f, name, device="cuda", full_attention=False):
+def load_weight(f, name, device="cuda", full_attention=False, rows32=False):
     """A packed matrix [rows, inner] on the device in the form its kernels read: Q4_K / Q5_K as planes
     (GgufPlanes.repack on the GPU), the other formats in their native blocks, a float type as Q8_0
     blocks; a gated-delta layer's head-ordered rows in the engine's order (GgufConvert.ggufPlanes,
     GgufConvert.swift:370-430). Planes round the rows up to whole tiles by zero blocks
-    (GgufConvert.swift:259-262)."""
+    (GgufConvert.swift:259-262). rows32=True puts native blocks in the ROWS32 order
+    (runtime.gguf_repack_rows32; faster from about 16 activation rows) where inner % 256 == 0."""
     import torch
     from . import runtime as rt
     t = f.tensor(name)
@@ -334,7 +335,8 @@ def load_weight(f, name, device="cuda", full_attention=False):
         elems, size = rt.GGUF_NATIVE[gtype]
         if order is not None:
             native = order_rows(native, t.rows, t.inner // elems * size, order)
-        return rt.GgufWeight(torch.from_numpy(np.ascontiguousarray(native)).to(device), gtype, t.rows, t.inner)
+        w = rt.GgufWeight(torch.from_numpy(np.ascontiguousarray(native)).to(device), gtype, t.rows, t.inner)
+        return rt.gguf_repack_rows32(w) if rows32 and t.inner % 256 == 0 else w
     if t.type not in (Q4_K, Q5_K):
         raise GgufError(f"tensor {name} has ggml type {t.type}; the device kernels take Q4_K, Q5_K, Q3_K, "
                         "Q6_K, Q8_0, IQ4_NL, IQ3_S and IQ4_XS")

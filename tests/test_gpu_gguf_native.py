@@ -288,6 +288,10 @@ def test_from_gguf_file(rt, tmp_path):
         got = rt.gemm(w, bf16_tensor(a_bits), out_dtype=torch.float32)
         check_close(got.cpu().numpy(), oracle.gemm_a_bf16_w_f32(a_bits, dense[name]), bf16_out=False, tight=True,
                     absref=abs_gemm(a_bits, dense[name]), label=f"file {name}")
+        w32 = gguf.load_weight(f, f"blk.0.{name}.weight", rows32=True)
+        assert w32.rows32 and (w32.rows, w32.inner) == (n, k)
+        assert np.array_equal(rt.gemm(w32, bf16_tensor(a_bits), out_dtype=torch.float32).cpu().numpy(),
+                              got.cpu().numpy())
 
 
 def test_rejects_other_types_and_bad_shapes(rt):
