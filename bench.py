@@ -48,9 +48,9 @@ MEASURED_TRAFFIC = {
     ("iq3s64", "gguf"): 30858.2 * 2 * 1024 + 4174.7 * 1024,  # mma_kernel<GgufFormat<21, 2, 4, 3>, 2, 2, 4, 3>
     ("q6k64r", "gguf"): 47010.9 * 2 * 1024 + 4340.4 * 1024,  # the same, Q6_K in the ROWS32 order
     ("q80_64r", "gguf"): 57538.1 * 2 * 1024 + 4337.7 * 1024,  # mma_kernel<GgufFormat<8, 2, 4, 3>, 2, 2, 4, 3>, ROWS32
-    ("q6k1", "gguf"): 36191.3 * 2 * 1024 + 10.0 * 1024,  # gguf_pairs_kernel<14, 4, 2>
-    ("q3k1", "gguf"): 19009.8 * 2 * 1024 + 10.0 * 1024,  # gguf_pairs_kernel<11, 4, 2>
-    ("iq3s1", "gguf"): 19068.8 * 2 * 1024 + 10.0 * 1024,  # gguf_pairs_kernel<21, 4, 2>
+    ("q6k1", "gguf"): 36194.4 * 2 * 1024 + 10.0 * 1024,  # gguf_pairs_kernel<14, 4, 2, 0>
+    ("q3k1", "gguf"): 19023.7 * 2 * 1024 + 10.0 * 1024,  # gguf_pairs_kernel<11, 4, 2, 0>
+    ("iq3s1", "gguf"): 19064.2 * 2 * 1024 + 10.0 * 1024,  # gguf_pairs_kernel<21, 4, 2, 0>
     ("q80_1", "gguf"): 46754.4 * 2 * 1024 + 10.0 * 1024,  # gguf_pairs_kernel<8, 4, 2, 2>
     ("q80_4", "gguf"): 47196.6 * 2 * 1024 + 40.0 * 1024,  # gguf_pairs_kernel<8, 4, 2, 1>
     ("q6k4", "gguf"): 36625.1 * 2 * 1024 + 40.0 * 1024,  # gguf_pairs_kernel<14, 4, 2, 1>
