@@ -182,12 +182,18 @@ int q4_gemm_impl(const splosh_q4_weight *w, const splosh_q4_weight *up, const ui
                               "q4 scalar launch");
         case SPLOSH_KERNEL_DEQUANT: {
             if (!mma_ok) return fail(SPLOSH_ERR_UNSUPPORTED, "dequant kernel needs rows <= 64 and aligned operands");
-            const splosh::MmaPlan plan =
-                splosh::plan_mma(rows, w->rows, w->inner / kGroupSize, up != nullptr, workspace ? workspace_bytes : 0);
             // The emit epilogue only when asked for by name: under AUTO the GEMM plus the separate
             // pass is the faster of the two at these row counts.
             const splosh::EmitOperand *mma_emit = kernel == SPLOSH_KERNEL_DEQUANT ? emit : nullptr;
             if (emitted) *emitted = mma_emit != nullptr;
+            // A wide single weight: its two column halves as a pair.
+            const bool split = !up && !mma_emit && splosh::mma_split(*w);
+            const splosh::MmaPlan plan = splosh::plan_mma(rows, split ? w->rows / 2 : w->rows, w->inner / kGroupSize,
+                                                          up != nullptr || split, workspace ? workspace_bytes : 0);
+            if (split)
+                return hip_status(splosh::launch_q4_mma_split(plan, *w, a, lda, out, ldc, out_dtype, residual, rows,
+                                                              workspace, stream),
+                                  "q4 mma launch");
             return hip_status(splosh::launch_q4_mma(plan, *w, up, a, lda, out, ldc, out_dtype, residual, rows,
                                                     workspace, stream, mma_emit),
                               "q4 mma launch");

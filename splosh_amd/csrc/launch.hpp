@@ -129,6 +129,13 @@ hipError_t launch_gguf_gemv(int type, const uint8_t *w, int64_t rows, int64_t in
                             void *out, int64_t ldc, int out_dtype, const void *residual, int64_t m,
                             hipStream_t stream, int hs = -1, int vph = 0);
 
+// One wide weight as the pair of its column halves (plan: columns / 2, mlp = true), where
+// mma_split says it pays.
+bool mma_split(const splosh_q4_weight &w);
+hipError_t launch_q4_mma_split(const MmaPlan &plan, const splosh_q4_weight &w, const uint16_t *a, int64_t lda,
+                               void *out, int64_t ldc, int out_dtype, const void *residual, int64_t rows,
+                               void *workspace, hipStream_t stream);
+
 // The same kernel over Q5_K planes; the plan's units are 256-element blocks.
 bool q5k_mma_fits(int64_t rows, int64_t columns, int64_t inner, int64_t lda);
 hipError_t launch_q5k_mma(const MmaPlan &plan, const splosh_q5k_weight &w, const uint16_t *a, int64_t lda, void *out,

@@ -116,11 +116,17 @@ struct MmaArgs {
 //
 // GROUPED (one tiled weight a band, of a grouped call): each job takes its band's weight, buffer
 // resources and column offset from the group table.
-template <int NW_, bool TILED, int CW, int KW, int D, bool GROUPED = false, bool EMIT = false>
+//
+// SPLIT (NW = 2): one weight's two column halves as the pair -- rows [0, n) and [n, 2n) of the
+// weight, the epilogue storing each half's sums to its own columns (no silu): half the jobs of a
+// wide weight, each over twice the columns of one activation chunk.
+template <int NW_, bool TILED, int CW, int KW, int D, bool GROUPED = false, bool EMIT = false, bool SPLIT = false>
 struct Q4Format {
     static_assert(!GROUPED || (NW_ == 1 && TILED), "grouped calls take single tiled weights");
+    static_assert(!SPLIT || NW_ == 2, "a split weight runs as a pair");
     static constexpr bool kGrouped = GROUPED;
     static constexpr bool kEmit = EMIT && !GROUPED;  // the epilogue emits the next norm's operand
+    static constexpr bool kSplit = SPLIT;
     static constexpr int kTblBytes = 0;
     __device__ void build_table(char *, int) {}
     static constexpr int NW = NW_;
@@ -295,6 +301,7 @@ template <int CW, int KW, int D, bool FIFTH = true>
 struct Q5Format {
     static constexpr bool kGrouped = false;
     static constexpr bool kEmit = false;
+    static constexpr bool kSplit = false;
     static constexpr int NW = 1;
     // The fifth bits of a plane1 byte x (four codes' worth for each of the two code words it
     // serves) at bit 4 of each byte: entry x = {((x & 0x33) * 0x880110) & 0x10101010, the same
@@ -434,6 +441,7 @@ template <int TYPE, int CW, int KW, int D>
 struct GgufFormat {
     static constexpr bool kGrouped = false;
     static constexpr bool kEmit = false;
+    static constexpr bool kSplit = false;
     static constexpr int NW = 1;
     // IQ3_S: the codebook's four magnitudes of each of its 512 entries as bytes, in LDS.
     static constexpr int kTblBytes = TYPE == 21 ? 512 * 4 : 0;
@@ -925,6 +933,28 @@ mma_kernel(MmaArgs args) {
             band -= args.gband[gi];
         }
         const int64_t ocol = (int64_t)band * S::kBandCols + bcol;
+        if constexpr (F::kSplit) {
+            // Half w's columns start at w n.
+#pragma unroll
+            for (int w = 0; w < 2; ++w)
+#pragma unroll
+                for (int f = 0; f < FM; ++f)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int m = own_row(f, i);
+                        if (m >= rows || ocol >= n) continue;
+                        const int64_t index = (int64_t)m * ldc + ocol + w * n;
+                        float value = v[w][f][i];
+                        if (args.out_dtype == SPLOSH_F32) {
+                            if (args.residual) value += ((const float *)args.residual)[index];
+                            ((float *)out)[index] = value;
+                        } else {
+                            if (args.residual) value += bf16_bits_to_f32(((const uint16_t *)args.residual)[index]);
+                            ((uint16_t *)out)[index] = f32_to_bf16(value);
+                        }
+                    }
+            return;
+        }
         float hv[FM][4];
 #pragma unroll
         for (int f = 0; f < FM; ++f)
@@ -1289,8 +1319,8 @@ static hipError_t launch_mma_fm(const MmaPlan &p, const MmaArgs &args, hipStream
 
 // EMIT: a build with the emit epilogue, kept apart so that its registers do not weigh on the
 // kernel without it.
-template <int NW, bool TILED, bool GROUPED = false, bool EMIT = false>
-using Q4F = Q4Format<NW, TILED, kMmaCW, kMmaKW, kMmaDepth, GROUPED, EMIT>;
+template <int NW, bool TILED, bool GROUPED = false, bool EMIT = false, bool SPLIT = false>
+using Q4F = Q4Format<NW, TILED, kMmaCW, kMmaKW, kMmaDepth, GROUPED, EMIT, SPLIT>;
 
 static void set_io(MmaArgs &args, const MmaPlan &plan, const uint16_t *a, int64_t lda, void *out, int64_t ldc,
                    int out_dtype, const void *residual, int64_t rows, int64_t inner, void *workspace, bool mlp) {
@@ -1343,6 +1373,43 @@ hipError_t launch_q4_mma(const MmaPlan &plan, const splosh_q4_weight &w, const s
     else
         err = tiled ? launch_mma_fm<Q4F<1, true>>(plan, args, stream) : launch_mma_fm<Q4F<1, false>>(plan, args, stream);
     return err;
+}
+
+// A wide single weight runs as the pair of its column halves (Q4Format SPLIT): from two bands a
+// CU, so that every workgroup has at least two jobs and halving them saves their fixed cost.
+// Measured at M=64 (M=16): K5120 N=248320 285 -> 242 us (226 -> 196), N=65536 75 -> 67 (61 ->
+// 55), N=34816 50 -> 47 (42 -> 40), K17408 N=34816 124 -> 115 (101 -> 90), K2048 N=131072 73 -> 63;
+// N=49152 (three jobs a CU) within the spread. Below two bands a CU (N=17408) the pair's longer
+// step costs more than the job it saves. The halves start on a 128-row tile (tiled) or a row.
+bool mma_split(const splosh_q4_weight &w) {
+    const int64_t bands = (w.rows + kMmaCW * 32 - 1) / (kMmaCW * 32);
+    const bool halves = w.order == SPLOSH_Q4_TILED128 ? w.rows % 256 == 0 : w.rows % 2 == 0;
+    return halves && bands >= 2 * (int64_t)device_cus();
+}
+
+hipError_t launch_q4_mma_split(const MmaPlan &plan, const splosh_q4_weight &w, const uint16_t *a, int64_t lda,
+                               void *out, int64_t ldc, int out_dtype, const void *residual, int64_t rows,
+                               void *workspace, hipStream_t stream) {
+    MmaArgs args = {};
+    const int64_t half = w.rows / 2, groups = w.inner / kGroup;
+    const bool tiled = w.order == SPLOSH_Q4_TILED128;
+    // Row `half`'s first record: tiled, (half / 128) G 128 records of 8 words; row-major, half rows.
+    const int64_t rec = tiled ? half / 128 * groups * 128 : half * groups;
+    const int64_t words = tiled ? rec * 8 : half * w.row_stride_words;
+    args.packed[0] = w.packed;
+    args.scales[0] = w.scales;
+    args.biases[0] = w.biases;
+    args.packed[1] = w.packed + words;
+    args.scales[1] = w.scales + rec;
+    args.biases[1] = w.biases + rec;
+    args.stride_words = w.row_stride_words;
+    args.n = half;
+    args.units = groups;
+    set_io(args, plan, a, lda, out, ldc, out_dtype, residual, rows, w.inner, workspace, true);
+    args.code_bytes = (uint32_t)(tiled ? half * groups * 32 : half * w.row_stride_words * 4);
+    args.sidecar_bytes = (uint32_t)(half * groups * 2);
+    return tiled ? launch_mma_fm<Q4F<2, true, false, false, true>>(plan, args, stream)
+                 : launch_mma_fm<Q4F<2, false, false, false, true>>(plan, args, stream);
 }
 
 // Several tiled weights of one inner size on one activation (the reference's concurrent encoder of

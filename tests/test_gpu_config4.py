@@ -49,6 +49,47 @@ def test_lm_head_sampled(rt, rows):
     torch.cuda.empty_cache()
 
 
+@pytest.mark.parametrize("order", ["tiled", "rowmajor"])
+@pytest.mark.parametrize("rows", [8, 33, 64])
+def test_wide_weight_as_split_pair(rt, order, rows):
+    """A single weight with at least four bands of 64 columns a CU runs as the pair of its column
+    halves (rows [0, N/2) and [N/2, N) of the weight through the fused-pair kernel, each half's sums
+    stored to its own columns). N = 66048: sampled columns of both halves, and the columns next to
+    the seam, against the oracle; with a workspace (stream-K) and without (whole bands); bf16 and
+    fp32 out with a residual."""
+    n, k = 66048, 512
+    g = k // 64
+    if order == "tiled":
+        w = _full_size_weight(rt, n, k, seed=400 + rows)
+    else:
+        gen = torch.Generator(device="cuda").manual_seed(401 + rows)
+        stride = 64  # 512 codes a row = 256 bytes, a whole number of 128-byte lines
+        packed = torch.randint(-2**31, 2**31, (n * stride,), dtype=torch.int64, device="cuda", generator=gen).to(torch.int32)
+        scales = (torch.randn(n * g, device="cuda", generator=gen) * 0.02).abs().to(torch.bfloat16).view(torch.int16)
+        biases = (torch.randn(n * g, device="cuda", generator=gen) * 0.01).to(torch.bfloat16).view(torch.int16)
+        w = rt.Q4Weight(packed, scales, biases, n, k, rt.ROW_MAJOR, stride)
+    a_bits = oracle.bf16_normal((rows, k), seed=402 + rows)
+    half = n // 2
+    cols = np.unique(np.concatenate([np.random.default_rng(rows).choice(n, 256, replace=False),
+                                     np.arange(half - 3, half + 3), [0, n - 1]]))
+    if order == "tiled":
+        ref, absref = _sampled_reference(w, a_bits, cols)
+    else:
+        words = w.packed.cpu().numpy().view(np.uint32).reshape(n, -1)
+        sc = w.scales.cpu().numpy().view(np.uint16).reshape(n, g)
+        bi = w.biases.cpu().numpy().view(np.uint16).reshape(n, g)
+        dense = oracle.q4_dequant_rowmajor(words[cols], words.shape[1], sc[cols], bi[cols], len(cols), k)
+        ref, absref = oracle.gemm_a_bf16_w_f32(a_bits, dense), abs_gemm(a_bits, dense)
+    a = bf16_tensor(a_bits)
+    for ws in (None, torch.empty(0, dtype=torch.uint8, device="cuda")):
+        got = to_f32(rt.gemm(w, a, workspace=ws))
+        check_close(got[:, cols], ref, bf16_out=True, tight=True, absref=absref,
+                    label=f"split {order} rows={rows} split-K={ws is None}")
+    res = torch.from_numpy(oracle.bf16_normal((rows, n), seed=403).astype(np.float32)).cuda()
+    got = rt.gemm(w, a, out=res.clone(), out_dtype=torch.float32, residual=res).cpu().numpy()
+    check_close(got[:, cols], ref + res.cpu().numpy()[:, cols], bf16_out=False, label=f"split {order} residual")
+
+
 @pytest.mark.parametrize("rows", [8, 64])
 def test_fused_gate_up_full_size_auto(rt, rows):
     """Config 1's fused gate+up (K=5120 -> 2 x 17408) through AUTO (the stream-K MFMA kernel the
