@@ -66,11 +66,12 @@ typedef enum splosh_dtype { SPLOSH_F32 = 0, SPLOSH_BF16 = 1 } splosh_dtype;
 typedef enum splosh_kernel {
     SPLOSH_KERNEL_AUTO = 0,     /* 1..4 rows of tiled weights whose staged activation rows fit 80 KB
                                    (one or two rows up to K of about 18700, four up to about 9100):
-                                   STREAM; else up to 64:
-                                   DEQUANT; more: PREFILL for tiled
-                                   weights with lda % 8 == 0 and ldc % 4 == 0 (one weight at 65..128
-                                   rows: TILE up to 80 rows or 8192 columns), else TILE; SCALAR for
-                                   operands no other kernel takes */
+                                   STREAM; else up to 64: DEQUANT (a single weight of at least two
+                                   64-column bands a CU as the pair of its column halves); 65..128:
+                                   rows 0..63 and the rest as two calls of the above (without the
+                                   emit); more: PREFILL for tiled weights with lda % 8 == 0 and
+                                   ldc % 4 == 0, else TILE; SCALAR for operands no other kernel
+                                   takes */
     SPLOSH_KERNEL_STREAM = 1,   /* weight streaming on raw codes: the every-CU decode kernel for
                                    1-4 rows of tiled weights (with a workspace it splits the last
                                    round of row blocks over K, so every CU gets the same share),
@@ -209,8 +210,8 @@ int splosh_q4_gemm_group(const splosh_q4_weight *weights, int count, const uint1
 
 /* Engine.mlpIn(gate:up:input:output:scratch:rows:) (Runtime/Engine.swift:1911-1966) with the
  * fused lane form sp_mlp_in_tiled_* (Shaders/engine.metal:1987-2055): out = silu(gate(a)) * up(a),
- * both weights read in one pass over a. AUTO as splosh_q4_gemm: above 64 rows, tiled weights take
- * the prefill kernel with both weights in each tile. */
+ * both weights read in one pass over a. AUTO as splosh_q4_gemm: 65..128 rows as two calls of at most 64,
+ * above that tiled weights take the prefill kernel with both weights in each tile. */
 int splosh_q4_mlp_in(const splosh_q4_weight *gate, const splosh_q4_weight *up, const uint16_t *a,
                      int64_t lda, void *out, int64_t ldc, int out_dtype, int64_t rows, int kernel,
                      void *workspace, size_t workspace_bytes, hipStream_t stream);

@@ -102,6 +102,22 @@ int q4_gemm_impl(const splosh_q4_weight *w, const splosh_q4_weight *up, const ui
     const bool eligible = q4_stream_eligible(*w, a, lda) && (!up || q4_stream_eligible(*up, a, lda));
     const bool wide16 = eligible && aligned(w->packed, 16) && (!up || aligned(up->packed, 16)) &&
                         (w->order == SPLOSH_Q4_TILED128 || w->row_stride_words % 4 == 0);
+    // 65..128 rows under AUTO: rows 0..63 and the rest as two calls of the M <= 64 kernels, one after
+    // the other on the stream (the workspace's counters are zero again between them). Measured at
+    // K5120 -> 2 x N17408 (gate+up) and K17408 -> N5120, against the one call on the tile or
+    // prefill kernel: gate+up M=65 91 -> 60 us, M=96 94 -> 72, M=128 97 -> 80; down M=65 54 -> 38,
+    // M=96 55 -> 47, M=128 58 -> 51; at 192 rows three calls lose (120 against 104 us).
+    if (kernel == SPLOSH_KERNEL_AUTO && !emit && rows > 64 && rows <= 128 && wide16 &&
+        splosh::mma_fits(64, w->rows, w->inner, w->row_stride_words, lda)) {
+        const char *res = (const char *)residual;
+        const size_t esize = out_dtype == SPLOSH_F32 ? 4 : 2;
+        if ((st = q4_gemm_impl(w, up, a, lda, out, ldc, out_dtype, residual, 64, kernel, workspace, workspace_bytes,
+                               stream)))
+            return st;
+        return q4_gemm_impl(w, up, a + 64 * lda, lda, (char *)out + 64 * ldc * esize, ldc, out_dtype,
+                            res ? res + 64 * ldc * esize : nullptr, rows - 64, kernel, workspace, workspace_bytes,
+                            stream);
+    }
     const bool tile_ok = wide16 && splosh::tile_fits(rows, w->rows, lda, w->row_stride_words);
     const bool mma_ok = wide16 && splosh::mma_fits(rows, w->rows, w->inner, w->row_stride_words, lda);
     const bool prefill_ok = wide16 && !up && w->order == SPLOSH_Q4_TILED128 && aligned(out, 16) &&
@@ -376,7 +392,8 @@ size_t splosh_workspace_bytes(int64_t rows, int64_t columns, int64_t inner) {
     if (rows <= 0 || columns <= 0 || inner < kGroupSize) return 0;
     const int64_t groups = inner / kGroupSize;
     const size_t tile = splosh::tile_workspace_bytes(rows, columns, groups, true);
-    const size_t mma = rows <= 64 ? splosh::mma_workspace_bytes(rows, columns, groups, true) : 0;
+    // (65..128 rows run as two calls of at most 64 rows.)
+    const size_t mma = rows <= 128 ? splosh::mma_workspace_bytes(rows < 64 ? rows : 64, columns, groups, true) : 0;
     // (2 columns: the fused gate+up plans its tiles over both weights' columns.)
     const size_t prefill = rows > 64 && columns % 128 == 0 ? splosh::prefill_workspace_bytes(rows, 2 * columns, groups) : 0;
     const size_t gguf = inner % 64 == 0 ? splosh::gguf_tile_workspace_bytes(rows, columns, inner) : 0;

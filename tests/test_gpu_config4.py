@@ -118,10 +118,11 @@ def test_workspace_shared_across_shapes(rt):
     need = max(rt.workspace_bytes(r, n, k) for r in (8, 64, 96) for n, k in ((2176, 5120), (640, 4352)))
     assert need > 0
     ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
-    # 96 rows: one tiled weight and a row-major pair go to the split-K tile kernel, whose partials
-    # must stay clear of the counters the M <= 64 calls after it rely on.
-    seq = [("mlp", 8), ("gemm", 64), ("q5k", 64), ("gemm", 96), ("mlp", 64), ("mlp_rm", 96), ("gemm", 8),
-           ("q5k", 16), ("mlp", 8), ("gemm", 64)]
+    # 96 rows: under AUTO two calls of the M <= 64 kernel (64 + 32 rows) on the one workspace; by
+    # name, the split-K tile kernel, whose partials must stay clear of the counters the M <= 64
+    # calls after it rely on.
+    seq = [("mlp", 8), ("gemm", 64), ("q5k", 64), ("gemm", 96), ("mlp", 64), ("mlp_rm", 96), ("gemm_tile", 96),
+           ("mlp_tile", 96), ("gemm", 8), ("q5k", 16), ("mlp", 8), ("gemm", 64)]
     for kind, rows in seq:
         k = 5120 if kind.startswith("mlp") else 4352
         a_bits = oracle.bf16_normal((rows, k), seed=rows + len(kind))
@@ -132,9 +133,15 @@ def test_workspace_shared_across_shapes(rt):
         elif kind == "mlp_rm":
             ref = oracle.silu_mul(oracle.gemm_a_bf16_w_f32(a_bits, gate.dense), oracle.gemm_a_bf16_w_f32(a_bits, up.dense))
             run = lambda: rt.mlp_in(gate.w_rm, up.w_rm, a, out_dtype=torch.float32, workspace=ws)
+        elif kind == "mlp_tile":
+            ref = oracle.silu_mul(oracle.gemm_a_bf16_w_f32(a_bits, gate.dense), oracle.gemm_a_bf16_w_f32(a_bits, up.dense))
+            run = lambda: rt.mlp_in(gate.w_tiled, up.w_tiled, a, out_dtype=torch.float32, workspace=ws, kernel=rt.TILE)
         elif kind == "gemm":
             ref = oracle.gemm_a_bf16_w_f32(a_bits, single.dense)
             run = lambda: rt.gemm(single.w_tiled, a, out_dtype=torch.float32, workspace=ws)
+        elif kind == "gemm_tile":
+            ref = oracle.gemm_a_bf16_w_f32(a_bits, single.dense)
+            run = lambda: rt.gemm(single.w_tiled, a, out_dtype=torch.float32, workspace=ws, kernel=rt.TILE)
         else:
             ref = oracle.gemm_a_bf16_w_f32(a_bits, dense5)
             run = lambda: rt.gemm(w5, a, out_dtype=torch.float32, workspace=ws)

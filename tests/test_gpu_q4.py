@@ -193,8 +193,9 @@ def test_mlp_in_fused(rt, kernel, rows):
 @pytest.mark.parametrize("rows,n,k", [(65, 384, 576), (300, 256, 640), (513, 128, 64)])
 @pytest.mark.parametrize("split", [True, False])
 def test_mlp_in_prefill(rt, rows, n, k, split):
-    """Fused gate+up through the prefill kernel (AUTO above 64 rows for tiled weights): tiles of 128
-    columns of each weight, silu(g) * u in the epilogue and in the stream-K finish pass, ragged rows."""
+    """Fused gate+up through the prefill kernel (AUTO above 128 rows for tiled weights; 65..128 rows
+    run as two calls of the M <= 64 kernel): tiles of 128 columns of each weight, silu(g) * u in the
+    epilogue and in the stream-K finish pass, ragged rows."""
     gate, up = Q4Case(n, k, seed=60 + rows), Q4Case(n, k, seed=61 + rows)
     a_bits = oracle.bf16_normal((rows, k), seed=62 + rows)
     g = oracle.gemm_a_bf16_w_f32(a_bits, gate.dense)
@@ -207,7 +208,11 @@ def test_mlp_in_prefill(rt, rows, n, k, split):
         check_close(to_f32(got), ref, bf16_out=out_dtype == torch.bfloat16,
                     label=f"mlp prefill {rows}x{n}x{k} split={split} {out_dtype}")
         auto = rt.mlp_in(gate.w_tiled, up.w_tiled, bf16_tensor(a_bits), out_dtype=out_dtype, workspace=ws)
-        assert torch.equal(auto, got), "AUTO takes the prefill kernel above 64 rows"
+        if rows > 128:
+            assert torch.equal(auto, got), "AUTO takes the prefill kernel above 128 rows"
+        else:
+            check_close(to_f32(auto), ref, bf16_out=out_dtype == torch.bfloat16,
+                        label=f"mlp auto (two M <= 64 calls) {rows}x{n}x{k} split={split} {out_dtype}")
 
 
 def test_workspace_shared_by_prefill_and_split_k(rt):

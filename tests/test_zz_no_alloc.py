@@ -55,8 +55,9 @@ SCRATCH_BYTES = 16384 + (8 << 20)
 
 @pytest.mark.parametrize("rows,n,k", [(100, 1024, 4352), (300, 640, 2048), (1, 17408, 1024), (2, 16896, 512)])
 def test_noalloc_planned_against_scratch(rows, n, k):
-    """Every kernel plans against the scratch's size: above 64 rows the split-K tile kernel (100
-    rows) and the prefill kernel (300), whose partials fit it or run unsplit; at one or two rows
+    """Every kernel plans against the scratch's size: at 100 rows two calls of the M <= 64 kernel
+    (64 + 36 rows, one after the other on the scratch), at 300 the prefill kernel, whose partials
+    fit it or run unsplit; at one or two rows
     the decode kernel, whose last round of row blocks is split over K in the scratch (544 and 528
     blocks on 256 CUs). The same call through splosh_q4_gemm with a zero-filled workspace of that
     size gives the same bits; both against the oracle. Run twice, so that the second call sees the
