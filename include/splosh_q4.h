@@ -240,7 +240,8 @@ int splosh_untile128(const void *src, void *dst, int64_t rows, int64_t groups, i
 /* Engine.gemm on a GGUF weight (Runtime/Engine.swift:1671-1697, kernels
  * Shaders/engine_gguf.metal:82-221 instantiated _q5k at :332-349). AUTO: one row takes the
  * every-CU decode kernel; 2..64 rows the dequant-to-bf16 MFMA kernel (DEQUANT; lda % 8 == 0 and
- * 16-byte aligned activations); more rows the 256 x 256 prefill kernel (PREFILL; also ldc % 4 == 0
+ * 16-byte aligned activations), 65..128 rows two calls of at most 64; more rows the 256 x 256
+ * prefill kernel (PREFILL; also ldc % 4 == 0
  * and 16-byte aligned outputs), else the LDS-tiled kernel (TILE), else the streaming kernel
  * (STREAM). DEQUANT and PREFILL use a workspace of splosh_workspace_bytes(rows, w->rows, w->inner)
  * to split K. Odd alignments fall back to SCALAR. */
@@ -310,8 +311,9 @@ int splosh_q4k_dequant(const splosh_q5k_weight *w, float *out, hipStream_t strea
  *
  * splosh_gguf_gemm: out[m][n] = sum_k a[m][k] w[n][k] (+ residual). Up to a few activation rows
  * (IQ4_NL 3, Q3_K 6, the others 4) a streaming kernel reads the weight once. Up to 64 rows
- * (inner % 256 == 0) the stream-K MFMA kernel of splosh_q4_gemm decodes each weight group once
- * (where it does not fit, the streaming kernel serves up to eight rows). Above that an LDS-tiled
+ * (inner % 256 == 0) the stream-K MFMA kernel of splosh_q4_gemm decodes each weight group once,
+ * and 65..128 rows run as two such calls but for Q3_K (where it does not fit, the streaming kernel
+ * serves up to eight rows). Above that an LDS-tiled
  * MFMA kernel (inner % 64 == 0) decodes each weight group once per 64 or 128 activation rows. From 256
  * rows (rows % 128 == 0, ldc % 4 == 0, 16-byte aligned outputs) the 256 x 256 prefill kernel
  * decodes each group once per 256 rows. The MFMA kernels split K over workgroups when their work

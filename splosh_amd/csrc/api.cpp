@@ -607,6 +607,19 @@ static int gguf_gemm(const splosh_q5k_weight *w_in, bool fifth, const uint16_t *
     const splosh_q5k_weight *w = &wv;
     if ((st = check_io(a, lda, out, ldc, out_dtype, rows, w->rows, w->inner))) return st;
     const bool planes_ok = aligned(w->plane0, 16) && (!fifth || aligned(w->plane1, 4)) && aligned(w->meta, 16);
+    // 65..128 rows under AUTO: two calls of at most 64 rows, as for q4 (K17408 -> N5120, against the
+    // prefill kernel: M=96 66 -> 54 us, M=128 69 -> 59).
+    if (kernel == SPLOSH_KERNEL_AUTO && rows > 64 && rows <= 128 && planes_ok && lda % 8 == 0 && aligned(a, 16) &&
+        splosh::q5k_mma_fits(64, w->rows, w->inner, lda)) {
+        const char *res = (const char *)residual;
+        const size_t esize = out_dtype == SPLOSH_F32 ? 4 : 2;
+        if ((st = gguf_gemm(w_in, fifth, a, lda, out, ldc, out_dtype, residual, 64, kernel, workspace,
+                            workspace_bytes, stream, key_heads)))
+            return st;
+        return gguf_gemm(w_in, fifth, a + 64 * lda, lda, (char *)out + 64 * ldc * esize, ldc, out_dtype,
+                             res ? res + 64 * ldc * esize : nullptr, rows - 64, kernel, workspace, workspace_bytes,
+                             stream, key_heads);
+    }
     if (kernel == SPLOSH_KERNEL_AUTO && planes_ok && lda % 4 == 0 && aligned(a, 16) &&
         splosh::q5k_decode_fits(rows, w->rows, w->inner))
         return hip_status(splosh::launch_q5k_decode(*w, a, out, out_dtype, residual, workspace,
@@ -778,6 +791,19 @@ static int gguf_native_gemm(int gguf_type, const uint8_t *native, int64_t rows, 
                          splosh::gguf_prefill_fits(gguf_type, m, rows, inner, lda, ldc);
     const int base_type = gguf_type & 0xFF;
     const int64_t stream_max = base_type == 11 ? 6 : base_type == 20 ? 3 : 4;
+    // 65..128 rows: two calls of at most 64 rows, as for q4. K17408 -> N5120, against the tiled
+    // kernel: M=96 Q8_0 80 -> 77 us (ROWS32 79 -> 66), Q6_K 100 -> 90, IQ3_S 105 -> 89, IQ4_NL 81 ->
+    // 63, IQ4_XS 81 -> 70; Q3_K, whose MFMA path is the slowest, 83 -> 96, keeps the tiled kernel.
+    if (base_type != 11 && m > 64 && m <= 128 && splosh::gguf_mma_fits(gguf_type, 64, rows, inner, lda)) {
+        const char *res = (const char *)residual;
+        const size_t esize = out_dtype == SPLOSH_F32 ? 4 : 2;
+        if ((st = gguf_native_gemm(gguf_type, native, rows, inner, a, lda, out, ldc, out_dtype, residual, 64,
+                                   workspace, workspace_bytes, stream, key_heads)))
+            return st;
+        return gguf_native_gemm(gguf_type, native, rows, inner, a + 64 * lda, lda, (char *)out + 64 * ldc * esize,
+                                ldc, out_dtype, res ? res + 64 * ldc * esize : nullptr, m - 64, workspace,
+                                workspace_bytes, stream, key_heads);
+    }
     const bool mma = !prefill && m > stream_max && splosh::gguf_mma_fits(gguf_type, m, rows, inner, lda);
     const bool tile = !prefill && !mma && m > 8 && splosh::gguf_tile_fits(m, rows, inner, lda);
     // The streaming kernels read the activations through head_group(); the other kernels get a
