@@ -121,17 +121,26 @@ def test_mma_kernel(rt, name, rows):
 
 
 @pytest.mark.parametrize("name", list(TYPES))
-def test_rows32_repack_on_device(rt, name):
+@pytest.mark.parametrize("n,k", [(203, 768), (5, 256)])
+def test_rows32_repack_on_device(rt, name, n, k):
     """splosh_gguf_repack_rows32 against the host restatement of the order, byte for byte (the
-    padding rows zero)."""
+    padding rows zero); with fewer rows than one group of 32, the GEMM at 1-64 activation rows and
+    the dequant against the file order's results, bit for bit."""
     from qcheck import rows32_order
     t = TYPES[name]
-    n, k = 203, 768
     native = oracle.gguf_random_native(t, n, k, seed=81 + t)
     w = rt.GgufWeight(torch.from_numpy(native).cuda(), t, n, k)
     w32 = rt.gguf_repack_rows32(w)
-    assert w32.rows32 and w32.native.numel() == 224 * native.size // n
+    assert w32.rows32 and w32.native.numel() == (n + 31) // 32 * 32 * native.size // n
     assert np.array_equal(w32.native.cpu().numpy(), rows32_order(native, t, n, k))
+    if n < 32:
+        dense = oracle.gguf_decode(t, native).reshape(n, k)
+        for rows in (1, 3, 9, 64):
+            a = bf16_tensor(oracle.bf16_normal((rows, k), seed=rows))
+            got = rt.gemm(w, a, out_dtype=torch.float32).cpu().numpy()
+            got32 = rt.gemm(w32, a, out_dtype=torch.float32).cpu().numpy()
+            assert np.array_equal(got, got32), f"{name} n={n} rows={rows}"
+        assert np.array_equal(rt.dequant(w32).cpu().numpy().view(np.uint32), dense.view(np.uint32))
 
 
 @pytest.mark.parametrize("name", list(TYPES))
