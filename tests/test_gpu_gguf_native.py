@@ -228,6 +228,27 @@ def test_streaming_long_k_sampled(rt, name, rows):
 
 
 @pytest.mark.parametrize("name", list(TYPES))
+@pytest.mark.parametrize("rows32", [False, True])
+def test_config3_shape_mma_sampled(rt, name, rows32):
+    """Config 3's shape (K=17408 -> N=5120) at 64 rows in every native format, through AUTO (the
+    stream-K MFMA kernel), in the file's order and the ROWS32 order: 256 sampled columns against
+    the oracle at the tight tolerance."""
+    t = TYPES[name]
+    n, k, rows = 5120, 17408, 64
+    elems, size = oracle.GGUF_BLOCK[t]
+    native = oracle.gguf_random_native(t, n, k, seed=60 + t)
+    w = rt.GgufWeight(torch.from_numpy(native).cuda(), t, n, k)
+    if rows32:
+        w = rt.gguf_repack_rows32(w)
+    a_bits = oracle.bf16_normal((rows, k), seed=61 + t)
+    got = rt.gemm(w, bf16_tensor(a_bits), out_dtype=torch.float32).cpu().numpy()
+    cols = np.sort(np.random.default_rng(62 + t).choice(n, 256, replace=False))
+    dense = oracle.gguf_decode(t, native.reshape(n, k // elems * size)[cols].reshape(-1)).reshape(len(cols), k)
+    check_close(got[:, cols], oracle.gemm_a_bf16_w_f32(a_bits, dense), bf16_out=False, tight=True,
+                absref=abs_gemm(a_bits, dense), label=f"{name} K17408 M=64 rows32={rows32}")
+
+
+@pytest.mark.parametrize("name", list(TYPES))
 @pytest.mark.parametrize("rows", [256, 513])
 @pytest.mark.parametrize("split", [True, False])
 def test_prefill_kernel(rt, name, rows, split):
