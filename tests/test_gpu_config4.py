@@ -90,10 +90,11 @@ def test_wide_weight_as_split_pair(rt, order, rows):
     check_close(got[:, cols], ref + res.cpu().numpy()[:, cols], bf16_out=False, label=f"split {order} residual")
 
 
-@pytest.mark.parametrize("rows", [8, 64])
+@pytest.mark.parametrize("rows", [8, 64, 96])
 def test_fused_gate_up_full_size_auto(rt, rows):
     """Config 1's fused gate+up (K=5120 -> 2 x 17408) through AUTO (the stream-K MFMA kernel the
-    bench times), bf16 out: 512 sampled columns against silu(gate) * up of the oracle."""
+    bench times; 96 rows as two calls of it), bf16 out: 512 sampled columns against silu(gate) * up
+    of the oracle."""
     n, k = 17408, 5120
     gate, up = _full_size_weight(rt, n, k, seed=201), _full_size_weight(rt, n, k, seed=202)
     a_bits = oracle.bf16_normal((rows, k), seed=203)
